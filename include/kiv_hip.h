@@ -1,0 +1,200 @@
+/*
+ * kiv_hip.h - C ABI of the MI355X (gfx950) tiered-KV-cache decode path.
+ *
+ * One opaque store per independent KV layer holds that layer's cold tier:
+ *   - page summaries (mean of the page's post-RoPE K rows) in HBM,
+ *   - the partial (not yet full) page in HBM,
+ *   - finished pages' K and V rows in an arena that lives either in pinned,
+ *     mapped host memory (read zero-copy by the kernels) or in HBM.
+ * All device work is enqueued on the caller's stream; no call synchronises
+ * the host except buffer growth (rare, documented per call) and the
+ * destroy/reset calls.
+ *
+ * Ownership: callers own every q / k / v / out / workspace pointer they pass;
+ * the store owns its summaries, partial page, arena and retrieval scratch.
+ * Threading: a store is not thread-safe; use one stream per store at a time.
+ * Errors: every call returns KIV_OK (0) or a KIV_ERR_* code; the message of
+ * the last failure on the calling thread is returned by kiv_last_error().
+ *
+ * Element strides are in elements, not bytes.  The innermost (head_dim)
+ * stride is always 1.
+ */
+#ifndef KIV_HIP_H
+#define KIV_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct kiv_store kiv_store_t;
+typedef void *kiv_stream_t; /* a hipStream_t; NULL selects the null stream */
+
+enum {
+  KIV_OK = 0,
+  KIV_ERR_INVALID = 1,     /* bad argument or shape */
+  KIV_ERR_HIP = 2,         /* a HIP runtime call failed */
+  KIV_ERR_OOM = 3,         /* device or pinned-host allocation failed */
+  KIV_ERR_UNSUPPORTED = 4, /* shape outside what the kernels handle */
+  KIV_ERR_STATE = 5        /* call not valid in the store's current state */
+};
+
+enum { KIV_DTYPE_F32 = 0, KIV_DTYPE_F16 = 1, KIV_DTYPE_BF16 = 2 };
+enum { KIV_TIER_HOST = 0, KIV_TIER_HBM = 1 };
+enum { KIV_ROUND_ACTIVATION = 0, KIV_ROUND_FP32 = 1 };
+enum { KIV_MASK_NONE = 0, KIV_MASK_BOOL = 1, KIV_MASK_F32 = 2, KIV_MASK_F16 = 3, KIV_MASK_BF16 = 4 };
+
+typedef struct {
+  int32_t batch;          /* B */
+  int32_t num_q_heads;    /* Hq */
+  int32_t num_kv_heads;   /* Hkv; Hq % Hkv == 0, q head h reads kv head h / (Hq/Hkv) */
+  int32_t head_dim;       /* D: 64, 96, 128 or 256 (any multiple of 8 up to 256) */
+  int32_t page_size;      /* tokens per page (>= 1) */
+  int32_t dtype;          /* KIV_DTYPE_* of K, V, Q and outputs */
+  int32_t cold_tier;      /* KIV_TIER_* placement of finished pages' rows */
+  int32_t score_rounding; /* KIV_ROUND_* */
+  int64_t reserve_tokens; /* capacity hint (0 = grow on demand) */
+} kiv_store_config_t;
+
+typedef struct {
+  int64_t cold_length;   /* finished-page tokens + partial tokens */
+  int64_t num_pages;     /* finished pages */
+  int64_t partial_len;   /* tokens in the partial page */
+  int64_t k_cold_bytes;  /* K rows of finished pages (arena, used part) */
+  int64_t v_cold_bytes;  /* V rows of finished pages (arena, used part) */
+  int64_t summary_bytes; /* dtype page summaries (used part) */
+  int64_t partial_bytes; /* K + V rows of the partial page */
+  int64_t reserved_bytes;/* everything the store holds, host + device */
+} kiv_store_info_t;
+
+/* Arguments of one retrieval: coarse page scan, union of per-row top
+ * pages, fine per-token scoring, top-P and K/V gather. */
+typedef struct {
+  const void *q;         /* [B, Hq, Q, D] activation dtype */
+  int64_t q_stride[4];   /* b, h, q, d (d stride must be 1) */
+  int32_t q_len;         /* Q >= 1 */
+  float scaling;         /* applied after the dot product */
+  int32_t top_pages;     /* pages kept per (b, q head, q position) */
+  int32_t out_width;     /* P' = min(top_p, cold_length, candidates) */
+  int32_t reuse_candidates; /* 1: skip the coarse pass, reuse the last union */
+  int32_t _pad;
+  void *k_out;           /* [B, Hkv, P', D] contiguous, score-descending */
+  void *v_out;           /* [B, Hkv, P', D] contiguous */
+  int64_t *idx_out;      /* [B, P'] global cold token ids, or NULL */
+  int32_t *pages_out;    /* [max_union] union page ids ascending, or NULL */
+  int32_t *union_count_out; /* [1] number of union pages U, or NULL */
+  float *stats_out;      /* [4] coarse top, coarse mean, fine top, fine mean, or NULL */
+  double *stats_accum;   /* [4] running sums of stats_out, or NULL */
+} kiv_retrieve_args_t;
+
+/* Arguments of the merged decode attention over [retrieved ; hot]. */
+typedef struct {
+  int32_t batch, num_q_heads, num_kv_heads, head_dim, q_len, dtype;
+  const void *q;           /* [B, Hq, Q, D] */
+  int64_t q_stride[4];
+  const void *cold_k;      /* [B, Hkv, P, D] contiguous, may be NULL when P == 0 */
+  const void *cold_v;
+  int32_t cold_len;        /* P */
+  int32_t hot_len;         /* T_hot */
+  const void *hot_k;       /* [B, Hkv, T_hot, D] */
+  const void *hot_v;
+  int64_t hot_k_stride[3]; /* b, h, t */
+  int64_t hot_v_stride[3];
+  const void *mask;        /* over hot columns only, or NULL */
+  int32_t mask_kind;       /* KIV_MASK_*; bool: nonzero = attend; float: additive */
+  int32_t _pad;
+  int64_t mask_stride[4];  /* b, h, q, t (0 broadcasts) */
+  float scaling;
+  int32_t _pad2;
+  void *out;               /* [B, Q, Hq, D] contiguous, activation dtype */
+  void *workspace;         /* device scratch, >= kiv_attention_workspace_size() */
+  size_t workspace_bytes;
+} kiv_attention_args_t;
+
+/* Library version (major * 10000 + minor * 100 + patch). */
+int kiv_version(void);
+
+/* Message of the last failed call on this thread ("" if none). */
+const char *kiv_last_error(void);
+
+/* Create a cold store on `device`.
+ * Replaces ColdKVStore.__init__ (kiv/cold_store.py:47-90). */
+int kiv_store_create(const kiv_store_config_t *cfg, int device, kiv_store_t **out);
+
+/* Release the store and everything it holds (synchronises the device). */
+int kiv_store_destroy(kiv_store_t *store);
+
+/* Drop all cold tokens, keep allocations for reuse (synchronises).
+ * Replaces ColdKVStore.reset (kiv/cold_store.py:374-389). */
+int kiv_store_reset(kiv_store_t *store);
+
+/* Sizes and per-tier bytes; host-side bookkeeping, no device work.
+ * Replaces ColdKVStore.cold_length / num_pages / memory_bytes
+ * (kiv/cold_store.py:111-120, 399-414). */
+int kiv_store_info(const kiv_store_t *store, kiv_store_info_t *out);
+
+/* Append T evicted rows [B, Hkv, T, D] (strides b, h, t in elements).
+ * Every page that fills gets its fp32 mean-K summary written to HBM (and
+ * its dtype rounding) and its K/V rows streamed to the arena.
+ * Replaces ColdKVStore.evict_from_hot (kiv/cold_store.py:142-184). */
+int kiv_evict(kiv_store_t *store, const void *k, const int64_t k_stride[3],
+              const void *v, const int64_t v_stride[3], int64_t num_tokens,
+              kiv_stream_t stream);
+
+/* Upper bound of the union size for a retrieval with these sizes:
+ * min(num_pages, B * Hq * q_len * min(top_pages, num_pages)). Host only. */
+int kiv_max_union_pages(const kiv_store_t *store, int32_t q_len, int32_t top_pages,
+                        int64_t *out);
+
+/* Coarse-to-fine retrieval into caller buffers.
+ * Replaces ColdKVStore._select_candidates + retrieve_top_kv
+ * (kiv/cold_store.py:186-280, 283-371). */
+int kiv_retrieve(kiv_store_t *store, const kiv_retrieve_args_t *args, kiv_stream_t stream);
+
+/* Copy `n_pages` page summaries starting at `first_page` into
+ * out_dtype ([n, B*Hkv, D] dtype) and/or out_f32 ([n, B*Hkv, D] fp32);
+ * either may be NULL.  Device-to-device, stream ordered. */
+int kiv_store_read_summaries(kiv_store_t *store, int64_t first_page, int64_t n_pages,
+                             void *out_dtype, float *out_f32, kiv_stream_t stream);
+
+/* Gather cold tokens [first, first + n) into k_out / v_out
+ * ([B, Hkv, n, D] contiguous, device).  Stream ordered. */
+int kiv_store_read_tokens(kiv_store_t *store, int64_t first, int64_t n, void *k_out,
+                          void *v_out, kiv_stream_t stream);
+
+/* Instrumentation (no counterpart in the reference; used by benchmarks).
+ * While enabled, every kernel the store launches is bracketed by a pair of
+ * HIP events on the caller's stream (the last 256 calls per stage are
+ * kept).  kiv_profile_read synchronises the device, writes per-stage launch
+ * counts and summed durations (ms) for the KIV_STAGE_* stages, and clears
+ * the record. */
+enum {
+  KIV_STAGE_EVICT_APPEND = 0,
+  KIV_STAGE_EVICT_FINALIZE = 1,
+  KIV_STAGE_COARSE_SCAN = 2,
+  KIV_STAGE_COARSE_SELECT = 3,
+  KIV_STAGE_FINE_SCAN = 4,
+  KIV_STAGE_FINE_SELECT = 5,
+  KIV_STAGE_GATHER = 6,
+  KIV_NUM_STAGES = 7
+};
+int kiv_profile_enable(kiv_store_t *store, int enable);
+int kiv_profile_read(kiv_store_t *store, int64_t counts[KIV_NUM_STAGES], double total_ms[KIV_NUM_STAGES]);
+
+/* Workspace bytes kiv_decode_attention needs for these sizes. */
+size_t kiv_attention_workspace_size(int32_t batch, int32_t num_q_heads, int32_t num_kv_heads,
+                                    int32_t head_dim, int32_t q_len, int32_t total_keys);
+
+/* One softmax over [retrieved ; hot] keys per query row, fp32 accumulate,
+ * output in the activation dtype.  Retrieved columns are never masked.
+ * Replaces the concatenation in kiv_attention plus the original attention
+ * call (kiv/middleware.py:330-354). */
+int kiv_decode_attention(const kiv_attention_args_t *args, kiv_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* KIV_HIP_H */

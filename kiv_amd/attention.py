@@ -1,0 +1,101 @@
+"""Merged decode attention over [retrieved ; hot] (kiv_decode_attention).
+
+One kernel launch replaces the wrapper's two ``torch.cat`` calls, the mask
+widening and the attention call (kiv/middleware.py:330-354): retrieved keys
+are always attended, an optional mask applies to the hot columns only.
+"""
+
+from __future__ import annotations
+
+import ctypes as C
+import threading
+
+import torch
+
+from . import _native as nat
+
+_ws_lock = threading.Lock()
+_workspaces: dict[int, torch.Tensor] = {}
+
+
+def _workspace(device: torch.device, nbytes: int) -> torch.Tensor:
+    """Zero-filled scratch per device; the kernel leaves its counters zeroed.
+
+    Shared by every call on the device, so concurrent calls on different
+    streams of one device must not overlap.
+    """
+    idx = device.index or 0
+    with _ws_lock:
+        ws = _workspaces.get(idx)
+        if ws is None or ws.numel() < nbytes:
+            ws = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
+            _workspaces[idx] = ws
+        return ws
+
+
+def _mask_view(mask: torch.Tensor | None, hot_len: int):
+    """(pointer, kind, strides b,h,q,t) of a 2-D or 4-D mask over hot columns."""
+    if mask is None:
+        return None, nat.MASK_NONE, (C.c_int64 * 4)()
+    if mask.shape[-1] != hot_len:
+        raise ValueError(f"mask covers {mask.shape[-1]} columns, hot window has {hot_len}")
+    if mask.dim() == 2:
+        mask = mask[:, None, None, :]
+    if mask.dim() != 4:
+        raise ValueError(f"unsupported mask rank {mask.dim()}")
+    return mask.data_ptr(), nat.mask_kind(mask.dtype), nat.strides(mask, 4)
+
+
+def decode_attention(query: torch.Tensor, cold_k: torch.Tensor | None, cold_v: torch.Tensor | None,
+                     hot_k: torch.Tensor, hot_v: torch.Tensor, mask: torch.Tensor | None,
+                     scaling: float) -> torch.Tensor:
+    """softmax(q [cold; hot]^T * scaling + [0; mask]) [cold; hot] -> [B, Q, Hq, D]."""
+    B, hq, Q, D = query.shape
+    hkv = hot_k.shape[1]
+    dt = query.dtype
+    if cold_k is not None and (cold_k.dtype != dt or not cold_k.is_contiguous()):
+        cold_k, cold_v = cold_k.to(dt).contiguous(), cold_v.to(dt).contiguous()
+    if hot_k.dtype != dt:
+        hot_k, hot_v = hot_k.to(dt), hot_v.to(dt)
+    if hot_k.stride(3) != 1:
+        hot_k = hot_k.contiguous()
+    if hot_v.stride(3) != 1:
+        hot_v = hot_v.contiguous()
+    q = query if query.stride(3) == 1 else query.contiguous()
+    P = 0 if cold_k is None else cold_k.shape[2]
+    T = hot_k.shape[2]
+    lib = nat.lib()
+    need = lib.kiv_attention_workspace_size(B, hq, hkv, D, Q, P + T)
+    ws = _workspace(query.device, need)
+    out = torch.empty(B, Q, hq, D, dtype=dt, device=query.device)
+    mptr, mkind, mstr = _mask_view(mask, T)
+    args = nat.AttentionArgs(
+        batch=B, num_q_heads=hq, num_kv_heads=hkv, head_dim=D, q_len=Q, dtype=nat.dtype_code(dt),
+        q=q.data_ptr(), q_stride=nat.strides(q, 4),
+        cold_k=nat.ptr(cold_k), cold_v=nat.ptr(cold_v), cold_len=P, hot_len=T,
+        hot_k=hot_k.data_ptr(), hot_v=hot_v.data_ptr(),
+        hot_k_stride=nat.strides(hot_k, 3), hot_v_stride=nat.strides(hot_v, 3),
+        mask=mptr, mask_kind=mkind, mask_stride=mstr, scaling=float(scaling),
+        out=out.data_ptr(), workspace=ws.data_ptr(), workspace_bytes=ws.numel(),
+    )
+    nat.check(lib.kiv_decode_attention(C.byref(args), nat.stream_ptr(query.device)), "kiv_decode_attention")
+    return out
+
+
+def fused_supported(query: torch.Tensor, hot_k: torch.Tensor, mask: torch.Tensor | None) -> bool:
+    """Shapes the merged kernel handles: one query position per step (decode),
+    GQA groups of at most 64 rows, head_dim a multiple of 16 bytes."""
+    if not query.is_cuda or query.dtype not in (torch.float16, torch.bfloat16, torch.float32):
+        return False
+    B, hq, Q, D = query.shape
+    hkv = hot_k.shape[1]
+    if Q != 1 or hq % hkv:
+        return False
+    g = hq // hkv
+    vec = 4 if query.dtype == torch.float32 else 8
+    if g > 64 or g * D > 8192 or D % vec or D // vec > 64:
+        return False
+    if mask is not None and (mask.dim() not in (2, 4) or mask.dtype not in
+                             (torch.bool, torch.float32, torch.float16, torch.bfloat16)):
+        return False
+    return True

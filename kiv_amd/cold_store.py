@@ -1,0 +1,381 @@
+"""Cold tier of one independent KV layer, backed by the gfx950 HIP kernels.
+
+Drop-in for the reference's ``ColdKVStore`` (kiv/cold_store.py:35-414): same
+constructor, ``evict_from_hot`` / ``retrieve_top_kv`` / ``cold_length`` /
+``num_pages`` / ``reset`` / ``telemetry_snapshot`` / ``reset_telemetry`` /
+``memory_bytes`` and the ``_cached_candidate_*`` / ``_cached_step``
+attributes other code clears.  The state lives in a native store
+(include/kiv_hip.h): page summaries and the partial page in HBM, finished
+pages' K/V rows in pinned mapped host memory (or HBM, ``cold_tier="hbm"``).
+
+Every device call is enqueued on torch's current stream; retrieval does not
+synchronise the host except when the output width depends on the union size
+(only possible when ``top_p > top_pages * page_size``).  There is no CPU
+implementation: a store on a non-GPU device raises on its first eviction.
+"""
+
+from __future__ import annotations
+
+import ctypes as C
+import math
+
+import torch
+
+from . import _native as nat
+from .config import KIVConfig
+from .model_topology import ModelTopology
+
+
+class _CandidateSet:
+    """Marker that the last coarse union may be reused (shape[0] = batch)."""
+
+    __slots__ = ("shape",)
+
+    def __init__(self, batch: int) -> None:
+        self.shape = (batch,)
+
+
+class ColdKVStore:
+    """Evicted tokens of one layer, paged, with coarse-to-fine retrieval."""
+
+    def __init__(self, kiv_config: KIVConfig, topology: ModelTopology, device: torch.device) -> None:
+        self.kiv_config = kiv_config
+        self.device = torch.device(device)
+        self._num_query_heads = topology.num_query_heads
+        self._num_kv_heads = topology.num_kv_heads
+        self._num_kv_groups = topology.num_query_heads // topology.num_kv_heads
+        self._head_dim = topology.head_dim
+        self._page_size = kiv_config.page_size
+        self._handle: int | None = None
+        self._batch: int | None = None
+        self._dtype: torch.dtype | None = None
+        self._num_finalized = 0
+        self._partial_len = 0
+        self._last_union_count: torch.Tensor | None = None
+        # Shared-layer reuse of the last coarse union (kiv/cold_store.py:81-85).
+        self._cached_candidate_k = None
+        self._cached_candidate_v = None
+        self._cached_candidate_idx = None
+        self._cached_step = -1
+        self._telemetry = _RetrievalTelemetry()
+
+    # ------------------------------------------------------------ lifetime
+    def __del__(self) -> None:
+        self._destroy()
+
+    def _destroy(self) -> None:
+        h, self._handle = getattr(self, "_handle", None), None
+        if h is not None:
+            try:
+                nat.lib().kiv_store_destroy(h)
+            except Exception:
+                pass
+
+    def _ensure_handle(self, k: torch.Tensor) -> None:
+        if self._handle is not None:
+            return
+        if k.device.type != "cuda":
+            raise RuntimeError(
+                "ColdKVStore needs a ROCm GPU tensor: the cold tier runs only as HIP kernels "
+                f"(got a tensor on {k.device})"
+            )
+        cfg = nat.StoreConfig(
+            batch=k.shape[0],
+            num_q_heads=self._num_query_heads,
+            num_kv_heads=self._num_kv_heads,
+            head_dim=self._head_dim,
+            page_size=self._page_size,
+            dtype=nat.dtype_code(k.dtype),
+            cold_tier=nat.TIER_HOST if self.kiv_config.cold_tier == "host" else nat.TIER_HBM,
+            score_rounding=(nat.ROUND_ACTIVATION if self.kiv_config.score_rounding == "activation"
+                            else nat.ROUND_FP32),
+            reserve_tokens=int(self.kiv_config.reserve_tokens),
+        )
+        handle = C.c_void_p()
+        nat.check(nat.lib().kiv_store_create(C.byref(cfg), k.device.index or 0, C.byref(handle)),
+                  "kiv_store_create")
+        self._handle = handle.value
+        self._batch = k.shape[0]
+        self._dtype = k.dtype
+        self.device = k.device
+
+    # ------------------------------------------------------------- sizes
+    @property
+    def cold_length(self) -> int:
+        return self._num_finalized + self._partial_len
+
+    @property
+    def num_pages(self) -> int:
+        return self._num_finalized // self._page_size
+
+    @property
+    def _partial_len_tokens(self) -> int:
+        return self._partial_len
+
+    # ----------------------------------------------------------- eviction
+    def evict_from_hot(self, k_evicted: torch.Tensor, v_evicted: torch.Tensor) -> None:
+        """Append [B, Hkv, T, D] rows; full pages get summaries and move to the arena.
+
+        Same contract as kiv/cold_store.py:142-184.
+        """
+        self._invalidate_candidates()
+        if k_evicted.dim() != 4 or k_evicted.shape != v_evicted.shape:
+            raise ValueError(f"expected matching [B, Hkv, T, D] K/V, got {tuple(k_evicted.shape)} "
+                             f"and {tuple(v_evicted.shape)}")
+        T = k_evicted.shape[2]
+        if T == 0:
+            return
+        self._ensure_handle(k_evicted)
+        B, hkv, _, d = k_evicted.shape
+        if B != self._batch or hkv != self._num_kv_heads or d != self._head_dim:
+            raise ValueError(f"evicted rows {tuple(k_evicted.shape)} do not match the store "
+                             f"(B={self._batch}, Hkv={self._num_kv_heads}, D={self._head_dim})")
+        if k_evicted.dtype != self._dtype or v_evicted.dtype != self._dtype:
+            raise TypeError(f"evicted rows are {k_evicted.dtype}, the store holds {self._dtype}")
+        k = k_evicted if k_evicted.stride(3) == 1 else k_evicted.contiguous()
+        v = v_evicted if v_evicted.stride(3) == 1 else v_evicted.contiguous()
+        nat.check(nat.lib().kiv_evict(self._handle, k.data_ptr(), nat.strides(k, 3), v.data_ptr(),
+                                      nat.strides(v, 3), T, nat.stream_ptr(self.device)), "kiv_evict")
+        total = self._partial_len + T
+        self._num_finalized += (total // self._page_size) * self._page_size
+        self._partial_len = total % self._page_size
+
+    def _invalidate_candidates(self) -> None:
+        self._cached_candidate_k = None
+        self._cached_candidate_v = None
+        self._cached_candidate_idx = None
+        self._cached_step = -1
+
+    # ---------------------------------------------------------- retrieval
+    def retrieve_top_kv(self, query: torch.Tensor, scaling: float, kiv_config: KIVConfig,
+                        step: int = -1):
+        """Top-P cold K/V ``[B, Hkv, P', D]`` in descending score order, or (None, None).
+
+        Same contract as kiv/cold_store.py:283-371: coarse page scores against
+        the summaries, union of every (batch, head, position)'s top pages,
+        fine scores max-reduced over heads and positions, top-P per batch row.
+        """
+        if self.cold_length == 0:
+            return None, None
+        if query.dim() != 4 or query.shape[1] != self._num_query_heads or query.shape[3] != self._head_dim:
+            raise ValueError(f"query must be [B, {self._num_query_heads}, Q, {self._head_dim}], "
+                             f"got {tuple(query.shape)}")
+        if query.shape[0] != self._batch:
+            raise ValueError(f"query batch {query.shape[0]} != store batch {self._batch}")
+        if query.device != self.device:
+            raise ValueError(f"query on {query.device}, store on {self.device}")
+        q = query if query.dtype == self._dtype else query.to(self._dtype)
+        if q.stride(3) != 1:
+            q = q.contiguous()
+        B, _, Q, D = q.shape
+        P = min(kiv_config.top_p, self.cold_length)
+        N = self.num_pages
+        reuse = (step >= 0 and step == self._cached_step and self._cached_candidate_k is not None
+                 and self._cached_candidate_k.shape[0] == B)
+        # Lower bound of the candidate count: the union holds at least
+        # min(top_pages, N) pages (exactly N when every page is selected).
+        c_low = min(kiv_config.top_pages, N) * self._page_size + self._partial_len
+        width = min(P, c_low)
+        exact = width == P
+        if not exact:
+            width = P  # buffer width; the true count follows from U below
+
+        lib = nat.lib()
+        umax = C.c_int64(0)
+        nat.check(lib.kiv_max_union_pages(self._handle, Q, kiv_config.top_pages, C.byref(umax)),
+                  "kiv_max_union_pages")
+        dev = self.device
+        k_out = torch.empty(B, self._num_kv_heads, width, D, dtype=self._dtype, device=dev)
+        v_out = torch.empty_like(k_out)
+        idx_out = torch.empty(B, width, dtype=torch.int64, device=dev)
+        coarse_runs = N > 0 and not reuse
+        # Kernels fill every entry they own, so no zero-fill launches here.
+        union_count = torch.empty(1, dtype=torch.int32, device=dev) if coarse_runs else None
+        pages_out = torch.empty(max(1, umax.value), dtype=torch.int32, device=dev) if coarse_runs else None
+        stats = torch.empty(4, dtype=torch.float32, device=dev)
+        accum = self._telemetry.accumulator(dev)
+        args = nat.RetrieveArgs(
+            q=q.data_ptr(), q_stride=nat.strides(q, 4), q_len=Q, scaling=float(scaling),
+            top_pages=int(kiv_config.top_pages), out_width=int(width), reuse_candidates=1 if reuse else 0,
+            k_out=k_out.data_ptr(), v_out=v_out.data_ptr(), idx_out=idx_out.data_ptr(),
+            pages_out=nat.ptr(pages_out), union_count_out=nat.ptr(union_count),
+            stats_out=stats.data_ptr(), stats_accum=accum.data_ptr(),
+        )
+        nat.check(lib.kiv_retrieve(self._handle, C.byref(args), nat.stream_ptr(dev)), "kiv_retrieve")
+
+        if coarse_runs:
+            self._last_union_count = union_count
+            self._telemetry.record_coarse(stats=stats, pages=pages_out, union_count=union_count,
+                                          num_pages=N, cold_length=self.cold_length)
+        else:
+            self._telemetry.record_coarse_skipped(cold_length=self.cold_length)
+        if not reuse:
+            self._cached_candidate_k = _CandidateSet(B)
+            self._cached_candidate_v = self._cached_candidate_k
+            self._cached_candidate_idx = self._cached_candidate_k
+            if step >= 0:
+                self._cached_step = step
+
+        if not exact:
+            # Only reachable when top_p > top_pages * page_size: the output
+            # width depends on the union size, so read U back.
+            U = int(self._last_union_count.item()) if N > 0 else 0
+            actual = min(P, U * self._page_size + self._partial_len)
+            k_out, v_out, idx_out = k_out[:, :, :actual], v_out[:, :, :actual], idx_out[:, :actual]
+            width = actual
+        self._telemetry.record_fine(stats=stats, selected=idx_out, actual_P=width,
+                                    requested_P=int(kiv_config.top_p), cold_length=self.cold_length)
+        return k_out, v_out
+
+    # ------------------------------------------------------ bookkeeping
+    def reset(self) -> None:
+        """Drop every cold token (kiv/cold_store.py:374-389); allocations are kept."""
+        if self._handle is not None:
+            nat.check(nat.lib().kiv_store_reset(self._handle), "kiv_store_reset")
+        self._num_finalized = 0
+        self._partial_len = 0
+        self._invalidate_candidates()
+
+    def telemetry_snapshot(self) -> dict:
+        return self._telemetry.snapshot()
+
+    def reset_telemetry(self) -> None:
+        self._telemetry = _RetrievalTelemetry()
+
+    def memory_bytes(self) -> dict[str, int]:
+        """Bytes per tier, keys as kiv/cold_store.py:399-414 (+ HBM-tier rows)."""
+        out = {"k_index_cpu": 0, "v_store_cpu": 0, "page_summaries_gpu": 0, "partial_gpu": 0,
+               "k_cold_gpu": 0, "v_cold_gpu": 0}
+        if self._handle is None:
+            return out
+        info = nat.StoreInfo()
+        nat.check(nat.lib().kiv_store_info(self._handle, C.byref(info)), "kiv_store_info")
+        if self.kiv_config.cold_tier == "host":
+            out["k_index_cpu"], out["v_store_cpu"] = info.k_cold_bytes, info.v_cold_bytes
+        else:
+            out["k_cold_gpu"], out["v_cold_gpu"] = info.k_cold_bytes, info.v_cold_bytes
+        out["page_summaries_gpu"] = info.summary_bytes
+        out["partial_gpu"] = info.partial_bytes
+        return out
+
+    # ------------------------------------------------- inspection (tests)
+    def read_summaries(self) -> tuple[torch.Tensor, torch.Tensor]:
+        """(dtype summaries, fp32 means), each [N, B, Hkv, D], copied from HBM."""
+        N = self.num_pages
+        shape = (N, self._batch or 1, self._num_kv_heads, self._head_dim)
+        s = torch.empty(shape, dtype=self._dtype or torch.float32, device=self.device)
+        s32 = torch.empty(shape, dtype=torch.float32, device=self.device)
+        if N:
+            nat.check(nat.lib().kiv_store_read_summaries(self._handle, 0, N, s.data_ptr(), s32.data_ptr(),
+                                                         nat.stream_ptr(self.device)), "read_summaries")
+        return s, s32
+
+    def read_tokens(self, first: int = 0, n: int | None = None) -> tuple[torch.Tensor, torch.Tensor]:
+        """Cold tokens [first, first+n) as [B, Hkv, n, D] K and V on the device."""
+        n = self.cold_length - first if n is None else n
+        k = torch.empty(self._batch or 1, self._num_kv_heads, n, self._head_dim,
+                        dtype=self._dtype or torch.float32, device=self.device)
+        v = torch.empty_like(k)
+        if n:
+            nat.check(nat.lib().kiv_store_read_tokens(self._handle, first, n, k.data_ptr(), v.data_ptr(),
+                                                      nat.stream_ptr(self.device)), "read_tokens")
+        return k, v
+
+
+class _RetrievalTelemetry:
+    """Per-call coarse/fine records in a 256-entry ring, read lazily.
+
+    Same schema as kiv/cold_store.py:417-581.  Kernels write each call's
+    statistics, union pages and selected ids into small device tensors and
+    add the scores to a device accumulator, so recording costs no host
+    synchronisation; :meth:`snapshot` converts everything at once.
+    """
+
+    _MAX_BUFFER = 256
+
+    def __init__(self) -> None:
+        self.total_calls = 0
+        self.coarse_calls = 0
+        self.coarse_real_calls = 0
+        self.coarse_cold_length_sum = 0
+        self.fine_calls = 0
+        self.selected_count_sum = 0
+        self._accum: torch.Tensor | None = None
+        self._ring: list[dict] = []
+
+    def accumulator(self, device: torch.device) -> torch.Tensor:
+        if self._accum is None:
+            self._accum = torch.zeros(4, dtype=torch.float64, device=device)
+        return self._accum
+
+    def _push(self, rec: dict) -> None:
+        self._ring.append(rec)
+        if len(self._ring) > self._MAX_BUFFER:
+            del self._ring[: len(self._ring) - self._MAX_BUFFER]
+
+    def record_coarse(self, *, stats, pages, union_count, num_pages, cold_length) -> None:
+        self.coarse_calls += 1
+        self.coarse_real_calls += 1
+        self.coarse_cold_length_sum += cold_length
+        self._push({"kind": "coarse", "cold_length": cold_length, "num_pages": num_pages,
+                    "_stats": stats, "_pages": pages, "_count": union_count, "skipped": False})
+
+    def record_coarse_skipped(self, *, cold_length: int) -> None:
+        self.coarse_calls += 1
+        self.coarse_cold_length_sum += cold_length
+        self._push({"kind": "coarse", "cold_length": cold_length, "num_pages": 0,
+                    "num_pages_selected": 0, "top_score": 0.0, "mean_score": 0.0, "score_ratio": 0.0,
+                    "pages_selected": [], "skipped": True})
+
+    def record_fine(self, *, stats, selected, actual_P, requested_P, cold_length) -> None:
+        self.fine_calls += 1
+        self.total_calls += 1
+        self.selected_count_sum += actual_P
+        self._push({"kind": "fine", "cold_length": cold_length, "actual_P": actual_P,
+                    "requested_P": requested_P, "_stats": stats, "_selected": selected})
+
+    @staticmethod
+    def _ratio(top: float, mean: float) -> float:
+        return (top / abs(mean)) if mean else math.inf
+
+    def _materialise(self, rec: dict) -> dict:
+        if "_stats" not in rec:
+            return dict(rec)
+        stats = rec["_stats"].tolist()
+        out = {k: v for k, v in rec.items() if not k.startswith("_")}
+        if rec["kind"] == "coarse":
+            n = int(rec["_count"].item())
+            pages = rec["_pages"][:n].tolist()
+            top, mean = stats[0], stats[1]
+            out.update(num_pages_selected=len(pages), top_score=top, mean_score=mean,
+                       score_ratio=self._ratio(top, mean), pages_selected=pages)
+            out = {k: out[k] for k in ("kind", "cold_length", "num_pages", "num_pages_selected",
+                                       "top_score", "mean_score", "score_ratio", "pages_selected",
+                                       "skipped")}
+        else:
+            top, mean = stats[2], stats[3]
+            out.update(top_score=top, mean_score=mean, score_ratio=self._ratio(top, mean),
+                       selected_token_indices=rec["_selected"].reshape(-1).tolist())
+            out = {k: out[k] for k in ("kind", "cold_length", "actual_P", "requested_P", "top_score",
+                                       "mean_score", "score_ratio", "selected_token_indices")}
+        return out
+
+    def snapshot(self) -> dict:
+        sums = self._accum.tolist() if self._accum is not None else [0.0] * 4
+        agg = {
+            "total_calls": self.total_calls,
+            "coarse_calls": self.coarse_calls,
+            "coarse_real_calls": self.coarse_real_calls,
+            "coarse_skipped_calls": self.coarse_calls - self.coarse_real_calls,
+            "fine_calls": self.fine_calls,
+        }
+        if self.coarse_real_calls:
+            agg["avg_coarse_top_score"] = sums[0] / self.coarse_real_calls
+            agg["avg_coarse_mean_score"] = sums[1] / self.coarse_real_calls
+        if self.coarse_calls:
+            agg["avg_cold_length"] = self.coarse_cold_length_sum / self.coarse_calls
+        if self.fine_calls:
+            agg["avg_fine_top_score"] = sums[2] / self.fine_calls
+            agg["avg_fine_mean_score"] = sums[3] / self.fine_calls
+            agg["avg_selected_P"] = self.selected_count_sum / self.fine_calls
+        return {"aggregates": agg, "recent": [self._materialise(r) for r in self._ring]}

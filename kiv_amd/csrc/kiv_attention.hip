@@ -1,0 +1,363 @@
+// Merged decode attention over [retrieved ; hot] keys.
+//
+// Replaces, for decode-sized queries, the wrapper's concatenation of the
+// retrieved K/V in front of the hot window plus the model's attention call
+// (kiv/middleware.py:330-354; eager attention: scores * scaling + mask,
+// softmax in fp32, weights @ V).  The two key sets are read in place - the
+// concatenated K/V and widened mask are never built.  Scores, softmax and
+// the weighted sum are fp32; the output is rounded once to the dtype.
+//
+// Grid (S, B*Hkv): block (s, r) takes keys [s*CH, (s+1)*CH) of the virtual
+// sequence for kv row r and all G*Q query rows reading it, writes the split's
+// running max m, sum l and unnormalised accumulator, and the last block of
+// row r merges the S splits (log-sum-exp) into the output.
+#include <algorithm>
+#include <type_traits>
+
+#include "kiv_common.h"
+#include "kiv_dispatch.h"
+#include "kiv_internal.h"
+
+namespace kiv {
+
+constexpr int kAttnThreads = 256;
+constexpr int kRowTile = 8;
+
+struct AttnParams {
+  const char *q;
+  int64_t qs0, qs1, qs2;
+  const char *cold_k, *cold_v;
+  int cold_len, hot_len;
+  const char *hot_k, *hot_v;
+  int64_t hks0, hks1, hks2, hvs0, hvs1, hvs2;
+  const char *mask;
+  int mask_kind;
+  int64_t ms0, ms1, ms2, ms3;
+  int batch, hq, hkv, qlen, head_dim;
+  float scale;
+  int chunk, nsplit;
+  float *ws_m, *ws_l, *ws_acc;
+  int *ws_cnt;
+  char *out;
+};
+
+__device__ __forceinline__ float mask_bias(const AttnParams &p, int b, int h, int qp, int t) {
+  const int64_t o = (int64_t)b * p.ms0 + (int64_t)h * p.ms1 + (int64_t)qp * p.ms2 + (int64_t)t * p.ms3;
+  switch (p.mask_kind) {
+    case KIV_MASK_BOOL: return p.mask[o] ? 0.f : -INFINITY;
+    case KIV_MASK_F32: return load_elem<DT_F32>(p.mask, o);
+    case KIV_MASK_F16: return load_elem<DT_F16>(p.mask, o);
+    case KIV_MASK_BF16: return load_elem<DT_BF16>(p.mask, o);
+  }
+  return 0.f;
+}
+
+template <int DT, int LG>
+__global__ void __launch_bounds__(kAttnThreads) decode_attn_kernel(AttnParams p) {
+  constexpr int VEC = Elem<DT>::VEC, EB = Elem<DT>::BYTES;
+  constexpr int NSLOT = kAttnThreads / LG;
+  constexpr int UT = 4;
+  const int s = blockIdx.x, r = blockIdx.y;
+  const int b = r / p.hkv, kvh = r % p.hkv;
+  const int G = p.hq / p.hkv, GQ = G * p.qlen, D = p.head_dim, CH = p.chunk;
+  const int cpr = D / VEC;
+  const int rows_total = p.batch * p.hq * p.qlen;
+  extern __shared__ float smem[];
+  float *qf = smem;                 // [GQ][D]
+  float *sc = qf + GQ * D;          // [GQ][CH]
+  float *red = sc + GQ * CH;        // [4 waves][kRowTile][D]
+  float *rm = red + 4 * kRowTile * D;  // [GQ] split max
+  float *rl = rm + GQ;                 // [GQ] split sum
+  __shared__ int is_last;
+  const int tid = threadIdx.x;
+  for (int i = tid; i < GQ * D; i += kAttnThreads) {
+    const int j = i / D, d = i % D;
+    const int h = kvh * G + j / p.qlen, qp = j % p.qlen;
+    qf[i] = load_elem<DT>(p.q, (int64_t)b * p.qs0 + (int64_t)h * p.qs1 + (int64_t)qp * p.qs2 + d);
+  }
+  const int L = p.cold_len + p.hot_len;
+  const int k0 = s * CH;
+  const int nk = min(CH, L - k0);
+  __syncthreads();
+
+  const int slot = tid / LG, lane = tid % LG;
+  const bool on = lane < cpr;
+  auto key_row = [&](int kk, bool value) -> const char * {
+    if (kk < p.cold_len)
+      return (value ? p.cold_v : p.cold_k) + (((int64_t)r * p.cold_len + kk) * D) * EB;
+    const int t = kk - p.cold_len;
+    return value ? p.hot_v + ((int64_t)b * p.hvs0 + (int64_t)kvh * p.hvs1 + (int64_t)t * p.hvs2) * EB
+                 : p.hot_k + ((int64_t)b * p.hks0 + (int64_t)kvh * p.hks1 + (int64_t)t * p.hks2) * EB;
+  };
+
+  // Phase A: scores of the chunk's keys for every row.
+  for (int kb = 0; kb < nk; kb += NSLOT * UT) {
+    float x[UT][VEC];
+#pragma unroll
+    for (int i = 0; i < UT; ++i) {
+      const int kl = kb + i * NSLOT + slot;
+      if (on && kl < nk) {
+        load_chunk<DT>(key_row(k0 + kl, false) + lane * VEC * EB, x[i]);
+      } else {
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) x[i][e] = 0.f;
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < UT; ++i) {
+      const int kl = kb + i * NSLOT + slot;
+      if (kl >= nk) break;
+      const int kk = k0 + kl;
+      for (int j = 0; j < GQ; ++j) {
+        float part = 0.f;
+        if (on) {
+          const float *qr = qf + j * D + lane * VEC;
+#pragma unroll
+          for (int e = 0; e < VEC; ++e) part = fmaf(x[i][e], qr[e], part);
+        }
+        const float dot = group_sum<LG>(part);
+        if (lane == (j % LG)) {
+          float v = dot * p.scale;
+          if (p.mask_kind != KIV_MASK_NONE && kk >= p.cold_len)
+            v += mask_bias(p, b, kvh * G + j / p.qlen, j % p.qlen, kk - p.cold_len);
+          sc[j * CH + kl] = v;
+        }
+      }
+    }
+  }
+  __syncthreads();
+
+  // Phase B: per-row max and exp-sum over the chunk (one wave per row).
+  const int wave = tid >> 6, wl = tid & 63;
+  for (int j = wave; j < GQ; j += kAttnThreads / 64) {
+    float m = -INFINITY;
+    for (int kl = wl; kl < nk; kl += 64) m = fmaxf(m, sc[j * CH + kl]);
+    m = wave_max(m);
+    float l = 0.f;
+    for (int kl = wl; kl < nk; kl += 64) {
+      const float e = (m == -INFINITY) ? 0.f : __expf(sc[j * CH + kl] - m);
+      sc[j * CH + kl] = e;
+      l += e;
+    }
+    l = wave_sum(l);
+    if (wl == 0) {
+      rm[j] = m;
+      rl[j] = l;
+    }
+  }
+  __syncthreads();
+
+  // Phase C: unnormalised weighted sum of V, kRowTile rows at a time.
+  constexpr int NG = kAttnThreads / LG;  // key groups
+  const int kg = slot;
+  for (int rt = 0; rt < GQ; rt += kRowTile) {
+    const int nr = min(kRowTile, GQ - rt);
+    float acc[kRowTile][VEC];
+#pragma unroll
+    for (int jj = 0; jj < kRowTile; ++jj)
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) acc[jj][e] = 0.f;
+    for (int kl = kg; kl < nk; kl += NG) {
+      float v[VEC];
+      if (on) load_chunk<DT>(key_row(k0 + kl, true) + lane * VEC * EB, v);
+      else {
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) v[e] = 0.f;
+      }
+#pragma unroll
+      for (int jj = 0; jj < kRowTile; ++jj) {
+        if (jj < nr) {
+          const float w = sc[(rt + jj) * CH + kl];
+#pragma unroll
+          for (int e = 0; e < VEC; ++e) acc[jj][e] = fmaf(w, v[e], acc[jj][e]);
+        }
+      }
+    }
+    // Reduce the key groups that share a wave, then across the 4 waves.
+#pragma unroll
+    for (int jj = 0; jj < kRowTile; ++jj)
+#pragma unroll
+      for (int e = 0; e < VEC; ++e)
+#pragma unroll
+        for (int m = LG; m < 64; m <<= 1) acc[jj][e] += __shfl_xor(acc[jj][e], m, 64);
+    if (wl < LG && on) {
+#pragma unroll
+      for (int jj = 0; jj < kRowTile; ++jj)
+        if (jj < nr)
+#pragma unroll
+          for (int e = 0; e < VEC; ++e) red[(wave * kRowTile + jj) * D + lane * VEC + e] = acc[jj][e];
+    }
+    __syncthreads();
+    for (int i = tid; i < nr * D; i += kAttnThreads) {
+      const int jj = i / D, d = i % D;
+      const int j = rt + jj;
+      const int h = kvh * G + j / p.qlen, qp = j % p.qlen;
+      const int row = (b * p.hq + h) * p.qlen + qp;
+      float a = 0.f;
+      for (int w = 0; w < kAttnThreads / 64; ++w) a += red[(w * kRowTile + jj) * D + d];
+      p.ws_acc[((int64_t)s * rows_total + row) * D + d] = a;
+    }
+    __syncthreads();
+  }
+  for (int j = tid; j < GQ; j += kAttnThreads) {
+    const int h = kvh * G + j / p.qlen, qp = j % p.qlen;
+    const int row = (b * p.hq + h) * p.qlen + qp;
+    p.ws_m[(int64_t)s * rows_total + row] = rm[j];
+    p.ws_l[(int64_t)s * rows_total + row] = rl[j];
+  }
+
+  // Phase D: the last split of kv row r merges all splits.
+  __syncthreads();
+  if (tid == 0) {
+    __threadfence();
+    is_last = atomic_add_acq_rel(&p.ws_cnt[r], 1) == p.nsplit - 1;
+  }
+  __syncthreads();
+  if (!is_last) return;
+  __threadfence();
+  for (int i = tid; i < GQ * D; i += kAttnThreads) {
+    const int j = i / D, d = i % D;
+    const int h = kvh * G + j / p.qlen, qp = j % p.qlen;
+    const int row = (b * p.hq + h) * p.qlen + qp;
+    float M = -INFINITY;
+    for (int ss = 0; ss < p.nsplit; ++ss) M = fmaxf(M, coherent_load_f32(&p.ws_m[(int64_t)ss * rows_total + row]));
+    float o = 0.f;
+    if (M != -INFINITY) {
+      float lsum = 0.f, acc = 0.f;
+      for (int ss = 0; ss < p.nsplit; ++ss) {
+        const int64_t o2 = (int64_t)ss * rows_total + row;
+        const float ms = coherent_load_f32(&p.ws_m[o2]);
+        const float w = (ms == -INFINITY) ? 0.f : __expf(ms - M);
+        lsum = fmaf(coherent_load_f32(&p.ws_l[o2]), w, lsum);
+        acc = fmaf(coherent_load_f32(&p.ws_acc[o2 * D + d]), w, acc);
+      }
+      o = lsum > 0.f ? acc / lsum : 0.f;
+    }
+    store_elem<DT>(p.out, (((int64_t)b * p.qlen + qp) * p.hq + h) * D + d, o);
+  }
+  if (tid == 0) p.ws_cnt[r] = 0;
+}
+
+static int pick_chunk(int total_keys, int kr) {
+  int ch = 64;
+  if (((total_keys + ch - 1) / ch) * kr < 192) ch = 32;
+  return ch;
+}
+
+// Workspace: a fixed 64 KiB block of per-kv-row counters first (zero
+// between calls: the merging block resets its counter), then the split
+// maxima, sums and accumulators, whose size depends on the key count.
+constexpr size_t kCounterBytes = 65536;
+
+static size_t ws_layout(int batch, int hq, int hkv, int head_dim, int qlen, int total_keys, size_t *off_m,
+                        size_t *off_l, size_t *off_acc) {
+  const int ch = pick_chunk(std::max(total_keys, 1), batch * hkv);
+  const size_t S = (size_t)std::max(1, (total_keys + ch - 1) / ch);
+  const size_t R = (size_t)batch * hq * qlen;
+  const size_t ml = (S * R * 4 + 255) & ~size_t(255);
+  *off_m = kCounterBytes;
+  *off_l = kCounterBytes + ml;
+  *off_acc = kCounterBytes + 2 * ml;
+  return *off_acc + ((S * R * head_dim * 4 + 255) & ~size_t(255));
+}
+
+}  // namespace kiv
+
+using namespace kiv;
+
+extern "C" {
+
+size_t kiv_attention_workspace_size(int32_t batch, int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
+                                    int32_t q_len, int32_t total_keys) {
+  size_t m, l, acc;
+  return ws_layout(batch, num_q_heads, num_kv_heads, head_dim, q_len, total_keys, &m, &l, &acc);
+}
+
+int kiv_decode_attention(const kiv_attention_args_t *a, kiv_stream_t stream) {
+  if (!a) return fail(KIV_ERR_INVALID, "kiv_decode_attention: null argument");
+  const int dt = a->dtype;
+  if (dt != KIV_DTYPE_F32 && dt != KIV_DTYPE_F16 && dt != KIV_DTYPE_BF16)
+    return fail(KIV_ERR_INVALID, "kiv_decode_attention: unknown dtype %d", dt);
+  const int B = a->batch, hq = a->num_q_heads, hkv = a->num_kv_heads, D = a->head_dim, Q = a->q_len;
+  if (B < 1 || hq < 1 || hkv < 1 || Q < 1 || hq % hkv)
+    return fail(KIV_ERR_INVALID, "kiv_decode_attention: bad head geometry");
+  const int vec = vec_elems(dt);
+  if (D < vec || D % vec || D / vec > 64)
+    return fail(KIV_ERR_UNSUPPORTED, "kiv_decode_attention: head_dim %d unsupported for this dtype", D);
+  const int G = hq / hkv, GQ = G * Q;
+  if (GQ > 64 || GQ * D > 8192)
+    return fail(KIV_ERR_UNSUPPORTED, "kiv_decode_attention: (Hq/Hkv)*Q = %d rows per kv head too many", GQ);
+  if (a->cold_len < 0 || a->hot_len < 0 || a->cold_len + a->hot_len < 1)
+    return fail(KIV_ERR_INVALID, "kiv_decode_attention: no keys");
+  if (!a->q || !a->out || !a->workspace || (a->cold_len && (!a->cold_k || !a->cold_v)) ||
+      (a->hot_len && (!a->hot_k || !a->hot_v)))
+    return fail(KIV_ERR_INVALID, "kiv_decode_attention: null pointer");
+  if (a->q_stride[3] != 1) return fail(KIV_ERR_INVALID, "kiv_decode_attention: q head_dim stride must be 1");
+  const uintptr_t ptrs = (uintptr_t)a->cold_k | (uintptr_t)a->cold_v | (uintptr_t)a->hot_k | (uintptr_t)a->hot_v;
+  if (ptrs & 15) return fail(KIV_ERR_INVALID, "kiv_decode_attention: K/V must be 16-byte aligned");
+  for (int i = 0; i < 3; ++i)
+    if ((a->hot_k_stride[i] % vec) || (a->hot_v_stride[i] % vec))
+      return fail(KIV_ERR_INVALID, "kiv_decode_attention: hot strides must be multiples of %d", vec);
+  if (a->mask && (a->mask_kind < KIV_MASK_BOOL || a->mask_kind > KIV_MASK_BF16))
+    return fail(KIV_ERR_INVALID, "kiv_decode_attention: unknown mask kind %d", a->mask_kind);
+  const int L = a->cold_len + a->hot_len;
+  if ((size_t)B * hkv * 4 > kCounterBytes)
+    return fail(KIV_ERR_UNSUPPORTED, "kiv_decode_attention: batch * Hkv too large");
+  size_t off_m, off_l, off_acc;
+  const size_t need = ws_layout(B, hq, hkv, D, Q, L, &off_m, &off_l, &off_acc);
+  if (a->workspace_bytes < need)
+    return fail(KIV_ERR_INVALID, "kiv_decode_attention: workspace %zu bytes, %zu needed", a->workspace_bytes, need);
+  const int ch = pick_chunk(L, B * hkv);
+  const int S = (L + ch - 1) / ch;
+  AttnParams p;
+  p.q = (const char *)a->q;
+  p.qs0 = a->q_stride[0];
+  p.qs1 = a->q_stride[1];
+  p.qs2 = a->q_stride[2];
+  p.cold_k = (const char *)a->cold_k;
+  p.cold_v = (const char *)a->cold_v;
+  p.cold_len = a->cold_len;
+  p.hot_len = a->hot_len;
+  p.hot_k = (const char *)a->hot_k;
+  p.hot_v = (const char *)a->hot_v;
+  p.hks0 = a->hot_k_stride[0];
+  p.hks1 = a->hot_k_stride[1];
+  p.hks2 = a->hot_k_stride[2];
+  p.hvs0 = a->hot_v_stride[0];
+  p.hvs1 = a->hot_v_stride[1];
+  p.hvs2 = a->hot_v_stride[2];
+  p.mask = (const char *)a->mask;
+  p.mask_kind = a->mask ? a->mask_kind : KIV_MASK_NONE;
+  p.ms0 = a->mask_stride[0];
+  p.ms1 = a->mask_stride[1];
+  p.ms2 = a->mask_stride[2];
+  p.ms3 = a->mask_stride[3];
+  p.batch = B;
+  p.hq = hq;
+  p.hkv = hkv;
+  p.qlen = Q;
+  p.head_dim = D;
+  p.scale = a->scaling;
+  p.chunk = ch;
+  p.nsplit = S;
+  char *ws = (char *)a->workspace;
+  p.ws_cnt = (int *)ws;
+  p.ws_m = (float *)(ws + off_m);
+  p.ws_l = (float *)(ws + off_l);
+  p.ws_acc = (float *)(ws + off_acc);
+  p.out = (char *)a->out;
+  const size_t lds = ((size_t)GQ * D + (size_t)GQ * ch + 4 * kRowTile * D + 2 * GQ) * 4;
+  const int lg = lanes_per_row(dt, D);
+  hipStream_t st = (hipStream_t)stream;
+  int rc = with_dt_lg(dt, lg, [&](auto dtc, auto lgc) {
+    auto kern = decode_attn_kernel<decltype(dtc)::value, decltype(lgc)::value>;
+    if (lds > 65536) KIV_HIP(hipFuncSetAttribute((const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
+    hipLaunchKernelGGL(kern, dim3(S, B * hkv), dim3(kAttnThreads), lds, st, p);
+    return (int)KIV_OK;
+  });
+  if (rc) return rc;
+  KIV_HIP(hipGetLastError());
+  return KIV_OK;
+}
+
+}  // extern "C"

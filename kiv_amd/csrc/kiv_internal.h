@@ -1,0 +1,104 @@
+// Host-side definition of a cold store and helpers shared by the .hip files.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <string>
+#include <vector>
+
+#include "../../include/kiv_hip.h"
+
+namespace kiv {
+
+// Thread-local error text + return code.
+int fail(int code, const char *fmt, ...);
+int hip_fail(hipError_t e, const char *what);
+
+#define KIV_HIP(expr)                                   \
+  do {                                                  \
+    hipError_t _e = (expr);                             \
+    if (_e != hipSuccess) return ::kiv::hip_fail(_e, #expr); \
+  } while (0)
+
+// Sets the store's device current for the lifetime of the guard.
+struct DeviceGuard {
+  int prev = -1;
+  bool changed = false;
+  explicit DeviceGuard(int dev) {
+    if (hipGetDevice(&prev) == hipSuccess && prev != dev) changed = (hipSetDevice(dev) == hipSuccess);
+  }
+  ~DeviceGuard() {
+    if (changed) (void)hipSetDevice(prev);
+  }
+};
+
+// A device buffer that only grows; growth waits for `stream` before the old
+// block is released so in-flight kernels never see freed memory.
+struct DevBuf {
+  void *ptr = nullptr;
+  size_t bytes = 0;
+  int ensure(size_t need, hipStream_t stream, bool keep_contents);
+  void release();
+};
+
+inline int elem_bytes(int dtype) { return dtype == KIV_DTYPE_F32 ? 4 : 2; }
+inline int vec_elems(int dtype) { return 16 / elem_bytes(dtype); }
+
+// Lanes that cooperate on one row: next power of two >= D / VEC.
+inline int lanes_per_row(int dtype, int head_dim) {
+  int cpr = head_dim / vec_elems(dtype);
+  int lg = 4;
+  while (lg < cpr) lg <<= 1;
+  return lg;
+}
+
+}  // namespace kiv
+
+struct kiv_store {
+  kiv_store_config_t cfg{};
+  int device = 0;
+  int kr = 0;               // B * Hkv rows per token
+  int64_t row_bytes = 0;    // D * elem
+  int64_t page_bytes = 0;   // kr * page_size * row_bytes (one page of K, all rows)
+
+  int64_t num_pages = 0;    // finished pages
+  int64_t partial_len = 0;  // tokens in the partial page
+
+  // Page summaries in HBM: [cap][kr][D] dtype and fp32.
+  kiv::DevBuf summ, summ32;
+  int64_t summ_cap = 0;
+
+  // Arena of finished pages: equal chunks of 2^chunk_shift pages.
+  int chunk_shift = 0;
+  int64_t pages_per_chunk = 1;
+  std::vector<void *> k_chunks, v_chunks;
+  kiv::DevBuf k_tab, v_tab;  // device arrays of chunk base addresses
+  int64_t tab_cap = 0;
+
+  // Partial page in HBM: [kr][page_size][D].
+  kiv::DevBuf k_part, v_part;
+
+  // Retrieval scratch.
+  kiv::DevBuf coarse_keys;   // [R][ld] u32
+  kiv::DevBuf row_stats;     // [R][2] f32 (max, sum) + [B][2] fine stats
+  kiv::DevBuf bitmap;        // [ceil(N/32)] u32, zero between calls
+  kiv::DevBuf page_list;     // [N] i32 union pages ascending
+  kiv::DevBuf counters;      // i32: [0]=U, [1]=coarse done, [2]=fine done, [3]=P actual
+  kiv::DevBuf fine_keys;     // [B][ld] u32
+  kiv::DevBuf sel_cand;      // [B][P'] i32 candidate index per output slot
+  bool union_valid = false;  // page_list / U hold the last coarse pass
+  int64_t union_rows = 0;    // B*Hq*Q of that pass (bounds reuse)
+  int64_t union_max = 0;     // grid bound of that pass
+
+  // Stage timing (kiv_profile_enable): ring of event pairs per stage.
+  static constexpr int kProfRing = 256;
+  bool prof_on = false;
+  std::vector<hipEvent_t> prof_ev;  // [stage][ring][2]
+  int64_t prof_n[KIV_NUM_STAGES] = {};
+  void prof_begin(int stage, hipStream_t st);
+  void prof_end(int stage, hipStream_t st);
+
+  int64_t reserved_host_bytes() const;
+  int64_t reserved_device_bytes() const;
+};

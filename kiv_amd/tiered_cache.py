@@ -1,0 +1,180 @@
+"""Hot window + cold tier cache for HuggingFace models.
+
+Drop-in for the reference's ``TieredKVCache`` (kiv/tiered_cache.py:17-286):
+still a ``transformers.DynamicCache`` so HF layers and callers that read
+``layers[i].keys`` keep working.  Global layers that own KV keep at most
+``hot_budget`` recent tokens after prefill; older rows go to the layer's
+:class:`ColdKVStore`.  Positions (``get_seq_length``) and mask sizes count
+hot + cold tokens.
+"""
+
+from __future__ import annotations
+
+import logging
+
+import torch
+from transformers import DynamicCache
+
+from .cold_store import ColdKVStore
+from .config import KIVConfig
+from .model_topology import ModelTopology
+
+logger = logging.getLogger(__name__)
+
+
+class TieredKVCache(DynamicCache):
+
+    def __init__(self, config, kiv_config: KIVConfig, topology: ModelTopology,
+                 device: torch.device | None = None) -> None:
+        super().__init__(config=config)
+        self.kiv_config = kiv_config
+        self.topology = topology
+        device = torch.device("cuda") if device is None else torch.device(device)
+        self.cold_stores: dict[int, ColdKVStore] = {
+            i: ColdKVStore(kiv_config, topology, device) for i in topology.independent_kv_layers
+        }
+        self._prefill_complete = False   # eviction starts after prefill
+        self._suppress_cold = False      # wrapper skips retrieval while set
+        self._total_tokens: dict[int, int] = {}
+        self._decode_step = 0            # shared-layer candidate reuse key
+
+    # -------------------------------------------------------------- helpers
+    def _kv_source_layer_idx(self, layer_idx: int) -> int:
+        return self.topology.kv_sharing_map.get(layer_idx, layer_idx)
+
+    def _owned_layers(self):
+        """(index, layer) of independent layers that hold tensors."""
+        for i in self.topology.independent_kv_layers:
+            if i < len(self.layers) and self.layers[i].is_initialized:
+                yield i, self.layers[i]
+
+    def _evict_layer(self, layer_idx: int, num_evict: int) -> None:
+        """Move the oldest ``num_evict`` hot rows of a layer to its cold store
+        (kiv/tiered_cache.py:55-72)."""
+        layer = self.layers[layer_idx]
+        self.cold_stores[layer_idx].evict_from_hot(layer.keys[:, :, :num_evict], layer.values[:, :, :num_evict])
+        layer.keys = layer.keys[:, :, num_evict:].contiguous()
+        layer.values = layer.values[:, :, num_evict:].contiguous()
+        self._total_tokens[layer_idx] = self.cold_stores[layer_idx].cold_length + layer.keys.shape[2]
+
+    def _evict_to_cap(self, cap: int) -> None:
+        """Bounded prefill: trim every owned hot window to ``cap`` tokens."""
+        for i, layer in self._owned_layers():
+            excess = layer.keys.shape[2] - cap
+            if excess > 0:
+                self._evict_layer(i, excess)
+
+    def _evict_excess_all_layers(self) -> None:
+        """Trim every owned hot window to ``hot_budget`` tokens."""
+        budget = self.kiv_config.hot_budget
+        for i, layer in self._owned_layers():
+            excess = layer.keys.shape[2] - budget
+            if excess > 0:
+                self._evict_layer(i, excess)
+                logger.debug("layer %d: evicted %d tokens (cold=%d)", i, excess,
+                             self.cold_stores[i].cold_length)
+
+    def mark_prefill_complete(self) -> None:
+        self._prefill_complete = True
+        self._evict_excess_all_layers()
+
+    # ----------------------------------------------------------------- HF API
+    def update(self, key_states: torch.Tensor, value_states: torch.Tensor, layer_idx: int, *args, **kwargs):
+        """Append, then (after prefill) evict past ``hot_budget`` (kiv/tiered_cache.py:107-142).
+
+        The token appended in this call stays hot; the evicted ones are
+        already cold candidates for the same layer call.
+        """
+        keys, values = super().update(key_states, value_states, layer_idx, *args, **kwargs)
+        owned = self.topology.independent_kv_layers
+        if layer_idx in owned:
+            if self._prefill_complete and layer_idx == owned[0]:
+                self._decode_step += 1
+            self._total_tokens[layer_idx] = self.cold_stores[layer_idx].cold_length + keys.shape[2]
+        if self._prefill_complete and layer_idx in self.cold_stores:
+            layer = self.layers[layer_idx]
+            excess = layer.keys.shape[2] - self.kiv_config.hot_budget
+            if excess > 0:
+                self._evict_layer(layer_idx, excess)
+                keys, values = layer.keys, layer.values
+        return keys, values
+
+    def get_cold_store(self, layer_idx: int) -> ColdKVStore | None:
+        """The store of ``layer_idx`` or of the layer it shares KV with."""
+        if layer_idx in self.cold_stores:
+            return self.cold_stores[layer_idx]
+        src = self.topology.kv_sharing_map.get(layer_idx)
+        return None if src is None else self.cold_stores.get(src)
+
+    def get_mask_sizes(self, query_length: int, layer_idx: int) -> tuple[int, int]:
+        """(hot + query length, cold length) once cold tokens exist
+        (kiv/tiered_cache.py:156-168); parent behaviour otherwise."""
+        store = self.get_cold_store(layer_idx)
+        src = self._kv_source_layer_idx(layer_idx)
+        if store is not None and src < len(self.layers) and store.cold_length > 0:
+            layer = self.layers[src]
+            hot = layer.get_seq_length() if layer.is_initialized else 0
+            return hot + query_length, store.cold_length
+        return super().get_mask_sizes(query_length, layer_idx)
+
+    def get_seq_length(self, layer_idx: int = 0) -> int:
+        """Hot + cold tokens, so position ids keep counting evicted tokens."""
+        if layer_idx in self._total_tokens:
+            return self._total_tokens[layer_idx]
+        src = self._kv_source_layer_idx(layer_idx)
+        if src in self._total_tokens:
+            return self._total_tokens[src]
+        return super().get_seq_length(src)
+
+    def reset(self) -> None:
+        super().reset()
+        for store in self.cold_stores.values():
+            store.reset()
+        self._total_tokens.clear()
+        self._prefill_complete = False
+        self._suppress_cold = False
+        self._decode_step = 0
+
+    def truncate_to(self, new_len: int) -> bool:
+        """Cut every owned layer back to ``new_len`` tokens, within the hot window only.
+
+        Same rules as kiv/tiered_cache.py:194-257: False (cache untouched)
+        when ``new_len`` exceeds the current total or falls inside the cold
+        tier; otherwise hot K/V are sliced, the candidate caches cleared and
+        the decode-step counter restarted.
+        """
+        owned = list(self._owned_layers())
+        for i, layer in owned:
+            cold = self.cold_stores[i].cold_length
+            if new_len > cold + layer.keys.shape[2] or new_len < cold:
+                return False
+        for i, layer in owned:
+            keep = new_len - self.cold_stores[i].cold_length
+            if keep < layer.keys.shape[2]:
+                layer.keys = layer.keys[:, :, :keep].contiguous()
+                layer.values = layer.values[:, :, :keep].contiguous()
+            self._total_tokens[i] = new_len
+        for store in self.cold_stores.values():
+            store._invalidate_candidates()
+        self._decode_step = 0
+        return True
+
+    def memory_report(self) -> dict:
+        """Bytes per tier (keys of kiv/tiered_cache.py:259-286, plus HBM-tier rows)."""
+        hot = sum(l.keys.nelement() * l.keys.element_size() + l.values.nelement() * l.values.element_size()
+                  for _, l in self._owned_layers())
+        tot = {"k_index_cpu": 0, "v_store_cpu": 0, "page_summaries_gpu": 0, "partial_gpu": 0,
+               "k_cold_gpu": 0, "v_cold_gpu": 0}
+        for store in self.cold_stores.values():
+            for key, val in store.memory_bytes().items():
+                tot[key] += val
+        return {
+            "hot_vram_bytes": hot,
+            "k_index_cpu_bytes": tot["k_index_cpu"],
+            "v_store_cpu_bytes": tot["v_store_cpu"],
+            "page_summaries_gpu_bytes": tot["page_summaries_gpu"],
+            "cold_rows_gpu_bytes": tot["k_cold_gpu"] + tot["v_cold_gpu"],
+            "total_vram_bytes": hot + tot["page_summaries_gpu"] + tot["partial_gpu"] + tot["k_cold_gpu"]
+            + tot["v_cold_gpu"],
+            "total_cpu_bytes": tot["k_index_cpu"] + tot["v_store_cpu"],
+        }

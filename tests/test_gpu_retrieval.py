@@ -1,0 +1,292 @@
+"""GPU parity of eviction, coarse/fine retrieval and the merged attention.
+
+Each case builds the same cold tier in the HIP store (through the C-ABI
+wrapper ColdKVStore) and in the CPU oracle, then checks:
+  * page summaries: fp32 mean within 1e-5 relative of the fp64 mean, and the
+    stored dtype summary equal to RNE(fp32 mean);
+  * cold rows bit-exact;
+  * union pages and top-P ids within the rounding bands of tests/_parity.py
+    (bit-exact wherever the boundary is determined);
+  * returned K/V bit-exact copies of the selected cold rows, in descending
+    score order;
+  * merged attention within max-abs 2e-3 of fp64 softmax attention.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from kiv_amd import ColdKVStore, KIVConfig, ModelTopology
+from kiv_amd.attention import decode_attention
+from kiv_amd.synthetic import WORKLOADS, Workload, generate
+from oracle import exact
+from oracle.torch_ref import OracleColdStore
+from tests._parity import check_topk, score_interval
+
+pytestmark = pytest.mark.gpu
+
+DT = {torch.float16: "float16", torch.bfloat16: "bfloat16", torch.float32: "float32"}
+
+
+def f64(t: torch.Tensor) -> np.ndarray:
+    return t.detach().float().cpu().numpy().astype(np.float64)
+
+
+def build(w: Workload, data: dict, device, chunks=(4096,), cold_tier="host", rounding="activation"):
+    cfg = KIVConfig(hot_budget=w.hot, top_p=w.top_p, page_size=w.page_size, top_pages=w.top_pages,
+                    cold_tier=cold_tier, score_rounding=rounding)
+    topo = ModelTopology.manual(global_layer_indices=(0,), num_query_heads=w.num_q_heads,
+                                num_kv_heads=w.num_kv_heads, head_dim=w.head_dim, num_hidden_layers=1)
+    store = ColdKVStore(cfg, topo, device)
+    oracle = OracleColdStore(w.page_size, w.groups)
+    ck, cv = data["cold_k"], data["cold_v"]
+    dk, dv = ck.to(device), cv.to(device)
+    t, i = 0, 0
+    while t < w.cold:
+        n = min(chunks[i % len(chunks)], w.cold - t)
+        store.evict_from_hot(dk[:, :, t:t + n], dv[:, :, t:t + n])
+        oracle.evict(ck[:, :, t:t + n], cv[:, :, t:t + n])
+        t += n
+        i += 1
+    return store, oracle, cfg
+
+
+def check_summaries(store: ColdKVStore, data: dict, w: Workload):
+    s, s32 = store.read_summaries()
+    N = store.num_pages
+    assert s.shape[0] == N
+    if N == 0:
+        return
+    m64 = exact.page_means(f64(data["cold_k"]), w.page_size)       # [B, H, N, D]
+    got32 = s32.cpu().numpy().astype(np.float64).transpose(1, 2, 0, 3)  # [B, H, N, D]
+    err = np.abs(got32 - m64)
+    assert np.all(err <= 1e-5 * np.abs(m64) + 1e-30), f"max rel err {np.max(err / (np.abs(m64) + 1e-30))}"
+    # Stored dtype summary is RNE(fp32 mean), bit for bit.
+    assert torch.equal(s.cpu(), s32.cpu().to(s.dtype))
+
+
+def check_rows(store: ColdKVStore, data: dict):
+    k, v = store.read_tokens()
+    assert torch.equal(k.cpu(), data["cold_k"]) and torch.equal(v.cpu(), data["cold_v"])
+
+
+def check_retrieval(store, oracle, cfg, w, data, q, rounding="activation"):
+    """Run one retrieval and check it; returns (k_out, v_out, sel ids [B, P'])."""
+    dev = store.device
+    dtype = DT[w.dtype]
+    k_out, v_out = store.retrieve_top_kv(q.to(dev), w.scaling, cfg)
+    snap = store.telemetry_snapshot()["recent"]
+    fine = snap[-1]
+    assert fine["kind"] == "fine"
+    B = q.shape[0]
+    width = k_out.shape[2]
+    sel = np.array(fine["selected_token_indices"], dtype=np.int64).reshape(B, width)
+    cold_k, cold_v = data["cold_k"], data["cold_v"]
+    q64 = q.cpu()
+    N, ps, p = store.num_pages, w.page_size, store.cold_length - store.num_pages * w.page_size
+    # Union of per-row top pages.
+    if N > 0:
+        coarse = snap[-2]
+        assert coarse["kind"] == "coarse" and not coarse["skipped"]
+        union = coarse["pages_selected"]
+        assert union == sorted(set(union))
+        summ, _ = store.read_summaries()
+        summ = summ.cpu().permute(1, 2, 0, 3)  # [B, H, N, D] dtype as the kernel reads it
+        lo, hi = score_interval(q64.float().numpy(), summ.float().numpy(), w.scaling, dtype, rounding)
+        det = check_topk(set(union), lo.reshape(-1, N), hi.reshape(-1, N), min(cfg.top_pages, N))
+        assert det > 0.5, f"only {det:.2f} of coarse rows determined"
+    else:
+        union = []
+    cand = exact.candidate_ids(np.array(union, dtype=np.int64), ps, N * ps, p)
+    P = min(cfg.top_p, store.cold_length, cand.size)
+    assert width == P
+    ck = cold_k[:, :, torch.from_numpy(cand)]
+    lo, hi = score_interval(q64.float().numpy(), ck.float().numpy(), w.scaling, dtype, rounding)
+    lo_agg, hi_agg = lo.max(axis=(1, 2)), hi.max(axis=(1, 2))  # [B, C]
+    pos = {int(g): i for i, g in enumerate(cand)}
+    for b in range(B):
+        local = np.array([pos[int(g)] for g in sel[b]])
+        assert len(set(local.tolist())) == width
+        check_topk(set(local.tolist()), lo_agg[b:b + 1], hi_agg[b:b + 1], P)
+        # Descending order: each entry can still be >= the next one.
+        assert np.all(hi_agg[b, local[:-1]] >= lo_agg[b, local[1:]])
+        # Returned rows are the selected cold rows, bit for bit.
+        idx = torch.from_numpy(sel[b])
+        assert torch.equal(k_out[b].cpu(), cold_k[b][:, idx]) and torch.equal(v_out[b].cpu(), cold_v[b][:, idx])
+    # The dtype-faithful CPU oracle's selection lies in the same bands.
+    ok, ov, trace = oracle.retrieve(q64, w.scaling, cfg.top_p, cfg.top_pages)
+    if N > 0 and rounding == "activation":
+        assert set(trace.pages.tolist()) <= set(range(N))
+    return k_out, v_out, sel
+
+
+def attention_check(q, cold_k, cold_v, hot_k, hot_v, scaling, mask=None, tol=2e-3):
+    out = decode_attention(q, cold_k, cold_v, hot_k, hot_v, mask, scaling)
+    keys = torch.cat([cold_k, hot_k], dim=2) if cold_k is not None else hot_k
+    vals = torch.cat([cold_v, hot_v], dim=2) if cold_v is not None else hot_v
+    m = None
+    if mask is not None:
+        mm = mask.float() if mask.dtype != torch.bool else torch.where(mask, 0.0, float("-inf"))
+        P = 0 if cold_k is None else cold_k.shape[2]
+        m = np.concatenate([np.zeros(mm.shape[:-1] + (P,)), f64(mm)], axis=-1)
+    ref = exact.attention64(f64(q), f64(keys), f64(vals), scaling, m)
+    err = np.abs(f64(out) - ref).max()
+    assert err <= tol, f"attention max-abs error {err}"
+    return err
+
+
+SMALL = [
+    # name, workload overrides, eviction chunk pattern
+    ("tiny_gqa_bf16", dict(num_q_heads=8, num_kv_heads=2, head_dim=64, dtype=torch.bfloat16, cold=3000,
+                           hot=300, top_pages=4, top_p=64, segment=256), (1, 7, 128, 300, 1000)),
+    ("tiny_mha_f16", dict(num_q_heads=4, num_kv_heads=4, head_dim=96, dtype=torch.float16, cold=2100,
+                          hot=100, top_pages=3, top_p=100, segment=128, n_targets=4), (2048, 52)),
+    ("tiny_mqa_bf16_d256", dict(num_q_heads=8, num_kv_heads=1, head_dim=256, dtype=torch.bfloat16, cold=5000,
+                                hot=64, top_pages=8, top_p=200, segment=512), (4096, 904)),
+    ("tiny_f32", dict(num_q_heads=4, num_kv_heads=2, head_dim=32, dtype=torch.float32, cold=1500, hot=50,
+                      top_pages=5, top_p=40, segment=100), (333,)),
+    ("small_pages", dict(num_q_heads=4, num_kv_heads=1, head_dim=64, dtype=torch.bfloat16, cold=777, hot=30,
+                         top_pages=6, top_p=50, segment=64, page_size=16), (5, 11)),
+]
+
+
+@pytest.mark.parametrize("name,over,chunks", SMALL, ids=[c[0] for c in SMALL])
+def test_small_parity(cuda, name, over, chunks):
+    w = Workload(name=name, **over)
+    data = generate(w, seed=1)
+    store, oracle, cfg = build(w, data, cuda, chunks)
+    assert store.cold_length == w.cold and store.num_pages == w.cold // w.page_size
+    check_summaries(store, data, w)
+    check_rows(store, data)
+    k_out, v_out, _ = check_retrieval(store, oracle, cfg, w, data, data["q"])
+    attention_check(data["q"].to(cuda), k_out, v_out, data["hot_k"].to(cuda), data["hot_v"].to(cuda), w.scaling)
+
+
+@pytest.mark.parametrize("key,cold", [("tinyllama_32k", 32768), ("qwen7b_256k", 24576 + 77),
+                                      ("phi35_128k", 8192 + 5), ("mqa_1m", 65536)])
+def test_workload_parity(cuda, key, cold):
+    w = WORKLOADS[key].with_cold(cold)
+    data = generate(w, seed=0)
+    store, oracle, cfg = build(w, data, cuda, chunks=(4096, 1000, 1))
+    check_summaries(store, data, w)
+    k_out, v_out, sel = check_retrieval(store, oracle, cfg, w, data, data["q"])
+    # The target segment's tokens dominate the selection.
+    seg = data["targets"][0].tolist()
+    in_target = np.isin(sel[0] // w.segment, seg).mean()
+    assert in_target > 0.9
+    attention_check(data["q"].to(cuda), k_out, v_out, data["hot_k"].to(cuda), data["hot_v"].to(cuda), w.scaling)
+
+
+def test_partial_only_and_small_cold(cuda):
+    """N == 0 (partial page only) and cold < top_p: everything is returned."""
+    w = Workload("partial", 8, 2, 64, torch.bfloat16, hot=16, cold=100, top_pages=4, top_p=256, segment=32)
+    data = generate(w, seed=3)
+    store, oracle, cfg = build(w, data, cuda, chunks=(1, 3, 40))
+    assert store.num_pages == 0 and store.cold_length == 100
+    k_out, v_out, sel = check_retrieval(store, oracle, cfg, w, data, data["q"])
+    assert sorted(sel[0].tolist()) == list(range(100))
+    snap = store.telemetry_snapshot()
+    assert snap["recent"][-2]["skipped"] is True
+    assert snap["aggregates"]["coarse_skipped_calls"] == 1
+
+
+def test_fewer_pages_than_top_pages(cuda):
+    w = Workload("fewpages", 4, 2, 64, torch.float16, hot=16, cold=3 * 128 + 9, top_pages=32, top_p=500,
+                 segment=100)
+    data = generate(w, seed=4)
+    store, oracle, cfg = build(w, data, cuda, chunks=(200,))
+    k_out, v_out, sel = check_retrieval(store, oracle, cfg, w, data, data["q"])
+    assert store.telemetry_snapshot()["recent"][-2]["pages_selected"] == [0, 1, 2]
+    assert sorted(sel[0].tolist()) == list(range(w.cold))
+
+
+def test_batch_and_multi_query(cuda):
+    """B = 2 and Q = 3: union over every (b, head, position); top-P per batch row."""
+    w = Workload("bq", 8, 2, 64, torch.bfloat16, hot=32, cold=4096 + 33, top_pages=3, top_p=96, segment=256)
+    data = generate(w, seed=5, batch=2)
+    g = torch.Generator().manual_seed(9)
+    q = data["q"].float().repeat(1, 1, 3, 1) + 0.05 * torch.randn(2, 8, 3, 64, generator=g)
+    q = q.to(w.dtype)
+    store, oracle, cfg = build(w, data, cuda, chunks=(1000, 7))
+    check_rows(store, data)
+    check_retrieval(store, oracle, cfg, w, data, q)
+
+
+def test_fp32_scores_and_hbm_tier(cuda):
+    w = Workload("f32rank", 8, 2, 128, torch.bfloat16, hot=64, cold=6000, top_pages=6, top_p=128, segment=512)
+    data = generate(w, seed=6)
+    store, oracle, cfg = build(w, data, cuda, chunks=(999,), cold_tier="hbm", rounding="fp32")
+    check_rows(store, data)
+    check_retrieval(store, oracle, cfg, w, data, data["q"], rounding="fp32")
+    mem = store.memory_bytes()
+    assert mem["k_index_cpu"] == 0 and mem["k_cold_gpu"] == store.num_pages * 128 * 2 * 128 * 2
+
+
+def test_width_depends_on_union(cuda):
+    """top_p > top_pages * page_size: the width follows the union size."""
+    w = Workload("wide", 4, 1, 64, torch.bfloat16, hot=8, cold=64 * 10, top_pages=2, top_p=300, segment=64,
+                 page_size=64)
+    data = generate(w, seed=7)
+    store, oracle, cfg = build(w, data, cuda, chunks=(640,))
+    k_out, _, sel = check_retrieval(store, oracle, cfg, w, data, data["q"])
+    union = store.telemetry_snapshot()["recent"][-2]["pages_selected"]
+    assert k_out.shape[2] == min(300, len(union) * 64)
+
+
+def test_reuse_candidates_by_step(cuda):
+    """Same decode step on a shared layer reuses the union (coarse skipped)."""
+    w = Workload("reuse", 8, 2, 64, torch.bfloat16, hot=8, cold=2048, top_pages=4, top_p=64, segment=256)
+    data = generate(w, seed=8)
+    store, _, cfg = build(w, data, cuda)
+    q = data["q"].to(cuda)
+    k1, v1 = store.retrieve_top_kv(q, w.scaling, cfg, step=5)
+    k2, v2 = store.retrieve_top_kv(q, w.scaling, cfg, step=5)
+    assert torch.equal(k1, k2) and torch.equal(v1, v2)
+    snap = store.telemetry_snapshot()
+    assert snap["aggregates"]["coarse_real_calls"] == 1 and snap["aggregates"]["coarse_skipped_calls"] == 1
+    store.evict_from_hot(data["hot_k"][:, :, :1].to(cuda), data["hot_v"][:, :, :1].to(cuda))
+    assert store._cached_candidate_k is None
+
+
+def test_tie_break_lowest_index(cuda):
+    """Identical K rows tie exactly: the lower token id wins, deterministically."""
+    dev = cuda
+    cfg = KIVConfig(top_p=5, top_pages=2, page_size=8)
+    topo = ModelTopology.manual(global_layer_indices=(0,), num_query_heads=2, num_kv_heads=1, head_dim=16,
+                                num_hidden_layers=1)
+    store = ColdKVStore(cfg, topo, dev)
+    k = torch.ones(1, 1, 64, 16, dtype=torch.bfloat16)
+    v = torch.arange(64, dtype=torch.bfloat16)[None, None, :, None].repeat(1, 1, 1, 16)
+    store.evict_from_hot(k.to(dev), v.to(dev))
+    q = torch.ones(1, 2, 1, 16, dtype=torch.bfloat16)
+    ko, vo = store.retrieve_top_kv(q.to(dev), 0.25, cfg)
+    snap = store.telemetry_snapshot()["recent"]
+    assert snap[-2]["pages_selected"] == [0, 1]
+    assert snap[-1]["selected_token_indices"] == [0, 1, 2, 3, 4]
+    assert torch.equal(vo[0, 0, :, 0].cpu(), torch.arange(5, dtype=torch.bfloat16))
+
+
+@pytest.mark.parametrize("mask_kind", ["none", "bool", "float"])
+def test_attention_masks_and_edges(cuda, mask_kind):
+    g = torch.Generator().manual_seed(11)
+    B, hq, hkv, D, P, T = 2, 12, 4, 128, 37, 301
+    q = torch.randn(B, hq, 1, D, generator=g).to(torch.bfloat16)
+    ck = torch.randn(B, hkv, P, D, generator=g).to(torch.bfloat16)
+    cv = torch.randn(B, hkv, P, D, generator=g).to(torch.bfloat16)
+    hk = torch.randn(B, hkv, T, D, generator=g).to(torch.bfloat16)
+    hv = torch.randn(B, hkv, T, D, generator=g).to(torch.bfloat16)
+    mask = None
+    if mask_kind == "bool":
+        mask = torch.rand(B, 1, 1, T, generator=g) > 0.3
+    elif mask_kind == "float":
+        mask = torch.where(torch.rand(B, 1, 1, T, generator=g) > 0.3, 0.0, -1e9).to(torch.bfloat16)
+    d = lambda t: None if t is None else t.to(cuda)
+    attention_check(d(q), d(ck), d(cv), d(hk), d(hv), D ** -0.5, d(mask))
+    attention_check(d(q), None, None, d(hk), d(hv), D ** -0.5, d(mask))       # no cold keys
+    attention_check(d(q), d(ck), d(cv), d(hk)[:, :, :0], d(hv)[:, :, :0], D ** -0.5)  # no hot keys
+    # Non-contiguous hot window (a slice of a longer cache).
+    big_k = torch.randn(B, hkv, T + 50, D, generator=g).to(torch.bfloat16)
+    big_v = torch.randn(B, hkv, T + 50, D, generator=g).to(torch.bfloat16)
+    attention_check(d(q), d(ck), d(cv), d(big_k)[:, :, 50:], d(big_v)[:, :, 50:], D ** -0.5)
