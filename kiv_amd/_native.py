@@ -9,12 +9,13 @@ fallback: every caller of :func:`lib` needs the HIP kernels.
 from __future__ import annotations
 
 import ctypes as C
+import os
 import threading
 from pathlib import Path
 
 import torch  # noqa: F401  (load torch's HIP runtime before the library)
 
-LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libkiv_hip.so"
+LIB_PATH = Path(os.environ.get("KIV_LIB_PATH") or Path(__file__).resolve().parent / "_lib" / "libkiv_hip.so")
 
 KIV_OK = 0
 DTYPE_F32, DTYPE_F16, DTYPE_BF16 = 0, 1, 2

@@ -62,18 +62,20 @@ __global__ void __launch_bounds__(kAttnThreads) decode_attn_kernel(AttnParams p)
   const int G = p.hq / p.hkv, GQ = G * p.qlen, D = p.head_dim, CH = p.chunk;
   const int cpr = D / VEC;
   const int rows_total = p.batch * p.hq * p.qlen;
-  extern __shared__ float smem[];
-  float *qf = smem;                 // [GQ][D]
-  float *sc = qf + GQ * D;          // [GQ][CH]
-  float *red = sc + GQ * CH;        // [4 waves][kRowTile][D]
-  float *rm = red + 4 * kRowTile * D;  // [GQ] split max
-  float *rl = rm + GQ;                 // [GQ] split sum
+  extern __shared__ uint4 smem4[];
+  char *qraw = reinterpret_cast<char *>(smem4);                            // [GQ][D] dtype
+  float *sc = reinterpret_cast<float *>(qraw + (size_t)GQ * D * EB);       // [GQ][CH]
+  float *red = sc + GQ * CH;                                               // [4 waves][kRowTile][D]
+  float *rm = red + 4 * kRowTile * D;                                      // [GQ] split max
+  float *rl = rm + GQ;                                                     // [GQ] split sum
+  float *wts = rl + GQ;                                                    // [GQ][nsplit] merge weights
   __shared__ int is_last;
   const int tid = threadIdx.x;
-  for (int i = tid; i < GQ * D; i += kAttnThreads) {
-    const int j = i / D, d = i % D;
+  for (int i = tid; i < GQ * cpr; i += kAttnThreads) {
+    const int j = i / cpr, c = i % cpr;
     const int h = kvh * G + j / p.qlen, qp = j % p.qlen;
-    qf[i] = load_elem<DT>(p.q, (int64_t)b * p.qs0 + (int64_t)h * p.qs1 + (int64_t)qp * p.qs2 + d);
+    *reinterpret_cast<uint4 *>(qraw + ((size_t)j * D + c * VEC) * EB) =
+        load16(p.q + ((int64_t)b * p.qs0 + (int64_t)h * p.qs1 + (int64_t)qp * p.qs2 + c * VEC) * EB);
   }
   const int L = p.cold_len + p.hot_len;
   const int k0 = s * CH;
@@ -92,16 +94,11 @@ __global__ void __launch_bounds__(kAttnThreads) decode_attn_kernel(AttnParams p)
 
   // Phase A: scores of the chunk's keys for every row.
   for (int kb = 0; kb < nk; kb += NSLOT * UT) {
-    float x[UT][VEC];
+    uint4 x[UT];
 #pragma unroll
     for (int i = 0; i < UT; ++i) {
       const int kl = kb + i * NSLOT + slot;
-      if (on && kl < nk) {
-        load_chunk<DT>(key_row(k0 + kl, false) + lane * VEC * EB, x[i]);
-      } else {
-#pragma unroll
-        for (int e = 0; e < VEC; ++e) x[i][e] = 0.f;
-      }
+      x[i] = (on && kl < nk) ? load16(key_row(k0 + kl, false) + lane * VEC * EB) : make_uint4(0, 0, 0, 0);
     }
 #pragma unroll
     for (int i = 0; i < UT; ++i) {
@@ -110,11 +107,7 @@ __global__ void __launch_bounds__(kAttnThreads) decode_attn_kernel(AttnParams p)
       const int kk = k0 + kl;
       for (int j = 0; j < GQ; ++j) {
         float part = 0.f;
-        if (on) {
-          const float *qr = qf + j * D + lane * VEC;
-#pragma unroll
-          for (int e = 0; e < VEC; ++e) part = fmaf(x[i][e], qr[e], part);
-        }
+        if (on) part = chunk_dot<DT>(x[i], load16(qraw + ((size_t)j * D + lane * VEC) * EB), 0.f);
         const float dot = group_sum<LG>(part);
         if (lane == (j % LG)) {
           float v = dot * p.scale;
@@ -147,9 +140,9 @@ __global__ void __launch_bounds__(kAttnThreads) decode_attn_kernel(AttnParams p)
   }
   __syncthreads();
 
-  // Phase C: unnormalised weighted sum of V, kRowTile rows at a time.
-  constexpr int NG = kAttnThreads / LG;  // key groups
-  const int kg = slot;
+  // Phase C: unnormalised weighted sum of V, kRowTile rows at a time.  Lane
+  // group `slot` takes keys slot, slot + NSLOT, ...; the groups of a wave are
+  // summed with DPP / permlane, the 4 waves through LDS.
   for (int rt = 0; rt < GQ; rt += kRowTile) {
     const int nr = min(kRowTile, GQ - rt);
     float acc[kRowTile][VEC];
@@ -157,7 +150,7 @@ __global__ void __launch_bounds__(kAttnThreads) decode_attn_kernel(AttnParams p)
     for (int jj = 0; jj < kRowTile; ++jj)
 #pragma unroll
       for (int e = 0; e < VEC; ++e) acc[jj][e] = 0.f;
-    for (int kl = kg; kl < nk; kl += NG) {
+    for (int kl = slot; kl < nk; kl += NSLOT) {
       float v[VEC];
       if (on) load_chunk<DT>(key_row(k0 + kl, true) + lane * VEC * EB, v);
       else {
@@ -173,13 +166,10 @@ __global__ void __launch_bounds__(kAttnThreads) decode_attn_kernel(AttnParams p)
         }
       }
     }
-    // Reduce the key groups that share a wave, then across the 4 waves.
 #pragma unroll
     for (int jj = 0; jj < kRowTile; ++jj)
 #pragma unroll
-      for (int e = 0; e < VEC; ++e)
-#pragma unroll
-        for (int m = LG; m < 64; m <<= 1) acc[jj][e] += __shfl_xor(acc[jj][e], m, 64);
+      for (int e = 0; e < VEC; ++e) acc[jj][e] = across_groups_sum<LG>(acc[jj][e]);
     if (wl < LG && on) {
 #pragma unroll
       for (int jj = 0; jj < kRowTile; ++jj)
@@ -206,7 +196,9 @@ __global__ void __launch_bounds__(kAttnThreads) decode_attn_kernel(AttnParams p)
     p.ws_l[(int64_t)s * rows_total + row] = rl[j];
   }
 
-  // Phase D: the last split of kv row r merges all splits.
+  // Phase D: the last split of kv row r merges all splits.  Every wave
+  // completes its own partial writes before the block signals.
+  __threadfence();
   __syncthreads();
   if (tid == 0) {
     __threadfence();
@@ -215,25 +207,61 @@ __global__ void __launch_bounds__(kAttnThreads) decode_attn_kernel(AttnParams p)
   __syncthreads();
   if (!is_last) return;
   __threadfence();
-  for (int i = tid; i < GQ * D; i += kAttnThreads) {
-    const int j = i / D, d = i % D;
+  // Per row: weights exp(m_s - M) / sum_s l_s exp(m_s - M), one wave per row.
+  for (int j = wave; j < GQ; j += kAttnThreads / 64) {
     const int h = kvh * G + j / p.qlen, qp = j % p.qlen;
     const int row = (b * p.hq + h) * p.qlen + qp;
     float M = -INFINITY;
-    for (int ss = 0; ss < p.nsplit; ++ss) M = fmaxf(M, coherent_load_f32(&p.ws_m[(int64_t)ss * rows_total + row]));
-    float o = 0.f;
-    if (M != -INFINITY) {
-      float lsum = 0.f, acc = 0.f;
-      for (int ss = 0; ss < p.nsplit; ++ss) {
-        const int64_t o2 = (int64_t)ss * rows_total + row;
-        const float ms = coherent_load_f32(&p.ws_m[o2]);
-        const float w = (ms == -INFINITY) ? 0.f : __expf(ms - M);
-        lsum = fmaf(coherent_load_f32(&p.ws_l[o2]), w, lsum);
-        acc = fmaf(coherent_load_f32(&p.ws_acc[o2 * D + d]), w, acc);
-      }
-      o = lsum > 0.f ? acc / lsum : 0.f;
+    for (int ss = wl; ss < p.nsplit; ss += 64) M = fmaxf(M, p.ws_m[(int64_t)ss * rows_total + row]);
+    M = wave_max(M);
+    float lsum = 0.f;
+    for (int ss = wl; ss < p.nsplit; ss += 64) {
+      const float ms = p.ws_m[(int64_t)ss * rows_total + row];
+      const float w = (ms == -INFINITY) ? 0.f : __expf(ms - M);
+      wts[j * p.nsplit + ss] = w;
+      lsum = fmaf(p.ws_l[(int64_t)ss * rows_total + row], w, lsum);
     }
-    store_elem<DT>(p.out, (((int64_t)b * p.qlen + qp) * p.hq + h) * D + d, o);
+    lsum = wave_sum(lsum);
+    const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
+    for (int ss = wl; ss < p.nsplit; ss += 64) wts[j * p.nsplit + ss] *= inv;
+  }
+  __syncthreads();
+  // Output: 4 consecutive d per thread, the splits' loads issued 8 at a time.
+  const int d4n = D / 4;
+  for (int i = tid; i < GQ * d4n; i += kAttnThreads) {
+    const int j = i / d4n, d = (i % d4n) * 4;
+    const int h = kvh * G + j / p.qlen, qp = j % p.qlen;
+    const int row = (b * p.hq + h) * p.qlen + qp;
+    const float *wj = wts + j * p.nsplit;
+    float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
+    int ss = 0;
+    for (; ss + 8 <= p.nsplit; ss += 8) {
+      float4 a[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u)
+        a[u] = *reinterpret_cast<const float4 *>(&p.ws_acc[((int64_t)(ss + u) * rows_total + row) * D + d]);
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const float w = wj[ss + u];
+        o.x = fmaf(a[u].x, w, o.x);
+        o.y = fmaf(a[u].y, w, o.y);
+        o.z = fmaf(a[u].z, w, o.z);
+        o.w = fmaf(a[u].w, w, o.w);
+      }
+    }
+    for (; ss < p.nsplit; ++ss) {
+      const float4 a = *reinterpret_cast<const float4 *>(&p.ws_acc[((int64_t)ss * rows_total + row) * D + d]);
+      const float w = wj[ss];
+      o.x = fmaf(a.x, w, o.x);
+      o.y = fmaf(a.y, w, o.y);
+      o.z = fmaf(a.z, w, o.z);
+      o.w = fmaf(a.w, w, o.w);
+    }
+    const int64_t ob = (((int64_t)b * p.qlen + qp) * p.hq + h) * D + d;
+    store_elem<DT>(p.out, ob, o.x);
+    store_elem<DT>(p.out, ob + 1, o.y);
+    store_elem<DT>(p.out, ob + 2, o.z);
+    store_elem<DT>(p.out, ob + 3, o.w);
   }
   if (tid == 0) p.ws_cnt[r] = 0;
 }
@@ -293,6 +321,8 @@ int kiv_decode_attention(const kiv_attention_args_t *a, kiv_stream_t stream) {
       (a->hot_len && (!a->hot_k || !a->hot_v)))
     return fail(KIV_ERR_INVALID, "kiv_decode_attention: null pointer");
   if (a->q_stride[3] != 1) return fail(KIV_ERR_INVALID, "kiv_decode_attention: q head_dim stride must be 1");
+  if (((uintptr_t)a->q & 15) || (a->q_stride[0] % vec) || (a->q_stride[1] % vec) || (a->q_stride[2] % vec))
+    return fail(KIV_ERR_INVALID, "kiv_decode_attention: q must be 16-byte aligned, strides multiple of %d", vec);
   const uintptr_t ptrs = (uintptr_t)a->cold_k | (uintptr_t)a->cold_v | (uintptr_t)a->hot_k | (uintptr_t)a->hot_v;
   if (ptrs & 15) return fail(KIV_ERR_INVALID, "kiv_decode_attention: K/V must be 16-byte aligned");
   for (int i = 0; i < 3; ++i)
@@ -346,7 +376,10 @@ int kiv_decode_attention(const kiv_attention_args_t *a, kiv_stream_t stream) {
   p.ws_l = (float *)(ws + off_l);
   p.ws_acc = (float *)(ws + off_acc);
   p.out = (char *)a->out;
-  const size_t lds = ((size_t)GQ * D + (size_t)GQ * ch + 4 * kRowTile * D + 2 * GQ) * 4;
+  const size_t lds = (size_t)GQ * D * elem_bytes(dt) + ((size_t)GQ * ch + 4 * kRowTile * D + 2 * GQ +
+                                                         (size_t)GQ * S) * 4;
+  if (lds > 160 * 1024)
+    return fail(KIV_ERR_UNSUPPORTED, "kiv_decode_attention: %d keys need %zu bytes of LDS", L, lds);
   const int lg = lanes_per_row(dt, D);
   hipStream_t st = (hipStream_t)stream;
   int rc = with_dt_lg(dt, lg, [&](auto dtc, auto lgc) {

@@ -51,6 +51,14 @@ template <int DT> __device__ __forceinline__ float score_of(float dot, float sca
   return dot * scale;
 }
 
+// Returns x unchanged but hides its origin from the optimiser, so that a
+// double -> float -> half sequence is not folded into one double -> half
+// rounding (which differs from rounding twice on rare values).
+__device__ __forceinline__ float opaque_f32(float x) {
+  asm volatile("" : "+v"(x));
+  return x;
+}
+
 // Order-preserving map float -> uint32 (larger float => larger key);
 // -0.0 is folded onto +0.0 first so equal values share one key.
 __device__ __forceinline__ uint32_t order_key(float f) {
@@ -116,23 +124,110 @@ template <int DT> __device__ __forceinline__ void store_elem(void *p, int64_t i,
   else reinterpret_cast<uint16_t *>(p)[i] = (uint16_t)f32_to_bf16_bits(x);
 }
 
-// Sum over an aligned group of LG lanes (butterfly; every lane gets the sum).
+// ---- cross-lane reductions (VALU only: DPP and gfx950 permlane swaps)
+// DPP controls: quad_perm [1,0,3,2] = 0xB1, [2,3,0,1] = 0x4E, row_ror:n =
+// 0x120 + n, row_half_mirror = 0x141, row_mirror = 0x140.
+template <int CTRL> __device__ __forceinline__ float dpp_f32(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, true));
+}
+template <int CTRL> __device__ __forceinline__ int dpp_i32(int v) {
+  return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, true);
+}
+// Sum of lane i and lane i ^ 16 (rows of 16 lanes, swapped in pairs).
+__device__ __forceinline__ float row_pair_sum(float v) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+// Sum of lane i and lane i ^ 32.
+__device__ __forceinline__ float half_wave_sum(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float row_pair_max(float v) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float half_wave_max(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+
+// Sum over an aligned group of LG lanes; every lane of the group gets it.
 template <int LG> __device__ __forceinline__ float group_sum(float v) {
-#pragma unroll
-  for (int m = LG / 2; m >= 1; m >>= 1) v += __shfl_xor(v, m, LG);
+  if constexpr (LG >= 2) v += dpp_f32<0xB1>(v);
+  if constexpr (LG >= 4) v += dpp_f32<0x4E>(v);
+  if constexpr (LG >= 8) v += dpp_f32<0x141>(v);
+  if constexpr (LG >= 16) v += dpp_f32<0x140>(v);
+  if constexpr (LG >= 32) v = row_pair_sum(v);
+  if constexpr (LG >= 64) v = half_wave_sum(v);
+  return v;
+}
+
+// Sum over the 64 / LG groups of a wave, lane by lane within the group
+// (lane i adds lanes i + LG, i + 2 LG, ...); every lane gets its column sum.
+template <int LG> __device__ __forceinline__ float across_groups_sum(float v) {
+  if constexpr (LG <= 1) v += dpp_f32<0x121>(v);
+  if constexpr (LG <= 2) v += dpp_f32<0x122>(v);
+  if constexpr (LG <= 4) v += dpp_f32<0x124>(v);
+  if constexpr (LG <= 8) v += dpp_f32<0x128>(v);
+  if constexpr (LG <= 16) v = row_pair_sum(v);
+  if constexpr (LG <= 32) v = half_wave_sum(v);
   return v;
 }
 
 __device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) v = fmaxf(v, __shfl_xor(v, m, 64));
-  return v;
+  v = fmaxf(v, dpp_f32<0xB1>(v));
+  v = fmaxf(v, dpp_f32<0x4E>(v));
+  v = fmaxf(v, dpp_f32<0x141>(v));
+  v = fmaxf(v, dpp_f32<0x140>(v));
+  v = row_pair_max(v);
+  return half_wave_max(v);
 }
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, 64);
-  return v;
+__device__ __forceinline__ float wave_sum(float v) { return group_sum<64>(v); }
+
+__device__ __forceinline__ int wave_sum_i32(int v) {
+  v += dpp_i32<0xB1>(v);
+  v += dpp_i32<0x4E>(v);
+  v += dpp_i32<0x141>(v);
+  v += dpp_i32<0x140>(v);
+  const auto r = __builtin_amdgcn_permlane16_swap((uint32_t)v, (uint32_t)v, false, false);
+  v = (int)(r[0] + r[1]);
+  const auto r2 = __builtin_amdgcn_permlane32_swap((uint32_t)v, (uint32_t)v, false, false);
+  return (int)(r2[0] + r2[1]);
 }
+
+// ---- packed dot products of one 16-byte chunk (fp32 accumulation)
+// The last pair is always accumulated with plain FMAs: every result of this
+// helper feeds a DPP reduction, and a v_dot2c result read directly by a DPP
+// operand needs more wait states than the compiler inserts after an EXEC
+// restore (measured on gfx950: wrong sums for 8-lane groups).  A plain FMA
+// as the final writer keeps the DPP read on the ordinary VALU hazard path.
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+
+template <int DT> __device__ __forceinline__ float chunk_dot(const uint4 &x, const uint4 &q, float acc) {
+  if constexpr (DT == DT_BF16) {
+    acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, x.x), __builtin_bit_cast(bf16x2_t, q.x), acc, false);
+    acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, x.y), __builtin_bit_cast(bf16x2_t, q.y), acc, false);
+    acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, x.z), __builtin_bit_cast(bf16x2_t, q.z), acc, false);
+    acc = fmaf(__uint_as_float(x.w << 16), __uint_as_float(q.w << 16), acc);
+    acc = fmaf(__uint_as_float(x.w & 0xffff0000u), __uint_as_float(q.w & 0xffff0000u), acc);
+  } else if constexpr (DT == DT_F16) {
+    acc = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2_t, x.x), __builtin_bit_cast(f16x2_t, q.x), acc, false);
+    acc = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2_t, x.y), __builtin_bit_cast(f16x2_t, q.y), acc, false);
+    acc = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2_t, x.z), __builtin_bit_cast(f16x2_t, q.z), acc, false);
+    acc = fmaf(f16_bits_to_f32(x.w & 0xffffu), f16_bits_to_f32(q.w & 0xffffu), acc);
+    acc = fmaf(f16_bits_to_f32(x.w >> 16), f16_bits_to_f32(q.w >> 16), acc);
+  } else {
+    acc = fmaf(__uint_as_float(x.x), __uint_as_float(q.x), acc);
+    acc = fmaf(__uint_as_float(x.y), __uint_as_float(q.y), acc);
+    acc = fmaf(__uint_as_float(x.z), __uint_as_float(q.z), acc);
+    acc = fmaf(__uint_as_float(x.w), __uint_as_float(q.w), acc);
+  }
+  return acc;
+}
+
+__device__ __forceinline__ uint4 load16(const void *p) { return *reinterpret_cast<const uint4 *>(p); }
 
 // Inclusive prefix sum over the NT threads of a block.  `tmp` is LDS with
 // room for NT / 64 ints.  Contains two barriers; every thread must call it.

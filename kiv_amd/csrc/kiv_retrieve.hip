@@ -24,134 +24,218 @@
 namespace kiv {
 
 constexpr int kSelThreads = 1024;
-constexpr int kKeyCache = 24576;   // keys held in LDS by the select kernels
-constexpr int kMaxOut = 4096;      // largest top-P the fine select sorts in LDS
-constexpr int kScanThreads = 512;  // coarse scan block
+constexpr int kSelWaves = kSelThreads / 64;
+constexpr int kMaxOut = 4096;                 // largest top-P the fine select sorts in LDS
+constexpr int kScanThreads = 512;             // coarse scan block
 
-// Per-row LDS of the two select kernels.
+// LDS of the 1024-thread select blocks.
 struct SelShared {
-  uint32_t hist[2048];
-  int scan_tmp[kSelThreads / 64];
-  int res[4];
-  float fred[kSelThreads / 64][2];
-  int counter;
+  int red[2][kSelWaves];
+  uint32_t band[kSelWaves], bor[kSelWaves];
+  float fmax[kSelWaves], fsum[kSelWaves];
+  int scan_tmp[kSelWaves];
   int is_last;
 };
 
-// Threshold T = k-th largest of keys[0, n) and the number of keys equal to T
-// that belong to the top k.  Three radix passes of 11, 11 and 10 bits over a
-// 2048-bin LDS histogram; every thread of the 1024-thread block must call.
-__device__ void radix_select(const uint32_t *keys, int n, int k, SelShared &sh, uint32_t &t_out,
-                             int &need_out) {
-  uint32_t prefix = 0, mask = 0;
-  int remaining = k;
-  const int tid = threadIdx.x;
-#pragma unroll 1
-  for (int pass = 0; pass < 3; ++pass) {
-    const int shift = pass == 0 ? 21 : (pass == 1 ? 10 : 0);
-    const uint32_t dmask = pass == 2 ? 0x3ffu : 0x7ffu;
-    sh.hist[tid] = 0;
-    sh.hist[tid + kSelThreads] = 0;
-    __syncthreads();
-    for (int i = tid; i < n; i += kSelThreads) {
-      const uint32_t kk = keys[i];
-      if ((kk & mask) == prefix) atomicAdd(&sh.hist[(kk >> shift) & dmask], 1u);
-    }
-    __syncthreads();
-    const int bhi = 2047 - 2 * tid, blo = bhi - 1;
-    const int chi = (int)sh.hist[bhi], clo = (int)sh.hist[blo];
-    const int incl = block_incl_scan<kSelThreads>(chi + clo, sh.scan_tmp, nullptr);
-    const int excl = incl - chi - clo;
-    if (excl < remaining && remaining <= excl + chi) {
-      sh.res[0] = bhi;
-      sh.res[1] = excl;
-    } else if (excl + chi < remaining && remaining <= incl) {
-      sh.res[0] = blo;
-      sh.res[1] = excl + chi;
-    }
-    __syncthreads();
-    remaining -= sh.res[1];
-    prefix |= (uint32_t)sh.res[0] << shift;
-    mask |= dmask << shift;
-    __syncthreads();
-  }
-  t_out = prefix;
-  need_out = remaining;
+// Block sum with one barrier: alternate halves of sh.red by `parity`.
+__device__ __forceinline__ int block_sum(int v, SelShared &sh, int &parity) {
+  v = wave_sum_i32(v);
+  if ((threadIdx.x & 63) == 0) sh.red[parity][threadIdx.x >> 6] = v;
+  __syncthreads();
+  int t = 0;
+#pragma unroll
+  for (int w = 0; w < kSelWaves; ++w) t += sh.red[parity][w];
+  parity ^= 1;
+  return t;
 }
 
-// Calls visit(i, key) for every index of the top k (keys > T, then the first
-// need_eq keys equal to T in index order).  Block-uniform loop.
-template <typename F>
-__device__ void for_each_selected(const uint32_t *keys, int n, uint32_t T, int need_eq, SelShared &sh,
-                                  F &&visit) {
-  int taken = 0;
-  for (int base = 0; base < n; base += kSelThreads) {
-    const int i = base + threadIdx.x;
-    const uint32_t kk = i < n ? keys[i] : 0u;
-    const int eq = (i < n && kk == T) ? 1 : 0;
-    int tot = 0;
-    int incl = 0;
-    if (taken < need_eq) incl = block_incl_scan<kSelThreads>(eq, sh.scan_tmp, &tot);
-    const bool sel = i < n && (kk > T || (eq && taken + incl - 1 < need_eq));
-    if (sel) visit(i, kk);
-    taken += tot;
+// Keys of one row, split over the block in index order: thread t owns the
+// contiguous range [base, base + cnt).  RegKeys holds up to KPT keys per
+// thread in registers; MemKeys re-reads them from memory (rows longer than
+// KPT * 1024).
+template <int KPT> struct RegKeys {
+  uint32_t v[KPT];
+  int base, cnt;
+  __device__ void load(const uint32_t *p, int n) {
+    base = threadIdx.x * KPT;
+    cnt = max(0, min(KPT, n - base));
+#pragma unroll
+    for (int i = 0; i < KPT; ++i) v[i] = i < cnt ? p[base + i] : 0u;
+  }
+  template <typename F> __device__ void each(F &&f) const {
+#pragma unroll
+    for (int i = 0; i < KPT; ++i)
+      if (i < cnt) f(v[i], base + i);
+  }
+};
+
+struct MemKeys {
+  const uint32_t *p;
+  int base, cnt;
+  __device__ void load(const uint32_t *src, int n) {
+    const int per = (n + kSelThreads - 1) / kSelThreads;
+    p = src;
+    base = threadIdx.x * per;
+    cnt = max(0, min(per, n - base));
+  }
+  template <typename F> __device__ void each(F &&f) const {
+    for (int i = 0; i < cnt; ++i) f(p[base + i], base + i);
+  }
+};
+
+// k-th largest key T of the row and the number of keys > T.  Bits equal in
+// every key are taken as they are; each varying bit, from the top, is
+// decided by one block-wide count of keys >= the candidate threshold.
+template <typename K>
+__device__ uint32_t kth_largest(const K &rk, int k, SelShared &sh, int &parity, int &gt) {
+  uint32_t a = 0xffffffffu, o = 0u;
+  rk.each([&](uint32_t key, int) { a &= key; o |= key; });
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) {
+    a &= __shfl_xor(a, m, 64);
+    o |= __shfl_xor(o, m, 64);
+  }
+  if ((threadIdx.x & 63) == 0) {
+    sh.band[threadIdx.x >> 6] = a;
+    sh.bor[threadIdx.x >> 6] = o;
+  }
+  __syncthreads();
+  a = 0xffffffffu;
+  o = 0u;
+#pragma unroll
+  for (int w = 0; w < kSelWaves; ++w) {
+    a &= sh.band[w];
+    o |= sh.bor[w];
+  }
+  uint32_t ans = a, var = a ^ o;
+  while (var) {
+    const int bit = 31 - __clz(var);
+    var &= ~(1u << bit);
+    const uint32_t cand = ans | (1u << bit);
+    int local = 0;
+    rk.each([&](uint32_t key, int) { local += key >= cand; });
+    if (block_sum(local, sh, parity) >= k) ans = cand;
+  }
+  int local = 0;
+  rk.each([&](uint32_t key, int) { local += key > ans; });
+  gt = block_sum(local, sh, parity);
+  return ans;
+}
+
+// Calls f(key, index) for the top k: every key > T and the first need_eq
+// keys == T in index order (ranks of equal keys from one block scan).
+template <typename K, typename F>
+__device__ void each_selected(const K &rk, uint32_t T, int need_eq, SelShared &sh, F &&f) {
+  int eq = 0;
+  rk.each([&](uint32_t key, int) { eq += key == T; });
+  int rank = block_incl_scan<kSelThreads>(eq, sh.scan_tmp, nullptr) - eq;
+  rk.each([&](uint32_t key, int idx) {
+    if (key > T) f(key, idx);
+    else if (key == T) {
+      if (rank < need_eq) f(key, idx);
+      ++rank;
+    }
+  });
+}
+
+// Block-wide max / sum of the key values (telemetry), in every thread.
+template <typename K>
+__device__ void row_stats(const K &rk, SelShared &sh, float &mx, float &sum) {
+  float m = -INFINITY, t = 0.f;
+  rk.each([&](uint32_t key, int) {
+    const float f = key_to_float(key);
+    m = fmaxf(m, f);
+    t += f;
+  });
+  m = wave_max(m);
+  t = wave_sum(t);
+  if ((threadIdx.x & 63) == 0) {
+    sh.fmax[threadIdx.x >> 6] = m;
+    sh.fsum[threadIdx.x >> 6] = t;
+  }
+  __syncthreads();
+  mx = sh.fmax[0];
+  sum = 0.f;
+  for (int w = 0; w < kSelWaves; ++w) {
+    mx = fmaxf(mx, sh.fmax[w]);
+    sum += sh.fsum[w];
+  }
+}
+
+// Max and sum over `count` (max, sum) pairs written by other blocks, read
+// in parallel with coherent loads and reduced across the block.  Every
+// thread of the block must call; the result is valid in every thread.
+__device__ void merge_row_stats(float *buf, int count, SelShared &sh, float &mx, double &sum) {
+  float m = -INFINITY, t = 0.f;
+  for (int r = threadIdx.x; r < count; r += kSelThreads) {
+    m = fmaxf(m, coherent_load_f32(&buf[2 * r]));
+    t += coherent_load_f32(&buf[2 * r + 1]);
+  }
+  m = wave_max(m);
+  t = wave_sum(t);
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) {
+    sh.fmax[threadIdx.x >> 6] = m;
+    sh.fsum[threadIdx.x >> 6] = t;
+  }
+  __syncthreads();
+  mx = -INFINITY;
+  sum = 0.0;
+  for (int w = 0; w < kSelWaves; ++w) {
+    mx = fmaxf(mx, sh.fmax[w]);
+    sum += sh.fsum[w];
   }
 }
 
 // ------------------------------------------------------------ coarse scan
-// Block handles pages [p0, p0 + ppw).  q rows live in LDS as fp32; each
-// group of LG lanes holds one (page, kv row) summary row in registers and
-// produces the scores of the G*Q query rows that read that kv row.
+// Block handles pages [p0, p0 + ppw).  The query rows sit in LDS in their
+// dtype, kv-major: row r' = kv_row * G*Q + j holds q head kv_head*G + j/Q at
+// position j%Q.  Each group of LG lanes holds one (page, kv row) summary row
+// in registers and scores it against the G*Q rows that read that kv row;
+// the keys go to row r' of the output.
 template <int DT, int LG>
 __global__ void __launch_bounds__(kScanThreads) coarse_scan_kernel(
     const char *__restrict__ summ, int64_t n_pages, int kr, int head_dim, const char *__restrict__ q,
     int64_t qs0, int64_t qs1, int64_t qs2, int hq, int hkv, int qlen, int rows, float scale, int round,
     int ppw, uint32_t *__restrict__ keys, int64_t ld) {
   constexpr int VEC = Elem<DT>::VEC, EB = Elem<DT>::BYTES;
-  extern __shared__ float smem[];
-  float *qf = smem;                                                       // [rows][D]
-  uint32_t *sk = reinterpret_cast<uint32_t *>(smem + (size_t)rows * head_dim);  // [rows][ppw]
+  constexpr int NSLOT = kScanThreads / LG;
+  constexpr int UT = 4;  // units in flight per lane group
+  extern __shared__ uint4 smem4[];
+  char *qraw = reinterpret_cast<char *>(smem4);                                  // [rows][D]
+  uint32_t *sk = reinterpret_cast<uint32_t *>(qraw + (size_t)rows * head_dim * EB);  // [rows][ppw]
+  const int G = hq / hkv, GQ = G * qlen, cpr = head_dim / VEC;
   const int tid = threadIdx.x;
-  for (int i = tid; i < rows * head_dim; i += kScanThreads) {
-    const int r = i / head_dim, d = i % head_dim;
-    const int qp = r % qlen, bh = r / qlen;
-    qf[i] = load_elem<DT>(q, (int64_t)(bh / hq) * qs0 + (int64_t)(bh % hq) * qs1 + (int64_t)qp * qs2 + d);
+  for (int i = tid; i < rows * cpr; i += kScanThreads) {
+    const int r = i / cpr, c = i % cpr;
+    const int kvr = r / GQ, j = r % GQ;
+    const int b = kvr / hkv, h = (kvr % hkv) * G + j / qlen, qp = j % qlen;
+    *reinterpret_cast<uint4 *>(qraw + ((size_t)r * head_dim + c * VEC) * EB) =
+        load16(q + ((int64_t)b * qs0 + (int64_t)h * qs1 + (int64_t)qp * qs2 + c * VEC) * EB);
   }
   const int64_t p0 = (int64_t)blockIdx.x * ppw;
   const int np = (int)min<int64_t>(ppw, n_pages - p0);
   __syncthreads();
-  const int G = hq / hkv, GQ = G * qlen, cpr = head_dim / VEC;
   const int slot = tid / LG, lane = tid % LG;
-  constexpr int NSLOT = kScanThreads / LG;
   const int units = np * kr;
   const bool on = lane < cpr;
-  constexpr int UT = 4;  // units in flight per lane group
   for (int ub = slot; ub < units; ub += NSLOT * UT) {
-    float x[UT][VEC];
+    uint4 x[UT];
 #pragma unroll
     for (int i = 0; i < UT; ++i) {
       const int u = ub + i * NSLOT;
-      if (on && u < units) {
-        load_chunk<DT>(summ + (((p0 + u / kr) * kr + u % kr) * head_dim + lane * VEC) * EB, x[i]);
-      } else {
-#pragma unroll
-        for (int e = 0; e < VEC; ++e) x[i][e] = 0.f;
-      }
+      x[i] = (on && u < units) ? load16(summ + (((p0 + u / kr) * kr + u % kr) * head_dim + lane * VEC) * EB)
+                               : make_uint4(0, 0, 0, 0);
     }
 #pragma unroll
     for (int i = 0; i < UT; ++i) {
       const int u = ub + i * NSLOT;
       if (u >= units) break;
       const int pl = u / kr, r = u % kr;
-      const int b = r / hkv, kvh = r % hkv;
       for (int j = 0; j < GQ; ++j) {
-        const int row = (b * hq + kvh * G + j / qlen) * qlen + j % qlen;
+        const int row = r * GQ + j;
         float part = 0.f;
-        if (on) {
-          const float *qr = qf + row * head_dim + lane * VEC;
-#pragma unroll
-          for (int e = 0; e < VEC; ++e) part = fmaf(x[i][e], qr[e], part);
-        }
+        if (on) part = chunk_dot<DT>(x[i], load16(qraw + ((size_t)row * head_dim + lane * VEC) * EB), 0.f);
         const float dot = group_sum<LG>(part);
         if (lane == (j % LG)) sk[row * ppw + pl] = order_key(score_of<DT>(dot, scale, round != 0));
       }
@@ -165,55 +249,42 @@ __global__ void __launch_bounds__(kScanThreads) coarse_scan_kernel(
 }
 
 // --------------------------------------------------------- coarse select
-// One block per query row: top-k pages of the row set in the shared page
-// bitmap.  The last block to finish compacts the bitmap into the ascending
-// union page list, writes U, clears the bitmap and the counter, and records
-// the coarse telemetry (max score over rows, mean over all scores).
-template <int DT>
+// One block per query row: its top-k pages go into the shared page bitmap.
+// The last block to finish compacts the bitmap into the ascending union
+// list, writes U, clears the bitmap and the counter, and records the coarse
+// telemetry (max score over rows, mean over all scores).
+template <typename K>
+__device__ void coarse_pick(const K &rk, int k, uint32_t *bitmap, SelShared &sh, float &mx, float &sum) {
+  row_stats(rk, sh, mx, sum);
+  int parity = 0, gt = 0;
+  const uint32_t T = kth_largest(rk, k, sh, parity, gt);
+  each_selected(rk, T, k - gt, sh, [&](uint32_t, int i) { atomicOr(&bitmap[i >> 5], 1u << (i & 31)); });
+}
+
+template <int DT, int KPT>
 __global__ void __launch_bounds__(kSelThreads) coarse_select_kernel(
     const uint32_t *__restrict__ keys, int64_t ld, int n, int k, int rows, uint32_t *bitmap,
-    int32_t *page_list, int32_t *counters, float *row_stats, int round, int32_t *pages_out,
+    int32_t *page_list, int32_t *counters, float *row_stats_buf, int round, int32_t *pages_out,
     int32_t *union_out, float *stats_out, double *stats_accum) {
   __shared__ SelShared sh;
-  __shared__ uint32_t cache[kKeyCache];
   const int tid = threadIdx.x, row = blockIdx.x;
   const uint32_t *src = keys + (int64_t)row * ld;
-  const bool cached = n <= kKeyCache;
-  uint32_t kmax = 0;
-  float ssum = 0.f;
-  for (int i = tid; i < n; i += kSelThreads) {
-    const uint32_t kk = src[i];
-    if (cached) cache[i] = kk;
-    kmax = max(kmax, kk);
-    ssum += key_to_float(kk);
+  float mx, sum;
+  if (n <= KPT * kSelThreads) {
+    RegKeys<KPT> rk;
+    rk.load(src, n);
+    coarse_pick(rk, k, bitmap, sh, mx, sum);
+  } else {
+    MemKeys rk;
+    rk.load(src, n);
+    coarse_pick(rk, k, bitmap, sh, mx, sum);
   }
-  // Row max / sum for telemetry.
-  {
-    float m = key_to_float(kmax);
-    m = wave_max(m);
-    const float s = wave_sum(ssum);
-    if ((tid & 63) == 0) {
-      sh.fred[tid >> 6][0] = m;
-      sh.fred[tid >> 6][1] = s;
-    }
-  }
-  __syncthreads();
-  const uint32_t *kp = cached ? cache : src;
-  uint32_t T;
-  int need;
-  radix_select(kp, n, k, sh, T, need);
-  for_each_selected(kp, n, T, need, sh, [&](int i, uint32_t) {
-    atomicOr(&bitmap[i >> 5], 1u << (i & 31));
-  });
   if (tid == 0) {
-    float m = sh.fred[0][0], s = 0.f;
-    for (int w = 0; w < kSelThreads / 64; ++w) {
-      m = fmaxf(m, sh.fred[w][0]);
-      s += sh.fred[w][1];
-    }
-    coherent_store_f32(&row_stats[2 * row], m);
-    coherent_store_f32(&row_stats[2 * row + 1], s);
+    coherent_store_f32(&row_stats_buf[2 * row], mx);
+    coherent_store_f32(&row_stats_buf[2 * row + 1], sum);
   }
+  // Every wave completes its own bitmap updates before the block signals.
+  __threadfence();
   __syncthreads();
   if (tid == 0) {
     __threadfence();
@@ -229,31 +300,26 @@ __global__ void __launch_bounds__(kSelThreads) coarse_select_kernel(
   int cnt = 0;
   for (int w = w0; w < w1; ++w) cnt += __popc(coherent_load_u32(&bitmap[w]));
   int total = 0;
-  const int incl = block_incl_scan<kSelThreads>(cnt, sh.scan_tmp, &total);
-  int pos = incl - cnt;
+  int pos = block_incl_scan<kSelThreads>(cnt, sh.scan_tmp, &total) - cnt;
   for (int w = w0; w < w1; ++w) {
     uint32_t bits = coherent_load_u32(&bitmap[w]);
     coherent_store_u32(&bitmap[w], 0u);
     while (bits) {
-      const int bit = __ffs(bits) - 1;
+      const int page = w * 32 + __ffs(bits) - 1;
       bits &= bits - 1;
-      const int page = w * 32 + bit;
       page_list[pos] = page;
       if (pages_out) pages_out[pos] = page;
       ++pos;
     }
   }
+  float m;
+  double t;
+  merge_row_stats(row_stats_buf, rows, sh, m, t);
   if (tid == 0) {
     counters[0] = total;
     counters[1] = 0;
     if (union_out) union_out[0] = total;
-    float m = -INFINITY;
-    double s = 0.0;
-    for (int r = 0; r < rows; ++r) {
-      m = fmaxf(m, coherent_load_f32(&row_stats[2 * r]));
-      s += coherent_load_f32(&row_stats[2 * r + 1]);
-    }
-    float mean = (float)(s / ((double)rows * (double)n));
+    float mean = (float)(t / ((double)rows * (double)n));
     if (round) mean = round_act<DT>(mean);
     if (stats_out) {
       stats_out[0] = m;
@@ -284,14 +350,16 @@ __global__ void __launch_bounds__(256) fine_scan_kernel(
   constexpr int VEC = Elem<DT>::VEC, EB = Elem<DT>::BYTES;
   constexpr int UT = 4;
   constexpr int NSLOT = 256 / LG;
-  extern __shared__ float qf[];  // [G*Q][D]
+  extern __shared__ uint4 smem4[];
+  char *qraw = reinterpret_cast<char *>(smem4);  // [G*Q][D] dtype
   const int r = blockIdx.y, b = r / hkv, kvh = r % hkv;
   const int G = hq / hkv, GQ = G * qlen, cpr = head_dim / VEC;
   const int tid = threadIdx.x;
-  for (int i = tid; i < GQ * head_dim; i += 256) {
-    const int j = i / head_dim, d = i % head_dim;
+  for (int i = tid; i < GQ * cpr; i += 256) {
+    const int j = i / cpr, c = i % cpr;
     const int h = kvh * G + j / qlen, qp = j % qlen;
-    qf[i] = load_elem<DT>(q, (int64_t)b * qs0 + (int64_t)h * qs1 + (int64_t)qp * qs2 + d);
+    *reinterpret_cast<uint4 *>(qraw + ((size_t)j * head_dim + c * VEC) * EB) =
+        load16(q + ((int64_t)b * qs0 + (int64_t)h * qs1 + (int64_t)qp * qs2 + c * VEC) * EB);
   }
   __syncthreads();
   const int U = has_pages ? counters[0] : 0;
@@ -320,16 +388,12 @@ __global__ void __launch_bounds__(256) fine_scan_kernel(
       ntok = min(tpi, partial_len - s * tpi);
     }
     for (int tb = 0; tb < ntok; tb += NSLOT * UT) {
-      float x[UT][VEC];
+      uint4 x[UT];
 #pragma unroll
       for (int i = 0; i < UT; ++i) {
         const int t = tb + i * NSLOT + slot;
-        if (on && t < ntok) {
-          load_chunk<DT>(rowbase + (int64_t)t * row_bytes + lane * VEC * EB, x[i]);
-        } else {
-#pragma unroll
-          for (int e = 0; e < VEC; ++e) x[i][e] = 0.f;
-        }
+        x[i] = (on && t < ntok) ? load16(rowbase + (int64_t)t * row_bytes + lane * VEC * EB)
+                                : make_uint4(0, 0, 0, 0);
       }
 #pragma unroll
       for (int i = 0; i < UT; ++i) {
@@ -338,11 +402,7 @@ __global__ void __launch_bounds__(256) fine_scan_kernel(
         float best = -INFINITY;
         for (int j = 0; j < GQ; ++j) {
           float part = 0.f;
-          if (on) {
-            const float *qr = qf + j * head_dim + lane * VEC;
-#pragma unroll
-            for (int e = 0; e < VEC; ++e) part = fmaf(x[i][e], qr[e], part);
-          }
+          if (on) part = chunk_dot<DT>(x[i], load16(qraw + ((size_t)j * head_dim + lane * VEC) * EB), 0.f);
           best = fmaxf(best, score_of<DT>(group_sum<LG>(part), scale, round != 0));
         }
         if (lane == 0) atomicMax(&out[(int64_t)b * ld + cand0 + t], order_key(best));
@@ -355,49 +415,46 @@ __global__ void __launch_bounds__(256) fine_scan_kernel(
 // One block per batch row: top-P' of the C candidate keys, sorted by score
 // descending (ties: lower candidate index first).  Writes the candidate
 // index per output slot, the global token id, P' and the fine telemetry
-// (max over rows, mean over all keys; combined by the last block).
-template <int DT>
+// (max over rows, mean over all keys; combined by the last block), and
+// zeroes the keys for the next scan.
+template <typename K>
+__device__ void fine_pick(const K &rk, int k, unsigned long long *ent, SelShared &sh, float &mx, float &sum) {
+  row_stats(rk, sh, mx, sum);
+  int parity = 0, gt = 0;
+  const uint32_t T = kth_largest(rk, k, sh, parity, gt);
+  // Selected entries in index order: positions from a block scan.
+  const int need = k - gt;
+  int mine = 0;
+  each_selected(rk, T, need, sh, [&](uint32_t, int) { ++mine; });
+  int pos = block_incl_scan<kSelThreads>(mine, sh.scan_tmp, nullptr) - mine;
+  each_selected(rk, T, need, sh, [&](uint32_t key, int i) {
+    ent[pos++] = ((unsigned long long)key << 32) | (unsigned long long)(0xffffffffu - (uint32_t)i);
+  });
+}
+
+template <int DT, int KPT>
 __global__ void __launch_bounds__(kSelThreads) fine_select_kernel(
     uint32_t *__restrict__ keys, int64_t ld, int32_t *counters, int has_pages, int page_size,
     int partial_len, int64_t num_finalized, const int32_t *__restrict__ page_list, int width,
-    int batch, int round, float *row_stats, int32_t *__restrict__ sel_cand, int64_t *__restrict__ idx_out,
+    int batch, int round, float *row_stats_buf, int32_t *__restrict__ sel_cand, int64_t *__restrict__ idx_out,
     float *stats_out, double *stats_accum) {
   __shared__ SelShared sh;
-  __shared__ uint32_t cache[kKeyCache];
   __shared__ unsigned long long ent[kMaxOut];
   const int tid = threadIdx.x, b = blockIdx.x;
   const int U = has_pages ? counters[0] : 0;
   const int n = U * page_size + partial_len;
   const int k = min(width, n);
   uint32_t *src = keys + (int64_t)b * ld;
-  const bool cached = n <= kKeyCache;
-  uint32_t kmax = 0;
-  float ssum = 0.f;
-  for (int i = tid; i < n; i += kSelThreads) {
-    const uint32_t kk = src[i];
-    if (cached) cache[i] = kk;
-    kmax = max(kmax, kk);
-    ssum += key_to_float(kk);
+  float mx, sum;
+  if (n <= KPT * kSelThreads) {
+    RegKeys<KPT> rk;
+    rk.load(src, n);
+    fine_pick(rk, k, ent, sh, mx, sum);
+  } else {
+    MemKeys rk;
+    rk.load(src, n);
+    fine_pick(rk, k, ent, sh, mx, sum);
   }
-  {
-    const float m = wave_max(key_to_float(kmax));
-    const float s = wave_sum(ssum);
-    if ((tid & 63) == 0) {
-      sh.fred[tid >> 6][0] = m;
-      sh.fred[tid >> 6][1] = s;
-    }
-  }
-  if (tid == 0) sh.counter = 0;
-  __syncthreads();
-  const uint32_t *kp = cached ? cache : src;
-  uint32_t T;
-  int need;
-  radix_select(kp, n, k, sh, T, need);
-  for_each_selected(kp, n, T, need, sh, [&](int i, uint32_t kk) {
-    const int slot = atomicAdd(&sh.counter, 1);
-    ent[slot] = ((unsigned long long)kk << 32) | (unsigned long long)(0xffffffffu - (uint32_t)i);
-  });
-  __syncthreads();
   int kp2 = 1;
   while (kp2 < k) kp2 <<= 1;
   for (int i = k + tid; i < kp2; i += kSelThreads) ent[i] = 0ull;
@@ -408,10 +465,10 @@ __global__ void __launch_bounds__(kSelThreads) fine_select_kernel(
       for (int t = tid; t < kp2 / 2; t += kSelThreads) {
         const int i = 2 * stride * (t / stride) + (t % stride), j = i + stride;
         const bool desc = (i & size) == 0;
-        const unsigned long long a = ent[i], c = ent[j];
-        if ((a < c) == desc) {
-          ent[i] = c;
-          ent[j] = a;
+        const unsigned long long x = ent[i], y = ent[j];
+        if ((x < y) == desc) {
+          ent[i] = y;
+          ent[j] = x;
         }
       }
       __syncthreads();
@@ -431,26 +488,19 @@ __global__ void __launch_bounds__(kSelThreads) fine_select_kernel(
     }
   }
   if (tid == 0) {
-    float m = sh.fred[0][0], s = 0.f;
-    for (int w = 0; w < kSelThreads / 64; ++w) {
-      m = fmaxf(m, sh.fred[w][0]);
-      s += sh.fred[w][1];
-    }
-    coherent_store_f32(&row_stats[2 * b], m);
-    coherent_store_f32(&row_stats[2 * b + 1], s);
+    coherent_store_f32(&row_stats_buf[2 * b], mx);
+    coherent_store_f32(&row_stats_buf[2 * b + 1], sum);
     __threadfence();
     sh.is_last = atomic_add_acq_rel(&counters[2], 1) == batch - 1;
   }
   __syncthreads();
-  if (!sh.is_last || tid != 0) return;
+  if (!sh.is_last) return;
   __threadfence();
-  float m = -INFINITY;
-  double s = 0.0;
-  for (int r = 0; r < batch; ++r) {
-    m = fmaxf(m, coherent_load_f32(&row_stats[2 * r]));
-    s += coherent_load_f32(&row_stats[2 * r + 1]);
-  }
-  float mean = (float)(s / ((double)batch * (double)n));
+  float m;
+  double t;
+  merge_row_stats(row_stats_buf, batch, sh, m, t);
+  if (tid != 0) return;
+  float mean = (float)(t / ((double)batch * (double)n));
   if (round) mean = round_act<DT>(mean);
   counters[2] = 0;
   counters[3] = k;
@@ -506,6 +556,15 @@ __global__ void __launch_bounds__(256) gather_kernel(
   *reinterpret_cast<uint4 *>(v_out + o) = *reinterpret_cast<const uint4 *>(vs);
 }
 
+// Keys per thread the selects hold in registers; rows longer than 32 * 1024
+// keys take the memory-backed path (chosen on the device from the row length).
+template <typename F> static int with_kpt(int64_t n, F &&f) {
+  if (n <= 4 * kSelThreads) return f(std::integral_constant<int, 4>{});
+  if (n <= 8 * kSelThreads) return f(std::integral_constant<int, 8>{});
+  if (n <= 16 * kSelThreads) return f(std::integral_constant<int, 16>{});
+  return f(std::integral_constant<int, 32>{});
+}
+
 }  // namespace kiv
 
 using namespace kiv;
@@ -538,6 +597,8 @@ int kiv_retrieve(kiv_store_t *s, const kiv_retrieve_args_t *a, kiv_stream_t stre
   if (((uintptr_t)a->k_out | (uintptr_t)a->v_out) & 15)
     return fail(KIV_ERR_INVALID, "kiv_retrieve: outputs must be 16-byte aligned");
   if (a->q_stride[3] != 1) return fail(KIV_ERR_INVALID, "kiv_retrieve: q head_dim stride must be 1");
+  if (((uintptr_t)a->q & 15) || (a->q_stride[0] % vec) || (a->q_stride[1] % vec) || (a->q_stride[2] % vec))
+    return fail(KIV_ERR_INVALID, "kiv_retrieve: q must be 16-byte aligned with strides multiple of %d", vec);
   const int rows = B * hq * Q;
   if ((int64_t)rows * D > 12288)
     return fail(KIV_ERR_UNSUPPORTED, "kiv_retrieve: B*Hq*Q*D = %lld exceeds 12288 (decode-sized queries only)",
@@ -571,7 +632,7 @@ int kiv_retrieve(kiv_store_t *s, const kiv_retrieve_args_t *a, kiv_stream_t stre
       int ppw = (int)std::max<int64_t>(1, ((int64_t)N + 255) / 256);
       ppw = std::min(ppw, std::max(1, 4096 / rows));
       const int blocks = (int)(((int64_t)N + ppw - 1) / ppw);
-      const size_t lds = ((size_t)rows * D + (size_t)rows * ppw) * 4;
+      const size_t lds = (size_t)rows * D * eb + (size_t)rows * ppw * 4;
       s->prof_begin(KIV_STAGE_COARSE_SCAN, st);
       rc = with_dt_lg(dt, lg, [&](auto dtc, auto lgc) {
         hipLaunchKernelGGL((coarse_scan_kernel<decltype(dtc)::value, decltype(lgc)::value>), dim3(blocks),
@@ -585,11 +646,14 @@ int kiv_retrieve(kiv_store_t *s, const kiv_retrieve_args_t *a, kiv_stream_t stre
       KIV_HIP(hipGetLastError());
       s->prof_begin(KIV_STAGE_COARSE_SELECT, st);
       rc = with_dt(dt, [&](auto dtc) {
-        hipLaunchKernelGGL((coarse_select_kernel<decltype(dtc)::value>), dim3(rows), dim3(kSelThreads), 0, st,
+        return with_kpt(N, [&](auto kpt) {
+        hipLaunchKernelGGL((coarse_select_kernel<decltype(dtc)::value, decltype(kpt)::value>), dim3(rows),
+                           dim3(kSelThreads), 0, st,
                            (const uint32_t *)s->coarse_keys.ptr, ld, N, k, rows, (uint32_t *)s->bitmap.ptr,
                            (int32_t *)s->page_list.ptr, (int32_t *)s->counters.ptr, (float *)s->row_stats.ptr,
                            round, a->pages_out, a->union_count_out, a->stats_out, a->stats_accum);
         return (int)KIV_OK;
+        });
       });
       s->prof_end(KIV_STAGE_COARSE_SELECT, st);
       if (rc) return rc;
@@ -621,7 +685,7 @@ int kiv_retrieve(kiv_store_t *s, const kiv_retrieve_args_t *a, kiv_stream_t stre
     const int64_t max_items = umax * nsplit + (s->partial_len + tpi - 1) / tpi;
     const int64_t nb = std::max<int64_t>(1, std::min<int64_t>(max_items, (1024 + s->kr - 1) / s->kr));
     const int G = hq / hkv;
-    const size_t lds = (size_t)G * Q * D * 4;
+    const size_t lds = (size_t)G * Q * D * eb;
     s->prof_begin(KIV_STAGE_FINE_SCAN, st);
     rc = with_dt_lg(dt, lg, [&](auto dtc, auto lgc) {
       hipLaunchKernelGGL((fine_scan_kernel<decltype(dtc)::value, decltype(lgc)::value>),
@@ -638,12 +702,15 @@ int kiv_retrieve(kiv_store_t *s, const kiv_retrieve_args_t *a, kiv_stream_t stre
   }
   s->prof_begin(KIV_STAGE_FINE_SELECT, st);
   rc = with_dt(dt, [&](auto dtc) {
-    hipLaunchKernelGGL((fine_select_kernel<decltype(dtc)::value>), dim3(B), dim3(kSelThreads), 0, st,
+    return with_kpt(cmax, [&](auto kpt) {
+    hipLaunchKernelGGL((fine_select_kernel<decltype(dtc)::value, decltype(kpt)::value>), dim3(B),
+                       dim3(kSelThreads), 0, st,
                        (uint32_t *)s->fine_keys.ptr, ldc, (int32_t *)s->counters.ptr, has_pages, ps,
                        (int)s->partial_len, s->num_pages * ps, (const int32_t *)s->page_list.ptr, a->out_width, B,
                        round, (float *)s->row_stats.ptr, (int32_t *)s->sel_cand.ptr, a->idx_out, a->stats_out,
                        a->stats_accum);
     return (int)KIV_OK;
+    });
   });
   s->prof_end(KIV_STAGE_FINE_SELECT, st);
   if (rc) return rc;

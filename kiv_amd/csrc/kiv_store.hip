@@ -158,7 +158,7 @@ __global__ void __launch_bounds__(256) evict_finalize_kernel(
   for (int d = threadIdx.x; d < head_dim; d += 256) {
     double s = 0.0;
     for (int gg = 0; gg < groups; ++gg) s += red[gg * head_dim + d];
-    const float m32 = (float)(s / (double)page_size);
+    const float m32 = opaque_f32((float)(s / (double)page_size));
     const int64_t o = ((int64_t)page * kr + r) * head_dim + d;
     summ32[o] = m32;
     store_elem<DT>(summ, o, m32);

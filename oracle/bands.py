@@ -1,5 +1,7 @@
 """Selection checks that allow exactly the ambiguity the arithmetic admits.
 
+Test infrastructure only (see oracle/__init__.py).
+
 A kernel score is an fp32 dot product (some summation order) optionally
 rounded to the activation dtype, times the scale, rounded again
 (oracle.exact.emulate_scores).  The exact dot ``dot64`` is known, and any
@@ -22,7 +24,7 @@ from __future__ import annotations
 
 import numpy as np
 
-from oracle import exact
+from . import exact
 
 U32 = 2.0 ** -24
 
