@@ -19,7 +19,7 @@ _workspaces: dict[int, torch.Tensor] = {}
 
 
 def _workspace(device: torch.device, nbytes: int) -> torch.Tensor:
-    """Zero-filled scratch per device; the kernel leaves its counters zeroed.
+    """Split-partials scratch per device (fully rewritten by every call).
 
     Shared by every call on the device, so concurrent calls on different
     streams of one device must not overlap.
@@ -28,7 +28,7 @@ def _workspace(device: torch.device, nbytes: int) -> torch.Tensor:
     with _ws_lock:
         ws = _workspaces.get(idx)
         if ws is None or ws.numel() < nbytes:
-            ws = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
+            ws = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
             _workspaces[idx] = ws
         return ws
 

@@ -7,10 +7,11 @@
 // concatenated K/V and widened mask are never built.  Scores, softmax and
 // the weighted sum are fp32; the output is rounded once to the dtype.
 //
-// Grid (S, B*Hkv): block (s, r) takes keys [s*CH, (s+1)*CH) of the virtual
-// sequence for kv row r and all G*Q query rows reading it, writes the split's
-// running max m, sum l and unnormalised accumulator, and the last block of
-// row r merges the S splits (log-sum-exp) into the output.
+// Split kernel, grid (S, B*Hkv): block (s, r) takes keys [s*CH, (s+1)*CH) of
+// the virtual sequence for kv row r and all G*Q query rows reading it, and
+// writes the split's max m, exp-sum l and unnormalised accumulator.
+// Combine kernel, one block per query row: log-sum-exp merge of the S splits
+// into the output.
 #include <algorithm>
 #include <type_traits>
 
@@ -22,6 +23,7 @@ namespace kiv {
 
 constexpr int kAttnThreads = 256;
 constexpr int kRowTile = 8;
+constexpr int kMaxSplits = 4096;
 
 struct AttnParams {
   const char *q;
@@ -37,7 +39,6 @@ struct AttnParams {
   float scale;
   int chunk, nsplit;
   float *ws_m, *ws_l, *ws_acc;
-  int *ws_cnt;
   char *out;
 };
 
@@ -68,8 +69,6 @@ __global__ void __launch_bounds__(kAttnThreads) decode_attn_kernel(AttnParams p)
   float *red = sc + GQ * CH;                                               // [4 waves][kRowTile][D]
   float *rm = red + 4 * kRowTile * D;                                      // [GQ] split max
   float *rl = rm + GQ;                                                     // [GQ] split sum
-  float *wts = rl + GQ;                                                    // [GQ][nsplit] merge weights
-  __shared__ int is_last;
   const int tid = threadIdx.x;
   for (int i = tid; i < GQ * cpr; i += kAttnThreads) {
     const int j = i / cpr, c = i % cpr;
@@ -195,75 +194,74 @@ __global__ void __launch_bounds__(kAttnThreads) decode_attn_kernel(AttnParams p)
     p.ws_m[(int64_t)s * rows_total + row] = rm[j];
     p.ws_l[(int64_t)s * rows_total + row] = rl[j];
   }
+}
 
-  // Phase D: the last split of kv row r merges all splits.  Every wave
-  // completes its own partial writes before the block signals.
-  __threadfence();
+// One block per query row (b, h, q position): weights exp(m_s - M) / L in
+// LDS, then 4 consecutive d per thread with the splits' loads issued 8 at a
+// time.
+template <int DT>
+__global__ void __launch_bounds__(kAttnThreads) decode_attn_combine_kernel(AttnParams p) {
+  __shared__ float wts[kMaxSplits];
+  __shared__ float red[kAttnThreads / 64];
+  const int row = blockIdx.x;  // (b*Hq + h)*Q + qp
+  const int qp = row % p.qlen, bh = row / p.qlen;
+  const int b = bh / p.hq, h = bh % p.hq;
+  const int rows_total = p.batch * p.hq * p.qlen;
+  const int D = p.head_dim, S = p.nsplit, tid = threadIdx.x;
+  float M = -INFINITY;
+  for (int s = tid; s < S; s += kAttnThreads) M = fmaxf(M, p.ws_m[(int64_t)s * rows_total + row]);
+  M = wave_max(M);
+  if ((tid & 63) == 0) red[tid >> 6] = M;
   __syncthreads();
-  if (tid == 0) {
-    __threadfence();
-    is_last = atomic_add_acq_rel(&p.ws_cnt[r], 1) == p.nsplit - 1;
+  M = red[0];
+  for (int w = 1; w < kAttnThreads / 64; ++w) M = fmaxf(M, red[w]);
+  __syncthreads();
+  float lsum = 0.f;
+  for (int s = tid; s < S; s += kAttnThreads) {
+    const float ms = p.ws_m[(int64_t)s * rows_total + row];
+    const float w = (ms == -INFINITY) ? 0.f : __expf(ms - M);
+    wts[s] = w;
+    lsum = fmaf(p.ws_l[(int64_t)s * rows_total + row], w, lsum);
   }
+  lsum = wave_sum(lsum);
+  if ((tid & 63) == 0) red[tid >> 6] = lsum;
   __syncthreads();
-  if (!is_last) return;
-  __threadfence();
-  // Per row: weights exp(m_s - M) / sum_s l_s exp(m_s - M), one wave per row.
-  for (int j = wave; j < GQ; j += kAttnThreads / 64) {
-    const int h = kvh * G + j / p.qlen, qp = j % p.qlen;
-    const int row = (b * p.hq + h) * p.qlen + qp;
-    float M = -INFINITY;
-    for (int ss = wl; ss < p.nsplit; ss += 64) M = fmaxf(M, p.ws_m[(int64_t)ss * rows_total + row]);
-    M = wave_max(M);
-    float lsum = 0.f;
-    for (int ss = wl; ss < p.nsplit; ss += 64) {
-      const float ms = p.ws_m[(int64_t)ss * rows_total + row];
-      const float w = (ms == -INFINITY) ? 0.f : __expf(ms - M);
-      wts[j * p.nsplit + ss] = w;
-      lsum = fmaf(p.ws_l[(int64_t)ss * rows_total + row], w, lsum);
-    }
-    lsum = wave_sum(lsum);
-    const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
-    for (int ss = wl; ss < p.nsplit; ss += 64) wts[j * p.nsplit + ss] *= inv;
-  }
-  __syncthreads();
-  // Output: 4 consecutive d per thread, the splits' loads issued 8 at a time.
+  lsum = 0.f;
+  for (int w = 0; w < kAttnThreads / 64; ++w) lsum += red[w];
+  const float inv = (M != -INFINITY && lsum > 0.f) ? 1.f / lsum : 0.f;
   const int d4n = D / 4;
-  for (int i = tid; i < GQ * d4n; i += kAttnThreads) {
-    const int j = i / d4n, d = (i % d4n) * 4;
-    const int h = kvh * G + j / p.qlen, qp = j % p.qlen;
-    const int row = (b * p.hq + h) * p.qlen + qp;
-    const float *wj = wts + j * p.nsplit;
+  for (int i = tid; i < d4n; i += kAttnThreads) {
+    const int d = i * 4;
     float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
-    int ss = 0;
-    for (; ss + 8 <= p.nsplit; ss += 8) {
+    int s = 0;
+    for (; s + 8 <= S; s += 8) {
       float4 a[8];
 #pragma unroll
       for (int u = 0; u < 8; ++u)
-        a[u] = *reinterpret_cast<const float4 *>(&p.ws_acc[((int64_t)(ss + u) * rows_total + row) * D + d]);
+        a[u] = *reinterpret_cast<const float4 *>(&p.ws_acc[((int64_t)(s + u) * rows_total + row) * D + d]);
 #pragma unroll
       for (int u = 0; u < 8; ++u) {
-        const float w = wj[ss + u];
+        const float w = wts[s + u];
         o.x = fmaf(a[u].x, w, o.x);
         o.y = fmaf(a[u].y, w, o.y);
         o.z = fmaf(a[u].z, w, o.z);
         o.w = fmaf(a[u].w, w, o.w);
       }
     }
-    for (; ss < p.nsplit; ++ss) {
-      const float4 a = *reinterpret_cast<const float4 *>(&p.ws_acc[((int64_t)ss * rows_total + row) * D + d]);
-      const float w = wj[ss];
+    for (; s < S; ++s) {
+      const float4 a = *reinterpret_cast<const float4 *>(&p.ws_acc[((int64_t)s * rows_total + row) * D + d]);
+      const float w = wts[s];
       o.x = fmaf(a.x, w, o.x);
       o.y = fmaf(a.y, w, o.y);
       o.z = fmaf(a.z, w, o.z);
       o.w = fmaf(a.w, w, o.w);
     }
     const int64_t ob = (((int64_t)b * p.qlen + qp) * p.hq + h) * D + d;
-    store_elem<DT>(p.out, ob, o.x);
-    store_elem<DT>(p.out, ob + 1, o.y);
-    store_elem<DT>(p.out, ob + 2, o.z);
-    store_elem<DT>(p.out, ob + 3, o.w);
+    store_elem<DT>(p.out, ob, o.x * inv);
+    store_elem<DT>(p.out, ob + 1, o.y * inv);
+    store_elem<DT>(p.out, ob + 2, o.z * inv);
+    store_elem<DT>(p.out, ob + 3, o.w * inv);
   }
-  if (tid == 0) p.ws_cnt[r] = 0;
 }
 
 static int pick_chunk(int total_keys, int kr) {
@@ -272,20 +270,16 @@ static int pick_chunk(int total_keys, int kr) {
   return ch;
 }
 
-// Workspace: a fixed 64 KiB block of per-kv-row counters first (zero
-// between calls: the merging block resets its counter), then the split
-// maxima, sums and accumulators, whose size depends on the key count.
-constexpr size_t kCounterBytes = 65536;
-
+// Workspace: split maxima [S][R], sums [S][R] and accumulators [S][R][D].
 static size_t ws_layout(int batch, int hq, int hkv, int head_dim, int qlen, int total_keys, size_t *off_m,
                         size_t *off_l, size_t *off_acc) {
   const int ch = pick_chunk(std::max(total_keys, 1), batch * hkv);
   const size_t S = (size_t)std::max(1, (total_keys + ch - 1) / ch);
   const size_t R = (size_t)batch * hq * qlen;
   const size_t ml = (S * R * 4 + 255) & ~size_t(255);
-  *off_m = kCounterBytes;
-  *off_l = kCounterBytes + ml;
-  *off_acc = kCounterBytes + 2 * ml;
+  *off_m = 0;
+  *off_l = ml;
+  *off_acc = 2 * ml;
   return *off_acc + ((S * R * head_dim * 4 + 255) & ~size_t(255));
 }
 
@@ -331,8 +325,6 @@ int kiv_decode_attention(const kiv_attention_args_t *a, kiv_stream_t stream) {
   if (a->mask && (a->mask_kind < KIV_MASK_BOOL || a->mask_kind > KIV_MASK_BF16))
     return fail(KIV_ERR_INVALID, "kiv_decode_attention: unknown mask kind %d", a->mask_kind);
   const int L = a->cold_len + a->hot_len;
-  if ((size_t)B * hkv * 4 > kCounterBytes)
-    return fail(KIV_ERR_UNSUPPORTED, "kiv_decode_attention: batch * Hkv too large");
   size_t off_m, off_l, off_acc;
   const size_t need = ws_layout(B, hq, hkv, D, Q, L, &off_m, &off_l, &off_acc);
   if (a->workspace_bytes < need)
@@ -371,13 +363,12 @@ int kiv_decode_attention(const kiv_attention_args_t *a, kiv_stream_t stream) {
   p.chunk = ch;
   p.nsplit = S;
   char *ws = (char *)a->workspace;
-  p.ws_cnt = (int *)ws;
   p.ws_m = (float *)(ws + off_m);
   p.ws_l = (float *)(ws + off_l);
   p.ws_acc = (float *)(ws + off_acc);
   p.out = (char *)a->out;
-  const size_t lds = (size_t)GQ * D * elem_bytes(dt) + ((size_t)GQ * ch + 4 * kRowTile * D + 2 * GQ +
-                                                         (size_t)GQ * S) * 4;
+  if (S > kMaxSplits) return fail(KIV_ERR_UNSUPPORTED, "kiv_decode_attention: %d keys is too many", L);
+  const size_t lds = (size_t)GQ * D * elem_bytes(dt) + ((size_t)GQ * ch + 4 * kRowTile * D + 2 * GQ) * 4;
   if (lds > 160 * 1024)
     return fail(KIV_ERR_UNSUPPORTED, "kiv_decode_attention: %d keys need %zu bytes of LDS", L, lds);
   const int lg = lanes_per_row(dt, D);
@@ -386,6 +377,9 @@ int kiv_decode_attention(const kiv_attention_args_t *a, kiv_stream_t stream) {
     auto kern = decode_attn_kernel<decltype(dtc)::value, decltype(lgc)::value>;
     if (lds > 65536) KIV_HIP(hipFuncSetAttribute((const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
     hipLaunchKernelGGL(kern, dim3(S, B * hkv), dim3(kAttnThreads), lds, st, p);
+    KIV_HIP(hipGetLastError());
+    hipLaunchKernelGGL((decode_attn_combine_kernel<decltype(dtc)::value>), dim3(B * hq * Q), dim3(kAttnThreads), 0,
+                       st, p);
     return (int)KIV_OK;
   });
   if (rc) return rc;

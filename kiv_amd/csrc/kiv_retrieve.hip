@@ -8,12 +8,19 @@
 // top-P, id mapping          :340-347 (topk, gather ids)        fine_select_kernel
 // K/V of the top-P           :358-362 (gather)                  gather_kernel
 //
-// Query rows are (b, q head, q position) triples, row = (b*Hq + h)*Q + q.
-// Row h reads KV row b*Hkv + h / (Hq/Hkv), so no GQA expansion is copied.
-// Scores are ranked through order-preserving uint32 keys; among equal keys
-// the lower page / candidate index wins, which the reference leaves to
-// torch.topk.  Candidates are the union pages in ascending order followed
-// by the partial page, i.e. ascending global token id.
+// Query rows are (b, q head, q position) triples.  Row h reads KV row
+// b*Hkv + h / (Hq/Hkv), so no GQA expansion is copied.  Scores are ranked
+// through order-preserving uint32 keys; among equal keys the lower page /
+// candidate index wins, which the reference leaves to torch.topk.
+// Candidates are the union pages in ascending order followed by the partial
+// page, i.e. ascending global token id.
+//
+// The kernels hand data to each other only across kernel boundaries: the
+// coarse select ORs each row's pages into a page bitmap; the fine scan and
+// fine select rank the bitmap themselves (a prefix count of its words in
+// LDS); the fine select's block 0 writes the compact union list; the gather
+// clears the bitmap and finishes the telemetry.  No kernel waits on another
+// block of its own grid.
 #include <algorithm>
 #include <type_traits>
 
@@ -23,168 +30,394 @@
 
 namespace kiv {
 
-constexpr int kSelThreads = 1024;
-constexpr int kSelWaves = kSelThreads / 64;
-constexpr int kMaxOut = 4096;                 // largest top-P the fine select sorts in LDS
-constexpr int kScanThreads = 512;             // coarse scan block
+constexpr int kMaxOut = 4096;       // largest top-P the fine select sorts in LDS
+constexpr int kScanThreads = 512;   // coarse scan block
+constexpr int kFineSelThreads = 512;
+constexpr int kMaxWords = 4096;     // bitmap words ranked in LDS (131072 pages)
+constexpr int kCandCap = 2048;      // candidates a select keeps in LDS
+constexpr int kWaveCap = 1024;      // candidates one wave selects from registers
 
-// LDS of the 1024-thread select blocks.
-struct SelShared {
-  int red[2][kSelWaves];
-  uint32_t band[kSelWaves], bor[kSelWaves];
-  float fmax[kSelWaves], fsum[kSelWaves];
-  int scan_tmp[kSelWaves];
-  int is_last;
+// Union source of the fine stages.
+enum { UNION_NONE = 0, UNION_BITMAP = 1, UNION_LIST = 2 };
+
+// ------------------------------------------------------ select machinery
+// A select ranks (key, index) pairs by key descending, then index
+// ascending, through the 64-bit composite key << 32 | ~index: composites are
+// distinct, so the top k are exactly the composites >= the k-th largest.
+__device__ __forceinline__ uint64_t comp_of(uint32_t key, int idx) {
+  return ((uint64_t)key << 32) | (uint64_t)(0xffffffffu - (uint32_t)idx);
+}
+__device__ __forceinline__ int comp_index(uint64_t c) { return (int)(0xffffffffu - (uint32_t)c); }
+__device__ __forceinline__ uint32_t comp_key(uint64_t c) { return (uint32_t)(c >> 32); }
+
+// LDS of an NT-thread select block.
+template <int NT> struct SelSh {
+  int cnt[3];  // rotating block-wide counters
+  int ncand, nsel;
+  uint32_t band[2], bor[2];
+  uint64_t bound, thresh;
+  float fmax[NT / 64], fsum[NT / 64];
+  int scan_tmp[NT / 64];
+  uint32_t kmax[NT];  // per-thread maximum key
 };
 
-// Block sum with one barrier: alternate halves of sh.red by `parity`.
-__device__ __forceinline__ int block_sum(int v, SelShared &sh, int &parity) {
-  v = wave_sum_i32(v);
-  if ((threadIdx.x & 63) == 0) sh.red[parity][threadIdx.x >> 6] = v;
+template <int NT> __device__ void sel_init(SelSh<NT> &sh) {
+  if (threadIdx.x == 0) {
+    sh.cnt[0] = sh.cnt[1] = sh.cnt[2] = 0;
+    sh.ncand = sh.nsel = 0;
+    sh.band[0] = sh.band[1] = 0xffffffffu;
+    sh.bor[0] = sh.bor[1] = 0u;
+  }
   __syncthreads();
-  int t = 0;
-#pragma unroll
-  for (int w = 0; w < kSelWaves; ++w) t += sh.red[parity][w];
-  parity ^= 1;
-  return t;
 }
 
-// Keys of one row, split over the block in index order: thread t owns the
-// contiguous range [base, base + cnt).  RegKeys holds up to KPT keys per
-// thread in registers; MemKeys re-reads them from memory (rows longer than
-// KPT * 1024).
-template <int KPT> struct RegKeys {
+// Sources of composites, strided over the block: thread t owns entries
+// t, t + NT, t + 2 NT, ...  each(f) calls f(composite) for the thread's own.
+// RegKeys holds a row's keys in registers (n <= NT * KPT), MemKeys re-reads
+// them, LdsComps walks composites already in LDS.
+template <int NT, int KPT> struct RegKeys {
   uint32_t v[KPT];
-  int base, cnt;
-  __device__ void load(const uint32_t *p, int n) {
-    base = threadIdx.x * KPT;
-    cnt = max(0, min(KPT, n - base));
+  int n;
+  __device__ void load(const uint32_t *p, int n_) {
+    n = n_;
 #pragma unroll
-    for (int i = 0; i < KPT; ++i) v[i] = i < cnt ? p[base + i] : 0u;
+    for (int i = 0; i < KPT; ++i) {
+      const int idx = threadIdx.x + i * NT;
+      v[i] = idx < n ? p[idx] : 0u;
+    }
   }
   template <typename F> __device__ void each(F &&f) const {
 #pragma unroll
-    for (int i = 0; i < KPT; ++i)
-      if (i < cnt) f(v[i], base + i);
+    for (int i = 0; i < KPT; ++i) {
+      const int idx = threadIdx.x + i * NT;
+      if (idx < n) f(comp_of(v[i], idx));
+    }
   }
 };
 
-struct MemKeys {
+template <int NT> struct MemKeys {
   const uint32_t *p;
-  int base, cnt;
-  __device__ void load(const uint32_t *src, int n) {
-    const int per = (n + kSelThreads - 1) / kSelThreads;
+  int n;
+  __device__ void load(const uint32_t *src, int n_) {
     p = src;
-    base = threadIdx.x * per;
-    cnt = max(0, min(per, n - base));
+    n = n_;
   }
   template <typename F> __device__ void each(F &&f) const {
-    for (int i = 0; i < cnt; ++i) f(p[base + i], base + i);
+    for (int idx = threadIdx.x; idx < n; idx += NT) f(comp_of(p[idx], idx));
   }
 };
 
-// k-th largest key T of the row and the number of keys > T.  Bits equal in
-// every key are taken as they are; each varying bit, from the top, is
-// decided by one block-wide count of keys >= the candidate threshold.
-template <typename K>
-__device__ uint32_t kth_largest(const K &rk, int k, SelShared &sh, int &parity, int &gt) {
-  uint32_t a = 0xffffffffu, o = 0u;
-  rk.each([&](uint32_t key, int) { a &= key; o |= key; });
+template <int NT> struct LdsComps {
+  const uint64_t *c;
+  int n;
+  template <typename F> __device__ void each(F &&f) const {
+    for (int i = threadIdx.x; i < n; i += NT) f(c[i]);
+  }
+};
+
+__device__ __forceinline__ void wave_and_or64(uint64_t &a, uint64_t &o) {
+  uint32_t al = (uint32_t)a, ah = (uint32_t)(a >> 32), ol = (uint32_t)o, oh = (uint32_t)(o >> 32);
 #pragma unroll
   for (int m = 32; m >= 1; m >>= 1) {
-    a &= __shfl_xor(a, m, 64);
-    o |= __shfl_xor(o, m, 64);
+    al &= __shfl_xor(al, m, 64);
+    ah &= __shfl_xor(ah, m, 64);
+    ol |= __shfl_xor(ol, m, 64);
+    oh |= __shfl_xor(oh, m, 64);
   }
-  if ((threadIdx.x & 63) == 0) {
-    sh.band[threadIdx.x >> 6] = a;
-    sh.bor[threadIdx.x >> 6] = o;
-  }
-  __syncthreads();
-  a = 0xffffffffu;
-  o = 0u;
+  a = ((uint64_t)ah << 32) | al;
+  o = ((uint64_t)oh << 32) | ol;
+}
+
+// k-th largest of a set of distinct nonzero composites (1 <= k <= size).
+// Bits are decided from the top in three passes (63..48, 47..32, 31..0);
+// each pass first takes the bits shared by every value that matches the
+// prefix decided so far, then decides each varying bit with one count of
+// values >= the candidate.  A pass whose prefix group has one value costs
+// no counts.  count(c) = #values >= c; and_or(mask, prefix, a, o) = AND and
+// OR of the values v with (v & mask) == prefix.
+template <typename CountF, typename AndOrF>
+__device__ uint64_t kth_search(int k, CountF &&count, AndOrF &&and_or) {
+  uint64_t ans = 0, fixed = 0;
 #pragma unroll
-  for (int w = 0; w < kSelWaves; ++w) {
-    a &= sh.band[w];
-    o |= sh.bor[w];
+  for (int pass = 0; pass < 3; ++pass) {
+    const uint64_t part = pass == 0 ? 0xffff000000000000ull : pass == 1 ? 0x0000ffff00000000ull
+                                                                        : 0x00000000ffffffffull;
+    uint64_t a, o;
+    and_or(fixed, ans, a, o);
+    ans |= a & part;
+    uint64_t var = (a ^ o) & part;
+    while (var) {
+      const uint64_t bit = 1ull << (63 - __clzll(var));
+      var &= ~bit;
+      if (count(ans | bit) >= k) ans |= bit;
+    }
+    fixed |= part;
   }
-  uint32_t ans = a, var = a ^ o;
-  while (var) {
-    const int bit = 31 - __clz(var);
-    var &= ~(1u << bit);
-    const uint32_t cand = ans | (1u << bit);
-    int local = 0;
-    rk.each([&](uint32_t key, int) { local += key >= cand; });
-    if (block_sum(local, sh, parity) >= k) ans = cand;
-  }
-  int local = 0;
-  rk.each([&](uint32_t key, int) { local += key > ans; });
-  gt = block_sum(local, sh, parity);
   return ans;
 }
 
-// Calls f(key, index) for the top k: every key > T and the first need_eq
-// keys == T in index order (ranks of equal keys from one block scan).
-template <typename K, typename F>
-__device__ void each_selected(const K &rk, uint32_t T, int need_eq, SelShared &sh, F &&f) {
-  int eq = 0;
-  rk.each([&](uint32_t key, int) { eq += key == T; });
-  int rank = block_incl_scan<kSelThreads>(eq, sh.scan_tmp, nullptr) - eq;
-  rk.each([&](uint32_t key, int idx) {
-    if (key > T) f(key, idx);
-    else if (key == T) {
-      if (rank < need_eq) f(key, idx);
-      ++rank;
+// Up to 64*V composites held by one wave (lane l: entries l, l + 64, ...);
+// zero marks an empty entry.
+template <int V> struct WaveVals {
+  uint64_t v[V];
+  __device__ void load(const uint64_t *src, int n) {
+    const int lane = threadIdx.x & 63;
+#pragma unroll
+    for (int i = 0; i < V; ++i) v[i] = lane + 64 * i < n ? src[lane + 64 * i] : 0ull;
+  }
+  __device__ int count_ge(uint64_t c) const {
+    int l = 0;
+#pragma unroll
+    for (int i = 0; i < V; ++i) l += v[i] >= c;
+    return wave_sum_i32(l);
+  }
+  __device__ void and_or(uint64_t mask, uint64_t prefix, uint64_t &a, uint64_t &o) const {
+    a = ~0ull;
+    o = 0ull;
+#pragma unroll
+    for (int i = 0; i < V; ++i)
+      if (v[i] && (v[i] & mask) == prefix) {
+        a &= v[i];
+        o |= v[i];
+      }
+    wave_and_or64(a, o);
+  }
+  __device__ uint64_t kth(int k) const {
+    return kth_search(k, [&](uint64_t c) { return count_ge(c); },
+                      [&](uint64_t m, uint64_t p, uint64_t &a, uint64_t &o) { and_or(m, p, a, o); });
+  }
+};
+
+// Up to 64*V 32-bit keys held by one wave; zero marks an empty entry.
+// kth(k) = the k-th largest key of the multiset (same search over bits
+// 31..16, then 15..0).
+template <int V> struct WaveKeys {
+  uint32_t v[V];
+  __device__ void load(const uint32_t *src, int n) {
+    const int lane = threadIdx.x & 63;
+#pragma unroll
+    for (int i = 0; i < V; ++i) v[i] = lane + 64 * i < n ? src[lane + 64 * i] : 0u;
+  }
+  __device__ uint32_t kth(int k) const {
+    uint32_t ans = 0, fixed = 0;
+#pragma unroll
+    for (int pass = 0; pass < 2; ++pass) {
+      const uint32_t part = pass == 0 ? 0xffff0000u : 0x0000ffffu;
+      uint32_t a = ~0u, o = 0u;
+#pragma unroll
+      for (int i = 0; i < V; ++i)
+        if (v[i] && (v[i] & fixed) == ans) {
+          a &= v[i];
+          o |= v[i];
+        }
+#pragma unroll
+      for (int m = 32; m >= 1; m >>= 1) {
+        a &= __shfl_xor(a, m, 64);
+        o |= __shfl_xor(o, m, 64);
+      }
+      ans |= a & part;
+      uint32_t var = (a ^ o) & part;
+      while (var) {
+        const uint32_t bit = 1u << (31 - __clz(var));
+        var &= ~bit;
+        int l = 0;
+#pragma unroll
+        for (int i = 0; i < V; ++i) l += v[i] >= (ans | bit);
+        if (wave_sum_i32(l) >= k) ans |= bit;
+      }
+      fixed |= part;
+    }
+    return ans;
+  }
+};
+
+// Block-wide count of composites >= c: wave sums, one LDS atomic per wave,
+// one barrier.  Three counters rotate so a counter is cleared two counts
+// before it is reused.
+template <int NT, typename Src>
+__device__ int block_count_ge(const Src &src, uint64_t c, SelSh<NT> &sh, int &slot) {
+  int local = 0;
+  src.each([&](uint64_t x) { local += x >= c; });
+  local = wave_sum_i32(local);
+  const int next = slot == 2 ? 0 : slot + 1;
+  if ((threadIdx.x & 63) == 0) atomicAdd(&sh.cnt[slot], local);
+  if (threadIdx.x == 0) sh.cnt[next] = 0;
+  __syncthreads();
+  const int total = sh.cnt[slot];
+  slot = next;
+  return total;
+}
+
+template <int NT, typename Src>
+__device__ void block_and_or(const Src &src, uint64_t mask, uint64_t prefix, SelSh<NT> &sh, uint64_t &a,
+                             uint64_t &o) {
+  a = ~0ull;
+  o = 0ull;
+  src.each([&](uint64_t x) {
+    if ((x & mask) == prefix) {
+      a &= x;
+      o |= x;
+    }
+  });
+  wave_and_or64(a, o);
+  if ((threadIdx.x & 63) == 0) {
+    atomicAnd(&sh.band[0], (uint32_t)a);
+    atomicAnd(&sh.band[1], (uint32_t)(a >> 32));
+    atomicOr(&sh.bor[0], (uint32_t)o);
+    atomicOr(&sh.bor[1], (uint32_t)(o >> 32));
+  }
+  __syncthreads();
+  a = ((uint64_t)sh.band[1] << 32) | sh.band[0];
+  o = ((uint64_t)sh.bor[1] << 32) | sh.bor[0];
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    sh.band[0] = sh.band[1] = 0xffffffffu;
+    sh.bor[0] = sh.bor[1] = 0u;
+  }
+  __syncthreads();
+}
+
+template <int NT, typename Src> __device__ uint64_t block_kth(const Src &src, int k, SelSh<NT> &sh) {
+  int slot = 0;
+  return kth_search(k, [&](uint64_t c) { return block_count_ge<NT>(src, c, sh, slot); },
+                    [&](uint64_t m, uint64_t p, uint64_t &a, uint64_t &o) { block_and_or<NT>(src, m, p, sh, a, o); });
+}
+
+// Appends the thread's composites satisfying pred to out[*counter ...]
+// (entries past cap are counted, not written).  One LDS atomic per wave;
+// the caller synchronises before reading *counter.
+template <int NT, typename Src, typename P>
+__device__ void block_compact(const Src &src, P &&pred, uint64_t *out, int cap, int *counter) {
+  int c = 0;
+  src.each([&](uint64_t x) { c += pred(x) ? 1 : 0; });
+  const int lane = threadIdx.x & 63;
+  int incl = c;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int t = __shfl_up(incl, o, 64);
+    if (lane >= o) incl += t;
+  }
+  int base = 0;
+  if (lane == 63) base = atomicAdd(counter, incl);
+  int pos = __shfl(base, 63, 64) + incl - c;
+  src.each([&](uint64_t x) {
+    if (pred(x)) {
+      if (pos < cap) out[pos] = x;
+      ++pos;
     }
   });
 }
 
-// Block-wide max / sum of the key values (telemetry), in every thread.
-template <typename K>
-__device__ void row_stats(const K &rk, SelShared &sh, float &mx, float &sum) {
-  float m = -INFINITY, t = 0.f;
-  rk.each([&](uint32_t key, int) {
-    const float f = key_to_float(key);
-    m = fmaxf(m, f);
-    t += f;
+// Top k of a row (1 <= k <= n): calls finish(s, T) once, where T is the
+// k-th largest composite and s a source holding every composite >= T (the
+// LDS candidates, or the row itself).  Also leaves the row's max and sum of
+// key values (as floats) in every thread.
+//  1. The k-th largest of the per-thread maximum keys, K0, bounds T from
+//     below (the k threads reaching it own k distinct composites with key
+//     >= K0); one wave finds it.
+//  2. The composites with key >= K0 go to cand[] in LDS (without ties at
+//     K0 at most k * keys per thread).
+//  3. T is the k-th largest candidate: found by one wave from registers when
+//     they fit, else by the block over LDS, else (more than kCandCap) by the
+//     block over the row.  The row's registers are dead on the first two
+//     paths.
+template <int NT, typename Src, typename Fin>
+__device__ void topk_select(const Src &src, int k, SelSh<NT> &sh, uint64_t *cand, float &mx, float &sum,
+                            Fin &&finish) {
+  const int tid = threadIdx.x, wave = tid >> 6;
+  uint32_t m = 0;
+  float fm = -INFINITY, fs = 0.f;
+  src.each([&](uint64_t x) {
+    m = max(m, comp_key(x));
+    const float f = key_to_float(comp_key(x));
+    fm = fmaxf(fm, f);
+    fs += f;
   });
-  m = wave_max(m);
-  t = wave_sum(t);
-  if ((threadIdx.x & 63) == 0) {
-    sh.fmax[threadIdx.x >> 6] = m;
-    sh.fsum[threadIdx.x >> 6] = t;
+  sh.kmax[tid] = m;
+  fm = wave_max(fm);
+  fs = wave_sum(fs);
+  if ((tid & 63) == 0) {
+    sh.fmax[wave] = fm;
+    sh.fsum[wave] = fs;
   }
   __syncthreads();
   mx = sh.fmax[0];
   sum = 0.f;
-  for (int w = 0; w < kSelWaves; ++w) {
+#pragma unroll
+  for (int w = 0; w < NT / 64; ++w) {
     mx = fmaxf(mx, sh.fmax[w]);
     sum += sh.fsum[w];
+  }
+  if (k <= NT) {
+    if (wave == 0) {
+      WaveKeys<NT / 64> wk;
+      wk.load(sh.kmax, NT);
+      const uint64_t b = (uint64_t)wk.kth(k) << 32;
+      if (tid == 0) sh.bound = b;
+    }
+  } else if (tid == 0) {
+    sh.bound = 1;  // every composite
+  }
+  __syncthreads();
+  const uint64_t bound = sh.bound;
+  block_compact<NT>(src, [bound](uint64_t x) { return x >= bound; }, cand, kCandCap, &sh.ncand);
+  __syncthreads();
+  const int C = sh.ncand;
+  if (C <= kCandCap) {
+    const LdsComps<NT> lc{cand, C};
+    uint64_t T;
+    if (C <= kWaveCap) {
+      if (wave == 0) {
+        WaveVals<kWaveCap / 64> wv;
+        wv.load(cand, C);
+        const uint64_t t = wv.kth(k);
+        if (tid == 0) sh.thresh = t;
+      }
+      __syncthreads();
+      T = sh.thresh;
+    } else {
+      T = block_kth<NT>(lc, k, sh);
+    }
+    finish(lc, T);
+  } else {
+    finish(src, block_kth<NT>(src, k, sh));
   }
 }
 
-// Max and sum over `count` (max, sum) pairs written by other blocks, read
-// in parallel with coherent loads and reduced across the block.  Every
-// thread of the block must call; the result is valid in every thread.
-__device__ void merge_row_stats(float *buf, int count, SelShared &sh, float &mx, double &sum) {
-  float m = -INFINITY, t = 0.f;
-  for (int r = threadIdx.x; r < count; r += kSelThreads) {
-    m = fmaxf(m, coherent_load_f32(&buf[2 * r]));
-    t += coherent_load_f32(&buf[2 * r + 1]);
+// -------------------------------------------------------- union ranking
+// Copies the page bitmap into LDS and writes rank[w] = set bits in words
+// before w (rank[W] = union size).  Returns the union size.
+template <int NT>
+__device__ int rank_union(const uint32_t *bitmap, int words, uint32_t *bits, int *rank, int *scan_tmp) {
+  int before = 0;
+  for (int base = 0; base < words; base += NT) {
+    const int w = base + threadIdx.x;
+    const uint32_t x = w < words ? bitmap[w] : 0u;
+    const int c = __popc(x);
+    int tot = 0;
+    const int incl = block_incl_scan<NT>(c, scan_tmp, &tot);
+    if (w < words) {
+      bits[w] = x;
+      rank[w] = before + incl - c;
+    }
+    before += tot;
   }
-  m = wave_max(m);
-  t = wave_sum(t);
+  if (threadIdx.x == 0) rank[words] = before;
   __syncthreads();
-  if ((threadIdx.x & 63) == 0) {
-    sh.fmax[threadIdx.x >> 6] = m;
-    sh.fsum[threadIdx.x >> 6] = t;
+  return before;
+}
+
+// Page id of the v-th union member (v < union size).
+__device__ __forceinline__ int union_page(const uint32_t *bits, const int *rank, int words, int v) {
+  int lo = 0, hi = words - 1;
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if (rank[mid] <= v) lo = mid;
+    else hi = mid - 1;
   }
-  __syncthreads();
-  mx = -INFINITY;
-  sum = 0.0;
-  for (int w = 0; w < kSelWaves; ++w) {
-    mx = fmaxf(mx, sh.fmax[w]);
-    sum += sh.fsum[w];
-  }
+  uint32_t x = bits[lo];
+  for (int r = v - rank[lo]; r > 0; --r) x &= x - 1;
+  return lo * 32 + __ffs(x) - 1;
 }
 
 // ------------------------------------------------------------ coarse scan
@@ -202,7 +435,7 @@ __global__ void __launch_bounds__(kScanThreads) coarse_scan_kernel(
   constexpr int NSLOT = kScanThreads / LG;
   constexpr int UT = 4;  // units in flight per lane group
   extern __shared__ uint4 smem4[];
-  char *qraw = reinterpret_cast<char *>(smem4);                                  // [rows][D]
+  char *qraw = reinterpret_cast<char *>(smem4);                                      // [rows][D]
   uint32_t *sk = reinterpret_cast<uint32_t *>(qraw + (size_t)rows * head_dim * EB);  // [rows][ppw]
   const int G = hq / hkv, GQ = G * qlen, cpr = head_dim / VEC;
   const int tid = threadIdx.x;
@@ -249,86 +482,41 @@ __global__ void __launch_bounds__(kScanThreads) coarse_scan_kernel(
 }
 
 // --------------------------------------------------------- coarse select
-// One block per query row: its top-k pages go into the shared page bitmap.
-// The last block to finish compacts the bitmap into the ascending union
-// list, writes U, clears the bitmap and the counter, and records the coarse
-// telemetry (max score over rows, mean over all scores).
-template <typename K>
-__device__ void coarse_pick(const K &rk, int k, uint32_t *bitmap, SelShared &sh, float &mx, float &sum) {
-  row_stats(rk, sh, mx, sum);
-  int parity = 0, gt = 0;
-  const uint32_t T = kth_largest(rk, k, sh, parity, gt);
-  each_selected(rk, T, k - gt, sh, [&](uint32_t, int i) { atomicOr(&bitmap[i >> 5], 1u << (i & 31)); });
+// One block per query row: the row's top-k pages are ORed into the page
+// bitmap and the row's (max, sum) score stay for the telemetry.
+template <int NT, typename Src>
+__device__ void coarse_pick(const Src &src, int k, uint32_t *bitmap, SelSh<NT> &sh, uint64_t *cand,
+                            float *stats, int row) {
+  float mx, sum;
+  topk_select<NT>(src, k, sh, cand, mx, sum, [&](const auto &s2, uint64_t T) {
+    s2.each([&](uint64_t x) {
+      if (x >= T) {
+        const int i = comp_index(x);
+        atomicOr(&bitmap[i >> 5], 1u << (i & 31));
+      }
+    });
+  });
+  if (threadIdx.x == 0) {
+    stats[2 * row] = mx;
+    stats[2 * row + 1] = sum;
+  }
 }
 
-template <int DT, int KPT>
-__global__ void __launch_bounds__(kSelThreads) coarse_select_kernel(
-    const uint32_t *__restrict__ keys, int64_t ld, int n, int k, int rows, uint32_t *bitmap,
-    int32_t *page_list, int32_t *counters, float *row_stats_buf, int round, int32_t *pages_out,
-    int32_t *union_out, float *stats_out, double *stats_accum) {
-  __shared__ SelShared sh;
-  const int tid = threadIdx.x, row = blockIdx.x;
-  const uint32_t *src = keys + (int64_t)row * ld;
-  float mx, sum;
-  if (n <= KPT * kSelThreads) {
-    RegKeys<KPT> rk;
+template <int NT, int KPT>
+__global__ void __launch_bounds__(NT) coarse_select_kernel(const uint32_t *__restrict__ keys, int64_t ld, int n,
+                                                            int k, uint32_t *bitmap, float *coarse_stats) {
+  __shared__ SelSh<NT> sh;
+  __shared__ uint64_t cand[kCandCap];
+  sel_init(sh);
+  const uint32_t *src = keys + (int64_t)blockIdx.x * ld;
+  if (KPT > 0) {
+    RegKeys<NT, (KPT > 0 ? KPT : 1)> rk;
     rk.load(src, n);
-    coarse_pick(rk, k, bitmap, sh, mx, sum);
+    coarse_pick<NT>(rk, k, bitmap, sh, cand, coarse_stats, blockIdx.x);
   } else {
-    MemKeys rk;
-    rk.load(src, n);
-    coarse_pick(rk, k, bitmap, sh, mx, sum);
-  }
-  if (tid == 0) {
-    coherent_store_f32(&row_stats_buf[2 * row], mx);
-    coherent_store_f32(&row_stats_buf[2 * row + 1], sum);
-  }
-  // Every wave completes its own bitmap updates before the block signals.
-  __threadfence();
-  __syncthreads();
-  if (tid == 0) {
-    __threadfence();
-    sh.is_last = atomic_add_acq_rel(&counters[1], 1) == rows - 1;
-  }
-  __syncthreads();
-  if (!sh.is_last) return;
-  __threadfence();
-  // Compact the bitmap: thread t owns words [w0, w1).
-  const int words = (n + 31) >> 5;
-  const int per = (words + kSelThreads - 1) / kSelThreads;
-  const int w0 = min(words, tid * per), w1 = min(words, w0 + per);
-  int cnt = 0;
-  for (int w = w0; w < w1; ++w) cnt += __popc(coherent_load_u32(&bitmap[w]));
-  int total = 0;
-  int pos = block_incl_scan<kSelThreads>(cnt, sh.scan_tmp, &total) - cnt;
-  for (int w = w0; w < w1; ++w) {
-    uint32_t bits = coherent_load_u32(&bitmap[w]);
-    coherent_store_u32(&bitmap[w], 0u);
-    while (bits) {
-      const int page = w * 32 + __ffs(bits) - 1;
-      bits &= bits - 1;
-      page_list[pos] = page;
-      if (pages_out) pages_out[pos] = page;
-      ++pos;
-    }
-  }
-  float m;
-  double t;
-  merge_row_stats(row_stats_buf, rows, sh, m, t);
-  if (tid == 0) {
-    counters[0] = total;
-    counters[1] = 0;
-    if (union_out) union_out[0] = total;
-    float mean = (float)(t / ((double)rows * (double)n));
-    if (round) mean = round_act<DT>(mean);
-    if (stats_out) {
-      stats_out[0] = m;
-      stats_out[1] = mean;
-    }
-    if (stats_accum) {
-      stats_accum[0] += (double)m;
-      stats_accum[1] += (double)mean;
-    }
+    MemKeys<NT> mk;
+    mk.load(src, n);
+    coarse_pick<NT>(mk, k, bitmap, sh, cand, coarse_stats, blockIdx.x);
   }
 }
 
@@ -336,24 +524,28 @@ __global__ void __launch_bounds__(kSelThreads) coarse_select_kernel(
 // Grid (nb, B*Hkv): block (x, r) keeps the G*Q query rows that read kv row
 // r = b*Hkv + h in LDS and walks work items x, x + nb, ...; an item is a
 // slice of `tpi` tokens of a union page (items [0, U*nsplit)) or of the
-// partial page (the items after).  Each lane group scores UT tokens at a
-// time; the max over the block's rows is folded into the candidate's key
-// with atomicMax, which completes the max over kv heads across blocks
-// (keys are order-preserving, and the select kernel leaves them zeroed).
+// partial page (the items after).  Union pages come from the bitmap
+// (ranked in LDS) or from the stored union list.  Each lane group scores UT
+// tokens at a time; the max over the block's rows is folded into the
+// candidate's key with atomicMax, which completes the max over kv heads
+// across blocks (keys are order-preserving; the select zeroes them).
 template <int DT, int LG>
 __global__ void __launch_bounds__(256) fine_scan_kernel(
-    const int32_t *__restrict__ page_list, const int32_t *__restrict__ counters, int has_pages,
-    const uint64_t *__restrict__ ktab, int chunk_shift, int64_t page_bytes, const char *__restrict__ part_k,
-    int partial_len, int page_size, int tpi, int hkv, int head_dim, const char *__restrict__ q, int64_t qs0,
-    int64_t qs1, int64_t qs2, int hq, int qlen, float scale, int round, uint32_t *__restrict__ out,
-    int64_t ld) {
+    int union_src, const uint32_t *__restrict__ bitmap, int words, const int32_t *__restrict__ page_list,
+    const int32_t *__restrict__ counters, const uint64_t *__restrict__ ktab, int chunk_shift, int64_t page_bytes,
+    const char *__restrict__ part_k, int partial_len, int page_size, int tpi, int hkv, int head_dim,
+    const char *__restrict__ q, int64_t qs0, int64_t qs1, int64_t qs2, int hq, int qlen, float scale, int round,
+    uint32_t *__restrict__ out, int64_t ld) {
   constexpr int VEC = Elem<DT>::VEC, EB = Elem<DT>::BYTES;
   constexpr int UT = 4;
   constexpr int NSLOT = 256 / LG;
   extern __shared__ uint4 smem4[];
-  char *qraw = reinterpret_cast<char *>(smem4);  // [G*Q][D] dtype
+  __shared__ int scan_tmp[4];
   const int r = blockIdx.y, b = r / hkv, kvh = r % hkv;
   const int G = hq / hkv, GQ = G * qlen, cpr = head_dim / VEC;
+  char *qraw = reinterpret_cast<char *>(smem4);  // [G*Q][D] dtype
+  uint32_t *ubits = reinterpret_cast<uint32_t *>(qraw + (size_t)GQ * head_dim * EB);
+  int *urank = reinterpret_cast<int *>(ubits + words);
   const int tid = threadIdx.x;
   for (int i = tid; i < GQ * cpr; i += 256) {
     const int j = i / cpr, c = i % cpr;
@@ -361,8 +553,10 @@ __global__ void __launch_bounds__(256) fine_scan_kernel(
     *reinterpret_cast<uint4 *>(qraw + ((size_t)j * head_dim + c * VEC) * EB) =
         load16(q + ((int64_t)b * qs0 + (int64_t)h * qs1 + (int64_t)qp * qs2 + c * VEC) * EB);
   }
+  int U = 0;
+  if (union_src == UNION_BITMAP) U = rank_union<256>(bitmap, words, ubits, urank, scan_tmp);
+  else if (union_src == UNION_LIST) U = counters[0];
   __syncthreads();
-  const int U = has_pages ? counters[0] : 0;
   const int nsplit = (page_size + tpi - 1) / tpi;
   const int page_items = U * nsplit;
   const int items = page_items + (partial_len + tpi - 1) / tpi;
@@ -375,7 +569,7 @@ __global__ void __launch_bounds__(256) fine_scan_kernel(
     int ntok;
     if (item < page_items) {
       const int v = item / nsplit, s = item % nsplit;
-      const int64_t page = page_list[v];
+      const int64_t page = union_src == UNION_BITMAP ? union_page(ubits, urank, words, v) : page_list[v];
       rowbase = reinterpret_cast<const char *>(ktab[page >> chunk_shift]) +
                 (page & ((int64_t(1) << chunk_shift) - 1)) * page_bytes +
                 ((int64_t)r * page_size + (int64_t)s * tpi) * row_bytes;
@@ -414,115 +608,180 @@ __global__ void __launch_bounds__(256) fine_scan_kernel(
 // ----------------------------------------------------------- fine select
 // One block per batch row: top-P' of the C candidate keys, sorted by score
 // descending (ties: lower candidate index first).  Writes the candidate
-// index per output slot, the global token id, P' and the fine telemetry
-// (max over rows, mean over all keys; combined by the last block), and
-// zeroes the keys for the next scan.
-template <typename K>
-__device__ void fine_pick(const K &rk, int k, unsigned long long *ent, SelShared &sh, float &mx, float &sum) {
-  row_stats(rk, sh, mx, sum);
-  int parity = 0, gt = 0;
-  const uint32_t T = kth_largest(rk, k, sh, parity, gt);
-  // Selected entries in index order: positions from a block scan.
-  const int need = k - gt;
-  int mine = 0;
-  each_selected(rk, T, need, sh, [&](uint32_t, int) { ++mine; });
-  int pos = block_incl_scan<kSelThreads>(mine, sh.scan_tmp, nullptr) - mine;
-  each_selected(rk, T, need, sh, [&](uint32_t key, int i) {
-    ent[pos++] = ((unsigned long long)key << 32) | (unsigned long long)(0xffffffffu - (uint32_t)i);
+// index per output slot, the global token id and the row's telemetry
+// (max, sum), and zeroes the keys for the next scan.  Block 0 also writes
+// P', and with a fresh union the compact union list, its size and the
+// coarse telemetry.
+template <typename Src>
+__device__ void fine_pick(const Src &src, int k, SelSh<kFineSelThreads> &sh, uint64_t *cand, uint64_t *sel,
+                          float &mx, float &sum) {
+  constexpr int NT = kFineSelThreads;
+  topk_select<NT>(src, k, sh, cand, mx, sum, [&](const auto &s2, uint64_t T) {
+    block_compact<NT>(s2, [T](uint64_t x) { return x >= T; }, sel, k, &sh.nsel);
   });
 }
 
+// Dynamic LDS: ubits[words] | urank[words + 1] | (8-aligned) cand[kCandCap] | sel[kp2].
 template <int DT, int KPT>
-__global__ void __launch_bounds__(kSelThreads) fine_select_kernel(
-    uint32_t *__restrict__ keys, int64_t ld, int32_t *counters, int has_pages, int page_size,
-    int partial_len, int64_t num_finalized, const int32_t *__restrict__ page_list, int width,
-    int batch, int round, float *row_stats_buf, int32_t *__restrict__ sel_cand, int64_t *__restrict__ idx_out,
+__global__ void __launch_bounds__(kFineSelThreads) fine_select_kernel(
+    uint32_t *__restrict__ keys, int64_t ld, int union_src, const uint32_t *__restrict__ bitmap, int words,
+    int32_t *page_list, int32_t *counters, int page_size, int partial_len, int64_t num_finalized, int width,
+    int round, const float *__restrict__ coarse_stats, int rows, int n_pages, float *fine_stats,
+    int32_t *__restrict__ sel_cand, int64_t *__restrict__ idx_out, int32_t *pages_out, int32_t *union_out,
     float *stats_out, double *stats_accum) {
-  __shared__ SelShared sh;
-  __shared__ unsigned long long ent[kMaxOut];
+  constexpr int NT = kFineSelThreads;
+  __shared__ SelSh<NT> sh;
+  extern __shared__ uint64_t fsm[];
   const int tid = threadIdx.x, b = blockIdx.x;
-  const int U = has_pages ? counters[0] : 0;
+  const int wpad = (2 * words + 2) & ~1;  // 32-bit slots of ubits + urank, even
+  uint32_t *ubits = reinterpret_cast<uint32_t *>(fsm);
+  int *urank = reinterpret_cast<int *>(ubits + words);
+  uint64_t *cand = fsm + wpad / 2;
+  uint64_t *sel = cand + kCandCap;
+  sel_init(sh);
+  int U = 0;
+  if (union_src == UNION_BITMAP) U = rank_union<NT>(bitmap, words, ubits, urank, sh.scan_tmp);
+  else if (union_src == UNION_LIST) U = counters[0];
   const int n = U * page_size + partial_len;
   const int k = min(width, n);
   uint32_t *src = keys + (int64_t)b * ld;
   float mx, sum;
-  if (n <= KPT * kSelThreads) {
-    RegKeys<KPT> rk;
+  if (KPT > 0) {
+    RegKeys<NT, (KPT > 0 ? KPT : 1)> rk;
     rk.load(src, n);
-    fine_pick(rk, k, ent, sh, mx, sum);
+    // The scan accumulates with atomicMax: leave the row zeroed for the next call.
+    for (int i = tid; i < n; i += NT) src[i] = 0u;
+    fine_pick(rk, k, sh, cand, sel, mx, sum);
   } else {
-    MemKeys rk;
-    rk.load(src, n);
-    fine_pick(rk, k, ent, sh, mx, sum);
-  }
-  int kp2 = 1;
-  while (kp2 < k) kp2 <<= 1;
-  for (int i = k + tid; i < kp2; i += kSelThreads) ent[i] = 0ull;
-  __syncthreads();
-  // Bitonic sort, descending.
-  for (int size = 2; size <= kp2; size <<= 1) {
-    for (int stride = size >> 1; stride > 0; stride >>= 1) {
-      for (int t = tid; t < kp2 / 2; t += kSelThreads) {
-        const int i = 2 * stride * (t / stride) + (t % stride), j = i + stride;
-        const bool desc = (i & size) == 0;
-        const unsigned long long x = ent[i], y = ent[j];
-        if ((x < y) == desc) {
-          ent[i] = y;
-          ent[j] = x;
-        }
-      }
-      __syncthreads();
-    }
-  }
-  // The scan accumulates with atomicMax: leave the row zeroed for the next call.
-  for (int i = tid; i < n; i += kSelThreads) src[i] = 0u;
-  const int64_t split = (int64_t)U * page_size;
-  for (int j = tid; j < k; j += kSelThreads) {
-    const uint32_t cand = 0xffffffffu - (uint32_t)(ent[j] & 0xffffffffull);
-    sel_cand[(int64_t)b * width + j] = (int32_t)cand;
-    if (idx_out) {
-      int64_t gid;
-      if ((int64_t)cand < split) gid = (int64_t)page_list[cand / page_size] * page_size + cand % page_size;
-      else gid = num_finalized + ((int64_t)cand - split);
-      idx_out[(int64_t)b * width + j] = gid;
-    }
+    MemKeys<NT> mk;
+    mk.load(src, n);
+    fine_pick(mk, k, sh, cand, sel, mx, sum);
+    __syncthreads();
+    for (int i = tid; i < n; i += NT) src[i] = 0u;
   }
   if (tid == 0) {
-    coherent_store_f32(&row_stats_buf[2 * b], mx);
-    coherent_store_f32(&row_stats_buf[2 * b + 1], sum);
-    __threadfence();
-    sh.is_last = atomic_add_acq_rel(&counters[2], 1) == batch - 1;
+    fine_stats[2 * b] = mx;
+    fine_stats[2 * b + 1] = sum;
   }
   __syncthreads();
-  if (!sh.is_last) return;
-  __threadfence();
-  float m;
-  double t;
-  merge_row_stats(row_stats_buf, batch, sh, m, t);
-  if (tid != 0) return;
-  float mean = (float)(t / ((double)batch * (double)n));
-  if (round) mean = round_act<DT>(mean);
-  counters[2] = 0;
-  counters[3] = k;
-  if (stats_out) {
-    stats_out[2] = m;
-    stats_out[3] = mean;
+  // Order the k selected composites descending: by counting for k <= NT,
+  // else by a bitonic sort in place.
+  const int64_t split = (int64_t)U * page_size;
+  auto emit = [&](int slot, uint64_t x) {
+    const int cand_i = comp_index(x);
+    sel_cand[(int64_t)b * width + slot] = cand_i;
+    if (idx_out) {
+      int64_t gid;
+      if ((int64_t)cand_i < split) {
+        const int v = cand_i / page_size;
+        const int64_t page = union_src == UNION_BITMAP ? union_page(ubits, urank, words, v) : page_list[v];
+        gid = page * page_size + cand_i % page_size;
+      } else {
+        gid = num_finalized + ((int64_t)cand_i - split);
+      }
+      idx_out[(int64_t)b * width + slot] = gid;
+    }
+  };
+  if (k <= NT) {
+    if (tid < k) {
+      const uint64_t x = sel[tid];
+      int r = 0;
+      for (int j = 0; j < k; ++j) r += sel[j] > x;
+      emit(r, x);
+    }
+  } else {
+    int kp2 = 1;
+    while (kp2 < k) kp2 <<= 1;
+    for (int i = k + tid; i < kp2; i += NT) sel[i] = 0ull;
+    __syncthreads();
+    for (int size = 2; size <= kp2; size <<= 1) {
+      for (int stride = size >> 1; stride > 0; stride >>= 1) {
+        for (int t = tid; t < kp2 / 2; t += NT) {
+          const int i = 2 * stride * (t / stride) + (t % stride), j = i + stride;
+          const bool desc = (i & size) == 0;
+          const uint64_t x = sel[i], y = sel[j];
+          if ((x < y) == desc) {
+            sel[i] = y;
+            sel[j] = x;
+          }
+        }
+        __syncthreads();
+      }
+    }
+    for (int j = tid; j < k; j += NT) emit(j, sel[j]);
   }
-  if (stats_accum) {
-    stats_accum[2] += (double)m;
-    stats_accum[3] += (double)mean;
+  if (b != 0) return;
+  if (tid == 0) counters[3] = k;
+  if (union_src != UNION_BITMAP) return;
+  for (int v = tid; v < U; v += NT) {
+    const int page = union_page(ubits, urank, words, v);
+    page_list[v] = page;
+    if (pages_out) pages_out[v] = page;
   }
+  if (tid == 0) {
+    counters[0] = U;
+    if (union_out) union_out[0] = U;
+    float m = -INFINITY;
+    double t = 0.0;
+    for (int r = 0; r < rows; ++r) {
+      m = fmaxf(m, coarse_stats[2 * r]);
+      t += coarse_stats[2 * r + 1];
+    }
+    float mean = (float)(t / ((double)rows * (double)n_pages));
+    if (round) mean = round_act<DT>(mean);
+    if (stats_out) {
+      stats_out[0] = m;
+      stats_out[1] = mean;
+    }
+    if (stats_accum) {
+      stats_accum[0] += (double)m;
+      stats_accum[1] += (double)mean;
+    }
+  }
+}
+
+static size_t fine_select_lds(int words, int k) {
+  int kp2 = 1;
+  while (kp2 < k) kp2 <<= 1;
+  return (size_t)((2 * words + 2) & ~1) * 4 + (size_t)kCandCap * 8 + (size_t)kp2 * 8;
 }
 
 // ----------------------------------------------------------------- gather
 // k_out / v_out [B][Hkv][width][D] slot j <- candidate sel_cand[b][j] of kv
-// head h, from the arena (finished pages) or the partial page.
+// head h, from the arena (finished pages) or the partial page.  Block 0
+// also finishes the fine telemetry and clears the page bitmap.
+template <int DT>
 __global__ void __launch_bounds__(256) gather_kernel(
     const int32_t *__restrict__ sel_cand, const int32_t *__restrict__ counters, int has_pages,
     const int32_t *__restrict__ page_list, const uint64_t *__restrict__ ktab,
     const uint64_t *__restrict__ vtab, int chunk_shift, int64_t page_bytes, const char *__restrict__ part_k,
-    const char *__restrict__ part_v, int page_size, int batch, int hkv, int head_dim, int width, int cpr,
-    int vec, int eb, char *__restrict__ k_out, char *__restrict__ v_out) {
+    const char *__restrict__ part_v, int page_size, int partial_len, int batch, int hkv, int head_dim, int width,
+    int cpr, char *__restrict__ k_out, char *__restrict__ v_out, uint32_t *bitmap, int clear_words,
+    const float *__restrict__ fine_stats, int round, float *stats_out, double *stats_accum) {
+  constexpr int VEC = Elem<DT>::VEC, EB = Elem<DT>::BYTES;
+  const int U = has_pages ? counters[0] : 0;
+  if (blockIdx.x == 0) {
+    for (int w = threadIdx.x; w < clear_words; w += 256) bitmap[w] = 0u;
+    if (threadIdx.x == 0) {
+      const int n = U * page_size + partial_len;
+      float m = -INFINITY;
+      double t = 0.0;
+      for (int r = 0; r < batch; ++r) {
+        m = fmaxf(m, fine_stats[2 * r]);
+        t += fine_stats[2 * r + 1];
+      }
+      float mean = (float)(t / ((double)batch * (double)n));
+      if (round) mean = round_act<DT>(mean);
+      if (stats_out) {
+        stats_out[2] = m;
+        stats_out[3] = mean;
+      }
+      if (stats_accum) {
+        stats_accum[2] += (double)m;
+        stats_accum[3] += (double)mean;
+      }
+    }
+  }
   const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   const int c = (int)(idx % cpr);
   int64_t rest = idx / cpr;
@@ -533,36 +792,46 @@ __global__ void __launch_bounds__(256) gather_kernel(
   if (b >= batch) return;
   const int k = counters[3];
   if (j >= k) return;
-  const int U = has_pages ? counters[0] : 0;
   const int64_t cand = sel_cand[(int64_t)b * width + j];
   const int r = b * hkv + kvh;
-  const int64_t e0 = (int64_t)c * vec;
+  const int64_t e0 = (int64_t)c * VEC;
   const char *ks;
   const char *vs;
   if (cand < (int64_t)U * page_size) {
     const int64_t page = page_list[cand / page_size], t = cand % page_size;
     const int64_t off = (page & ((int64_t(1) << chunk_shift) - 1)) * page_bytes +
-                        (((int64_t)r * page_size + t) * head_dim + e0) * eb;
+                        (((int64_t)r * page_size + t) * head_dim + e0) * EB;
     ks = reinterpret_cast<const char *>(ktab[page >> chunk_shift]) + off;
     vs = reinterpret_cast<const char *>(vtab[page >> chunk_shift]) + off;
   } else {
     const int64_t t = cand - (int64_t)U * page_size;
-    const int64_t off = (((int64_t)r * page_size + t) * head_dim + e0) * eb;
+    const int64_t off = (((int64_t)r * page_size + t) * head_dim + e0) * EB;
     ks = part_k + off;
     vs = part_v + off;
   }
-  const int64_t o = (((int64_t)r * width + j) * head_dim + e0) * eb;
-  *reinterpret_cast<uint4 *>(k_out + o) = *reinterpret_cast<const uint4 *>(ks);
-  *reinterpret_cast<uint4 *>(v_out + o) = *reinterpret_cast<const uint4 *>(vs);
+  const int64_t o = (((int64_t)r * width + j) * head_dim + e0) * EB;
+  *reinterpret_cast<uint4 *>(k_out + o) = load16(ks);
+  *reinterpret_cast<uint4 *>(v_out + o) = load16(vs);
 }
 
-// Keys per thread the selects hold in registers; rows longer than 32 * 1024
-// keys take the memory-backed path (chosen on the device from the row length).
-template <typename F> static int with_kpt(int64_t n, F &&f) {
-  if (n <= 4 * kSelThreads) return f(std::integral_constant<int, 4>{});
-  if (n <= 8 * kSelThreads) return f(std::integral_constant<int, 8>{});
-  if (n <= 16 * kSelThreads) return f(std::integral_constant<int, 16>{});
-  return f(std::integral_constant<int, 32>{});
+// Block size and keys per thread of a select over a row of n keys (KPT 0:
+// the keys are re-read from memory).  At most 512 threads keep the keys in
+// registers: a 1024-thread block has 128 VGPRs per lane, too few next to
+// the wave-held candidates.
+template <typename F> static int with_sel_shape(int64_t n, F &&f) {
+  using std::integral_constant;
+  if (n <= 256 * 16) return f(integral_constant<int, 256>{}, integral_constant<int, 16>{});
+  if (n <= 512 * 16) return f(integral_constant<int, 512>{}, integral_constant<int, 16>{});
+  if (n <= 512 * 32) return f(integral_constant<int, 512>{}, integral_constant<int, 32>{});
+  return f(integral_constant<int, 1024>{}, integral_constant<int, 0>{});
+}
+
+// Keys per thread of the fine select for a row of n candidates.
+template <typename F> static int with_fine_kpt(int64_t n, F &&f) {
+  using std::integral_constant;
+  if (n <= kFineSelThreads * 16) return f(integral_constant<int, 16>{});
+  if (n <= kFineSelThreads * 32) return f(integral_constant<int, 32>{});
+  return f(integral_constant<int, 0>{});
 }
 
 }  // namespace kiv
@@ -603,28 +872,32 @@ int kiv_retrieve(kiv_store_t *s, const kiv_retrieve_args_t *a, kiv_stream_t stre
   if ((int64_t)rows * D > 12288)
     return fail(KIV_ERR_UNSUPPORTED, "kiv_retrieve: B*Hq*Q*D = %lld exceeds 12288 (decode-sized queries only)",
                 (long long)rows * D);
-  if (s->num_pages > INT32_MAX / 2) return fail(KIV_ERR_UNSUPPORTED, "kiv_retrieve: too many pages");
+  if (s->num_pages > (int64_t)kMaxWords * 32)
+    return fail(KIV_ERR_UNSUPPORTED, "kiv_retrieve: more than %d pages", kMaxWords * 32);
   DeviceGuard guard(s->device);
   hipStream_t st = (hipStream_t)stream;
   const int lg = lanes_per_row(dt, D);
   const int round = c.score_rounding == KIV_ROUND_ACTIVATION ? 1 : 0;
   const int N = (int)s->num_pages;
-  const int has_pages = N > 0 ? 1 : 0;
+  const int words = (N + 31) / 32;
   int rc;
+  if ((rc = s->row_stats.ensure((size_t)(rows + B) * 8, st, false))) return rc;
+  float *coarse_stats = (float *)s->row_stats.ptr;
+  float *fine_stats = coarse_stats + 2 * rows;
 
-  // ---- coarse: page scan + per-row top pages + union
-  bool run_coarse = has_pages && !(a->reuse_candidates && s->union_valid && s->union_rows == rows);
+  // ---- coarse: page scan + per-row top pages into the bitmap
+  int union_src = UNION_NONE;
   int64_t umax = 0;
-  if (has_pages) {
-    if (run_coarse) {
+  if (N > 0) {
+    const bool reuse = a->reuse_candidates && s->union_valid && s->union_rows == rows;
+    if (!reuse) {
+      union_src = UNION_BITMAP;
       const int k = std::min(a->top_pages, N);
       umax = std::min<int64_t>(N, (int64_t)rows * k);
       const int64_t ld = ((int64_t)N + 63) & ~int64_t(63);
       if ((rc = s->coarse_keys.ensure((size_t)rows * ld * 4, st, false))) return rc;
-      if ((rc = s->row_stats.ensure((size_t)std::max(rows, B) * 8, st, false))) return rc;
-      const size_t words = ((size_t)N + 31) / 32;
-      if (s->bitmap.bytes < words * 4) {
-        if ((rc = s->bitmap.ensure(words * 4, st, false))) return rc;
+      if (s->bitmap.bytes < (size_t)words * 4) {
+        if ((rc = s->bitmap.ensure((size_t)words * 4, st, false))) return rc;
         KIV_HIP(hipMemsetAsync(s->bitmap.ptr, 0, s->bitmap.bytes, st));
       }
       if ((rc = s->page_list.ensure((size_t)N * 4, st, false))) return rc;
@@ -645,23 +918,20 @@ int kiv_retrieve(kiv_store_t *s, const kiv_retrieve_args_t *a, kiv_stream_t stre
       if (rc) return rc;
       KIV_HIP(hipGetLastError());
       s->prof_begin(KIV_STAGE_COARSE_SELECT, st);
-      rc = with_dt(dt, [&](auto dtc) {
-        return with_kpt(N, [&](auto kpt) {
-        hipLaunchKernelGGL((coarse_select_kernel<decltype(dtc)::value, decltype(kpt)::value>), dim3(rows),
-                           dim3(kSelThreads), 0, st,
-                           (const uint32_t *)s->coarse_keys.ptr, ld, N, k, rows, (uint32_t *)s->bitmap.ptr,
-                           (int32_t *)s->page_list.ptr, (int32_t *)s->counters.ptr, (float *)s->row_stats.ptr,
-                           round, a->pages_out, a->union_count_out, a->stats_out, a->stats_accum);
+      with_sel_shape(N, [&](auto nt, auto kpt) {
+        constexpr int NT = decltype(nt)::value, KPT = decltype(kpt)::value;
+        hipLaunchKernelGGL((coarse_select_kernel<NT, KPT>), dim3(rows), dim3(NT), 0, st,
+                           (const uint32_t *)s->coarse_keys.ptr, ld, N, k, (uint32_t *)s->bitmap.ptr,
+                           coarse_stats);
         return (int)KIV_OK;
-        });
       });
       s->prof_end(KIV_STAGE_COARSE_SELECT, st);
-      if (rc) return rc;
       KIV_HIP(hipGetLastError());
       s->union_valid = true;
       s->union_rows = rows;
       s->union_max = umax;
     } else {
+      union_src = UNION_LIST;
       umax = s->union_max;
     }
   }
@@ -673,43 +943,48 @@ int kiv_retrieve(kiv_store_t *s, const kiv_retrieve_args_t *a, kiv_stream_t stre
     if ((rc = s->fine_keys.ensure((size_t)B * ldc * 4, st, false))) return rc;
     KIV_HIP(hipMemsetAsync(s->fine_keys.ptr, 0, s->fine_keys.bytes, st));
   }
-  if ((rc = s->row_stats.ensure((size_t)std::max(rows, B) * 8, st, false))) return rc;
   if ((rc = s->sel_cand.ensure((size_t)B * a->out_width * 4, st, false))) return rc;
+  const int bwords = union_src == UNION_BITMAP ? words : 0;
   {
     // Token slices per item: small enough that even the smallest union
     // (min(top_pages, N) pages) spreads over the GPU.
-    const int64_t umin = has_pages ? std::min<int64_t>(a->top_pages, N) : 0;
+    const int64_t umin = N > 0 ? std::min<int64_t>(a->top_pages, N) : 0;
     int tpi = ps;
     while (tpi > 32 && (umin * ((ps + tpi - 1) / tpi) * s->kr) < 1024) tpi = (tpi + 1) / 2;
     const int nsplit = (ps + tpi - 1) / tpi;
     const int64_t max_items = umax * nsplit + (s->partial_len + tpi - 1) / tpi;
     const int64_t nb = std::max<int64_t>(1, std::min<int64_t>(max_items, (1024 + s->kr - 1) / s->kr));
     const int G = hq / hkv;
-    const size_t lds = (size_t)G * Q * D * eb;
+    const size_t lds = (size_t)G * Q * D * eb + (size_t)bwords * 4 + (size_t)(bwords + 1) * 4;
     s->prof_begin(KIV_STAGE_FINE_SCAN, st);
     rc = with_dt_lg(dt, lg, [&](auto dtc, auto lgc) {
       hipLaunchKernelGGL((fine_scan_kernel<decltype(dtc)::value, decltype(lgc)::value>),
-                         dim3((unsigned)nb, (unsigned)s->kr), dim3(256), lds, st,
-                         (const int32_t *)s->page_list.ptr, (const int32_t *)s->counters.ptr, has_pages,
-                         (const uint64_t *)s->k_tab.ptr, s->chunk_shift, s->page_bytes, (const char *)s->k_part.ptr,
-                         (int)s->partial_len, ps, tpi, hkv, D, (const char *)a->q, a->q_stride[0], a->q_stride[1],
-                         a->q_stride[2], hq, Q, a->scaling, round, (uint32_t *)s->fine_keys.ptr, ldc);
+                         dim3((unsigned)nb, (unsigned)s->kr), dim3(256), lds, st, union_src,
+                         (const uint32_t *)s->bitmap.ptr, bwords, (const int32_t *)s->page_list.ptr,
+                         (const int32_t *)s->counters.ptr, (const uint64_t *)s->k_tab.ptr, s->chunk_shift,
+                         s->page_bytes, (const char *)s->k_part.ptr, (int)s->partial_len, ps, tpi, hkv, D,
+                         (const char *)a->q, a->q_stride[0], a->q_stride[1], a->q_stride[2], hq, Q, a->scaling,
+                         round, (uint32_t *)s->fine_keys.ptr, ldc);
       return (int)KIV_OK;
     });
     s->prof_end(KIV_STAGE_FINE_SCAN, st);
     if (rc) return rc;
     KIV_HIP(hipGetLastError());
   }
+  const int fwords = union_src == UNION_BITMAP ? words : 0;
+  const size_t flds = fine_select_lds(fwords, (int)std::min<int64_t>(a->out_width, cmax));
   s->prof_begin(KIV_STAGE_FINE_SELECT, st);
   rc = with_dt(dt, [&](auto dtc) {
-    return with_kpt(cmax, [&](auto kpt) {
-    hipLaunchKernelGGL((fine_select_kernel<decltype(dtc)::value, decltype(kpt)::value>), dim3(B),
-                       dim3(kSelThreads), 0, st,
-                       (uint32_t *)s->fine_keys.ptr, ldc, (int32_t *)s->counters.ptr, has_pages, ps,
-                       (int)s->partial_len, s->num_pages * ps, (const int32_t *)s->page_list.ptr, a->out_width, B,
-                       round, (float *)s->row_stats.ptr, (int32_t *)s->sel_cand.ptr, a->idx_out, a->stats_out,
-                       a->stats_accum);
-    return (int)KIV_OK;
+    return with_fine_kpt(cmax, [&](auto kpt) {
+      auto kern = fine_select_kernel<decltype(dtc)::value, decltype(kpt)::value>;
+      if (flds > 65536)
+        KIV_HIP(hipFuncSetAttribute((const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)flds));
+      hipLaunchKernelGGL(kern, dim3(B), dim3(kFineSelThreads), flds, st, (uint32_t *)s->fine_keys.ptr, ldc,
+                         union_src, (const uint32_t *)s->bitmap.ptr, fwords, (int32_t *)s->page_list.ptr,
+                         (int32_t *)s->counters.ptr, ps, (int)s->partial_len, s->num_pages * ps, a->out_width,
+                         round, (const float *)coarse_stats, rows, N, fine_stats, (int32_t *)s->sel_cand.ptr,
+                         a->idx_out, a->pages_out, a->union_count_out, a->stats_out, a->stats_accum);
+      return (int)KIV_OK;
     });
   });
   s->prof_end(KIV_STAGE_FINE_SELECT, st);
@@ -718,13 +993,18 @@ int kiv_retrieve(kiv_store_t *s, const kiv_retrieve_args_t *a, kiv_stream_t stre
   {
     const int64_t work = (int64_t)B * a->out_width * hkv * cpr;
     s->prof_begin(KIV_STAGE_GATHER, st);
-    hipLaunchKernelGGL(gather_kernel, dim3((unsigned)((work + 255) / 256)), dim3(256), 0, st,
-                       (const int32_t *)s->sel_cand.ptr, (const int32_t *)s->counters.ptr, has_pages,
-                       (const int32_t *)s->page_list.ptr, (const uint64_t *)s->k_tab.ptr,
-                       (const uint64_t *)s->v_tab.ptr, s->chunk_shift, s->page_bytes, (const char *)s->k_part.ptr,
-                       (const char *)s->v_part.ptr, ps, B, hkv, D, a->out_width, cpr, vec, eb, (char *)a->k_out,
-                       (char *)a->v_out);
+    rc = with_dt(dt, [&](auto dtc) {
+      hipLaunchKernelGGL((gather_kernel<decltype(dtc)::value>), dim3((unsigned)((work + 255) / 256)), dim3(256), 0,
+                         st, (const int32_t *)s->sel_cand.ptr, (const int32_t *)s->counters.ptr, N > 0 ? 1 : 0,
+                         (const int32_t *)s->page_list.ptr, (const uint64_t *)s->k_tab.ptr,
+                         (const uint64_t *)s->v_tab.ptr, s->chunk_shift, s->page_bytes,
+                         (const char *)s->k_part.ptr, (const char *)s->v_part.ptr, ps, (int)s->partial_len, B, hkv,
+                         D, a->out_width, cpr, (char *)a->k_out, (char *)a->v_out, (uint32_t *)s->bitmap.ptr,
+                         bwords, (const float *)fine_stats, round, a->stats_out, a->stats_accum);
+      return (int)KIV_OK;
+    });
     s->prof_end(KIV_STAGE_GATHER, st);
+    if (rc) return rc;
     KIV_HIP(hipGetLastError());
   }
   return KIV_OK;

@@ -330,6 +330,35 @@ def test_large_union_multi_tile(cuda):
     assert len(union) * 128 > 32768
 
 
+@pytest.mark.parametrize("n_pages,top_pages,top_p", [(1500, 300, 200), (3000, 300, 600)])
+def test_select_large_k_paths(cuda, n_pages, top_pages, top_p):
+    """top-k larger than the select block makes every key a candidate: the
+    coarse threshold then comes from the block search over the LDS
+    candidates (1500 <= 2048) or over the row itself (3000), and with
+    top_p = 600 the fine select searches its row and orders by bitonic sort."""
+    w = Workload("largek", 4, 1, 32, torch.float32, hot=8, cold=n_pages * 16 + 5, top_pages=top_pages,
+                 top_p=top_p, segment=64, page_size=16)
+    data = generate(w, seed=16)
+    q = torch.randn(1, 4, 1, 32, generator=torch.Generator().manual_seed(17))
+    store, oracle, cfg = build(w, data, cuda, chunks=(8192,))
+    check_retrieval(store, oracle, cfg, w, data, q)
+    union = store.telemetry_snapshot()["recent"][-2]["pages_selected"]
+    assert len(union) >= top_pages
+
+
+def test_fine_select_lds_search(cuda):
+    """top_p above the fine select block with 1024 < candidates <= 2048: the
+    threshold comes from the block search over the LDS candidates."""
+    w = Workload("fineB", 4, 1, 32, torch.float32, hot=8, cold=4000, top_pages=16, top_p=600, segment=64,
+                 page_size=32)
+    data = generate(w, seed=18)
+    q = torch.randn(1, 4, 1, 32, generator=torch.Generator().manual_seed(19))
+    store, oracle, cfg = build(w, data, cuda, chunks=(4000,))
+    check_retrieval(store, oracle, cfg, w, data, q)
+    union = store.telemetry_snapshot()["recent"][-2]["pages_selected"]
+    assert 1024 < len(union) * 32 <= 2048
+
+
 def test_attention_repeated_calls_share_workspace(cuda):
     """Consecutive calls reuse one workspace (split partials and counters)."""
     g = torch.Generator().manual_seed(15)
