@@ -183,6 +183,15 @@ enum {
 int kiv_profile_enable(kiv_store_t *store, int enable);
 int kiv_profile_read(kiv_store_t *store, int64_t counts[KIV_NUM_STAGES], double total_ms[KIV_NUM_STAGES]);
 
+/* Read-bandwidth probe (no reference counterpart; gives measured ceilings
+ * for the retrieval kernels' bandwidth figures).  Allocates `bytes` of HBM
+ * (where = KIV_TIER_HBM) or of mapped pinned host memory read through its
+ * device address (KIV_TIER_HOST), streams it `iters` times with `blocks`
+ * x 256 threads (0: 1024 blocks) on `stream`, frees it, and writes the
+ * average GB/s (1e9 bytes per second).  Synchronises the stream. */
+int kiv_probe_read_bandwidth(int32_t where, size_t bytes, int32_t blocks, int32_t iters, double *gbps,
+                             kiv_stream_t stream);
+
 /* Workspace bytes kiv_decode_attention needs for these sizes. */
 size_t kiv_attention_workspace_size(int32_t batch, int32_t num_q_heads, int32_t num_kv_heads,
                                     int32_t head_dim, int32_t q_len, int32_t total_keys);

@@ -369,7 +369,7 @@ int kiv_decode_attention(const kiv_attention_args_t *a, kiv_stream_t stream) {
   p.out = (char *)a->out;
   if (S > kMaxSplits) return fail(KIV_ERR_UNSUPPORTED, "kiv_decode_attention: %d keys is too many", L);
   const size_t lds = (size_t)GQ * D * elem_bytes(dt) + ((size_t)GQ * ch + 4 * kRowTile * D + 2 * GQ) * 4;
-  if (lds > 160 * 1024)
+  if (lds > device_lds_limit())
     return fail(KIV_ERR_UNSUPPORTED, "kiv_decode_attention: %d keys need %zu bytes of LDS", L, lds);
   const int lg = lanes_per_row(dt, D);
   hipStream_t st = (hipStream_t)stream;

@@ -152,6 +152,50 @@ __device__ __forceinline__ float half_wave_max(float v) {
   return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
 
+// AND and OR over the wave; every lane gets both.  All 64 lanes must be
+// active (DPP reads of inactive lanes return 0).
+__device__ __forceinline__ void wave_and_or_u32(uint32_t &a, uint32_t &o) {
+  a &= (uint32_t)dpp_i32<0xB1>((int)a);
+  o |= (uint32_t)dpp_i32<0xB1>((int)o);
+  a &= (uint32_t)dpp_i32<0x4E>((int)a);
+  o |= (uint32_t)dpp_i32<0x4E>((int)o);
+  a &= (uint32_t)dpp_i32<0x141>((int)a);
+  o |= (uint32_t)dpp_i32<0x141>((int)o);
+  a &= (uint32_t)dpp_i32<0x140>((int)a);
+  o |= (uint32_t)dpp_i32<0x140>((int)o);
+  const auto ra = __builtin_amdgcn_permlane16_swap(a, a, false, false);
+  const auto ro = __builtin_amdgcn_permlane16_swap(o, o, false, false);
+  a = ra[0] & ra[1];
+  o = ro[0] | ro[1];
+  const auto sa = __builtin_amdgcn_permlane32_swap(a, a, false, false);
+  const auto so = __builtin_amdgcn_permlane32_swap(o, o, false, false);
+  a = sa[0] & sa[1];
+  o = so[0] | so[1];
+}
+
+// Minimum over the wave; every lane gets it.  All 64 lanes must be active.
+__device__ __forceinline__ uint32_t wave_min_u32(uint32_t v) {
+  v = min(v, (uint32_t)dpp_i32<0xB1>((int)v));
+  v = min(v, (uint32_t)dpp_i32<0x4E>((int)v));
+  v = min(v, (uint32_t)dpp_i32<0x141>((int)v));
+  v = min(v, (uint32_t)dpp_i32<0x140>((int)v));
+  const auto r = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+  v = min(r[0], r[1]);
+  const auto t = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+  return min(t[0], t[1]);
+}
+
+// Number of set bits of a wave mask below the calling lane.
+__device__ __forceinline__ int lane_rank(uint64_t mask) {
+  return (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(mask >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)mask, 0u));
+}
+
+// The value of the first active lane, as a wave-uniform (scalar) value.
+__device__ __forceinline__ uint32_t uniform_u32(uint32_t x) { return (uint32_t)__builtin_amdgcn_readfirstlane((int)x); }
+__device__ __forceinline__ uint64_t uniform_u64(uint64_t x) {
+  return ((uint64_t)uniform_u32((uint32_t)(x >> 32)) << 32) | uniform_u32((uint32_t)x);
+}
+
 // Sum over an aligned group of LG lanes; every lane of the group gets it.
 template <int LG> __device__ __forceinline__ float group_sum(float v) {
   if constexpr (LG >= 2) v += dpp_f32<0xB1>(v);

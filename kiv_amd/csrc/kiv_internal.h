@@ -14,6 +14,8 @@ namespace kiv {
 // Thread-local error text + return code.
 int fail(int code, const char *fmt, ...);
 int hip_fail(hipError_t e, const char *what);
+// LDS bytes one workgroup may use on the current device (cached per device).
+size_t device_lds_limit();
 
 #define KIV_HIP(expr)                                   \
   do {                                                  \

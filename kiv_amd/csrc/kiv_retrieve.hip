@@ -31,7 +31,7 @@
 namespace kiv {
 
 constexpr int kMaxOut = 4096;       // largest top-P the fine select sorts in LDS
-constexpr int kScanThreads = 512;   // coarse scan block
+constexpr int kScanThreads = 256;   // coarse scan block (4 waves)
 constexpr int kFineSelThreads = 512;
 constexpr int kMaxWords = 4096;     // bitmap words ranked in LDS (131072 pages)
 constexpr int kCandCap = 2048;      // candidates a select keeps in LDS
@@ -103,7 +103,25 @@ template <int NT> struct MemKeys {
     n = n_;
   }
   template <typename F> __device__ void each(F &&f) const {
-    for (int idx = threadIdx.x; idx < n; idx += NT) f(comp_of(p[idx], idx));
+    constexpr int B = 8;  // loads in flight per thread
+    int idx = threadIdx.x;
+    for (; idx + (B - 1) * NT < n; idx += B * NT) {
+      uint32_t v[B];
+#pragma unroll
+      for (int u = 0; u < B; ++u) v[u] = p[idx + u * NT];
+#pragma unroll
+      for (int u = 0; u < B; ++u) f(comp_of(v[u], idx + u * NT));
+    }
+    for (; idx < n; idx += NT) f(comp_of(p[idx], idx));
+  }
+};
+
+// Keys of a row staged in LDS.
+template <int NT> struct LdsKeys {
+  const uint32_t *k;
+  int n;
+  template <typename F> __device__ void each(F &&f) const {
+    for (int idx = threadIdx.x; idx < n; idx += NT) f(comp_of(k[idx], idx));
   }
 };
 
@@ -117,13 +135,8 @@ template <int NT> struct LdsComps {
 
 __device__ __forceinline__ void wave_and_or64(uint64_t &a, uint64_t &o) {
   uint32_t al = (uint32_t)a, ah = (uint32_t)(a >> 32), ol = (uint32_t)o, oh = (uint32_t)(o >> 32);
-#pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) {
-    al &= __shfl_xor(al, m, 64);
-    ah &= __shfl_xor(ah, m, 64);
-    ol |= __shfl_xor(ol, m, 64);
-    oh |= __shfl_xor(oh, m, 64);
-  }
+  wave_and_or_u32(al, ol);
+  wave_and_or_u32(ah, oh);
   a = ((uint64_t)ah << 32) | al;
   o = ((uint64_t)oh << 32) | ol;
 }
@@ -144,6 +157,8 @@ __device__ uint64_t kth_search(int k, CountF &&count, AndOrF &&and_or) {
                                                                         : 0x00000000ffffffffull;
     uint64_t a, o;
     and_or(fixed, ans, a, o);
+    a = uniform_u64(a);
+    o = uniform_u64(o);
     ans |= a & part;
     uint64_t var = (a ^ o) & part;
     while (var) {
@@ -156,41 +171,43 @@ __device__ uint64_t kth_search(int k, CountF &&count, AndOrF &&and_or) {
   return ans;
 }
 
-// Up to 64*V composites held by one wave (lane l: entries l, l + 64, ...);
-// zero marks an empty entry.
-template <int V> struct WaveVals {
-  uint64_t v[V];
-  __device__ void load(const uint64_t *src, int n) {
-    const int lane = threadIdx.x & 63;
+// k-th largest of the nonzero entries of a wave-held multiset of 32-bit
+// values (1 <= k <= their count; lane l holds entries l, l + 64, ...).
+// Bits 31..16 are decided first, then bits 15..0 among the values sharing
+// the high half found: bits common to the group are taken as they are,
+// each varying bit costs one count.  Counts are ballots: a compare per
+// entry and a scalar popcount, no cross-lane reduction.
+template <int V> __device__ uint32_t wave_kth_u32(const uint32_t (&v)[V], int k) {
+  uint32_t ans = 0, fixed = 0;
 #pragma unroll
-    for (int i = 0; i < V; ++i) v[i] = lane + 64 * i < n ? src[lane + 64 * i] : 0ull;
-  }
-  __device__ int count_ge(uint64_t c) const {
-    int l = 0;
-#pragma unroll
-    for (int i = 0; i < V; ++i) l += v[i] >= c;
-    return wave_sum_i32(l);
-  }
-  __device__ void and_or(uint64_t mask, uint64_t prefix, uint64_t &a, uint64_t &o) const {
-    a = ~0ull;
-    o = 0ull;
+  for (int pass = 0; pass < 2; ++pass) {
+    const uint32_t part = pass == 0 ? 0xffff0000u : 0x0000ffffu;
+    uint32_t a = ~0u, o = 0u;
 #pragma unroll
     for (int i = 0; i < V; ++i)
-      if (v[i] && (v[i] & mask) == prefix) {
+      if (v[i] && (v[i] & fixed) == ans) {
         a &= v[i];
         o |= v[i];
       }
-    wave_and_or64(a, o);
+    wave_and_or_u32(a, o);
+    a = uniform_u32(a);
+    o = uniform_u32(o);
+    ans |= a & part;
+    uint32_t var = (a ^ o) & part;
+    while (var) {
+      const uint32_t bit = 1u << (31 - __clz(var));
+      var &= ~bit;
+      int c = 0;
+#pragma unroll
+      for (int i = 0; i < V; ++i) c += __popcll(__ballot(v[i] >= (ans | bit)));
+      if (c >= k) ans |= bit;
+    }
+    fixed |= part;
   }
-  __device__ uint64_t kth(int k) const {
-    return kth_search(k, [&](uint64_t c) { return count_ge(c); },
-                      [&](uint64_t m, uint64_t p, uint64_t &a, uint64_t &o) { and_or(m, p, a, o); });
-  }
-};
+  return ans;
+}
 
 // Up to 64*V 32-bit keys held by one wave; zero marks an empty entry.
-// kth(k) = the k-th largest key of the multiset (same search over bits
-// 31..16, then 15..0).
 template <int V> struct WaveKeys {
   uint32_t v[V];
   __device__ void load(const uint32_t *src, int n) {
@@ -198,38 +215,73 @@ template <int V> struct WaveKeys {
 #pragma unroll
     for (int i = 0; i < V; ++i) v[i] = lane + 64 * i < n ? src[lane + 64 * i] : 0u;
   }
-  __device__ uint32_t kth(int k) const {
-    uint32_t ans = 0, fixed = 0;
+  __device__ uint32_t kth(int k) const { return wave_kth_u32<V>(v, k); }
+};
+
+// Up to 64*V composites held by one wave; zero marks an empty entry (keys
+// are never zero).
+template <int V> struct WaveVals {
+  uint64_t v[V];
+  int n;
+  __device__ void load(const uint64_t *src, int n_) {
+    const int lane = threadIdx.x & 63;
+    n = n_;
 #pragma unroll
-    for (int pass = 0; pass < 2; ++pass) {
-      const uint32_t part = pass == 0 ? 0xffff0000u : 0x0000ffffu;
-      uint32_t a = ~0u, o = 0u;
+    for (int i = 0; i < V; ++i) v[i] = lane + 64 * i < n ? src[lane + 64 * i] : 0ull;
+  }
+  // A threshold T of the top k (1 <= k <= n): the entries >= T are exactly
+  // the k largest.  The key K of the k-th largest comes first (the minimum
+  // when k == n); if more entries than k have keys >= K, the index bits of
+  // the k-th largest are decided among the entries with key K.
+  __device__ uint64_t kth(int k) const {
+    uint32_t hi[V];
+#pragma unroll
+    for (int i = 0; i < V; ++i) hi[i] = (uint32_t)(v[i] >> 32);
+    uint32_t K;
+    if (k == n) {
+      uint32_t m = ~0u;
 #pragma unroll
       for (int i = 0; i < V; ++i)
-        if (v[i] && (v[i] & fixed) == ans) {
-          a &= v[i];
-          o |= v[i];
-        }
-#pragma unroll
-      for (int m = 32; m >= 1; m >>= 1) {
-        a &= __shfl_xor(a, m, 64);
-        o |= __shfl_xor(o, m, 64);
-      }
-      ans |= a & part;
-      uint32_t var = (a ^ o) & part;
-      while (var) {
-        const uint32_t bit = 1u << (31 - __clz(var));
-        var &= ~bit;
-        int l = 0;
-#pragma unroll
-        for (int i = 0; i < V; ++i) l += v[i] >= (ans | bit);
-        if (wave_sum_i32(l) >= k) ans |= bit;
-      }
-      fixed |= part;
+        if (hi[i]) m = min(m, hi[i]);
+      K = uniform_u32(wave_min_u32(m));
+    } else {
+      K = wave_kth_u32<V>(hi, k);
     }
-    return ans;
+    const uint64_t base = (uint64_t)K << 32;
+    int ge = 0;
+#pragma unroll
+    for (int i = 0; i < V; ++i) ge += __popcll(__ballot(hi[i] >= K));
+    if (ge == k) return base;
+    uint32_t a = ~0u, o = 0u;
+#pragma unroll
+    for (int i = 0; i < V; ++i)
+      if (hi[i] == K) {
+        a &= (uint32_t)v[i];
+        o |= (uint32_t)v[i];
+      }
+    wave_and_or_u32(a, o);
+    uint32_t lo = uniform_u32(a), var = uniform_u32(a ^ o);
+    while (var) {
+      const uint32_t bit = 1u << (31 - __clz(var));
+      var &= ~bit;
+      int c = 0;
+#pragma unroll
+      for (int i = 0; i < V; ++i) c += __popcll(__ballot(v[i] >= (base | lo | bit)));
+      if (c >= k) lo |= bit;
+    }
+    return base | lo;
   }
 };
+
+// Runs f(integral_constant<V>) with the fewest entries per lane that hold n.
+template <typename F> __device__ void with_wave_entries(int n, F &&f) {
+  using std::integral_constant;
+  if (n <= 64) f(integral_constant<int, 1>{});
+  else if (n <= 128) f(integral_constant<int, 2>{});
+  else if (n <= 256) f(integral_constant<int, 4>{});
+  else if (n <= 512) f(integral_constant<int, 8>{});
+  else f(integral_constant<int, kWaveCap / 64>{});
+}
 
 // Block-wide count of composites >= c: wave sums, one LDS atomic per wave,
 // one barrier.  Three counters rotate so a counter is cleared two counts
@@ -283,27 +335,24 @@ template <int NT, typename Src> __device__ uint64_t block_kth(const Src &src, in
                     [&](uint64_t m, uint64_t p, uint64_t &a, uint64_t &o) { block_and_or<NT>(src, m, p, sh, a, o); });
 }
 
-// Appends the thread's composites satisfying pred to out[*counter ...]
-// (entries past cap are counted, not written).  One LDS atomic per wave;
-// the caller synchronises before reading *counter.
+// Appends the composites satisfying pred to out[*counter ...] in one pass
+// (entries past cap are counted, not written): per source step, a ballot,
+// one LDS atomic by the first active lane, and the lane's rank in the
+// ballot.  The caller synchronises before reading *counter.
 template <int NT, typename Src, typename P>
 __device__ void block_compact(const Src &src, P &&pred, uint64_t *out, int cap, int *counter) {
-  int c = 0;
-  src.each([&](uint64_t x) { c += pred(x) ? 1 : 0; });
-  const int lane = threadIdx.x & 63;
-  int incl = c;
-#pragma unroll
-  for (int o = 1; o < 64; o <<= 1) {
-    const int t = __shfl_up(incl, o, 64);
-    if (lane >= o) incl += t;
-  }
-  int base = 0;
-  if (lane == 63) base = atomicAdd(counter, incl);
-  int pos = __shfl(base, 63, 64) + incl - c;
   src.each([&](uint64_t x) {
-    if (pred(x)) {
-      if (pos < cap) out[pos] = x;
-      ++pos;
+    const bool f = pred(x);
+    const uint64_t mask = __ballot(f);
+    if (mask) {
+      const uint64_t active = __ballot(1);
+      int base = 0;
+      if (lane_rank(active) == 0) base = atomicAdd(counter, __popcll(mask));
+      base = (int)uniform_u32((uint32_t)base);
+      if (f) {
+        const int pos = base + lane_rank(mask);
+        if (pos < cap) out[pos] = x;
+      }
     }
   });
 }
@@ -368,10 +417,12 @@ __device__ void topk_select(const Src &src, int k, SelSh<NT> &sh, uint64_t *cand
     uint64_t T;
     if (C <= kWaveCap) {
       if (wave == 0) {
-        WaveVals<kWaveCap / 64> wv;
-        wv.load(cand, C);
-        const uint64_t t = wv.kth(k);
-        if (tid == 0) sh.thresh = t;
+        with_wave_entries(C, [&](auto vc) {
+          WaveVals<decltype(vc)::value> wv;
+          wv.load(cand, C);
+          const uint64_t t = wv.kth(k);
+          if (tid == 0) sh.thresh = t;
+        });
       }
       __syncthreads();
       T = sh.thresh;
@@ -421,64 +472,238 @@ __device__ __forceinline__ int union_page(const uint32_t *bits, const int *rank,
 }
 
 // ------------------------------------------------------------ coarse scan
-// Block handles pages [p0, p0 + ppw).  The query rows sit in LDS in their
-// dtype, kv-major: row r' = kv_row * G*Q + j holds q head kv_head*G + j/Q at
-// position j%Q.  Each group of LG lanes holds one (page, kv row) summary row
-// in registers and scores it against the G*Q rows that read that kv row;
-// the keys go to row r' of the output.
-template <int DT, int LG>
-__global__ void __launch_bounds__(kScanThreads) coarse_scan_kernel(
-    const char *__restrict__ summ, int64_t n_pages, int kr, int head_dim, const char *__restrict__ q,
-    int64_t qs0, int64_t qs1, int64_t qs2, int hq, int hkv, int qlen, int rows, float scale, int round,
-    int ppw, uint32_t *__restrict__ keys, int64_t ld) {
-  constexpr int VEC = Elem<DT>::VEC, EB = Elem<DT>::BYTES;
-  constexpr int NSLOT = kScanThreads / LG;
-  constexpr int UT = 4;  // units in flight per lane group
-  extern __shared__ uint4 smem4[];
-  char *qraw = reinterpret_cast<char *>(smem4);                                      // [rows][D]
-  uint32_t *sk = reinterpret_cast<uint32_t *>(qraw + (size_t)rows * head_dim * EB);  // [rows][ppw]
-  const int G = hq / hkv, GQ = G * qlen, cpr = head_dim / VEC;
-  const int tid = threadIdx.x;
-  for (int i = tid; i < rows * cpr; i += kScanThreads) {
-    const int r = i / cpr, c = i % cpr;
-    const int kvr = r / GQ, j = r % GQ;
-    const int b = kvr / hkv, h = (kvr % hkv) * G + j / qlen, qp = j % qlen;
-    *reinterpret_cast<uint4 *>(qraw + ((size_t)r * head_dim + c * VEC) * EB) =
-        load16(q + ((int64_t)b * qs0 + (int64_t)h * qs1 + (int64_t)qp * qs2 + c * VEC) * EB);
+// Grid (page blocks, B*Hkv); block (x, r) scores kv row r of its pages.
+// A lane owns one page and holds a segment of that page's summary row in
+// registers; the DS waves of a page group hold the DS segments of the row
+// (no summary byte is loaded twice).  Each wave walks the G*Q query rows
+// reading kv row r: a query row's segment is the same for every lane, so
+// its loads are uniform and come through the scalar cache into SGPRs (the
+// next row's while the current one is used); the per-lane dot products
+// need no cross-lane reduction.  The DS partial sums meet in LDS.
+//
+// CPR = 16-byte chunks per summary row, a template parameter so that the
+// loads and dot products are straight-line code.  Lanes past the last page
+// read the last page and store nothing.
+constexpr int kScanRowTile = 32;  // query rows per LDS round
+
+template <int DT> __device__ __forceinline__ float dot_chunk(const uint4 &x, const uint4 &q, float acc) {
+  if constexpr (DT == DT_BF16) {
+    acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, x.x), __builtin_bit_cast(bf16x2_t, q.x), acc, false);
+    acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, x.y), __builtin_bit_cast(bf16x2_t, q.y), acc, false);
+    acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, x.z), __builtin_bit_cast(bf16x2_t, q.z), acc, false);
+    acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, x.w), __builtin_bit_cast(bf16x2_t, q.w), acc, false);
+  } else if constexpr (DT == DT_F16) {
+    acc = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2_t, x.x), __builtin_bit_cast(f16x2_t, q.x), acc, false);
+    acc = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2_t, x.y), __builtin_bit_cast(f16x2_t, q.y), acc, false);
+    acc = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2_t, x.z), __builtin_bit_cast(f16x2_t, q.z), acc, false);
+    acc = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2_t, x.w), __builtin_bit_cast(f16x2_t, q.w), acc, false);
+  } else {
+    acc = fmaf(__uint_as_float(x.x), __uint_as_float(q.x), acc);
+    acc = fmaf(__uint_as_float(x.y), __uint_as_float(q.y), acc);
+    acc = fmaf(__uint_as_float(x.z), __uint_as_float(q.z), acc);
+    acc = fmaf(__uint_as_float(x.w), __uint_as_float(q.w), acc);
   }
-  const int64_t p0 = (int64_t)blockIdx.x * ppw;
-  const int np = (int)min<int64_t>(ppw, n_pages - p0);
-  __syncthreads();
-  const int slot = tid / LG, lane = tid % LG;
-  const int units = np * kr;
-  const bool on = lane < cpr;
-  for (int ub = slot; ub < units; ub += NSLOT * UT) {
-    uint4 x[UT];
+  return acc;
+}
+
+// Segments (waves) per summary row: 4 where the row splits evenly into 4
+// segments of >= 3 chunks, else 2 or 1.  More segments put more waves on
+// each SIMD (one wave's scalar-load wait overlaps another's arithmetic).
+__host__ __device__ constexpr int scan_segments(int cpr) {
+  return (cpr % 4 == 0 && cpr >= 12) ? 4 : (cpr % 2 == 0 && cpr >= 6) ? 2 : 1;
+}
+
+template <int DT, int CPR, bool Q1>
+__global__ void __launch_bounds__(kScanThreads) coarse_scan_kernel(
+    const char *__restrict__ summ, int64_t n_pages, int kr, const char *__restrict__ q, int64_t qs0,
+    int64_t qs1, int64_t qs2, int hq, int hkv, int qlen, float scale, int round, uint32_t *__restrict__ keys,
+    int64_t ld) {
+  constexpr int EB = Elem<DT>::BYTES, VEC = Elem<DT>::VEC;
+  constexpr int DS = scan_segments(CPR);  // segments (waves) per page
+  constexpr int CS = CPR / DS;            // chunks per segment
+  // Query rows per batch of scalar loads (at most 64 SGPRs of row data).
+  constexpr int RB = CS >= 16 ? 1 : CS >= 8 ? 2 : 4;
+  static_assert(kScanRowTile % RB == 0, "row batches must tile the row tile");
+  constexpr int kWaves = kScanThreads / 64, kGroups = kWaves / DS;
+  static_assert(CPR % DS == 0, "segments must split the row evenly");
+  __shared__ float part[kWaves][kScanRowTile][64];
+  const int r = blockIdx.y, b = r / hkv, kvh = r % hkv;
+  const int G = hq / hkv, GQ = G * qlen;
+  // The wave index through readfirstlane: uniform to the compiler, so the
+  // query-row loads below become scalar loads.
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+  const int pg = wave / DS, seg = wave % DS;
+  const int64_t p = ((int64_t)blockIdx.x * kGroups + pg) * 64 + lane;
+  const bool valid = p < n_pages;
+  const char *row = summ + (min(p, n_pages - 1) * kr + r) * (int64_t)CPR * 16 + (int64_t)seg * CS * 16;
+  uint4 x[CS];
 #pragma unroll
-    for (int i = 0; i < UT; ++i) {
-      const int u = ub + i * NSLOT;
-      x[i] = (on && u < units) ? load16(summ + (((p0 + u / kr) * kr + u % kr) * head_dim + lane * VEC) * EB)
-                               : make_uint4(0, 0, 0, 0);
+  for (int i = 0; i < CS; ++i) x[i] = load16(row + (int64_t)i * 16);
+  // Query row j of kv row r: head kvh*G + j/Q at position j%Q (Q1: Q == 1,
+  // rows are heads, linear in j).
+  const char *qbase = q + ((int64_t)b * qs0 + (int64_t)kvh * G * qs1 + (int64_t)seg * CS * VEC) * EB;
+  auto qseg = [&](int j) {
+    if constexpr (Q1) return qbase + (int64_t)j * qs1 * EB;
+    else return qbase + ((int64_t)(j / qlen) * qs1 + (int64_t)(j % qlen) * qs2) * EB;
+  };
+  // Scalar loads return out of order (a wait covers every one in flight),
+  // so a row's loads cannot overlap the previous row's arithmetic.  Instead
+  // one batch of single-dword loads touches every 64-byte line of the
+  // wave's query segments first, while the summary loads are in flight,
+  // and the per-row loads below hit the scalar cache.
+  constexpr int kLines = (CS * 16 + 63) / 64;
+  {
+    const int nrow = min(GQ, kScanRowTile);
+    for (int j0 = 0; j0 < nrow; j0 += 8) {
+      uint32_t t[8][kLines];
+#pragma unroll
+      for (int jj = 0; jj < 8; ++jj) {
+        const char *qj = qseg(min(j0 + jj, nrow - 1));
+#pragma unroll
+        for (int l = 0; l < kLines; ++l) t[jj][l] = *reinterpret_cast<const uint32_t *>(qj + l * 64);
+      }
+      uint32_t touch = 0;
+#pragma unroll
+      for (int jj = 0; jj < 8; ++jj)
+#pragma unroll
+        for (int l = 0; l < kLines; ++l) touch ^= t[jj][l];
+      asm volatile("" ::"s"(touch));
     }
+  }
+  for (int t0 = 0; t0 < GQ; t0 += kScanRowTile) {
+    const int nt = min(kScanRowTile, GQ - t0);
+    // RB rows per batch of scalar loads: one wait per batch.
+    for (int jt = 0; jt < nt; jt += RB) {
+      uint4 qv[RB][CS];
 #pragma unroll
-    for (int i = 0; i < UT; ++i) {
-      const int u = ub + i * NSLOT;
-      if (u >= units) break;
-      const int pl = u / kr, r = u % kr;
-      for (int j = 0; j < GQ; ++j) {
-        const int row = r * GQ + j;
-        float part = 0.f;
-        if (on) part = chunk_dot<DT>(x[i], load16(qraw + ((size_t)row * head_dim + lane * VEC) * EB), 0.f);
-        const float dot = group_sum<LG>(part);
-        if (lane == (j % LG)) sk[row * ppw + pl] = order_key(score_of<DT>(dot, scale, round != 0));
+      for (int u = 0; u < RB; ++u) {
+        const char *qu = qseg(t0 + min(jt + u, nt - 1));
+#pragma unroll
+        for (int i = 0; i < CS; ++i) qv[u][i] = load16(qu + (int64_t)i * 16);
+      }
+      __builtin_amdgcn_sched_barrier(0);  // issue the batch's loads before any use
+      float acc[RB];
+#pragma unroll
+      for (int u = 0; u < RB; ++u) acc[u] = 0.f;
+#pragma unroll
+      for (int i = 0; i < CS; ++i)
+#pragma unroll
+        for (int u = 0; u < RB; ++u) acc[u] = dot_chunk<DT>(x[i], qv[u][i], acc[u]);
+      // jt is a multiple of RB and nt <= kScanRowTile, so jt + u is in
+      // bounds; rows past nt are never read.
+#pragma unroll
+      for (int u = 0; u < RB; ++u) part[wave][jt + u][lane] = acc[u];
+    }
+    __syncthreads();
+    // Wave `seg` of each page group finishes rows jt = seg, seg + DS, ...
+    if (valid) {
+      for (int jt = seg; jt < nt; jt += DS) {
+        float d = 0.f;
+#pragma unroll
+        for (int s2 = 0; s2 < DS; ++s2) d += part[pg * DS + s2][jt][lane];
+        keys[(int64_t)(r * GQ + t0 + jt) * ld + p] = order_key(score_of<DT>(d, scale, round != 0));
+      }
+    }
+    if (t0 + kScanRowTile < GQ) __syncthreads();
+  }
+}
+
+// MFMA variant for 16-bit dtypes with head_dim % 32 == 0.  Per wave, the
+// G*Q query rows reading kv row r (16 at a time, zero-padded) against 16
+// pages is a small dense product: one v_mfma_f32_16x16x32 per 32 dims.
+// Operand layout (64 lanes): lane l supplies A[row l%16][k 8(l/16)..+7]
+// (query) and B[k 8(l/16)..+7][page l%16] (summary), i.e. one 16-byte chunk
+// each per instruction; D[row 4(l/16)+i][page l%16] comes back in the
+// lane's i-th accumulator.  Products of 16-bit values are exact in fp32
+// and accumulate in fp32, like the dot products of the scalar kernel.
+// Every summary byte is loaded once, the query rows by ordinary loads
+// issued together with it; no LDS, no barrier.
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+
+template <int DT> __device__ __forceinline__ f32x4_t mfma_16x16x32(const uint4 &a, const uint4 &b, f32x4_t c) {
+  if constexpr (DT == DT_BF16)
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a), __builtin_bit_cast(bf16x8_t, b),
+                                                    c, 0, 0, 0);
+  else
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8_t, a), __builtin_bit_cast(f16x8_t, b), c,
+                                                   0, 0, 0);
+}
+
+constexpr int kScanMfmaPages = 16;  // pages per wave
+
+template <int DT, int KT>  // KT = head_dim / 32
+__global__ void __launch_bounds__(kScanThreads) coarse_scan_mfma_kernel(
+    const char *__restrict__ summ, int64_t n_pages, int kr, const char *__restrict__ q, int64_t qs0,
+    int64_t qs1, int64_t qs2, int hq, int hkv, int qlen, float scale, int round, uint32_t *__restrict__ keys,
+    int64_t ld) {
+  static_assert(DT != DT_F32, "16-bit dtypes only");
+  constexpr int64_t kRowBytes = (int64_t)KT * 64;  // 32 two-byte elements per K step
+  const int r = blockIdx.y, b = r / hkv, kvh = r % hkv;
+  const int G = hq / hkv, GQ = G * qlen;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int col = lane & 15, kg = lane >> 4;
+  const int64_t p = ((int64_t)blockIdx.x * (kScanThreads / 64) + wave) * kScanMfmaPages + col;
+  const char *row = summ + (min(p, n_pages - 1) * kr + r) * kRowBytes + kg * 16;
+  uint4 x[KT];
+#pragma unroll
+  for (int kk = 0; kk < KT; ++kk) x[kk] = load16(row + kk * 64);
+  for (int m0 = 0; m0 < GQ; m0 += 16) {
+    const int j = m0 + col;
+    uint4 qa[KT];
+    if (j < GQ) {
+      const char *qr = q + ((int64_t)b * qs0 + (int64_t)(kvh * G + j / qlen) * qs1 + (int64_t)(j % qlen) * qs2) * 2 +
+                       kg * 16;
+#pragma unroll
+      for (int kk = 0; kk < KT; ++kk) qa[kk] = load16(qr + kk * 64);
+    } else {
+#pragma unroll
+      for (int kk = 0; kk < KT; ++kk) qa[kk] = make_uint4(0, 0, 0, 0);
+    }
+    f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int kk = 0; kk < KT; ++kk) acc = mfma_16x16x32<DT>(qa[kk], x[kk], acc);
+    if (p < n_pages) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int row_j = m0 + 4 * kg + i;
+        if (row_j < GQ) keys[(int64_t)(r * GQ + row_j) * ld + p] = order_key(score_of<DT>(acc[i], scale, round != 0));
       }
     }
   }
-  __syncthreads();
-  for (int i = tid; i < rows * np; i += kScanThreads) {
-    const int r = i / np, pl = i % np;
-    keys[(int64_t)r * ld + p0 + pl] = sk[r * ppw + pl];
+}
+
+template <typename F> static int with_kt(int kt, F &&f) {
+  using std::integral_constant;
+  switch (kt) {
+    case 1: return f(integral_constant<int, 1>{});
+    case 2: return f(integral_constant<int, 2>{});
+    case 3: return f(integral_constant<int, 3>{});
+    case 4: return f(integral_constant<int, 4>{});
+    case 6: return f(integral_constant<int, 6>{});
+    case 8: return f(integral_constant<int, 8>{});
+    case 16: return f(integral_constant<int, 16>{});
   }
+  return fail(KIV_ERR_UNSUPPORTED, "no MFMA coarse scan for head_dim %d", kt * 32);
+}
+
+// Runs f(integral_constant<CPR>) for the chunks per row of a head dim.
+template <typename F> static int with_cpr(int cpr, F &&f) {
+  using std::integral_constant;
+  switch (cpr) {
+    case 2: return f(integral_constant<int, 2>{});
+    case 4: return f(integral_constant<int, 4>{});
+    case 6: return f(integral_constant<int, 6>{});
+    case 8: return f(integral_constant<int, 8>{});
+    case 12: return f(integral_constant<int, 12>{});
+    case 16: return f(integral_constant<int, 16>{});
+    case 24: return f(integral_constant<int, 24>{});
+    case 32: return f(integral_constant<int, 32>{});
+    case 48: return f(integral_constant<int, 48>{});
+    case 64: return f(integral_constant<int, 64>{});
+  }
+  return fail(KIV_ERR_UNSUPPORTED, "no coarse scan for %d 16-byte chunks per row", cpr);
 }
 
 // --------------------------------------------------------- coarse select
@@ -621,14 +846,16 @@ __device__ void fine_pick(const Src &src, int k, SelSh<kFineSelThreads> &sh, uin
   });
 }
 
-// Dynamic LDS: ubits[words] | urank[words + 1] | (8-aligned) cand[kCandCap] | sel[kp2].
-template <int DT, int KPT>
+// Dynamic LDS: ubits[words] | urank[words + 1] | (8-aligned) cand[kCandCap]
+// | sel[kp2] | stage[stage_cap].  A row of at most stage_cap keys is copied
+// to LDS once (zeroing it in memory on the way); longer rows are re-read.
+template <int DT>
 __global__ void __launch_bounds__(kFineSelThreads) fine_select_kernel(
     uint32_t *__restrict__ keys, int64_t ld, int union_src, const uint32_t *__restrict__ bitmap, int words,
-    int32_t *page_list, int32_t *counters, int page_size, int partial_len, int64_t num_finalized, int width,
-    int round, const float *__restrict__ coarse_stats, int rows, int n_pages, float *fine_stats,
-    int32_t *__restrict__ sel_cand, int64_t *__restrict__ idx_out, int32_t *pages_out, int32_t *union_out,
-    float *stats_out, double *stats_accum) {
+    int kp2, int stage_cap, int32_t *page_list, int32_t *counters, int page_size, int partial_len,
+    int64_t num_finalized, int width, int round, const float *__restrict__ coarse_stats, int rows, int n_pages,
+    float *fine_stats, int32_t *__restrict__ sel_cand, int64_t *__restrict__ idx_out, int32_t *pages_out,
+    int32_t *union_out, float *stats_out, double *stats_accum) {
   constexpr int NT = kFineSelThreads;
   __shared__ SelSh<NT> sh;
   extern __shared__ uint64_t fsm[];
@@ -638,20 +865,27 @@ __global__ void __launch_bounds__(kFineSelThreads) fine_select_kernel(
   int *urank = reinterpret_cast<int *>(ubits + words);
   uint64_t *cand = fsm + wpad / 2;
   uint64_t *sel = cand + kCandCap;
+  uint32_t *stage = reinterpret_cast<uint32_t *>(sel + kp2);
   sel_init(sh);
   int U = 0;
   if (union_src == UNION_BITMAP) U = rank_union<NT>(bitmap, words, ubits, urank, sh.scan_tmp);
   else if (union_src == UNION_LIST) U = counters[0];
   const int n = U * page_size + partial_len;
   const int k = min(width, n);
-  uint32_t *src = keys + (int64_t)b * ld;
+  uint32_t *src = keys + (int64_t)b * ld;  // 256-byte aligned rows
   float mx, sum;
-  if (KPT > 0) {
-    RegKeys<NT, (KPT > 0 ? KPT : 1)> rk;
-    rk.load(src, n);
+  if (n <= stage_cap) {
     // The scan accumulates with atomicMax: leave the row zeroed for the next call.
-    for (int i = tid; i < n; i += NT) src[i] = 0u;
-    fine_pick(rk, k, sh, cand, sel, mx, sum);
+    uint4 *src4 = reinterpret_cast<uint4 *>(src);
+    uint4 *st4 = reinterpret_cast<uint4 *>(stage);
+    const int n4 = (n + 3) / 4;  // the row's padding past n is zero
+#pragma unroll 8
+    for (int i = tid; i < n4; i += NT) {
+      st4[i] = src4[i];
+      src4[i] = make_uint4(0, 0, 0, 0);
+    }
+    __syncthreads();
+    fine_pick(LdsKeys<NT>{stage, n}, k, sh, cand, sel, mx, sum);
   } else {
     MemKeys<NT> mk;
     mk.load(src, n);
@@ -683,15 +917,28 @@ __global__ void __launch_bounds__(kFineSelThreads) fine_select_kernel(
     }
   };
   if (k <= NT) {
-    if (tid < k) {
-      const uint64_t x = sel[tid];
-      int r = 0;
-      for (int j = 0; j < k; ++j) r += sel[j] > x;
-      emit(r, x);
+    // Rank of sel[i] = entries greater than it; with k <= NT / 2 two
+    // threads count one half each.  cand is free once sel holds the top k.
+    const int parts = 2 * k <= NT ? 2 : 1, half = (k + parts - 1) / parts;
+    int *part_rank = reinterpret_cast<int *>(cand);
+    if (tid < parts * k) {
+      const int i = tid % k, part = tid / k;
+      const uint64_t x = sel[i];
+      const int j1 = min(k, (part + 1) * half);
+      int r = 0, j = part * half;
+      for (; j + 8 <= j1; j += 8) {
+        uint64_t y[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) y[u] = sel[j + u];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) r += y[u] > x;
+      }
+      for (; j < j1; ++j) r += sel[j] > x;
+      part_rank[part * k + i] = r;
     }
+    __syncthreads();
+    if (tid < k) emit(part_rank[tid] + (parts == 2 ? part_rank[k + tid] : 0), sel[tid]);
   } else {
-    int kp2 = 1;
-    while (kp2 < k) kp2 <<= 1;
     for (int i = k + tid; i < kp2; i += NT) sel[i] = 0ull;
     __syncthreads();
     for (int size = 2; size <= kp2; size <<= 1) {
@@ -718,15 +965,19 @@ __global__ void __launch_bounds__(kFineSelThreads) fine_select_kernel(
     page_list[v] = page;
     if (pages_out) pages_out[v] = page;
   }
-  if (tid == 0) {
-    counters[0] = U;
-    if (union_out) union_out[0] = U;
+  if (tid < 64) {
     float m = -INFINITY;
     double t = 0.0;
-    for (int r = 0; r < rows; ++r) {
+    for (int r = tid; r < rows; r += 64) {
       m = fmaxf(m, coarse_stats[2 * r]);
       t += coarse_stats[2 * r + 1];
     }
+    m = wave_max(m);
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) t += __shfl_xor(t, o, 64);
+    if (tid != 0) return;
+    counters[0] = U;
+    if (union_out) union_out[0] = U;
     float mean = (float)(t / ((double)rows * (double)n_pages));
     if (round) mean = round_act<DT>(mean);
     if (stats_out) {
@@ -740,9 +991,10 @@ __global__ void __launch_bounds__(kFineSelThreads) fine_select_kernel(
   }
 }
 
-static size_t fine_select_lds(int words, int k) {
-  int kp2 = 1;
-  while (kp2 < k) kp2 <<= 1;
+// LDS of the fine select: room kept for the static part, and the dynamic
+// part before the key stage.
+constexpr size_t kFineStaticLds = 8192;
+static size_t fine_select_lds(int words, int kp2) {
   return (size_t)((2 * words + 2) & ~1) * 4 + (size_t)kCandCap * 8 + (size_t)kp2 * 8;
 }
 
@@ -826,14 +1078,6 @@ template <typename F> static int with_sel_shape(int64_t n, F &&f) {
   return f(integral_constant<int, 1024>{}, integral_constant<int, 0>{});
 }
 
-// Keys per thread of the fine select for a row of n candidates.
-template <typename F> static int with_fine_kpt(int64_t n, F &&f) {
-  using std::integral_constant;
-  if (n <= kFineSelThreads * 16) return f(integral_constant<int, 16>{});
-  if (n <= kFineSelThreads * 32) return f(integral_constant<int, 32>{});
-  return f(integral_constant<int, 0>{});
-}
-
 }  // namespace kiv
 
 using namespace kiv;
@@ -901,19 +1145,42 @@ int kiv_retrieve(kiv_store_t *s, const kiv_retrieve_args_t *a, kiv_stream_t stre
         KIV_HIP(hipMemsetAsync(s->bitmap.ptr, 0, s->bitmap.bytes, st));
       }
       if ((rc = s->page_list.ensure((size_t)N * 4, st, false))) return rc;
-      // Pages per block: ~one block per CU, bounded by the LDS staging.
-      int ppw = (int)std::max<int64_t>(1, ((int64_t)N + 255) / 256);
-      ppw = std::min(ppw, std::max(1, 4096 / rows));
-      const int blocks = (int)(((int64_t)N + ppw - 1) / ppw);
-      const size_t lds = (size_t)rows * D * eb + (size_t)rows * ppw * 4;
+      const int kt = D / 32;
+      const bool mfma = dt != KIV_DTYPE_F32 && D % 32 == 0 && (kt <= 4 || kt == 6 || kt == 8 || kt == 16);
       s->prof_begin(KIV_STAGE_COARSE_SCAN, st);
-      rc = with_dt_lg(dt, lg, [&](auto dtc, auto lgc) {
-        hipLaunchKernelGGL((coarse_scan_kernel<decltype(dtc)::value, decltype(lgc)::value>), dim3(blocks),
-                           dim3(kScanThreads), lds, st, (const char *)s->summ.ptr, (int64_t)N, s->kr, D,
-                           (const char *)a->q, a->q_stride[0], a->q_stride[1], a->q_stride[2], hq, hkv, Q,
-                           rows, a->scaling, round, ppw, (uint32_t *)s->coarse_keys.ptr, ld);
-        return (int)KIV_OK;
-      });
+      if (mfma) {
+        const int pages_per_block = (kScanThreads / 64) * kScanMfmaPages;
+        const int blocks = (int)(((int64_t)N + pages_per_block - 1) / pages_per_block);
+        rc = with_dt(dt, [&](auto dtc) {
+          constexpr int DTV = decltype(dtc)::value;
+          if constexpr (DTV == DT_F32) {
+            return (int)KIV_ERR_UNSUPPORTED;
+          } else {
+            return with_kt(kt, [&](auto ktc) {
+              hipLaunchKernelGGL((coarse_scan_mfma_kernel<DTV, decltype(ktc)::value>), dim3(blocks, s->kr),
+                                 dim3(kScanThreads), 0, st, (const char *)s->summ.ptr, (int64_t)N, s->kr,
+                                 (const char *)a->q, a->q_stride[0], a->q_stride[1], a->q_stride[2], hq, hkv, Q,
+                                 a->scaling, round, (uint32_t *)s->coarse_keys.ptr, ld);
+              return (int)KIV_OK;
+            });
+          }
+        });
+      } else {
+        // Pages per block: 64 per page group, 4 / segments page groups.
+        const int segs = scan_segments(cpr);
+        const int pages_per_block = (kScanThreads / 64 / segs) * 64;
+        const int blocks = (int)(((int64_t)N + pages_per_block - 1) / pages_per_block);
+        rc = with_dt(dt, [&](auto dtc) {
+          return with_cpr(cpr, [&](auto cc) {
+            constexpr int DTV = decltype(dtc)::value, CPRV = decltype(cc)::value;
+            auto kern = Q == 1 ? coarse_scan_kernel<DTV, CPRV, true> : coarse_scan_kernel<DTV, CPRV, false>;
+            hipLaunchKernelGGL(kern, dim3(blocks, s->kr), dim3(kScanThreads), 0, st, (const char *)s->summ.ptr,
+                               (int64_t)N, s->kr, (const char *)a->q, a->q_stride[0], a->q_stride[1],
+                               a->q_stride[2], hq, hkv, Q, a->scaling, round, (uint32_t *)s->coarse_keys.ptr, ld);
+            return (int)KIV_OK;
+          });
+        });
+      }
       s->prof_end(KIV_STAGE_COARSE_SCAN, st);
       if (rc) return rc;
       KIV_HIP(hipGetLastError());
@@ -972,20 +1239,25 @@ int kiv_retrieve(kiv_store_t *s, const kiv_retrieve_args_t *a, kiv_stream_t stre
     KIV_HIP(hipGetLastError());
   }
   const int fwords = union_src == UNION_BITMAP ? words : 0;
-  const size_t flds = fine_select_lds(fwords, (int)std::min<int64_t>(a->out_width, cmax));
+  int kp2 = 1;
+  while (kp2 < std::min<int64_t>(a->out_width, cmax)) kp2 <<= 1;
+  const size_t fbase = fine_select_lds(fwords, kp2);
+  const size_t lds_limit = device_lds_limit();
+  if (fbase + kFineStaticLds > lds_limit)
+    return fail(KIV_ERR_UNSUPPORTED, "kiv_retrieve: fine select needs %zu bytes of LDS", fbase + kFineStaticLds);
+  const int stage_cap = (int)(((lds_limit - kFineStaticLds - fbase) / 4) & ~size_t(3));
+  const size_t flds = fbase + (size_t)std::min<int64_t>(stage_cap, (cmax + 3) & ~int64_t(3)) * 4;
   s->prof_begin(KIV_STAGE_FINE_SELECT, st);
   rc = with_dt(dt, [&](auto dtc) {
-    return with_fine_kpt(cmax, [&](auto kpt) {
-      auto kern = fine_select_kernel<decltype(dtc)::value, decltype(kpt)::value>;
-      if (flds > 65536)
-        KIV_HIP(hipFuncSetAttribute((const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)flds));
-      hipLaunchKernelGGL(kern, dim3(B), dim3(kFineSelThreads), flds, st, (uint32_t *)s->fine_keys.ptr, ldc,
-                         union_src, (const uint32_t *)s->bitmap.ptr, fwords, (int32_t *)s->page_list.ptr,
-                         (int32_t *)s->counters.ptr, ps, (int)s->partial_len, s->num_pages * ps, a->out_width,
-                         round, (const float *)coarse_stats, rows, N, fine_stats, (int32_t *)s->sel_cand.ptr,
-                         a->idx_out, a->pages_out, a->union_count_out, a->stats_out, a->stats_accum);
-      return (int)KIV_OK;
-    });
+    auto kern = fine_select_kernel<decltype(dtc)::value>;
+    if (flds > 65536)
+      KIV_HIP(hipFuncSetAttribute((const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)flds));
+    hipLaunchKernelGGL(kern, dim3(B), dim3(kFineSelThreads), flds, st, (uint32_t *)s->fine_keys.ptr, ldc, union_src,
+                       (const uint32_t *)s->bitmap.ptr, fwords, kp2, stage_cap, (int32_t *)s->page_list.ptr,
+                       (int32_t *)s->counters.ptr, ps, (int)s->partial_len, s->num_pages * ps, a->out_width, round,
+                       (const float *)coarse_stats, rows, N, fine_stats, (int32_t *)s->sel_cand.ptr, a->idx_out,
+                       a->pages_out, a->union_count_out, a->stats_out, a->stats_accum);
+    return (int)KIV_OK;
   });
   s->prof_end(KIV_STAGE_FINE_SELECT, st);
   if (rc) return rc;

@@ -12,6 +12,7 @@
 #include <string.h>
 
 #include <algorithm>
+#include <atomic>
 
 #include "kiv_common.h"
 #include "kiv_internal.h"
@@ -33,6 +34,18 @@ int fail(int code, const char *fmt, ...) {
 int hip_fail(hipError_t e, const char *what) {
   return fail(e == hipErrorOutOfMemory ? KIV_ERR_OOM : KIV_ERR_HIP, "%s failed: %s", what,
               hipGetErrorString(e));
+}
+
+size_t device_lds_limit() {
+  static std::atomic<int> cache[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 65536;
+  int v = cache[dev].load(std::memory_order_relaxed);
+  if (v == 0) {
+    if (hipDeviceGetAttribute(&v, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess || v <= 0) v = 65536;
+    cache[dev].store(v, std::memory_order_relaxed);
+  }
+  return (size_t)v;
 }
 
 int DevBuf::ensure(size_t need, hipStream_t stream, bool keep_contents) {
