@@ -1,6 +1,7 @@
 """Decode µs/layer of the tiered-cache hot path on one MI355X.
 
     python bench.py [--steps K] [--warmup W] [--workload qwen7b_1m] [--cold-tier host|hbm]
+                    [--cache cold|warm]
 
 One step = one global layer's decode step for one new token: evict the
 oldest hot row to the cold tier, coarse-to-fine retrieval over the cold
@@ -9,11 +10,19 @@ and the merged softmax over [retrieved ; hot].  Inputs are resident before
 the timed region: the cold tier is filled (1,048,576 tokens for the default
 workload) and the query / hot window live in HBM.
 
-The JSON line carries the headline µs/layer/step, a second timed pass with
-HIP events bracketing every kernel on its launch stream (per-stage average
-durations, the roofline of the dominant HBM kernel and the host-link
-traffic), the union size, the same step with the cold rows in HBM, and the
-reference's op sequence timed on the host CPU (the oracle, as a baseline).
+Caches.  In a model, a layer's summaries and hot window are evicted from
+L2 and the memory-side cache by the other layers' traffic before the layer
+runs again, so by default every step starts cold: an untimed 512 MiB read
+precedes it and HIP events bracket the step alone.  --cache warm times
+back-to-back steps of the one layer instead (reported as a variant too).
+
+The JSON line carries the headline µs/layer/step, a second pass with HIP
+events bracketing every kernel on its launch stream (per-stage average
+durations), the summary scan's HBM roofline and the host-link kernels'
+bandwidth against vendor peaks and against measured ceilings (the
+kiv_probe_read_bandwidth read probes, same cache state), the union size,
+the other cold tier, warm caches, and the reference's op sequence timed on
+the host CPU (the oracle, as a baseline).
 """
 
 from __future__ import annotations
@@ -45,7 +54,26 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=15.0, help="CPU baseline sample budget")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--cache", default="cold", choices=("cold", "warm"))
+    ap.add_argument("--profile-pass", action="store_true",
+                    help="for rocprofv3 runs: the headline tier's steps only, plus a 64 MiB device copy "
+                         "that calibrates the FETCH_SIZE / WRITE_SIZE counters")
     return ap.parse_args()
+
+
+SCRUB_BYTES = 512 << 20  # larger than L2 (8 x 4 MiB) plus the 256 MiB memory-side cache
+
+
+def make_scrub(dev):
+    """A read of SCRUB_BYTES that leaves no workload data in L2 or the MALL."""
+    import torch
+
+    buf = torch.ones(SCRUB_BYTES // 4, dtype=torch.int32, device=dev)
+
+    def scrub():
+        buf.sum()
+
+    return scrub
 
 
 def build_cold(w, cfg, dev, seed):
@@ -70,39 +98,52 @@ def build_cold(w, cfg, dev, seed):
     return store, hot_k, hot_v, q
 
 
-def run_steps(store, cfg, q, hot_k, hot_v, n, scaling, attn_events=None):
-    """n decode steps; the evicted row cycles through the hot window's rows."""
+def one_step(store, cfg, q, hot_k, hot_v, i, scaling, attn_events=None):
+    """One decode step; the evicted row cycles through the hot window's rows."""
     from kiv_amd.attention import decode_attention
 
     T = hot_k.shape[2]
-    for i in range(n):
-        j = (store.cold_length + i) % T
-        store.evict_from_hot(hot_k[:, :, j:j + 1], hot_v[:, :, j:j + 1])
-        k_out, v_out = store.retrieve_top_kv(q, scaling, cfg)
-        if attn_events is not None:
-            attn_events[i][0].record()
-        decode_attention(q, k_out, v_out, hot_k, hot_v, None, scaling)
-        if attn_events is not None:
-            attn_events[i][1].record()
+    j = (store.cold_length + i) % T
+    store.evict_from_hot(hot_k[:, :, j:j + 1], hot_v[:, :, j:j + 1])
+    k_out, v_out = store.retrieve_top_kv(q, scaling, cfg)
+    if attn_events is not None:
+        attn_events[0].record()
+    decode_attention(q, k_out, v_out, hot_k, hot_v, None, scaling)
+    if attn_events is not None:
+        attn_events[1].record()
 
 
-def time_steps(store, cfg, q, hot_k, hot_v, steps, warmup, scaling):
+def time_steps(store, cfg, q, hot_k, hot_v, steps, warmup, scaling, scrub):
+    """Mean µs per step: back-to-back (scrub None) or each step timed alone after a scrub."""
     import torch
 
-    run_steps(store, cfg, q, hot_k, hot_v, warmup, scaling)
+    for i in range(warmup):
+        one_step(store, cfg, q, hot_k, hot_v, i, scaling)
     torch.cuda.synchronize()
-    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     t0 = time.perf_counter()
-    ev0.record()
-    run_steps(store, cfg, q, hot_k, hot_v, steps, scaling)
-    ev1.record()
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
-    return ev0.elapsed_time(ev1) / steps, wall / steps * 1e3
+    if scrub is None:
+        ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        ev0.record()
+        for i in range(steps):
+            one_step(store, cfg, q, hot_k, hot_v, i, scaling)
+        ev1.record()
+        torch.cuda.synchronize()
+        gpu_us = ev0.elapsed_time(ev1) * 1e3 / steps
+    else:
+        ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+        for i in range(steps):
+            scrub()
+            ev[i][0].record()
+            one_step(store, cfg, q, hot_k, hot_v, i, scaling)
+            ev[i][1].record()
+        torch.cuda.synchronize()
+        gpu_us = sum(a.elapsed_time(b) for a, b in ev) * 1e3 / steps
+    wall_us = (time.perf_counter() - t0) * 1e6 / steps
+    return gpu_us, wall_us
 
 
-def profile_steps(store, cfg, q, hot_k, hot_v, steps, scaling):
-    """Per-stage average launch durations (ms) from HIP events on the launch stream."""
+def profile_steps(store, cfg, q, hot_k, hot_v, steps, scaling, scrub):
+    """Per-stage average durations (µs) from HIP events bracketing each launch on its stream."""
     import torch
 
     from kiv_amd import _native as nat
@@ -113,7 +154,10 @@ def profile_steps(store, cfg, q, hot_k, hot_v, steps, scaling):
     counts, totals = (C.c_int64 * 7)(), (C.c_double * 7)()
     nat.check(lib.kiv_profile_read(store._handle, counts, totals), "kiv_profile_read")  # clear
     ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(n)]
-    run_steps(store, cfg, q, hot_k, hot_v, n, scaling, attn_events=ev)
+    for i in range(n):
+        if scrub is not None:
+            scrub()
+        one_step(store, cfg, q, hot_k, hot_v, i, scaling, attn_events=ev[i])
     torch.cuda.synchronize()
     nat.check(lib.kiv_profile_read(store._handle, counts, totals), "kiv_profile_read")
     nat.check(lib.kiv_profile_enable(store._handle, 0), "kiv_profile_enable")
@@ -124,6 +168,29 @@ def profile_steps(store, cfg, q, hot_k, hot_v, steps, scaling):
     att = [a.elapsed_time(b) for a, b in ev]
     stages["attention"] = {"launches": n, "avg_us": sum(att) / n * 1e3}
     return stages
+
+
+def probes(dev, summary_bytes, host_bytes, cold):
+    """Measured read ceilings (GB/s): HBM streaming, HBM at the summary scan's size and
+    grid in the same cache state, and the host link (mapped pinned memory)."""
+    from kiv_amd import _native as nat
+
+    lib = nat.lib()
+    st = nat.stream_ptr(dev)
+
+    def run(where, nbytes, blocks, iters, cold_flag):
+        g = C.c_double(0)
+        nat.check(lib.kiv_probe_read_bandwidth(where, nbytes, blocks, iters, 1 if cold_flag else 0, C.byref(g), st),
+                  "kiv_probe_read_bandwidth")
+        return round(g.value, 1)
+
+    scan_blocks = max(1, (summary_bytes // 16 + 2047) // 2048)  # 8 x 16 B per thread, as the scan's lanes
+    return {
+        "hbm_stream_2GiB": run(nat.TIER_HBM, 2 << 30, 4096, 5, False),
+        "hbm_summary_size": run(nat.TIER_HBM, summary_bytes, scan_blocks, 20, cold),
+        "host_link_256MiB": run(nat.TIER_HOST, 256 << 20, 2048, 3, False),
+        "host_link_fine_size": run(nat.TIER_HOST, max(host_bytes, 1 << 20), 1024, 5, False),
+    }
 
 
 def roofline_and_links(w, store, stages, union_pages, tier):
@@ -184,6 +251,39 @@ def cpu_baseline(w, seed, budget_s):
                       "reference sequence in bf16"}
 
 
+def profile_pass(w, args, dev, scrub):
+    """The steps a profiler attributes per kernel, and the counters' calibration copy."""
+    import torch
+
+    from kiv_amd import KIVConfig
+
+    cfg = KIVConfig(hot_budget=w.hot, top_p=w.top_p, page_size=w.page_size, top_pages=w.top_pages,
+                    cold_tier=args.cold_tier, reserve_tokens=w.cold + args.steps + args.warmup + 1024)
+    store, hot_k, hot_v, q = build_cold(w, cfg, dev, args.seed)
+    us, _ = time_steps(store, cfg, q, hot_k, hot_v, args.steps, args.warmup, w.scaling, scrub)
+    src = torch.ones(64 << 20, dtype=torch.uint8, device=dev)
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        if scrub is not None:
+            scrub()
+        dst.copy_(src)  # calibration: reads and writes 64 MiB
+    torch.cuda.synchronize()
+    print(json.dumps({"profile_pass": w.name, "cold_tier": args.cold_tier, "caches": args.cache, "steps": args.steps,
+                      "us_per_step": round(us, 2), "calibration_copy_bytes": 64 << 20}), flush=True)
+
+
+def load_pmc(kernel, workload):
+    """HBM bytes per launch of `kernel` from the rocprofv3 --pmc summary committed under
+    profiles/ (FETCH_SIZE and WRITE_SIZE, scaled by the same counters' reading for a copy
+    kernel of known size), or None when there is none."""
+    path = os.path.join(ROOT, "profiles", f"{kernel}_{workload}_pmc.json")
+    if not os.path.exists(path):
+        return None
+    with open(path) as f:
+        d = json.load(f)
+    return d.get("traffic_bytes_per_launch")
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -197,7 +297,11 @@ def main():
 
     w = WORKLOADS[args.workload]
     dev = torch.device("cuda", 0)
-    extra = args.steps + args.warmup + 512
+    scrub = make_scrub(dev) if args.cache == "cold" else None
+    if args.profile_pass:
+        profile_pass(w, args, dev, scrub)
+        return
+    extra = 3 * (args.steps + args.warmup) + 1024
     results = {}
     tiers = [args.cold_tier] + ([] if args.no_variant else [t for t in ("host", "hbm") if t != args.cold_tier])
     for tier in tiers:
@@ -208,31 +312,57 @@ def main():
         fill_s = time.perf_counter() - t0
         print(f"[bench] {tier}: filled {store.cold_length} cold tokens in {fill_s:.1f}s", file=sys.stderr,
               flush=True)
-        ms_gpu, ms_wall = time_steps(store, cfg, q, hot_k, hot_v, args.steps, args.warmup, w.scaling)
-        print(f"[bench] {tier}: {ms_gpu * 1e3:.1f} us/step (wall {ms_wall * 1e3:.1f})", file=sys.stderr, flush=True)
-        stages = profile_steps(store, cfg, q, hot_k, hot_v, args.steps, w.scaling)
+        us, wall = time_steps(store, cfg, q, hot_k, hot_v, args.steps, args.warmup, w.scaling, scrub)
+        print(f"[bench] {tier} ({args.cache} caches): {us:.1f} us/step (wall {wall:.1f})", file=sys.stderr,
+              flush=True)
+        stages = profile_steps(store, cfg, q, hot_k, hot_v, args.steps, w.scaling, scrub)
+        entry = {"us_per_step": us, "wall_us_per_step": wall, "stages": stages}
+        if tier == args.cold_tier and scrub is not None and not args.no_variant:
+            warm_us, _ = time_steps(store, cfg, q, hot_k, hot_v, args.steps, 0, w.scaling, None)
+            entry["warm_us_per_step"] = warm_us
+            print(f"[bench] {tier} (warm caches): {warm_us:.1f} us/step", file=sys.stderr, flush=True)
         snap = store.telemetry_snapshot()
         unions = [r["num_pages_selected"] for r in snap["recent"] if r["kind"] == "coarse" and not r["skipped"]]
-        U = int(round(sum(unions) / len(unions))) if unions else 0
-        links = roofline_and_links(w, store, stages, U, tier)
-        results[tier] = {"us_per_step": ms_gpu * 1e3, "wall_us_per_step": ms_wall * 1e3, "stages": stages,
-                         "traffic": links, "union_pages": U, "cold_tokens": store.cold_length}
+        entry["union_pages"] = int(round(sum(unions) / len(unions))) if unions else 0
+        entry["traffic"] = roofline_and_links(w, store, stages, entry["union_pages"], tier)
+        entry["num_pages"] = store.num_pages
+        results[tier] = entry
         del store
         torch.cuda.synchronize()
         torch.cuda.empty_cache()
 
     head = results[args.cold_tier]
     links = head["traffic"]
-    hbm_kernels = {k: v for k, v in links.items() if v["from"] == "hbm"}
-    dominant = max(hbm_kernels, key=lambda k: hbm_kernels[k]["avg_us"])
-    dom = hbm_kernels[dominant]
-    roofline = {"kernel": dominant, "bound": "hbm", "achieved": round(dom["GB_s"], 1), "peak": HBM_PEAK_GBS,
-                "unit": "GB/s", "frac": round(dom["GB_s"] / HBM_PEAK_GBS, 4), "traffic": None,
-                "bytes_per_launch": dom["bytes"], "avg_us": round(dom["avg_us"], 2)}
     scan = links["coarse_scan"]
     host = {k: v for k, v in links.items() if v["from"] == "host"}
     host_bytes = sum(v["bytes"] for v in host.values())
     host_us = sum(v["avg_us"] for v in host.values())
+    ceil = probes(dev, scan["bytes"], links["fine_scan"]["bytes"], scrub is not None)
+    print(f"[bench] probes: {ceil}", file=sys.stderr, flush=True)
+    scan_us = scan["avg_us"]
+    scan_gbs = scan["GB_s"]
+    roofline = {
+        "kernel": "coarse_scan (summary scan)", "bound": "hbm", "achieved": round(scan_gbs, 1),
+        "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(scan_gbs / HBM_PEAK_GBS, 4),
+        "traffic": load_pmc("coarse_scan", w.name), "bytes_per_launch": scan["bytes"],
+        "avg_us": round(scan_us, 2),
+        "achievable": {"same_size_read": ceil["hbm_summary_size"], "stream_2GiB": ceil["hbm_stream_2GiB"]},
+        "frac_of_achievable": round(scan_gbs / ceil["hbm_summary_size"], 4),
+        "frac_of_stream": round(scan_gbs / ceil["hbm_stream_2GiB"], 4),
+    }
+    host_link = None
+    if host:
+        gbs = host_bytes / (host_us * 1e-6) / 1e9
+        host_link = {"kernels": sorted(host), "achieved": round(gbs, 2), "peak": HOST_LINK_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gbs / HOST_LINK_PEAK_GBS, 4), "bytes_per_step": host_bytes,
+                     "achievable": {"same_size_read": ceil["host_link_fine_size"],
+                                    "read_256MiB": ceil["host_link_256MiB"]},
+                     "frac_of_achievable": round(gbs / ceil["host_link_fine_size"], 4)}
+    variants = {t: {"us_per_step": round(r["us_per_step"], 2), "union_pages": r["union_pages"],
+                    "stages_us": {k: round(v["avg_us"], 2) for k, v in r["stages"].items()}}
+                for t, r in results.items() if t != args.cold_tier}
+    if "warm_us_per_step" in head:
+        variants["warm_caches"] = {"us_per_step": round(head["warm_us_per_step"], 2)}
     line = {
         "metric": METRIC,
         "value": round(head["us_per_step"], 2),
@@ -249,20 +379,14 @@ def main():
         "config": {"workload": f"{w.name}: one decode layer, Hq={w.num_q_heads} Hkv={w.num_kv_heads} "
                                f"D={w.head_dim}, hot {w.hot}, cold {w.cold}", "batch": 1,
                    "top_pages": w.top_pages, "top_p": w.top_p, "page_size": w.page_size,
-                   "cold_tier": args.cold_tier},
+                   "cold_tier": args.cold_tier, "caches": args.cache},
         "roofline": roofline,
-        "summary_scan": {"achieved": round(scan["GB_s"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                         "frac": round(scan["GB_s"] / HBM_PEAK_GBS, 4), "avg_us": round(scan["avg_us"], 2),
-                         "bytes_per_launch": scan["bytes"]},
-        "host_link": ({"achieved": round(host_bytes / (host_us * 1e-6) / 1e9, 2), "peak": HOST_LINK_PEAK_GBS,
-                       "unit": "GB/s", "frac": round(host_bytes / (host_us * 1e-6) / 1e9 / HOST_LINK_PEAK_GBS, 4),
-                       "bytes_per_step": host_bytes, "kernels": sorted(host)} if host else None),
+        "host_link": host_link,
         "union_pages": head["union_pages"],
         "stages_us": {k: round(v["avg_us"], 2) for k, v in head["stages"].items()},
         "wall_us_per_step": round(head["wall_us_per_step"], 2),
-        "variants": {t: {"us_per_step": round(r["us_per_step"], 2),
-                         "stages_us": {k: round(v["avg_us"], 2) for k, v in r["stages"].items()}}
-                     for t, r in results.items() if t != args.cold_tier},
+        "probes_GB_s": ceil,
+        "variants": variants,
     }
     if not args.no_cpu_baseline:
         print("[bench] CPU baseline ...", file=sys.stderr, flush=True)

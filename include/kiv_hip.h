@@ -166,8 +166,8 @@ int kiv_store_read_tokens(kiv_store_t *store, int64_t first, int64_t n, void *k_
 
 /* Instrumentation (no counterpart in the reference; used by benchmarks).
  * While enabled, every kernel the store launches is bracketed by a pair of
- * HIP events on the caller's stream (the last 256 calls per stage are
- * kept).  kiv_profile_read synchronises the device, writes per-stage launch
+ * timing-only HIP events (no system-scope fence) on the caller's stream
+ * (the last 256 calls per stage are kept).  kiv_profile_read synchronises the device, writes per-stage launch
  * counts and summed durations (ms) for the KIV_STAGE_* stages, and clears
  * the record. */
 enum {
@@ -186,11 +186,14 @@ int kiv_profile_read(kiv_store_t *store, int64_t counts[KIV_NUM_STAGES], double 
 /* Read-bandwidth probe (no reference counterpart; gives measured ceilings
  * for the retrieval kernels' bandwidth figures).  Allocates `bytes` of HBM
  * (where = KIV_TIER_HBM) or of mapped pinned host memory read through its
- * device address (KIV_TIER_HOST), streams it `iters` times with `blocks`
- * x 256 threads (0: 1024 blocks) on `stream`, frees it, and writes the
- * average GB/s (1e9 bytes per second).  Synchronises the stream. */
-int kiv_probe_read_bandwidth(int32_t where, size_t bytes, int32_t blocks, int32_t iters, double *gbps,
-                             kiv_stream_t stream);
+ * device address (KIV_TIER_HOST), streams it with `blocks` x 256 threads
+ * (0: 1024 blocks) on `stream`, frees it, and writes the average GB/s (1e9
+ * bytes per second) between timing-only events (no system-scope fence).
+ * Warm (cold == 0): `iters` back-to-back reads in one timed interval.  Cold: each of `iters` reads timed on its own, after an
+ * untimed 512 MiB read that evicts L2 and the memory-side cache.
+ * Synchronises the stream. */
+int kiv_probe_read_bandwidth(int32_t where, size_t bytes, int32_t blocks, int32_t iters, int32_t cold,
+                             double *gbps, kiv_stream_t stream);
 
 /* Workspace bytes kiv_decode_attention needs for these sizes. */
 size_t kiv_attention_workspace_size(int32_t batch, int32_t num_q_heads, int32_t num_kv_heads,

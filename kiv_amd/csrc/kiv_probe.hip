@@ -14,6 +14,7 @@ namespace kiv {
 
 constexpr int kProbeThreads = 256;
 constexpr int kProbeUnroll = 8;
+constexpr size_t kScrubBytes = size_t(512) << 20;  // > L2 + MALL
 
 // Each thread reads kProbeUnroll 16-byte words per step (all issued before
 // any is used), grid-stride over the buffer, and folds them into one word.
@@ -44,13 +45,13 @@ using namespace kiv;
 
 extern "C" {
 
-int kiv_probe_read_bandwidth(int32_t where, size_t bytes, int32_t blocks, int32_t iters, double *gbps,
-                             kiv_stream_t stream) {
+int kiv_probe_read_bandwidth(int32_t where, size_t bytes, int32_t blocks, int32_t iters, int32_t cold,
+                             double *gbps, kiv_stream_t stream) {
   if (!gbps || bytes < 16 || iters < 1 || blocks < 0 || (where != KIV_TIER_HOST && where != KIV_TIER_HBM))
     return fail(KIV_ERR_INVALID, "kiv_probe_read_bandwidth: bad argument");
   bytes &= ~size_t(15);
   hipStream_t st = (hipStream_t)stream;
-  void *host = nullptr, *buf = nullptr;
+  void *host = nullptr, *buf = nullptr, *scrub = nullptr;
   uint32_t *sink = nullptr;
   hipEvent_t e0 = nullptr, e1 = nullptr;
   int rc = KIV_OK;
@@ -66,25 +67,38 @@ int kiv_probe_read_bandwidth(int32_t where, size_t bytes, int32_t blocks, int32_
   } else if (check(hipMalloc(&buf, bytes), "hipMalloc")) {
     check(hipMemsetAsync(buf, 0x5a, bytes, st), "hipMemsetAsync");
   }
-  if (rc == KIV_OK) check(hipMalloc((void **)&sink, (size_t)nb * 4), "hipMalloc");
-  if (rc == KIV_OK) check(hipEventCreate(&e0), "hipEventCreate");
-  if (rc == KIV_OK) check(hipEventCreate(&e1), "hipEventCreate");
+  if (rc == KIV_OK && cold && check(hipMalloc(&scrub, kScrubBytes), "hipMalloc"))
+    check(hipMemsetAsync(scrub, 0x33, kScrubBytes, st), "hipMemsetAsync");
+  if (rc == KIV_OK) check(hipMalloc((void **)&sink, (size_t)std::max(nb, 4096) * 4), "hipMalloc");
+  // Timing-only events: no system-scope fence to time with the reads.
+  if (rc == KIV_OK) check(hipEventCreateWithFlags(&e0, hipEventDisableSystemFence), "hipEventCreateWithFlags");
+  if (rc == KIV_OK) check(hipEventCreateWithFlags(&e1, hipEventDisableSystemFence), "hipEventCreateWithFlags");
   if (rc == KIV_OK) {
     const int64_t n16 = (int64_t)(bytes / 16);
     hipLaunchKernelGGL(probe_read_kernel, dim3(nb), dim3(kProbeThreads), 0, st, (const uint4 *)buf, n16, sink);
-    check(hipEventRecord(e0, st), "hipEventRecord");
-    for (int it = 0; it < iters && rc == KIV_OK; ++it)
-      hipLaunchKernelGGL(probe_read_kernel, dim3(nb), dim3(kProbeThreads), 0, st, (const uint4 *)buf, n16, sink);
-    check(hipGetLastError(), "probe_read_kernel");
-    check(hipEventRecord(e1, st), "hipEventRecord");
-    check(hipEventSynchronize(e1), "hipEventSynchronize");
-    float ms = 0.f;
-    if (check(hipEventElapsedTime(&ms, e0, e1), "hipEventElapsedTime"))
-      *gbps = (double)bytes * iters / ((double)ms * 1e-3) / 1e9;
+    double total_ms = 0.0;
+    // Warm: one interval over all launches.  Cold: each launch timed on its
+    // own, after a streaming read of kScrubBytes that evicts the caches.
+    const int rounds = cold ? iters : 1, per_round = cold ? 1 : iters;
+    for (int it = 0; it < rounds && rc == KIV_OK; ++it) {
+      if (cold)
+        hipLaunchKernelGGL(probe_read_kernel, dim3(4096), dim3(kProbeThreads), 0, st, (const uint4 *)scrub,
+                           (int64_t)(kScrubBytes / 16), sink);
+      check(hipEventRecord(e0, st), "hipEventRecord");
+      for (int k = 0; k < per_round; ++k)
+        hipLaunchKernelGGL(probe_read_kernel, dim3(nb), dim3(kProbeThreads), 0, st, (const uint4 *)buf, n16, sink);
+      check(hipGetLastError(), "probe_read_kernel");
+      check(hipEventRecord(e1, st), "hipEventRecord");
+      check(hipEventSynchronize(e1), "hipEventSynchronize");
+      float ms = 0.f;
+      if (check(hipEventElapsedTime(&ms, e0, e1), "hipEventElapsedTime")) total_ms += ms;
+    }
+    if (rc == KIV_OK) *gbps = (double)bytes * iters / (total_ms * 1e-3) / 1e9;
   }
   if (e0) (void)hipEventDestroy(e0);
   if (e1) (void)hipEventDestroy(e1);
   if (sink) (void)hipFree(sink);
+  if (scrub) (void)hipFree(scrub);
   if (host) (void)hipHostFree(host);
   else if (buf) (void)hipFree(buf);
   return rc;

@@ -529,7 +529,9 @@ int kiv_profile_enable(kiv_store_t *s, int enable) {
   DeviceGuard guard(s->device);
   if (enable && s->prof_ev.empty()) {
     s->prof_ev.resize((size_t)KIV_NUM_STAGES * kiv_store::kProfRing * 2);
-    for (hipEvent_t &e : s->prof_ev) KIV_HIP(hipEventCreate(&e));
+    // Timing-only events: no system-scope fence (its cache writeback and
+    // invalidation would be timed with the kernel).
+    for (hipEvent_t &e : s->prof_ev) KIV_HIP(hipEventCreateWithFlags(&e, hipEventDisableSystemFence));
   }
   s->prof_on = enable != 0;
   return KIV_OK;
