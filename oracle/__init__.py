@@ -21,7 +21,8 @@ which check shapes only):
                        checked bit-exactly against torch's own rounding
   selections, union    brute-force sort on small inputs; N=0, N<top_pages,
                        cold<top_p special cases; golden vectors written by
-                       the reference itself (tests/golden)
+                       the reference itself (tests/golden): torch_ref
+                       reproduces them bit for bit, exact ties included
   attention            textbook fp64 softmax attention; P=all losslessness;
                        cold=0 identity; key-permutation invariance
 """
