@@ -47,6 +47,17 @@ struct DevBuf {
 inline int elem_bytes(int dtype) { return dtype == KIV_DTYPE_F32 ? 4 : 2; }
 inline int vec_elems(int dtype) { return 16 / elem_bytes(dtype); }
 
+// 16-byte chunks per row the coarse scan is compiled for (it unrolls over
+// them): head_dim = chunks * (16 / element bytes).
+inline bool scan_supports_chunks(int cpr) {
+  switch (cpr) {
+    case 2: case 4: case 6: case 8: case 10: case 12: case 14: case 16: case 20: case 24: case 28: case 32:
+    case 40: case 48: case 64:
+      return true;
+  }
+  return false;
+}
+
 // Lanes that cooperate on one row: next power of two >= D / VEC.
 inline int lanes_per_row(int dtype, int head_dim) {
   int cpr = head_dim / vec_elems(dtype);

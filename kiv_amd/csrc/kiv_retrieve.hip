@@ -522,7 +522,7 @@ __global__ void __launch_bounds__(kScanThreads) coarse_scan_kernel(
   constexpr int DS = scan_segments(CPR);  // segments (waves) per page
   constexpr int CS = CPR / DS;            // chunks per segment
   // Query rows per batch of scalar loads (at most 64 SGPRs of row data).
-  constexpr int RB = CS >= 16 ? 1 : CS >= 8 ? 2 : 4;
+  constexpr int RB = CS > 8 ? 1 : CS > 4 ? 2 : 4;
   static_assert(kScanRowTile % RB == 0, "row batches must tile the row tile");
   constexpr int kWaves = kScanThreads / 64, kGroups = kWaves / DS;
   static_assert(CPR % DS == 0, "segments must split the row evenly");
@@ -696,10 +696,15 @@ template <typename F> static int with_cpr(int cpr, F &&f) {
     case 4: return f(integral_constant<int, 4>{});
     case 6: return f(integral_constant<int, 6>{});
     case 8: return f(integral_constant<int, 8>{});
+    case 10: return f(integral_constant<int, 10>{});
     case 12: return f(integral_constant<int, 12>{});
+    case 14: return f(integral_constant<int, 14>{});
     case 16: return f(integral_constant<int, 16>{});
+    case 20: return f(integral_constant<int, 20>{});
     case 24: return f(integral_constant<int, 24>{});
+    case 28: return f(integral_constant<int, 28>{});
     case 32: return f(integral_constant<int, 32>{});
+    case 40: return f(integral_constant<int, 40>{});
     case 48: return f(integral_constant<int, 48>{});
     case 64: return f(integral_constant<int, 64>{});
   }

@@ -336,10 +336,11 @@ int kiv_store_create(const kiv_store_config_t *cfg, int device, kiv_store_t **ou
   if (c.dtype != KIV_DTYPE_F32 && c.dtype != KIV_DTYPE_F16 && c.dtype != KIV_DTYPE_BF16)
     return fail(KIV_ERR_INVALID, "kiv_store_create: unknown dtype %d", c.dtype);
   const int vec = vec_elems(c.dtype);
-  if (c.head_dim < vec || c.head_dim % vec || c.head_dim / vec > 64)
+  if (c.head_dim < vec || c.head_dim % vec || !scan_supports_chunks(c.head_dim / vec))
     return fail(KIV_ERR_UNSUPPORTED,
-                "kiv_store_create: head_dim %d must be a multiple of %d and at most %d for this dtype",
-                c.head_dim, vec, 64 * vec);
+                "kiv_store_create: head_dim %d unsupported for this dtype (head_dim / %d must be one of "
+                "2 4 6 8 10 12 14 16 20 24 28 32 40 48 64)",
+                c.head_dim, vec);
   if (c.cold_tier != KIV_TIER_HOST && c.cold_tier != KIV_TIER_HBM)
     return fail(KIV_ERR_INVALID, "kiv_store_create: unknown cold_tier %d", c.cold_tier);
   if (c.score_rounding != KIV_ROUND_ACTIVATION && c.score_rounding != KIV_ROUND_FP32)

@@ -162,6 +162,11 @@ SMALL = [
                       top_pages=5, top_p=40, segment=100), (333,)),
     ("small_pages", dict(num_q_heads=4, num_kv_heads=1, head_dim=64, dtype=torch.bfloat16, cold=777, hot=30,
                          top_pages=6, top_p=50, segment=64, page_size=16), (5, 11)),
+    # head dims off the MFMA scan's multiples of 32: the SGPR-query scan
+    ("d80_bf16", dict(num_q_heads=8, num_kv_heads=2, head_dim=80, dtype=torch.bfloat16, cold=2000, hot=64,
+                      top_pages=4, top_p=64, segment=256), (2000,)),
+    ("d112_f32", dict(num_q_heads=6, num_kv_heads=2, head_dim=112, dtype=torch.float32, cold=1500, hot=40,
+                      top_pages=3, top_p=50, segment=200), (700, 800)),
 ]
 
 
