@@ -753,12 +753,20 @@ __global__ void __launch_bounds__(NT) coarse_select_kernel(const uint32_t *__res
 // ------------------------------------------------------------- fine scan
 // Grid (nb, B*Hkv): block (x, r) keeps the G*Q query rows that read kv row
 // r = b*Hkv + h in LDS and walks work items x, x + nb, ...; an item is a
-// slice of `tpi` tokens of a union page (items [0, U*nsplit)) or of the
+// slice of tpi tokens of a union page (items [0, U*nsplit)) or of the
 // partial page (the items after).  Union pages come from the bitmap
-// (ranked in LDS) or from the stored union list.  Each lane group scores UT
-// tokens at a time; the max over the block's rows is folded into the
-// candidate's key with atomicMax, which completes the max over kv heads
-// across blocks (keys are order-preserving; the select zeroes them).
+// (ranked in LDS) or from the stored union list.  The max over the block's
+// rows is folded into the candidate's key with atomicMax, which completes
+// the max over kv heads across blocks (keys are order-preserving; the
+// select zeroes them).
+//
+// Slice size and grid are the host's choice per cold tier (measured on
+// MI355X, Qwen2.5-7B shape, 154 union pages): zero-copy reads of mapped
+// host memory stream best with about 2 MiB in flight over the whole grid
+// (1024 blocks x ~2 KiB slices: 55 GB/s; 8 MiB in flight: 51 GB/s, 16 MiB:
+// 49 GB/s); HBM rows best in 32-token slices over 2048 blocks.
+constexpr int kFineUT = 4;  // tokens in flight per lane group
+
 template <int DT, int LG>
 __global__ void __launch_bounds__(256) fine_scan_kernel(
     int union_src, const uint32_t *__restrict__ bitmap, int words, const int32_t *__restrict__ page_list,
@@ -767,7 +775,7 @@ __global__ void __launch_bounds__(256) fine_scan_kernel(
     const char *__restrict__ q, int64_t qs0, int64_t qs1, int64_t qs2, int hq, int qlen, float scale, int round,
     uint32_t *__restrict__ out, int64_t ld) {
   constexpr int VEC = Elem<DT>::VEC, EB = Elem<DT>::BYTES;
-  constexpr int UT = 4;
+  constexpr int UT = kFineUT;
   constexpr int NSLOT = 256 / LG;
   extern __shared__ uint4 smem4[];
   __shared__ int scan_tmp[4];
@@ -1218,14 +1226,16 @@ int kiv_retrieve(kiv_store_t *s, const kiv_retrieve_args_t *a, kiv_stream_t stre
   if ((rc = s->sel_cand.ensure((size_t)B * a->out_width * 4, st, false))) return rc;
   const int bwords = union_src == UNION_BITMAP ? words : 0;
   {
-    // Token slices per item: small enough that even the smallest union
-    // (min(top_pages, N) pages) spreads over the GPU.
-    const int64_t umin = N > 0 ? std::min<int64_t>(a->top_pages, N) : 0;
-    int tpi = ps;
-    while (tpi > 32 && (umin * ((ps + tpi - 1) / tpi) * s->kr) < 1024) tpi = (tpi + 1) / 2;
+    // Slices and grid per tier (see the fine scan kernel): host rows in
+    // ~2 KiB slices over ~1024 blocks, HBM rows in 32-token slices over
+    // ~2048 blocks.
+    const bool host_tier = c.cold_tier == KIV_TIER_HOST;
+    int tpi = host_tier ? (int)std::max<int64_t>(1, 2048 / ((int64_t)D * eb)) : 32;
+    tpi = std::min(tpi, ps);
     const int nsplit = (ps + tpi - 1) / tpi;
     const int64_t max_items = umax * nsplit + (s->partial_len + tpi - 1) / tpi;
-    const int64_t nb = std::max<int64_t>(1, std::min<int64_t>(max_items, (1024 + s->kr - 1) / s->kr));
+    const int64_t want = host_tier ? 1024 : 2048;
+    const int64_t nb = std::max<int64_t>(1, std::min<int64_t>(max_items, (want + s->kr - 1) / s->kr));
     const int G = hq / hkv;
     const size_t lds = (size_t)G * Q * D * eb + (size_t)bwords * 4 + (size_t)(bwords + 1) * 4;
     s->prof_begin(KIV_STAGE_FINE_SCAN, st);
