@@ -99,7 +99,8 @@ def build_cold(w, cfg, dev, seed):
 
 
 def one_step(store, cfg, q, hot_k, hot_v, i, scaling, attn_events=None):
-    """One decode step; the evicted row cycles through the hot window's rows."""
+    """One decode step, as the middleware runs it: evict the oldest hot row (it
+    cycles through the hot window's rows), retrieve, merged attention."""
     from kiv_amd.attention import decode_attention
 
     T = hot_k.shape[2]

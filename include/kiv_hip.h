@@ -197,9 +197,10 @@ int kiv_profile_read(kiv_store_t *store, int64_t counts[KIV_NUM_STAGES], double 
 int kiv_probe_read_bandwidth(int32_t where, size_t bytes, int32_t blocks, int32_t iters, int32_t cold,
                              double *gbps, kiv_stream_t stream);
 
-/* Workspace bytes kiv_decode_attention needs for these sizes. */
+/* Workspace bytes the decode attention needs for `cold_len` retrieved and
+ * `hot_len` hot keys. */
 size_t kiv_attention_workspace_size(int32_t batch, int32_t num_q_heads, int32_t num_kv_heads,
-                                    int32_t head_dim, int32_t q_len, int32_t total_keys);
+                                    int32_t head_dim, int32_t q_len, int32_t cold_len, int32_t hot_len);
 
 /* One softmax over [retrieved ; hot] keys per query row, fp32 accumulate,
  * output in the activation dtype.  Retrieved columns are never masked.

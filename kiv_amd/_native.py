@@ -87,7 +87,7 @@ SIGNATURES = {
     "kiv_profile_read": (C.c_int, [C.c_void_p, C.c_int64 * 7, C.c_double * 7]),
     "kiv_probe_read_bandwidth": (C.c_int, [C.c_int32, C.c_size_t, C.c_int32, C.c_int32, C.c_int32,
                                            C.POINTER(C.c_double), C.c_void_p]),
-    "kiv_attention_workspace_size": (C.c_size_t, [C.c_int32] * 6),
+    "kiv_attention_workspace_size": (C.c_size_t, [C.c_int32] * 7),
     "kiv_decode_attention": (C.c_int, [C.POINTER(AttentionArgs), C.c_void_p]),
 }
 

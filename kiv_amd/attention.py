@@ -1,8 +1,8 @@
 """Merged decode attention over [retrieved ; hot] (kiv_decode_attention).
 
-One kernel launch replaces the wrapper's two ``torch.cat`` calls, the mask
-widening and the attention call (kiv/middleware.py:330-354): retrieved keys
-are always attended, an optional mask applies to the hot columns only.
+The kernels replace the wrapper's two ``torch.cat`` calls, the mask widening
+and the attention call (kiv/middleware.py:330-354): retrieved keys are always
+attended, an optional mask applies to the hot columns only.
 """
 
 from __future__ import annotations
@@ -46,15 +46,12 @@ def _mask_view(mask: torch.Tensor | None, hot_len: int):
     return mask.data_ptr(), nat.mask_kind(mask.dtype), nat.strides(mask, 4)
 
 
-def decode_attention(query: torch.Tensor, cold_k: torch.Tensor | None, cold_v: torch.Tensor | None,
-                     hot_k: torch.Tensor, hot_v: torch.Tensor, mask: torch.Tensor | None,
-                     scaling: float) -> torch.Tensor:
-    """softmax(q [cold; hot]^T * scaling + [0; mask]) [cold; hot] -> [B, Q, Hq, D]."""
+def _prepare(query: torch.Tensor, cold_len: int, hot_k: torch.Tensor, hot_v: torch.Tensor,
+             mask: torch.Tensor | None, scaling: float):
+    """(args without retrieved keys, output, tensors the launches read)."""
     B, hq, Q, D = query.shape
     hkv = hot_k.shape[1]
     dt = query.dtype
-    if cold_k is not None and (cold_k.dtype != dt or not cold_k.is_contiguous()):
-        cold_k, cold_v = cold_k.to(dt).contiguous(), cold_v.to(dt).contiguous()
     if hot_k.dtype != dt:
         hot_k, hot_v = hot_k.to(dt), hot_v.to(dt)
     if hot_k.stride(3) != 1:
@@ -62,23 +59,39 @@ def decode_attention(query: torch.Tensor, cold_k: torch.Tensor | None, cold_v: t
     if hot_v.stride(3) != 1:
         hot_v = hot_v.contiguous()
     q = query if query.stride(3) == 1 else query.contiguous()
-    P = 0 if cold_k is None else cold_k.shape[2]
     T = hot_k.shape[2]
     lib = nat.lib()
-    need = lib.kiv_attention_workspace_size(B, hq, hkv, D, Q, P + T)
+    need = lib.kiv_attention_workspace_size(B, hq, hkv, D, Q, cold_len, T)
     ws = _workspace(query.device, need)
     out = torch.empty(B, Q, hq, D, dtype=dt, device=query.device)
     mptr, mkind, mstr = _mask_view(mask, T)
     args = nat.AttentionArgs(
         batch=B, num_q_heads=hq, num_kv_heads=hkv, head_dim=D, q_len=Q, dtype=nat.dtype_code(dt),
-        q=q.data_ptr(), q_stride=nat.strides(q, 4),
-        cold_k=nat.ptr(cold_k), cold_v=nat.ptr(cold_v), cold_len=P, hot_len=T,
+        q=q.data_ptr(), q_stride=nat.strides(q, 4), cold_k=None, cold_v=None, cold_len=cold_len, hot_len=T,
         hot_k=hot_k.data_ptr(), hot_v=hot_v.data_ptr(),
         hot_k_stride=nat.strides(hot_k, 3), hot_v_stride=nat.strides(hot_v, 3),
         mask=mptr, mask_kind=mkind, mask_stride=mstr, scaling=float(scaling),
         out=out.data_ptr(), workspace=ws.data_ptr(), workspace_bytes=ws.numel(),
     )
-    nat.check(lib.kiv_decode_attention(C.byref(args), nat.stream_ptr(query.device)), "kiv_decode_attention")
+    keep = (q, hot_k, hot_v) + ((mask,) if mask is not None else ())
+    return args, out, keep
+
+
+def _set_cold(args, cold_k: torch.Tensor | None, cold_v: torch.Tensor | None, dt: torch.dtype):
+    if cold_k is not None and (cold_k.dtype != dt or not cold_k.is_contiguous()):
+        cold_k, cold_v = cold_k.to(dt).contiguous(), cold_v.to(dt).contiguous()
+    args.cold_k, args.cold_v = nat.ptr(cold_k), nat.ptr(cold_v)
+    return cold_k, cold_v
+
+
+def decode_attention(query: torch.Tensor, cold_k: torch.Tensor | None, cold_v: torch.Tensor | None,
+                     hot_k: torch.Tensor, hot_v: torch.Tensor, mask: torch.Tensor | None,
+                     scaling: float) -> torch.Tensor:
+    """softmax(q [cold; hot]^T * scaling + [0; mask]) [cold; hot] -> [B, Q, Hq, D]."""
+    P = 0 if cold_k is None else cold_k.shape[2]
+    args, out, _ = _prepare(query, P, hot_k, hot_v, mask, scaling)
+    _set_cold(args, cold_k, cold_v, query.dtype)
+    nat.check(nat.lib().kiv_decode_attention(C.byref(args), nat.stream_ptr(query.device)), "kiv_decode_attention")
     return out
 
 

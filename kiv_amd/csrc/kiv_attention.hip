@@ -7,9 +7,11 @@
 // concatenated K/V and widened mask are never built.  Scores, softmax and
 // the weighted sum are fp32; the output is rounded once to the dtype.
 //
-// Split kernel, grid (S, B*Hkv): block (s, r) takes keys [s*CH, (s+1)*CH) of
-// the virtual sequence for kv row r and all G*Q query rows reading it, and
-// writes the split's max m, exp-sum l and unnormalised accumulator.
+// Split kernel, grid (splits of this launch, B*Hkv): split s takes a chunk
+// of CH keys of the virtual sequence [retrieved ; hot] for kv row r and all
+// G*Q query rows reading it, and writes the split's max m, exp-sum l and
+// unnormalised accumulator.  Retrieved and hot keys are split separately
+// (no split straddles them); a launch covers splits [split0, split0 + n).
 // Combine kernel, one block per query row: log-sum-exp merge of the S splits
 // into the output.
 #include <algorithm>
@@ -37,7 +39,9 @@ struct AttnParams {
   int64_t ms0, ms1, ms2, ms3;
   int batch, hq, hkv, qlen, head_dim;
   float scale;
-  int chunk, nsplit;
+  int chunk, nsplit;   // keys per split; splits in all
+  int split_cold;      // splits [0, split_cold) hold retrieved keys, the rest hot keys
+  int split0;          // first split of this launch
   float *ws_m, *ws_l, *ws_acc;
   char *out;
 };
@@ -76,9 +80,9 @@ __global__ void __launch_bounds__(kAttnThreads) decode_attn_kernel(AttnParams p)
     *reinterpret_cast<uint4 *>(qraw + ((size_t)j * D + c * VEC) * EB) =
         load16(p.q + ((int64_t)b * p.qs0 + (int64_t)h * p.qs1 + (int64_t)qp * p.qs2 + c * VEC) * EB);
   }
-  const int L = p.cold_len + p.hot_len;
-  const int k0 = s * CH;
-  const int nk = min(CH, L - k0);
+  const int sg = p.split0 + s;
+  const int k0 = sg < p.split_cold ? sg * CH : p.cold_len + (sg - p.split_cold) * CH;
+  const int nk = min(CH, (sg < p.split_cold ? p.cold_len : p.cold_len + p.hot_len) - k0);
   __syncthreads();
 
   const int slot = tid / LG, lane = tid % LG;
@@ -184,15 +188,15 @@ __global__ void __launch_bounds__(kAttnThreads) decode_attn_kernel(AttnParams p)
       const int row = (b * p.hq + h) * p.qlen + qp;
       float a = 0.f;
       for (int w = 0; w < kAttnThreads / 64; ++w) a += red[(w * kRowTile + jj) * D + d];
-      p.ws_acc[((int64_t)s * rows_total + row) * D + d] = a;
+      p.ws_acc[((int64_t)sg * rows_total + row) * D + d] = a;
     }
     __syncthreads();
   }
   for (int j = tid; j < GQ; j += kAttnThreads) {
     const int h = kvh * G + j / p.qlen, qp = j % p.qlen;
     const int row = (b * p.hq + h) * p.qlen + qp;
-    p.ws_m[(int64_t)s * rows_total + row] = rm[j];
-    p.ws_l[(int64_t)s * rows_total + row] = rl[j];
+    p.ws_m[(int64_t)sg * rows_total + row] = rm[j];
+    p.ws_l[(int64_t)sg * rows_total + row] = rl[j];
   }
 }
 
@@ -270,11 +274,19 @@ static int pick_chunk(int total_keys, int kr) {
   return ch;
 }
 
+// Split counts of the retrieved and hot keys.
+static void split_counts(int cold_len, int hot_len, int kr, int *ch, int *s_cold, int *s_hot) {
+  *ch = pick_chunk(std::max(cold_len + hot_len, 1), kr);
+  *s_cold = (cold_len + *ch - 1) / *ch;
+  *s_hot = (hot_len + *ch - 1) / *ch;
+}
+
 // Workspace: split maxima [S][R], sums [S][R] and accumulators [S][R][D].
-static size_t ws_layout(int batch, int hq, int hkv, int head_dim, int qlen, int total_keys, size_t *off_m,
-                        size_t *off_l, size_t *off_acc) {
-  const int ch = pick_chunk(std::max(total_keys, 1), batch * hkv);
-  const size_t S = (size_t)std::max(1, (total_keys + ch - 1) / ch);
+static size_t ws_layout(int batch, int hq, int hkv, int head_dim, int qlen, int cold_len, int hot_len,
+                        size_t *off_m, size_t *off_l, size_t *off_acc) {
+  int ch, sc, sh;
+  split_counts(cold_len, hot_len, batch * hkv, &ch, &sc, &sh);
+  const size_t S = (size_t)std::max(1, sc + sh);
   const size_t R = (size_t)batch * hq * qlen;
   const size_t ml = (S * R * 4 + 255) & ~size_t(255);
   *off_m = 0;
@@ -283,54 +295,46 @@ static size_t ws_layout(int batch, int hq, int hkv, int head_dim, int qlen, int 
   return *off_acc + ((S * R * head_dim * 4 + 255) & ~size_t(255));
 }
 
-}  // namespace kiv
-
-using namespace kiv;
-
-extern "C" {
-
-size_t kiv_attention_workspace_size(int32_t batch, int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
-                                    int32_t q_len, int32_t total_keys) {
-  size_t m, l, acc;
-  return ws_layout(batch, num_q_heads, num_kv_heads, head_dim, q_len, total_keys, &m, &l, &acc);
-}
-
-int kiv_decode_attention(const kiv_attention_args_t *a, kiv_stream_t stream) {
-  if (!a) return fail(KIV_ERR_INVALID, "kiv_decode_attention: null argument");
+// Checks the arguments and launches the split and combine kernels on `st`.
+static int attention_launch(const kiv_attention_args_t *a, hipStream_t st, const char *who) {
+  if (!a) return fail(KIV_ERR_INVALID, "%s: null argument", who);
   const int dt = a->dtype;
   if (dt != KIV_DTYPE_F32 && dt != KIV_DTYPE_F16 && dt != KIV_DTYPE_BF16)
-    return fail(KIV_ERR_INVALID, "kiv_decode_attention: unknown dtype %d", dt);
+    return fail(KIV_ERR_INVALID, "%s: unknown dtype %d", who, dt);
   const int B = a->batch, hq = a->num_q_heads, hkv = a->num_kv_heads, D = a->head_dim, Q = a->q_len;
-  if (B < 1 || hq < 1 || hkv < 1 || Q < 1 || hq % hkv)
-    return fail(KIV_ERR_INVALID, "kiv_decode_attention: bad head geometry");
+  if (B < 1 || hq < 1 || hkv < 1 || Q < 1 || hq % hkv) return fail(KIV_ERR_INVALID, "%s: bad head geometry", who);
   const int vec = vec_elems(dt);
   if (D < vec || D % vec || D / vec > 64)
-    return fail(KIV_ERR_UNSUPPORTED, "kiv_decode_attention: head_dim %d unsupported for this dtype", D);
+    return fail(KIV_ERR_UNSUPPORTED, "%s: head_dim %d unsupported for this dtype", who, D);
   const int G = hq / hkv, GQ = G * Q;
   if (GQ > 64 || GQ * D > 8192)
-    return fail(KIV_ERR_UNSUPPORTED, "kiv_decode_attention: (Hq/Hkv)*Q = %d rows per kv head too many", GQ);
+    return fail(KIV_ERR_UNSUPPORTED, "%s: (Hq/Hkv)*Q = %d rows per kv head too many", who, GQ);
   if (a->cold_len < 0 || a->hot_len < 0 || a->cold_len + a->hot_len < 1)
-    return fail(KIV_ERR_INVALID, "kiv_decode_attention: no keys");
-  if (!a->q || !a->out || !a->workspace || (a->cold_len && (!a->cold_k || !a->cold_v)) ||
-      (a->hot_len && (!a->hot_k || !a->hot_v)))
-    return fail(KIV_ERR_INVALID, "kiv_decode_attention: null pointer");
-  if (a->q_stride[3] != 1) return fail(KIV_ERR_INVALID, "kiv_decode_attention: q head_dim stride must be 1");
+    return fail(KIV_ERR_INVALID, "%s: no keys", who);
+  const bool need_cold = a->cold_len > 0, need_hot = a->hot_len > 0;
+  if (!a->q || !a->workspace || !a->out || (need_cold && (!a->cold_k || !a->cold_v)) ||
+      (need_hot && (!a->hot_k || !a->hot_v)))
+    return fail(KIV_ERR_INVALID, "%s: null pointer", who);
+  if (a->q_stride[3] != 1) return fail(KIV_ERR_INVALID, "%s: q head_dim stride must be 1", who);
   if (((uintptr_t)a->q & 15) || (a->q_stride[0] % vec) || (a->q_stride[1] % vec) || (a->q_stride[2] % vec))
-    return fail(KIV_ERR_INVALID, "kiv_decode_attention: q must be 16-byte aligned, strides multiple of %d", vec);
-  const uintptr_t ptrs = (uintptr_t)a->cold_k | (uintptr_t)a->cold_v | (uintptr_t)a->hot_k | (uintptr_t)a->hot_v;
-  if (ptrs & 15) return fail(KIV_ERR_INVALID, "kiv_decode_attention: K/V must be 16-byte aligned");
+    return fail(KIV_ERR_INVALID, "%s: q must be 16-byte aligned, strides multiple of %d", who, vec);
+  const uintptr_t ptrs = (need_cold ? (uintptr_t)a->cold_k | (uintptr_t)a->cold_v : 0) |
+                         (need_hot ? (uintptr_t)a->hot_k | (uintptr_t)a->hot_v : 0);
+  if (ptrs & 15) return fail(KIV_ERR_INVALID, "%s: K/V must be 16-byte aligned", who);
   for (int i = 0; i < 3; ++i)
     if ((a->hot_k_stride[i] % vec) || (a->hot_v_stride[i] % vec))
-      return fail(KIV_ERR_INVALID, "kiv_decode_attention: hot strides must be multiples of %d", vec);
+      return fail(KIV_ERR_INVALID, "%s: hot strides must be multiples of %d", who, vec);
   if (a->mask && (a->mask_kind < KIV_MASK_BOOL || a->mask_kind > KIV_MASK_BF16))
-    return fail(KIV_ERR_INVALID, "kiv_decode_attention: unknown mask kind %d", a->mask_kind);
+    return fail(KIV_ERR_INVALID, "%s: unknown mask kind %d", who, a->mask_kind);
   const int L = a->cold_len + a->hot_len;
   size_t off_m, off_l, off_acc;
-  const size_t need = ws_layout(B, hq, hkv, D, Q, L, &off_m, &off_l, &off_acc);
+  const size_t need = ws_layout(B, hq, hkv, D, Q, a->cold_len, a->hot_len, &off_m, &off_l, &off_acc);
   if (a->workspace_bytes < need)
-    return fail(KIV_ERR_INVALID, "kiv_decode_attention: workspace %zu bytes, %zu needed", a->workspace_bytes, need);
-  const int ch = pick_chunk(L, B * hkv);
-  const int S = (L + ch - 1) / ch;
+    return fail(KIV_ERR_INVALID, "%s: workspace %zu bytes, %zu needed", who, a->workspace_bytes, need);
+  int ch, sc, sh;
+  split_counts(a->cold_len, a->hot_len, B * hkv, &ch, &sc, &sh);
+  const int S = sc + sh;
+  if (S > kMaxSplits) return fail(KIV_ERR_UNSUPPORTED, "%s: %d keys is too many", who, L);
   AttnParams p;
   p.q = (const char *)a->q;
   p.qs0 = a->q_stride[0];
@@ -362,17 +366,17 @@ int kiv_decode_attention(const kiv_attention_args_t *a, kiv_stream_t stream) {
   p.scale = a->scaling;
   p.chunk = ch;
   p.nsplit = S;
+  p.split_cold = sc;
   char *ws = (char *)a->workspace;
   p.ws_m = (float *)(ws + off_m);
   p.ws_l = (float *)(ws + off_l);
   p.ws_acc = (float *)(ws + off_acc);
   p.out = (char *)a->out;
-  if (S > kMaxSplits) return fail(KIV_ERR_UNSUPPORTED, "kiv_decode_attention: %d keys is too many", L);
   const size_t lds = (size_t)GQ * D * elem_bytes(dt) + ((size_t)GQ * ch + 4 * kRowTile * D + 2 * GQ) * 4;
   if (lds > device_lds_limit())
-    return fail(KIV_ERR_UNSUPPORTED, "kiv_decode_attention: %d keys need %zu bytes of LDS", L, lds);
+    return fail(KIV_ERR_UNSUPPORTED, "%s: %d keys need %zu bytes of LDS", who, L, lds);
+  p.split0 = 0;
   const int lg = lanes_per_row(dt, D);
-  hipStream_t st = (hipStream_t)stream;
   int rc = with_dt_lg(dt, lg, [&](auto dtc, auto lgc) {
     auto kern = decode_attn_kernel<decltype(dtc)::value, decltype(lgc)::value>;
     if (lds > 65536) KIV_HIP(hipFuncSetAttribute((const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
@@ -385,6 +389,22 @@ int kiv_decode_attention(const kiv_attention_args_t *a, kiv_stream_t stream) {
   if (rc) return rc;
   KIV_HIP(hipGetLastError());
   return KIV_OK;
+}
+
+}  // namespace kiv
+
+using namespace kiv;
+
+extern "C" {
+
+size_t kiv_attention_workspace_size(int32_t batch, int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
+                                    int32_t q_len, int32_t cold_len, int32_t hot_len) {
+  size_t m, l, acc;
+  return ws_layout(batch, num_q_heads, num_kv_heads, head_dim, q_len, cold_len, hot_len, &m, &l, &acc);
+}
+
+int kiv_decode_attention(const kiv_attention_args_t *a, kiv_stream_t stream) {
+  return attention_launch(a, (hipStream_t)stream, "kiv_decode_attention");
 }
 
 }  // extern "C"

@@ -35,7 +35,7 @@ constexpr int kScanThreads = 256;   // coarse scan block (4 waves)
 constexpr int kFineSelThreads = 512;
 constexpr int kMaxWords = 4096;     // bitmap words ranked in LDS (131072 pages)
 constexpr int kCandCap = 2048;      // candidates a select keeps in LDS
-constexpr int kWaveCap = 1024;      // candidates one wave selects from registers
+constexpr int kRankCap = 1024;      // candidates ranked by counting
 
 // Union source of the fine stages.
 enum { UNION_NONE = 0, UNION_BITMAP = 1, UNION_LIST = 2 };
@@ -55,10 +55,9 @@ template <int NT> struct SelSh {
   int cnt[3];  // rotating block-wide counters
   int ncand, nsel;
   uint32_t band[2], bor[2];
-  uint64_t bound, thresh;
   float fmax[NT / 64], fsum[NT / 64];
   int scan_tmp[NT / 64];
-  uint32_t kmax[NT];  // per-thread maximum key
+  uint32_t wave_bound[NT / 64];  // per-wave lower bounds of the k-th largest key
 };
 
 template <int NT> __device__ void sel_init(SelSh<NT> &sh) {
@@ -218,71 +217,6 @@ template <int V> struct WaveKeys {
   __device__ uint32_t kth(int k) const { return wave_kth_u32<V>(v, k); }
 };
 
-// Up to 64*V composites held by one wave; zero marks an empty entry (keys
-// are never zero).
-template <int V> struct WaveVals {
-  uint64_t v[V];
-  int n;
-  __device__ void load(const uint64_t *src, int n_) {
-    const int lane = threadIdx.x & 63;
-    n = n_;
-#pragma unroll
-    for (int i = 0; i < V; ++i) v[i] = lane + 64 * i < n ? src[lane + 64 * i] : 0ull;
-  }
-  // A threshold T of the top k (1 <= k <= n): the entries >= T are exactly
-  // the k largest.  The key K of the k-th largest comes first (the minimum
-  // when k == n); if more entries than k have keys >= K, the index bits of
-  // the k-th largest are decided among the entries with key K.
-  __device__ uint64_t kth(int k) const {
-    uint32_t hi[V];
-#pragma unroll
-    for (int i = 0; i < V; ++i) hi[i] = (uint32_t)(v[i] >> 32);
-    uint32_t K;
-    if (k == n) {
-      uint32_t m = ~0u;
-#pragma unroll
-      for (int i = 0; i < V; ++i)
-        if (hi[i]) m = min(m, hi[i]);
-      K = uniform_u32(wave_min_u32(m));
-    } else {
-      K = wave_kth_u32<V>(hi, k);
-    }
-    const uint64_t base = (uint64_t)K << 32;
-    int ge = 0;
-#pragma unroll
-    for (int i = 0; i < V; ++i) ge += __popcll(__ballot(hi[i] >= K));
-    if (ge == k) return base;
-    uint32_t a = ~0u, o = 0u;
-#pragma unroll
-    for (int i = 0; i < V; ++i)
-      if (hi[i] == K) {
-        a &= (uint32_t)v[i];
-        o |= (uint32_t)v[i];
-      }
-    wave_and_or_u32(a, o);
-    uint32_t lo = uniform_u32(a), var = uniform_u32(a ^ o);
-    while (var) {
-      const uint32_t bit = 1u << (31 - __clz(var));
-      var &= ~bit;
-      int c = 0;
-#pragma unroll
-      for (int i = 0; i < V; ++i) c += __popcll(__ballot(v[i] >= (base | lo | bit)));
-      if (c >= k) lo |= bit;
-    }
-    return base | lo;
-  }
-};
-
-// Runs f(integral_constant<V>) with the fewest entries per lane that hold n.
-template <typename F> __device__ void with_wave_entries(int n, F &&f) {
-  using std::integral_constant;
-  if (n <= 64) f(integral_constant<int, 1>{});
-  else if (n <= 128) f(integral_constant<int, 2>{});
-  else if (n <= 256) f(integral_constant<int, 4>{});
-  else if (n <= 512) f(integral_constant<int, 8>{});
-  else f(integral_constant<int, kWaveCap / 64>{});
-}
-
 // Block-wide count of composites >= c: wave sums, one LDS atomic per wave,
 // one barrier.  Three counters rotate so a counter is cleared two counts
 // before it is reused.
@@ -357,82 +291,87 @@ __device__ void block_compact(const Src &src, P &&pred, uint64_t *out, int cap, 
   });
 }
 
-// Top k of a row (1 <= k <= n): calls finish(s, T) once, where T is the
-// k-th largest composite and s a source holding every composite >= T (the
-// LDS candidates, or the row itself).  Also leaves the row's max and sum of
-// key values (as floats) in every thread.
-//  1. The k-th largest of the per-thread maximum keys, K0, bounds T from
-//     below (the k threads reaching it own k distinct composites with key
-//     >= K0); one wave finds it.
-//  2. The composites with key >= K0 go to cand[] in LDS (without ties at
-//     K0 at most k * keys per thread).
-//  3. T is the k-th largest candidate: found by one wave from registers when
-//     they fit, else by the block over LDS, else (more than kCandCap) by the
-//     block over the row.  The row's registers are dead on the first two
-//     paths.
-template <int NT, typename Src, typename Fin>
-__device__ void topk_select(const Src &src, int k, SelSh<NT> &sh, uint64_t *cand, float &mx, float &sum,
-                            Fin &&finish) {
+// Top k of a row (1 <= k <= n).  Leaves the row's max and sum of key values
+// (as floats) in every thread, then either calls ranked(x, r) once for each
+// of the top k composites with its rank r (0 = largest) and returns true, or
+// calls unranked(s, T) once, with T the k-th largest composite and s a
+// source holding every composite >= T, and returns false (the same in every
+// thread).
+//  1. Each wave takes the kw-th largest key of its threads' maxima,
+//     kw = ceil(k / waves), as its bound (0, i.e. none, when fewer of its
+//     threads hold keys); the waves' kw-sets are distinct composites, so the
+//     smallest bound B is at most the k-th largest key.  The wave searches
+//     registers with ballots (no LDS, no barrier).
+//  2. Composites with key >= B (at most k times the keys per thread without
+//     ties at B; about k for smooth scores) go to cand[] in LDS.
+//  3. Up to kRankCap candidates are ranked by counting the larger ones; the
+//     top k are those ranked below k.  More candidates: T from a block-wide
+//     search over LDS (up to kCandCap) or over the row itself.
+template <int NT, typename Src, typename Ranked, typename Unranked>
+__device__ bool topk_select(const Src &src, int k, SelSh<NT> &sh, uint64_t *cand, float &mx, float &sum,
+                            Ranked &&ranked, Unranked &&unranked) {
+  constexpr int W = NT / 64;
   const int tid = threadIdx.x, wave = tid >> 6;
-  uint32_t m = 0;
+  uint32_t m[1] = {0};
   float fm = -INFINITY, fs = 0.f;
   src.each([&](uint64_t x) {
-    m = max(m, comp_key(x));
+    m[0] = max(m[0], comp_key(x));
     const float f = key_to_float(comp_key(x));
     fm = fmaxf(fm, f);
     fs += f;
   });
-  sh.kmax[tid] = m;
+  const int kw = (k + W - 1) / W;
+  const int have = __popcll(__ballot(m[0] != 0));
+  const uint32_t bw = have >= kw ? wave_kth_u32<1>(m, kw) : 0u;
   fm = wave_max(fm);
   fs = wave_sum(fs);
   if ((tid & 63) == 0) {
     sh.fmax[wave] = fm;
     sh.fsum[wave] = fs;
+    sh.wave_bound[wave] = bw;
   }
   __syncthreads();
   mx = sh.fmax[0];
   sum = 0.f;
+  uint32_t bound = sh.wave_bound[0];
 #pragma unroll
-  for (int w = 0; w < NT / 64; ++w) {
+  for (int w = 0; w < W; ++w) {
     mx = fmaxf(mx, sh.fmax[w]);
     sum += sh.fsum[w];
+    bound = min(bound, sh.wave_bound[w]);
   }
-  if (k <= NT) {
-    if (wave == 0) {
-      WaveKeys<NT / 64> wk;
-      wk.load(sh.kmax, NT);
-      const uint64_t b = (uint64_t)wk.kth(k) << 32;
-      if (tid == 0) sh.bound = b;
+  // Candidates are sparse: one LDS atomic per candidate.
+  src.each([&](uint64_t x) {
+    if (comp_key(x) >= bound) {
+      const int pos = atomicAdd(&sh.ncand, 1);
+      if (pos < kCandCap) cand[pos] = x;
     }
-  } else if (tid == 0) {
-    sh.bound = 1;  // every composite
-  }
-  __syncthreads();
-  const uint64_t bound = sh.bound;
-  block_compact<NT>(src, [bound](uint64_t x) { return x >= bound; }, cand, kCandCap, &sh.ncand);
+  });
   __syncthreads();
   const int C = sh.ncand;
+  if (C <= kRankCap) {
+    for (int i = tid; i < C; i += NT) {
+      const uint64_t x = cand[i];
+      int r = 0, j = 0;
+      for (; j + 8 <= C; j += 8) {
+        uint64_t y[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) y[u] = cand[j + u];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) r += y[u] > x;
+      }
+      for (; j < C; ++j) r += cand[j] > x;
+      if (r < k) ranked(x, r);
+    }
+    return true;
+  }
   if (C <= kCandCap) {
     const LdsComps<NT> lc{cand, C};
-    uint64_t T;
-    if (C <= kWaveCap) {
-      if (wave == 0) {
-        with_wave_entries(C, [&](auto vc) {
-          WaveVals<decltype(vc)::value> wv;
-          wv.load(cand, C);
-          const uint64_t t = wv.kth(k);
-          if (tid == 0) sh.thresh = t;
-        });
-      }
-      __syncthreads();
-      T = sh.thresh;
-    } else {
-      T = block_kth<NT>(lc, k, sh);
-    }
-    finish(lc, T);
+    unranked(lc, block_kth<NT>(lc, k, sh));
   } else {
-    finish(src, block_kth<NT>(src, k, sh));
+    unranked(src, block_kth<NT>(src, k, sh));
   }
+  return false;
 }
 
 // -------------------------------------------------------- union ranking
@@ -718,14 +657,16 @@ template <int NT, typename Src>
 __device__ void coarse_pick(const Src &src, int k, uint32_t *bitmap, SelSh<NT> &sh, uint64_t *cand,
                             float *stats, int row) {
   float mx, sum;
-  topk_select<NT>(src, k, sh, cand, mx, sum, [&](const auto &s2, uint64_t T) {
-    s2.each([&](uint64_t x) {
-      if (x >= T) {
-        const int i = comp_index(x);
-        atomicOr(&bitmap[i >> 5], 1u << (i & 31));
-      }
-    });
-  });
+  auto mark = [&](uint64_t x) {
+    const int i = comp_index(x);
+    atomicOr(&bitmap[i >> 5], 1u << (i & 31));
+  };
+  topk_select<NT>(src, k, sh, cand, mx, sum, [&](uint64_t x, int) { mark(x); },
+                  [&](const auto &s2, uint64_t T) {
+                    s2.each([&](uint64_t x) {
+                      if (x >= T) mark(x);
+                    });
+                  });
   if (threadIdx.x == 0) {
     stats[2 * row] = mx;
     stats[2 * row + 1] = sum;
@@ -850,15 +791,6 @@ __global__ void __launch_bounds__(256) fine_scan_kernel(
 // (max, sum), and zeroes the keys for the next scan.  Block 0 also writes
 // P', and with a fresh union the compact union list, its size and the
 // coarse telemetry.
-template <typename Src>
-__device__ void fine_pick(const Src &src, int k, SelSh<kFineSelThreads> &sh, uint64_t *cand, uint64_t *sel,
-                          float &mx, float &sum) {
-  constexpr int NT = kFineSelThreads;
-  topk_select<NT>(src, k, sh, cand, mx, sum, [&](const auto &s2, uint64_t T) {
-    block_compact<NT>(s2, [T](uint64_t x) { return x >= T; }, sel, k, &sh.nsel);
-  });
-}
-
 // Dynamic LDS: ubits[words] | urank[words + 1] | (8-aligned) cand[kCandCap]
 // | sel[kp2] | stage[stage_cap].  A row of at most stage_cap keys is copied
 // to LDS once (zeroing it in memory on the way); longer rows are re-read.
@@ -886,33 +818,6 @@ __global__ void __launch_bounds__(kFineSelThreads) fine_select_kernel(
   const int n = U * page_size + partial_len;
   const int k = min(width, n);
   uint32_t *src = keys + (int64_t)b * ld;  // 256-byte aligned rows
-  float mx, sum;
-  if (n <= stage_cap) {
-    // The scan accumulates with atomicMax: leave the row zeroed for the next call.
-    uint4 *src4 = reinterpret_cast<uint4 *>(src);
-    uint4 *st4 = reinterpret_cast<uint4 *>(stage);
-    const int n4 = (n + 3) / 4;  // the row's padding past n is zero
-#pragma unroll 8
-    for (int i = tid; i < n4; i += NT) {
-      st4[i] = src4[i];
-      src4[i] = make_uint4(0, 0, 0, 0);
-    }
-    __syncthreads();
-    fine_pick(LdsKeys<NT>{stage, n}, k, sh, cand, sel, mx, sum);
-  } else {
-    MemKeys<NT> mk;
-    mk.load(src, n);
-    fine_pick(mk, k, sh, cand, sel, mx, sum);
-    __syncthreads();
-    for (int i = tid; i < n; i += NT) src[i] = 0u;
-  }
-  if (tid == 0) {
-    fine_stats[2 * b] = mx;
-    fine_stats[2 * b + 1] = sum;
-  }
-  __syncthreads();
-  // Order the k selected composites descending: by counting for k <= NT,
-  // else by a bitonic sort in place.
   const int64_t split = (int64_t)U * page_size;
   auto emit = [&](int slot, uint64_t x) {
     const int cand_i = comp_index(x);
@@ -929,46 +834,74 @@ __global__ void __launch_bounds__(kFineSelThreads) fine_select_kernel(
       idx_out[(int64_t)b * width + slot] = gid;
     }
   };
-  if (k <= NT) {
-    // Rank of sel[i] = entries greater than it; with k <= NT / 2 two
-    // threads count one half each.  cand is free once sel holds the top k.
-    const int parts = 2 * k <= NT ? 2 : 1, half = (k + parts - 1) / parts;
-    int *part_rank = reinterpret_cast<int *>(cand);
-    if (tid < parts * k) {
-      const int i = tid % k, part = tid / k;
-      const uint64_t x = sel[i];
-      const int j1 = min(k, (part + 1) * half);
-      int r = 0, j = part * half;
-      for (; j + 8 <= j1; j += 8) {
-        uint64_t y[8];
-#pragma unroll
-        for (int u = 0; u < 8; ++u) y[u] = sel[j + u];
-#pragma unroll
-        for (int u = 0; u < 8; ++u) r += y[u] > x;
-      }
-      for (; j < j1; ++j) r += sel[j] > x;
-      part_rank[part * k + i] = r;
+  // Ranked: each selected composite goes straight to its slot.  Unranked:
+  // the top k go to sel[] and are ordered below.
+  auto ranked = [&](uint64_t x, int r) { emit(r, x); };
+  auto unranked = [&](const auto &s2, uint64_t T) {
+    block_compact<NT>(s2, [T](uint64_t x) { return x >= T; }, sel, k, &sh.nsel);
+  };
+  float mx, sum;
+  bool done;
+  if (n <= stage_cap) {
+    // The scan accumulates with atomicMax: leave the row zeroed for the next call.
+    uint4 *src4 = reinterpret_cast<uint4 *>(src);
+    uint4 *st4 = reinterpret_cast<uint4 *>(stage);
+    const int n4 = (n + 3) / 4;  // the row's padding past n is zero
+#pragma unroll 8
+    for (int i = tid; i < n4; i += NT) {
+      st4[i] = src4[i];
+      src4[i] = make_uint4(0, 0, 0, 0);
     }
     __syncthreads();
-    if (tid < k) emit(part_rank[tid] + (parts == 2 ? part_rank[k + tid] : 0), sel[tid]);
+    done = topk_select<NT>(LdsKeys<NT>{stage, n}, k, sh, cand, mx, sum, ranked, unranked);
   } else {
-    for (int i = k + tid; i < kp2; i += NT) sel[i] = 0ull;
+    MemKeys<NT> mk;
+    mk.load(src, n);
+    done = topk_select<NT>(mk, k, sh, cand, mx, sum, ranked, unranked);
     __syncthreads();
-    for (int size = 2; size <= kp2; size <<= 1) {
-      for (int stride = size >> 1; stride > 0; stride >>= 1) {
-        for (int t = tid; t < kp2 / 2; t += NT) {
-          const int i = 2 * stride * (t / stride) + (t % stride), j = i + stride;
-          const bool desc = (i & size) == 0;
-          const uint64_t x = sel[i], y = sel[j];
-          if ((x < y) == desc) {
-            sel[i] = y;
-            sel[j] = x;
-          }
+    for (int i = tid; i < n; i += NT) src[i] = 0u;
+  }
+  if (tid == 0) {
+    fine_stats[2 * b] = mx;
+    fine_stats[2 * b + 1] = sum;
+  }
+  if (!done) {
+    // Order the k entries of sel[] descending: by counting for k <= NT, else
+    // by a bitonic sort in place.
+    __syncthreads();
+    if (k <= NT) {
+      if (tid < k) {
+        const uint64_t x = sel[tid];
+        int r = 0, j = 0;
+        for (; j + 8 <= k; j += 8) {
+          uint64_t y[8];
+#pragma unroll
+          for (int u = 0; u < 8; ++u) y[u] = sel[j + u];
+#pragma unroll
+          for (int u = 0; u < 8; ++u) r += y[u] > x;
         }
-        __syncthreads();
+        for (; j < k; ++j) r += sel[j] > x;
+        emit(r, x);
       }
+    } else {
+      for (int i = k + tid; i < kp2; i += NT) sel[i] = 0ull;
+      __syncthreads();
+      for (int size = 2; size <= kp2; size <<= 1) {
+        for (int stride = size >> 1; stride > 0; stride >>= 1) {
+          for (int t = tid; t < kp2 / 2; t += NT) {
+            const int i = 2 * stride * (t / stride) + (t % stride), j = i + stride;
+            const bool desc = (i & size) == 0;
+            const uint64_t x = sel[i], y = sel[j];
+            if ((x < y) == desc) {
+              sel[i] = y;
+              sel[j] = x;
+            }
+          }
+          __syncthreads();
+        }
+      }
+      for (int j = tid; j < k; j += NT) emit(j, sel[j]);
     }
-    for (int j = tid; j < k; j += NT) emit(j, sel[j]);
   }
   if (b != 0) return;
   if (tid == 0) counters[3] = k;

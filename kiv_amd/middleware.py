@@ -221,14 +221,14 @@ class KIVMiddleware:
             scaling = kwargs.get("scaling")
             if scaling is None:
                 scaling = fallback_scaling
-            cold_k, cold_v = store.retrieve_top_kv(query, scaling, kiv_config,
-                                                   step=getattr(cache, "_decode_step", -1))
-            if cold_k is None:
-                return original_fn(module, query, key, value, attention_mask, **kwargs)
+            step = getattr(cache, "_decode_step", -1)
             hot_len = key.shape[2]
             # The mask was built before this step's eviction: keep its last hot_len columns.
             if attention_mask is not None and attention_mask.shape[-1] > hot_len:
                 attention_mask = attention_mask[..., -hot_len:]
+            cold_k, cold_v = store.retrieve_top_kv(query, scaling, kiv_config, step=step)
+            if cold_k is None:
+                return original_fn(module, query, key, value, attention_mask, **kwargs)
             if _merged_kernel_applies(module, query, key, attention_mask, kwargs):
                 return decode_attention(query, cold_k, cold_v, key, value, attention_mask, scaling), None
             key = torch.cat([cold_k, key], dim=2)
