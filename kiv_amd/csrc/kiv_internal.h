@@ -97,9 +97,9 @@ struct kiv_store {
   kiv::DevBuf row_stats;     // [R][2] f32 (max, sum) + [B][2] fine stats
   kiv::DevBuf bitmap;        // [ceil(N/32)] u32, zero between calls
   kiv::DevBuf page_list;     // [N] i32 union pages ascending
-  kiv::DevBuf counters;      // i32: [0]=U, [1]=coarse done, [2]=fine done, [3]=P actual
+  kiv::DevBuf counters;      // i32: [0] = U, the union size of the last coarse pass
   kiv::DevBuf fine_keys;     // [B][ld] u32
-  kiv::DevBuf sel_cand;      // [B][P'] i32 candidate index per output slot
+  kiv::DevBuf sel_list;      // [B][list_ld] u64 top-P' candidates + [B] i32 counts
   bool union_valid = false;  // page_list / U hold the last coarse pass
   int64_t union_rows = 0;    // B*Hq*Q of that pass (bounds reuse)
   int64_t union_max = 0;     // grid bound of that pass

@@ -5,8 +5,8 @@
 // per-row top pages, union  :211-212, :224 (topk, unique)     coarse_select_kernel
 // fine per-token scores,    :332-338 (matmul * scaling,        fine_scan_kernel
 //   max over heads/queries    amax over dims 1, 2)
-// top-P, id mapping          :340-347 (topk, gather ids)        fine_select_kernel
-// K/V of the top-P           :358-362 (gather)                  gather_kernel
+// top-P, id mapping          :340-347 (topk, gather ids)        fine_select_kernel +
+// K/V of the top-P           :358-362 (gather)                    gather_kernel
 //
 // Query rows are (b, q head, q position) triples.  Row h reads KV row
 // b*Hkv + h / (Hq/Hkv), so no GQA expansion is copied.  Scores are ranked
@@ -16,9 +16,11 @@
 // page, i.e. ascending global token id.
 //
 // The kernels hand data to each other only across kernel boundaries: the
-// coarse select ORs each row's pages into a page bitmap; the fine scan and
-// fine select rank the bitmap themselves (a prefix count of its words in
-// LDS); the fine select's block 0 writes the compact union list; the gather
+// coarse select ORs each row's pages into a page bitmap; every fine scan
+// block ranks the bitmap itself (a prefix count of its words in LDS) and
+// block (0, 0) also writes the compact union list, its size and the coarse
+// telemetry; the fine select lists each batch row's candidates for the
+// top P'; the gather ranks the list, places each selected row at its rank,
 // clears the bitmap and finishes the telemetry.  No kernel waits on another
 // block of its own grid.
 #include <algorithm>
@@ -30,7 +32,7 @@
 
 namespace kiv {
 
-constexpr int kMaxOut = 4096;       // largest top-P the fine select sorts in LDS
+constexpr int kMaxOut = 4096;       // largest top-P (list entries the gather ranks)
 constexpr int kScanThreads = 256;   // coarse scan block (4 waves)
 constexpr int kFineSelThreads = 512;
 constexpr int kMaxWords = 4096;     // bitmap words ranked in LDS (131072 pages)
@@ -112,15 +114,6 @@ template <int NT> struct MemKeys {
       for (int u = 0; u < B; ++u) f(comp_of(v[u], idx + u * NT));
     }
     for (; idx < n; idx += NT) f(comp_of(p[idx], idx));
-  }
-};
-
-// Keys of a row staged in LDS.
-template <int NT> struct LdsKeys {
-  const uint32_t *k;
-  int n;
-  template <typename F> __device__ void each(F &&f) const {
-    for (int idx = threadIdx.x; idx < n; idx += NT) f(comp_of(k[idx], idx));
   }
 };
 
@@ -696,7 +689,10 @@ __global__ void __launch_bounds__(NT) coarse_select_kernel(const uint32_t *__res
 // r = b*Hkv + h in LDS and walks work items x, x + nb, ...; an item is a
 // slice of tpi tokens of a union page (items [0, U*nsplit)) or of the
 // partial page (the items after).  Union pages come from the bitmap
-// (ranked in LDS) or from the stored union list.  The max over the block's
+// (ranked in LDS) or from the stored union list; with the bitmap, block
+// (0, 0) also stores the union list, its size and the coarse telemetry
+// (max over rows, mean over rows and pages) for the later kernels.  The
+// max over the block's
 // rows is folded into the candidate's key with atomicMax, which completes
 // the max over kv heads across blocks (keys are order-preserving; the
 // select zeroes them).
@@ -708,13 +704,51 @@ __global__ void __launch_bounds__(NT) coarse_select_kernel(const uint32_t *__res
 // 49 GB/s); HBM rows best in 32-token slices over 2048 blocks.
 constexpr int kFineUT = 4;  // tokens in flight per lane group
 
+// Block (0, 0) of a fresh union: page_list / pages_out <- the union pages
+// ascending, counters[0] / union_out <- U, and the coarse telemetry.
+template <int DT>
+__device__ void publish_union(const uint32_t *ubits, const int *urank, int words, int U, int32_t *page_list,
+                              int32_t *pages_out, int32_t *counters, int32_t *union_out,
+                              const float *coarse_stats, int rows, int n_pages, int round, float *stats_out,
+                              double *stats_accum) {
+  for (int v = threadIdx.x; v < U; v += blockDim.x) {
+    const int page = union_page(ubits, urank, words, v);
+    page_list[v] = page;
+    if (pages_out) pages_out[v] = page;
+  }
+  if (threadIdx.x >= 64) return;
+  float m = -INFINITY;
+  double t = 0.0;
+  for (int r = threadIdx.x; r < rows; r += 64) {
+    m = fmaxf(m, coarse_stats[2 * r]);
+    t += coarse_stats[2 * r + 1];
+  }
+  m = wave_max(m);
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) t += __shfl_xor(t, o, 64);
+  if (threadIdx.x != 0) return;
+  counters[0] = U;
+  if (union_out) union_out[0] = U;
+  float mean = (float)(t / ((double)rows * (double)n_pages));
+  if (round) mean = round_act<DT>(mean);
+  if (stats_out) {
+    stats_out[0] = m;
+    stats_out[1] = mean;
+  }
+  if (stats_accum) {
+    stats_accum[0] += (double)m;
+    stats_accum[1] += (double)mean;
+  }
+}
+
 template <int DT, int LG>
 __global__ void __launch_bounds__(256) fine_scan_kernel(
-    int union_src, const uint32_t *__restrict__ bitmap, int words, const int32_t *__restrict__ page_list,
-    const int32_t *__restrict__ counters, const uint64_t *__restrict__ ktab, int chunk_shift, int64_t page_bytes,
-    const char *__restrict__ part_k, int partial_len, int page_size, int tpi, int hkv, int head_dim,
-    const char *__restrict__ q, int64_t qs0, int64_t qs1, int64_t qs2, int hq, int qlen, float scale, int round,
-    uint32_t *__restrict__ out, int64_t ld) {
+    int union_src, const uint32_t *__restrict__ bitmap, int words, int32_t *page_list, int32_t *counters,
+    const uint64_t *__restrict__ ktab, int chunk_shift, int64_t page_bytes, const char *__restrict__ part_k,
+    int partial_len, int page_size, int tpi, int hkv, int head_dim, const char *__restrict__ q, int64_t qs0,
+    int64_t qs1, int64_t qs2, int hq, int qlen, float scale, int round, uint32_t *__restrict__ out, int64_t ld,
+    const float *__restrict__ coarse_stats, int rows, int n_pages, int32_t *pages_out, int32_t *union_out,
+    float *stats_out, double *stats_accum) {
   constexpr int VEC = Elem<DT>::VEC, EB = Elem<DT>::BYTES;
   constexpr int UT = kFineUT;
   constexpr int NSLOT = 256 / LG;
@@ -733,8 +767,14 @@ __global__ void __launch_bounds__(256) fine_scan_kernel(
         load16(q + ((int64_t)b * qs0 + (int64_t)h * qs1 + (int64_t)qp * qs2 + c * VEC) * EB);
   }
   int U = 0;
-  if (union_src == UNION_BITMAP) U = rank_union<256>(bitmap, words, ubits, urank, scan_tmp);
-  else if (union_src == UNION_LIST) U = counters[0];
+  if (union_src == UNION_BITMAP) {
+    U = rank_union<256>(bitmap, words, ubits, urank, scan_tmp);
+    if (blockIdx.x == 0 && blockIdx.y == 0)
+      publish_union<DT>(ubits, urank, words, U, page_list, pages_out, counters, union_out, coarse_stats, rows,
+                        n_pages, round, stats_out, stats_accum);
+  } else if (union_src == UNION_LIST) {
+    U = counters[0];
+  }
   __syncthreads();
   const int nsplit = (page_size + tpi - 1) / tpi;
   const int page_items = U * nsplit;
@@ -785,183 +825,209 @@ __global__ void __launch_bounds__(256) fine_scan_kernel(
 }
 
 // ----------------------------------------------------------- fine select
-// One block per batch row: top-P' of the C candidate keys, sorted by score
-// descending (ties: lower candidate index first).  Writes the candidate
-// index per output slot, the global token id and the row's telemetry
-// (max, sum), and zeroes the keys for the next scan.  Block 0 also writes
-// P', and with a fresh union the compact union list, its size and the
-// coarse telemetry.
-// Dynamic LDS: ubits[words] | urank[words + 1] | (8-aligned) cand[kCandCap]
-// | sel[kp2] | stage[stage_cap].  A row of at most stage_cap keys is copied
-// to LDS once (zeroing it in memory on the way); longer rows are re-read.
-template <int DT>
-__global__ void __launch_bounds__(kFineSelThreads) fine_select_kernel(
-    uint32_t *__restrict__ keys, int64_t ld, int union_src, const uint32_t *__restrict__ bitmap, int words,
-    int kp2, int stage_cap, int32_t *page_list, int32_t *counters, int page_size, int partial_len,
-    int64_t num_finalized, int width, int round, const float *__restrict__ coarse_stats, int rows, int n_pages,
-    float *fine_stats, int32_t *__restrict__ sel_cand, int64_t *__restrict__ idx_out, int32_t *pages_out,
-    int32_t *union_out, float *stats_out, double *stats_accum) {
-  constexpr int NT = kFineSelThreads;
-  __shared__ SelSh<NT> sh;
-  extern __shared__ uint64_t fsm[];
-  const int tid = threadIdx.x, b = blockIdx.x;
-  const int wpad = (2 * words + 2) & ~1;  // 32-bit slots of ubits + urank, even
-  uint32_t *ubits = reinterpret_cast<uint32_t *>(fsm);
-  int *urank = reinterpret_cast<int *>(ubits + words);
-  uint64_t *cand = fsm + wpad / 2;
-  uint64_t *sel = cand + kCandCap;
-  uint32_t *stage = reinterpret_cast<uint32_t *>(sel + kp2);
-  sel_init(sh);
-  int U = 0;
-  if (union_src == UNION_BITMAP) U = rank_union<NT>(bitmap, words, ubits, urank, sh.scan_tmp);
-  else if (union_src == UNION_LIST) U = counters[0];
-  const int n = U * page_size + partial_len;
-  const int k = min(width, n);
-  uint32_t *src = keys + (int64_t)b * ld;  // 256-byte aligned rows
-  const int64_t split = (int64_t)U * page_size;
-  auto emit = [&](int slot, uint64_t x) {
-    const int cand_i = comp_index(x);
-    sel_cand[(int64_t)b * width + slot] = cand_i;
-    if (idx_out) {
-      int64_t gid;
-      if ((int64_t)cand_i < split) {
-        const int v = cand_i / page_size;
-        const int64_t page = union_src == UNION_BITMAP ? union_page(ubits, urank, words, v) : page_list[v];
-        gid = page * page_size + cand_i % page_size;
-      } else {
-        gid = num_finalized + ((int64_t)cand_i - split);
+// One block per batch row b lists the candidates of the row's top k =
+// min(P', C) keys: the composites whose key is at least a bound B <= the
+// k-th largest key (so the top k are among them, ties at B included).  The
+// gather ranks the list by counting.  The bound: each wave takes the kw-th
+// largest (kw = ceil(k / waves)) of the maxima of its threads' four key
+// subsets (sub-slots); the maxima are distinct keys, so every wave holds kw
+// keys >= its bound and the smallest bound B leaves at least k keys >= B.
+// A wave with fewer than kw nonzero maxima sets no bound.  When more than
+// kRankCap composites pass B, the block finds the k-th largest composite T
+// and lists exactly the k composites >= T instead.  The block also writes
+// the row's telemetry (max, sum of scores) and zeroes the keys for the next
+// scan, which accumulates with atomicMax.
+
+// A row's keys in registers as 16-byte chunks (keys 4c .. 4c + 3), dealt
+// round-robin to the waves: lane l of wave w owns chunks
+// w + W * (l + 64 i).  Any run of high keys (the pages of one hot segment
+// are consecutive candidates) then spreads over every wave, which keeps the
+// per-wave bounds close to the k-th largest key.  Sub-slot j of a thread
+// holds its keys 4c + j.
+template <int NT, int V> struct RegKeys4 {
+  static constexpr int W = NT / 64;
+  uint4 v[V];
+  int n;
+  __device__ static int chunk(int i) { return (threadIdx.x >> 6) + W * ((threadIdx.x & 63) + 64 * i); }
+  __device__ void load(const uint32_t *p, int n_) {
+    n = n_;
+    const int n4 = (n + 3) >> 2;
+    const uint4 *p4 = reinterpret_cast<const uint4 *>(p);
+#pragma unroll
+    for (int i = 0; i < V; ++i) {
+      const int c = chunk(i);
+      v[i] = c < n4 ? p4[c] : make_uint4(0, 0, 0, 0);
+    }
+  }
+  template <typename F> __device__ void each_slot(F &&f) const {
+#pragma unroll
+    for (int i = 0; i < V; ++i) {
+      const int base = 4 * chunk(i);
+      if (base < n) {
+        f(comp_of(v[i].x, base), 0);
+        if (base + 1 < n) f(comp_of(v[i].y, base + 1), 1);
+        if (base + 2 < n) f(comp_of(v[i].z, base + 2), 2);
+        if (base + 3 < n) f(comp_of(v[i].w, base + 3), 3);
       }
-      idx_out[(int64_t)b * width + slot] = gid;
     }
-  };
-  // Ranked: each selected composite goes straight to its slot.  Unranked:
-  // the top k go to sel[] and are ordered below.
-  auto ranked = [&](uint64_t x, int r) { emit(r, x); };
-  auto unranked = [&](const auto &s2, uint64_t T) {
-    block_compact<NT>(s2, [T](uint64_t x) { return x >= T; }, sel, k, &sh.nsel);
-  };
-  float mx, sum;
-  bool done;
-  if (n <= stage_cap) {
-    // The scan accumulates with atomicMax: leave the row zeroed for the next call.
-    uint4 *src4 = reinterpret_cast<uint4 *>(src);
-    uint4 *st4 = reinterpret_cast<uint4 *>(stage);
-    const int n4 = (n + 3) / 4;  // the row's padding past n is zero
-#pragma unroll 8
-    for (int i = tid; i < n4; i += NT) {
-      st4[i] = src4[i];
-      src4[i] = make_uint4(0, 0, 0, 0);
+  }
+  template <typename F> __device__ void each(F &&f) const {
+    each_slot([&](uint64_t x, int) { f(x); });
+  }
+};
+
+// A row's keys re-read from memory for each pass (rows too long for
+// registers), strided over the block; sub-slot = load batch position & 3.
+template <int NT> struct MemKeys4 {
+  const uint32_t *p;
+  int n;
+  template <typename F> __device__ void each_slot(F &&f) const {
+    constexpr int B = 8;  // loads in flight per thread
+    int idx = threadIdx.x;
+    for (; idx + (B - 1) * NT < n; idx += B * NT) {
+      uint32_t v[B];
+#pragma unroll
+      for (int u = 0; u < B; ++u) v[u] = p[idx + u * NT];
+#pragma unroll
+      for (int u = 0; u < B; ++u) f(comp_of(v[u], idx + u * NT), u & 3);
     }
-    __syncthreads();
-    done = topk_select<NT>(LdsKeys<NT>{stage, n}, k, sh, cand, mx, sum, ranked, unranked);
+    for (; idx < n; idx += NT) f(comp_of(p[idx], idx), 0);
+  }
+  template <typename F> __device__ void each(F &&f) const {
+    each_slot([&](uint64_t x, int) { f(x); });
+  }
+};
+
+// Lists the candidates of the top k (1 <= k <= n) of src into out[] (at
+// most kRankCap, or exactly k after the fallback) and returns their count;
+// leaves the row's max and sum of scores in mx / sum (thread 0).  The
+// k-th largest search over the whole row, needed only when more than
+// kCandCap keys pass the bound (mass ties), walks `mem`, the row in memory.
+template <int NT, typename Src>
+__device__ int fine_candidates(const Src &src, const MemKeys4<NT> &mem, int k, SelSh<NT> &sh, uint64_t *cand,
+                               uint64_t *out, float &mx, float &sum) {
+  constexpr int W = NT / 64;
+  const int tid = threadIdx.x, wave = tid >> 6;
+  uint32_t m[4] = {0u, 0u, 0u, 0u};
+  float fm = -INFINITY, fs = 0.f;
+  src.each_slot([&](uint64_t x, int j) {
+    const uint32_t key = comp_key(x);
+    m[j] = max(m[j], key);
+    const float f = key_to_float(key);
+    fm = fmaxf(fm, f);
+    fs += f;
+  });
+  const int kw = (k + W - 1) / W;
+  int have = 0;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) have += __popcll(__ballot(m[j] != 0u));
+  const uint32_t bw = have >= kw ? wave_kth_u32<4>(m, kw) : 0u;
+  fm = wave_max(fm);
+  fs = wave_sum(fs);
+  if ((tid & 63) == 0) {
+    sh.fmax[wave] = fm;
+    sh.fsum[wave] = fs;
+    sh.wave_bound[wave] = bw;
+  }
+  __syncthreads();
+  mx = sh.fmax[0];
+  sum = 0.f;
+  uint32_t bound = sh.wave_bound[0];
+#pragma unroll
+  for (int w = 0; w < W; ++w) {
+    mx = fmaxf(mx, sh.fmax[w]);
+    sum += sh.fsum[w];
+    bound = min(bound, sh.wave_bound[w]);
+  }
+  // Candidates are sparse: one LDS atomic per candidate.
+  src.each([&](uint64_t x) {
+    if (comp_key(x) >= bound) {
+      const int pos = atomicAdd(&sh.ncand, 1);
+      if (pos < kCandCap) cand[pos] = x;
+    }
+  });
+  __syncthreads();
+  const int C = sh.ncand;
+  if (C <= kRankCap) {
+    for (int i = tid; i < C; i += NT) out[i] = cand[i];
+    return C;
+  }
+  auto ge = [](uint64_t t) { return [t](uint64_t x) { return x >= t; }; };
+  if (C <= kCandCap) {
+    const LdsComps<NT> lc{cand, C};
+    block_compact<NT>(lc, ge(block_kth<NT>(lc, k, sh)), out, k, &sh.nsel);
   } else {
-    MemKeys<NT> mk;
-    mk.load(src, n);
-    done = topk_select<NT>(mk, k, sh, cand, mx, sum, ranked, unranked);
-    __syncthreads();
-    for (int i = tid; i < n; i += NT) src[i] = 0u;
+    block_compact<NT>(mem, ge(block_kth<NT>(mem, k, sh)), out, k, &sh.nsel);
   }
-  if (tid == 0) {
-    fine_stats[2 * b] = mx;
-    fine_stats[2 * b + 1] = sum;
-  }
-  if (!done) {
-    // Order the k entries of sel[] descending: by counting for k <= NT, else
-    // by a bitonic sort in place.
-    __syncthreads();
-    if (k <= NT) {
-      if (tid < k) {
-        const uint64_t x = sel[tid];
-        int r = 0, j = 0;
-        for (; j + 8 <= k; j += 8) {
-          uint64_t y[8];
-#pragma unroll
-          for (int u = 0; u < 8; ++u) y[u] = sel[j + u];
-#pragma unroll
-          for (int u = 0; u < 8; ++u) r += y[u] > x;
-        }
-        for (; j < k; ++j) r += sel[j] > x;
-        emit(r, x);
-      }
-    } else {
-      for (int i = k + tid; i < kp2; i += NT) sel[i] = 0ull;
-      __syncthreads();
-      for (int size = 2; size <= kp2; size <<= 1) {
-        for (int stride = size >> 1; stride > 0; stride >>= 1) {
-          for (int t = tid; t < kp2 / 2; t += NT) {
-            const int i = 2 * stride * (t / stride) + (t % stride), j = i + stride;
-            const bool desc = (i & size) == 0;
-            const uint64_t x = sel[i], y = sel[j];
-            if ((x < y) == desc) {
-              sel[i] = y;
-              sel[j] = x;
-            }
-          }
-          __syncthreads();
-        }
-      }
-      for (int j = tid; j < k; j += NT) emit(j, sel[j]);
-    }
-  }
-  if (b != 0) return;
-  if (tid == 0) counters[3] = k;
-  if (union_src != UNION_BITMAP) return;
-  for (int v = tid; v < U; v += NT) {
-    const int page = union_page(ubits, urank, words, v);
-    page_list[v] = page;
-    if (pages_out) pages_out[v] = page;
-  }
-  if (tid < 64) {
-    float m = -INFINITY;
-    double t = 0.0;
-    for (int r = tid; r < rows; r += 64) {
-      m = fmaxf(m, coarse_stats[2 * r]);
-      t += coarse_stats[2 * r + 1];
-    }
-    m = wave_max(m);
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) t += __shfl_xor(t, o, 64);
-    if (tid != 0) return;
-    counters[0] = U;
-    if (union_out) union_out[0] = U;
-    float mean = (float)(t / ((double)rows * (double)n_pages));
-    if (round) mean = round_act<DT>(mean);
-    if (stats_out) {
-      stats_out[0] = m;
-      stats_out[1] = mean;
-    }
-    if (stats_accum) {
-      stats_accum[0] += (double)m;
-      stats_accum[1] += (double)mean;
-    }
-  }
+  return k;
 }
 
-// LDS of the fine select: room kept for the static part, and the dynamic
-// part before the key stage.
-constexpr size_t kFineStaticLds = 8192;
-static size_t fine_select_lds(int words, int kp2) {
-  return (size_t)((2 * words + 2) & ~1) * 4 + (size_t)kCandCap * 8 + (size_t)kp2 * 8;
+// V = 16-byte key chunks per thread kept in registers: rows of up to
+// 4 * V * kFineSelThreads keys are read once; longer rows are re-read.
+template <int V>
+__global__ void __launch_bounds__(kFineSelThreads) fine_select_kernel(
+    uint32_t *__restrict__ keys, int64_t ld, const int32_t *__restrict__ counters, int has_pages, int page_size,
+    int partial_len, int width, float *__restrict__ fine_stats, uint64_t *__restrict__ list, int64_t list_ld,
+    int32_t *__restrict__ list_count) {
+  constexpr int NT = kFineSelThreads;
+  __shared__ SelSh<NT> sh;
+  __shared__ uint64_t cand[kCandCap];
+  sel_init(sh);
+  const int b = blockIdx.x;
+  const int U = has_pages ? counters[0] : 0;
+  const int n = U * page_size + partial_len;
+  const int k = min(width, n);
+  uint32_t *row = keys + (int64_t)b * ld;  // 256-byte aligned rows, zero past n
+  uint64_t *out = list + (int64_t)b * list_ld;
+  const MemKeys4<NT> mk{row, n};
+  float mx, sum;
+  int C;
+  if (n <= 4 * V * NT) {
+    RegKeys4<NT, V> rk;
+    rk.load(row, n);
+    C = fine_candidates<NT>(rk, mk, k, sh, cand, out, mx, sum);
+  } else {
+    C = fine_candidates<NT>(mk, mk, k, sh, cand, out, mx, sum);
+  }
+  __syncthreads();
+  uint4 *row4 = reinterpret_cast<uint4 *>(row);
+  for (int i = threadIdx.x; i < (n + 3) / 4; i += NT) row4[i] = make_uint4(0, 0, 0, 0);
+  if (threadIdx.x == 0) {
+    fine_stats[2 * b] = mx;
+    fine_stats[2 * b + 1] = sum;
+    list_count[b] = C;
+  }
 }
 
 // ----------------------------------------------------------------- gather
-// k_out / v_out [B][Hkv][width][D] slot j <- candidate sel_cand[b][j] of kv
-// head h, from the arena (finished pages) or the partial page.  Block 0
-// also finishes the fine telemetry and clears the page bitmap.
+// Grid (ceil(max list / kGatherCands), B).  Block (x, b) takes list entries
+// x * kGatherCands + w (w = wave): each wave ranks its entry by counting
+// the larger entries of the list; an entry ranked r < k is selected, and
+// the block copies its K and V rows of every kv head to slot r of k_out /
+// v_out ([B][Hkv][width][D]) from the arena (union pages) or the partial
+// page, and its global token id to idx_out[b][r].  Block (0, 0) also
+// finishes the fine telemetry and clears the page bitmap.
+constexpr int kGatherCands = 4;
+
 template <int DT>
 __global__ void __launch_bounds__(256) gather_kernel(
-    const int32_t *__restrict__ sel_cand, const int32_t *__restrict__ counters, int has_pages,
-    const int32_t *__restrict__ page_list, const uint64_t *__restrict__ ktab,
-    const uint64_t *__restrict__ vtab, int chunk_shift, int64_t page_bytes, const char *__restrict__ part_k,
-    const char *__restrict__ part_v, int page_size, int partial_len, int batch, int hkv, int head_dim, int width,
-    int cpr, char *__restrict__ k_out, char *__restrict__ v_out, uint32_t *bitmap, int clear_words,
+    const uint64_t *__restrict__ list, int64_t list_ld, const int32_t *__restrict__ list_count,
+    const int32_t *__restrict__ counters, int has_pages, const int32_t *__restrict__ page_list,
+    const uint64_t *__restrict__ ktab, const uint64_t *__restrict__ vtab, int chunk_shift, int64_t page_bytes,
+    const char *__restrict__ part_k, const char *__restrict__ part_v, int page_size, int partial_len,
+    int64_t num_finalized, int batch, int hkv, int head_dim, int width, int cpr, char *__restrict__ k_out,
+    char *__restrict__ v_out, int64_t *__restrict__ idx_out, uint32_t *bitmap, int clear_words,
     const float *__restrict__ fine_stats, int round, float *stats_out, double *stats_accum) {
   constexpr int VEC = Elem<DT>::VEC, EB = Elem<DT>::BYTES;
+  __shared__ int slot_of[kGatherCands], cand_of[kGatherCands];
+  const int b = blockIdx.y, tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int U = has_pages ? counters[0] : 0;
-  if (blockIdx.x == 0) {
-    for (int w = threadIdx.x; w < clear_words; w += 256) bitmap[w] = 0u;
-    if (threadIdx.x == 0) {
-      const int n = U * page_size + partial_len;
+  const int64_t split = (int64_t)U * page_size;
+  const int n = (int)split + partial_len;
+  const int k = min(width, n);
+  if (blockIdx.x == 0 && b == 0) {
+    for (int w = tid; w < clear_words; w += 256) bitmap[w] = 0u;
+    if (tid == 0) {
       float m = -INFINITY;
       double t = 0.0;
       for (int r = 0; r < batch; ++r) {
@@ -980,36 +1046,60 @@ __global__ void __launch_bounds__(256) gather_kernel(
       }
     }
   }
-  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  const int c = (int)(idx % cpr);
-  int64_t rest = idx / cpr;
-  const int kvh = (int)(rest % hkv);
-  rest /= hkv;
-  const int j = (int)(rest % width);
-  const int b = (int)(rest / width);
-  if (b >= batch) return;
-  const int k = counters[3];
-  if (j >= k) return;
-  const int64_t cand = sel_cand[(int64_t)b * width + j];
-  const int r = b * hkv + kvh;
-  const int64_t e0 = (int64_t)c * VEC;
-  const char *ks;
-  const char *vs;
-  if (cand < (int64_t)U * page_size) {
-    const int64_t page = page_list[cand / page_size], t = cand % page_size;
-    const int64_t off = (page & ((int64_t(1) << chunk_shift) - 1)) * page_bytes +
-                        (((int64_t)r * page_size + t) * head_dim + e0) * EB;
-    ks = reinterpret_cast<const char *>(ktab[page >> chunk_shift]) + off;
-    vs = reinterpret_cast<const char *>(vtab[page >> chunk_shift]) + off;
-  } else {
-    const int64_t t = cand - (int64_t)U * page_size;
-    const int64_t off = (((int64_t)r * page_size + t) * head_dim + e0) * EB;
-    ks = part_k + off;
-    vs = part_v + off;
+  const int C = list_count[b];
+  const int first = blockIdx.x * kGatherCands;
+  if (first >= C) return;
+  const uint64_t *L = list + (int64_t)b * list_ld;
+  const int i = first + wave;
+  if (i < C) {
+    const uint64_t x = L[i];
+    int r = 0, j = lane;
+    for (; j + 192 < C; j += 256) {
+      const uint64_t y0 = L[j], y1 = L[j + 64], y2 = L[j + 128], y3 = L[j + 192];
+      r += (y0 > x) + (y1 > x) + (y2 > x) + (y3 > x);
+    }
+    for (; j < C; j += 64) r += L[j] > x;
+    r = wave_sum_i32(r);
+    if (lane == 0) {
+      slot_of[wave] = r < k ? r : -1;
+      cand_of[wave] = comp_index(x);
+    }
+  } else if (lane == 0) {
+    slot_of[wave] = -1;
   }
-  const int64_t o = (((int64_t)r * width + j) * head_dim + e0) * EB;
-  *reinterpret_cast<uint4 *>(k_out + o) = load16(ks);
-  *reinterpret_cast<uint4 *>(v_out + o) = load16(vs);
+  __syncthreads();
+  const int per = hkv * cpr;
+  for (int item = tid; item < kGatherCands * per; item += 256) {
+    const int w = item / per, rest = item - w * per;
+    const int slot = slot_of[w];
+    if (slot < 0) continue;
+    const int kvh = rest / cpr, c = rest - kvh * cpr;
+    const int64_t cand = cand_of[w];
+    const int r = b * hkv + kvh;
+    const int64_t e0 = (int64_t)c * VEC;
+    const char *ks;
+    const char *vs;
+    int64_t gid;
+    if (cand < split) {
+      const int64_t page = page_list[cand / page_size], t = cand % page_size;
+      const int64_t off = (page & ((int64_t(1) << chunk_shift) - 1)) * page_bytes +
+                          (((int64_t)r * page_size + t) * head_dim + e0) * EB;
+      ks = reinterpret_cast<const char *>(ktab[page >> chunk_shift]) + off;
+      vs = reinterpret_cast<const char *>(vtab[page >> chunk_shift]) + off;
+      gid = page * page_size + t;
+    } else {
+      const int64_t t = cand - split;
+      const int64_t off = (((int64_t)r * page_size + t) * head_dim + e0) * EB;
+      ks = part_k + off;
+      vs = part_v + off;
+      gid = num_finalized + t;
+    }
+    const int64_t o = (((int64_t)r * width + slot) * head_dim + e0) * EB;
+    const uint4 kx = load16(ks), vx = load16(vs);
+    *reinterpret_cast<uint4 *>(k_out + o) = kx;
+    *reinterpret_cast<uint4 *>(v_out + o) = vx;
+    if (rest == 0 && idx_out) idx_out[(int64_t)b * width + slot] = gid;
+  }
 }
 
 // Block size and keys per thread of a select over a row of n keys (KPT 0:
@@ -1156,7 +1246,12 @@ int kiv_retrieve(kiv_store_t *s, const kiv_retrieve_args_t *a, kiv_stream_t stre
     if ((rc = s->fine_keys.ensure((size_t)B * ldc * 4, st, false))) return rc;
     KIV_HIP(hipMemsetAsync(s->fine_keys.ptr, 0, s->fine_keys.bytes, st));
   }
-  if ((rc = s->sel_cand.ensure((size_t)B * a->out_width * 4, st, false))) return rc;
+  // Candidate lists of the fine select: [B][list_ld] composites, then [B] counts.
+  const int64_t lmax = std::min<int64_t>(cmax, std::max<int64_t>(kRankCap, a->out_width));
+  const int64_t list_ld = (std::max<int64_t>(kRankCap, a->out_width) + 31) & ~int64_t(31);
+  if ((rc = s->sel_list.ensure((size_t)B * list_ld * 8 + (size_t)B * 4, st, false))) return rc;
+  uint64_t *list = (uint64_t *)s->sel_list.ptr;
+  int32_t *list_count = (int32_t *)(list + (size_t)B * list_ld);
   const int bwords = union_src == UNION_BITMAP ? words : 0;
   {
     // Slices and grid per tier (see the fine scan kernel): host rows in
@@ -1175,52 +1270,47 @@ int kiv_retrieve(kiv_store_t *s, const kiv_retrieve_args_t *a, kiv_stream_t stre
     rc = with_dt_lg(dt, lg, [&](auto dtc, auto lgc) {
       hipLaunchKernelGGL((fine_scan_kernel<decltype(dtc)::value, decltype(lgc)::value>),
                          dim3((unsigned)nb, (unsigned)s->kr), dim3(256), lds, st, union_src,
-                         (const uint32_t *)s->bitmap.ptr, bwords, (const int32_t *)s->page_list.ptr,
-                         (const int32_t *)s->counters.ptr, (const uint64_t *)s->k_tab.ptr, s->chunk_shift,
-                         s->page_bytes, (const char *)s->k_part.ptr, (int)s->partial_len, ps, tpi, hkv, D,
-                         (const char *)a->q, a->q_stride[0], a->q_stride[1], a->q_stride[2], hq, Q, a->scaling,
-                         round, (uint32_t *)s->fine_keys.ptr, ldc);
+                         (const uint32_t *)s->bitmap.ptr, bwords, (int32_t *)s->page_list.ptr,
+                         (int32_t *)s->counters.ptr, (const uint64_t *)s->k_tab.ptr, s->chunk_shift, s->page_bytes,
+                         (const char *)s->k_part.ptr, (int)s->partial_len, ps, tpi, hkv, D, (const char *)a->q,
+                         a->q_stride[0], a->q_stride[1], a->q_stride[2], hq, Q, a->scaling, round,
+                         (uint32_t *)s->fine_keys.ptr, ldc, (const float *)coarse_stats, rows, N, a->pages_out,
+                         a->union_count_out, a->stats_out, a->stats_accum);
       return (int)KIV_OK;
     });
     s->prof_end(KIV_STAGE_FINE_SCAN, st);
     if (rc) return rc;
     KIV_HIP(hipGetLastError());
   }
-  const int fwords = union_src == UNION_BITMAP ? words : 0;
-  int kp2 = 1;
-  while (kp2 < std::min<int64_t>(a->out_width, cmax)) kp2 <<= 1;
-  const size_t fbase = fine_select_lds(fwords, kp2);
-  const size_t lds_limit = device_lds_limit();
-  if (fbase + kFineStaticLds > lds_limit)
-    return fail(KIV_ERR_UNSUPPORTED, "kiv_retrieve: fine select needs %zu bytes of LDS", fbase + kFineStaticLds);
-  const int stage_cap = (int)(((lds_limit - kFineStaticLds - fbase) / 4) & ~size_t(3));
-  const size_t flds = fbase + (size_t)std::min<int64_t>(stage_cap, (cmax + 3) & ~int64_t(3)) * 4;
-  s->prof_begin(KIV_STAGE_FINE_SELECT, st);
-  rc = with_dt(dt, [&](auto dtc) {
-    auto kern = fine_select_kernel<decltype(dtc)::value>;
-    if (flds > 65536)
-      KIV_HIP(hipFuncSetAttribute((const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)flds));
-    hipLaunchKernelGGL(kern, dim3(B), dim3(kFineSelThreads), flds, st, (uint32_t *)s->fine_keys.ptr, ldc, union_src,
-                       (const uint32_t *)s->bitmap.ptr, fwords, kp2, stage_cap, (int32_t *)s->page_list.ptr,
-                       (int32_t *)s->counters.ptr, ps, (int)s->partial_len, s->num_pages * ps, a->out_width, round,
-                       (const float *)coarse_stats, rows, N, fine_stats, (int32_t *)s->sel_cand.ptr, a->idx_out,
-                       a->pages_out, a->union_count_out, a->stats_out, a->stats_accum);
-    return (int)KIV_OK;
-  });
-  s->prof_end(KIV_STAGE_FINE_SELECT, st);
-  if (rc) return rc;
-  KIV_HIP(hipGetLastError());
   {
-    const int64_t work = (int64_t)B * a->out_width * hkv * cpr;
+    // Register chunks per thread: the smallest shape that holds a row of
+    // cmax keys, at most 16 (longer rows are re-read from memory).
+    const int64_t per = ((cmax + 3) / 4 + kFineSelThreads - 1) / kFineSelThreads;
+    s->prof_begin(KIV_STAGE_FINE_SELECT, st);
+    auto launch = [&](auto kern) {
+      hipLaunchKernelGGL(kern, dim3(B), dim3(kFineSelThreads), 0, st, (uint32_t *)s->fine_keys.ptr, ldc,
+                         (const int32_t *)s->counters.ptr, N > 0 ? 1 : 0, ps, (int)s->partial_len, a->out_width,
+                         fine_stats, list, list_ld, list_count);
+    };
+    if (per <= 2) launch(fine_select_kernel<2>);
+    else if (per <= 4) launch(fine_select_kernel<4>);
+    else if (per <= 8) launch(fine_select_kernel<8>);
+    else launch(fine_select_kernel<16>);
+    s->prof_end(KIV_STAGE_FINE_SELECT, st);
+    KIV_HIP(hipGetLastError());
+  }
+  {
+    const unsigned gx = (unsigned)((lmax + kGatherCands - 1) / kGatherCands);
     s->prof_begin(KIV_STAGE_GATHER, st);
     rc = with_dt(dt, [&](auto dtc) {
-      hipLaunchKernelGGL((gather_kernel<decltype(dtc)::value>), dim3((unsigned)((work + 255) / 256)), dim3(256), 0,
-                         st, (const int32_t *)s->sel_cand.ptr, (const int32_t *)s->counters.ptr, N > 0 ? 1 : 0,
-                         (const int32_t *)s->page_list.ptr, (const uint64_t *)s->k_tab.ptr,
-                         (const uint64_t *)s->v_tab.ptr, s->chunk_shift, s->page_bytes,
-                         (const char *)s->k_part.ptr, (const char *)s->v_part.ptr, ps, (int)s->partial_len, B, hkv,
-                         D, a->out_width, cpr, (char *)a->k_out, (char *)a->v_out, (uint32_t *)s->bitmap.ptr,
-                         bwords, (const float *)fine_stats, round, a->stats_out, a->stats_accum);
+      hipLaunchKernelGGL((gather_kernel<decltype(dtc)::value>), dim3(gx, (unsigned)B), dim3(256), 0, st,
+                         (const uint64_t *)list, list_ld, (const int32_t *)list_count,
+                         (const int32_t *)s->counters.ptr, N > 0 ? 1 : 0, (const int32_t *)s->page_list.ptr,
+                         (const uint64_t *)s->k_tab.ptr, (const uint64_t *)s->v_tab.ptr, s->chunk_shift,
+                         s->page_bytes, (const char *)s->k_part.ptr, (const char *)s->v_part.ptr, ps,
+                         (int)s->partial_len, s->num_pages * ps, B, hkv, D, a->out_width, cpr, (char *)a->k_out,
+                         (char *)a->v_out, a->idx_out, (uint32_t *)s->bitmap.ptr, bwords,
+                         (const float *)fine_stats, round, a->stats_out, a->stats_accum);
       return (int)KIV_OK;
     });
     s->prof_end(KIV_STAGE_GATHER, st);

@@ -329,7 +329,8 @@ def test_full_wave_rows(cuda, dtype, d):
 
 def test_large_union_multi_tile(cuda):
     """Random queries spread the per-head top pages: the union exceeds 256
-    pages, so the fine select ranks more than one register tile of keys."""
+    pages, more keys (> 32768) than the fine select holds in registers, so
+    it reads the row from memory on every pass."""
     w = Workload("bigunion", 32, 8, 64, torch.bfloat16, hot=16, cold=65536 + 50, top_pages=32, top_p=512,
                  segment=128)
     data = generate(w, seed=13)
@@ -341,12 +342,15 @@ def test_large_union_multi_tile(cuda):
     assert len(union) * 128 > 32768
 
 
-@pytest.mark.parametrize("n_pages,top_pages,top_p", [(1500, 300, 200), (3000, 300, 600)])
+@pytest.mark.parametrize("n_pages,top_pages,top_p", [(1500, 300, 200), (3000, 300, 600), (3000, 300, 2500)])
 def test_select_large_k_paths(cuda, n_pages, top_pages, top_p):
     """top-k larger than the select block makes every key a candidate: the
     coarse threshold then comes from the block search over the LDS
-    candidates (1500 <= 2048) or over the row itself (3000), and with
-    top_p = 600 the fine select searches its row and orders by bitonic sort."""
+    candidates (1500 <= 2048) or over the row itself (3000).  In the fine
+    select, top_p = 2500 leaves every wave short of its share of maxima, so
+    all of the row's keys (more than 2048) are candidates: the k-th largest
+    comes from the search over the row in memory and the gather ranks 2500
+    listed entries."""
     w = Workload("largek", 4, 1, 32, torch.float32, hot=8, cold=n_pages * 16 + 5, top_pages=top_pages,
                  top_p=top_p, segment=64, page_size=16)
     data = generate(w, seed=16)
@@ -358,8 +362,10 @@ def test_select_large_k_paths(cuda, n_pages, top_pages, top_p):
 
 
 def test_fine_select_lds_search(cuda):
-    """top_p above the fine select block with 1024 < candidates <= 2048: the
-    threshold comes from the block search over the LDS candidates."""
+    """Fewer keys (1024 < n <= 2048) than the fine select block has key
+    sub-slots: the waves set no bound, all n keys are candidates, more than
+    the 1024 the gather ranks, so the k-th largest comes from the block
+    search over the LDS candidates."""
     w = Workload("fineB", 4, 1, 32, torch.float32, hot=8, cold=4000, top_pages=16, top_p=600, segment=64,
                  page_size=32)
     data = generate(w, seed=18)
