@@ -185,6 +185,18 @@ __device__ __forceinline__ uint32_t wave_min_u32(uint32_t v) {
   return min(t[0], t[1]);
 }
 
+// Maximum over the wave; every lane gets it.  All 64 lanes must be active.
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+  v = max(v, (uint32_t)dpp_i32<0xB1>((int)v));
+  v = max(v, (uint32_t)dpp_i32<0x4E>((int)v));
+  v = max(v, (uint32_t)dpp_i32<0x141>((int)v));
+  v = max(v, (uint32_t)dpp_i32<0x140>((int)v));
+  const auto r = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+  v = max(r[0], r[1]);
+  const auto t = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+  return max(t[0], t[1]);
+}
+
 // Number of set bits of a wave mask below the calling lane.
 __device__ __forceinline__ int lane_rank(uint64_t mask) {
   return (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(mask >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)mask, 0u));
@@ -294,24 +306,6 @@ template <int NT> __device__ __forceinline__ int block_incl_scan(int v, int *tmp
   if (total) *total = all;
   __syncthreads();
   return v + before;
-}
-
-// Agent-scope (whole-GPU) atomics and coherent loads/stores for data that
-// blocks of one grid exchange.
-__device__ __forceinline__ int atomic_add_acq_rel(int *p, int v) {
-  return __hip_atomic_fetch_add(p, v, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ void coherent_store_u32(uint32_t *p, uint32_t v) {
-  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ uint32_t coherent_load_u32(uint32_t *p) {
-  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ void coherent_store_f32(float *p, float v) {
-  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ float coherent_load_f32(float *p) {
-  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 }  // namespace kiv

@@ -95,7 +95,7 @@ struct kiv_store {
   // Retrieval scratch.
   kiv::DevBuf coarse_keys;   // [R][ld] u32
   kiv::DevBuf row_stats;     // [R][2] f32 (max, sum) + [B][2] fine stats
-  kiv::DevBuf bitmap;        // [ceil(N/32)] u32, zero between calls
+  kiv::DevBuf row_pages;     // [R][top pages] i32 each query row's top pages
   kiv::DevBuf page_list;     // [N] i32 union pages ascending
   kiv::DevBuf counters;      // i32: [0] = U, the union size of the last coarse pass
   kiv::DevBuf fine_keys;     // [B][ld] u32

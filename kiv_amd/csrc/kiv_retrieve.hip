@@ -16,13 +16,13 @@
 // page, i.e. ascending global token id.
 //
 // The kernels hand data to each other only across kernel boundaries: the
-// coarse select ORs each row's pages into a page bitmap; every fine scan
-// block ranks the bitmap itself (a prefix count of its words in LDS) and
-// block (0, 0) also writes the compact union list, its size and the coarse
-// telemetry; the fine select lists each batch row's candidates for the
-// top P'; the gather ranks the list, places each selected row at its rank,
-// clears the bitmap and finishes the telemetry.  No kernel waits on another
-// block of its own grid.
+// coarse select writes each row's top pages; every fine scan block builds
+// and ranks the union's page bitmap itself (in LDS) and block (0, 0) also
+// writes the compact union list, its size and the coarse telemetry; the
+// fine select lists each batch row's candidates for the top P'; the gather
+// ranks the list, places each selected row at its rank and finishes the
+// telemetry.  No kernel waits on another block of its own grid, and no
+// kernel uses device-scope atomics.
 #include <algorithm>
 #include <type_traits>
 
@@ -34,13 +34,14 @@ namespace kiv {
 
 constexpr int kMaxOut = 4096;       // largest top-P (list entries the gather ranks)
 constexpr int kScanThreads = 256;   // coarse scan block (4 waves)
-constexpr int kFineSelThreads = 512;
+constexpr int kSelThreads = 512;       // select block (8 waves)
 constexpr int kMaxWords = 4096;     // bitmap words ranked in LDS (131072 pages)
 constexpr int kCandCap = 2048;      // candidates a select keeps in LDS
 constexpr int kRankCap = 1024;      // candidates ranked by counting
 
-// Union source of the fine stages.
-enum { UNION_NONE = 0, UNION_BITMAP = 1, UNION_LIST = 2 };
+// Union source of the fine stages: none (no finished pages), the coarse
+// select's row page lists (a fresh coarse pass) or the stored union list.
+enum { UNION_NONE = 0, UNION_ROWS = 1, UNION_LIST = 2 };
 
 // ------------------------------------------------------ select machinery
 // A select ranks (key, index) pairs by key descending, then index
@@ -71,51 +72,6 @@ template <int NT> __device__ void sel_init(SelSh<NT> &sh) {
   }
   __syncthreads();
 }
-
-// Sources of composites, strided over the block: thread t owns entries
-// t, t + NT, t + 2 NT, ...  each(f) calls f(composite) for the thread's own.
-// RegKeys holds a row's keys in registers (n <= NT * KPT), MemKeys re-reads
-// them, LdsComps walks composites already in LDS.
-template <int NT, int KPT> struct RegKeys {
-  uint32_t v[KPT];
-  int n;
-  __device__ void load(const uint32_t *p, int n_) {
-    n = n_;
-#pragma unroll
-    for (int i = 0; i < KPT; ++i) {
-      const int idx = threadIdx.x + i * NT;
-      v[i] = idx < n ? p[idx] : 0u;
-    }
-  }
-  template <typename F> __device__ void each(F &&f) const {
-#pragma unroll
-    for (int i = 0; i < KPT; ++i) {
-      const int idx = threadIdx.x + i * NT;
-      if (idx < n) f(comp_of(v[i], idx));
-    }
-  }
-};
-
-template <int NT> struct MemKeys {
-  const uint32_t *p;
-  int n;
-  __device__ void load(const uint32_t *src, int n_) {
-    p = src;
-    n = n_;
-  }
-  template <typename F> __device__ void each(F &&f) const {
-    constexpr int B = 8;  // loads in flight per thread
-    int idx = threadIdx.x;
-    for (; idx + (B - 1) * NT < n; idx += B * NT) {
-      uint32_t v[B];
-#pragma unroll
-      for (int u = 0; u < B; ++u) v[u] = p[idx + u * NT];
-#pragma unroll
-      for (int u = 0; u < B; ++u) f(comp_of(v[u], idx + u * NT));
-    }
-    for (; idx < n; idx += NT) f(comp_of(p[idx], idx));
-  }
-};
 
 template <int NT> struct LdsComps {
   const uint64_t *c;
@@ -199,17 +155,6 @@ template <int V> __device__ uint32_t wave_kth_u32(const uint32_t (&v)[V], int k)
   return ans;
 }
 
-// Up to 64*V 32-bit keys held by one wave; zero marks an empty entry.
-template <int V> struct WaveKeys {
-  uint32_t v[V];
-  __device__ void load(const uint32_t *src, int n) {
-    const int lane = threadIdx.x & 63;
-#pragma unroll
-    for (int i = 0; i < V; ++i) v[i] = lane + 64 * i < n ? src[lane + 64 * i] : 0u;
-  }
-  __device__ uint32_t kth(int k) const { return wave_kth_u32<V>(v, k); }
-};
-
 // Block-wide count of composites >= c: wave sums, one LDS atomic per wave,
 // one barrier.  Three counters rotate so a counter is cleared two counts
 // before it is reused.
@@ -262,12 +207,13 @@ template <int NT, typename Src> __device__ uint64_t block_kth(const Src &src, in
                     [&](uint64_t m, uint64_t p, uint64_t &a, uint64_t &o) { block_and_or<NT>(src, m, p, sh, a, o); });
 }
 
-// Appends the composites satisfying pred to out[*counter ...] in one pass
-// (entries past cap are counted, not written): per source step, a ballot,
-// one LDS atomic by the first active lane, and the lane's rank in the
-// ballot.  The caller synchronises before reading *counter.
-template <int NT, typename Src, typename P>
-__device__ void block_compact(const Src &src, P &&pred, uint64_t *out, int cap, int *counter) {
+// Calls emit(pos, x) for the composites satisfying pred, pos = 0, 1, ...
+// from *counter on, in one pass (positions past cap are counted, not
+// emitted): per source step, a ballot, one LDS atomic by the first active
+// lane, and the lane's rank in the ballot.  The caller synchronises before
+// reading *counter.
+template <int NT, typename Src, typename P, typename E>
+__device__ void block_compact(const Src &src, P &&pred, E &&emit, int cap, int *counter) {
   src.each([&](uint64_t x) {
     const bool f = pred(x);
     const uint64_t mask = __ballot(f);
@@ -278,45 +224,105 @@ __device__ void block_compact(const Src &src, P &&pred, uint64_t *out, int cap, 
       base = (int)uniform_u32((uint32_t)base);
       if (f) {
         const int pos = base + lane_rank(mask);
-        if (pos < cap) out[pos] = x;
+        if (pos < cap) emit(pos, x);
       }
     }
   });
 }
 
-// Top k of a row (1 <= k <= n).  Leaves the row's max and sum of key values
-// (as floats) in every thread, then either calls ranked(x, r) once for each
-// of the top k composites with its rank r (0 = largest) and returns true, or
-// calls unranked(s, T) once, with T the k-th largest composite and s a
-// source holding every composite >= T, and returns false (the same in every
-// thread).
-//  1. Each wave takes the kw-th largest key of its threads' maxima,
-//     kw = ceil(k / waves), as its bound (0, i.e. none, when fewer of its
-//     threads hold keys); the waves' kw-sets are distinct composites, so the
-//     smallest bound B is at most the k-th largest key.  The wave searches
-//     registers with ballots (no LDS, no barrier).
-//  2. Composites with key >= B (at most k times the keys per thread without
-//     ties at B; about k for smooth scores) go to cand[] in LDS.
-//  3. Up to kRankCap candidates are ranked by counting the larger ones; the
-//     top k are those ranked below k.  More candidates: T from a block-wide
-//     search over LDS (up to kCandCap) or over the row itself.
-template <int NT, typename Src, typename Ranked, typename Unranked>
-__device__ bool topk_select(const Src &src, int k, SelSh<NT> &sh, uint64_t *cand, float &mx, float &sum,
-                            Ranked &&ranked, Unranked &&unranked) {
+// A row's keys in registers as 16-byte chunks (keys 4c .. 4c + 3), dealt
+// round-robin to the waves: lane l of wave w owns chunks
+// w + W * (l + 64 i).  Any run of high keys (the pages of one hot segment
+// are consecutive candidates) then spreads over every wave, which keeps the
+// per-wave bounds close to the k-th largest key.  Sub-slot j of a thread
+// holds its keys 4c + j.
+template <int NT, int V> struct RegKeys4 {
+  static constexpr int W = NT / 64;
+  uint4 v[V];
+  int n;
+  __device__ static int chunk(int i) { return (threadIdx.x >> 6) + W * ((threadIdx.x & 63) + 64 * i); }
+  __device__ void load(const uint32_t *p, int n_) {
+    n = n_;
+    const int n4 = (n + 3) >> 2;
+    const uint4 *p4 = reinterpret_cast<const uint4 *>(p);
+#pragma unroll
+    for (int i = 0; i < V; ++i) {
+      const int c = chunk(i);
+      v[i] = c < n4 ? p4[c] : make_uint4(0, 0, 0, 0);
+    }
+  }
+  template <typename F> __device__ void each_slot(F &&f) const {
+#pragma unroll
+    for (int i = 0; i < V; ++i) {
+      const int base = 4 * chunk(i);
+      if (base < n) {
+        f(comp_of(v[i].x, base), 0);
+        if (base + 1 < n) f(comp_of(v[i].y, base + 1), 1);
+        if (base + 2 < n) f(comp_of(v[i].z, base + 2), 2);
+        if (base + 3 < n) f(comp_of(v[i].w, base + 3), 3);
+      }
+    }
+  }
+  template <typename F> __device__ void each(F &&f) const {
+    each_slot([&](uint64_t x, int) { f(x); });
+  }
+};
+
+// A row's keys re-read from memory for each pass (rows too long for
+// registers), strided over the block; sub-slot = load batch position & 3.
+template <int NT> struct MemKeys4 {
+  const uint32_t *p;
+  int n;
+  template <typename F> __device__ void each_slot(F &&f) const {
+    constexpr int B = 8;  // loads in flight per thread
+    int idx = threadIdx.x;
+    for (; idx + (B - 1) * NT < n; idx += B * NT) {
+      uint32_t v[B];
+#pragma unroll
+      for (int u = 0; u < B; ++u) v[u] = p[idx + u * NT];
+#pragma unroll
+      for (int u = 0; u < B; ++u) f(comp_of(v[u], idx + u * NT), u & 3);
+    }
+    for (; idx < n; idx += NT) f(comp_of(p[idx], idx), 0);
+  }
+  template <typename F> __device__ void each(F &&f) const {
+    each_slot([&](uint64_t x, int) { f(x); });
+  }
+};
+
+// Candidates of the top k (1 <= k <= n) of a row: every composite whose
+// key is at least a bound B <= the k-th largest key goes to cand[] in LDS
+// (up to kCandCap; the count, possibly larger, is returned).  The top k are
+// among them, ties at B included.  The bound: each wave takes the kw-th
+// largest (kw = ceil(k / waves)) of the maxima of its threads' four key
+// sub-slots; the maxima are distinct keys, so every wave holds kw keys >=
+// its bound and the smallest bound B leaves at least k keys >= B.  A wave
+// with fewer than kw nonzero maxima sets no bound (B = 0).  The wave search
+// runs on registers with ballots and one barrier publishes the bounds.
+// Candidates are placed with ballots: a first pass sums the per-step ballot
+// counts, one LDS atomic per wave reserves the wave's range, a second pass
+// places each candidate at its step's offset plus its rank in the ballot.
+// (A lane whose entries run out never gets more, so lane 0 sees every
+// step.)  Also leaves the row's max and sum of scores (as floats) in mx /
+// sum.
+template <int NT, typename Src>
+__device__ int bound_candidates(const Src &src, int k, SelSh<NT> &sh, uint64_t *cand, float &mx, float &sum) {
   constexpr int W = NT / 64;
   const int tid = threadIdx.x, wave = tid >> 6;
-  uint32_t m[1] = {0};
-  float fm = -INFINITY, fs = 0.f;
-  src.each([&](uint64_t x) {
-    m[0] = max(m[0], comp_key(x));
-    const float f = key_to_float(comp_key(x));
-    fm = fmaxf(fm, f);
-    fs += f;
+  uint32_t m[4] = {0u, 0u, 0u, 0u};
+  float fs = 0.f;
+  src.each_slot([&](uint64_t x, int j) {
+    const uint32_t key = comp_key(x);
+    m[j] = max(m[j], key);
+    fs += key_to_float(key);
   });
   const int kw = (k + W - 1) / W;
-  const int have = __popcll(__ballot(m[0] != 0));
-  const uint32_t bw = have >= kw ? wave_kth_u32<1>(m, kw) : 0u;
-  fm = wave_max(fm);
+  int have = 0;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) have += __popcll(__ballot(m[j] != 0u));
+  const uint32_t bw = have >= kw ? wave_kth_u32<4>(m, kw) : 0u;
+  const uint32_t top = max(max(m[0], m[1]), max(m[2], m[3]));
+  float fm = have ? key_to_float(wave_max_u32(top)) : -INFINITY;
   fs = wave_sum(fs);
   if ((tid & 63) == 0) {
     sh.fmax[wave] = fm;
@@ -333,56 +339,94 @@ __device__ bool topk_select(const Src &src, int k, SelSh<NT> &sh, uint64_t *cand
     sum += sh.fsum[w];
     bound = min(bound, sh.wave_bound[w]);
   }
-  // Candidates are sparse: one LDS atomic per candidate.
-  src.each([&](uint64_t x) {
-    if (comp_key(x) >= bound) {
-      const int pos = atomicAdd(&sh.ncand, 1);
-      if (pos < kCandCap) cand[pos] = x;
-    }
-  });
-  __syncthreads();
-  const int C = sh.ncand;
-  if (C <= kRankCap) {
-    for (int i = tid; i < C; i += NT) {
-      const uint64_t x = cand[i];
-      int r = 0, j = 0;
-      for (; j + 8 <= C; j += 8) {
-        uint64_t y[8];
-#pragma unroll
-        for (int u = 0; u < 8; ++u) y[u] = cand[j + u];
-#pragma unroll
-        for (int u = 0; u < 8; ++u) r += y[u] > x;
+  int total = 0;
+  src.each([&](uint64_t x) { total += __popcll(__ballot(comp_key(x) >= bound)); });
+  total = (int)uniform_u32((uint32_t)total);  // lane 0's count
+  if (total) {
+    int off = 0;
+    if ((tid & 63) == 0) off = atomicAdd(&sh.ncand, total);
+    off = (int)uniform_u32((uint32_t)off);
+    src.each([&](uint64_t x) {
+      const bool f = comp_key(x) >= bound;
+      const uint64_t mask = __ballot(f);
+      if (f) {
+        const int pos = off + lane_rank(mask);
+        if (pos < kCandCap) cand[pos] = x;
       }
-      for (; j < C; ++j) r += cand[j] > x;
-      if (r < k) ranked(x, r);
-    }
-    return true;
+      off += __popcll(mask);
+    });
   }
+  __syncthreads();
+  return sh.ncand;
+}
+
+// Calls ranked(x, r) for each of the top k composites of the C candidates
+// in cand[] (C <= kRankCap), r = its rank (0 = largest): a candidate's rank
+// is the number of larger candidates.  A group of tpc lanes (a power of two,
+// tpc * C <= NT where possible) counts for one candidate, each lane over a
+// strided share of the list, and the group sums with lane shuffles.
+template <int NT, typename F> __device__ void rank_candidates(const uint64_t *cand, int C, int k, F &&ranked) {
+  int tpc = 1;
+  while (tpc < 64 && 2 * tpc * C <= NT) tpc <<= 1;
+  const int sub = threadIdx.x & (tpc - 1), groups = NT / tpc;
+  for (int i = threadIdx.x / tpc; i < C; i += groups) {
+    const uint64_t x = cand[i];
+    int r = 0, j = sub;
+    for (; j + 3 * tpc < C; j += 4 * tpc) {
+      const uint64_t y0 = cand[j], y1 = cand[j + tpc], y2 = cand[j + 2 * tpc], y3 = cand[j + 3 * tpc];
+      r += (y0 > x) + (y1 > x) + (y2 > x) + (y3 > x);
+    }
+    for (; j < C; j += tpc) r += cand[j] > x;
+    for (int o = 1; o < tpc; o <<= 1) r += __shfl_xor(r, o, 64);
+    if (sub == 0 && r < k) ranked(x, r);
+  }
+}
+
+// Calls emit(pos, x), pos = 0 .. k-1, for the top k composites (unordered)
+// when more than kRankCap candidates passed the bound: the k-th largest
+// comes from a block search over the LDS candidates (C <= kCandCap) or over
+// `mem`, the row re-read from memory.
+template <int NT, typename Src, typename E>
+__device__ void emit_topk_unranked(const Src &mem, const uint64_t *cand, int C, int k, SelSh<NT> &sh, E &&emit) {
+  auto ge = [](uint64_t t) { return [t](uint64_t x) { return x >= t; }; };
   if (C <= kCandCap) {
     const LdsComps<NT> lc{cand, C};
-    unranked(lc, block_kth<NT>(lc, k, sh));
+    block_compact<NT>(lc, ge(block_kth<NT>(lc, k, sh)), emit, k, &sh.nsel);
   } else {
-    unranked(src, block_kth<NT>(src, k, sh));
+    block_compact<NT>(mem, ge(block_kth<NT>(mem, k, sh)), emit, k, &sh.nsel);
   }
-  return false;
 }
 
 // -------------------------------------------------------- union ranking
-// Copies the page bitmap into LDS and writes rank[w] = set bits in words
-// before w (rank[W] = union size).  Returns the union size.
+// Builds the union of the rows' top pages (row_pages, nk entries) as a page
+// bitmap bits[words] in LDS and writes rank[w] = set bits in words before w
+// (rank[words] = union size).  Returns the union size.
 template <int NT>
-__device__ int rank_union(const uint32_t *bitmap, int words, uint32_t *bits, int *rank, int *scan_tmp) {
+__device__ int rank_union(const int32_t *row_pages, int nk, int words, uint32_t *bits, int *rank, int *scan_tmp) {
+  constexpr int PF = 4;  // list entries per thread loaded before the bitmap is cleared
+  int first[PF];
+#pragma unroll
+  for (int u = 0; u < PF; ++u) {
+    const int i = threadIdx.x + u * NT;
+    first[u] = i < nk ? row_pages[i] : -1;
+  }
+  for (int w = threadIdx.x; w < words; w += NT) bits[w] = 0u;
+  __syncthreads();
+#pragma unroll
+  for (int u = 0; u < PF; ++u)
+    if (first[u] >= 0) atomicOr(&bits[first[u] >> 5], 1u << (first[u] & 31));
+  for (int i = threadIdx.x + PF * NT; i < nk; i += NT) {
+    const int page = row_pages[i];
+    atomicOr(&bits[page >> 5], 1u << (page & 31));
+  }
+  __syncthreads();
   int before = 0;
   for (int base = 0; base < words; base += NT) {
     const int w = base + threadIdx.x;
-    const uint32_t x = w < words ? bitmap[w] : 0u;
-    const int c = __popc(x);
+    const int c = w < words ? __popc(bits[w]) : 0;
     int tot = 0;
     const int incl = block_incl_scan<NT>(c, scan_tmp, &tot);
-    if (w < words) {
-      bits[w] = x;
-      rank[w] = before + incl - c;
-    }
+    if (w < words) rank[w] = before + incl - c;
     before += tot;
   }
   if (threadIdx.x == 0) rank[words] = before;
@@ -644,43 +688,38 @@ template <typename F> static int with_cpr(int cpr, F &&f) {
 }
 
 // --------------------------------------------------------- coarse select
-// One block per query row: the row's top-k pages are ORed into the page
-// bitmap and the row's (max, sum) score stay for the telemetry.
-template <int NT, typename Src>
-__device__ void coarse_pick(const Src &src, int k, uint32_t *bitmap, SelSh<NT> &sh, uint64_t *cand,
-                            float *stats, int row) {
-  float mx, sum;
-  auto mark = [&](uint64_t x) {
-    const int i = comp_index(x);
-    atomicOr(&bitmap[i >> 5], 1u << (i & 31));
-  };
-  topk_select<NT>(src, k, sh, cand, mx, sum, [&](uint64_t x, int) { mark(x); },
-                  [&](const auto &s2, uint64_t T) {
-                    s2.each([&](uint64_t x) {
-                      if (x >= T) mark(x);
-                    });
-                  });
-  if (threadIdx.x == 0) {
-    stats[2 * row] = mx;
-    stats[2 * row + 1] = sum;
-  }
-}
-
-template <int NT, int KPT>
+// One block per query row: the row's top k pages go to row_pages[row][0, k)
+// (in rank order, or unordered after the mass-tie fallback) and the row's
+// (max, sum) of scores stay for the telemetry.  The fine scan builds the
+// union from these lists.  V = 16-byte key chunks per thread in registers
+// (rows of more than 4 * V * NT keys are re-read from memory).
+template <int NT, int V>
 __global__ void __launch_bounds__(NT) coarse_select_kernel(const uint32_t *__restrict__ keys, int64_t ld, int n,
-                                                            int k, uint32_t *bitmap, float *coarse_stats) {
+                                                            int k, int32_t *__restrict__ row_pages,
+                                                            float *__restrict__ coarse_stats) {
   __shared__ SelSh<NT> sh;
   __shared__ uint64_t cand[kCandCap];
   sel_init(sh);
-  const uint32_t *src = keys + (int64_t)blockIdx.x * ld;
-  if (KPT > 0) {
-    RegKeys<NT, (KPT > 0 ? KPT : 1)> rk;
+  const int row = blockIdx.x;
+  const uint32_t *src = keys + (int64_t)row * ld;  // 256-byte aligned rows
+  int32_t *out = row_pages + (int64_t)row * k;
+  const MemKeys4<NT> mk{src, n};
+  float mx, sum;
+  int C;
+  if (n <= 4 * V * NT) {
+    RegKeys4<NT, V> rk;
     rk.load(src, n);
-    coarse_pick<NT>(rk, k, bitmap, sh, cand, coarse_stats, blockIdx.x);
+    C = bound_candidates<NT>(rk, k, sh, cand, mx, sum);
   } else {
-    MemKeys<NT> mk;
-    mk.load(src, n);
-    coarse_pick<NT>(mk, k, bitmap, sh, cand, coarse_stats, blockIdx.x);
+    C = bound_candidates<NT>(mk, k, sh, cand, mx, sum);
+  }
+  if (C <= kRankCap)
+    rank_candidates<NT>(cand, C, k, [&](uint64_t x, int r) { out[r] = comp_index(x); });
+  else
+    emit_topk_unranked<NT>(mk, cand, C, k, sh, [&](int pos, uint64_t x) { out[pos] = comp_index(x); });
+  if (threadIdx.x == 0) {
+    coarse_stats[2 * row] = mx;
+    coarse_stats[2 * row + 1] = sum;
   }
 }
 
@@ -688,8 +727,9 @@ __global__ void __launch_bounds__(NT) coarse_select_kernel(const uint32_t *__res
 // Grid (nb, B*Hkv): block (x, r) keeps the G*Q query rows that read kv row
 // r = b*Hkv + h in LDS and walks work items x, x + nb, ...; an item is a
 // slice of tpi tokens of a union page (items [0, U*nsplit)) or of the
-// partial page (the items after).  Union pages come from the bitmap
-// (ranked in LDS) or from the stored union list; with the bitmap, block
+// partial page (the items after).  Union pages come from the coarse
+// select's row lists (a page bitmap ranked in LDS) or from the stored union
+// list; with the row lists, block
 // (0, 0) also stores the union list, its size and the coarse telemetry
 // (max over rows, mean over rows and pages) for the later kernels.  The
 // max over the block's
@@ -743,7 +783,8 @@ __device__ void publish_union(const uint32_t *ubits, const int *urank, int words
 
 template <int DT, int LG>
 __global__ void __launch_bounds__(256) fine_scan_kernel(
-    int union_src, const uint32_t *__restrict__ bitmap, int words, int32_t *page_list, int32_t *counters,
+    int union_src, const int32_t *__restrict__ row_pages, int row_pages_n, int words, int32_t *page_list,
+    int32_t *counters,
     const uint64_t *__restrict__ ktab, int chunk_shift, int64_t page_bytes, const char *__restrict__ part_k,
     int partial_len, int page_size, int tpi, int hkv, int head_dim, const char *__restrict__ q, int64_t qs0,
     int64_t qs1, int64_t qs2, int hq, int qlen, float scale, int round, uint32_t *__restrict__ out, int64_t ld,
@@ -767,8 +808,8 @@ __global__ void __launch_bounds__(256) fine_scan_kernel(
         load16(q + ((int64_t)b * qs0 + (int64_t)h * qs1 + (int64_t)qp * qs2 + c * VEC) * EB);
   }
   int U = 0;
-  if (union_src == UNION_BITMAP) {
-    U = rank_union<256>(bitmap, words, ubits, urank, scan_tmp);
+  if (union_src == UNION_ROWS) {
+    U = rank_union<256>(row_pages, row_pages_n, words, ubits, urank, scan_tmp);
     if (blockIdx.x == 0 && blockIdx.y == 0)
       publish_union<DT>(ubits, urank, words, U, page_list, pages_out, counters, union_out, coarse_stats, rows,
                         n_pages, round, stats_out, stats_accum);
@@ -788,7 +829,7 @@ __global__ void __launch_bounds__(256) fine_scan_kernel(
     int ntok;
     if (item < page_items) {
       const int v = item / nsplit, s = item % nsplit;
-      const int64_t page = union_src == UNION_BITMAP ? union_page(ubits, urank, words, v) : page_list[v];
+      const int64_t page = union_src == UNION_ROWS ? union_page(ubits, urank, words, v) : page_list[v];
       rowbase = reinterpret_cast<const char *>(ktab[page >> chunk_shift]) +
                 (page & ((int64_t(1) << chunk_shift) - 1)) * page_bytes +
                 ((int64_t)r * page_size + (int64_t)s * tpi) * row_bytes;
@@ -826,150 +867,19 @@ __global__ void __launch_bounds__(256) fine_scan_kernel(
 
 // ----------------------------------------------------------- fine select
 // One block per batch row b lists the candidates of the row's top k =
-// min(P', C) keys: the composites whose key is at least a bound B <= the
-// k-th largest key (so the top k are among them, ties at B included).  The
-// gather ranks the list by counting.  The bound: each wave takes the kw-th
-// largest (kw = ceil(k / waves)) of the maxima of its threads' four key
-// subsets (sub-slots); the maxima are distinct keys, so every wave holds kw
-// keys >= its bound and the smallest bound B leaves at least k keys >= B.
-// A wave with fewer than kw nonzero maxima sets no bound.  When more than
-// kRankCap composites pass B, the block finds the k-th largest composite T
-// and lists exactly the k composites >= T instead.  The block also writes
-// the row's telemetry (max, sum of scores) and zeroes the keys for the next
-// scan, which accumulates with atomicMax.
-
-// A row's keys in registers as 16-byte chunks (keys 4c .. 4c + 3), dealt
-// round-robin to the waves: lane l of wave w owns chunks
-// w + W * (l + 64 i).  Any run of high keys (the pages of one hot segment
-// are consecutive candidates) then spreads over every wave, which keeps the
-// per-wave bounds close to the k-th largest key.  Sub-slot j of a thread
-// holds its keys 4c + j.
-template <int NT, int V> struct RegKeys4 {
-  static constexpr int W = NT / 64;
-  uint4 v[V];
-  int n;
-  __device__ static int chunk(int i) { return (threadIdx.x >> 6) + W * ((threadIdx.x & 63) + 64 * i); }
-  __device__ void load(const uint32_t *p, int n_) {
-    n = n_;
-    const int n4 = (n + 3) >> 2;
-    const uint4 *p4 = reinterpret_cast<const uint4 *>(p);
-#pragma unroll
-    for (int i = 0; i < V; ++i) {
-      const int c = chunk(i);
-      v[i] = c < n4 ? p4[c] : make_uint4(0, 0, 0, 0);
-    }
-  }
-  template <typename F> __device__ void each_slot(F &&f) const {
-#pragma unroll
-    for (int i = 0; i < V; ++i) {
-      const int base = 4 * chunk(i);
-      if (base < n) {
-        f(comp_of(v[i].x, base), 0);
-        if (base + 1 < n) f(comp_of(v[i].y, base + 1), 1);
-        if (base + 2 < n) f(comp_of(v[i].z, base + 2), 2);
-        if (base + 3 < n) f(comp_of(v[i].w, base + 3), 3);
-      }
-    }
-  }
-  template <typename F> __device__ void each(F &&f) const {
-    each_slot([&](uint64_t x, int) { f(x); });
-  }
-};
-
-// A row's keys re-read from memory for each pass (rows too long for
-// registers), strided over the block; sub-slot = load batch position & 3.
-template <int NT> struct MemKeys4 {
-  const uint32_t *p;
-  int n;
-  template <typename F> __device__ void each_slot(F &&f) const {
-    constexpr int B = 8;  // loads in flight per thread
-    int idx = threadIdx.x;
-    for (; idx + (B - 1) * NT < n; idx += B * NT) {
-      uint32_t v[B];
-#pragma unroll
-      for (int u = 0; u < B; ++u) v[u] = p[idx + u * NT];
-#pragma unroll
-      for (int u = 0; u < B; ++u) f(comp_of(v[u], idx + u * NT), u & 3);
-    }
-    for (; idx < n; idx += NT) f(comp_of(p[idx], idx), 0);
-  }
-  template <typename F> __device__ void each(F &&f) const {
-    each_slot([&](uint64_t x, int) { f(x); });
-  }
-};
-
-// Lists the candidates of the top k (1 <= k <= n) of src into out[] (at
-// most kRankCap, or exactly k after the fallback) and returns their count;
-// leaves the row's max and sum of scores in mx / sum (thread 0).  The
-// k-th largest search over the whole row, needed only when more than
-// kCandCap keys pass the bound (mass ties), walks `mem`, the row in memory.
-template <int NT, typename Src>
-__device__ int fine_candidates(const Src &src, const MemKeys4<NT> &mem, int k, SelSh<NT> &sh, uint64_t *cand,
-                               uint64_t *out, float &mx, float &sum) {
-  constexpr int W = NT / 64;
-  const int tid = threadIdx.x, wave = tid >> 6;
-  uint32_t m[4] = {0u, 0u, 0u, 0u};
-  float fm = -INFINITY, fs = 0.f;
-  src.each_slot([&](uint64_t x, int j) {
-    const uint32_t key = comp_key(x);
-    m[j] = max(m[j], key);
-    const float f = key_to_float(key);
-    fm = fmaxf(fm, f);
-    fs += f;
-  });
-  const int kw = (k + W - 1) / W;
-  int have = 0;
-#pragma unroll
-  for (int j = 0; j < 4; ++j) have += __popcll(__ballot(m[j] != 0u));
-  const uint32_t bw = have >= kw ? wave_kth_u32<4>(m, kw) : 0u;
-  fm = wave_max(fm);
-  fs = wave_sum(fs);
-  if ((tid & 63) == 0) {
-    sh.fmax[wave] = fm;
-    sh.fsum[wave] = fs;
-    sh.wave_bound[wave] = bw;
-  }
-  __syncthreads();
-  mx = sh.fmax[0];
-  sum = 0.f;
-  uint32_t bound = sh.wave_bound[0];
-#pragma unroll
-  for (int w = 0; w < W; ++w) {
-    mx = fmaxf(mx, sh.fmax[w]);
-    sum += sh.fsum[w];
-    bound = min(bound, sh.wave_bound[w]);
-  }
-  // Candidates are sparse: one LDS atomic per candidate.
-  src.each([&](uint64_t x) {
-    if (comp_key(x) >= bound) {
-      const int pos = atomicAdd(&sh.ncand, 1);
-      if (pos < kCandCap) cand[pos] = x;
-    }
-  });
-  __syncthreads();
-  const int C = sh.ncand;
-  if (C <= kRankCap) {
-    for (int i = tid; i < C; i += NT) out[i] = cand[i];
-    return C;
-  }
-  auto ge = [](uint64_t t) { return [t](uint64_t x) { return x >= t; }; };
-  if (C <= kCandCap) {
-    const LdsComps<NT> lc{cand, C};
-    block_compact<NT>(lc, ge(block_kth<NT>(lc, k, sh)), out, k, &sh.nsel);
-  } else {
-    block_compact<NT>(mem, ge(block_kth<NT>(mem, k, sh)), out, k, &sh.nsel);
-  }
-  return k;
-}
-
+// min(P', C) keys (bound_candidates) for the gather, which ranks them by
+// counting.  When more than kRankCap keys pass the bound, the block lists
+// exactly the k composites >= the k-th largest instead.  The block also
+// writes the row's telemetry (max, sum of scores) and zeroes the keys for
+// the next scan, which accumulates with atomicMax.
 // V = 16-byte key chunks per thread kept in registers: rows of up to
-// 4 * V * kFineSelThreads keys are read once; longer rows are re-read.
+// 4 * V * kSelThreads keys are read once; longer rows are re-read.
 template <int V>
-__global__ void __launch_bounds__(kFineSelThreads) fine_select_kernel(
+__global__ void __launch_bounds__(kSelThreads) fine_select_kernel(
     uint32_t *__restrict__ keys, int64_t ld, const int32_t *__restrict__ counters, int has_pages, int page_size,
     int partial_len, int width, float *__restrict__ fine_stats, uint64_t *__restrict__ list, int64_t list_ld,
     int32_t *__restrict__ list_count) {
-  constexpr int NT = kFineSelThreads;
+  constexpr int NT = kSelThreads;
   __shared__ SelSh<NT> sh;
   __shared__ uint64_t cand[kCandCap];
   sel_init(sh);
@@ -985,9 +895,15 @@ __global__ void __launch_bounds__(kFineSelThreads) fine_select_kernel(
   if (n <= 4 * V * NT) {
     RegKeys4<NT, V> rk;
     rk.load(row, n);
-    C = fine_candidates<NT>(rk, mk, k, sh, cand, out, mx, sum);
+    C = bound_candidates<NT>(rk, k, sh, cand, mx, sum);
   } else {
-    C = fine_candidates<NT>(mk, mk, k, sh, cand, out, mx, sum);
+    C = bound_candidates<NT>(mk, k, sh, cand, mx, sum);
+  }
+  if (C <= kRankCap) {
+    for (int i = threadIdx.x; i < C; i += NT) out[i] = cand[i];
+  } else {
+    emit_topk_unranked<NT>(mk, cand, C, k, sh, [&](int pos, uint64_t x) { out[pos] = x; });
+    C = k;
   }
   __syncthreads();
   uint4 *row4 = reinterpret_cast<uint4 *>(row);
@@ -1006,7 +922,7 @@ __global__ void __launch_bounds__(kFineSelThreads) fine_select_kernel(
 // the block copies its K and V rows of every kv head to slot r of k_out /
 // v_out ([B][Hkv][width][D]) from the arena (union pages) or the partial
 // page, and its global token id to idx_out[b][r].  Block (0, 0) also
-// finishes the fine telemetry and clears the page bitmap.
+// finishes the fine telemetry.
 constexpr int kGatherCands = 4;
 
 template <int DT>
@@ -1016,8 +932,8 @@ __global__ void __launch_bounds__(256) gather_kernel(
     const uint64_t *__restrict__ ktab, const uint64_t *__restrict__ vtab, int chunk_shift, int64_t page_bytes,
     const char *__restrict__ part_k, const char *__restrict__ part_v, int page_size, int partial_len,
     int64_t num_finalized, int batch, int hkv, int head_dim, int width, int cpr, char *__restrict__ k_out,
-    char *__restrict__ v_out, int64_t *__restrict__ idx_out, uint32_t *bitmap, int clear_words,
-    const float *__restrict__ fine_stats, int round, float *stats_out, double *stats_accum) {
+    char *__restrict__ v_out, int64_t *__restrict__ idx_out, const float *__restrict__ fine_stats, int round,
+    float *stats_out, double *stats_accum) {
   constexpr int VEC = Elem<DT>::VEC, EB = Elem<DT>::BYTES;
   __shared__ int slot_of[kGatherCands], cand_of[kGatherCands];
   const int b = blockIdx.y, tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
@@ -1026,7 +942,6 @@ __global__ void __launch_bounds__(256) gather_kernel(
   const int n = (int)split + partial_len;
   const int k = min(width, n);
   if (blockIdx.x == 0 && b == 0) {
-    for (int w = tid; w < clear_words; w += 256) bitmap[w] = 0u;
     if (tid == 0) {
       float m = -INFINITY;
       double t = 0.0;
@@ -1102,16 +1017,16 @@ __global__ void __launch_bounds__(256) gather_kernel(
   }
 }
 
-// Block size and keys per thread of a select over a row of n keys (KPT 0:
-// the keys are re-read from memory).  At most 512 threads keep the keys in
-// registers: a 1024-thread block has 128 VGPRs per lane, too few next to
-// the wave-held candidates.
-template <typename F> static int with_sel_shape(int64_t n, F &&f) {
+// Launches the select kernel kern_of(V) whose register chunks per thread V
+// is the smallest of 2, 4, 8, 16 that holds a row of n keys (16 for longer
+// rows, which are then re-read from memory).
+template <typename L, typename K> static void with_select_chunks(int64_t n, L &&launch, K &&kern_of) {
   using std::integral_constant;
-  if (n <= 256 * 16) return f(integral_constant<int, 256>{}, integral_constant<int, 16>{});
-  if (n <= 512 * 16) return f(integral_constant<int, 512>{}, integral_constant<int, 16>{});
-  if (n <= 512 * 32) return f(integral_constant<int, 512>{}, integral_constant<int, 32>{});
-  return f(integral_constant<int, 1024>{}, integral_constant<int, 0>{});
+  const int64_t per = ((n + 3) / 4 + kSelThreads - 1) / kSelThreads;
+  if (per <= 2) launch(kern_of(integral_constant<int, 2>{}));
+  else if (per <= 4) launch(kern_of(integral_constant<int, 4>{}));
+  else if (per <= 8) launch(kern_of(integral_constant<int, 8>{}));
+  else launch(kern_of(integral_constant<int, 16>{}));
 }
 
 }  // namespace kiv
@@ -1165,21 +1080,19 @@ int kiv_retrieve(kiv_store_t *s, const kiv_retrieve_args_t *a, kiv_stream_t stre
   float *coarse_stats = (float *)s->row_stats.ptr;
   float *fine_stats = coarse_stats + 2 * rows;
 
-  // ---- coarse: page scan + per-row top pages into the bitmap
+  // ---- coarse: page scan + per-row top pages
   int union_src = UNION_NONE;
   int64_t umax = 0;
+  int kc = 0;  // pages per row of a fresh coarse pass
   if (N > 0) {
     const bool reuse = a->reuse_candidates && s->union_valid && s->union_rows == rows;
     if (!reuse) {
-      union_src = UNION_BITMAP;
-      const int k = std::min(a->top_pages, N);
-      umax = std::min<int64_t>(N, (int64_t)rows * k);
+      union_src = UNION_ROWS;
+      kc = std::min(a->top_pages, N);
+      umax = std::min<int64_t>(N, (int64_t)rows * kc);
       const int64_t ld = ((int64_t)N + 63) & ~int64_t(63);
       if ((rc = s->coarse_keys.ensure((size_t)rows * ld * 4, st, false))) return rc;
-      if (s->bitmap.bytes < (size_t)words * 4) {
-        if ((rc = s->bitmap.ensure((size_t)words * 4, st, false))) return rc;
-        KIV_HIP(hipMemsetAsync(s->bitmap.ptr, 0, s->bitmap.bytes, st));
-      }
+      if ((rc = s->row_pages.ensure((size_t)rows * kc * 4, st, false))) return rc;
       if ((rc = s->page_list.ensure((size_t)N * 4, st, false))) return rc;
       const int kt = D / 32;
       const bool mfma = dt != KIV_DTYPE_F32 && D % 32 == 0 && (kt <= 4 || kt == 6 || kt == 8 || kt == 16);
@@ -1221,13 +1134,10 @@ int kiv_retrieve(kiv_store_t *s, const kiv_retrieve_args_t *a, kiv_stream_t stre
       if (rc) return rc;
       KIV_HIP(hipGetLastError());
       s->prof_begin(KIV_STAGE_COARSE_SELECT, st);
-      with_sel_shape(N, [&](auto nt, auto kpt) {
-        constexpr int NT = decltype(nt)::value, KPT = decltype(kpt)::value;
-        hipLaunchKernelGGL((coarse_select_kernel<NT, KPT>), dim3(rows), dim3(NT), 0, st,
-                           (const uint32_t *)s->coarse_keys.ptr, ld, N, k, (uint32_t *)s->bitmap.ptr,
-                           coarse_stats);
-        return (int)KIV_OK;
-      });
+      with_select_chunks(N, [&](auto kern) {
+        hipLaunchKernelGGL(kern, dim3(rows), dim3(kSelThreads), 0, st, (const uint32_t *)s->coarse_keys.ptr, ld, N,
+                           kc, (int32_t *)s->row_pages.ptr, coarse_stats);
+      }, [](auto vc) { return coarse_select_kernel<kSelThreads, decltype(vc)::value>; });
       s->prof_end(KIV_STAGE_COARSE_SELECT, st);
       KIV_HIP(hipGetLastError());
       s->union_valid = true;
@@ -1252,7 +1162,7 @@ int kiv_retrieve(kiv_store_t *s, const kiv_retrieve_args_t *a, kiv_stream_t stre
   if ((rc = s->sel_list.ensure((size_t)B * list_ld * 8 + (size_t)B * 4, st, false))) return rc;
   uint64_t *list = (uint64_t *)s->sel_list.ptr;
   int32_t *list_count = (int32_t *)(list + (size_t)B * list_ld);
-  const int bwords = union_src == UNION_BITMAP ? words : 0;
+  const int bwords = union_src == UNION_ROWS ? words : 0;
   {
     // Slices and grid per tier (see the fine scan kernel): host rows in
     // ~2 KiB slices over ~1024 blocks, HBM rows in 32-token slices over
@@ -1270,7 +1180,7 @@ int kiv_retrieve(kiv_store_t *s, const kiv_retrieve_args_t *a, kiv_stream_t stre
     rc = with_dt_lg(dt, lg, [&](auto dtc, auto lgc) {
       hipLaunchKernelGGL((fine_scan_kernel<decltype(dtc)::value, decltype(lgc)::value>),
                          dim3((unsigned)nb, (unsigned)s->kr), dim3(256), lds, st, union_src,
-                         (const uint32_t *)s->bitmap.ptr, bwords, (int32_t *)s->page_list.ptr,
+                         (const int32_t *)s->row_pages.ptr, rows * kc, bwords, (int32_t *)s->page_list.ptr,
                          (int32_t *)s->counters.ptr, (const uint64_t *)s->k_tab.ptr, s->chunk_shift, s->page_bytes,
                          (const char *)s->k_part.ptr, (int)s->partial_len, ps, tpi, hkv, D, (const char *)a->q,
                          a->q_stride[0], a->q_stride[1], a->q_stride[2], hq, Q, a->scaling, round,
@@ -1283,19 +1193,12 @@ int kiv_retrieve(kiv_store_t *s, const kiv_retrieve_args_t *a, kiv_stream_t stre
     KIV_HIP(hipGetLastError());
   }
   {
-    // Register chunks per thread: the smallest shape that holds a row of
-    // cmax keys, at most 16 (longer rows are re-read from memory).
-    const int64_t per = ((cmax + 3) / 4 + kFineSelThreads - 1) / kFineSelThreads;
     s->prof_begin(KIV_STAGE_FINE_SELECT, st);
-    auto launch = [&](auto kern) {
-      hipLaunchKernelGGL(kern, dim3(B), dim3(kFineSelThreads), 0, st, (uint32_t *)s->fine_keys.ptr, ldc,
+    with_select_chunks(cmax, [&](auto kern) {
+      hipLaunchKernelGGL(kern, dim3(B), dim3(kSelThreads), 0, st, (uint32_t *)s->fine_keys.ptr, ldc,
                          (const int32_t *)s->counters.ptr, N > 0 ? 1 : 0, ps, (int)s->partial_len, a->out_width,
                          fine_stats, list, list_ld, list_count);
-    };
-    if (per <= 2) launch(fine_select_kernel<2>);
-    else if (per <= 4) launch(fine_select_kernel<4>);
-    else if (per <= 8) launch(fine_select_kernel<8>);
-    else launch(fine_select_kernel<16>);
+    }, [](auto vc) { return fine_select_kernel<decltype(vc)::value>; });
     s->prof_end(KIV_STAGE_FINE_SELECT, st);
     KIV_HIP(hipGetLastError());
   }
@@ -1309,8 +1212,7 @@ int kiv_retrieve(kiv_store_t *s, const kiv_retrieve_args_t *a, kiv_stream_t stre
                          (const uint64_t *)s->k_tab.ptr, (const uint64_t *)s->v_tab.ptr, s->chunk_shift,
                          s->page_bytes, (const char *)s->k_part.ptr, (const char *)s->v_part.ptr, ps,
                          (int)s->partial_len, s->num_pages * ps, B, hkv, D, a->out_width, cpr, (char *)a->k_out,
-                         (char *)a->v_out, a->idx_out, (uint32_t *)s->bitmap.ptr, bwords,
-                         (const float *)fine_stats, round, a->stats_out, a->stats_accum);
+                         (char *)a->v_out, a->idx_out, (const float *)fine_stats, round, a->stats_out, a->stats_accum);
       return (int)KIV_OK;
     });
     s->prof_end(KIV_STAGE_GATHER, st);
