@@ -74,17 +74,9 @@ __global__ void __launch_bounds__(kAttnThreads) decode_attn_kernel(AttnParams p)
   float *rm = red + 4 * kRowTile * D;                                      // [GQ] split max
   float *rl = rm + GQ;                                                     // [GQ] split sum
   const int tid = threadIdx.x;
-  for (int i = tid; i < GQ * cpr; i += kAttnThreads) {
-    const int j = i / cpr, c = i % cpr;
-    const int h = kvh * G + j / p.qlen, qp = j % p.qlen;
-    *reinterpret_cast<uint4 *>(qraw + ((size_t)j * D + c * VEC) * EB) =
-        load16(p.q + ((int64_t)b * p.qs0 + (int64_t)h * p.qs1 + (int64_t)qp * p.qs2 + c * VEC) * EB);
-  }
   const int sg = p.split0 + s;
   const int k0 = sg < p.split_cold ? sg * CH : p.cold_len + (sg - p.split_cold) * CH;
   const int nk = min(CH, (sg < p.split_cold ? p.cold_len : p.cold_len + p.hot_len) - k0);
-  __syncthreads();
-
   const int slot = tid / LG, lane = tid % LG;
   const bool on = lane < cpr;
   auto key_row = [&](int kk, bool value) -> const char * {
@@ -94,6 +86,24 @@ __global__ void __launch_bounds__(kAttnThreads) decode_attn_kernel(AttnParams p)
     return value ? p.hot_v + ((int64_t)b * p.hvs0 + (int64_t)kvh * p.hvs1 + (int64_t)t * p.hvs2) * EB
                  : p.hot_k + ((int64_t)b * p.hks0 + (int64_t)kvh * p.hks1 + (int64_t)t * p.hks2) * EB;
   };
+  // The K and V rows of the first NSLOT * UT keys (the whole chunk for
+  // head_dim <= 16 chunks) are loaded before q is staged, so the two reads
+  // overlap; the V rows stay in registers for phase C.
+  uint4 kx[UT], vx[UT];
+#pragma unroll
+  for (int i = 0; i < UT; ++i) {
+    const int kl = i * NSLOT + slot;
+    const bool in = on && kl < nk;
+    kx[i] = in ? load16(key_row(k0 + kl, false) + lane * VEC * EB) : make_uint4(0, 0, 0, 0);
+    vx[i] = in ? load16(key_row(k0 + kl, true) + lane * VEC * EB) : make_uint4(0, 0, 0, 0);
+  }
+  for (int i = tid; i < GQ * cpr; i += kAttnThreads) {
+    const int j = i / cpr, c = i % cpr;
+    const int h = kvh * G + j / p.qlen, qp = j % p.qlen;
+    *reinterpret_cast<uint4 *>(qraw + ((size_t)j * D + c * VEC) * EB) =
+        load16(p.q + ((int64_t)b * p.qs0 + (int64_t)h * p.qs1 + (int64_t)qp * p.qs2 + c * VEC) * EB);
+  }
+  __syncthreads();
 
   // Phase A: scores of the chunk's keys for every row.
   for (int kb = 0; kb < nk; kb += NSLOT * UT) {
@@ -101,7 +111,8 @@ __global__ void __launch_bounds__(kAttnThreads) decode_attn_kernel(AttnParams p)
 #pragma unroll
     for (int i = 0; i < UT; ++i) {
       const int kl = kb + i * NSLOT + slot;
-      x[i] = (on && kl < nk) ? load16(key_row(k0 + kl, false) + lane * VEC * EB) : make_uint4(0, 0, 0, 0);
+      if (kb == 0) x[i] = kx[i];
+      else x[i] = (on && kl < nk) ? load16(key_row(k0 + kl, false) + lane * VEC * EB) : make_uint4(0, 0, 0, 0);
     }
 #pragma unroll
     for (int i = 0; i < UT; ++i) {
@@ -153,19 +164,25 @@ __global__ void __launch_bounds__(kAttnThreads) decode_attn_kernel(AttnParams p)
     for (int jj = 0; jj < kRowTile; ++jj)
 #pragma unroll
       for (int e = 0; e < VEC; ++e) acc[jj][e] = 0.f;
-    for (int kl = slot; kl < nk; kl += NSLOT) {
-      float v[VEC];
-      if (on) load_chunk<DT>(key_row(k0 + kl, true) + lane * VEC * EB, v);
-      else {
+    for (int kb = 0; kb < nk; kb += NSLOT * UT) {
 #pragma unroll
-        for (int e = 0; e < VEC; ++e) v[e] = 0.f;
-      }
+      for (int i = 0; i < UT; ++i) {
+        const int kl = kb + i * NSLOT + slot;
+        if (kl >= nk) break;
+        float v[VEC];
+        if (kb == 0) unpack_chunk<DT>(vx[i], v);
+        else if (on) load_chunk<DT>(key_row(k0 + kl, true) + lane * VEC * EB, v);
+        else {
 #pragma unroll
-      for (int jj = 0; jj < kRowTile; ++jj) {
-        if (jj < nr) {
-          const float w = sc[(rt + jj) * CH + kl];
+          for (int e = 0; e < VEC; ++e) v[e] = 0.f;
+        }
 #pragma unroll
-          for (int e = 0; e < VEC; ++e) acc[jj][e] = fmaf(w, v[e], acc[jj][e]);
+        for (int jj = 0; jj < kRowTile; ++jj) {
+          if (jj < nr) {
+            const float w = sc[(rt + jj) * CH + kl];
+#pragma unroll
+            for (int e = 0; e < VEC; ++e) acc[jj][e] = fmaf(w, v[e], acc[jj][e]);
+          }
         }
       }
     }
@@ -200,72 +217,238 @@ __global__ void __launch_bounds__(kAttnThreads) decode_attn_kernel(AttnParams p)
   }
 }
 
-// One block per query row (b, h, q position): weights exp(m_s - M) / L in
-// LDS, then 4 consecutive d per thread with the splits' loads issued 8 at a
-// time.
+// MFMA split kernel for 16-bit dtypes with head_dim = 32 * KT; same
+// grid, split layout and outputs as decode_attn_kernel, CH <= 64.
+//  - Scores: wave w takes keys 16w .. 16w + 15 of the split and computes
+//    S^T = K Q^T with v_mfma_f32_16x16x32 over 16 query rows per tile: lane l
+//    supplies key row 16w + l % 16 (A) and q row l % 16 (B), dims
+//    32 s + 8 (l / 16) .. + 7 of step s; it gets the scores of keys
+//    16w + 4 (l / 16) + i (i < 4) for q row l % 16.  K and q come straight
+//    from memory, no LDS and no cross-lane reduction.
+//  - The split's V rows are staged in LDS with the K loads in flight.
+//  - Weighted sum: a thread owns one (q row, 8-dim chunk) and a share of
+//    the keys (ks of nks key groups); the groups' partial sums meet in LDS.
+template <int DT, int KT>
+__global__ void __launch_bounds__(kAttnThreads) decode_attn_mfma_kernel(AttnParams p) {
+  constexpr int EB = 2, VEC = 8, D = 32 * KT, CPR = D / VEC;
+  const int s = blockIdx.x, r = blockIdx.y;
+  const int b = r / p.hkv, kvh = r % p.hkv;
+  const int G = p.hq / p.hkv, GQ = G * p.qlen, CH = p.chunk;
+  const int rows_total = p.batch * p.hq * p.qlen;
+  extern __shared__ uint4 smem4[];
+  uint4 *vs = smem4;                                        // [CH][CPR] V rows
+  float *sc = reinterpret_cast<float *>(vs + CH * CPR);     // [GQ][CH] scores, then weights
+  float *rm = sc + GQ * CH;                                 // [GQ] split max
+  float *rl = rm + GQ;                                      // [GQ] split sum
+  float4 *part = reinterpret_cast<float4 *>(rl + ((2 * GQ + 3) & ~3) - GQ);  // [nks][GQ * CPR][2]
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int sg = p.split0 + s;
+  const int k0 = sg < p.split_cold ? sg * CH : p.cold_len + (sg - p.split_cold) * CH;
+  const int nk = min(CH, (sg < p.split_cold ? p.cold_len : p.cold_len + p.hot_len) - k0);
+  auto key_row = [&](int kk, bool value) -> const char * {
+    if (kk < p.cold_len)
+      return (value ? p.cold_v : p.cold_k) + (((int64_t)r * p.cold_len + kk) * D) * EB;
+    const int t = kk - p.cold_len;
+    return value ? p.hot_v + ((int64_t)b * p.hvs0 + (int64_t)kvh * p.hvs1 + (int64_t)t * p.hvs2) * EB
+                 : p.hot_k + ((int64_t)b * p.hks0 + (int64_t)kvh * p.hks1 + (int64_t)t * p.hks2) * EB;
+  };
+  // K operand rows (loads first), then the V rows into LDS.
+  const int kl = 16 * wave + (lane & 15), dsub = 8 * (lane >> 4);
+  uint4 kx[KT];
+#pragma unroll
+  for (int st = 0; st < KT; ++st)
+    kx[st] = kl < nk ? load16(key_row(k0 + kl, false) + (32 * st + dsub) * EB) : make_uint4(0, 0, 0, 0);
+  constexpr int VB = 4;  // V chunks per thread per batch
+  for (int i0 = 0; i0 < CH * CPR; i0 += VB * kAttnThreads) {
+    uint4 v[VB];
+#pragma unroll
+    for (int u = 0; u < VB; ++u) {
+      const int i = i0 + u * kAttnThreads + tid, key = i / CPR, c = i % CPR;
+      v[u] = (i < CH * CPR && key < nk) ? load16(key_row(k0 + key, true) + c * VEC * EB) : make_uint4(0, 0, 0, 0);
+    }
+#pragma unroll
+    for (int u = 0; u < VB; ++u) {
+      const int i = i0 + u * kAttnThreads + tid;
+      if (i < CH * CPR) vs[i] = v[u];
+    }
+  }
+  // Scores, 16 q rows per tile.
+  for (int rt = 0; rt < GQ; rt += 16) {
+    const int j = rt + (lane & 15);
+    const int h = kvh * G + j / p.qlen, qp = j % p.qlen;
+    const char *qrow = p.q + ((int64_t)b * p.qs0 + (int64_t)h * p.qs1 + (int64_t)qp * p.qs2) * EB;
+    f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int st = 0; st < KT; ++st) {
+      const uint4 qx = j < GQ ? load16(qrow + (32 * st + dsub) * EB) : make_uint4(0, 0, 0, 0);
+      acc = mfma_16x16x32<DT>(kx[st], qx, acc);
+    }
+    if (j < GQ) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int kk = 16 * wave + 4 * (lane >> 4) + i;
+        if (kk < nk) {
+          float v = acc[i] * p.scale;
+          if (p.mask_kind != KIV_MASK_NONE && k0 + kk >= p.cold_len)
+            v += mask_bias(p, b, h, qp, k0 + kk - p.cold_len);
+          sc[j * CH + kk] = v;
+        }
+      }
+    }
+  }
+  __syncthreads();
+
+  // Per-row max and exp-sum over the chunk (one wave per row).
+  for (int j = wave; j < GQ; j += kAttnThreads / 64) {
+    float m = -INFINITY;
+    for (int kk = lane; kk < nk; kk += 64) m = fmaxf(m, sc[j * CH + kk]);
+    m = wave_max(m);
+    float l = 0.f;
+    for (int kk = lane; kk < nk; kk += 64) {
+      const float e = (m == -INFINITY) ? 0.f : __expf(sc[j * CH + kk] - m);
+      sc[j * CH + kk] = e;
+      l += e;
+    }
+    l = wave_sum(l);
+    if (lane == 0) {
+      rm[j] = m;
+      rl[j] = l;
+    }
+  }
+  __syncthreads();
+
+  // Unnormalised weighted sum of V: item = (q row, chunk), key group ks.
+  const int items = GQ * CPR;
+  const int nks = items >= kAttnThreads ? 1 : min(4, kAttnThreads / items);
+  for (int t = tid; t < items * nks; t += kAttnThreads) {
+    const int ks = t / items, it = t - ks * items;
+    const int j = it / CPR, c = it - j * CPR;
+    float a[VEC];
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) a[e] = 0.f;
+    const float *w = sc + j * CH;
+    for (int kk = ks; kk < nk; kk += nks) {
+      float v[VEC];
+      unpack_chunk<DT>(vs[kk * CPR + c], v);
+      const float wk = w[kk];
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) a[e] = fmaf(wk, v[e], a[e]);
+    }
+    if (nks == 1) {
+      const int h = kvh * G + j / p.qlen, qp = j % p.qlen;
+      const int row = (b * p.hq + h) * p.qlen + qp;
+      float4 *dst = reinterpret_cast<float4 *>(&p.ws_acc[((int64_t)sg * rows_total + row) * D + c * VEC]);
+      dst[0] = make_float4(a[0], a[1], a[2], a[3]);
+      dst[1] = make_float4(a[4], a[5], a[6], a[7]);
+    } else {
+      part[2 * (ks * items + it)] = make_float4(a[0], a[1], a[2], a[3]);
+      part[2 * (ks * items + it) + 1] = make_float4(a[4], a[5], a[6], a[7]);
+    }
+  }
+  if (nks > 1) {
+    __syncthreads();
+    for (int it = tid; it < items; it += kAttnThreads) {
+      float4 x0 = part[2 * it], x1 = part[2 * it + 1];
+      for (int ks = 1; ks < nks; ++ks) {
+        const float4 y0 = part[2 * (ks * items + it)], y1 = part[2 * (ks * items + it) + 1];
+        x0.x += y0.x; x0.y += y0.y; x0.z += y0.z; x0.w += y0.w;
+        x1.x += y1.x; x1.y += y1.y; x1.z += y1.z; x1.w += y1.w;
+      }
+      const int j = it / CPR, c = it - j * CPR;
+      const int h = kvh * G + j / p.qlen, qp = j % p.qlen;
+      const int row = (b * p.hq + h) * p.qlen + qp;
+      float4 *dst = reinterpret_cast<float4 *>(&p.ws_acc[((int64_t)sg * rows_total + row) * D + c * VEC]);
+      dst[0] = x0;
+      dst[1] = x1;
+    }
+  }
+  for (int j = tid; j < GQ; j += kAttnThreads) {
+    const int h = kvh * G + j / p.qlen, qp = j % p.qlen;
+    const int row = (b * p.hq + h) * p.qlen + qp;
+    p.ws_m[(int64_t)sg * rows_total + row] = rm[j];
+    p.ws_l[(int64_t)sg * rows_total + row] = rl[j];
+  }
+}
+
+// LDS bytes of the MFMA split kernel.
+static size_t mfma_attn_lds(int gq, int head_dim, int ch) {
+  const int items = gq * (head_dim / 8);
+  const int nks = items >= kAttnThreads ? 1 : std::min(4, kAttnThreads / items);
+  const size_t head = (size_t)ch * head_dim * 2 + (size_t)gq * ch * 4 + (size_t)((2 * gq + 3) & ~3) * 4;
+  return head + (nks > 1 ? (size_t)nks * items * 32 : 0);
+}
+
+// One block per query row (b, h, q position).  Thread (g, i) takes the
+// 4 output dims 4i .. 4i + 3 of splits g, g + groups, ...: the loads of up
+// to kCombineBatch splits are issued together, and the thread folds them
+// into a running (max, sum, accumulator) by log-sum-exp merging.  The
+// groups' partial results then meet in LDS.
+constexpr int kCombineBatch = 8;
+
+__device__ __forceinline__ void lse_merge(float &m, float &l, float4 &o, float m2, float l2, const float4 &o2) {
+  if (m2 == -INFINITY) return;
+  if (m == -INFINITY) {
+    m = m2;
+    l = l2;
+    o = o2;
+    return;
+  }
+  const float M = fmaxf(m, m2), a = __expf(m - M), c = __expf(m2 - M);
+  m = M;
+  l = l * a + l2 * c;
+  o.x = o.x * a + o2.x * c;
+  o.y = o.y * a + o2.y * c;
+  o.z = o.z * a + o2.z * c;
+  o.w = o.w * a + o2.w * c;
+}
+
 template <int DT>
 __global__ void __launch_bounds__(kAttnThreads) decode_attn_combine_kernel(AttnParams p) {
-  __shared__ float wts[kMaxSplits];
-  __shared__ float red[kAttnThreads / 64];
+  __shared__ float sm[kAttnThreads], sl[kAttnThreads];
+  __shared__ float4 so[kAttnThreads];
   const int row = blockIdx.x;  // (b*Hq + h)*Q + qp
   const int qp = row % p.qlen, bh = row / p.qlen;
   const int b = bh / p.hq, h = bh % p.hq;
   const int rows_total = p.batch * p.hq * p.qlen;
   const int D = p.head_dim, S = p.nsplit, tid = threadIdx.x;
-  float M = -INFINITY;
-  for (int s = tid; s < S; s += kAttnThreads) M = fmaxf(M, p.ws_m[(int64_t)s * rows_total + row]);
-  M = wave_max(M);
-  if ((tid & 63) == 0) red[tid >> 6] = M;
-  __syncthreads();
-  M = red[0];
-  for (int w = 1; w < kAttnThreads / 64; ++w) M = fmaxf(M, red[w]);
-  __syncthreads();
-  float lsum = 0.f;
-  for (int s = tid; s < S; s += kAttnThreads) {
-    const float ms = p.ws_m[(int64_t)s * rows_total + row];
-    const float w = (ms == -INFINITY) ? 0.f : __expf(ms - M);
-    wts[s] = w;
-    lsum = fmaf(p.ws_l[(int64_t)s * rows_total + row], w, lsum);
-  }
-  lsum = wave_sum(lsum);
-  if ((tid & 63) == 0) red[tid >> 6] = lsum;
-  __syncthreads();
-  lsum = 0.f;
-  for (int w = 0; w < kAttnThreads / 64; ++w) lsum += red[w];
-  const float inv = (M != -INFINITY && lsum > 0.f) ? 1.f / lsum : 0.f;
-  const int d4n = D / 4;
-  for (int i = tid; i < d4n; i += kAttnThreads) {
-    const int d = i * 4;
-    float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
-    int s = 0;
-    for (; s + 8 <= S; s += 8) {
-      float4 a[8];
+  const int d4n = D / 4, groups = kAttnThreads / d4n;
+  const int g = tid / d4n, i = tid - g * d4n;
+  float m = -INFINITY, l = 0.f;
+  float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
+  if (g < groups) {
+    for (int s0 = g; s0 < S; s0 += groups * kCombineBatch) {
+      float ms[kCombineBatch], ls[kCombineBatch];
+      float4 as[kCombineBatch];
 #pragma unroll
-      for (int u = 0; u < 8; ++u)
-        a[u] = *reinterpret_cast<const float4 *>(&p.ws_acc[((int64_t)(s + u) * rows_total + row) * D + d]);
-#pragma unroll
-      for (int u = 0; u < 8; ++u) {
-        const float w = wts[s + u];
-        o.x = fmaf(a[u].x, w, o.x);
-        o.y = fmaf(a[u].y, w, o.y);
-        o.z = fmaf(a[u].z, w, o.z);
-        o.w = fmaf(a[u].w, w, o.w);
+      for (int u = 0; u < kCombineBatch; ++u) {
+        const int sp = s0 + u * groups;
+        if (sp < S) {
+          const int64_t at = (int64_t)sp * rows_total + row;
+          ms[u] = p.ws_m[at];
+          ls[u] = p.ws_l[at];
+          as[u] = *reinterpret_cast<const float4 *>(&p.ws_acc[at * D + 4 * i]);
+        } else {
+          ms[u] = -INFINITY;
+          ls[u] = 0.f;
+          as[u] = make_float4(0.f, 0.f, 0.f, 0.f);
+        }
       }
+#pragma unroll
+      for (int u = 0; u < kCombineBatch; ++u) lse_merge(m, l, o, ms[u], ls[u], as[u]);
     }
-    for (; s < S; ++s) {
-      const float4 a = *reinterpret_cast<const float4 *>(&p.ws_acc[((int64_t)s * rows_total + row) * D + d]);
-      const float w = wts[s];
-      o.x = fmaf(a.x, w, o.x);
-      o.y = fmaf(a.y, w, o.y);
-      o.z = fmaf(a.z, w, o.z);
-      o.w = fmaf(a.w, w, o.w);
-    }
-    const int64_t ob = (((int64_t)b * p.qlen + qp) * p.hq + h) * D + d;
-    store_elem<DT>(p.out, ob, o.x * inv);
-    store_elem<DT>(p.out, ob + 1, o.y * inv);
-    store_elem<DT>(p.out, ob + 2, o.z * inv);
-    store_elem<DT>(p.out, ob + 3, o.w * inv);
   }
+  sm[tid] = m;
+  sl[tid] = l;
+  so[tid] = o;
+  __syncthreads();
+  if (g != 0) return;
+  for (int gg = 1; gg < groups; ++gg) lse_merge(m, l, o, sm[gg * d4n + i], sl[gg * d4n + i], so[gg * d4n + i]);
+  const float inv = (m != -INFINITY && l > 0.f) ? 1.f / l : 0.f;
+  const int64_t ob = (((int64_t)b * p.qlen + qp) * p.hq + h) * D + 4 * i;
+  store_elem<DT>(p.out, ob, o.x * inv);
+  store_elem<DT>(p.out, ob + 1, o.y * inv);
+  store_elem<DT>(p.out, ob + 2, o.z * inv);
+  store_elem<DT>(p.out, ob + 3, o.w * inv);
 }
 
 static int pick_chunk(int total_keys, int kr) {
@@ -372,18 +555,30 @@ static int attention_launch(const kiv_attention_args_t *a, hipStream_t st, const
   p.ws_l = (float *)(ws + off_l);
   p.ws_acc = (float *)(ws + off_acc);
   p.out = (char *)a->out;
-  const size_t lds = (size_t)GQ * D * elem_bytes(dt) + ((size_t)GQ * ch + 4 * kRowTile * D + 2 * GQ) * 4;
+  p.split0 = 0;
+  const int kt = D / 32;
+  const bool mfma = dt != KIV_DTYPE_F32 && D % 32 == 0 && (kt <= 4 || kt == 6 || kt == 8 || kt == 16);
+  const size_t lds = mfma ? mfma_attn_lds(GQ, D, ch)
+                          : (size_t)GQ * D * elem_bytes(dt) + ((size_t)GQ * ch + 4 * kRowTile * D + 2 * GQ) * 4;
   if (lds > device_lds_limit())
     return fail(KIV_ERR_UNSUPPORTED, "%s: %d keys need %zu bytes of LDS", who, L, lds);
-  p.split0 = 0;
-  const int lg = lanes_per_row(dt, D);
-  int rc = with_dt_lg(dt, lg, [&](auto dtc, auto lgc) {
-    auto kern = decode_attn_kernel<decltype(dtc)::value, decltype(lgc)::value>;
+  auto launch_split = [&](auto kern) -> int {
     if (lds > 65536) KIV_HIP(hipFuncSetAttribute((const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
     hipLaunchKernelGGL(kern, dim3(S, B * hkv), dim3(kAttnThreads), lds, st, p);
     KIV_HIP(hipGetLastError());
-    hipLaunchKernelGGL((decode_attn_combine_kernel<decltype(dtc)::value>), dim3(B * hq * Q), dim3(kAttnThreads), 0,
-                       st, p);
+    return (int)KIV_OK;
+  };
+  int rc = with_dt(dt, [&](auto dtc) {
+    constexpr int DTV = decltype(dtc)::value;
+    int r2;
+    if constexpr (DTV != DT_F32) {
+      if (mfma) r2 = with_kt(kt, [&](auto ktc) { return launch_split(decode_attn_mfma_kernel<DTV, decltype(ktc)::value>); });
+      else r2 = with_lg<DTV>(lanes_per_row(dt, D), [&](auto, auto lgc) { return launch_split(decode_attn_kernel<DTV, decltype(lgc)::value>); });
+    } else {
+      r2 = with_lg<DTV>(lanes_per_row(dt, D), [&](auto, auto lgc) { return launch_split(decode_attn_kernel<DTV, decltype(lgc)::value>); });
+    }
+    if (r2) return r2;
+    hipLaunchKernelGGL((decode_attn_combine_kernel<DTV>), dim3(B * hq * Q), dim3(kAttnThreads), 0, st, p);
     return (int)KIV_OK;
   });
   if (rc) return rc;

@@ -71,9 +71,8 @@ __device__ __forceinline__ float key_to_float(uint32_t k) {
   return __uint_as_float(u);
 }
 
-// 16-byte load of one chunk, widened to fp32.
-template <int DT> __device__ __forceinline__ void load_chunk(const void *p, float *out) {
-  const uint4 v = *reinterpret_cast<const uint4 *>(p);
+// One 16-byte chunk held in registers, widened to fp32.
+template <int DT> __device__ __forceinline__ void unpack_chunk(const uint4 &v, float *out) {
   if constexpr (DT == DT_F32) {
     out[0] = __uint_as_float(v.x); out[1] = __uint_as_float(v.y);
     out[2] = __uint_as_float(v.z); out[3] = __uint_as_float(v.w);
@@ -90,6 +89,11 @@ template <int DT> __device__ __forceinline__ void load_chunk(const void *p, floa
       }
     }
   }
+}
+
+// 16-byte load of one chunk, widened to fp32.
+template <int DT> __device__ __forceinline__ void load_chunk(const void *p, float *out) {
+  unpack_chunk<DT>(*reinterpret_cast<const uint4 *>(p), out);
 }
 
 // Store VEC fp32 values rounded (RNE) to the dtype as one 16-byte chunk.
@@ -260,6 +264,19 @@ __device__ __forceinline__ int wave_sum_i32(int v) {
 // as the final writer keeps the DPP read on the ordinary VALU hazard path.
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+
+// D += A B on one 16x16 tile, K = 32 (8 consecutive k of one A row / B column per lane).
+template <int DT> __device__ __forceinline__ f32x4_t mfma_16x16x32(const uint4 &a, const uint4 &b, f32x4_t c) {
+  if constexpr (DT == DT_BF16)
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a), __builtin_bit_cast(bf16x8_t, b),
+                                                    c, 0, 0, 0);
+  else
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8_t, a), __builtin_bit_cast(f16x8_t, b), c,
+                                                   0, 0, 0);
+}
 
 template <int DT> __device__ __forceinline__ float chunk_dot(const uint4 &x, const uint4 &q, float acc) {
   if constexpr (DT == DT_BF16) {

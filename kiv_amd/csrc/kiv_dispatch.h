@@ -33,4 +33,19 @@ template <typename F> inline int with_dt(int dt, F &&f) {
   return f(std::integral_constant<int, DT_BF16>{});
 }
 
+// Runs f(integral_constant<KT>) for head_dim = 32 * KT (KT in 1-4, 6, 8, 16).
+template <typename F> static int with_kt(int kt, F &&f) {
+  using std::integral_constant;
+  switch (kt) {
+    case 1: return f(integral_constant<int, 1>{});
+    case 2: return f(integral_constant<int, 2>{});
+    case 3: return f(integral_constant<int, 3>{});
+    case 4: return f(integral_constant<int, 4>{});
+    case 6: return f(integral_constant<int, 6>{});
+    case 8: return f(integral_constant<int, 8>{});
+    case 16: return f(integral_constant<int, 16>{});
+  }
+  return fail(KIV_ERR_UNSUPPORTED, "no MFMA kernel for head_dim %d", kt * 32);
+}
+
 }  // namespace kiv

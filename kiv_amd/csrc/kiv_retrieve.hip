@@ -594,19 +594,6 @@ __global__ void __launch_bounds__(kScanThreads) coarse_scan_kernel(
 // and accumulate in fp32, like the dot products of the scalar kernel.
 // Every summary byte is loaded once, the query rows by ordinary loads
 // issued together with it; no LDS, no barrier.
-typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
-typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
-typedef float f32x4_t __attribute__((ext_vector_type(4)));
-
-template <int DT> __device__ __forceinline__ f32x4_t mfma_16x16x32(const uint4 &a, const uint4 &b, f32x4_t c) {
-  if constexpr (DT == DT_BF16)
-    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a), __builtin_bit_cast(bf16x8_t, b),
-                                                    c, 0, 0, 0);
-  else
-    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8_t, a), __builtin_bit_cast(f16x8_t, b), c,
-                                                   0, 0, 0);
-}
-
 constexpr int kScanMfmaPages = 16;  // pages per wave
 
 template <int DT, int KT>  // KT = head_dim / 32
@@ -648,20 +635,6 @@ __global__ void __launch_bounds__(kScanThreads) coarse_scan_mfma_kernel(
       }
     }
   }
-}
-
-template <typename F> static int with_kt(int kt, F &&f) {
-  using std::integral_constant;
-  switch (kt) {
-    case 1: return f(integral_constant<int, 1>{});
-    case 2: return f(integral_constant<int, 2>{});
-    case 3: return f(integral_constant<int, 3>{});
-    case 4: return f(integral_constant<int, 4>{});
-    case 6: return f(integral_constant<int, 6>{});
-    case 8: return f(integral_constant<int, 8>{});
-    case 16: return f(integral_constant<int, 16>{});
-  }
-  return fail(KIV_ERR_UNSUPPORTED, "no MFMA coarse scan for head_dim %d", kt * 32);
 }
 
 // Runs f(integral_constant<CPR>) for the chunks per row of a head dim.
