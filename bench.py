@@ -209,7 +209,9 @@ def roofline_and_links(w, store, stages, union_pages, tier):
         "coarse_select": (rows * N * 4, "hbm"),
         "fine_scan": (union_pages * w.page_size * row, tier),
         "fine_select": (cand * 4, "hbm"),
-        "gather": (2 * P * row, tier),
+        # Host tier: K of the selected rows comes from the fine scan's HBM
+        # staging, so only V crosses the host link.
+        "gather": ((1 if tier == "host" else 2) * P * row, tier),
         "attention": (2 * (P + w.hot) * row, "hbm"),
     }
     out = {}

@@ -100,6 +100,7 @@ struct kiv_store {
   kiv::DevBuf counters;      // i32: [0] = U, the union size of the last coarse pass
   kiv::DevBuf fine_keys;     // [B][ld] u32
   kiv::DevBuf sel_list;      // [B][list_ld] u64 top-P' candidates + [B] i32 counts
+  kiv::DevBuf k_stage;       // [B*Hkv][ld][D] candidates' K rows (host tier)
   bool union_valid = false;  // page_list / U hold the last coarse pass
   int64_t union_rows = 0;    // B*Hq*Q of that pass (bounds reuse)
   int64_t union_max = 0;     // grid bound of that pass

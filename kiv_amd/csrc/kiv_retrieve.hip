@@ -38,6 +38,7 @@ constexpr int kSelThreads = 512;       // select block (8 waves)
 constexpr int kMaxWords = 4096;     // bitmap words ranked in LDS (131072 pages)
 constexpr int kCandCap = 2048;      // candidates a select keeps in LDS
 constexpr int kRankCap = 1024;      // candidates ranked by counting
+constexpr size_t kMaxStageBytes = size_t(256) << 20;  // HBM staging of candidate K rows per store
 
 // Union source of the fine stages: none (no finished pages), the coarse
 // select's row page lists (a fresh coarse pass) or the stored union list.
@@ -702,7 +703,8 @@ __global__ void __launch_bounds__(NT) coarse_select_kernel(const uint32_t *__res
 // slice of tpi tokens of a union page (items [0, U*nsplit)) or of the
 // partial page (the items after).  Union pages come from the coarse
 // select's row lists (a page bitmap ranked in LDS) or from the stored union
-// list; with the row lists, block
+// list.  With k_stage set, every candidate's K row is also written there
+// ([B*Hkv][ld][D]), so the gather takes K from HBM.  With the row lists, block
 // (0, 0) also stores the union list, its size and the coarse telemetry
 // (max over rows, mean over rows and pages) for the later kernels.  The
 // max over the block's
@@ -762,7 +764,7 @@ __global__ void __launch_bounds__(256) fine_scan_kernel(
     int partial_len, int page_size, int tpi, int hkv, int head_dim, const char *__restrict__ q, int64_t qs0,
     int64_t qs1, int64_t qs2, int hq, int qlen, float scale, int round, uint32_t *__restrict__ out, int64_t ld,
     const float *__restrict__ coarse_stats, int rows, int n_pages, int32_t *pages_out, int32_t *union_out,
-    float *stats_out, double *stats_accum) {
+    float *stats_out, double *stats_accum, char *__restrict__ k_stage) {
   constexpr int VEC = Elem<DT>::VEC, EB = Elem<DT>::BYTES;
   constexpr int UT = kFineUT;
   constexpr int NSLOT = 256 / LG;
@@ -821,6 +823,14 @@ __global__ void __launch_bounds__(256) fine_scan_kernel(
         const int t = tb + i * NSLOT + slot;
         x[i] = (on && t < ntok) ? load16(rowbase + (int64_t)t * row_bytes + lane * VEC * EB)
                                 : make_uint4(0, 0, 0, 0);
+      }
+      if (k_stage) {
+#pragma unroll
+        for (int i = 0; i < UT; ++i) {
+          const int t = tb + i * NSLOT + slot;
+          if (on && t < ntok)
+            *reinterpret_cast<uint4 *>(k_stage + (((int64_t)r * ld + cand0 + t) * head_dim + lane * VEC) * EB) = x[i];
+        }
       }
 #pragma unroll
       for (int i = 0; i < UT; ++i) {
@@ -894,8 +904,8 @@ __global__ void __launch_bounds__(kSelThreads) fine_select_kernel(
 // the larger entries of the list; an entry ranked r < k is selected, and
 // the block copies its K and V rows of every kv head to slot r of k_out /
 // v_out ([B][Hkv][width][D]) from the arena (union pages) or the partial
-// page, and its global token id to idx_out[b][r].  Block (0, 0) also
-// finishes the fine telemetry.
+// page (K from k_stage when the fine scan staged it), and its global token
+// id to idx_out[b][r].  Block (0, 0) also finishes the fine telemetry.
 constexpr int kGatherCands = 4;
 
 template <int DT>
@@ -903,8 +913,9 @@ __global__ void __launch_bounds__(256) gather_kernel(
     const uint64_t *__restrict__ list, int64_t list_ld, const int32_t *__restrict__ list_count,
     const int32_t *__restrict__ counters, int has_pages, const int32_t *__restrict__ page_list,
     const uint64_t *__restrict__ ktab, const uint64_t *__restrict__ vtab, int chunk_shift, int64_t page_bytes,
-    const char *__restrict__ part_k, const char *__restrict__ part_v, int page_size, int partial_len,
-    int64_t num_finalized, int batch, int hkv, int head_dim, int width, int cpr, char *__restrict__ k_out,
+    const char *__restrict__ part_k, const char *__restrict__ part_v, const char *__restrict__ k_stage,
+    int64_t stage_ld, int page_size, int partial_len, int64_t num_finalized, int batch, int hkv, int head_dim,
+    int width, int cpr, char *__restrict__ k_out,
     char *__restrict__ v_out, int64_t *__restrict__ idx_out, const float *__restrict__ fine_stats, int round,
     float *stats_out, double *stats_accum) {
   constexpr int VEC = Elem<DT>::VEC, EB = Elem<DT>::BYTES;
@@ -982,6 +993,7 @@ __global__ void __launch_bounds__(256) gather_kernel(
       vs = part_v + off;
       gid = num_finalized + t;
     }
+    if (k_stage) ks = k_stage + (((int64_t)r * stage_ld + cand) * head_dim + e0) * EB;
     const int64_t o = (((int64_t)r * width + slot) * head_dim + e0) * EB;
     const uint4 kx = load16(ks), vx = load16(vs);
     *reinterpret_cast<uint4 *>(k_out + o) = kx;
@@ -1136,6 +1148,15 @@ int kiv_retrieve(kiv_store_t *s, const kiv_retrieve_args_t *a, kiv_stream_t stre
   uint64_t *list = (uint64_t *)s->sel_list.ptr;
   int32_t *list_count = (int32_t *)(list + (size_t)B * list_ld);
   const int bwords = union_src == UNION_ROWS ? words : 0;
+  // Host tier: the fine scan copies the candidates' K rows to HBM as it
+  // streams them, so the gather reads only V over the host link (up to
+  // kMaxStageBytes of staging per store).
+  char *k_stage = nullptr;
+  const size_t stage_bytes = (size_t)s->kr * ldc * s->row_bytes;
+  if (c.cold_tier == KIV_TIER_HOST && stage_bytes <= kMaxStageBytes) {
+    if ((rc = s->k_stage.ensure(stage_bytes, st, false))) return rc;
+    k_stage = (char *)s->k_stage.ptr;
+  }
   {
     // Slices and grid per tier (see the fine scan kernel): host rows in
     // ~2 KiB slices over ~1024 blocks, HBM rows in 32-token slices over
@@ -1158,7 +1179,7 @@ int kiv_retrieve(kiv_store_t *s, const kiv_retrieve_args_t *a, kiv_stream_t stre
                          (const char *)s->k_part.ptr, (int)s->partial_len, ps, tpi, hkv, D, (const char *)a->q,
                          a->q_stride[0], a->q_stride[1], a->q_stride[2], hq, Q, a->scaling, round,
                          (uint32_t *)s->fine_keys.ptr, ldc, (const float *)coarse_stats, rows, N, a->pages_out,
-                         a->union_count_out, a->stats_out, a->stats_accum);
+                         a->union_count_out, a->stats_out, a->stats_accum, k_stage);
       return (int)KIV_OK;
     });
     s->prof_end(KIV_STAGE_FINE_SCAN, st);
@@ -1183,8 +1204,9 @@ int kiv_retrieve(kiv_store_t *s, const kiv_retrieve_args_t *a, kiv_stream_t stre
                          (const uint64_t *)list, list_ld, (const int32_t *)list_count,
                          (const int32_t *)s->counters.ptr, N > 0 ? 1 : 0, (const int32_t *)s->page_list.ptr,
                          (const uint64_t *)s->k_tab.ptr, (const uint64_t *)s->v_tab.ptr, s->chunk_shift,
-                         s->page_bytes, (const char *)s->k_part.ptr, (const char *)s->v_part.ptr, ps,
-                         (int)s->partial_len, s->num_pages * ps, B, hkv, D, a->out_width, cpr, (char *)a->k_out,
+                         s->page_bytes, (const char *)s->k_part.ptr, (const char *)s->v_part.ptr,
+                         (const char *)k_stage, ldc, ps, (int)s->partial_len, s->num_pages * ps, B, hkv, D,
+                         a->out_width, cpr, (char *)a->k_out,
                          (char *)a->v_out, a->idx_out, (const float *)fine_stats, round, a->stats_out, a->stats_accum);
       return (int)KIV_OK;
     });
