@@ -2,6 +2,7 @@
 
     python bench.py [--steps K] [--warmup W] [--workload qwen7b_1m] [--cold-tier host|hbm]
                     [--cache cold|warm]
+    python bench.py --workload qwen15b_model_1m [--model-tokens T] [--decode-steps S]
 
 One step = one global layer's decode step for one new token: evict the
 oldest hot row to the cold tier, coarse-to-fine retrieval over the cold
@@ -23,6 +24,15 @@ bandwidth against vendor peaks and against measured ceilings (the
 kiv_probe_read_bandwidth read probes, same cache state), the union size,
 the other cold tier, warm caches, and the reference's op sequence timed on
 the host CPU (the oracle, as a baseline).
+
+--workload qwen15b_model_1m runs a whole model instead: a random-init
+Qwen2.5-1.5B-shaped decoder (28 layers, hidden 1536, 12 q / 2 kv heads,
+head_dim 128, bf16) through KIVMiddleware: chunked prefill of 1,048,576
+uniform random token ids (chunk 4096, hot cap 4096), then greedy decode
+steps with retrieval in every layer.  It reports the prefill time and its
+dense-FLOP rate against the bf16 MFMA peak, the decode step time, the
+per-layer retrieval stages (store events) and the same model's step over
+a plain 2048-token cache (no cold tier) for comparison.
 """
 
 from __future__ import annotations
@@ -55,6 +65,8 @@ def parse():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--cache", default="cold", choices=("cold", "warm"))
+    ap.add_argument("--model-tokens", type=int, default=1 << 20, help="prompt length of the model workload")
+    ap.add_argument("--decode-steps", type=int, default=128, help="greedy decode steps of the model workload")
     ap.add_argument("--profile-pass", action="store_true",
                     help="for rocprofv3 runs: the headline tier's steps only, plus a 64 MiB device copy "
                          "that calibrates the FETCH_SIZE / WRITE_SIZE counters")
@@ -62,6 +74,8 @@ def parse():
 
 
 SCRUB_BYTES = 512 << 20  # larger than L2 (8 x 4 MiB) plus the 256 MiB memory-side cache
+MFMA_BF16_PEAK_TFLOPS = 2500.0  # dense
+MODEL_WORKLOAD = "qwen15b_model_1m"
 
 
 def make_scrub(dev):
@@ -287,6 +301,180 @@ def load_pmc(kernel, workload):
     return d.get("traffic_bytes_per_launch")
 
 
+def model_flops(cfg, tokens, chunk, cap):
+    """Dense FLOPs of the chunked prefill: projections and MLP (2 per weight per
+    token), attention QK^T and PV over each chunk's keys (hot cap + causal
+    chunk), and the last token's LM head."""
+    d, f, L = cfg.hidden_size, cfg.intermediate_size, cfg.num_hidden_layers
+    hq, hkv, hd = cfg.num_attention_heads, cfg.num_key_value_heads, cfg.hidden_size // cfg.num_attention_heads
+    per_layer = d * hq * hd + 2 * d * hkv * hd + hq * hd * d + 3 * d * f
+    linear = 2 * per_layer * L * tokens
+    attn = 0
+    for start in range(0, tokens, chunk):
+        q = min(chunk, tokens - start)
+        hot = min(start, cap)
+        keys = q * hot + q * (q + 1) // 2          # query i sees the hot window and chunk rows <= i
+        attn += 4 * hq * hd * keys * L
+    head = 2 * d * cfg.vocab_size
+    return linear + attn + head
+
+
+def model_run(args):
+    """Whole-model prefill + decode through KIVMiddleware (see the module docstring)."""
+    import torch
+    from transformers import DynamicCache, Qwen2Config, Qwen2ForCausalLM
+
+    from kiv_amd import KIVConfig, KIVMiddleware
+    from kiv_amd import _native as nat
+
+    dev = torch.device("cuda", 0)
+    T, chunk, cap = args.model_tokens, 4096, 4096
+    cfg = Qwen2Config(vocab_size=151936, hidden_size=1536, intermediate_size=8960, num_hidden_layers=28,
+                      num_attention_heads=12, num_key_value_heads=2, max_position_embeddings=T + 8192,
+                      rope_theta=1e6, tie_word_embeddings=True)
+    cfg._attn_implementation = "sdpa"
+    torch.manual_seed(args.seed)
+    with torch.device(dev):
+        model = Qwen2ForCausalLM(cfg)
+    model = model.to(torch.bfloat16).eval()
+    kcfg = KIVConfig(hot_budget=2048, top_p=256, page_size=128, top_pages=32)
+    mw = KIVMiddleware(model, kcfg)
+    mw.install()
+    cache = mw.create_cache(dev)
+    ids = torch.randint(0, cfg.vocab_size, (1, T), generator=torch.Generator().manual_seed(args.seed)).to(dev)
+    calls = [0]
+
+    def progress(*_):
+        calls[0] += 1
+        if calls[0] % 32 == 0:
+            print(f"[bench] prefill chunk {calls[0]}/{(T + chunk - 1) // chunk}", file=sys.stderr, flush=True)
+
+    hook = model.register_forward_hook(progress)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    logits = mw.chunked_prefill(ids, cache, chunk_size=chunk, prefill_hot_cap=cap)
+    torch.cuda.synchronize()
+    prefill_s = time.perf_counter() - t0
+    hook.remove()
+    cold = cache.get_cold_store(0).cold_length
+    flops = model_flops(cfg, T, chunk, cap)
+    print(f"[bench] prefill {T} tokens in {prefill_s:.1f}s; cold {cold} per layer", file=sys.stderr, flush=True)
+
+    def decode(cache_, tok, n, events=None):
+        with torch.no_grad():
+            for i in range(n):
+                if events is not None:
+                    events[i][0].record()
+                out = model(input_ids=tok, past_key_values=cache_, use_cache=True)
+                tok = out.logits[:, -1:].argmax(-1)
+                if events is not None:
+                    events[i][1].record()
+        return tok
+
+    tok = logits.argmax(-1, keepdim=True)
+    tok = decode(cache, tok, args.warmup)
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+          for _ in range(args.decode_steps)]
+    tok = decode(cache, tok, args.decode_steps, ev)
+    torch.cuda.synchronize()
+    step_ms = sorted(a.elapsed_time(b) for a, b in ev)
+    print(f"[bench] decode median {step_ms[len(step_ms) // 2]:.2f} ms/step", file=sys.stderr, flush=True)
+
+    # Per-layer stages over a few more steps: the store's events bracket the
+    # eviction and retrieval kernels; events around each merged-attention
+    # call (a timing wrapper installed here only) give the attention.
+    import kiv_amd.middleware as kmw
+
+    attn_ev = []
+    plain_attention = kmw.decode_attention
+
+    def timed_attention(*a, **k):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        out = plain_attention(*a, **k)
+        e1.record()
+        attn_ev.append((e0, e1))
+        return out
+
+    kmw.decode_attention = timed_attention
+    lib = nat.lib()
+    stores = [st for st in cache.cold_stores.values() if st._handle]
+    counts, totals = (C.c_int64 * 7)(), (C.c_double * 7)()
+    for st in stores:
+        nat.check(lib.kiv_profile_enable(st._handle, 1), "kiv_profile_enable")
+        nat.check(lib.kiv_profile_read(st._handle, counts, totals), "kiv_profile_read")
+    prof_steps = 16
+    try:
+        tok = decode(cache, tok, prof_steps)
+        torch.cuda.synchronize()
+    finally:
+        kmw.decode_attention = plain_attention
+    stage_us = {}
+    for st in stores:
+        nat.check(lib.kiv_profile_read(st._handle, counts, totals), "kiv_profile_read")
+        nat.check(lib.kiv_profile_enable(st._handle, 0), "kiv_profile_enable")
+        for i, name in enumerate(nat.STAGES):
+            if counts[i]:
+                stage_us.setdefault(name, []).append(totals[i] / counts[i] * 1e3)
+    stage_us = {k: round(sum(v) / len(v), 2) for k, v in stage_us.items()}
+    if attn_ev:
+        stage_us["attention"] = round(sum(a.elapsed_time(b) for a, b in attn_ev) / len(attn_ev) * 1e3, 2)
+    layer_us = sum(v for k, v in stage_us.items() if k != "evict_finalize")
+    union = [r["num_pages_selected"] for st in stores for r in st.telemetry_snapshot()["recent"]
+             if r["kind"] == "coarse" and not r["skipped"]]
+
+    # The same model over a plain 2048-token cache (no cold tier).
+    mw.uninstall()
+    plain = DynamicCache()
+    with torch.no_grad():
+        out = model(input_ids=ids[:, :2048], past_key_values=plain, use_cache=True, logits_to_keep=1)
+    ptok = decode(plain, out.logits[:, -1:].argmax(-1), args.warmup)
+    pev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+           for _ in range(args.decode_steps)]
+    decode(plain, ptok, args.decode_steps, pev)
+    torch.cuda.synchronize()
+    plain_ms = sorted(a.elapsed_time(b) for a, b in pev)
+    step = step_ms[len(step_ms) // 2]
+    pstep = plain_ms[len(plain_ms) // 2]
+    L = cfg.num_hidden_layers
+    line = {
+        "metric": METRIC,
+        "value": round(layer_us, 2),
+        "unit": "us/layer/step",
+        "n_gpus": 1,
+        "steps": args.decode_steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(step, 4),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (random-init weights, uniform random token ids)",
+        "config": {"workload": f"{MODEL_WORKLOAD}: Qwen2.5-1.5B-shaped decoder, {L} layers, hidden 1536, "
+                               f"12/2 heads, D 128; prompt {T} tokens", "chunk_size": chunk,
+                   "prefill_hot_cap": cap, "hot_budget": kcfg.hot_budget, "top_pages": kcfg.top_pages,
+                   "top_p": kcfg.top_p, "cold_tier": kcfg.cold_tier},
+        "value_meaning": "GPU time per layer per decode step of the tiered-cache path: eviction append, "
+                         "retrieval kernels and merged attention (HIP events, averaged over all 28 layers)",
+        "decode_ms_per_step": {"kiv": round(step, 3), "plain_2048": round(pstep, 3),
+                               "kiv_min": round(step_ms[0], 3), "kiv_max": round(step_ms[-1], 3),
+                               "kiv_minus_plain_per_layer_us": round((step - pstep) * 1e3 / L, 2)},
+        "per_layer_stages_us": stage_us,
+        "union_pages": int(round(sum(union) / len(union))) if union else 0,
+        "cold_tokens_per_layer": cold,
+        "prefill": {"seconds": round(prefill_s, 2), "tokens_per_s": round(T / prefill_s, 1),
+                    "dense_tflop": round(flops / 1e12, 1),
+                    "tflops": round(flops / prefill_s / 1e12, 1),
+                    "frac_of_mfma_bf16_peak": round(flops / prefill_s / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4)},
+    }
+    if not args.no_cpu_baseline:
+        from kiv_amd.synthetic import WORKLOADS
+
+        print("[bench] CPU baseline (one layer's retrieval + attention) ...", file=sys.stderr, flush=True)
+        line["cpu_baseline"] = cpu_baseline(WORKLOADS["qwen15b_layer_1m"], args.seed, args.cpu_seconds)
+    print(json.dumps(line), flush=True)
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -294,6 +482,10 @@ def main():
               "runs per GPU; see DESIGN.md for how it would shard)", file=sys.stderr)
         sys.exit(2)
     import torch
+
+    if args.workload == MODEL_WORKLOAD:
+        model_run(args)
+        return
 
     from kiv_amd import KIVConfig
     from kiv_amd.synthetic import WORKLOADS

@@ -54,6 +54,8 @@ WORKLOADS = {
     "phi35_128k": Workload("phi35_128k", 32, 32, 96, torch.float16, 2048, 131072, 64, 512, 512, n_targets=4),
     # MQA shape, 1,048,576 cold tokens.
     "mqa_1m": Workload("mqa_1m", 8, 1, 256, torch.bfloat16, 4096, 1048576, 64, 1024, 2048),
+    # Qwen2.5-1.5B attention shape, one layer of the whole-model run's cold tier.
+    "qwen15b_layer_1m": Workload("qwen15b_layer_1m", 12, 2, 128, torch.bfloat16, 2048, 1046528, 32, 256, 1024),
     # Qwen2.5-7B attention shape, 1,048,576 cold tokens (the headline workload).
     "qwen7b_1m": Workload("qwen7b_1m", 28, 4, 128, torch.bfloat16, 2048, 1048576, 32, 256, 1024),
 }
