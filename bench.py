@@ -112,14 +112,20 @@ def build_cold(w, cfg, dev, seed):
     return store, hot_k, hot_v, q
 
 
-def one_step(store, cfg, q, hot_k, hot_v, i, scaling, attn_events=None):
+def one_step(store, cfg, q, hot_k, hot_v, i, scaling, attn_events=None, fused=True):
     """One decode step, as the middleware runs it: evict the oldest hot row (it
-    cycles through the hot window's rows), retrieve, merged attention."""
+    cycles through the hot window's rows), then retrieval and the merged
+    attention in one call (kiv_retrieve_attend).  fused=False runs them as
+    two calls (kiv_retrieve, kiv_decode_attention), with attn_events around
+    the attention."""
     from kiv_amd.attention import decode_attention
 
     T = hot_k.shape[2]
     j = (store.cold_length + i) % T
     store.evict_from_hot(hot_k[:, :, j:j + 1], hot_v[:, :, j:j + 1])
+    if fused:
+        store.retrieve_attend(q, scaling, cfg, hot_k, hot_v, None)
+        return
     k_out, v_out = store.retrieve_top_kv(q, scaling, cfg)
     if attn_events is not None:
         attn_events[0].record()
@@ -128,19 +134,19 @@ def one_step(store, cfg, q, hot_k, hot_v, i, scaling, attn_events=None):
         attn_events[1].record()
 
 
-def time_steps(store, cfg, q, hot_k, hot_v, steps, warmup, scaling, scrub):
+def time_steps(store, cfg, q, hot_k, hot_v, steps, warmup, scaling, scrub, fused=True):
     """Mean µs per step: back-to-back (scrub None) or each step timed alone after a scrub."""
     import torch
 
     for i in range(warmup):
-        one_step(store, cfg, q, hot_k, hot_v, i, scaling)
+        one_step(store, cfg, q, hot_k, hot_v, i, scaling, fused=fused)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     if scrub is None:
         ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         ev0.record()
         for i in range(steps):
-            one_step(store, cfg, q, hot_k, hot_v, i, scaling)
+            one_step(store, cfg, q, hot_k, hot_v, i, scaling, fused=fused)
         ev1.record()
         torch.cuda.synchronize()
         gpu_us = ev0.elapsed_time(ev1) * 1e3 / steps
@@ -149,7 +155,7 @@ def time_steps(store, cfg, q, hot_k, hot_v, steps, warmup, scaling, scrub):
         for i in range(steps):
             scrub()
             ev[i][0].record()
-            one_step(store, cfg, q, hot_k, hot_v, i, scaling)
+            one_step(store, cfg, q, hot_k, hot_v, i, scaling, fused=fused)
             ev[i][1].record()
         torch.cuda.synchronize()
         gpu_us = sum(a.elapsed_time(b) for a, b in ev) * 1e3 / steps
@@ -157,8 +163,10 @@ def time_steps(store, cfg, q, hot_k, hot_v, steps, warmup, scaling, scrub):
     return gpu_us, wall_us
 
 
-def profile_steps(store, cfg, q, hot_k, hot_v, steps, scaling, scrub):
-    """Per-stage average durations (µs) from HIP events bracketing each launch on its stream."""
+def profile_steps(store, cfg, q, hot_k, hot_v, steps, scaling, scrub, fused=True):
+    """Per-stage average durations (µs) from HIP events bracketing each launch
+    on its stream (the store's events; for the two-call step, events around
+    the attention call)."""
     import torch
 
     from kiv_amd import _native as nat
@@ -166,13 +174,13 @@ def profile_steps(store, cfg, q, hot_k, hot_v, steps, scaling, scrub):
     lib = nat.lib()
     n = min(steps, 256)
     nat.check(lib.kiv_profile_enable(store._handle, 1), "kiv_profile_enable")
-    counts, totals = (C.c_int64 * 7)(), (C.c_double * 7)()
+    counts, totals = (C.c_int64 * len(nat.STAGES))(), (C.c_double * len(nat.STAGES))()
     nat.check(lib.kiv_profile_read(store._handle, counts, totals), "kiv_profile_read")  # clear
     ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(n)]
     for i in range(n):
         if scrub is not None:
             scrub()
-        one_step(store, cfg, q, hot_k, hot_v, i, scaling, attn_events=ev[i])
+        one_step(store, cfg, q, hot_k, hot_v, i, scaling, attn_events=ev[i], fused=fused)
     torch.cuda.synchronize()
     nat.check(lib.kiv_profile_read(store._handle, counts, totals), "kiv_profile_read")
     nat.check(lib.kiv_profile_enable(store._handle, 0), "kiv_profile_enable")
@@ -180,8 +188,9 @@ def profile_steps(store, cfg, q, hot_k, hot_v, steps, scaling, scrub):
     for i, name in enumerate(nat.STAGES):
         if counts[i]:
             stages[name] = {"launches": int(counts[i]), "avg_us": totals[i] / counts[i] * 1e3}
-    att = [a.elapsed_time(b) for a, b in ev]
-    stages["attention"] = {"launches": n, "avg_us": sum(att) / n * 1e3}
+    if not fused:
+        att = [a.elapsed_time(b) for a, b in ev]
+        stages["attention"] = {"launches": n, "avg_us": sum(att) / n * 1e3}
     return stages
 
 
@@ -224,8 +233,11 @@ def roofline_and_links(w, store, stages, union_pages, tier):
         "fine_scan": (union_pages * w.page_size * row, tier),
         "fine_select": (cand * 4, "hbm"),
         # Host tier: K of the selected rows comes from the fine scan's HBM
-        # staging, so only V crosses the host link.
+        # staging, so only V crosses the host link.  (The fused step's gather
+        # launch also runs the hot-window attention splits, which read the
+        # hot K/V from HBM; they are not host-link bytes.)
         "gather": ((1 if tier == "host" else 2) * P * row, tier),
+        "attend": (2 * P * row, "hbm"),
         "attention": (2 * (P + w.hot) * row, "hbm"),
     }
     out = {}
@@ -381,34 +393,16 @@ def model_run(args):
     print(f"[bench] decode median {step_ms[len(step_ms) // 2]:.2f} ms/step", file=sys.stderr, flush=True)
 
     # Per-layer stages over a few more steps: the store's events bracket the
-    # eviction and retrieval kernels; events around each merged-attention
-    # call (a timing wrapper installed here only) give the attention.
-    import kiv_amd.middleware as kmw
-
-    attn_ev = []
-    plain_attention = kmw.decode_attention
-
-    def timed_attention(*a, **k):
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record()
-        out = plain_attention(*a, **k)
-        e1.record()
-        attn_ev.append((e0, e1))
-        return out
-
-    kmw.decode_attention = timed_attention
+    # eviction, retrieval and attention kernels of every layer.
     lib = nat.lib()
     stores = [st for st in cache.cold_stores.values() if st._handle]
-    counts, totals = (C.c_int64 * 7)(), (C.c_double * 7)()
+    counts, totals = (C.c_int64 * len(nat.STAGES))(), (C.c_double * len(nat.STAGES))()
     for st in stores:
         nat.check(lib.kiv_profile_enable(st._handle, 1), "kiv_profile_enable")
         nat.check(lib.kiv_profile_read(st._handle, counts, totals), "kiv_profile_read")
     prof_steps = 16
-    try:
-        tok = decode(cache, tok, prof_steps)
-        torch.cuda.synchronize()
-    finally:
-        kmw.decode_attention = plain_attention
+    tok = decode(cache, tok, prof_steps)
+    torch.cuda.synchronize()
     stage_us = {}
     for st in stores:
         nat.check(lib.kiv_profile_read(st._handle, counts, totals), "kiv_profile_read")
@@ -417,8 +411,6 @@ def model_run(args):
             if counts[i]:
                 stage_us.setdefault(name, []).append(totals[i] / counts[i] * 1e3)
     stage_us = {k: round(sum(v) / len(v), 2) for k, v in stage_us.items()}
-    if attn_ev:
-        stage_us["attention"] = round(sum(a.elapsed_time(b) for a, b in attn_ev) / len(attn_ev) * 1e3, 2)
     layer_us = sum(v for k, v in stage_us.items() if k != "evict_finalize")
     union = [r["num_pages_selected"] for st in stores for r in st.telemetry_snapshot()["recent"]
              if r["kind"] == "coarse" and not r["skipped"]]
@@ -455,7 +447,8 @@ def model_run(args):
                    "prefill_hot_cap": cap, "hot_budget": kcfg.hot_budget, "top_pages": kcfg.top_pages,
                    "top_p": kcfg.top_p, "cold_tier": kcfg.cold_tier},
         "value_meaning": "GPU time per layer per decode step of the tiered-cache path: eviction append, "
-                         "retrieval kernels and merged attention (HIP events, averaged over all 28 layers)",
+                         "retrieval kernels and merged attention (the store's HIP events, averaged over all "
+                         "28 layers)",
         "decode_ms_per_step": {"kiv": round(step, 3), "plain_2048": round(pstep, 3),
                                "kiv_min": round(step_ms[0], 3), "kiv_max": round(step_ms[-1], 3),
                                "kiv_minus_plain_per_layer_us": round((step - pstep) * 1e3 / L, 2)},
@@ -516,6 +509,11 @@ def main():
             warm_us, _ = time_steps(store, cfg, q, hot_k, hot_v, args.steps, 0, w.scaling, None)
             entry["warm_us_per_step"] = warm_us
             print(f"[bench] {tier} (warm caches): {warm_us:.1f} us/step", file=sys.stderr, flush=True)
+            two_us, _ = time_steps(store, cfg, q, hot_k, hot_v, args.steps, 0, w.scaling, scrub, fused=False)
+            two_stages = profile_steps(store, cfg, q, hot_k, hot_v, args.steps, w.scaling, scrub, fused=False)
+            entry["two_call"] = {"us_per_step": round(two_us, 2),
+                                 "stages_us": {k: round(v["avg_us"], 2) for k, v in two_stages.items()}}
+            print(f"[bench] {tier} (retrieve, then attention): {two_us:.1f} us/step", file=sys.stderr, flush=True)
         snap = store.telemetry_snapshot()
         unions = [r["num_pages_selected"] for r in snap["recent"] if r["kind"] == "coarse" and not r["skipped"]]
         entry["union_pages"] = int(round(sum(unions) / len(unions))) if unions else 0
@@ -558,6 +556,8 @@ def main():
                 for t, r in results.items() if t != args.cold_tier}
     if "warm_us_per_step" in head:
         variants["warm_caches"] = {"us_per_step": round(head["warm_us_per_step"], 2)}
+    if "two_call" in head:
+        variants["two_call"] = head["two_call"]
     line = {
         "metric": METRIC,
         "value": round(head["us_per_step"], 2),

@@ -179,8 +179,9 @@ enum {
   KIV_STAGE_COARSE_SELECT = 3,
   KIV_STAGE_FINE_SCAN = 4,
   KIV_STAGE_FINE_SELECT = 5,
-  KIV_STAGE_GATHER = 6,
-  KIV_NUM_STAGES = 7
+  KIV_STAGE_GATHER = 6,          /* with kiv_retrieve_attend: also the hot-window attention splits */
+  KIV_STAGE_ATTEND = 7,          /* kiv_retrieve_attend's final attention kernel */
+  KIV_NUM_STAGES = 8
 };
 int kiv_profile_enable(kiv_store_t *store, int enable);
 int kiv_profile_read(kiv_store_t *store, int64_t counts[KIV_NUM_STAGES], double total_ms[KIV_NUM_STAGES]);
@@ -207,6 +208,17 @@ size_t kiv_attention_workspace_size(int32_t batch, int32_t num_q_heads, int32_t 
  * Replaces the concatenation in kiv_attention plus the original attention
  * call (kiv/middleware.py:330-354). */
 int kiv_decode_attention(const kiv_attention_args_t *args, kiv_stream_t stream);
+
+/* kiv_retrieve followed by kiv_decode_attention over its outputs, in fewer
+ * launches: the hot window's attention splits run alongside the retrieval's
+ * gather, and one final kernel attends the retrieved keys and merges.  The
+ * attention's cold_k / cold_v / cold_len must be the retrieval's k_out /
+ * v_out / out_width, and its shapes the store's.  Outputs are those of the
+ * two calls (shapes the fused path does not cover run as the two calls).
+ * Replaces retrieve_top_kv plus the wrapper's concatenation and attention
+ * call (kiv/cold_store.py:283-371, kiv/middleware.py:330-354). */
+int kiv_retrieve_attend(kiv_store_t *store, const kiv_retrieve_args_t *retrieve, const kiv_attention_args_t *attention,
+                        kiv_stream_t stream);
 
 #ifdef __cplusplus
 }

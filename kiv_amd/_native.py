@@ -23,7 +23,7 @@ TIER_HOST, TIER_HBM = 0, 1
 ROUND_ACTIVATION, ROUND_FP32 = 0, 1
 MASK_NONE, MASK_BOOL, MASK_F32, MASK_F16, MASK_BF16 = 0, 1, 2, 3, 4
 STAGES = ("evict_append", "evict_finalize", "coarse_scan", "coarse_select", "fine_scan", "fine_select",
-          "gather")
+          "gather", "attend")
 
 _I64x3 = C.c_int64 * 3
 _I64x4 = C.c_int64 * 4
@@ -84,11 +84,12 @@ SIGNATURES = {
     "kiv_store_read_tokens": (C.c_int, [C.c_void_p, C.c_int64, C.c_int64, C.c_void_p, C.c_void_p,
                                         C.c_void_p]),
     "kiv_profile_enable": (C.c_int, [C.c_void_p, C.c_int]),
-    "kiv_profile_read": (C.c_int, [C.c_void_p, C.c_int64 * 7, C.c_double * 7]),
+    "kiv_profile_read": (C.c_int, [C.c_void_p, C.c_int64 * len(STAGES), C.c_double * len(STAGES)]),
     "kiv_probe_read_bandwidth": (C.c_int, [C.c_int32, C.c_size_t, C.c_int32, C.c_int32, C.c_int32,
                                            C.POINTER(C.c_double), C.c_void_p]),
     "kiv_attention_workspace_size": (C.c_size_t, [C.c_int32] * 7),
     "kiv_decode_attention": (C.c_int, [C.POINTER(AttentionArgs), C.c_void_p]),
+    "kiv_retrieve_attend": (C.c_int, [C.c_void_p, C.POINTER(RetrieveArgs), C.POINTER(AttentionArgs), C.c_void_p]),
 }
 
 _lock = threading.Lock()

@@ -22,6 +22,7 @@ import math
 import torch
 
 from . import _native as nat
+from . import attention
 from .config import KIVConfig
 from .model_topology import ModelTopology
 
@@ -157,6 +158,26 @@ class ColdKVStore:
         """
         if self.cold_length == 0:
             return None, None
+        k_out, v_out, _ = self._retrieve(query, scaling, kiv_config, step, None)
+        return k_out, v_out
+
+    def retrieve_attend(self, query: torch.Tensor, scaling: float, kiv_config: KIVConfig,
+                        hot_k: torch.Tensor, hot_v: torch.Tensor, mask: torch.Tensor | None,
+                        step: int = -1) -> torch.Tensor | None:
+        """retrieve_top_kv followed by the merged attention over [retrieved ; hot]
+        (kiv_retrieve_attend), or None when the cold tier is empty.
+
+        Returns the attention output ``[B, Q, Hq, D]``; the retrieval's
+        telemetry and candidate cache are updated as by retrieve_top_kv.
+        """
+        if self.cold_length == 0:
+            return None
+        _, _, out = self._retrieve(query, scaling, kiv_config, step, (hot_k, hot_v, mask))
+        return out
+
+    def _retrieve(self, query, scaling, kiv_config, step, attend):
+        """One retrieval; with ``attend = (hot_k, hot_v, mask)`` also the merged
+        attention (fused when the output width is known on the host)."""
         if query.dim() != 4 or query.shape[1] != self._num_query_heads or query.shape[3] != self._head_dim:
             raise ValueError(f"query must be [B, {self._num_query_heads}, Q, {self._head_dim}], "
                              f"got {tuple(query.shape)}")
@@ -201,7 +222,15 @@ class ColdKVStore:
             pages_out=nat.ptr(pages_out), union_count_out=nat.ptr(union_count),
             stats_out=stats.data_ptr(), stats_accum=accum.data_ptr(),
         )
-        nat.check(lib.kiv_retrieve(self._handle, C.byref(args), nat.stream_ptr(dev)), "kiv_retrieve")
+        out = None
+        if attend is not None and exact:
+            hot_k, hot_v, mask = attend
+            aargs, out, _keep = attention._prepare(q, width, hot_k, hot_v, mask, scaling)
+            attention._set_cold(aargs, k_out, v_out, self._dtype)
+            nat.check(lib.kiv_retrieve_attend(self._handle, C.byref(args), C.byref(aargs), nat.stream_ptr(dev)),
+                      "kiv_retrieve_attend")
+        else:
+            nat.check(lib.kiv_retrieve(self._handle, C.byref(args), nat.stream_ptr(dev)), "kiv_retrieve")
 
         if coarse_runs:
             self._last_union_count = union_count
@@ -225,7 +254,10 @@ class ColdKVStore:
             width = actual
         self._telemetry.record_fine(stats=stats, selected=idx_out, actual_P=width,
                                     requested_P=int(kiv_config.top_p), cold_length=self.cold_length)
-        return k_out, v_out
+        if attend is not None and out is None:
+            hot_k, hot_v, mask = attend
+            out = attention.decode_attention(q, k_out, v_out, hot_k, hot_v, mask, scaling)
+        return k_out, v_out, out
 
     # ------------------------------------------------------ bookkeeping
     def reset(self) -> None:

@@ -17,44 +17,18 @@
 #include <algorithm>
 #include <type_traits>
 
+#include "kiv_attn_device.h"
 #include "kiv_common.h"
 #include "kiv_dispatch.h"
 #include "kiv_internal.h"
 
 namespace kiv {
 
-constexpr int kAttnThreads = 256;
-constexpr int kRowTile = 8;
-constexpr int kMaxSplits = 4096;
+constexpr int kFinalUT = 16;  // retrieved keys per lane group in the final kernel
 
-struct AttnParams {
-  const char *q;
-  int64_t qs0, qs1, qs2;
-  const char *cold_k, *cold_v;
-  int cold_len, hot_len;
-  const char *hot_k, *hot_v;
-  int64_t hks0, hks1, hks2, hvs0, hvs1, hvs2;
-  const char *mask;
-  int mask_kind;
-  int64_t ms0, ms1, ms2, ms3;
-  int batch, hq, hkv, qlen, head_dim;
-  float scale;
-  int chunk, nsplit;   // keys per split; splits in all
-  int split_cold;      // splits [0, split_cold) hold retrieved keys, the rest hot keys
-  int split0;          // first split of this launch
-  float *ws_m, *ws_l, *ws_acc;
-  char *out;
-};
-
-__device__ __forceinline__ float mask_bias(const AttnParams &p, int b, int h, int qp, int t) {
-  const int64_t o = (int64_t)b * p.ms0 + (int64_t)h * p.ms1 + (int64_t)qp * p.ms2 + (int64_t)t * p.ms3;
-  switch (p.mask_kind) {
-    case KIV_MASK_BOOL: return p.mask[o] ? 0.f : -INFINITY;
-    case KIV_MASK_F32: return load_elem<DT_F32>(p.mask, o);
-    case KIV_MASK_F16: return load_elem<DT_F16>(p.mask, o);
-    case KIV_MASK_BF16: return load_elem<DT_BF16>(p.mask, o);
-  }
-  return 0.f;
+template <int DT, int KT>
+__global__ void __launch_bounds__(kAttnThreads) decode_attn_mfma_kernel(AttnParams p) {
+  attn_mfma_split<DT, KT>(p, blockIdx.x, blockIdx.y);
 }
 
 template <int DT, int LG>
@@ -217,191 +191,11 @@ __global__ void __launch_bounds__(kAttnThreads) decode_attn_kernel(AttnParams p)
   }
 }
 
-// MFMA split kernel for 16-bit dtypes with head_dim = 32 * KT; same
-// grid, split layout and outputs as decode_attn_kernel, CH <= 64.
-//  - Scores: wave w takes keys 16w .. 16w + 15 of the split and computes
-//    S^T = K Q^T with v_mfma_f32_16x16x32 over 16 query rows per tile: lane l
-//    supplies key row 16w + l % 16 (A) and q row l % 16 (B), dims
-//    32 s + 8 (l / 16) .. + 7 of step s; it gets the scores of keys
-//    16w + 4 (l / 16) + i (i < 4) for q row l % 16.  K and q come straight
-//    from memory, no LDS and no cross-lane reduction.
-//  - The split's V rows are staged in LDS with the K loads in flight.
-//  - Weighted sum: a thread owns one (q row, 8-dim chunk) and a share of
-//    the keys (ks of nks key groups); the groups' partial sums meet in LDS.
-template <int DT, int KT>
-__global__ void __launch_bounds__(kAttnThreads) decode_attn_mfma_kernel(AttnParams p) {
-  constexpr int EB = 2, VEC = 8, D = 32 * KT, CPR = D / VEC;
-  const int s = blockIdx.x, r = blockIdx.y;
-  const int b = r / p.hkv, kvh = r % p.hkv;
-  const int G = p.hq / p.hkv, GQ = G * p.qlen, CH = p.chunk;
-  const int rows_total = p.batch * p.hq * p.qlen;
-  extern __shared__ uint4 smem4[];
-  uint4 *vs = smem4;                                        // [CH][CPR] V rows
-  float *sc = reinterpret_cast<float *>(vs + CH * CPR);     // [GQ][CH] scores, then weights
-  float *rm = sc + GQ * CH;                                 // [GQ] split max
-  float *rl = rm + GQ;                                      // [GQ] split sum
-  float4 *part = reinterpret_cast<float4 *>(rl + ((2 * GQ + 3) & ~3) - GQ);  // [nks][GQ * CPR][2]
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-  const int sg = p.split0 + s;
-  const int k0 = sg < p.split_cold ? sg * CH : p.cold_len + (sg - p.split_cold) * CH;
-  const int nk = min(CH, (sg < p.split_cold ? p.cold_len : p.cold_len + p.hot_len) - k0);
-  auto key_row = [&](int kk, bool value) -> const char * {
-    if (kk < p.cold_len)
-      return (value ? p.cold_v : p.cold_k) + (((int64_t)r * p.cold_len + kk) * D) * EB;
-    const int t = kk - p.cold_len;
-    return value ? p.hot_v + ((int64_t)b * p.hvs0 + (int64_t)kvh * p.hvs1 + (int64_t)t * p.hvs2) * EB
-                 : p.hot_k + ((int64_t)b * p.hks0 + (int64_t)kvh * p.hks1 + (int64_t)t * p.hks2) * EB;
-  };
-  // K operand rows (loads first), then the V rows into LDS.
-  const int kl = 16 * wave + (lane & 15), dsub = 8 * (lane >> 4);
-  uint4 kx[KT];
-#pragma unroll
-  for (int st = 0; st < KT; ++st)
-    kx[st] = kl < nk ? load16(key_row(k0 + kl, false) + (32 * st + dsub) * EB) : make_uint4(0, 0, 0, 0);
-  constexpr int VB = 4;  // V chunks per thread per batch
-  for (int i0 = 0; i0 < CH * CPR; i0 += VB * kAttnThreads) {
-    uint4 v[VB];
-#pragma unroll
-    for (int u = 0; u < VB; ++u) {
-      const int i = i0 + u * kAttnThreads + tid, key = i / CPR, c = i % CPR;
-      v[u] = (i < CH * CPR && key < nk) ? load16(key_row(k0 + key, true) + c * VEC * EB) : make_uint4(0, 0, 0, 0);
-    }
-#pragma unroll
-    for (int u = 0; u < VB; ++u) {
-      const int i = i0 + u * kAttnThreads + tid;
-      if (i < CH * CPR) vs[i] = v[u];
-    }
-  }
-  // Scores, 16 q rows per tile.
-  for (int rt = 0; rt < GQ; rt += 16) {
-    const int j = rt + (lane & 15);
-    const int h = kvh * G + j / p.qlen, qp = j % p.qlen;
-    const char *qrow = p.q + ((int64_t)b * p.qs0 + (int64_t)h * p.qs1 + (int64_t)qp * p.qs2) * EB;
-    f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int st = 0; st < KT; ++st) {
-      const uint4 qx = j < GQ ? load16(qrow + (32 * st + dsub) * EB) : make_uint4(0, 0, 0, 0);
-      acc = mfma_16x16x32<DT>(kx[st], qx, acc);
-    }
-    if (j < GQ) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int kk = 16 * wave + 4 * (lane >> 4) + i;
-        if (kk < nk) {
-          float v = acc[i] * p.scale;
-          if (p.mask_kind != KIV_MASK_NONE && k0 + kk >= p.cold_len)
-            v += mask_bias(p, b, h, qp, k0 + kk - p.cold_len);
-          sc[j * CH + kk] = v;
-        }
-      }
-    }
-  }
-  __syncthreads();
-
-  // Per-row max and exp-sum over the chunk (one wave per row).
-  for (int j = wave; j < GQ; j += kAttnThreads / 64) {
-    float m = -INFINITY;
-    for (int kk = lane; kk < nk; kk += 64) m = fmaxf(m, sc[j * CH + kk]);
-    m = wave_max(m);
-    float l = 0.f;
-    for (int kk = lane; kk < nk; kk += 64) {
-      const float e = (m == -INFINITY) ? 0.f : __expf(sc[j * CH + kk] - m);
-      sc[j * CH + kk] = e;
-      l += e;
-    }
-    l = wave_sum(l);
-    if (lane == 0) {
-      rm[j] = m;
-      rl[j] = l;
-    }
-  }
-  __syncthreads();
-
-  // Unnormalised weighted sum of V: item = (q row, chunk), key group ks.
-  const int items = GQ * CPR;
-  const int nks = items >= kAttnThreads ? 1 : min(4, kAttnThreads / items);
-  for (int t = tid; t < items * nks; t += kAttnThreads) {
-    const int ks = t / items, it = t - ks * items;
-    const int j = it / CPR, c = it - j * CPR;
-    float a[VEC];
-#pragma unroll
-    for (int e = 0; e < VEC; ++e) a[e] = 0.f;
-    const float *w = sc + j * CH;
-    for (int kk = ks; kk < nk; kk += nks) {
-      float v[VEC];
-      unpack_chunk<DT>(vs[kk * CPR + c], v);
-      const float wk = w[kk];
-#pragma unroll
-      for (int e = 0; e < VEC; ++e) a[e] = fmaf(wk, v[e], a[e]);
-    }
-    if (nks == 1) {
-      const int h = kvh * G + j / p.qlen, qp = j % p.qlen;
-      const int row = (b * p.hq + h) * p.qlen + qp;
-      float4 *dst = reinterpret_cast<float4 *>(&p.ws_acc[((int64_t)sg * rows_total + row) * D + c * VEC]);
-      dst[0] = make_float4(a[0], a[1], a[2], a[3]);
-      dst[1] = make_float4(a[4], a[5], a[6], a[7]);
-    } else {
-      part[2 * (ks * items + it)] = make_float4(a[0], a[1], a[2], a[3]);
-      part[2 * (ks * items + it) + 1] = make_float4(a[4], a[5], a[6], a[7]);
-    }
-  }
-  if (nks > 1) {
-    __syncthreads();
-    for (int it = tid; it < items; it += kAttnThreads) {
-      float4 x0 = part[2 * it], x1 = part[2 * it + 1];
-      for (int ks = 1; ks < nks; ++ks) {
-        const float4 y0 = part[2 * (ks * items + it)], y1 = part[2 * (ks * items + it) + 1];
-        x0.x += y0.x; x0.y += y0.y; x0.z += y0.z; x0.w += y0.w;
-        x1.x += y1.x; x1.y += y1.y; x1.z += y1.z; x1.w += y1.w;
-      }
-      const int j = it / CPR, c = it - j * CPR;
-      const int h = kvh * G + j / p.qlen, qp = j % p.qlen;
-      const int row = (b * p.hq + h) * p.qlen + qp;
-      float4 *dst = reinterpret_cast<float4 *>(&p.ws_acc[((int64_t)sg * rows_total + row) * D + c * VEC]);
-      dst[0] = x0;
-      dst[1] = x1;
-    }
-  }
-  for (int j = tid; j < GQ; j += kAttnThreads) {
-    const int h = kvh * G + j / p.qlen, qp = j % p.qlen;
-    const int row = (b * p.hq + h) * p.qlen + qp;
-    p.ws_m[(int64_t)sg * rows_total + row] = rm[j];
-    p.ws_l[(int64_t)sg * rows_total + row] = rl[j];
-  }
-}
-
-// LDS bytes of the MFMA split kernel.
-static size_t mfma_attn_lds(int gq, int head_dim, int ch) {
-  const int items = gq * (head_dim / 8);
-  const int nks = items >= kAttnThreads ? 1 : std::min(4, kAttnThreads / items);
-  const size_t head = (size_t)ch * head_dim * 2 + (size_t)gq * ch * 4 + (size_t)((2 * gq + 3) & ~3) * 4;
-  return head + (nks > 1 ? (size_t)nks * items * 32 : 0);
-}
-
 // One block per query row (b, h, q position).  Thread (g, i) takes the
 // 4 output dims 4i .. 4i + 3 of splits g, g + groups, ...: the loads of up
 // to kCombineBatch splits are issued together, and the thread folds them
 // into a running (max, sum, accumulator) by log-sum-exp merging.  The
 // groups' partial results then meet in LDS.
-constexpr int kCombineBatch = 8;
-
-__device__ __forceinline__ void lse_merge(float &m, float &l, float4 &o, float m2, float l2, const float4 &o2) {
-  if (m2 == -INFINITY) return;
-  if (m == -INFINITY) {
-    m = m2;
-    l = l2;
-    o = o2;
-    return;
-  }
-  const float M = fmaxf(m, m2), a = __expf(m - M), c = __expf(m2 - M);
-  m = M;
-  l = l * a + l2 * c;
-  o.x = o.x * a + o2.x * c;
-  o.y = o.y * a + o2.y * c;
-  o.z = o.z * a + o2.z * c;
-  o.w = o.w * a + o2.w * c;
-}
-
 template <int DT>
 __global__ void __launch_bounds__(kAttnThreads) decode_attn_combine_kernel(AttnParams p) {
   __shared__ float sm[kAttnThreads], sl[kAttnThreads];
@@ -433,8 +227,10 @@ __global__ void __launch_bounds__(kAttnThreads) decode_attn_combine_kernel(AttnP
           as[u] = make_float4(0.f, 0.f, 0.f, 0.f);
         }
       }
-#pragma unroll
-      for (int u = 0; u < kCombineBatch; ++u) lse_merge(m, l, o, ms[u], ls[u], as[u]);
+      float bm, bl;
+      float4 bo;
+      lse_fold<kCombineBatch>(ms, ls, as, bm, bl, bo);
+      lse_merge(m, l, o, bm, bl, bo);
     }
   }
   sm[tid] = m;
@@ -442,9 +238,140 @@ __global__ void __launch_bounds__(kAttnThreads) decode_attn_combine_kernel(AttnP
   so[tid] = o;
   __syncthreads();
   if (g != 0) return;
-  for (int gg = 1; gg < groups; ++gg) lse_merge(m, l, o, sm[gg * d4n + i], sl[gg * d4n + i], so[gg * d4n + i]);
+  lse_fold_lds(sm, sl, so, groups, d4n, i, m, l, o);
   const float inv = (m != -INFINITY && l > 0.f) ? 1.f / l : 0.f;
   const int64_t ob = (((int64_t)b * p.qlen + qp) * p.hq + h) * D + 4 * i;
+  store_elem<DT>(p.out, ob, o.x * inv);
+  store_elem<DT>(p.out, ob + 1, o.y * inv);
+  store_elem<DT>(p.out, ob + 2, o.z * inv);
+  store_elem<DT>(p.out, ob + 3, o.w * inv);
+}
+
+// Final kernel of the fused path, one block per query row (b, h, q
+// position): attention over the row's P retrieved keys in one pass - lane
+// group `slot` of LG lanes takes keys slot, slot + NSLOT, ... (at most
+// kFinalUT of them), each lane one 16-byte chunk of the key, with every K
+// and V chunk and the hot partials loaded up front - then a log-sum-exp
+// merge with the hot window's split partials (m, l, acc) that the fused
+// gather launch left in the workspace.  Retrieved keys are never masked.
+template <int DT, int LG>
+__global__ void __launch_bounds__(kAttnThreads) decode_attn_final_kernel(AttnParams p, int s_hot) {
+  constexpr int VEC = Elem<DT>::VEC, EB = Elem<DT>::BYTES;
+  constexpr int NSLOT = kAttnThreads / LG, UT = kFinalUT, W = kAttnThreads / 64;
+  __shared__ float red[W][512];  // per-wave V sums (head_dim <= 512)
+  __shared__ float bm[W], bl[W];
+  __shared__ float sm[kAttnThreads], sl[kAttnThreads];
+  __shared__ float4 so[kAttnThreads];
+  const int row = blockIdx.x;  // (b*Hq + h)*Q + qp
+  const int qp = row % p.qlen, bh = row / p.qlen;
+  const int b = bh / p.hq, h = bh % p.hq;
+  const int r = b * p.hkv + h / (p.hq / p.hkv);
+  const int D = p.head_dim, cpr = D / VEC, P = p.cold_len;
+  const int rows_total = p.batch * p.hq * p.qlen;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int slot = tid / LG, gl = tid % LG;
+  const bool on = gl < cpr;
+  const char *kbase = p.cold_k + (int64_t)r * P * D * EB;
+  const char *vbase = p.cold_v + (int64_t)r * P * D * EB;
+  uint4 kx[UT], vx[UT];
+#pragma unroll
+  for (int i = 0; i < UT; ++i) {
+    const int kk = slot + i * NSLOT;
+    const bool in = on && kk < P;
+    kx[i] = in ? load16(kbase + ((int64_t)kk * D + gl * VEC) * EB) : make_uint4(0, 0, 0, 0);
+    vx[i] = in ? load16(vbase + ((int64_t)kk * D + gl * VEC) * EB) : make_uint4(0, 0, 0, 0);
+  }
+  // Hot partials: thread (g, i4) owns output dims 4 i4 .. 4 i4 + 3 of
+  // splits g, g + groups, ...
+  const int d4n = D / 4, groups = kAttnThreads / d4n, g = tid / d4n, i4 = tid - g * d4n;
+  float hm[kCombineBatch], hl[kCombineBatch];
+  float4 ha[kCombineBatch];
+#pragma unroll
+  for (int u = 0; u < kCombineBatch; ++u) {
+    const int sp = g + u * groups;
+    if (g < groups && sp < s_hot) {
+      const int64_t at = (int64_t)sp * rows_total + row;
+      hm[u] = p.ws_m[at];
+      hl[u] = p.ws_l[at];
+      ha[u] = *reinterpret_cast<const float4 *>(&p.ws_acc[at * D + 4 * i4]);
+    } else {
+      hm[u] = -INFINITY;
+      hl[u] = 0.f;
+      ha[u] = make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+  }
+  const uint4 qx = on ? load16(p.q + ((int64_t)b * p.qs0 + (int64_t)h * p.qs1 + (int64_t)qp * p.qs2 + gl * VEC) * EB)
+                      : make_uint4(0, 0, 0, 0);
+  // Scores; every lane of a group holds its key's score.
+  float sc[UT];
+  float mloc = -INFINITY;
+#pragma unroll
+  for (int i = 0; i < UT; ++i) {
+    const float part = on ? chunk_dot<DT>(kx[i], qx, 0.f) : 0.f;
+    sc[i] = group_sum<LG>(part) * p.scale;
+    if (slot + i * NSLOT < P) mloc = fmaxf(mloc, sc[i]);
+  }
+  mloc = wave_max(mloc);
+  if (lane == 0) bm[wave] = mloc;
+  __syncthreads();
+  float M = bm[0];
+#pragma unroll
+  for (int w = 1; w < W; ++w) M = fmaxf(M, bm[w]);
+  float lsum = 0.f;
+  float acc[VEC];
+#pragma unroll
+  for (int e = 0; e < VEC; ++e) acc[e] = 0.f;
+#pragma unroll
+  for (int i = 0; i < UT; ++i) {
+    const float w = slot + i * NSLOT < P ? __expf(sc[i] - M) : 0.f;
+    if (gl == 0) lsum += w;
+    float v[VEC];
+    unpack_chunk<DT>(vx[i], v);
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) acc[e] = fmaf(w, v[e], acc[e]);
+  }
+  lsum = wave_sum(lsum);
+#pragma unroll
+  for (int e = 0; e < VEC; ++e) acc[e] = across_groups_sum<LG>(acc[e]);
+  if (lane < LG && on) {
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) red[wave][gl * VEC + e] = acc[e];
+  }
+  if (lane == 0) bl[wave] = lsum;
+  __syncthreads();
+  // Merge: each thread folds its hot partials (max first, then the scaled
+  // sums, so the exponentials are independent); group 0 also folds the
+  // retrieved keys' partial.  The groups then meet in LDS.
+  float m, l;
+  float4 o;
+  lse_fold<kCombineBatch>(hm, hl, ha, m, l, o);
+  if (g < groups) {
+    for (int sp = g + kCombineBatch * groups; sp < s_hot; sp += groups) {
+      const int64_t at = (int64_t)sp * rows_total + row;
+      lse_merge(m, l, o, p.ws_m[at], p.ws_l[at], *reinterpret_cast<const float4 *>(&p.ws_acc[at * D + 4 * i4]));
+    }
+  }
+  if (g == 0) {
+    float L = 0.f;
+    float4 ar = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (int w = 0; w < W; ++w) {
+      L += bl[w];
+      ar.x += red[w][4 * i4];
+      ar.y += red[w][4 * i4 + 1];
+      ar.z += red[w][4 * i4 + 2];
+      ar.w += red[w][4 * i4 + 3];
+    }
+    lse_merge(m, l, o, M, L, ar);
+  }
+  sm[tid] = m;
+  sl[tid] = l;
+  so[tid] = o;
+  __syncthreads();
+  if (g != 0) return;
+  lse_fold_lds(sm, sl, so, groups, d4n, i4, m, l, o);
+  const float inv = (m != -INFINITY && l > 0.f) ? 1.f / l : 0.f;
+  const int64_t ob = (((int64_t)b * p.qlen + qp) * p.hq + h) * D + 4 * i4;
   store_elem<DT>(p.out, ob, o.x * inv);
   store_elem<DT>(p.out, ob + 1, o.y * inv);
   store_elem<DT>(p.out, ob + 2, o.z * inv);
@@ -478,8 +405,8 @@ static size_t ws_layout(int batch, int hq, int hkv, int head_dim, int qlen, int 
   return *off_acc + ((S * R * head_dim * 4 + 255) & ~size_t(255));
 }
 
-// Checks the arguments and launches the split and combine kernels on `st`.
-static int attention_launch(const kiv_attention_args_t *a, hipStream_t st, const char *who) {
+// Checks the arguments shared by both attention entry points.
+static int attention_check(const kiv_attention_args_t *a, const char *who) {
   if (!a) return fail(KIV_ERR_INVALID, "%s: null argument", who);
   const int dt = a->dtype;
   if (dt != KIV_DTYPE_F32 && dt != KIV_DTYPE_F16 && dt != KIV_DTYPE_BF16)
@@ -509,15 +436,26 @@ static int attention_launch(const kiv_attention_args_t *a, hipStream_t st, const
       return fail(KIV_ERR_INVALID, "%s: hot strides must be multiples of %d", who, vec);
   if (a->mask && (a->mask_kind < KIV_MASK_BOOL || a->mask_kind > KIV_MASK_BF16))
     return fail(KIV_ERR_INVALID, "%s: unknown mask kind %d", who, a->mask_kind);
-  const int L = a->cold_len + a->hot_len;
   size_t off_m, off_l, off_acc;
   const size_t need = ws_layout(B, hq, hkv, D, Q, a->cold_len, a->hot_len, &off_m, &off_l, &off_acc);
   if (a->workspace_bytes < need)
     return fail(KIV_ERR_INVALID, "%s: workspace %zu bytes, %zu needed", who, a->workspace_bytes, need);
   int ch, sc, sh;
   split_counts(a->cold_len, a->hot_len, B * hkv, &ch, &sc, &sh);
-  const int S = sc + sh;
-  if (S > kMaxSplits) return fail(KIV_ERR_UNSUPPORTED, "%s: %d keys is too many", who, L);
+  if (sc + sh > kMaxSplits)
+    return fail(KIV_ERR_UNSUPPORTED, "%s: %d keys is too many", who, a->cold_len + a->hot_len);
+  return KIV_OK;
+}
+
+// Kernel parameters for the splits of [retrieved ; hot] in the workspace
+// layout of kiv_attention_workspace_size.  hot_only: the splits cover the
+// hot keys only (split_cold = 0; the retrieved keys go to the final kernel).
+static AttnParams attention_params(const kiv_attention_args_t *a, bool hot_only) {
+  const int B = a->batch, hq = a->num_q_heads, hkv = a->num_kv_heads, D = a->head_dim, Q = a->q_len;
+  size_t off_m, off_l, off_acc;
+  ws_layout(B, hq, hkv, D, Q, a->cold_len, a->hot_len, &off_m, &off_l, &off_acc);
+  int ch, sc, sh;
+  split_counts(a->cold_len, a->hot_len, B * hkv, &ch, &sc, &sh);
   AttnParams p;
   p.q = (const char *)a->q;
   p.qs0 = a->q_stride[0];
@@ -548,27 +486,44 @@ static int attention_launch(const kiv_attention_args_t *a, hipStream_t st, const
   p.head_dim = D;
   p.scale = a->scaling;
   p.chunk = ch;
-  p.nsplit = S;
-  p.split_cold = sc;
+  p.nsplit = hot_only ? sh : sc + sh;
+  p.split_cold = hot_only ? 0 : sc;
+  p.split0 = 0;
   char *ws = (char *)a->workspace;
   p.ws_m = (float *)(ws + off_m);
   p.ws_l = (float *)(ws + off_l);
   p.ws_acc = (float *)(ws + off_acc);
   p.out = (char *)a->out;
-  p.split0 = 0;
+  return p;
+}
+
+static bool mfma_head_dim(int dt, int D) {
   const int kt = D / 32;
-  const bool mfma = dt != KIV_DTYPE_F32 && D % 32 == 0 && (kt <= 4 || kt == 6 || kt == 8 || kt == 16);
+  return dt != KIV_DTYPE_F32 && D % 32 == 0 && (kt <= 4 || kt == 6 || kt == 8 || kt == 16);
+}
+
+// Checks the arguments and launches the split and combine kernels on `st`.
+static int attention_launch(const kiv_attention_args_t *a, hipStream_t st, const char *who) {
+  int rc = attention_check(a, who);
+  if (rc) return rc;
+  const int dt = a->dtype, B = a->batch, hq = a->num_q_heads, hkv = a->num_kv_heads, D = a->head_dim,
+            Q = a->q_len;
+  const int GQ = hq / hkv * Q;
+  const AttnParams p = attention_params(a, false);
+  const int S = p.nsplit, ch = p.chunk;
+  const int kt = D / 32;
+  const bool mfma = mfma_head_dim(dt, D);
   const size_t lds = mfma ? mfma_attn_lds(GQ, D, ch)
                           : (size_t)GQ * D * elem_bytes(dt) + ((size_t)GQ * ch + 4 * kRowTile * D + 2 * GQ) * 4;
   if (lds > device_lds_limit())
-    return fail(KIV_ERR_UNSUPPORTED, "%s: %d keys need %zu bytes of LDS", who, L, lds);
+    return fail(KIV_ERR_UNSUPPORTED, "%s: %d keys need %zu bytes of LDS", who, a->cold_len + a->hot_len, lds);
   auto launch_split = [&](auto kern) -> int {
     if (lds > 65536) KIV_HIP(hipFuncSetAttribute((const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
     hipLaunchKernelGGL(kern, dim3(S, B * hkv), dim3(kAttnThreads), lds, st, p);
     KIV_HIP(hipGetLastError());
     return (int)KIV_OK;
   };
-  int rc = with_dt(dt, [&](auto dtc) {
+  rc = with_dt(dt, [&](auto dtc) {
     constexpr int DTV = decltype(dtc)::value;
     int r2;
     if constexpr (DTV != DT_F32) {
@@ -579,6 +534,41 @@ static int attention_launch(const kiv_attention_args_t *a, hipStream_t st, const
     }
     if (r2) return r2;
     hipLaunchKernelGGL((decode_attn_combine_kernel<DTV>), dim3(B * hq * Q), dim3(kAttnThreads), 0, st, p);
+    return (int)KIV_OK;
+  });
+  if (rc) return rc;
+  KIV_HIP(hipGetLastError());
+  return KIV_OK;
+}
+
+// Retrieved keys the final kernel takes in its one pass (lane groups of lg
+// lanes, kFinalUT keys per group).
+static int final_capacity(int lg) { return kAttnThreads / lg * kFinalUT; }
+
+int fused_attention_plan(const kiv_attention_args_t *a, FusedAttention *f) {
+  int rc = attention_check(a, "kiv_retrieve_attend");
+  if (rc) return rc;
+  const int dt = a->dtype, D = a->head_dim;
+  const int GQ = a->num_q_heads / a->num_kv_heads * a->q_len;
+  const int lg = lanes_per_row(dt, D);
+  if (!mfma_head_dim(dt, D) || a->q_len != 1 || a->cold_len < 1 || a->cold_len > final_capacity(lg))
+    return KIV_ERR_UNSUPPORTED;
+  f->p = attention_params(a, true);
+  f->s_hot = f->p.nsplit;
+  f->lds = mfma_attn_lds(GQ, D, f->p.chunk);
+  if (f->lds > device_lds_limit()) return KIV_ERR_UNSUPPORTED;
+  f->kt = D / 32;
+  f->lg = lg;
+  f->dtype = dt;
+  return KIV_OK;
+}
+
+int fused_attention_finish(const FusedAttention &f, hipStream_t st) {
+  const AttnParams &p = f.p;
+  const int rows = p.batch * p.hq * p.qlen;
+  int rc = with_dt_lg(f.dtype, f.lg, [&](auto dtc, auto lgc) {
+    hipLaunchKernelGGL((decode_attn_final_kernel<decltype(dtc)::value, decltype(lgc)::value>), dim3(rows),
+                       dim3(kAttnThreads), 0, st, p, f.s_hot);
     return (int)KIV_OK;
   });
   if (rc) return rc;

@@ -26,6 +26,7 @@
 #include <algorithm>
 #include <type_traits>
 
+#include "kiv_attn_device.h"
 #include "kiv_common.h"
 #include "kiv_dispatch.h"
 #include "kiv_internal.h"
@@ -908,24 +909,51 @@ __global__ void __launch_bounds__(kSelThreads) fine_select_kernel(
 // id to idx_out[b][r].  Block (0, 0) also finishes the fine telemetry.
 constexpr int kGatherCands = 4;
 
-template <int DT>
-__global__ void __launch_bounds__(256) gather_kernel(
-    const uint64_t *__restrict__ list, int64_t list_ld, const int32_t *__restrict__ list_count,
-    const int32_t *__restrict__ counters, int has_pages, const int32_t *__restrict__ page_list,
-    const uint64_t *__restrict__ ktab, const uint64_t *__restrict__ vtab, int chunk_shift, int64_t page_bytes,
-    const char *__restrict__ part_k, const char *__restrict__ part_v, const char *__restrict__ k_stage,
-    int64_t stage_ld, int page_size, int partial_len, int64_t num_finalized, int batch, int hkv, int head_dim,
-    int width, int cpr, char *__restrict__ k_out,
-    char *__restrict__ v_out, int64_t *__restrict__ idx_out, const float *__restrict__ fine_stats, int round,
-    float *stats_out, double *stats_accum) {
+struct GatherArgs {
+  const uint64_t *list;
+  int64_t list_ld;
+  const int32_t *list_count, *counters;
+  int has_pages;
+  const int32_t *page_list;
+  const uint64_t *ktab, *vtab;
+  int chunk_shift;
+  int64_t page_bytes;
+  const char *part_k, *part_v, *k_stage;
+  int64_t stage_ld;
+  int page_size, partial_len;
+  int64_t num_finalized;
+  int batch, hkv, head_dim, width, cpr;
+  char *k_out, *v_out;
+  int64_t *idx_out;
+  const float *fine_stats;
+  int round;
+  float *stats_out;
+  double *stats_accum;
+};
+
+template <int DT> __device__ void gather_block(const GatherArgs &ga, int bx, int b) {
   constexpr int VEC = Elem<DT>::VEC, EB = Elem<DT>::BYTES;
   __shared__ int slot_of[kGatherCands], cand_of[kGatherCands];
-  const int b = blockIdx.y, tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const uint64_t *list = ga.list;
+  const int64_t list_ld = ga.list_ld;
+  const int32_t *list_count = ga.list_count, *counters = ga.counters, *page_list = ga.page_list;
+  const uint64_t *ktab = ga.ktab, *vtab = ga.vtab;
+  const int has_pages = ga.has_pages, chunk_shift = ga.chunk_shift, page_size = ga.page_size;
+  const int partial_len = ga.partial_len, batch = ga.batch, hkv = ga.hkv, head_dim = ga.head_dim;
+  const int width = ga.width, cpr = ga.cpr, round = ga.round;
+  const int64_t page_bytes = ga.page_bytes, stage_ld = ga.stage_ld, num_finalized = ga.num_finalized;
+  const char *part_k = ga.part_k, *part_v = ga.part_v, *k_stage = ga.k_stage;
+  char *k_out = ga.k_out, *v_out = ga.v_out;
+  int64_t *idx_out = ga.idx_out;
+  const float *fine_stats = ga.fine_stats;
+  float *stats_out = ga.stats_out;
+  double *stats_accum = ga.stats_accum;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int U = has_pages ? counters[0] : 0;
   const int64_t split = (int64_t)U * page_size;
   const int n = (int)split + partial_len;
   const int k = min(width, n);
-  if (blockIdx.x == 0 && b == 0) {
+  if (bx == 0 && b == 0) {
     if (tid == 0) {
       float m = -INFINITY;
       double t = 0.0;
@@ -946,7 +974,7 @@ __global__ void __launch_bounds__(256) gather_kernel(
     }
   }
   const int C = list_count[b];
-  const int first = blockIdx.x * kGatherCands;
+  const int first = bx * kGatherCands;
   if (first >= C) return;
   const uint64_t *L = list + (int64_t)b * list_ld;
   const int i = first + wave;
@@ -1002,6 +1030,25 @@ __global__ void __launch_bounds__(256) gather_kernel(
   }
 }
 
+template <int DT> __global__ void __launch_bounds__(256) gather_kernel(GatherArgs ga) {
+  gather_block<DT>(ga, blockIdx.x, blockIdx.y);
+}
+
+// The gather plus the hot window's attention splits (kiv_retrieve_attend):
+// blocks [0, gx * B) gather, the s_hot * R blocks after them each run one
+// hot split of one kv row.  The splits do not depend on the retrieval, so
+// they run alongside the gather instead of after it.
+template <int DT, int KT>
+__global__ void __launch_bounds__(256) gather_attn_kernel(GatherArgs ga, AttnParams p, int gx, int s_hot) {
+  const int gather_blocks = gx * ga.batch;
+  if ((int)blockIdx.x < gather_blocks) {
+    gather_block<DT>(ga, blockIdx.x % gx, blockIdx.x / gx);
+    return;
+  }
+  const int i = blockIdx.x - gather_blocks;
+  attn_mfma_split<DT, KT>(p, i % s_hot, i / s_hot);
+}
+
 // Launches the select kernel kern_of(V) whose register chunks per thread V
 // is the smallest of 2, 4, 8, 16 that holds a row of n keys (16 for longer
 // rows, which are then re-read from memory).
@@ -1029,7 +1076,9 @@ int kiv_max_union_pages(const kiv_store_t *s, int32_t q_len, int32_t top_pages, 
   return KIV_OK;
 }
 
-int kiv_retrieve(kiv_store_t *s, const kiv_retrieve_args_t *a, kiv_stream_t stream) {
+// The retrieval; with `fa`, the gather launch also runs the hot window's
+// attention splits of the fused path.
+static int retrieve_impl(kiv_store_t *s, const kiv_retrieve_args_t *a, hipStream_t st, const FusedAttention *fa) {
   if (!s || !a) return fail(KIV_ERR_INVALID, "kiv_retrieve: null argument");
   const kiv_store_config_t &c = s->cfg;
   const int dt = c.dtype, D = c.head_dim, ps = c.page_size, B = c.batch, hq = c.num_q_heads,
@@ -1055,7 +1104,6 @@ int kiv_retrieve(kiv_store_t *s, const kiv_retrieve_args_t *a, kiv_stream_t stre
   if (s->num_pages > (int64_t)kMaxWords * 32)
     return fail(KIV_ERR_UNSUPPORTED, "kiv_retrieve: more than %d pages", kMaxWords * 32);
   DeviceGuard guard(s->device);
-  hipStream_t st = (hipStream_t)stream;
   const int lg = lanes_per_row(dt, D);
   const int round = c.score_rounding == KIV_ROUND_ACTIVATION ? 1 : 0;
   const int N = (int)s->num_pages;
@@ -1198,23 +1246,96 @@ int kiv_retrieve(kiv_store_t *s, const kiv_retrieve_args_t *a, kiv_stream_t stre
   }
   {
     const unsigned gx = (unsigned)((lmax + kGatherCands - 1) / kGatherCands);
+    GatherArgs ga;
+    ga.list = list;
+    ga.list_ld = list_ld;
+    ga.list_count = list_count;
+    ga.counters = (const int32_t *)s->counters.ptr;
+    ga.has_pages = N > 0 ? 1 : 0;
+    ga.page_list = (const int32_t *)s->page_list.ptr;
+    ga.ktab = (const uint64_t *)s->k_tab.ptr;
+    ga.vtab = (const uint64_t *)s->v_tab.ptr;
+    ga.chunk_shift = s->chunk_shift;
+    ga.page_bytes = s->page_bytes;
+    ga.part_k = (const char *)s->k_part.ptr;
+    ga.part_v = (const char *)s->v_part.ptr;
+    ga.k_stage = k_stage;
+    ga.stage_ld = ldc;
+    ga.page_size = ps;
+    ga.partial_len = (int)s->partial_len;
+    ga.num_finalized = s->num_pages * ps;
+    ga.batch = B;
+    ga.hkv = hkv;
+    ga.head_dim = D;
+    ga.width = a->out_width;
+    ga.cpr = cpr;
+    ga.k_out = (char *)a->k_out;
+    ga.v_out = (char *)a->v_out;
+    ga.idx_out = a->idx_out;
+    ga.fine_stats = fine_stats;
+    ga.round = round;
+    ga.stats_out = a->stats_out;
+    ga.stats_accum = a->stats_accum;
     s->prof_begin(KIV_STAGE_GATHER, st);
-    rc = with_dt(dt, [&](auto dtc) {
-      hipLaunchKernelGGL((gather_kernel<decltype(dtc)::value>), dim3(gx, (unsigned)B), dim3(256), 0, st,
-                         (const uint64_t *)list, list_ld, (const int32_t *)list_count,
-                         (const int32_t *)s->counters.ptr, N > 0 ? 1 : 0, (const int32_t *)s->page_list.ptr,
-                         (const uint64_t *)s->k_tab.ptr, (const uint64_t *)s->v_tab.ptr, s->chunk_shift,
-                         s->page_bytes, (const char *)s->k_part.ptr, (const char *)s->v_part.ptr,
-                         (const char *)k_stage, ldc, ps, (int)s->partial_len, s->num_pages * ps, B, hkv, D,
-                         a->out_width, cpr, (char *)a->k_out,
-                         (char *)a->v_out, a->idx_out, (const float *)fine_stats, round, a->stats_out, a->stats_accum);
-      return (int)KIV_OK;
-    });
+    if (fa) {
+      const unsigned blocks = gx * (unsigned)B + (unsigned)(fa->s_hot * s->kr);
+      rc = with_dt(dt, [&](auto dtc) {
+        constexpr int DTV = decltype(dtc)::value;
+        if constexpr (DTV == DT_F32) {
+          return fail(KIV_ERR_UNSUPPORTED, "kiv_retrieve_attend: no fused path for fp32");
+        } else {
+          return with_kt(fa->kt, [&](auto ktc) {
+            auto kern = gather_attn_kernel<DTV, decltype(ktc)::value>;
+            if (fa->lds > 65536)
+              KIV_HIP(hipFuncSetAttribute((const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                          (int)fa->lds));
+            hipLaunchKernelGGL(kern, dim3(blocks), dim3(256), fa->lds, st, ga, fa->p, (int)gx, fa->s_hot);
+            return (int)KIV_OK;
+          });
+        }
+      });
+    } else {
+      rc = with_dt(dt, [&](auto dtc) {
+        hipLaunchKernelGGL((gather_kernel<decltype(dtc)::value>), dim3(gx, (unsigned)B), dim3(256), 0, st, ga);
+        return (int)KIV_OK;
+      });
+    }
     s->prof_end(KIV_STAGE_GATHER, st);
     if (rc) return rc;
     KIV_HIP(hipGetLastError());
   }
   return KIV_OK;
+}
+
+int kiv_retrieve(kiv_store_t *s, const kiv_retrieve_args_t *a, kiv_stream_t stream) {
+  return retrieve_impl(s, a, (hipStream_t)stream, nullptr);
+}
+
+int kiv_retrieve_attend(kiv_store_t *s, const kiv_retrieve_args_t *ra, const kiv_attention_args_t *aa,
+                        kiv_stream_t stream) {
+  if (!s || !ra || !aa) return fail(KIV_ERR_INVALID, "kiv_retrieve_attend: null argument");
+  const kiv_store_config_t &c = s->cfg;
+  if (aa->cold_k != ra->k_out || aa->cold_v != ra->v_out || aa->cold_len != ra->out_width)
+    return fail(KIV_ERR_INVALID, "kiv_retrieve_attend: the attention's retrieved keys must be the retrieval's "
+                "outputs (cold_k = k_out, cold_v = v_out, cold_len = out_width)");
+  if (aa->batch != c.batch || aa->num_q_heads != c.num_q_heads || aa->num_kv_heads != c.num_kv_heads ||
+      aa->head_dim != c.head_dim || aa->dtype != c.dtype || aa->q_len != ra->q_len)
+    return fail(KIV_ERR_INVALID, "kiv_retrieve_attend: attention shapes differ from the store's");
+  DeviceGuard guard(s->device);
+  hipStream_t st = (hipStream_t)stream;
+  FusedAttention f;
+  int rc = fused_attention_plan(aa, &f);
+  if (rc == KIV_ERR_UNSUPPORTED) {
+    // Shapes outside the fused path: the two launches one after the other.
+    if ((rc = retrieve_impl(s, ra, st, nullptr))) return rc;
+    return kiv_decode_attention(aa, stream);
+  }
+  if (rc) return rc;
+  if ((rc = retrieve_impl(s, ra, st, &f))) return rc;
+  s->prof_begin(KIV_STAGE_ATTEND, st);
+  rc = fused_attention_finish(f, st);
+  s->prof_end(KIV_STAGE_ATTEND, st);
+  return rc;
 }
 
 }  // extern "C"

@@ -226,11 +226,14 @@ class KIVMiddleware:
             # The mask was built before this step's eviction: keep its last hot_len columns.
             if attention_mask is not None and attention_mask.shape[-1] > hot_len:
                 attention_mask = attention_mask[..., -hot_len:]
+            if _merged_kernel_applies(module, query, key, attention_mask, kwargs):
+                # Retrieval and the merged attention in one call (hot-window
+                # splits overlap the retrieval's gather).
+                out = store.retrieve_attend(query, scaling, kiv_config, key, value, attention_mask, step=step)
+                return out.to(query.dtype), None
             cold_k, cold_v = store.retrieve_top_kv(query, scaling, kiv_config, step=step)
             if cold_k is None:
                 return original_fn(module, query, key, value, attention_mask, **kwargs)
-            if _merged_kernel_applies(module, query, key, attention_mask, kwargs):
-                return decode_attention(query, cold_k, cold_v, key, value, attention_mask, scaling), None
             key = torch.cat([cold_k, key], dim=2)
             value = torch.cat([cold_v, value], dim=2)
             if attention_mask is not None:

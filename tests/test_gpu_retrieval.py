@@ -136,8 +136,10 @@ def check_retrieval(store, oracle, cfg, w, data, q, rounding="activation"):
     return k_out, v_out, sel
 
 
-def attention_check(q, cold_k, cold_v, hot_k, hot_v, scaling, mask=None, tol=2e-3):
-    out = decode_attention(q, cold_k, cold_v, hot_k, hot_v, mask, scaling)
+def attention_check(q, cold_k, cold_v, hot_k, hot_v, scaling, mask=None, tol=2e-3, out=None):
+    """decode_attention (or a given output of the same attention) against fp64 softmax attention."""
+    if out is None:
+        out = decode_attention(q, cold_k, cold_v, hot_k, hot_v, mask, scaling)
     keys = torch.cat([cold_k, hot_k], dim=2) if cold_k is not None else hot_k
     vals = torch.cat([cold_v, hot_v], dim=2) if cold_v is not None else hot_v
     m = None
@@ -398,3 +400,43 @@ def test_attention_repeated_calls_share_workspace(cuda):
         mk = lambda *s: torch.randn(*s, generator=g).to(torch.bfloat16).to(cuda)
         attention_check(mk(B, hq, 1, D), mk(B, hkv, P, D), mk(B, hkv, P, D), mk(B, hkv, T, D), mk(B, hkv, T, D),
                         D ** -0.5)
+
+
+FUSED = [
+    # name, workload overrides, hot-column mask
+    ("qwen_shape_bf16", dict(num_q_heads=28, num_kv_heads=4, head_dim=128, dtype=torch.bfloat16, cold=9000,
+                             hot=2048, top_pages=8, top_p=256, segment=1024), None),
+    ("gqa_f16_masked", dict(num_q_heads=32, num_kv_heads=4, head_dim=64, dtype=torch.float16, cold=5000, hot=300,
+                            top_pages=4, top_p=200, segment=512), "bool"),
+    ("mqa_d256_at_capacity", dict(num_q_heads=8, num_kv_heads=1, head_dim=256, dtype=torch.bfloat16, cold=5000,
+                                  hot=64, top_pages=4, top_p=128, segment=512), None),
+    ("one_hot_row", dict(num_q_heads=8, num_kv_heads=2, head_dim=96, dtype=torch.bfloat16, cold=3000, hot=1,
+                         top_pages=4, top_p=100, segment=256), None),
+    # outside the fused path: two launches behind the same call
+    ("over_capacity", dict(num_q_heads=8, num_kv_heads=1, head_dim=256, dtype=torch.bfloat16, cold=5000, hot=64,
+                           top_pages=8, top_p=300, segment=512), None),
+    ("fp32", dict(num_q_heads=4, num_kv_heads=2, head_dim=32, dtype=torch.float32, cold=1500, hot=50,
+                  top_pages=5, top_p=40, segment=100), "float"),
+]
+
+
+@pytest.mark.parametrize("name,over,mask_kind", FUSED, ids=[c[0] for c in FUSED])
+def test_retrieve_attend(cuda, name, over, mask_kind):
+    """kiv_retrieve_attend: the hot window's splits run in the gather launch
+    and one final kernel per query row attends the retrieved keys and merges.
+    The output must meet the attention bar over the rows the retrieval
+    selects (checked by a second, identical retrieval)."""
+    w = Workload(name, **over)
+    data = generate(w, seed=31)
+    store, oracle, cfg = build(w, data, cuda)
+    q, hk, hv = data["q"].to(cuda), data["hot_k"].to(cuda), data["hot_v"].to(cuda)
+    g = torch.Generator().manual_seed(32)
+    mask = None
+    if mask_kind == "bool":
+        mask = (torch.rand(1, 1, 1, w.hot, generator=g) > 0.3).to(cuda)
+    elif mask_kind == "float":
+        mask = torch.where(torch.rand(1, 1, 1, w.hot, generator=g) > 0.3, 0.0, -1e4).to(cuda)
+    out = store.retrieve_attend(q, w.scaling, cfg, hk, hv, mask)
+    assert out.shape == (1, 1, w.num_q_heads, w.head_dim) and out.dtype == w.dtype
+    k_out, v_out, _ = check_retrieval(store, oracle, cfg, w, data, data["q"])
+    attention_check(q, k_out, v_out, hk, hv, w.scaling, mask, out=out)
