@@ -97,6 +97,7 @@ struct kiv_store {
   kiv::DevBuf row_stats;     // [R][2] f32 (max, sum) + [B][2] fine stats
   kiv::DevBuf row_pages;     // [R][top pages] i32 each query row's top pages
   kiv::DevBuf page_list;     // [N] i32 union pages ascending
+  kiv::DevBuf union_bits;    // [ceil(N/32)] u32 page bitmap of long row lists, zero between calls
   kiv::DevBuf counters;      // i32: [0] = U, the union size of the last coarse pass
   kiv::DevBuf fine_keys;     // [B][ld] u32
   kiv::DevBuf sel_list;      // [B][list_ld] u64 top-P' candidates + [B] i32 counts

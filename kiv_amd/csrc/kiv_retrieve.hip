@@ -40,6 +40,9 @@ constexpr int kMaxWords = 4096;     // bitmap words ranked in LDS (131072 pages)
 constexpr int kCandCap = 2048;      // candidates a select keeps in LDS
 constexpr int kRankCap = 1024;      // candidates ranked by counting
 constexpr size_t kMaxStageBytes = size_t(256) << 20;  // HBM staging of candidate K rows per store
+constexpr int64_t kFineQueryBytes = 48 << 10;  // query rows per kv row the fine scan keeps in LDS
+constexpr int64_t kRowListInScan = 8192;        // row-list entries a fine-scan block ORs into its union
+constexpr int kUnionThreads = 1024;
 
 // Union source of the fine stages: none (no finished pages), the coarse
 // select's row page lists (a fresh coarse pass) or the stored union list.
@@ -434,6 +437,80 @@ __device__ int rank_union(const int32_t *row_pages, int nk, int words, uint32_t 
   if (threadIdx.x == 0) rank[words] = before;
   __syncthreads();
   return before;
+}
+
+// Union of long row lists (several query passes, or a long query): marks
+// the listed pages in a page bitmap in memory.
+__global__ void __launch_bounds__(256) union_mark_kernel(const int32_t *__restrict__ row_pages, int64_t n,
+                                                         uint32_t *bitmap) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
+    const int page = row_pages[i];
+    atomicOr(&bitmap[page >> 5], 1u << (page & 31));
+  }
+}
+
+// One block: the marked pages in ascending order into page_list (and
+// pages_out), U into counters[0] (and union_out), the coarse telemetry
+// (max over rows, mean over rows and pages); leaves the bitmap zeroed.
+template <int DT>
+__global__ void __launch_bounds__(kUnionThreads) union_list_kernel(
+    uint32_t *bitmap, int words, int32_t *page_list, int32_t *counters, int32_t *pages_out, int32_t *union_out,
+    const float *__restrict__ coarse_stats, int rows, int n_pages, int round, float *stats_out,
+    double *stats_accum) {
+  constexpr int NT = kUnionThreads, W = NT / 64;
+  __shared__ int scan_tmp[W];
+  __shared__ float red_m[W];
+  __shared__ double red_s[W];
+  const int tid = threadIdx.x;
+  int before = 0;
+  for (int base = 0; base < words; base += NT) {
+    const int w = base + tid;
+    uint32_t x = w < words ? bitmap[w] : 0u;
+    const int c = __popc(x);
+    int tot = 0;
+    const int incl = block_incl_scan<NT>(c, scan_tmp, &tot);
+    int pos = before + incl - c;
+    if (w < words) bitmap[w] = 0u;
+    while (x) {
+      const int page = w * 32 + __ffs(x) - 1;
+      x &= x - 1;
+      page_list[pos] = page;
+      if (pages_out) pages_out[pos] = page;
+      ++pos;
+    }
+    before += tot;
+  }
+  float m = -INFINITY;
+  double t = 0.0;
+  for (int r = tid; r < rows; r += NT) {
+    m = fmaxf(m, coarse_stats[2 * r]);
+    t += coarse_stats[2 * r + 1];
+  }
+  m = wave_max(m);
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) t += __shfl_xor(t, o, 64);
+  if ((tid & 63) == 0) {
+    red_m[tid >> 6] = m;
+    red_s[tid >> 6] = t;
+  }
+  __syncthreads();
+  if (tid != 0) return;
+  for (int w = 1; w < W; ++w) {
+    m = fmaxf(m, red_m[w]);
+    t += red_s[w];
+  }
+  counters[0] = before;
+  if (union_out) union_out[0] = before;
+  float mean = (float)(t / ((double)rows * (double)n_pages));
+  if (round) mean = round_act<DT>(mean);
+  if (stats_out) {
+    stats_out[0] = m;
+    stats_out[1] = mean;
+  }
+  if (stats_accum) {
+    stats_accum[0] += (double)m;
+    stats_accum[1] += (double)mean;
+  }
 }
 
 // Page id of the v-th union member (v < union size).
@@ -1098,9 +1175,6 @@ static int retrieve_impl(kiv_store_t *s, const kiv_retrieve_args_t *a, hipStream
   if (((uintptr_t)a->q & 15) || (a->q_stride[0] % vec) || (a->q_stride[1] % vec) || (a->q_stride[2] % vec))
     return fail(KIV_ERR_INVALID, "kiv_retrieve: q must be 16-byte aligned with strides multiple of %d", vec);
   const int rows = B * hq * Q;
-  if ((int64_t)rows * D > 12288)
-    return fail(KIV_ERR_UNSUPPORTED, "kiv_retrieve: B*Hq*Q*D = %lld exceeds 12288 (decode-sized queries only)",
-                (long long)rows * D);
   if (s->num_pages > (int64_t)kMaxWords * 32)
     return fail(KIV_ERR_UNSUPPORTED, "kiv_retrieve: more than %d pages", kMaxWords * 32);
   DeviceGuard guard(s->device);
@@ -1108,6 +1182,15 @@ static int retrieve_impl(kiv_store_t *s, const kiv_retrieve_args_t *a, hipStream
   const int round = c.score_rounding == KIV_ROUND_ACTIVATION ? 1 : 0;
   const int N = (int)s->num_pages;
   const int words = (N + 31) / 32;
+  const int G = hq / hkv;
+  // Query positions per pass: the fine scan keeps the G*Qb query rows of a
+  // kv row in LDS.  Longer queries (a prefill chunk with live retrieval) run
+  // the scans once per pass of Qb positions: the union is the union of the
+  // passes' row lists and the fine keys accumulate with atomicMax, which is
+  // the max over every head and position.
+  const int Qb = std::max(1, std::min(Q, (int)(kFineQueryBytes / ((int64_t)G * D * eb))));
+  const int passes = (Q + Qb - 1) / Qb;
+  const int64_t qstep = (int64_t)Qb * a->q_stride[2] * eb;  // bytes between passes' first positions
   int rc;
   if ((rc = s->row_stats.ensure((size_t)(rows + B) * 8, st, false))) return rc;
   float *coarse_stats = (float *)s->row_stats.ptr;
@@ -1120,59 +1203,92 @@ static int retrieve_impl(kiv_store_t *s, const kiv_retrieve_args_t *a, hipStream
   if (N > 0) {
     const bool reuse = a->reuse_candidates && s->union_valid && s->union_rows == rows;
     if (!reuse) {
-      union_src = UNION_ROWS;
       kc = std::min(a->top_pages, N);
       umax = std::min<int64_t>(N, (int64_t)rows * kc);
+      // The fine scan's blocks build the union themselves from short row
+      // lists; long ones (or several passes) get the union kernels.
+      union_src = passes == 1 && (int64_t)rows * kc <= kRowListInScan ? UNION_ROWS : UNION_LIST;
       const int64_t ld = ((int64_t)N + 63) & ~int64_t(63);
-      if ((rc = s->coarse_keys.ensure((size_t)rows * ld * 4, st, false))) return rc;
+      const int rows_pass = B * hq * Qb;
+      if ((rc = s->coarse_keys.ensure((size_t)rows_pass * ld * 4, st, false))) return rc;
       if ((rc = s->row_pages.ensure((size_t)rows * kc * 4, st, false))) return rc;
       if ((rc = s->page_list.ensure((size_t)N * 4, st, false))) return rc;
       const int kt = D / 32;
       const bool mfma = dt != KIV_DTYPE_F32 && D % 32 == 0 && (kt <= 4 || kt == 6 || kt == 8 || kt == 16);
-      s->prof_begin(KIV_STAGE_COARSE_SCAN, st);
-      if (mfma) {
-        const int pages_per_block = (kScanThreads / 64) * kScanMfmaPages;
-        const int blocks = (int)(((int64_t)N + pages_per_block - 1) / pages_per_block);
-        rc = with_dt(dt, [&](auto dtc) {
-          constexpr int DTV = decltype(dtc)::value;
-          if constexpr (DTV == DT_F32) {
-            return (int)KIV_ERR_UNSUPPORTED;
-          } else {
-            return with_kt(kt, [&](auto ktc) {
-              hipLaunchKernelGGL((coarse_scan_mfma_kernel<DTV, decltype(ktc)::value>), dim3(blocks, s->kr),
-                                 dim3(kScanThreads), 0, st, (const char *)s->summ.ptr, (int64_t)N, s->kr,
-                                 (const char *)a->q, a->q_stride[0], a->q_stride[1], a->q_stride[2], hq, hkv, Q,
+      int row0 = 0;
+      for (int pass = 0; pass < passes; ++pass) {
+        const int Qp = std::min(Qb, Q - pass * Qb);
+        const int rows_p = B * hq * Qp;
+        const char *qp = (const char *)a->q + pass * qstep;
+        s->prof_begin(KIV_STAGE_COARSE_SCAN, st);
+        if (mfma) {
+          const int pages_per_block = (kScanThreads / 64) * kScanMfmaPages;
+          const int blocks = (int)(((int64_t)N + pages_per_block - 1) / pages_per_block);
+          rc = with_dt(dt, [&](auto dtc) {
+            constexpr int DTV = decltype(dtc)::value;
+            if constexpr (DTV == DT_F32) {
+              return (int)KIV_ERR_UNSUPPORTED;
+            } else {
+              return with_kt(kt, [&](auto ktc) {
+                hipLaunchKernelGGL((coarse_scan_mfma_kernel<DTV, decltype(ktc)::value>), dim3(blocks, s->kr),
+                                   dim3(kScanThreads), 0, st, (const char *)s->summ.ptr, (int64_t)N, s->kr, qp,
+                                   a->q_stride[0], a->q_stride[1], a->q_stride[2], hq, hkv, Qp, a->scaling, round,
+                                   (uint32_t *)s->coarse_keys.ptr, ld);
+                return (int)KIV_OK;
+              });
+            }
+          });
+        } else {
+          // Pages per block: 64 per page group, 4 / segments page groups.
+          const int segs = scan_segments(cpr);
+          const int pages_per_block = (kScanThreads / 64 / segs) * 64;
+          const int blocks = (int)(((int64_t)N + pages_per_block - 1) / pages_per_block);
+          rc = with_dt(dt, [&](auto dtc) {
+            return with_cpr(cpr, [&](auto cc) {
+              constexpr int DTV = decltype(dtc)::value, CPRV = decltype(cc)::value;
+              auto kern = Qp == 1 ? coarse_scan_kernel<DTV, CPRV, true> : coarse_scan_kernel<DTV, CPRV, false>;
+              hipLaunchKernelGGL(kern, dim3(blocks, s->kr), dim3(kScanThreads), 0, st, (const char *)s->summ.ptr,
+                                 (int64_t)N, s->kr, qp, a->q_stride[0], a->q_stride[1], a->q_stride[2], hq, hkv, Qp,
                                  a->scaling, round, (uint32_t *)s->coarse_keys.ptr, ld);
               return (int)KIV_OK;
             });
-          }
-        });
-      } else {
-        // Pages per block: 64 per page group, 4 / segments page groups.
-        const int segs = scan_segments(cpr);
-        const int pages_per_block = (kScanThreads / 64 / segs) * 64;
-        const int blocks = (int)(((int64_t)N + pages_per_block - 1) / pages_per_block);
-        rc = with_dt(dt, [&](auto dtc) {
-          return with_cpr(cpr, [&](auto cc) {
-            constexpr int DTV = decltype(dtc)::value, CPRV = decltype(cc)::value;
-            auto kern = Q == 1 ? coarse_scan_kernel<DTV, CPRV, true> : coarse_scan_kernel<DTV, CPRV, false>;
-            hipLaunchKernelGGL(kern, dim3(blocks, s->kr), dim3(kScanThreads), 0, st, (const char *)s->summ.ptr,
-                               (int64_t)N, s->kr, (const char *)a->q, a->q_stride[0], a->q_stride[1],
-                               a->q_stride[2], hq, hkv, Q, a->scaling, round, (uint32_t *)s->coarse_keys.ptr, ld);
-            return (int)KIV_OK;
           });
-        });
+        }
+        s->prof_end(KIV_STAGE_COARSE_SCAN, st);
+        if (rc) return rc;
+        KIV_HIP(hipGetLastError());
+        s->prof_begin(KIV_STAGE_COARSE_SELECT, st);
+        with_select_chunks(N, [&](auto kern) {
+          hipLaunchKernelGGL(kern, dim3(rows_p), dim3(kSelThreads), 0, st, (const uint32_t *)s->coarse_keys.ptr,
+                             ld, N, kc, (int32_t *)s->row_pages.ptr + (int64_t)row0 * kc, coarse_stats + 2 * row0);
+        }, [](auto vc) { return coarse_select_kernel<kSelThreads, decltype(vc)::value>; });
+        s->prof_end(KIV_STAGE_COARSE_SELECT, st);
+        KIV_HIP(hipGetLastError());
+        row0 += rows_p;
       }
-      s->prof_end(KIV_STAGE_COARSE_SCAN, st);
-      if (rc) return rc;
-      KIV_HIP(hipGetLastError());
-      s->prof_begin(KIV_STAGE_COARSE_SELECT, st);
-      with_select_chunks(N, [&](auto kern) {
-        hipLaunchKernelGGL(kern, dim3(rows), dim3(kSelThreads), 0, st, (const uint32_t *)s->coarse_keys.ptr, ld, N,
-                           kc, (int32_t *)s->row_pages.ptr, coarse_stats);
-      }, [](auto vc) { return coarse_select_kernel<kSelThreads, decltype(vc)::value>; });
-      s->prof_end(KIV_STAGE_COARSE_SELECT, st);
-      KIV_HIP(hipGetLastError());
+      if (union_src == UNION_LIST) {
+        // The union of every row list: marks in a page bitmap, then one
+        // block ranks it into the union list, publishes U and the coarse
+        // telemetry, and clears the bitmap.
+        if (s->union_bits.bytes < (size_t)words * 4) {
+          if ((rc = s->union_bits.ensure((size_t)words * 4, st, false))) return rc;
+          KIV_HIP(hipMemsetAsync(s->union_bits.ptr, 0, s->union_bits.bytes, st));
+        }
+        const int64_t n_marks = (int64_t)rows * kc;
+        const unsigned mark_blocks = (unsigned)std::min<int64_t>(1024, (n_marks + 255) / 256);
+        hipLaunchKernelGGL(union_mark_kernel, dim3(mark_blocks), dim3(256), 0, st, (const int32_t *)s->row_pages.ptr,
+                           n_marks, (uint32_t *)s->union_bits.ptr);
+        KIV_HIP(hipGetLastError());
+        rc = with_dt(dt, [&](auto dtc) {
+          hipLaunchKernelGGL((union_list_kernel<decltype(dtc)::value>), dim3(1), dim3(kUnionThreads), 0, st,
+                             (uint32_t *)s->union_bits.ptr, words, (int32_t *)s->page_list.ptr,
+                             (int32_t *)s->counters.ptr, a->pages_out, a->union_count_out,
+                             (const float *)coarse_stats, rows, N, round, a->stats_out, a->stats_accum);
+          return (int)KIV_OK;
+        });
+        if (rc) return rc;
+        KIV_HIP(hipGetLastError());
+      }
       s->union_valid = true;
       s->union_rows = rows;
       s->union_max = umax;
@@ -1216,23 +1332,28 @@ static int retrieve_impl(kiv_store_t *s, const kiv_retrieve_args_t *a, hipStream
     const int64_t max_items = umax * nsplit + (s->partial_len + tpi - 1) / tpi;
     const int64_t want = host_tier ? 1024 : 2048;
     const int64_t nb = std::max<int64_t>(1, std::min<int64_t>(max_items, (want + s->kr - 1) / s->kr));
-    const int G = hq / hkv;
-    const size_t lds = (size_t)G * Q * D * eb + (size_t)bwords * 4 + (size_t)(bwords + 1) * 4;
-    s->prof_begin(KIV_STAGE_FINE_SCAN, st);
-    rc = with_dt_lg(dt, lg, [&](auto dtc, auto lgc) {
-      hipLaunchKernelGGL((fine_scan_kernel<decltype(dtc)::value, decltype(lgc)::value>),
-                         dim3((unsigned)nb, (unsigned)s->kr), dim3(256), lds, st, union_src,
-                         (const int32_t *)s->row_pages.ptr, rows * kc, bwords, (int32_t *)s->page_list.ptr,
-                         (int32_t *)s->counters.ptr, (const uint64_t *)s->k_tab.ptr, s->chunk_shift, s->page_bytes,
-                         (const char *)s->k_part.ptr, (int)s->partial_len, ps, tpi, hkv, D, (const char *)a->q,
-                         a->q_stride[0], a->q_stride[1], a->q_stride[2], hq, Q, a->scaling, round,
-                         (uint32_t *)s->fine_keys.ptr, ldc, (const float *)coarse_stats, rows, N, a->pages_out,
-                         a->union_count_out, a->stats_out, a->stats_accum, k_stage);
-      return (int)KIV_OK;
-    });
-    s->prof_end(KIV_STAGE_FINE_SCAN, st);
-    if (rc) return rc;
-    KIV_HIP(hipGetLastError());
+    for (int pass = 0; pass < passes; ++pass) {
+      const int Qp = std::min(Qb, Q - pass * Qb);
+      const size_t lds = (size_t)G * Qp * D * eb + (size_t)bwords * 4 + (size_t)(bwords + 1) * 4;
+      s->prof_begin(KIV_STAGE_FINE_SCAN, st);
+      rc = with_dt_lg(dt, lg, [&](auto dtc, auto lgc) {
+        auto kern = fine_scan_kernel<decltype(dtc)::value, decltype(lgc)::value>;
+        if (lds > 65536)
+          KIV_HIP(hipFuncSetAttribute((const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
+        hipLaunchKernelGGL(kern, dim3((unsigned)nb, (unsigned)s->kr), dim3(256), lds, st, union_src,
+                           (const int32_t *)s->row_pages.ptr, rows * kc, bwords, (int32_t *)s->page_list.ptr,
+                           (int32_t *)s->counters.ptr, (const uint64_t *)s->k_tab.ptr, s->chunk_shift,
+                           s->page_bytes, (const char *)s->k_part.ptr, (int)s->partial_len, ps, tpi, hkv, D,
+                           (const char *)a->q + pass * qstep, a->q_stride[0], a->q_stride[1], a->q_stride[2], hq,
+                           Qp, a->scaling, round, (uint32_t *)s->fine_keys.ptr, ldc, (const float *)coarse_stats,
+                           rows, N, a->pages_out, a->union_count_out, a->stats_out, a->stats_accum,
+                           pass == 0 ? k_stage : nullptr);
+        return (int)KIV_OK;
+      });
+      s->prof_end(KIV_STAGE_FINE_SCAN, st);
+      if (rc) return rc;
+      KIV_HIP(hipGetLastError());
+    }
   }
   {
     s->prof_begin(KIV_STAGE_FINE_SELECT, st);

@@ -311,7 +311,7 @@ int64_t kiv_store::reserved_host_bytes() const {
 int64_t kiv_store::reserved_device_bytes() const {
   int64_t d = (int64_t)(summ.bytes + summ32.bytes + k_tab.bytes + v_tab.bytes + k_part.bytes +
                         v_part.bytes + coarse_keys.bytes + row_stats.bytes + row_pages.bytes +
-                        page_list.bytes + counters.bytes + fine_keys.bytes + sel_list.bytes + k_stage.bytes);
+                        page_list.bytes + union_bits.bytes + counters.bytes + fine_keys.bytes + sel_list.bytes + k_stage.bytes);
   if (cfg.cold_tier == KIV_TIER_HBM)
     d += (int64_t)(k_chunks.size() + v_chunks.size()) * pages_per_chunk * page_bytes;
   return d;
@@ -392,7 +392,7 @@ int kiv_store_destroy(kiv_store_t *s) {
   for (void *p : s->v_chunks) (void)(host ? hipHostFree(p) : hipFree(p));
   for (hipEvent_t e : s->prof_ev) (void)hipEventDestroy(e);
   DevBuf *bufs[] = {&s->summ, &s->summ32, &s->k_tab, &s->v_tab, &s->k_part, &s->v_part,
-                    &s->coarse_keys, &s->row_stats, &s->row_pages, &s->page_list, &s->counters,
+                    &s->coarse_keys, &s->row_stats, &s->row_pages, &s->page_list, &s->union_bits, &s->counters,
                     &s->fine_keys, &s->sel_list, &s->k_stage};
   for (DevBuf *b : bufs) b->release();
   delete s;

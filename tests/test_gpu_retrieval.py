@@ -440,3 +440,29 @@ def test_retrieve_attend(cuda, name, over, mask_kind):
     assert out.shape == (1, 1, w.num_q_heads, w.head_dim) and out.dtype == w.dtype
     k_out, v_out, _ = check_retrieval(store, oracle, cfg, w, data, data["q"])
     attention_check(q, k_out, v_out, hk, hv, w.scaling, mask, out=out)
+
+
+LONG_QUERIES = [
+    # name, workload, batch, positions: long queries run the scans in passes
+    # of query positions and build the union with the union kernels
+    ("qwen_shape_two_passes", Workload("lq1", 28, 4, 128, torch.bfloat16, hot=64, cold=9000 + 21, top_pages=8,
+                                       top_p=256, segment=1024), 1, 40),
+    ("mha_long_row_list", Workload("lq2", 32, 32, 64, torch.float16, hot=64, cold=6000, top_pages=32, top_p=300,
+                                   segment=512, n_targets=4), 1, 16),
+    ("fp32_many_passes", Workload("lq3", 4, 2, 64, torch.float32, hot=16, cold=3000 + 5, top_pages=4, top_p=128,
+                                  segment=256), 2, 200),
+]
+
+
+@pytest.mark.parametrize("name,w,batch,positions", LONG_QUERIES, ids=[c[0] for c in LONG_QUERIES])
+def test_long_query_retrieval(cuda, name, w, batch, positions):
+    """Queries with many positions (a prefill chunk with live retrieval, as
+    the reference's reuse-path prefill runs it): the union over every
+    (batch, head, position) and the fine max over heads and positions must
+    meet the same bar as decode."""
+    data = generate(w, seed=41, batch=batch)
+    g = torch.Generator().manual_seed(42)
+    q = data["q"].float().repeat(1, 1, positions, 1)
+    q = (q + 0.2 * torch.randn(q.shape, generator=g)).to(w.dtype)
+    store, oracle, cfg = build(w, data, cuda)
+    check_retrieval(store, oracle, cfg, w, data, q)
