@@ -74,7 +74,7 @@ def test_hip_retrieval_matches_reference(cuda, case, data):
         assert torch.equal(k_out[b].cpu(), t["k"][b][:, idx]) and torch.equal(v_out[b].cpu(), t["v"][b][:, idx])
 
 
-def test_tiny_qwen2_end_to_end_matches_reference(cuda):
+def tiny_qwen2(cuda):
     from safetensors.torch import load_file
     from transformers import Qwen2Config, Qwen2ForCausalLM
 
@@ -87,6 +87,11 @@ def test_tiny_qwen2_end_to_end_matches_reference(cuda):
     model = Qwen2ForCausalLM(cfg).eval()
     model.load_state_dict(load_file(os.path.join(HERE, "tiny_qwen2.safetensors")))
     model.to(cuda)
+    return model, meta, gold
+
+
+def test_tiny_qwen2_end_to_end_matches_reference(cuda):
+    model, meta, gold = tiny_qwen2(cuda)
     mw = KIVMiddleware(model, KIVConfig(**meta["kiv"]))
     mw.install()
     try:
@@ -107,3 +112,31 @@ def test_tiny_qwen2_end_to_end_matches_reference(cuda):
     err = np.abs(got - ref).max()
     assert err <= 1e-3, f"max abs logit difference {err}"
     assert np.array_equal(got.argmax(-1)[:-1], gold["tokens"])
+
+
+def test_tiny_qwen2_multi_token_forward_with_cold_tier(cuda):
+    """After prefill and decode, a 400-token forward on the same cache (a
+    follow-up prompt, as the reference's reuse-path prefill runs it) takes
+    the retrieval with 400 query positions (more than one pass of the scans)
+    and the model's own attention over [retrieved ; hot], and must give
+    finite logits for every position."""
+    model, meta, gold = tiny_qwen2(cuda)
+    mw = KIVMiddleware(model, KIVConfig(**meta["kiv"]))
+    mw.install()
+    try:
+        cache = mw.create_cache(cuda)
+        ids = torch.from_numpy(gold["input_ids"]).to(cuda)
+        with torch.no_grad():
+            mw.chunked_prefill(ids, cache, chunk_size=meta["prefill"]["chunk_size"])
+            for tok in gold["tokens"].tolist()[:3]:
+                model(input_ids=torch.tensor([[tok]], device=cuda), past_key_values=cache, use_cache=True)
+            store = cache.get_cold_store(0)
+            assert store.cold_length > 0
+            before = len(store.telemetry_snapshot()["recent"])
+            follow = torch.randint(0, model.config.vocab_size, (1, 400), generator=torch.Generator().manual_seed(3))
+            out = model(input_ids=follow.to(cuda), past_key_values=cache, use_cache=True)
+        assert out.logits.shape[:2] == (1, 400)
+        assert torch.isfinite(out.logits).all()
+        assert len(store.telemetry_snapshot()["recent"]) > before  # the forward retrieved from the cold tier
+    finally:
+        mw.uninstall()
