@@ -59,8 +59,8 @@ def parse():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--workload", default="qwen7b_1m")
-    ap.add_argument("--cold-tier", default="host", choices=("host", "hbm"))
-    ap.add_argument("--no-variant", action="store_true", help="skip the other cold tier")
+    ap.add_argument("--cold-tier", default="host", choices=("host", "hbm", "split"))
+    ap.add_argument("--no-variant", action="store_true", help="skip the other cold tiers")
     ap.add_argument("--cpu-seconds", type=float, default=15.0, help="CPU baseline sample budget")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--seed", type=int, default=0)
@@ -135,7 +135,24 @@ def one_step(store, cfg, q, hot_k, hot_v, i, scaling, attn_events=None, fused=Tr
 
 
 def time_steps(store, cfg, q, hot_k, hot_v, steps, warmup, scaling, scrub, fused=True):
-    """Mean µs per step: back-to-back (scrub None) or each step timed alone after a scrub."""
+    """Mean µs per step: back-to-back (scrub None) or each step timed alone after a scrub.
+
+    Python's cyclic garbage collector is paused while the steps are enqueued:
+    a collection pass stalls the launching thread for milliseconds, which
+    the GPU events would count as idle time inside a step."""
+    import gc
+
+    import torch
+
+    gc.collect()
+    gc.disable()
+    try:
+        return _time_steps(store, cfg, q, hot_k, hot_v, steps, warmup, scaling, scrub, fused)
+    finally:
+        gc.enable()
+
+
+def _time_steps(store, cfg, q, hot_k, hot_v, steps, warmup, scaling, scrub, fused):
     import torch
 
     for i in range(warmup):
@@ -230,13 +247,14 @@ def roofline_and_links(w, store, stages, union_pages, tier):
         # (bytes per launch, memory it streams from)
         "coarse_scan": (N * row, "hbm"),
         "coarse_select": (rows * N * 4, "hbm"),
-        "fine_scan": (union_pages * w.page_size * row, tier),
+        "fine_scan": (union_pages * w.page_size * row, "host" if tier == "host" else "hbm"),
         "fine_select": (cand * 4, "hbm"),
-        # Host tier: K of the selected rows comes from the fine scan's HBM
-        # staging, so only V crosses the host link.  (The fused step's gather
-        # launch also runs the hot-window attention splits, which read the
-        # hot K/V from HBM; they are not host-link bytes.)
-        "gather": ((1 if tier == "host" else 2) * P * row, tier),
+        # Host and split tiers: only V of the selected rows crosses the host
+        # link (the host tier takes K from the fine scan's HBM staging, the
+        # split tier keeps K in HBM).  The fused step's gather launch also
+        # runs the hot-window attention splits, which read the hot K/V from
+        # HBM; they are not host-link bytes.
+        "gather": ((2 if tier == "hbm" else 1) * P * row, "hbm" if tier == "hbm" else "host"),
         "attend": (2 * P * row, "hbm"),
         "attention": (2 * (P + w.hot) * row, "hbm"),
     }
@@ -491,7 +509,8 @@ def main():
         return
     extra = 3 * (args.steps + args.warmup) + 1024
     results = {}
-    tiers = [args.cold_tier] + ([] if args.no_variant else [t for t in ("host", "hbm") if t != args.cold_tier])
+    tiers = [args.cold_tier] + ([] if args.no_variant else [t for t in ("host", "hbm", "split")
+                                                             if t != args.cold_tier])
     for tier in tiers:
         cfg = KIVConfig(hot_budget=w.hot, top_p=w.top_p, page_size=w.page_size, top_pages=w.top_pages,
                         cold_tier=tier, reserve_tokens=w.cold + extra)

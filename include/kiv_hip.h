@@ -42,7 +42,10 @@ enum {
 };
 
 enum { KIV_DTYPE_F32 = 0, KIV_DTYPE_F16 = 1, KIV_DTYPE_BF16 = 2 };
-enum { KIV_TIER_HOST = 0, KIV_TIER_HBM = 1 };
+/* Placement of finished pages' rows: both in pinned mapped host memory, both in
+ * HBM, or K in HBM and V in host memory (the fine scan reads K of every union
+ * page; only the selected rows' V crosses the host link). */
+enum { KIV_TIER_HOST = 0, KIV_TIER_HBM = 1, KIV_TIER_SPLIT = 2 };
 enum { KIV_ROUND_ACTIVATION = 0, KIV_ROUND_FP32 = 1 };
 enum { KIV_MASK_NONE = 0, KIV_MASK_BOOL = 1, KIV_MASK_F32 = 2, KIV_MASK_F16 = 3, KIV_MASK_BF16 = 4 };
 

@@ -19,7 +19,7 @@ LIB_PATH = Path(os.environ.get("KIV_LIB_PATH") or Path(__file__).resolve().paren
 
 KIV_OK = 0
 DTYPE_F32, DTYPE_F16, DTYPE_BF16 = 0, 1, 2
-TIER_HOST, TIER_HBM = 0, 1
+TIER_HOST, TIER_HBM, TIER_SPLIT = 0, 1, 2
 ROUND_ACTIVATION, ROUND_FP32 = 0, 1
 MASK_NONE, MASK_BOOL, MASK_F32, MASK_F16, MASK_BF16 = 0, 1, 2, 3, 4
 STAGES = ("evict_append", "evict_finalize", "coarse_scan", "coarse_select", "fine_scan", "fine_select",

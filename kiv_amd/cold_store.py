@@ -6,7 +6,8 @@ constructor, ``evict_from_hot`` / ``retrieve_top_kv`` / ``cold_length`` /
 ``memory_bytes`` and the ``_cached_candidate_*`` / ``_cached_step``
 attributes other code clears.  The state lives in a native store
 (include/kiv_hip.h): page summaries and the partial page in HBM, finished
-pages' K/V rows in pinned mapped host memory (or HBM, ``cold_tier="hbm"``).
+pages' K/V rows in pinned mapped host memory (or HBM, ``cold_tier="hbm"``;
+or K in HBM and V in host memory, ``cold_tier="split"``).
 
 Every device call is enqueued on torch's current stream; retrieval does not
 synchronise the host except when the output width depends on the union size
@@ -87,7 +88,7 @@ class ColdKVStore:
             head_dim=self._head_dim,
             page_size=self._page_size,
             dtype=nat.dtype_code(k.dtype),
-            cold_tier=nat.TIER_HOST if self.kiv_config.cold_tier == "host" else nat.TIER_HBM,
+            cold_tier={"host": nat.TIER_HOST, "hbm": nat.TIER_HBM, "split": nat.TIER_SPLIT}[self.kiv_config.cold_tier],
             score_rounding=(nat.ROUND_ACTIVATION if self.kiv_config.score_rounding == "activation"
                             else nat.ROUND_FP32),
             reserve_tokens=int(self.kiv_config.reserve_tokens),
@@ -282,10 +283,9 @@ class ColdKVStore:
             return out
         info = nat.StoreInfo()
         nat.check(nat.lib().kiv_store_info(self._handle, C.byref(info)), "kiv_store_info")
-        if self.kiv_config.cold_tier == "host":
-            out["k_index_cpu"], out["v_store_cpu"] = info.k_cold_bytes, info.v_cold_bytes
-        else:
-            out["k_cold_gpu"], out["v_cold_gpu"] = info.k_cold_bytes, info.v_cold_bytes
+        tier = self.kiv_config.cold_tier
+        out["k_index_cpu" if tier == "host" else "k_cold_gpu"] = info.k_cold_bytes
+        out["v_cold_gpu" if tier == "hbm" else "v_store_cpu"] = info.v_cold_bytes
         out["page_summaries_gpu"] = info.summary_bytes
         out["partial_gpu"] = info.partial_bytes
         return out

@@ -23,7 +23,9 @@ class KIVConfig:
                      rows in-kernel, so there is no separate copy stream.
     cold_tier        where evicted K/V rows live: "host" (pinned, mapped host
                      memory read zero-copy by the kernels, the reference's
-                     placement) or "hbm" (device memory).
+                     placement), "hbm" (device memory) or "split" (K rows in
+                     HBM, where the fine scan reads every union page; V rows
+                     in host memory, of which only the selected rows are read).
     score_rounding   "activation": round scores to the activation dtype after
                      the dot product and again after scaling, as the
                      reference's dtype matmul does (kiv/cold_store.py:206-208);
@@ -42,8 +44,8 @@ class KIVConfig:
     reserve_tokens: int = 0
 
     def __post_init__(self) -> None:
-        if self.cold_tier not in ("host", "hbm"):
-            raise ValueError(f"cold_tier must be 'host' or 'hbm', got {self.cold_tier!r}")
+        if self.cold_tier not in ("host", "hbm", "split"):
+            raise ValueError(f"cold_tier must be 'host', 'hbm' or 'split', got {self.cold_tier!r}")
         if self.score_rounding not in ("activation", "fp32"):
             raise ValueError(
                 f"score_rounding must be 'activation' or 'fp32', got {self.score_rounding!r}"

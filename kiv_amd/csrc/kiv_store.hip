@@ -237,7 +237,8 @@ static int ensure_arena(kiv_store *s, int64_t pages, hipStream_t st) {
   int rc = grow_tables(s, need, st);
   if (rc) return rc;
   const size_t chunk_bytes = (size_t)(s->pages_per_chunk * s->page_bytes);
-  const bool host = s->cfg.cold_tier == KIV_TIER_HOST;
+  const bool k_host = s->cfg.cold_tier == KIV_TIER_HOST;
+  const bool v_host = s->cfg.cold_tier != KIV_TIER_HBM;
   while ((int64_t)s->k_chunks.size() < need) {
     const int64_t first = (int64_t)s->k_chunks.size();
     TabEntries e{};
@@ -245,20 +246,16 @@ static int ensure_arena(kiv_store *s, int64_t pages, hipStream_t st) {
     while (n < 8 && first + n < need) {
       void *kp = nullptr, *vp = nullptr;
       hipError_t err;
-      if (host) {
-        err = hipHostMalloc(&kp, chunk_bytes, hipHostMallocMapped);
-        if (err == hipSuccess) err = hipHostMalloc(&vp, chunk_bytes, hipHostMallocMapped);
-      } else {
-        err = hipMalloc(&kp, chunk_bytes);
-        if (err == hipSuccess) err = hipMalloc(&vp, chunk_bytes);
-      }
+      err = k_host ? hipHostMalloc(&kp, chunk_bytes, hipHostMallocMapped) : hipMalloc(&kp, chunk_bytes);
+      if (err == hipSuccess)
+        err = v_host ? hipHostMalloc(&vp, chunk_bytes, hipHostMallocMapped) : hipMalloc(&vp, chunk_bytes);
       if (err != hipSuccess) {
-        if (kp) (void)(host ? hipHostFree(kp) : hipFree(kp));
-        return hip_fail(err, host ? "hipHostMalloc(cold arena)" : "hipMalloc(cold arena)");
+        if (kp) (void)(k_host ? hipHostFree(kp) : hipFree(kp));
+        return hip_fail(err, "allocation of the cold arena");
       }
       void *kd = kp, *vd = vp;
-      if (host) {
-        KIV_HIP(hipHostGetDevicePointer(&kd, kp, 0));
+      if (k_host) KIV_HIP(hipHostGetDevicePointer(&kd, kp, 0));
+      if (v_host) {
         KIV_HIP(hipHostGetDevicePointer(&vd, vp, 0));
       }
       s->k_chunks.push_back(kp);
@@ -304,16 +301,18 @@ void kiv_store::prof_end(int stage, hipStream_t st) {
 }
 
 int64_t kiv_store::reserved_host_bytes() const {
-  if (cfg.cold_tier != KIV_TIER_HOST) return 0;
-  return (int64_t)(k_chunks.size() + v_chunks.size()) * pages_per_chunk * page_bytes;
+  const int64_t chunk = pages_per_chunk * page_bytes;
+  return (cfg.cold_tier == KIV_TIER_HOST ? (int64_t)k_chunks.size() * chunk : 0) +
+         (cfg.cold_tier != KIV_TIER_HBM ? (int64_t)v_chunks.size() * chunk : 0);
 }
 
 int64_t kiv_store::reserved_device_bytes() const {
   int64_t d = (int64_t)(summ.bytes + summ32.bytes + k_tab.bytes + v_tab.bytes + k_part.bytes +
                         v_part.bytes + coarse_keys.bytes + row_stats.bytes + row_pages.bytes +
                         page_list.bytes + union_bits.bytes + counters.bytes + fine_keys.bytes + sel_list.bytes + k_stage.bytes);
-  if (cfg.cold_tier == KIV_TIER_HBM)
-    d += (int64_t)(k_chunks.size() + v_chunks.size()) * pages_per_chunk * page_bytes;
+  const int64_t chunk = pages_per_chunk * page_bytes;
+  if (cfg.cold_tier != KIV_TIER_HOST) d += (int64_t)k_chunks.size() * chunk;
+  if (cfg.cold_tier == KIV_TIER_HBM) d += (int64_t)v_chunks.size() * chunk;
   return d;
 }
 
@@ -341,7 +340,7 @@ int kiv_store_create(const kiv_store_config_t *cfg, int device, kiv_store_t **ou
                 "kiv_store_create: head_dim %d unsupported for this dtype (head_dim / %d must be one of "
                 "2 4 6 8 10 12 14 16 20 24 28 32 40 48 64)",
                 c.head_dim, vec);
-  if (c.cold_tier != KIV_TIER_HOST && c.cold_tier != KIV_TIER_HBM)
+  if (c.cold_tier != KIV_TIER_HOST && c.cold_tier != KIV_TIER_HBM && c.cold_tier != KIV_TIER_SPLIT)
     return fail(KIV_ERR_INVALID, "kiv_store_create: unknown cold_tier %d", c.cold_tier);
   if (c.score_rounding != KIV_ROUND_ACTIVATION && c.score_rounding != KIV_ROUND_FP32)
     return fail(KIV_ERR_INVALID, "kiv_store_create: unknown score_rounding %d", c.score_rounding);
@@ -387,9 +386,9 @@ int kiv_store_destroy(kiv_store_t *s) {
   if (!s) return KIV_OK;
   DeviceGuard guard(s->device);
   (void)hipDeviceSynchronize();
-  const bool host = s->cfg.cold_tier == KIV_TIER_HOST;
-  for (void *p : s->k_chunks) (void)(host ? hipHostFree(p) : hipFree(p));
-  for (void *p : s->v_chunks) (void)(host ? hipHostFree(p) : hipFree(p));
+  const bool k_host = s->cfg.cold_tier == KIV_TIER_HOST, v_host = s->cfg.cold_tier != KIV_TIER_HBM;
+  for (void *p : s->k_chunks) (void)(k_host ? hipHostFree(p) : hipFree(p));
+  for (void *p : s->v_chunks) (void)(v_host ? hipHostFree(p) : hipFree(p));
   for (hipEvent_t e : s->prof_ev) (void)hipEventDestroy(e);
   DevBuf *bufs[] = {&s->summ, &s->summ32, &s->k_tab, &s->v_tab, &s->k_part, &s->v_part,
                     &s->coarse_keys, &s->row_stats, &s->row_pages, &s->page_list, &s->union_bits, &s->counters,

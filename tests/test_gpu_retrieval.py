@@ -250,6 +250,25 @@ def test_fp32_scores_and_hbm_tier(cuda):
     assert mem["k_index_cpu"] == 0 and mem["k_cold_gpu"] == store.num_pages * 128 * 2 * 128 * 2
 
 
+@pytest.mark.parametrize("attend", [False, True])
+def test_split_tier(cuda, attend):
+    """K rows of finished pages in HBM, V rows in pinned host memory: the
+    same selection and rows, alone and through the fused attention call."""
+    w = Workload("split", 28, 4, 128, torch.bfloat16, hot=128, cold=9000 + 3, top_pages=8, top_p=256, segment=1024)
+    data = generate(w, seed=7)
+    store, oracle, cfg = build(w, data, cuda, chunks=(1000, 1), cold_tier="split")
+    check_rows(store, data)
+    q, hk, hv = data["q"].to(cuda), data["hot_k"].to(cuda), data["hot_v"].to(cuda)
+    out = store.retrieve_attend(q, w.scaling, cfg, hk, hv, None) if attend else None
+    k_out, v_out, _ = check_retrieval(store, oracle, cfg, w, data, data["q"])
+    if attend:
+        attention_check(q, k_out, v_out, hk, hv, w.scaling, None, out=out)
+    mem = store.memory_bytes()
+    row = store.num_pages * 128 * 4 * 128 * 2
+    assert mem["k_cold_gpu"] == row and mem["v_store_cpu"] == row
+    assert mem["k_index_cpu"] == 0 and mem["v_cold_gpu"] == 0
+
+
 def test_width_depends_on_union(cuda):
     """top_p > top_pages * page_size: the width follows the union size."""
     w = Workload("wide", 4, 1, 64, torch.bfloat16, hot=8, cold=64 * 10, top_pages=2, top_p=300, segment=64,
