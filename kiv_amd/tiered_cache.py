@@ -6,6 +6,13 @@ still a ``transformers.DynamicCache`` so HF layers and callers that read
 ``hot_budget`` recent tokens after prefill; older rows go to the layer's
 :class:`ColdKVStore`.  Positions (``get_seq_length``) and mask sizes count
 hot + cold tokens.
+
+The hot window of an owned layer lives in a preallocated buffer with slack
+(:class:`_HotLayer`): a decode step writes its one new row in place and an
+eviction moves the window's start, where DynamicLayer's ``torch.cat`` and
+the reference's slice-and-``.contiguous()`` eviction each copy the whole
+window (kiv/tiered_cache.py:55-72).  ``layers[i].keys`` is then a view of
+the buffer ([B, H, T, D], unit stride over D).
 """
 
 from __future__ import annotations
@@ -14,12 +21,78 @@ import logging
 
 import torch
 from transformers import DynamicCache
+from transformers.cache_utils import DynamicLayer
 
 from .cold_store import ColdKVStore
 from .config import KIVConfig
 from .model_topology import ModelTopology
 
 logger = logging.getLogger(__name__)
+
+
+class _HotLayer(DynamicLayer):
+    """A DynamicLayer whose rows [start, end) live in [B, H, cap, D] buffers.
+
+    ``update`` copies only the new rows (at ``end``); ``drop_front`` evicts by
+    advancing ``start``.  When an append would run past ``cap``, the window
+    moves to a fresh buffer with ``slack`` free rows (one copy per ``slack``
+    appended rows in decode).  Any other code that replaces ``keys`` /
+    ``values`` (crop, batch selection, truncation) is picked up at the next
+    update, which copies the replacement into a new buffer.
+    """
+
+    slack = 256
+
+    def __init__(self) -> None:
+        super().__init__()
+        self._kb = self._vb = None
+        self._start = self._end = 0
+        self._view = None
+
+    def _window(self) -> None:
+        self.keys = self._kb[:, :, self._start:self._end]
+        self.values = self._vb[:, :, self._start:self._end]
+        self._view = self.keys
+
+    def _move(self, k: torch.Tensor, v: torch.Tensor, extra: int) -> None:
+        """New buffers holding k / v at the front, with room for ``extra`` more rows."""
+        B, H, T, D = k.shape
+        cap = T + extra + self.slack
+        kb = torch.empty(B, H, cap, D, dtype=k.dtype, device=k.device)
+        vb = torch.empty(B, H, cap, v.shape[3], dtype=v.dtype, device=v.device)
+        if T:
+            kb[:, :, :T].copy_(k)
+            vb[:, :, :T].copy_(v)
+        self._kb, self._vb, self._start, self._end = kb, vb, 0, T
+
+    def update(self, key_states: torch.Tensor, value_states: torch.Tensor, *args, **kwargs):
+        if not self.is_initialized:
+            self.lazy_initialization(key_states, value_states)
+        n = key_states.shape[-2]
+        if self._kb is None or self.keys is not self._view:
+            # First rows, or keys replaced from outside.
+            k, v = self.keys, self.values
+            if k.numel() == 0:
+                k = key_states[:, :, :0]
+                v = value_states[:, :, :0]
+            self._move(k, v, n)
+        elif (self._end + n > self._kb.shape[2] or key_states.shape[:2] != self._kb.shape[:2]
+              or key_states.dtype != self._kb.dtype):
+            self._move(self.keys, self.values, n)
+        self._kb[:, :, self._end:self._end + n].copy_(key_states)
+        self._vb[:, :, self._end:self._end + n].copy_(value_states)
+        self._end += n
+        self._window()
+        return self.keys, self.values
+
+    def drop_front(self, n: int) -> None:
+        """Forget the oldest ``n`` rows (already copied to the cold tier)."""
+        if self._kb is None or self.keys is not self._view:
+            self.keys = self.keys[:, :, n:]
+            self.values = self.values[:, :, n:]
+            return
+        self._start += n
+        self._window()
 
 
 class TieredKVCache(DynamicCache):
@@ -33,6 +106,10 @@ class TieredKVCache(DynamicCache):
         self.cold_stores: dict[int, ColdKVStore] = {
             i: ColdKVStore(kiv_config, topology, device) for i in topology.independent_kv_layers
         }
+        # Owned full-attention layers keep their hot window in a buffer.
+        for i in topology.independent_kv_layers:
+            if i < len(self.layers) and type(self.layers[i]) is DynamicLayer:
+                self.layers[i] = _HotLayer()
         self._prefill_complete = False   # eviction starts after prefill
         self._suppress_cold = False      # wrapper skips retrieval while set
         self._total_tokens: dict[int, int] = {}
@@ -53,8 +130,11 @@ class TieredKVCache(DynamicCache):
         (kiv/tiered_cache.py:55-72)."""
         layer = self.layers[layer_idx]
         self.cold_stores[layer_idx].evict_from_hot(layer.keys[:, :, :num_evict], layer.values[:, :, :num_evict])
-        layer.keys = layer.keys[:, :, num_evict:].contiguous()
-        layer.values = layer.values[:, :, num_evict:].contiguous()
+        if isinstance(layer, _HotLayer):
+            layer.drop_front(num_evict)
+        else:
+            layer.keys = layer.keys[:, :, num_evict:].contiguous()
+            layer.values = layer.values[:, :, num_evict:].contiguous()
         self._total_tokens[layer_idx] = self.cold_stores[layer_idx].cold_length + layer.keys.shape[2]
 
     def _evict_to_cap(self, cap: int) -> None:

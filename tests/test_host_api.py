@@ -307,3 +307,47 @@ def test_install_registers_and_uninstall_restores():
         mw.uninstall()
         assert model.config._attn_implementation == impl and key not in ALL_ATTENTION_FUNCTIONS
         assert not hasattr(model.model.layers[0].self_attn, "_kiv_cache")
+
+
+def test_hot_layer_appends_in_place_and_evicts_by_moving_the_start():
+    """The buffered hot window (kiv_amd.tiered_cache._HotLayer) behaves as
+    DynamicLayer.update + slice eviction would, copying only new rows."""
+    from kiv_amd.tiered_cache import _HotLayer
+
+    g = torch.Generator().manual_seed(0)
+    rows = lambda n: torch.randn(1, 2, n, 8, generator=g)
+    layer = _HotLayer()
+    k0, v0 = rows(5), rows(5)
+    keys, values = layer.update(k0, v0)
+    ref_k, ref_v = k0.clone(), v0.clone()
+    assert torch.equal(keys, ref_k) and torch.equal(values, ref_v)
+    base = layer._kb.data_ptr()
+    for step in range(300):  # crosses the buffer's slack: one move to a new buffer
+        k1, v1 = rows(1), rows(1)
+        keys, values = layer.update(k1, v1)
+        ref_k, ref_v = torch.cat([ref_k, k1], 2), torch.cat([ref_v, v1], 2)
+        layer.drop_front(1)
+        ref_k, ref_v = ref_k[:, :, 1:], ref_v[:, :, 1:]
+        assert torch.equal(layer.keys, ref_k) and torch.equal(layer.values, ref_v)
+        assert keys.stride(3) == 1 and layer.get_seq_length() == 5
+    assert layer._kb.data_ptr() != base
+    # A replacement from outside (crop, truncation) is adopted at the next update.
+    layer.crop(-2)
+    ref_k, ref_v = ref_k[:, :, :-2], ref_v[:, :, :-2]
+    k2, v2 = rows(4), rows(4)
+    layer.update(k2, v2)
+    assert torch.equal(layer.keys, torch.cat([ref_k, k2], 2)) and torch.equal(layer.values, torch.cat([ref_v, v2], 2))
+
+
+def test_tiered_cache_uses_buffered_hot_layers_for_owned_layers():
+    from transformers import Qwen2Config
+
+    from kiv_amd.tiered_cache import _HotLayer
+
+    cfg = Qwen2Config(hidden_size=64, num_attention_heads=4, num_key_value_heads=2, num_hidden_layers=3,
+                      intermediate_size=128, vocab_size=100)
+    topo = ModelTopology.manual(global_layer_indices=(0, 2), num_query_heads=4, num_kv_heads=2, head_dim=16,
+                                num_hidden_layers=3)
+    cache = TieredKVCache(cfg, KIVConfig(), topo, device="cpu")
+    assert isinstance(cache.layers[0], _HotLayer) and isinstance(cache.layers[2], _HotLayer)
+    assert not isinstance(cache.layers[1], _HotLayer)
