@@ -47,7 +47,11 @@ enum { KIV_DTYPE_F32 = 0, KIV_DTYPE_F16 = 1, KIV_DTYPE_BF16 = 2 };
  * page; only the selected rows' V crosses the host link). */
 enum { KIV_TIER_HOST = 0, KIV_TIER_HBM = 1, KIV_TIER_SPLIT = 2 };
 enum { KIV_ROUND_ACTIVATION = 0, KIV_ROUND_FP32 = 1 };
-enum { KIV_MASK_NONE = 0, KIV_MASK_BOOL = 1, KIV_MASK_F32 = 2, KIV_MASK_F16 = 3, KIV_MASK_BF16 = 4 };
+enum { KIV_MASK_NONE = 0, KIV_MASK_BOOL = 1, KIV_MASK_F32 = 2, KIV_MASK_F16 = 3, KIV_MASK_BF16 = 4,
+       /* No mask tensor: hot column t is visible to query row i iff
+        * t <= i + hot_len - q_len (kiv_prefill_attention; with q_len == 1 it
+        * hides nothing). */
+       KIV_MASK_CAUSAL = 5 };
 
 typedef struct {
   int32_t batch;          /* B */
@@ -222,6 +226,22 @@ int kiv_decode_attention(const kiv_attention_args_t *args, kiv_stream_t stream);
  * call (kiv/cold_store.py:283-371, kiv/middleware.py:330-354). */
 int kiv_retrieve_attend(kiv_store_t *store, const kiv_retrieve_args_t *retrieve, const kiv_attention_args_t *attention,
                         kiv_stream_t stream);
+
+/* Attention of a query of many positions (a prefill chunk, or a long query
+ * over [retrieved ; hot]) on the matrix cores: fp16/bf16, head_dim 32, 64,
+ * 96, 128, 192 or 256.  Same arguments as kiv_decode_attention; the
+ * workspace is needed only with a mask tensor (kiv_prefill_workspace_size
+ * bytes); mask NULL with mask_kind KIV_MASK_CAUSAL applies the causal rule
+ * to the hot columns.  Softmax statistics in fp32; probabilities are rounded
+ * to the dtype before they weight V.  Rows that see no key are zero.
+ * Replaces the original attention call for prefill chunks
+ * (kiv/middleware.py:174-260) and for multi-position queries after the
+ * concatenation (kiv/middleware.py:343-352). */
+int kiv_prefill_attention(const kiv_attention_args_t *args, kiv_stream_t stream);
+
+/* Workspace bytes kiv_prefill_attention needs with a mask tensor (one byte
+ * per 64 x 64 tile of query rows x hot columns, per batch and q head). */
+size_t kiv_prefill_workspace_size(int32_t batch, int32_t num_q_heads, int32_t q_len, int32_t hot_len);
 
 #ifdef __cplusplus
 }

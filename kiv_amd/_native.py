@@ -21,7 +21,7 @@ KIV_OK = 0
 DTYPE_F32, DTYPE_F16, DTYPE_BF16 = 0, 1, 2
 TIER_HOST, TIER_HBM, TIER_SPLIT = 0, 1, 2
 ROUND_ACTIVATION, ROUND_FP32 = 0, 1
-MASK_NONE, MASK_BOOL, MASK_F32, MASK_F16, MASK_BF16 = 0, 1, 2, 3, 4
+MASK_NONE, MASK_BOOL, MASK_F32, MASK_F16, MASK_BF16, MASK_CAUSAL = 0, 1, 2, 3, 4, 5
 STAGES = ("evict_append", "evict_finalize", "coarse_scan", "coarse_select", "fine_scan", "fine_select",
           "gather", "attend")
 
@@ -90,6 +90,8 @@ SIGNATURES = {
     "kiv_attention_workspace_size": (C.c_size_t, [C.c_int32] * 7),
     "kiv_decode_attention": (C.c_int, [C.POINTER(AttentionArgs), C.c_void_p]),
     "kiv_retrieve_attend": (C.c_int, [C.c_void_p, C.POINTER(RetrieveArgs), C.POINTER(AttentionArgs), C.c_void_p]),
+    "kiv_prefill_attention": (C.c_int, [C.POINTER(AttentionArgs), C.c_void_p]),
+    "kiv_prefill_workspace_size": (C.c_size_t, [C.c_int32] * 4),
 }
 
 _lock = threading.Lock()

@@ -1,8 +1,12 @@
-"""Merged decode attention over [retrieved ; hot] (kiv_decode_attention).
+"""Attention over [retrieved ; hot] on the HIP kernels.
 
-The kernels replace the wrapper's two ``torch.cat`` calls, the mask widening
-and the attention call (kiv/middleware.py:330-354): retrieved keys are always
+``decode_attention`` (kiv_decode_attention) replaces the wrapper's two
+``torch.cat`` calls, the mask widening and the attention call
+(kiv/middleware.py:330-354) for decode steps: retrieved keys are always
 attended, an optional mask applies to the hot columns only.
+``prefill_attention`` (kiv_prefill_attention) does the same for queries of
+many positions on the matrix cores: prefill chunks (the original attention
+of kiv/middleware.py:174-260) and long queries with a cold tier.
 """
 
 from __future__ import annotations
@@ -33,10 +37,10 @@ def _workspace(device: torch.device, nbytes: int) -> torch.Tensor:
         return ws
 
 
-def _mask_view(mask: torch.Tensor | None, hot_len: int):
+def _mask_view(mask: torch.Tensor | None, hot_len: int, causal: bool = False):
     """(pointer, kind, strides b,h,q,t) of a 2-D or 4-D mask over hot columns."""
     if mask is None:
-        return None, nat.MASK_NONE, (C.c_int64 * 4)()
+        return None, nat.MASK_CAUSAL if causal else nat.MASK_NONE, (C.c_int64 * 4)()
     if mask.shape[-1] != hot_len:
         raise ValueError(f"mask covers {mask.shape[-1]} columns, hot window has {hot_len}")
     if mask.dim() == 2:
@@ -47,7 +51,7 @@ def _mask_view(mask: torch.Tensor | None, hot_len: int):
 
 
 def _prepare(query: torch.Tensor, cold_len: int, hot_k: torch.Tensor, hot_v: torch.Tensor,
-             mask: torch.Tensor | None, scaling: float):
+             mask: torch.Tensor | None, scaling: float, causal: bool = False, workspace: bool = True):
     """(args without retrieved keys, output, tensors the launches read)."""
     B, hq, Q, D = query.shape
     hkv = hot_k.shape[1]
@@ -61,17 +65,20 @@ def _prepare(query: torch.Tensor, cold_len: int, hot_k: torch.Tensor, hot_v: tor
     q = query if query.stride(3) == 1 else query.contiguous()
     T = hot_k.shape[2]
     lib = nat.lib()
-    need = lib.kiv_attention_workspace_size(B, hq, hkv, D, Q, cold_len, T)
-    ws = _workspace(query.device, need)
+    if workspace:
+        ws = _workspace(query.device, lib.kiv_attention_workspace_size(B, hq, hkv, D, Q, cold_len, T))
+        ws_ptr, ws_bytes = ws.data_ptr(), ws.numel()
+    else:
+        ws_ptr, ws_bytes = None, 0
     out = torch.empty(B, Q, hq, D, dtype=dt, device=query.device)
-    mptr, mkind, mstr = _mask_view(mask, T)
+    mptr, mkind, mstr = _mask_view(mask, T, causal)
     args = nat.AttentionArgs(
         batch=B, num_q_heads=hq, num_kv_heads=hkv, head_dim=D, q_len=Q, dtype=nat.dtype_code(dt),
         q=q.data_ptr(), q_stride=nat.strides(q, 4), cold_k=None, cold_v=None, cold_len=cold_len, hot_len=T,
         hot_k=hot_k.data_ptr(), hot_v=hot_v.data_ptr(),
         hot_k_stride=nat.strides(hot_k, 3), hot_v_stride=nat.strides(hot_v, 3),
         mask=mptr, mask_kind=mkind, mask_stride=mstr, scaling=float(scaling),
-        out=out.data_ptr(), workspace=ws.data_ptr(), workspace_bytes=ws.numel(),
+        out=out.data_ptr(), workspace=ws_ptr, workspace_bytes=ws_bytes,
     )
     keep = (q, hot_k, hot_v) + ((mask,) if mask is not None else ())
     return args, out, keep
@@ -107,6 +114,48 @@ def fused_supported(query: torch.Tensor, hot_k: torch.Tensor, mask: torch.Tensor
     g = hq // hkv
     vec = 4 if query.dtype == torch.float32 else 8
     if g > 64 or g * D > 8192 or D % vec or D // vec > 64:
+        return False
+    if mask is not None and (mask.dim() not in (2, 4) or mask.dtype not in
+                             (torch.bool, torch.float32, torch.float16, torch.bfloat16)):
+        return False
+    return True
+
+
+def prefill_attention(query: torch.Tensor, cold_k: torch.Tensor | None, cold_v: torch.Tensor | None,
+                      hot_k: torch.Tensor, hot_v: torch.Tensor, mask: torch.Tensor | None, scaling: float,
+                      causal: bool = False) -> torch.Tensor:
+    """softmax(q [cold; hot]^T * scaling + [0; mask]) [cold; hot] -> [B, Q, Hq, D]
+    on the matrix cores.  With ``mask=None`` and ``causal`` the hot column t
+    is visible to query row i iff t <= i + hot_len - Q."""
+    P = 0 if cold_k is None else cold_k.shape[2]
+    if mask is not None and mask.dim() == 4:
+        B, hq, Q, _ = query.shape
+        for n, (have, want) in enumerate(zip(mask.shape[:3], (B, hq, Q))):
+            if have not in (1, want):
+                raise ValueError(f"mask dim {n} is {have}, expected 1 or {want}")
+    args, out, _ = _prepare(query, P, hot_k, hot_v, mask, scaling, causal=causal, workspace=False)
+    if mask is not None:
+        B, hq, Q, _ = query.shape
+        need = nat.lib().kiv_prefill_workspace_size(B, hq, Q, hot_k.shape[2])
+        ws = _workspace(query.device, need)
+        args.workspace, args.workspace_bytes = ws.data_ptr(), ws.numel()
+    _set_cold(args, cold_k, cold_v, query.dtype)
+    nat.check(nat.lib().kiv_prefill_attention(C.byref(args), nat.stream_ptr(query.device)),
+              "kiv_prefill_attention")
+    return out
+
+
+_PREFILL_HEAD_DIMS = (32, 64, 96, 128, 192, 256)
+
+
+def prefill_supported(query: torch.Tensor, hot_k: torch.Tensor, mask: torch.Tensor | None) -> bool:
+    """Shapes the matrix-core attention handles: fp16/bf16, head_dim in
+    32/64/96/128/192/256, a 2-D or 4-D mask of a supported dtype (or none)."""
+    if not query.is_cuda or query.dtype not in (torch.float16, torch.bfloat16):
+        return False
+    B, hq, Q, D = query.shape
+    hkv = hot_k.shape[1]
+    if hq % hkv or D not in _PREFILL_HEAD_DIMS or B * hq > 65535:
         return False
     if mask is not None and (mask.dim() not in (2, 4) or mask.dtype not in
                              (torch.bool, torch.float32, torch.float16, torch.bfloat16)):

@@ -21,7 +21,7 @@ PKG = Path(__file__).resolve().parent
 CSRC = PKG / "csrc"
 LIBDIR = PKG / "_lib"
 LIB = LIBDIR / "libkiv_hip.so"
-SOURCES = ("kiv_store.hip", "kiv_retrieve.hip", "kiv_attention.hip", "kiv_probe.hip")
+SOURCES = ("kiv_store.hip", "kiv_retrieve.hip", "kiv_attention.hip", "kiv_prefill.hip", "kiv_probe.hip")
 ARCH = os.environ.get("KIV_OFFLOAD_ARCH", "gfx950")
 
 COMMON = [

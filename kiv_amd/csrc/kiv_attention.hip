@@ -436,6 +436,8 @@ static int attention_check(const kiv_attention_args_t *a, const char *who) {
       return fail(KIV_ERR_INVALID, "%s: hot strides must be multiples of %d", who, vec);
   if (a->mask && (a->mask_kind < KIV_MASK_BOOL || a->mask_kind > KIV_MASK_BF16))
     return fail(KIV_ERR_INVALID, "%s: unknown mask kind %d", who, a->mask_kind);
+  if (!a->mask && a->mask_kind == KIV_MASK_CAUSAL && Q > 1)
+    return fail(KIV_ERR_UNSUPPORTED, "%s: the causal rule needs kiv_prefill_attention for %d query positions", who, Q);
   size_t off_m, off_l, off_acc;
   const size_t need = ws_layout(B, hq, hkv, D, Q, a->cold_len, a->hot_len, &off_m, &off_l, &off_acc);
   if (a->workspace_bytes < need)

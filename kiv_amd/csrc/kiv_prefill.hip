@@ -1,0 +1,483 @@
+// MFMA attention for queries of many positions: prefill chunks and
+// multi-position queries over [retrieved ; hot].
+//
+// Replaces the model's own attention where the reference calls it for a
+// query of many positions: every prefill chunk (kiv/middleware.py:174-260
+// runs the original attention there) and a multi-position query over
+// [retrieved ; hot] (kiv/middleware.py:343-352).  Semantics of the eager
+// reference (third-party modeling_qwen2.py:150-172): scores * scaling +
+// mask, softmax in fp32, probabilities rounded to the activation dtype,
+// then @ V.  Here the probabilities are rounded before the normalisation
+// (flash style), which moves each output by at most the probabilities'
+// own rounding, u * sum_k p_k |v_k|.
+//
+// Grid (ceil(Q / 64), B * Hq), 256 threads; wave w owns query rows
+// q0 + 16 w .. + 15 of one q head.  Keys come in tiles of 64: first the
+// retrieved keys, then the hot keys (a tile never mixes the two, so hot
+// tiles line up with the mask's column tiles).  Per tile:
+//  - K rows ([64][D], rows padded by 16 bytes) and V transposed ([D][64],
+//    rows padded by 8 bytes) go to LDS from registers that were loaded
+//    while the previous tile was being computed;
+//  - S^T = K Q^T with v_mfma_f32_16x16x32: lane l gives row l % 16 of a
+//    16-key sub-tile of K (A) and its own query row l % 16 (B, held in
+//    registers for the whole kernel), dims 32 s + 8 (l / 16) .. + 7 of
+//    step s, and receives keys 4 (l / 16) + i of the sub-tile for its row;
+//  - online softmax in base 2 per query row: the lane's 16 scores, the row
+//    maximum across the four lanes that share the row (l, l ^ 16, l ^ 32,
+//    l ^ 48).  The running maximum is raised, and the accumulators
+//    rescaled, only when a score exceeds it by more than 2^8, so
+//    probabilities stay below 256 and most tiles skip the rescale;
+//  - O^T += V^T P^T with v_mfma_f32_16x16x32 over 32 keys: the B operand is
+//    exactly the lane's probabilities of two sub-tiles (k index 8 g + i is
+//    key 4 g + i of the first sub-tile for i < 4, of the second for i >= 4),
+//    the A operand the same keys of one dim from the V^T tile.  All O^T
+//    entries of a lane belong to its query row.
+// Tile classes: SKIP (no row of the block sees a key of the tile), FULL
+// (every key present and visible with zero bias: no per-element work) and
+// MIXED.  The causal rule and the tile edges give them arithmetically; for
+// a mask tensor a first kernel classifies every (mask row block, column
+// tile) once, so the attention reads mask elements only in MIXED tiles.
+#include "kiv_common.h"
+#include "kiv_dispatch.h"
+#include "kiv_internal.h"
+
+namespace kiv {
+
+constexpr int kPfThreads = 256;
+constexpr int kPfRows = 64;  // query rows per block (16 per wave)
+constexpr int kPfKeys = 64;  // keys per tile
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kRescaleSlack = 8.f;  // base-2 headroom before the running max moves
+enum { TILE_SKIP = 0, TILE_FULL = 1, TILE_MIXED = 2 };
+enum { PF_ARITH = 0, PF_BOOL = 1, PF_FLOAT = 2 };  // how MIXED tiles get their bias
+
+struct PrefillParams {
+  const char *q;
+  int64_t qs0, qs1, qs2;
+  const char *cold_k, *cold_v;
+  int cold_len, hot_len;
+  const char *hot_k, *hot_v;
+  int64_t hks0, hks1, hks2, hvs0, hvs1, hvs2;
+  const char *mask;
+  int mask_kind;  // KIV_MASK_*
+  int mask_vec4;  // bool mask with 4-byte aligned rows of unit stride
+  int64_t ms0, ms1, ms2, ms3;
+  uint8_t *tiles;  // [Bm][Hm][ceil(Q/64)][ceil(T/64)] TILE_* of the hot columns
+  int mask_b, mask_h;    // Bm, Hm: 1 where the mask broadcasts
+  int hq, hkv, qlen;
+  float scale_log2;  // scaling * log2(e)
+  char *out;
+};
+
+// Two fp32 values rounded to the dtype (hardware conversion, nearest even),
+// packed low-first.
+template <int DT> __device__ __forceinline__ uint32_t pack2(float a, float b) {
+  if constexpr (DT == DT_BF16) return __builtin_bit_cast(uint32_t, bf16x2_t{(__bf16)a, (__bf16)b});
+  else return __builtin_bit_cast(uint32_t, f16x2_t{(_Float16)a, (_Float16)b});
+}
+
+__device__ __forceinline__ int64_t mask_off(const PrefillParams &p, int b, int h, int i, int t) {
+  return (int64_t)b * p.ms0 + (int64_t)h * p.ms1 + (int64_t)i * p.ms2 + (int64_t)t * p.ms3;
+}
+
+// Additive bias (base 2) of a float mask element.
+__device__ __forceinline__ float float_bias(const PrefillParams &p, int64_t o) {
+  switch (p.mask_kind) {
+    case KIV_MASK_F32: return load_elem<DT_F32>(p.mask, o) * kLog2e;
+    case KIV_MASK_F16: return load_elem<DT_F16>(p.mask, o) * kLog2e;
+    default: return load_elem<DT_BF16>(p.mask, o) * kLog2e;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Tile classes of a mask tensor: grid (column tiles, row blocks, Bm * Hm),
+// 256 threads; thread t covers row q0 + t / 4, columns 16 (t % 4) .. + 15 of
+// the tile.  Rows past Q do not count; columns past T make a tile MIXED.
+__global__ void __launch_bounds__(kPfThreads) mask_tiles_kernel(PrefillParams p) {
+  const int kt = blockIdx.x, qb = blockIdx.y, bh = blockIdx.z;
+  const int mb = bh / p.mask_h, mh = bh - mb * p.mask_h;
+  const int row = qb * kPfRows + (threadIdx.x >> 2), c0 = kt * kPfKeys + 16 * (threadIdx.x & 3);
+  int any = 0, all = 1;
+  if (row < p.qlen) {
+    const int64_t o = mask_off(p, mb, mh, row, 0);
+    if (p.mask_kind == KIV_MASK_BOOL && p.ms3 == 1 && c0 + 16 <= p.hot_len && !(((uintptr_t)p.mask + o + c0) & 15)) {
+      const uint4 v = load16(p.mask + o + c0);
+      const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const bool vis = (w[j] >> (8 * e)) & 0xffu;
+          any |= vis;
+          all &= vis;
+        }
+    } else {
+      for (int j = 0; j < 16; ++j) {
+        const int t = c0 + j;
+        if (t >= p.hot_len) {
+          all = 0;
+          continue;
+        }
+        const int64_t oe = o + (int64_t)t * p.ms3;
+        if (p.mask_kind == KIV_MASK_BOOL) {
+          const bool vis = p.mask[oe] != 0;
+          any |= vis;
+          all &= vis;
+        } else {
+          const float v = float_bias(p, oe);
+          any |= v != -INFINITY;
+          all &= v == 0.f;
+        }
+      }
+    }
+  }
+  any = __syncthreads_or(any);
+  all = __syncthreads_and(all);
+  if (threadIdx.x == 0) {
+    const int nqb = (p.qlen + kPfRows - 1) / kPfRows, nkt = (p.hot_len + kPfKeys - 1) / kPfKeys;
+    p.tiles[((int64_t)bh * nqb + qb) * nkt + kt] =
+        (uint8_t)(!any ? TILE_SKIP : all ? TILE_FULL : TILE_MIXED);
+  }
+}
+
+// ---------------------------------------------------------------------------
+template <int DT, int KT, int MK>
+__global__ void __launch_bounds__(kPfThreads) prefill_attn_kernel(PrefillParams p) {
+  constexpr int D = 32 * KT, CPR = D / 8;
+  constexpr int KROW = D + 8;        // K tile row stride in elements
+  constexpr int VROW = kPfKeys + 4;  // V^T tile row stride in elements
+  constexpr int KJ = (kPfKeys * CPR + kPfThreads - 1) / kPfThreads;        // K chunks per thread
+  constexpr int VJ = ((kPfKeys / 4) * CPR + kPfThreads - 1) / kPfThreads;  // V key quads per thread
+  __shared__ __align__(16) uint16_t ks[kPfKeys * KROW];
+  __shared__ __align__(16) uint16_t vt[D * VROW];
+  const int bh = blockIdx.y, b = bh / p.hq, h = bh - b * p.hq, kvh = h / (p.hq / p.hkv);
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, col = lane & 15, grp = lane >> 4;
+  const int qb = blockIdx.x, q0 = qb * kPfRows;
+  const int qi = q0 + 16 * wave + col;  // the lane's query row (rows past Q repeat row Q - 1's data)
+  const int qc = min(qi, p.qlen - 1);
+  const int qlast = min(q0 + kPfRows, p.qlen) - 1;
+  const int off = p.hot_len - p.qlen;  // causal: hot column t visible to row i iff t <= i + off
+  const bool causal = p.mask_kind == KIV_MASK_CAUSAL;
+  const int nct = (p.cold_len + kPfKeys - 1) / kPfKeys, nht = (p.hot_len + kPfKeys - 1) / kPfKeys;
+  const int ntiles = nct + nht;
+  const uint8_t *tile_row = nullptr;
+  if constexpr (MK != PF_ARITH) {
+    const int mb = p.mask_b == 1 ? 0 : b, mh = p.mask_h == 1 ? 0 : h;
+    const int nqb = (p.qlen + kPfRows - 1) / kPfRows;
+    tile_row = p.tiles + ((int64_t)(mb * p.mask_h + mh) * nqb + qb) * nht;
+  }
+  // Class of tile t for this block (uniform over the block).
+  auto tile_class = [&](int t) -> int {
+    if (t < nct) return (t + 1) * kPfKeys <= p.cold_len ? TILE_FULL : TILE_MIXED;
+    const int key0 = (t - nct) * kPfKeys;
+    if constexpr (MK == PF_ARITH) {
+      const bool whole = key0 + kPfKeys <= p.hot_len;
+      if (!causal) return whole ? TILE_FULL : TILE_MIXED;
+      if (key0 > qlast + off) return TILE_SKIP;
+      return whole && key0 + kPfKeys - 1 <= q0 + off ? TILE_FULL : TILE_MIXED;
+    } else {
+      return tile_row[t - nct];
+    }
+  };
+  auto next_tile = [&](int t) -> int {
+    for (++t; t < ntiles; ++t) {
+      if (t >= nct) {
+        if constexpr (MK == PF_ARITH) {
+          // The causal rule hides every tile after the first hidden one.
+          if (causal && (t - nct) * kPfKeys > qlast + off) return ntiles;
+        }
+      }
+      if (tile_class(t) != TILE_SKIP) return t;
+    }
+    return ntiles;
+  };
+  const char *cold_kb = p.cold_k + ((int64_t)b * p.hkv + kvh) * p.cold_len * (int64_t)D * 2;
+  const char *cold_vb = p.cold_v + ((int64_t)b * p.hkv + kvh) * p.cold_len * (int64_t)D * 2;
+  const char *hot_kb = p.hot_k + ((int64_t)b * p.hks0 + (int64_t)kvh * p.hks1) * 2;
+  const char *hot_vb = p.hot_v + ((int64_t)b * p.hvs0 + (int64_t)kvh * p.hvs1) * 2;
+  uint4 kreg[KJ], vreg[VJ][4];
+  // Loads tile t's K chunks and V key quads into registers (zeros past the
+  // segment: a zero probability times an uninitialised V element could be NaN).
+  auto load_tile = [&](int t) {
+    const bool cold = t < nct;
+    const int key0 = (cold ? t : t - nct) * kPfKeys, n = (cold ? p.cold_len : p.hot_len) - key0;
+    const char *kb = cold ? cold_kb : hot_kb, *vb = cold ? cold_vb : hot_vb;
+    const int64_t krs = cold ? (int64_t)D * 2 : p.hks2 * 2, vrs = cold ? (int64_t)D * 2 : p.hvs2 * 2;
+#pragma unroll
+    for (int j = 0; j < KJ; ++j) {
+      const int i = tid + j * kPfThreads, key = i / CPR, c = i - key * CPR;
+      kreg[j] = (i < kPfKeys * CPR && key < n) ? load16(kb + (int64_t)(key0 + key) * krs + c * 16)
+                                                 : make_uint4(0, 0, 0, 0);
+    }
+#pragma unroll
+    for (int j = 0; j < VJ; ++j) {
+      const int i = tid + j * kPfThreads, quad = i % (kPfKeys / 4), c = i / (kPfKeys / 4);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int key = 4 * quad + r;
+        vreg[j][r] = (i < (kPfKeys / 4) * CPR && key < n) ? load16(vb + (int64_t)(key0 + key) * vrs + c * 16)
+                                                            : make_uint4(0, 0, 0, 0);
+      }
+    }
+  };
+  auto store_tile = [&]() {
+#pragma unroll
+    for (int j = 0; j < KJ; ++j) {
+      const int i = tid + j * kPfThreads, key = i / CPR, c = i - key * CPR;
+      if (i < kPfKeys * CPR) *reinterpret_cast<uint4 *>(&ks[key * KROW + c * 8]) = kreg[j];
+    }
+#pragma unroll
+    for (int j = 0; j < VJ; ++j) {
+      const int i = tid + j * kPfThreads, quad = i % (kPfKeys / 4), c = i / (kPfKeys / 4);
+      if (i < (kPfKeys / 4) * CPR) {
+        const uint32_t w[4][4] = {{vreg[j][0].x, vreg[j][0].y, vreg[j][0].z, vreg[j][0].w},
+                                  {vreg[j][1].x, vreg[j][1].y, vreg[j][1].z, vreg[j][1].w},
+                                  {vreg[j][2].x, vreg[j][2].y, vreg[j][2].z, vreg[j][2].w},
+                                  {vreg[j][3].x, vreg[j][3].y, vreg[j][3].z, vreg[j][3].w}};
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+          // dims 2m (low halves) and 2m + 1 (high halves) of the four keys
+          const uint2 lo = make_uint2((w[0][m] & 0xffffu) | (w[1][m] << 16), (w[2][m] & 0xffffu) | (w[3][m] << 16));
+          const uint2 hi = make_uint2((w[0][m] >> 16) | (w[1][m] & 0xffff0000u),
+                                      (w[2][m] >> 16) | (w[3][m] & 0xffff0000u));
+          *reinterpret_cast<uint2 *>(&vt[(c * 8 + 2 * m) * VROW + 4 * quad]) = lo;
+          *reinterpret_cast<uint2 *>(&vt[(c * 8 + 2 * m + 1) * VROW + 4 * quad]) = hi;
+        }
+      }
+    }
+  };
+
+  const char *qrow = p.q + ((int64_t)b * p.qs0 + (int64_t)h * p.qs1 + (int64_t)qc * p.qs2) * 2;
+  uint4 qx[KT];
+#pragma unroll
+  for (int st = 0; st < KT; ++st) qx[st] = load16(qrow + (32 * st + 8 * grp) * 2);
+  f32x4_t o[D / 16];
+#pragma unroll
+  for (int dt = 0; dt < D / 16; ++dt) o[dt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  float m_run = -INFINITY, l_lane = 0.f;  // l_lane: this lane's share of the row sum
+
+  int t = tile_class(0) != TILE_SKIP ? 0 : next_tile(0);
+  if (t < ntiles) load_tile(t);
+  while (t < ntiles) {
+    const int cls = tile_class(t), tn = next_tile(t);
+    __syncthreads();  // the previous tile's reads of ks / vt are done
+    store_tile();
+    __syncthreads();
+    if (tn < ntiles) load_tile(tn);
+    float s[4][4];
+#pragma unroll
+    for (int sub = 0; sub < 4; ++sub) {
+      f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int st = 0; st < KT; ++st) {
+        const uint4 a = *reinterpret_cast<const uint4 *>(&ks[(16 * sub + col) * KROW + 32 * st + 8 * grp]);
+        acc = mfma_16x16x32<DT>(a, qx[st], acc);
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) s[sub][i] = acc[i] * p.scale_log2;
+    }
+    if (cls == TILE_MIXED) {
+      const bool cold = t < nct;
+      const int key0 = (cold ? t : t - nct) * kPfKeys, n = (cold ? p.cold_len : p.hot_len) - key0;
+#pragma unroll
+      for (int sub = 0; sub < 4; ++sub) {
+        const int k4 = 16 * sub + 4 * grp;  // first of the lane's four keys in the tile
+        float bias[4];
+        if (cold || MK == PF_ARITH) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const bool vis = k4 + i < n && (cold || !causal || key0 + k4 + i <= qc + off);
+            bias[i] = vis ? 0.f : -INFINITY;
+          }
+        } else if (MK == PF_BOOL) {
+          const int64_t mo = mask_off(p, b, h, qc, key0 + k4);
+          uint32_t bits = 0;
+          if (p.mask_vec4 && k4 + 4 <= n) {
+            bits = *reinterpret_cast<const uint32_t *>(p.mask + mo);
+          } else {
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+              if (k4 + i < n && p.mask[mo + (int64_t)i * p.ms3]) bits |= 0xffu << (8 * i);
+          }
+#pragma unroll
+          for (int i = 0; i < 4; ++i) bias[i] = (bits >> (8 * i)) & 0xffu ? 0.f : -INFINITY;
+        } else {
+          const int64_t mo = mask_off(p, b, h, qc, key0 + k4);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) bias[i] = k4 + i < n ? float_bias(p, mo + (int64_t)i * p.ms3) : -INFINITY;
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) s[sub][i] += bias[i];
+      }
+    }
+    float mt = s[0][0];
+#pragma unroll
+    for (int sub = 0; sub < 4; ++sub)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) mt = fmaxf(mt, s[sub][i]);
+    mt = row_pair_max(mt);
+    mt = half_wave_max(mt);
+    // Raise the running max (and rescale) only when a score is more than
+    // 2^kRescaleSlack above it; the wave skips the rescale when no lane needs it.
+    const bool raise = mt > m_run + kRescaleSlack;
+    if (__ballot(raise)) {
+      const float m_new = raise ? mt : m_run;
+      const float alpha = m_run == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m_run - m_new);
+      l_lane *= alpha;
+#pragma unroll
+      for (int dt = 0; dt < D / 16; ++dt) o[dt] *= alpha;
+      m_run = m_new;
+    }
+    // A row that has seen no key keeps m = -inf; its probabilities are 0.
+    const float m_use = m_run == -INFINITY ? 0.f : m_run;
+    uint4 pb[2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      float e[8];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        e[i] = __builtin_amdgcn_exp2f(s[2 * j][i] - m_use);
+        e[4 + i] = __builtin_amdgcn_exp2f(s[2 * j + 1][i] - m_use);
+      }
+#pragma unroll
+      for (int i = 0; i < 8; ++i) l_lane += e[i];
+      pb[j] = make_uint4(pack2<DT>(e[0], e[1]), pack2<DT>(e[2], e[3]), pack2<DT>(e[4], e[5]), pack2<DT>(e[6], e[7]));
+    }
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int dt = 0; dt < D / 16; ++dt) {
+        const uint16_t *vr = &vt[(16 * dt + col) * VROW + 32 * j + 4 * grp];
+        const uint2 lo = *reinterpret_cast<const uint2 *>(vr), hi = *reinterpret_cast<const uint2 *>(vr + 16);
+        o[dt] = mfma_16x16x32<DT>(make_uint4(lo.x, lo.y, hi.x, hi.y), pb[j], o[dt]);
+      }
+    t = tn;
+  }
+  const float l_row = half_wave_sum(row_pair_sum(l_lane));
+  if (qi >= p.qlen) return;
+  // A row with no visible key (fully masked) gets zeros.
+  const float inv = l_row > 0.f ? 1.f / l_row : 0.f;
+  char *orow = p.out + (((int64_t)b * p.qlen + qi) * p.hq + h) * (int64_t)D * 2;
+#pragma unroll
+  for (int dt = 0; dt < D / 16; ++dt)
+    *reinterpret_cast<uint2 *>(orow + (16 * dt + 4 * grp) * 2) =
+        make_uint2(pack2<DT>(o[dt][0] * inv, o[dt][1] * inv), pack2<DT>(o[dt][2] * inv, o[dt][3] * inv));
+}
+
+static int64_t div_up(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+}  // namespace kiv
+
+using namespace kiv;
+
+extern "C" {
+
+size_t kiv_prefill_workspace_size(int32_t batch, int32_t num_q_heads, int32_t q_len, int32_t hot_len) {
+  if (batch < 1 || num_q_heads < 1 || q_len < 1 || hot_len < 1) return 0;
+  return (size_t)batch * num_q_heads * div_up(q_len, kPfRows) * div_up(hot_len, kPfKeys);
+}
+
+int kiv_prefill_attention(const kiv_attention_args_t *a, kiv_stream_t stream) {
+  const char *who = "kiv_prefill_attention";
+  if (!a) return fail(KIV_ERR_INVALID, "%s: null argument", who);
+  const int dt = a->dtype;
+  if (dt != KIV_DTYPE_F16 && dt != KIV_DTYPE_BF16) return fail(KIV_ERR_UNSUPPORTED, "%s: fp16/bf16 only", who);
+  const int B = a->batch, hq = a->num_q_heads, hkv = a->num_kv_heads, D = a->head_dim, Q = a->q_len;
+  if (B < 1 || hq < 1 || hkv < 1 || Q < 1 || hq % hkv) return fail(KIV_ERR_INVALID, "%s: bad head geometry", who);
+  const int kt = D / 32;
+  if (D % 32 || !(kt <= 4 || kt == 6 || kt == 8))
+    return fail(KIV_ERR_UNSUPPORTED, "%s: head_dim %d unsupported (32, 64, 96, 128, 192, 256)", who, D);
+  if (a->cold_len < 0 || a->hot_len < 0 || a->cold_len + a->hot_len < 1)
+    return fail(KIV_ERR_INVALID, "%s: no keys", who);
+  const bool need_cold = a->cold_len > 0, need_hot = a->hot_len > 0;
+  if (!a->q || !a->out || (need_cold && (!a->cold_k || !a->cold_v)) || (need_hot && (!a->hot_k || !a->hot_v)))
+    return fail(KIV_ERR_INVALID, "%s: null pointer", who);
+  if (a->q_stride[3] != 1) return fail(KIV_ERR_INVALID, "%s: q head_dim stride must be 1", who);
+  const uintptr_t ptrs = (uintptr_t)a->q | (uintptr_t)a->out |
+                         (need_cold ? (uintptr_t)a->cold_k | (uintptr_t)a->cold_v : 0) |
+                         (need_hot ? (uintptr_t)a->hot_k | (uintptr_t)a->hot_v : 0);
+  if (ptrs & 15) return fail(KIV_ERR_INVALID, "%s: q, K, V and out must be 16-byte aligned", who);
+  for (int i = 0; i < 3; ++i)
+    if ((a->q_stride[i] % 8) || (a->hot_k_stride[i] % 8) || (a->hot_v_stride[i] % 8))
+      return fail(KIV_ERR_INVALID, "%s: strides must be multiples of 8 elements", who);
+  if ((int64_t)B * hq > 65535) return fail(KIV_ERR_UNSUPPORTED, "%s: batch * heads above 65535", who);
+  int mk = a->mask_kind;
+  const bool explicit_mask = a->mask != nullptr;
+  if (explicit_mask) {
+    if (mk < KIV_MASK_BOOL || mk > KIV_MASK_BF16) return fail(KIV_ERR_INVALID, "%s: unknown mask kind %d", who, mk);
+    if (!need_hot) mk = KIV_MASK_NONE;  // the mask covers hot columns only
+  } else if (mk != KIV_MASK_CAUSAL) {
+    mk = KIV_MASK_NONE;
+  }
+  PrefillParams p;
+  p.q = (const char *)a->q;
+  p.qs0 = a->q_stride[0];
+  p.qs1 = a->q_stride[1];
+  p.qs2 = a->q_stride[2];
+  p.cold_k = (const char *)a->cold_k;
+  p.cold_v = (const char *)a->cold_v;
+  p.cold_len = a->cold_len;
+  p.hot_len = a->hot_len;
+  p.hot_k = (const char *)a->hot_k;
+  p.hot_v = (const char *)a->hot_v;
+  p.hks0 = a->hot_k_stride[0];
+  p.hks1 = a->hot_k_stride[1];
+  p.hks2 = a->hot_k_stride[2];
+  p.hvs0 = a->hot_v_stride[0];
+  p.hvs1 = a->hot_v_stride[1];
+  p.hvs2 = a->hot_v_stride[2];
+  p.mask = (const char *)a->mask;
+  p.mask_kind = mk;
+  p.ms0 = a->mask_stride[0];
+  p.ms1 = a->mask_stride[1];
+  p.ms2 = a->mask_stride[2];
+  p.ms3 = a->mask_stride[3];
+  p.mask_vec4 = mk == KIV_MASK_BOOL && p.ms3 == 1 && !(((uintptr_t)a->mask | p.ms0 | p.ms1 | p.ms2) & 3);
+  p.mask_b = p.ms0 == 0 ? 1 : B;
+  p.mask_h = p.ms1 == 0 ? 1 : hq;
+  p.tiles = nullptr;
+  p.hq = hq;
+  p.hkv = hkv;
+  p.qlen = Q;
+  p.scale_log2 = a->scaling * kLog2e;
+  p.out = (char *)a->out;
+  hipStream_t st = (hipStream_t)stream;
+  const int mode = mk == KIV_MASK_BOOL ? PF_BOOL : (mk == KIV_MASK_NONE || mk == KIV_MASK_CAUSAL) ? PF_ARITH : PF_FLOAT;
+  if (mode != PF_ARITH) {
+    const size_t need = (size_t)p.mask_b * p.mask_h * div_up(Q, kPfRows) * div_up(a->hot_len, kPfKeys);
+    if (!a->workspace || a->workspace_bytes < need)
+      return fail(KIV_ERR_INVALID, "%s: a mask tensor needs a workspace of %zu bytes (kiv_prefill_workspace_size)", who,
+                  need);
+    p.tiles = (uint8_t *)a->workspace;
+    const dim3 cgrid((unsigned)div_up(a->hot_len, kPfKeys), (unsigned)div_up(Q, kPfRows),
+                     (unsigned)(p.mask_b * p.mask_h));
+    if (cgrid.y > 65535 || cgrid.z > 65535) return fail(KIV_ERR_UNSUPPORTED, "%s: too many query rows", who);
+    hipLaunchKernelGGL(mask_tiles_kernel, cgrid, dim3(kPfThreads), 0, st, p);
+  }
+  const dim3 grid((unsigned)div_up(Q, kPfRows), (unsigned)(B * hq));
+  int rc = with_kt(kt, [&](auto ktc) {
+    constexpr int KTV = decltype(ktc)::value;
+    if constexpr (KTV == 16) {
+      return (int)fail(KIV_ERR_UNSUPPORTED, "%s: head_dim 512 unsupported", who);
+    } else {
+      auto launch = [&](auto dtc, auto mkc) {
+        hipLaunchKernelGGL((prefill_attn_kernel<decltype(dtc)::value, KTV, decltype(mkc)::value>), grid,
+                           dim3(kPfThreads), 0, st, p);
+      };
+      using std::integral_constant;
+      auto by_mode = [&](auto dtc) {
+        if (mode == PF_ARITH) launch(dtc, integral_constant<int, PF_ARITH>{});
+        else if (mode == PF_BOOL) launch(dtc, integral_constant<int, PF_BOOL>{});
+        else launch(dtc, integral_constant<int, PF_FLOAT>{});
+      };
+      if (dt == KIV_DTYPE_BF16) by_mode(integral_constant<int, DT_BF16>{});
+      else by_mode(integral_constant<int, DT_F16>{});
+      return (int)KIV_OK;
+    }
+  });
+  if (rc) return rc;
+  KIV_HIP(hipGetLastError());
+  return KIV_OK;
+}
+
+}  // extern "C"
