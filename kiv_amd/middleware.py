@@ -4,13 +4,15 @@ Drop-in for the reference's ``KIVMiddleware`` (kiv/middleware.py:43-356):
 ``install`` registers a wrapper under ``ALL_ATTENTION_FUNCTIONS["kiv_<impl>"]``
 (mirroring the mask function), ``create_cache`` / ``activate_cache`` bind a
 :class:`TieredKVCache` to the global attention modules and
-``chunked_prefill`` runs long prompts chunk by chunk with the original
-attention.  At decode the wrapper retrieves the top-P cold K/V with the HIP
-kernels and, for single-position queries, runs one merged softmax over
-[retrieved ; hot] (:func:`kiv_amd.attention.decode_attention`) instead of
-concatenating and calling the original attention.  Shapes the merged kernel
-does not cover take the reference's route: concatenate, widen the mask,
-call the original attention function.
+``chunked_prefill`` runs long prompts chunk by chunk without retrieval.  At
+decode the wrapper retrieves the top-P cold K/V with the HIP kernels and,
+for single-position queries, runs one merged softmax over [retrieved ; hot]
+(``ColdKVStore.retrieve_attend``) instead of concatenating and
+calling the original attention.  Queries of many positions (prefill chunks,
+and long queries with a cold tier) run on the matrix-core attention
+(:func:`kiv_amd.attention.prefill_attention`).  Shapes the kernels do not
+cover take the reference's route: concatenate, widen the mask, call the
+original attention function.
 """
 
 from __future__ import annotations
@@ -24,7 +26,7 @@ import torch
 from transformers.masking_utils import ALL_MASK_ATTENTION_FUNCTIONS
 from transformers.modeling_utils import ALL_ATTENTION_FUNCTIONS
 
-from .attention import decode_attention, fused_supported
+from .attention import fused_supported, prefill_attention, prefill_supported
 from .config import KIVConfig
 from .hf_topology import _find_text_model, detect_topology
 from .mask_utils import extend_mask_for_cold
@@ -46,14 +48,30 @@ def _prefill_logits_kwargs(model: Any, logits_to_keep: int = 1) -> dict[str, int
     return {"logits_to_keep": logits_to_keep} if "logits_to_keep" in params else {}
 
 
-def _merged_kernel_applies(module, query, key, mask, kwargs) -> bool:
-    """The merged kernel reproduces plain softmax attention only: no dropout,
-    soft-capping or attention sinks."""
+def _plain_softmax(module, kwargs) -> bool:
+    """The HIP attention kernels reproduce plain softmax attention only: no
+    dropout, soft-capping or attention sinks."""
     if kwargs.get("dropout", 0.0) and getattr(module, "training", False):
         return False
-    if kwargs.get("softcap") is not None or kwargs.get("s_aux") is not None or kwargs.get("sinks") is not None:
-        return False
-    return fused_supported(query, key, mask)
+    return kwargs.get("softcap") is None and kwargs.get("s_aux") is None and kwargs.get("sinks") is None
+
+
+def _merged_kernel_applies(module, query, key, mask, kwargs) -> bool:
+    return _plain_softmax(module, kwargs) and fused_supported(query, key, mask)
+
+
+def _none_mask_rule(impl: str | None, module, q_len: int, kv_len: int) -> str | None:
+    """What a missing mask means to the original attention for a query of
+    q_len positions over kv_len keys: "causal" (SDPA's is_causal, which HF
+    sets when the mask is None; top-left aligned, so only q_len == kv_len is
+    taken here), "none" (eager adds no mask), or None (not handled)."""
+    if impl == "eager":
+        return "none"
+    if impl == "sdpa":
+        if not getattr(module, "is_causal", True):
+            return "none"
+        return "causal" if q_len == kv_len else None
+    return None
 
 
 class KIVMiddleware:
@@ -67,6 +85,7 @@ class KIVMiddleware:
         self._installed = False
         self._original_impl: str | None = None
         self._kiv_key: str | None = None
+        self._prefilling = False  # chunked_prefill: the wrapper attends without retrieval
 
     # -------------------------------------------------------------- install
     def install(self) -> None:
@@ -144,11 +163,15 @@ class KIVMiddleware:
                         prefill_hot_cap: int | None = None, empty_cache_interval: int | None = None) -> torch.Tensor:
         """Prefill ``input_ids`` [B, T] in chunks; returns last-token logits [B, vocab].
 
-        Same control flow as kiv/middleware.py:174-260: the original attention
-        runs every chunk (no retrieval during prefill); with
+        Same control flow as kiv/middleware.py:174-260: plain attention over
+        the hot window for every chunk (no retrieval during prefill); with
         ``prefill_hot_cap`` the hot windows are trimmed to the cap after each
         chunk; the wrapper is restored even when a forward raises; finally
-        the hot windows are trimmed to ``hot_budget``.
+        the hot windows are trimmed to ``hot_budget``.  Where the reference
+        switches to the original attention function, the wrapper stays
+        installed in a no-retrieval mode and runs the chunk's attention on
+        the matrix-core kernel (kiv_prefill_attention), falling back to the
+        original function for shapes the kernel does not cover.
         """
         if not self._installed:
             raise RuntimeError("Call install() before chunked_prefill().")
@@ -157,7 +180,7 @@ class KIVMiddleware:
         extra = _prefill_logits_kwargs(self.model, logits_to_keep=1)
         if prefill_hot_cap is not None:
             cache._suppress_cold = True
-        self._set_attn_impl(self._original_impl)
+        self._prefilling = True
         try:
             for n, start in enumerate(range(0, total, chunk_size)):
                 end = min(start + chunk_size, total)
@@ -173,7 +196,7 @@ class KIVMiddleware:
                     torch.cuda.empty_cache()
         finally:
             cache._suppress_cold = False
-            self._set_attn_impl(self._kiv_key)
+            self._prefilling = False
         if prefill_hot_cap is None:
             cache.mark_prefill_complete()
         else:
@@ -210,14 +233,34 @@ class KIVMiddleware:
         if fallback_scaling is None:
             fallback_scaling = self.topology.head_dim ** -0.5
 
+        middleware = self
+        impl = self._original_impl
+
+        def dense_attention(module, query, key, value, attention_mask, kwargs):
+            """Attention over the given keys only: the matrix-core kernel for
+            queries of many positions, the original function otherwise."""
+            if (query.shape[2] > 1 and kwargs.get("sliding_window") is None and _plain_softmax(module, kwargs)
+                    and prefill_supported(query, key, attention_mask)):
+                rule = None if attention_mask is not None else _none_mask_rule(impl, module, query.shape[2],
+                                                                             key.shape[2])
+                if attention_mask is not None or rule is not None:
+                    scaling = kwargs.get("scaling")
+                    if scaling is None:
+                        scaling = getattr(module, "scaling", None) or fallback_scaling
+                    out = prefill_attention(query, None, None, key, value, attention_mask, scaling,
+                                            causal=rule == "causal")
+                    return out, None
+            return original_fn(module, query, key, value, attention_mask, **kwargs)
+
         def kiv_attention(module, query, key, value, attention_mask, **kwargs):
             cache = getattr(module, "_kiv_cache", None)
             layer_idx = getattr(module, "_kiv_layer_idx", None)
-            if cache is None or layer_idx is None or getattr(cache, "_suppress_cold", False):
-                return original_fn(module, query, key, value, attention_mask, **kwargs)
+            if (middleware._prefilling or cache is None or layer_idx is None
+                    or getattr(cache, "_suppress_cold", False)):
+                return dense_attention(module, query, key, value, attention_mask, kwargs)
             store = cache.get_cold_store(layer_idx)
             if store is None or store.cold_length == 0:
-                return original_fn(module, query, key, value, attention_mask, **kwargs)
+                return dense_attention(module, query, key, value, attention_mask, kwargs)
             scaling = kwargs.get("scaling")
             if scaling is None:
                 scaling = fallback_scaling
@@ -233,7 +276,13 @@ class KIVMiddleware:
                 return out.to(query.dtype), None
             cold_k, cold_v = store.retrieve_top_kv(query, scaling, kiv_config, step=step)
             if cold_k is None:
-                return original_fn(module, query, key, value, attention_mask, **kwargs)
+                return dense_attention(module, query, key, value, attention_mask, kwargs)
+            if (attention_mask is not None and query.shape[2] > 1 and _plain_softmax(module, kwargs)
+                    and prefill_supported(query, key, attention_mask)):
+                # A query of many positions: one matrix-core pass over
+                # [retrieved ; hot], the mask applying to the hot columns.
+                out = prefill_attention(query, cold_k, cold_v, key, value, attention_mask, scaling)
+                return out, None
             key = torch.cat([cold_k, key], dim=2)
             value = torch.cat([cold_v, value], dim=2)
             if attention_mask is not None:

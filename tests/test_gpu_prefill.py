@@ -42,8 +42,10 @@ def causal_bias(Q: int, T: int) -> np.ndarray:
     return np.where(t <= i + (T - Q), 0.0, -np.inf)
 
 
-def check(q, cold_k, cold_v, hot_k, hot_v, scaling, mask=None, causal=False):
-    out = prefill_attention(q, cold_k, cold_v, hot_k, hot_v, mask, scaling, causal=causal)
+def check(q, cold_k, cold_v, hot_k, hot_v, scaling, mask=None, causal=False, out=None):
+    """prefill_attention (or its given output ``out``) against the fp64 bound."""
+    if out is None:
+        out = prefill_attention(q, cold_k, cold_v, hot_k, hot_v, mask, scaling, causal=causal)
     torch.cuda.synchronize()
     B, hq, Q, D = q.shape
     T = hot_k.shape[2]

@@ -242,7 +242,9 @@ def test_chunked_prefill_restores_wrapper_on_error():
     cache = _FakeCache()
     with pytest.raises(RuntimeError, match="boom"):
         mw.chunked_prefill(torch.ones(1, 5, dtype=torch.long), cache, chunk_size=2, prefill_hot_cap=4)
-    assert model.config._attn_implementation == "kiv_eager" and cache._suppress_cold is False
+    # The wrapper stays registered; its no-retrieval mode and the cache flag are reset.
+    assert not hasattr(model.config, "_attn_implementation")
+    assert mw._prefilling is False and cache._suppress_cold is False
 
 
 def test_chunked_prefill_requires_install():
