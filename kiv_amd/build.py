@@ -22,6 +22,10 @@ CSRC = PKG / "csrc"
 LIBDIR = PKG / "_lib"
 LIB = LIBDIR / "libkiv_hip.so"
 SOURCES = ("kiv_store.hip", "kiv_retrieve.hip", "kiv_attention.hip", "kiv_prefill.hip", "kiv_probe.hip")
+# Per-source flags.  The prefill attention keeps its MFMA accumulators in
+# ordinary VGPRs (the softmax rescales them every few tiles; in AGPRs every
+# tile would pay a copy in and out).
+EXTRA = {"kiv_prefill.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=true"]}
 ARCH = os.environ.get("KIV_OFFLOAD_ARCH", "gfx950")
 
 COMMON = [
@@ -61,7 +65,7 @@ def build(verbose: bool = False) -> Path:
     jobs = []
     for name in SOURCES:
         obj = objdir / (name + ".o")
-        jobs.append((obj, [hipcc, *COMMON, "-c", str(CSRC / name), "-o", str(obj)]))
+        jobs.append((obj, [hipcc, *COMMON, *EXTRA.get(name, []), "-c", str(CSRC / name), "-o", str(obj)]))
     with cf.ThreadPoolExecutor(max_workers=min(len(jobs), os.cpu_count() or 1)) as ex:
         logs = list(ex.map(lambda j: _run(j[1]), jobs))
     tmp = LIB.with_suffix(".so.tmp")

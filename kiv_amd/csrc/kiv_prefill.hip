@@ -44,7 +44,7 @@
 namespace kiv {
 
 constexpr int kPfThreads = 256;
-constexpr int kPfRows = 64;  // query rows per block (16 per wave)
+constexpr int kPfRows = 64;  // query rows per mask tile class entry
 constexpr int kPfKeys = 64;  // keys per tile
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kRescaleSlack = 8.f;  // base-2 headroom before the running max moves
@@ -141,30 +141,68 @@ __global__ void __launch_bounds__(kPfThreads) mask_tiles_kernel(PrefillParams p)
 }
 
 // ---------------------------------------------------------------------------
+// Row groups of 16 query rows per wave: two up to head_dim 128 (each K and
+// V^T operand read from LDS then feeds two MFMAs, halving LDS and L2 traffic
+// per flop), one above (the accumulators would not fit twice).
+template <int KT> struct PfShape {
+  static constexpr int RG = KT <= 4 ? 2 : 1;
+  static constexpr int ROWS = 64 * RG;  // query rows per block
+};
+constexpr int kPfLdsTiles = 4096;  // tile classes a block keeps in LDS (hot windows up to 256K keys)
+
 template <int DT, int KT, int MK>
-__global__ void __launch_bounds__(kPfThreads) prefill_attn_kernel(PrefillParams p) {
-  constexpr int D = 32 * KT, CPR = D / 8;
+__global__ void __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(2)))
+prefill_attn_kernel(PrefillParams p) {
+  constexpr int D = 32 * KT, CPR = D / 8, RG = PfShape<KT>::RG, ROWS = PfShape<KT>::ROWS;
   constexpr int KROW = D + 8;        // K tile row stride in elements
   constexpr int VROW = kPfKeys + 4;  // V^T tile row stride in elements
   constexpr int KJ = (kPfKeys * CPR + kPfThreads - 1) / kPfThreads;        // K chunks per thread
   constexpr int VJ = ((kPfKeys / 4) * CPR + kPfThreads - 1) / kPfThreads;  // V key quads per thread
+  static_assert((kPfKeys * CPR) % kPfThreads == 0, "K tile items must fill the block");
   __shared__ __align__(16) uint16_t ks[kPfKeys * KROW];
   __shared__ __align__(16) uint16_t vt[D * VROW];
+  __shared__ uint8_t tcls[MK == PF_ARITH ? 1 : kPfLdsTiles];
   const int bh = blockIdx.y, b = bh / p.hq, h = bh - b * p.hq, kvh = h / (p.hq / p.hkv);
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, col = lane & 15, grp = lane >> 4;
-  const int qb = blockIdx.x, q0 = qb * kPfRows;
-  const int qi = q0 + 16 * wave + col;  // the lane's query row (rows past Q repeat row Q - 1's data)
-  const int qc = min(qi, p.qlen - 1);
-  const int qlast = min(q0 + kPfRows, p.qlen) - 1;
+  // Row blocks in reverse: under the causal rule later rows see more tiles,
+  // and starting the longest blocks first shortens the tail of the launch.
+  const int qb = gridDim.x - 1 - blockIdx.x, q0 = qb * ROWS;
+  int qi[RG], qc[RG];  // the lane's query rows (rows past Q repeat row Q - 1's data)
+#pragma unroll
+  for (int g = 0; g < RG; ++g) {
+    qi[g] = q0 + 16 * (RG * wave + g) + col;
+    qc[g] = min(qi[g], p.qlen - 1);
+  }
+  const int qlast = min(q0 + ROWS, p.qlen) - 1;
   const int off = p.hot_len - p.qlen;  // causal: hot column t visible to row i iff t <= i + off
   const bool causal = p.mask_kind == KIV_MASK_CAUSAL;
   const int nct = (p.cold_len + kPfKeys - 1) / kPfKeys, nht = (p.hot_len + kPfKeys - 1) / kPfKeys;
   const int ntiles = nct + nht;
-  const uint8_t *tile_row = nullptr;
+  // Mask tensors: the classes of this block's rows (the 64-row entries it
+  // spans, combined), in LDS when they fit.
+  const uint8_t *cls_rows = nullptr;
+  int cls_n = 0;
+  bool cls_lds = false;
   if constexpr (MK != PF_ARITH) {
     const int mb = p.mask_b == 1 ? 0 : b, mh = p.mask_h == 1 ? 0 : h;
-    const int nqb = (p.qlen + kPfRows - 1) / kPfRows;
-    tile_row = p.tiles + ((int64_t)(mb * p.mask_h + mh) * nqb + qb) * nht;
+    const int nqb = (p.qlen + 63) / 64, r0 = q0 / 64;
+    cls_n = min(RG, nqb - r0);
+    cls_rows = p.tiles + ((int64_t)(mb * p.mask_h + mh) * nqb + r0) * nht;
+    cls_lds = nht <= kPfLdsTiles;
+  }
+  auto combine = [&](int k) -> int {
+    int c = cls_rows[k];
+    for (int r = 1; r < cls_n; ++r) {
+      const int d = cls_rows[(int64_t)r * nht + k];
+      c = c == d ? c : (c == TILE_SKIP && d == TILE_SKIP) ? TILE_SKIP : TILE_MIXED;
+    }
+    return c;
+  };
+  if constexpr (MK != PF_ARITH) {
+    if (cls_lds) {
+      for (int k = tid; k < nht; k += kPfThreads) tcls[k] = (uint8_t)combine(k);
+      __syncthreads();
+    }
   }
   // Class of tile t for this block (uniform over the block).
   auto tile_class = [&](int t) -> int {
@@ -176,16 +214,14 @@ __global__ void __launch_bounds__(kPfThreads) prefill_attn_kernel(PrefillParams 
       if (key0 > qlast + off) return TILE_SKIP;
       return whole && key0 + kPfKeys - 1 <= q0 + off ? TILE_FULL : TILE_MIXED;
     } else {
-      return tile_row[t - nct];
+      return cls_lds ? (int)tcls[t - nct] : combine(t - nct);
     }
   };
   auto next_tile = [&](int t) -> int {
     for (++t; t < ntiles; ++t) {
-      if (t >= nct) {
-        if constexpr (MK == PF_ARITH) {
-          // The causal rule hides every tile after the first hidden one.
-          if (causal && (t - nct) * kPfKeys > qlast + off) return ntiles;
-        }
+      if constexpr (MK == PF_ARITH) {
+        // The causal rule hides every tile after the first hidden one.
+        if (causal && t >= nct && (t - nct) * kPfKeys > qlast + off) return ntiles;
       }
       if (tile_class(t) != TILE_SKIP) return t;
     }
@@ -196,27 +232,31 @@ __global__ void __launch_bounds__(kPfThreads) prefill_attn_kernel(PrefillParams 
   const char *hot_kb = p.hot_k + ((int64_t)b * p.hks0 + (int64_t)kvh * p.hks1) * 2;
   const char *hot_vb = p.hot_v + ((int64_t)b * p.hvs0 + (int64_t)kvh * p.hvs1) * 2;
   uint4 kreg[KJ], vreg[VJ][4];
-  // Loads tile t's K chunks and V key quads into registers (zeros past the
-  // segment: a zero probability times an uninitialised V element could be NaN).
+  // Loads tile t's K chunks and V key quads into registers.  Rows past the
+  // segment's end repeat its last row: their scores get a -inf bias, so the
+  // finite duplicates contribute exactly nothing.
   auto load_tile = [&](int t) {
     const bool cold = t < nct;
-    const int key0 = (cold ? t : t - nct) * kPfKeys, n = (cold ? p.cold_len : p.hot_len) - key0;
-    const char *kb = cold ? cold_kb : hot_kb, *vb = cold ? cold_vb : hot_vb;
-    const int64_t krs = cold ? (int64_t)D * 2 : p.hks2 * 2, vrs = cold ? (int64_t)D * 2 : p.hvs2 * 2;
+    const int key0 = (cold ? t : t - nct) * kPfKeys, last = (cold ? p.cold_len : p.hot_len) - key0 - 1;
+    const uint32_t krs = cold ? D * 2 : (uint32_t)p.hks2 * 2, vrs = cold ? D * 2 : (uint32_t)p.hvs2 * 2;
+    const char *kb = (cold ? cold_kb : hot_kb) + (int64_t)key0 * krs;
+    const char *vb = (cold ? cold_vb : hot_vb) + (int64_t)key0 * vrs;
+    const bool whole = last >= kPfKeys - 1;
 #pragma unroll
     for (int j = 0; j < KJ; ++j) {
       const int i = tid + j * kPfThreads, key = i / CPR, c = i - key * CPR;
-      kreg[j] = (i < kPfKeys * CPR && key < n) ? load16(kb + (int64_t)(key0 + key) * krs + c * 16)
-                                                 : make_uint4(0, 0, 0, 0);
+      const uint32_t kr = whole ? key : min(key, last);
+      kreg[j] = load16(kb + (kr * krs + c * 16));
     }
 #pragma unroll
     for (int j = 0; j < VJ; ++j) {
       const int i = tid + j * kPfThreads, quad = i % (kPfKeys / 4), c = i / (kPfKeys / 4);
+      if (i < (kPfKeys / 4) * CPR) {
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int key = 4 * quad + r;
-        vreg[j][r] = (i < (kPfKeys / 4) * CPR && key < n) ? load16(vb + (int64_t)(key0 + key) * vrs + c * 16)
-                                                            : make_uint4(0, 0, 0, 0);
+        for (int r = 0; r < 4; ++r) {
+          const uint32_t kr = whole ? 4 * quad + r : min(4 * quad + r, last);
+          vreg[j][r] = load16(vb + (kr * vrs + c * 16));
+        }
       }
     }
   };
@@ -224,7 +264,7 @@ __global__ void __launch_bounds__(kPfThreads) prefill_attn_kernel(PrefillParams 
 #pragma unroll
     for (int j = 0; j < KJ; ++j) {
       const int i = tid + j * kPfThreads, key = i / CPR, c = i - key * CPR;
-      if (i < kPfKeys * CPR) *reinterpret_cast<uint4 *>(&ks[key * KROW + c * 8]) = kreg[j];
+      *reinterpret_cast<uint4 *>(&ks[key * KROW + c * 8]) = kreg[j];
     }
 #pragma unroll
     for (int j = 0; j < VJ; ++j) {
@@ -247,14 +287,24 @@ __global__ void __launch_bounds__(kPfThreads) prefill_attn_kernel(PrefillParams 
     }
   };
 
-  const char *qrow = p.q + ((int64_t)b * p.qs0 + (int64_t)h * p.qs1 + (int64_t)qc * p.qs2) * 2;
-  uint4 qx[KT];
+  uint4 qx[RG][KT];
 #pragma unroll
-  for (int st = 0; st < KT; ++st) qx[st] = load16(qrow + (32 * st + 8 * grp) * 2);
-  f32x4_t o[D / 16];
+  for (int g = 0; g < RG; ++g) {
+    const char *qrow = p.q + ((int64_t)b * p.qs0 + (int64_t)h * p.qs1 + (int64_t)qc[g] * p.qs2) * 2;
 #pragma unroll
-  for (int dt = 0; dt < D / 16; ++dt) o[dt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-  float m_run = -INFINITY, l_lane = 0.f;  // l_lane: this lane's share of the row sum
+    for (int st = 0; st < KT; ++st) qx[g][st] = load16(qrow + (32 * st + 8 * grp) * 2);
+  }
+  f32x4_t o[RG][D / 16];
+#pragma unroll
+  for (int g = 0; g < RG; ++g)
+#pragma unroll
+    for (int dt = 0; dt < D / 16; ++dt) o[g][dt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  float m_run[RG], l_lane[RG];  // l_lane: this lane's share of the row sum
+#pragma unroll
+  for (int g = 0; g < RG; ++g) {
+    m_run[g] = -INFINITY;
+    l_lane[g] = 0.f;
+  }
 
   int t = tile_class(0) != TILE_SKIP ? 0 : next_tile(0);
   if (t < ntiles) load_tile(t);
@@ -264,84 +314,111 @@ __global__ void __launch_bounds__(kPfThreads) prefill_attn_kernel(PrefillParams 
     store_tile();
     __syncthreads();
     if (tn < ntiles) load_tile(tn);
-    float s[4][4];
+    // Scores in base-2 units are cc * s: FULL tiles keep the raw dot products
+    // (cc = scaling * log2 e, folded into the exponent), MIXED tiles add the
+    // bias first (cc = 1).
+    f32x4_t acc[RG][4];
 #pragma unroll
-    for (int sub = 0; sub < 4; ++sub) {
-      f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+    for (int g = 0; g < RG; ++g)
 #pragma unroll
-      for (int st = 0; st < KT; ++st) {
+      for (int sub = 0; sub < 4; ++sub) acc[g][sub] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int st = 0; st < KT; ++st)
+#pragma unroll
+      for (int sub = 0; sub < 4; ++sub) {
         const uint4 a = *reinterpret_cast<const uint4 *>(&ks[(16 * sub + col) * KROW + 32 * st + 8 * grp]);
-        acc = mfma_16x16x32<DT>(a, qx[st], acc);
-      }
 #pragma unroll
-      for (int i = 0; i < 4; ++i) s[sub][i] = acc[i] * p.scale_log2;
-    }
+        for (int g = 0; g < RG; ++g) acc[g][sub] = mfma_16x16x32<DT>(a, qx[g][st], acc[g][sub]);
+      }
+    float s[RG][4][4];
+    float cc = p.scale_log2;
+#pragma unroll
+    for (int g = 0; g < RG; ++g)
+#pragma unroll
+      for (int sub = 0; sub < 4; ++sub)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) s[g][sub][i] = acc[g][sub][i];
     if (cls == TILE_MIXED) {
+      cc = 1.f;
       const bool cold = t < nct;
       const int key0 = (cold ? t : t - nct) * kPfKeys, n = (cold ? p.cold_len : p.hot_len) - key0;
 #pragma unroll
-      for (int sub = 0; sub < 4; ++sub) {
-        const int k4 = 16 * sub + 4 * grp;  // first of the lane's four keys in the tile
-        float bias[4];
-        if (cold || MK == PF_ARITH) {
+      for (int g = 0; g < RG; ++g)
 #pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const bool vis = k4 + i < n && (cold || !causal || key0 + k4 + i <= qc + off);
-            bias[i] = vis ? 0.f : -INFINITY;
-          }
-        } else if (MK == PF_BOOL) {
-          const int64_t mo = mask_off(p, b, h, qc, key0 + k4);
-          uint32_t bits = 0;
-          if (p.mask_vec4 && k4 + 4 <= n) {
-            bits = *reinterpret_cast<const uint32_t *>(p.mask + mo);
+        for (int sub = 0; sub < 4; ++sub) {
+          const int k4 = 16 * sub + 4 * grp;  // first of the lane's four keys in the tile
+          float bias[4];
+          if (cold || MK == PF_ARITH) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              const bool vis = k4 + i < n && (cold || !causal || key0 + k4 + i <= qc[g] + off);
+              bias[i] = vis ? 0.f : -INFINITY;
+            }
+          } else if (MK == PF_BOOL) {
+            const int64_t mo = mask_off(p, b, h, qc[g], key0 + k4);
+            uint32_t bits = 0;
+            if (p.mask_vec4 && k4 + 4 <= n) {
+              bits = *reinterpret_cast<const uint32_t *>(p.mask + mo);
+            } else {
+#pragma unroll
+              for (int i = 0; i < 4; ++i)
+                if (k4 + i < n && p.mask[mo + (int64_t)i * p.ms3]) bits |= 0xffu << (8 * i);
+            }
+#pragma unroll
+            for (int i = 0; i < 4; ++i) bias[i] = (bits >> (8 * i)) & 0xffu ? 0.f : -INFINITY;
           } else {
+            const int64_t mo = mask_off(p, b, h, qc[g], key0 + k4);
 #pragma unroll
-            for (int i = 0; i < 4; ++i)
-              if (k4 + i < n && p.mask[mo + (int64_t)i * p.ms3]) bits |= 0xffu << (8 * i);
+            for (int i = 0; i < 4; ++i) bias[i] = k4 + i < n ? float_bias(p, mo + (int64_t)i * p.ms3) : -INFINITY;
           }
 #pragma unroll
-          for (int i = 0; i < 4; ++i) bias[i] = (bits >> (8 * i)) & 0xffu ? 0.f : -INFINITY;
-        } else {
-          const int64_t mo = mask_off(p, b, h, qc, key0 + k4);
+          for (int i = 0; i < 4; ++i) s[g][sub][i] = fmaf(s[g][sub][i], p.scale_log2, bias[i]);
+        }
+    }
+    // Raise a row's running max (and rescale) only when a score is more than
+    // 2^kRescaleSlack above it; the wave skips the rescale when no lane needs it.
+    bool raise[RG], any_raise = false;
+    float mt[RG];
 #pragma unroll
-          for (int i = 0; i < 4; ++i) bias[i] = k4 + i < n ? float_bias(p, mo + (int64_t)i * p.ms3) : -INFINITY;
+    for (int g = 0; g < RG; ++g) {
+      float x = s[g][0][0];
+#pragma unroll
+      for (int sub = 0; sub < 4; ++sub)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) x = fmaxf(x, s[g][sub][i]);
+      mt[g] = half_wave_max(row_pair_max(x)) * cc;
+      raise[g] = mt[g] > m_run[g] + kRescaleSlack;
+      any_raise |= raise[g];
+    }
+    if (__ballot(any_raise)) {
+#pragma unroll
+      for (int g = 0; g < RG; ++g) {
+        const float m_new = raise[g] ? mt[g] : m_run[g];
+        const float alpha = m_run[g] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m_run[g] - m_new);
+        l_lane[g] *= alpha;
+#pragma unroll
+        for (int dt = 0; dt < D / 16; ++dt) o[g][dt] *= alpha;
+        m_run[g] = m_new;
+      }
+    }
+    uint4 pb[RG][2];
+#pragma unroll
+    for (int g = 0; g < RG; ++g) {
+      // A row that has seen no key keeps m = -inf; its probabilities are 0.
+      const float m_neg = m_run[g] == -INFINITY ? 0.f : -m_run[g];
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        float e[8];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          e[i] = __builtin_amdgcn_exp2f(fmaf(s[g][2 * j][i], cc, m_neg));
+          e[4 + i] = __builtin_amdgcn_exp2f(fmaf(s[g][2 * j + 1][i], cc, m_neg));
         }
 #pragma unroll
-        for (int i = 0; i < 4; ++i) s[sub][i] += bias[i];
+        for (int i = 0; i < 8; ++i) l_lane[g] += e[i];
+        pb[g][j] =
+            make_uint4(pack2<DT>(e[0], e[1]), pack2<DT>(e[2], e[3]), pack2<DT>(e[4], e[5]), pack2<DT>(e[6], e[7]));
       }
-    }
-    float mt = s[0][0];
-#pragma unroll
-    for (int sub = 0; sub < 4; ++sub)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) mt = fmaxf(mt, s[sub][i]);
-    mt = row_pair_max(mt);
-    mt = half_wave_max(mt);
-    // Raise the running max (and rescale) only when a score is more than
-    // 2^kRescaleSlack above it; the wave skips the rescale when no lane needs it.
-    const bool raise = mt > m_run + kRescaleSlack;
-    if (__ballot(raise)) {
-      const float m_new = raise ? mt : m_run;
-      const float alpha = m_run == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m_run - m_new);
-      l_lane *= alpha;
-#pragma unroll
-      for (int dt = 0; dt < D / 16; ++dt) o[dt] *= alpha;
-      m_run = m_new;
-    }
-    // A row that has seen no key keeps m = -inf; its probabilities are 0.
-    const float m_use = m_run == -INFINITY ? 0.f : m_run;
-    uint4 pb[2];
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      float e[8];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        e[i] = __builtin_amdgcn_exp2f(s[2 * j][i] - m_use);
-        e[4 + i] = __builtin_amdgcn_exp2f(s[2 * j + 1][i] - m_use);
-      }
-#pragma unroll
-      for (int i = 0; i < 8; ++i) l_lane += e[i];
-      pb[j] = make_uint4(pack2<DT>(e[0], e[1]), pack2<DT>(e[2], e[3]), pack2<DT>(e[4], e[5]), pack2<DT>(e[6], e[7]));
     }
 #pragma unroll
     for (int j = 0; j < 2; ++j)
@@ -349,19 +426,24 @@ __global__ void __launch_bounds__(kPfThreads) prefill_attn_kernel(PrefillParams 
       for (int dt = 0; dt < D / 16; ++dt) {
         const uint16_t *vr = &vt[(16 * dt + col) * VROW + 32 * j + 4 * grp];
         const uint2 lo = *reinterpret_cast<const uint2 *>(vr), hi = *reinterpret_cast<const uint2 *>(vr + 16);
-        o[dt] = mfma_16x16x32<DT>(make_uint4(lo.x, lo.y, hi.x, hi.y), pb[j], o[dt]);
+        const uint4 a = make_uint4(lo.x, lo.y, hi.x, hi.y);
+#pragma unroll
+        for (int g = 0; g < RG; ++g) o[g][dt] = mfma_16x16x32<DT>(a, pb[g][j], o[g][dt]);
       }
     t = tn;
   }
-  const float l_row = half_wave_sum(row_pair_sum(l_lane));
-  if (qi >= p.qlen) return;
-  // A row with no visible key (fully masked) gets zeros.
-  const float inv = l_row > 0.f ? 1.f / l_row : 0.f;
-  char *orow = p.out + (((int64_t)b * p.qlen + qi) * p.hq + h) * (int64_t)D * 2;
 #pragma unroll
-  for (int dt = 0; dt < D / 16; ++dt)
-    *reinterpret_cast<uint2 *>(orow + (16 * dt + 4 * grp) * 2) =
-        make_uint2(pack2<DT>(o[dt][0] * inv, o[dt][1] * inv), pack2<DT>(o[dt][2] * inv, o[dt][3] * inv));
+  for (int g = 0; g < RG; ++g) {
+    const float l_row = half_wave_sum(row_pair_sum(l_lane[g]));
+    if (qi[g] >= p.qlen) continue;
+    // A row with no visible key (fully masked) gets zeros.
+    const float inv = l_row > 0.f ? 1.f / l_row : 0.f;
+    char *orow = p.out + (((int64_t)b * p.qlen + qi[g]) * p.hq + h) * (int64_t)D * 2;
+#pragma unroll
+    for (int dt = 0; dt < D / 16; ++dt)
+      *reinterpret_cast<uint2 *>(orow + (16 * dt + 4 * grp) * 2) = make_uint2(
+          pack2<DT>(o[g][dt][0] * inv, o[g][dt][1] * inv), pack2<DT>(o[g][dt][2] * inv, o[g][dt][3] * inv));
+  }
 }
 
 static int64_t div_up(int64_t a, int64_t b) { return (a + b - 1) / b; }
@@ -401,6 +483,11 @@ int kiv_prefill_attention(const kiv_attention_args_t *a, kiv_stream_t stream) {
     if ((a->q_stride[i] % 8) || (a->hot_k_stride[i] % 8) || (a->hot_v_stride[i] % 8))
       return fail(KIV_ERR_INVALID, "%s: strides must be multiples of 8 elements", who);
   if ((int64_t)B * hq > 65535) return fail(KIV_ERR_UNSUPPORTED, "%s: batch * heads above 65535", who);
+  // Row offsets within a tile are 32-bit; the softmax takes the row maximum
+  // of the unscaled dot products, which needs a positive scale.
+  if (a->hot_k_stride[2] >= (1 << 24) || a->hot_v_stride[2] >= (1 << 24))
+    return fail(KIV_ERR_UNSUPPORTED, "%s: hot row stride too large", who);
+  if (!(a->scaling > 0.f)) return fail(KIV_ERR_UNSUPPORTED, "%s: scaling must be positive", who);
   int mk = a->mask_kind;
   const bool explicit_mask = a->mask != nullptr;
   if (explicit_mask) {
@@ -454,12 +541,12 @@ int kiv_prefill_attention(const kiv_attention_args_t *a, kiv_stream_t stream) {
     if (cgrid.y > 65535 || cgrid.z > 65535) return fail(KIV_ERR_UNSUPPORTED, "%s: too many query rows", who);
     hipLaunchKernelGGL(mask_tiles_kernel, cgrid, dim3(kPfThreads), 0, st, p);
   }
-  const dim3 grid((unsigned)div_up(Q, kPfRows), (unsigned)(B * hq));
   int rc = with_kt(kt, [&](auto ktc) {
     constexpr int KTV = decltype(ktc)::value;
     if constexpr (KTV == 16) {
       return (int)fail(KIV_ERR_UNSUPPORTED, "%s: head_dim 512 unsupported", who);
     } else {
+      const dim3 grid((unsigned)div_up(Q, PfShape<KTV>::ROWS), (unsigned)(B * hq));
       auto launch = [&](auto dtc, auto mkc) {
         hipLaunchKernelGGL((prefill_attn_kernel<decltype(dtc)::value, KTV, decltype(mkc)::value>), grid,
                            dim3(kPfThreads), 0, st, p);
