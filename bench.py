@@ -3,6 +3,7 @@
     python bench.py [--steps K] [--warmup W] [--workload qwen7b_1m] [--cold-tier host|hbm]
                     [--cache cold|warm]
     python bench.py --workload qwen15b_model_1m [--model-tokens T] [--decode-steps S]
+    python bench.py --workload qwen15b_prefill_chunk [--steps K] [--warmup W]
 
 One step = one global layer's decode step for one new token: evict the
 oldest hot row to the cold tier, coarse-to-fine retrieval over the cold
@@ -33,6 +34,13 @@ steps with retrieval in every layer.  It reports the prefill time and its
 dense-FLOP rate against the bf16 MFMA peak, the decode step time, the
 per-layer retrieval stages (store events) and the same model's step over
 a plain 2048-token cache (no cold tier) for comparison.
+
+--workload qwen15b_prefill_chunk times the matrix-core attention of one
+prefill chunk of that model on its own: 4096 query positions over a hot
+window of 8192 keys (the 4096-token cap plus the chunk), 12 q / 2 kv heads,
+head_dim 128, bf16, under the boolean causal mask the model builds (mask
+classification kernel included), against the bf16 MFMA peak, with torch's
+SDPA on the same inputs beside it.
 """
 
 from __future__ import annotations
@@ -76,6 +84,7 @@ def parse():
 SCRUB_BYTES = 512 << 20  # larger than L2 (8 x 4 MiB) plus the 256 MiB memory-side cache
 MFMA_BF16_PEAK_TFLOPS = 2500.0  # dense
 MODEL_WORKLOAD = "qwen15b_model_1m"
+CHUNK_WORKLOAD = "qwen15b_prefill_chunk"
 
 
 def make_scrub(dev):
@@ -486,6 +495,70 @@ def model_run(args):
     print(json.dumps(line), flush=True)
 
 
+def prefill_chunk_run(args):
+    """The MFMA attention of one prefill chunk (kiv_prefill_attention)."""
+    import torch
+    import torch.nn.functional as F
+
+    from kiv_amd.attention import prefill_attention
+
+    dev = torch.device("cuda", 0)
+    Q, T, hq, hkv, D = 4096, 8192, 12, 2, 128
+    gen = torch.Generator(device=dev).manual_seed(args.seed)
+    q = torch.randn(1, Q, hq, D, device=dev, dtype=torch.bfloat16, generator=gen).transpose(1, 2)
+    k = torch.randn(1, hkv, T, D, device=dev, dtype=torch.bfloat16, generator=gen)
+    v = torch.randn(1, hkv, T, D, device=dev, dtype=torch.bfloat16, generator=gen)
+    mask = torch.ones(Q, T, dtype=torch.bool, device=dev).tril(T - Q)[None, None]
+    scaling = D ** -0.5
+    visible = int(mask.sum().item())
+    useful_flop = 4.0 * D * hq * visible  # QK^T and PV over the visible (row, key) pairs
+
+    def timed(fn, steps, warmup):
+        for _ in range(warmup):
+            fn()
+        ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+        torch.cuda.synchronize()
+        for a, b in ev:
+            a.record()
+            fn()
+            b.record()
+        torch.cuda.synchronize()
+        ts = sorted(a.elapsed_time(b) * 1e3 for a, b in ev)
+        return ts[len(ts) // 2], sum(ts) / len(ts)
+
+    steps, warmup = min(args.steps, 100), min(args.warmup, 10)
+    med, avg = timed(lambda: prefill_attention(q, None, None, k, v, mask, scaling), steps, warmup)
+    kk = k.repeat_interleave(hq // hkv, 1)
+    vv = v.repeat_interleave(hq // hkv, 1)
+    sdpa_med, _ = timed(lambda: F.scaled_dot_product_attention(q, kk, vv, attn_mask=mask, scale=scaling),
+                        max(steps // 4, 5), 2)
+    tflops = useful_flop / (avg * 1e-6) / 1e12
+    line = {
+        "metric": "prefill chunk attention TFLOP/s (useful, visible pairs)",
+        "value": round(tflops, 1),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": steps,
+        "warmup": warmup,
+        "ms_per_step": round(avg / 1e3, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (standard normal q, K, V)",
+        "config": {"workload": f"{CHUNK_WORKLOAD}: 4096 query positions over 8192 hot keys (hot cap 4096 + "
+                               "chunk 4096), 12/2 heads, D 128, boolean causal mask with offset 4096"},
+        "roofline": {"kernel": "prefill_attn_kernel (+ mask_tiles_kernel)", "bound": "mfma",
+                     "achieved": round(tflops, 1), "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4), "traffic": None,
+                     "flop_per_launch": useful_flop, "avg_us": round(avg, 2), "median_us": round(med, 2)},
+        "sdpa_same_inputs_us": round(sdpa_med, 2),
+        "speedup_vs_sdpa": round(sdpa_med / med, 2),
+        "cpu_baseline": None,
+    }
+    print(json.dumps(line), flush=True)
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -496,6 +569,9 @@ def main():
 
     if args.workload == MODEL_WORKLOAD:
         model_run(args)
+        return
+    if args.workload == CHUNK_WORKLOAD:
+        prefill_chunk_run(args)
         return
 
     from kiv_amd import KIVConfig
