@@ -782,7 +782,9 @@ __global__ void __launch_bounds__(NT) coarse_select_kernel(const uint32_t *__res
 // partial page (the items after).  Union pages come from the coarse
 // select's row lists (a page bitmap ranked in LDS) or from the stored union
 // list.  With k_stage set, every candidate's K row is also written there
-// ([B*Hkv][ld][D]), so the gather takes K from HBM.  With the row lists, block
+// ([B*Hkv][ld][D]), so the gather takes K from HBM; with k_read set (the
+// later query passes of a long query) the rows are read from that copy
+// instead of the cold tier.  With the row lists, block
 // (0, 0) also stores the union list, its size and the coarse telemetry
 // (max over rows, mean over rows and pages) for the later kernels.  The
 // max over the block's
@@ -842,7 +844,7 @@ __global__ void __launch_bounds__(256) fine_scan_kernel(
     int partial_len, int page_size, int tpi, int hkv, int head_dim, const char *__restrict__ q, int64_t qs0,
     int64_t qs1, int64_t qs2, int hq, int qlen, float scale, int round, uint32_t *__restrict__ out, int64_t ld,
     const float *__restrict__ coarse_stats, int rows, int n_pages, int32_t *pages_out, int32_t *union_out,
-    float *stats_out, double *stats_accum, char *__restrict__ k_stage) {
+    float *stats_out, double *stats_accum, char *__restrict__ k_stage, const char *__restrict__ k_read) {
   constexpr int VEC = Elem<DT>::VEC, EB = Elem<DT>::BYTES;
   constexpr int UT = kFineUT;
   constexpr int NSLOT = 256 / LG;
@@ -894,6 +896,7 @@ __global__ void __launch_bounds__(256) fine_scan_kernel(
       cand0 = (int64_t)U * page_size + (int64_t)s * tpi;
       ntok = min(tpi, partial_len - s * tpi);
     }
+    if (k_read) rowbase = k_read + ((int64_t)r * ld + cand0) * row_bytes;
     for (int tb = 0; tb < ntok; tb += NSLOT * UT) {
       uint4 x[UT];
 #pragma unroll
@@ -923,6 +926,116 @@ __global__ void __launch_bounds__(256) fine_scan_kernel(
         if (lane == 0) atomicMax(&out[(int64_t)b * ld + cand0 + t], order_key(best));
       }
     }
+  }
+}
+
+// MFMA fine scan for queries of many rows (G * Q >= kFineMfmaRows per kv
+// row): the same items, union and outputs as fine_scan_kernel, but the
+// per-token max over the block's query rows is a dense product.  Per item
+// the block stages the slice's K rows (up to kFineMfmaTok tokens) in LDS
+// (coalesced rows; the K staging copy is written from the same loads), then
+// wave w scores tokens 16 w .. + 15 against the query rows 16 at a time with
+// v_mfma_f32_16x16x32: lane l gives query row l % 16 (A) and token l % 16
+// (B), dims 32 s + 8 (l / 16) .. + 7 of step s, and receives query rows
+// 4 (l / 16) + i for its token.  The token's maximum over rows is taken on
+// the raw dot products (the dtype rounding and the positive scale preserve
+// order) and folded into its key with atomicMax.
+constexpr int kFineMfmaRows = 32;  // query rows per kv row from which the MFMA scan is used
+constexpr int kFineMfmaTok = 64;   // tokens per item (LDS tile)
+
+template <int DT, int KT>
+__global__ void __launch_bounds__(256) fine_scan_mfma_kernel(
+    int union_src, const int32_t *__restrict__ row_pages, int row_pages_n, int words, int32_t *page_list,
+    int32_t *counters,
+    const uint64_t *__restrict__ ktab, int chunk_shift, int64_t page_bytes, const char *__restrict__ part_k,
+    int partial_len, int page_size, int tpi, int hkv, const char *__restrict__ q, int64_t qs0,
+    int64_t qs1, int64_t qs2, int hq, int qlen, float scale, int round, uint32_t *__restrict__ out, int64_t ld,
+    const float *__restrict__ coarse_stats, int rows, int n_pages, int32_t *pages_out, int32_t *union_out,
+    float *stats_out, double *stats_accum, char *__restrict__ k_stage, const char *__restrict__ k_read) {
+  static_assert(DT != DT_F32, "16-bit dtypes only");
+  constexpr int D = 32 * KT, CPR = D / 8, ROW = D + 8;  // LDS rows padded by 16 bytes
+  extern __shared__ uint4 smem4[];
+  __shared__ int scan_tmp[4];
+  const int r = blockIdx.y, b = r / hkv, kvh = r % hkv;
+  const int G = hq / hkv, GQ = G * qlen, GQ16 = (GQ + 15) & ~15;
+  uint16_t *qs = reinterpret_cast<uint16_t *>(smem4);  // [GQ16][ROW], rows past GQ zero
+  uint16_t *tk = qs + (size_t)GQ16 * ROW;              // [kFineMfmaTok][ROW]
+  uint32_t *ubits = reinterpret_cast<uint32_t *>(tk + (size_t)kFineMfmaTok * ROW);
+  int *urank = reinterpret_cast<int *>(ubits + words);
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, col = lane & 15, grp = lane >> 4;
+  for (int i = tid; i < GQ16 * CPR; i += 256) {
+    const int j = i / CPR, c = i % CPR;
+    uint4 x = make_uint4(0, 0, 0, 0);
+    if (j < GQ) {
+      const int h = kvh * G + j / qlen, qp = j % qlen;
+      x = load16(q + ((int64_t)b * qs0 + (int64_t)h * qs1 + (int64_t)qp * qs2 + c * 8) * 2);
+    }
+    *reinterpret_cast<uint4 *>(qs + (size_t)j * ROW + c * 8) = x;
+  }
+  int U = 0;
+  if (union_src == UNION_ROWS) {
+    U = rank_union<256>(row_pages, row_pages_n, words, ubits, urank, scan_tmp);
+    if (blockIdx.x == 0 && blockIdx.y == 0)
+      publish_union<DT>(ubits, urank, words, U, page_list, pages_out, counters, union_out, coarse_stats, rows,
+                        n_pages, round, stats_out, stats_accum);
+  } else if (union_src == UNION_LIST) {
+    U = counters[0];
+  }
+  __syncthreads();
+  const int nsplit = (page_size + tpi - 1) / tpi;
+  const int page_items = U * nsplit;
+  const int items = page_items + (partial_len + tpi - 1) / tpi;
+  constexpr int64_t row_bytes = (int64_t)D * 2;
+  for (int item = blockIdx.x; item < items; item += gridDim.x) {
+    const char *rowbase;
+    int64_t cand0;
+    int ntok;
+    if (item < page_items) {
+      const int v = item / nsplit, sp = item % nsplit;
+      const int64_t page = union_src == UNION_ROWS ? union_page(ubits, urank, words, v) : page_list[v];
+      rowbase = reinterpret_cast<const char *>(ktab[page >> chunk_shift]) +
+                (page & ((int64_t(1) << chunk_shift) - 1)) * page_bytes +
+                ((int64_t)r * page_size + (int64_t)sp * tpi) * row_bytes;
+      cand0 = (int64_t)v * page_size + (int64_t)sp * tpi;
+      ntok = min(tpi, page_size - sp * tpi);
+    } else {
+      const int sp = item - page_items;
+      rowbase = part_k + ((int64_t)r * page_size + (int64_t)sp * tpi) * row_bytes;
+      cand0 = (int64_t)U * page_size + (int64_t)sp * tpi;
+      ntok = min(tpi, partial_len - sp * tpi);
+    }
+    if (k_read) rowbase = k_read + ((int64_t)r * ld + cand0) * row_bytes;
+    __syncthreads();  // the previous item's reads of tk are done
+    for (int i = tid; i < kFineMfmaTok * CPR; i += 256) {
+      const int t = i / CPR, c = i % CPR;
+      uint4 x = make_uint4(0, 0, 0, 0);
+      if (t < ntok) {
+        x = load16(rowbase + (int64_t)t * row_bytes + c * 16);
+        if (k_stage) *reinterpret_cast<uint4 *>(k_stage + ((r * ld + cand0 + t) * D + c * 8) * 2) = x;
+      }
+      *reinterpret_cast<uint4 *>(tk + (size_t)t * ROW + c * 8) = x;
+    }
+    __syncthreads();
+    if (16 * wave >= ntok) continue;
+    uint4 kb[KT];
+#pragma unroll
+    for (int st = 0; st < KT; ++st)
+      kb[st] = *reinterpret_cast<const uint4 *>(tk + (size_t)(16 * wave + col) * ROW + 32 * st + 8 * grp);
+    float best = -INFINITY;
+    for (int g16 = 0; g16 < GQ; g16 += 16) {
+      f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int st = 0; st < KT; ++st)
+        acc = mfma_16x16x32<DT>(*reinterpret_cast<const uint4 *>(qs + (size_t)(g16 + col) * ROW + 32 * st + 8 * grp),
+                                kb[st], acc);
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        if (g16 + 4 * grp + i < GQ) best = fmaxf(best, acc[i]);
+    }
+    best = half_wave_max(row_pair_max(best));
+    const int t = 16 * wave + col;
+    if (grp == 0 && t < ntok)
+      atomicMax(&out[(int64_t)b * ld + cand0 + t], order_key(score_of<DT>(best, scale, round != 0)));
   }
 }
 
@@ -1332,7 +1445,55 @@ static int retrieve_impl(kiv_store_t *s, const kiv_retrieve_args_t *a, hipStream
     const int64_t max_items = umax * nsplit + (s->partial_len + tpi - 1) / tpi;
     const int64_t want = host_tier ? 1024 : 2048;
     const int64_t nb = std::max<int64_t>(1, std::min<int64_t>(max_items, (want + s->kr - 1) / s->kr));
-    for (int pass = 0; pass < passes; ++pass) {
+    // Queries of many rows per kv row take the MFMA scan (whole 64-token
+    // slices staged in LDS).
+    const int kt = D / 32;
+    const bool mfma = dt != KIV_DTYPE_F32 && D % 32 == 0 && (kt <= 4 || kt == 6 || kt == 8) &&
+                      G * Qb >= kFineMfmaRows && a->scaling > 0.f;
+    if (mfma) {
+      tpi = std::min(kFineMfmaTok, ps);
+    }
+    const int nsplit_m = (ps + tpi - 1) / tpi;
+    const int64_t items_m = umax * nsplit_m + (s->partial_len + tpi - 1) / tpi;
+    const int64_t nb_m = std::max<int64_t>(1, std::min<int64_t>(items_m, (want + s->kr - 1) / s->kr));
+    for (int pass = 0; pass < passes && mfma; ++pass) {
+      const int Qp = std::min(Qb, Q - pass * Qb);
+      const int gq16 = (G * Qp + 15) & ~15;
+      const size_t lds = ((size_t)gq16 + kFineMfmaTok) * (D + 8) * 2 + (size_t)bwords * 4 + (size_t)(bwords + 1) * 4;
+      s->prof_begin(KIV_STAGE_FINE_SCAN, st);
+      rc = with_dt(dt, [&](auto dtc) {
+        constexpr int DTV = decltype(dtc)::value;
+        if constexpr (DTV == DT_F32) {
+          return (int)KIV_ERR_UNSUPPORTED;
+        } else {
+          return with_kt(kt, [&](auto ktc) {
+            constexpr int KTV = decltype(ktc)::value;
+            if constexpr (KTV == 16) {
+              return (int)KIV_ERR_UNSUPPORTED;
+            } else {
+              auto kern = fine_scan_mfma_kernel<DTV, KTV>;
+              if (lds > 65536)
+                KIV_HIP(hipFuncSetAttribute((const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                            (int)lds));
+              hipLaunchKernelGGL(kern, dim3((unsigned)nb_m, (unsigned)s->kr), dim3(256), lds, st, union_src,
+                                 (const int32_t *)s->row_pages.ptr, rows * kc, bwords, (int32_t *)s->page_list.ptr,
+                                 (int32_t *)s->counters.ptr, (const uint64_t *)s->k_tab.ptr, s->chunk_shift,
+                                 s->page_bytes, (const char *)s->k_part.ptr, (int)s->partial_len, ps, tpi, hkv,
+                                 (const char *)a->q + pass * qstep, a->q_stride[0], a->q_stride[1],
+                                 a->q_stride[2], hq, Qp, a->scaling, round, (uint32_t *)s->fine_keys.ptr, ldc,
+                                 (const float *)coarse_stats, rows, N, a->pages_out, a->union_count_out,
+                                 a->stats_out, a->stats_accum, pass == 0 ? k_stage : nullptr,
+                                 pass == 0 ? nullptr : k_stage);
+              return (int)KIV_OK;
+            }
+          });
+        }
+      });
+      s->prof_end(KIV_STAGE_FINE_SCAN, st);
+      if (rc) return rc;
+      KIV_HIP(hipGetLastError());
+    }
+    for (int pass = 0; pass < passes && !mfma; ++pass) {
       const int Qp = std::min(Qb, Q - pass * Qb);
       const size_t lds = (size_t)G * Qp * D * eb + (size_t)bwords * 4 + (size_t)(bwords + 1) * 4;
       s->prof_begin(KIV_STAGE_FINE_SCAN, st);
@@ -1347,7 +1508,7 @@ static int retrieve_impl(kiv_store_t *s, const kiv_retrieve_args_t *a, hipStream
                            (const char *)a->q + pass * qstep, a->q_stride[0], a->q_stride[1], a->q_stride[2], hq,
                            Qp, a->scaling, round, (uint32_t *)s->fine_keys.ptr, ldc, (const float *)coarse_stats,
                            rows, N, a->pages_out, a->union_count_out, a->stats_out, a->stats_accum,
-                           pass == 0 ? k_stage : nullptr);
+                           pass == 0 ? k_stage : nullptr, pass == 0 ? nullptr : k_stage);
         return (int)KIV_OK;
       });
       s->prof_end(KIV_STAGE_FINE_SCAN, st);

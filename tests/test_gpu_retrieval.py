@@ -470,6 +470,10 @@ LONG_QUERIES = [
                                    segment=512, n_targets=4), 1, 16),
     ("fp32_many_passes", Workload("lq3", 4, 2, 64, torch.float32, hot=16, cold=3000 + 5, top_pages=4, top_p=128,
                                   segment=256), 2, 200),
+    # G * Q >= 32 query rows per kv row: the MFMA fine scan (first case too);
+    # 32-token pages make slices shorter than its 64-token tile
+    ("gqa_f16_mfma_scan_small_pages", Workload("lq4", 8, 2, 64, torch.float16, hot=32, cold=5000 + 77, top_pages=6,
+                                               top_p=200, segment=256, page_size=32), 2, 24),
 ]
 
 
