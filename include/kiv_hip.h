@@ -229,19 +229,22 @@ int kiv_retrieve_attend(kiv_store_t *store, const kiv_retrieve_args_t *retrieve,
 
 /* Attention of a query of many positions (a prefill chunk, or a long query
  * over [retrieved ; hot]) on the matrix cores: fp16/bf16, head_dim 32, 64,
- * 96, 128, 192 or 256.  Same arguments as kiv_decode_attention; the
- * workspace is needed only with a mask tensor (kiv_prefill_workspace_size
- * bytes); mask NULL with mask_kind KIV_MASK_CAUSAL applies the causal rule
- * to the hot columns.  Softmax statistics in fp32; probabilities are rounded
+ * 96, 128, 192 or 256.  Same arguments as kiv_decode_attention, with a
+ * workspace of kiv_prefill_workspace_size bytes; mask NULL with mask_kind
+ * KIV_MASK_CAUSAL applies the causal rule to the hot columns.  Softmax statistics in fp32; probabilities are rounded
  * to the dtype before they weight V.  Rows that see no key are zero.
  * Replaces the original attention call for prefill chunks
  * (kiv/middleware.py:174-260) and for multi-position queries after the
  * concatenation (kiv/middleware.py:343-352). */
 int kiv_prefill_attention(const kiv_attention_args_t *args, kiv_stream_t stream);
 
-/* Workspace bytes kiv_prefill_attention needs with a mask tensor (one byte
- * per 64 x 64 tile of query rows x hot columns, per batch and q head). */
-size_t kiv_prefill_workspace_size(int32_t batch, int32_t num_q_heads, int32_t q_len, int32_t hot_len);
+/* Workspace bytes kiv_prefill_attention needs for this shape (0: none): one
+ * byte per 64 x 64 tile of query rows x hot columns per batch and q head for
+ * a mask tensor's tile classes, plus fp32 partial rows when the keys are
+ * split across blocks (queries too short to fill the GPU).  The workspace
+ * must be 256-byte aligned. */
+size_t kiv_prefill_workspace_size(int32_t batch, int32_t num_q_heads, int32_t head_dim, int32_t q_len,
+                                  int32_t cold_len, int32_t hot_len);
 
 #ifdef __cplusplus
 }

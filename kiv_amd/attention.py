@@ -134,9 +134,9 @@ def prefill_attention(query: torch.Tensor, cold_k: torch.Tensor | None, cold_v: 
             if have not in (1, want):
                 raise ValueError(f"mask dim {n} is {have}, expected 1 or {want}")
     args, out, _ = _prepare(query, P, hot_k, hot_v, mask, scaling, causal=causal, workspace=False)
-    if mask is not None:
-        B, hq, Q, _ = query.shape
-        need = nat.lib().kiv_prefill_workspace_size(B, hq, Q, hot_k.shape[2])
+    B, hq, Q, D = query.shape
+    need = nat.lib().kiv_prefill_workspace_size(B, hq, D, Q, P, hot_k.shape[2])
+    if need:
         ws = _workspace(query.device, need)
         args.workspace, args.workspace_bytes = ws.data_ptr(), ws.numel()
     _set_cold(args, cold_k, cold_v, query.dtype)

@@ -37,6 +37,8 @@
 // MIXED.  The causal rule and the tile edges give them arithmetically; for
 // a mask tensor a first kernel classifies every (mask row block, column
 // tile) once, so the attention reads mask elements only in MIXED tiles.
+#include <algorithm>
+
 #include "kiv_common.h"
 #include "kiv_dispatch.h"
 #include "kiv_internal.h"
@@ -64,9 +66,13 @@ struct PrefillParams {
   int64_t ms0, ms1, ms2, ms3;
   uint8_t *tiles;  // [Bm][Hm][ceil(Q/64)][ceil(T/64)] TILE_* of the hot columns
   int mask_b, mask_h;    // Bm, Hm: 1 where the mask broadcasts
-  int hq, hkv, qlen;
+  int batch, hq, hkv, qlen;
   float scale_log2;  // scaling * log2(e)
   char *out;
+  // Key splits (grid z): with nsplit > 1 each split writes its unnormalised
+  // rows and (running max, row sum) here and prefill_combine_kernel merges.
+  int nsplit;
+  float *ws_m, *ws_l, *ws_o;  // [nsplit][B*Q*Hq], [nsplit][B*Q*Hq], [nsplit][B*Q*Hq][D]
 };
 
 // Two fp32 values rounded to the dtype (hardware conversion, nearest even),
@@ -178,6 +184,10 @@ prefill_attn_kernel(PrefillParams p) {
   const bool causal = p.mask_kind == KIV_MASK_CAUSAL;
   const int nct = (p.cold_len + kPfKeys - 1) / kPfKeys, nht = (p.hot_len + kPfKeys - 1) / kPfKeys;
   const int ntiles = nct + nht;
+  // This block's share of the tiles (all of them without key splits).
+  const int z = blockIdx.z;
+  const int t_end = (int)((int64_t)(z + 1) * ntiles / p.nsplit);
+  const int t_begin = (int)((int64_t)z * ntiles / p.nsplit);
   // Mask tensors: the classes of this block's rows (the 64-row entries it
   // spans, combined), in LDS when they fit.
   const uint8_t *cls_rows = nullptr;
@@ -218,14 +228,14 @@ prefill_attn_kernel(PrefillParams p) {
     }
   };
   auto next_tile = [&](int t) -> int {
-    for (++t; t < ntiles; ++t) {
+    for (++t; t < t_end; ++t) {
       if constexpr (MK == PF_ARITH) {
         // The causal rule hides every tile after the first hidden one.
-        if (causal && t >= nct && (t - nct) * kPfKeys > qlast + off) return ntiles;
+        if (causal && t >= nct && (t - nct) * kPfKeys > qlast + off) return t_end;
       }
       if (tile_class(t) != TILE_SKIP) return t;
     }
-    return ntiles;
+    return t_end;
   };
   const char *cold_kb = p.cold_k + ((int64_t)b * p.hkv + kvh) * p.cold_len * (int64_t)D * 2;
   const char *cold_vb = p.cold_v + ((int64_t)b * p.hkv + kvh) * p.cold_len * (int64_t)D * 2;
@@ -306,14 +316,14 @@ prefill_attn_kernel(PrefillParams p) {
     l_lane[g] = 0.f;
   }
 
-  int t = tile_class(0) != TILE_SKIP ? 0 : next_tile(0);
-  if (t < ntiles) load_tile(t);
-  while (t < ntiles) {
+  int t = t_begin < t_end && tile_class(t_begin) != TILE_SKIP ? t_begin : next_tile(t_begin);
+  if (t < t_end) load_tile(t);
+  while (t < t_end) {
     const int cls = tile_class(t), tn = next_tile(t);
     __syncthreads();  // the previous tile's reads of ks / vt are done
     store_tile();
     __syncthreads();
-    if (tn < ntiles) load_tile(tn);
+    if (tn < t_end) load_tile(tn);
     // Scores in base-2 units are cc * s: FULL tiles keep the raw dot products
     // (cc = scaling * log2 e, folded into the exponent), MIXED tiles add the
     // bias first (cc = 1).
@@ -432,6 +442,23 @@ prefill_attn_kernel(PrefillParams p) {
       }
     t = tn;
   }
+  if (p.nsplit > 1) {
+    const int64_t nrows = (int64_t)p.batch * p.qlen * p.hq;
+#pragma unroll
+    for (int g = 0; g < RG; ++g) {
+      const float l_row = half_wave_sum(row_pair_sum(l_lane[g]));
+      if (qi[g] >= p.qlen) continue;
+      const int64_t sr = (int64_t)z * nrows + ((int64_t)b * p.qlen + qi[g]) * p.hq + h;
+      float *po = p.ws_o + sr * D;
+#pragma unroll
+      for (int dt = 0; dt < D / 16; ++dt) *reinterpret_cast<f32x4_t *>(po + 16 * dt + 4 * grp) = o[g][dt];
+      if (grp == 0) {
+        p.ws_m[sr] = m_run[g];
+        p.ws_l[sr] = l_row;
+      }
+    }
+    return;
+  }
 #pragma unroll
   for (int g = 0; g < RG; ++g) {
     const float l_row = half_wave_sum(row_pair_sum(l_lane[g]));
@@ -446,7 +473,65 @@ prefill_attn_kernel(PrefillParams p) {
   }
 }
 
+// Merges the key splits: out = sum_s 2^(m_s - M) o_s / sum_s 2^(m_s - M) l_s
+// with M the largest running max.  D / 4 threads per output row, 4 dims
+// each; a row that saw no key in any split gets zeros.
+template <int DT>
+__global__ void __launch_bounds__(kPfThreads) prefill_combine_kernel(PrefillParams p, int D) {
+  const int tpr = D / 4, rows_per_block = kPfThreads / tpr;
+  if ((int)threadIdx.x >= rows_per_block * tpr) return;
+  const int64_t nrows = (int64_t)p.batch * p.qlen * p.hq;
+  const int64_t row = (int64_t)blockIdx.x * rows_per_block + threadIdx.x / tpr;
+  const int d0 = 4 * (threadIdx.x % tpr);
+  if (row >= nrows) return;
+  float M = -INFINITY;
+  for (int sp = 0; sp < p.nsplit; ++sp) M = fmaxf(M, p.ws_m[sp * nrows + row]);
+  float L = 0.f;
+  f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+  if (M != -INFINITY) {
+    for (int sp = 0; sp < p.nsplit; ++sp) {
+      const float m = p.ws_m[sp * nrows + row];
+      if (m == -INFINITY) continue;
+      const float w = __builtin_amdgcn_exp2f(m - M);
+      L += w * p.ws_l[sp * nrows + row];
+      acc += w * *reinterpret_cast<const f32x4_t *>(p.ws_o + (sp * nrows + row) * D + d0);
+    }
+  }
+  const float inv = L > 0.f ? 1.f / L : 0.f;
+  *reinterpret_cast<uint2 *>(p.out + (row * D + d0) * 2) =
+      make_uint2(pack2<DT>(acc[0] * inv, acc[1] * inv), pack2<DT>(acc[2] * inv, acc[3] * inv));
+}
+
 static int64_t div_up(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+// Key splits for a launch of `blocks` blocks over `tiles` key tiles: enough
+// blocks to fill the chip (about 1024), at least two tiles per split, at
+// most 64 splits.
+static int prefill_splits(int64_t blocks, int64_t tiles) {
+  if (blocks >= 512) return 1;
+  const int64_t want = div_up(1024, blocks), most = std::max<int64_t>(1, tiles / 2);
+  return (int)std::max<int64_t>(1, std::min<int64_t>({want, most, 64}));
+}
+
+struct PrefillWorkspace {
+  size_t tiles_bytes, m_off, l_off, o_off, total;
+  int nsplit;
+};
+
+static PrefillWorkspace prefill_workspace(int B, int hq, int D, int Q, int cold_len, int hot_len, int mask_b,
+                                          int mask_h) {
+  PrefillWorkspace w;
+  const int rows = D <= 128 ? 128 : 64;  // query rows per block (PfShape)
+  const int64_t ntiles = div_up(cold_len, kPfKeys) + div_up(hot_len, kPfKeys);
+  w.nsplit = prefill_splits(div_up(Q, rows) * B * hq, ntiles);
+  w.tiles_bytes = hot_len > 0 ? (size_t)mask_b * mask_h * div_up(Q, kPfRows) * div_up(hot_len, kPfKeys) : 0;
+  const size_t nrows = (size_t)B * Q * hq;
+  w.m_off = (w.tiles_bytes + 255) & ~size_t(255);
+  w.l_off = w.m_off + ((nrows * w.nsplit * 4 + 255) & ~size_t(255));
+  w.o_off = w.l_off + ((nrows * w.nsplit * 4 + 255) & ~size_t(255));
+  w.total = w.nsplit > 1 ? w.o_off + nrows * w.nsplit * D * 4 : w.tiles_bytes;
+  return w;
+}
 
 }  // namespace kiv
 
@@ -454,9 +539,10 @@ using namespace kiv;
 
 extern "C" {
 
-size_t kiv_prefill_workspace_size(int32_t batch, int32_t num_q_heads, int32_t q_len, int32_t hot_len) {
-  if (batch < 1 || num_q_heads < 1 || q_len < 1 || hot_len < 1) return 0;
-  return (size_t)batch * num_q_heads * div_up(q_len, kPfRows) * div_up(hot_len, kPfKeys);
+size_t kiv_prefill_workspace_size(int32_t batch, int32_t num_q_heads, int32_t head_dim, int32_t q_len,
+                                  int32_t cold_len, int32_t hot_len) {
+  if (batch < 1 || num_q_heads < 1 || head_dim < 1 || q_len < 1 || cold_len < 0 || hot_len < 0) return 0;
+  return prefill_workspace(batch, num_q_heads, head_dim, q_len, cold_len, hot_len, batch, num_q_heads).total;
 }
 
 int kiv_prefill_attention(const kiv_attention_args_t *a, kiv_stream_t stream) {
@@ -523,6 +609,7 @@ int kiv_prefill_attention(const kiv_attention_args_t *a, kiv_stream_t stream) {
   p.mask_b = p.ms0 == 0 ? 1 : B;
   p.mask_h = p.ms1 == 0 ? 1 : hq;
   p.tiles = nullptr;
+  p.batch = B;
   p.hq = hq;
   p.hkv = hkv;
   p.qlen = Q;
@@ -530,11 +617,20 @@ int kiv_prefill_attention(const kiv_attention_args_t *a, kiv_stream_t stream) {
   p.out = (char *)a->out;
   hipStream_t st = (hipStream_t)stream;
   const int mode = mk == KIV_MASK_BOOL ? PF_BOOL : (mk == KIV_MASK_NONE || mk == KIV_MASK_CAUSAL) ? PF_ARITH : PF_FLOAT;
+  const PrefillWorkspace w = prefill_workspace(B, hq, D, Q, a->cold_len, a->hot_len,
+                                               mode != PF_ARITH ? p.mask_b : 0, mode != PF_ARITH ? p.mask_h : 0);
+  p.nsplit = w.nsplit;
+  p.ws_m = p.ws_l = p.ws_o = nullptr;
+  if (w.total > 0 && (!a->workspace || a->workspace_bytes < w.total || ((uintptr_t)a->workspace & 255)))
+    return fail(KIV_ERR_INVALID, "%s: needs a 256-byte aligned workspace of %zu bytes (kiv_prefill_workspace_size)",
+                who, w.total);
+  if (w.nsplit > 1) {
+    char *ws = (char *)a->workspace;
+    p.ws_m = (float *)(ws + w.m_off);
+    p.ws_l = (float *)(ws + w.l_off);
+    p.ws_o = (float *)(ws + w.o_off);
+  }
   if (mode != PF_ARITH) {
-    const size_t need = (size_t)p.mask_b * p.mask_h * div_up(Q, kPfRows) * div_up(a->hot_len, kPfKeys);
-    if (!a->workspace || a->workspace_bytes < need)
-      return fail(KIV_ERR_INVALID, "%s: a mask tensor needs a workspace of %zu bytes (kiv_prefill_workspace_size)", who,
-                  need);
     p.tiles = (uint8_t *)a->workspace;
     const dim3 cgrid((unsigned)div_up(a->hot_len, kPfKeys), (unsigned)div_up(Q, kPfRows),
                      (unsigned)(p.mask_b * p.mask_h));
@@ -546,7 +642,7 @@ int kiv_prefill_attention(const kiv_attention_args_t *a, kiv_stream_t stream) {
     if constexpr (KTV == 16) {
       return (int)fail(KIV_ERR_UNSUPPORTED, "%s: head_dim 512 unsupported", who);
     } else {
-      const dim3 grid((unsigned)div_up(Q, PfShape<KTV>::ROWS), (unsigned)(B * hq));
+      const dim3 grid((unsigned)div_up(Q, PfShape<KTV>::ROWS), (unsigned)(B * hq), (unsigned)p.nsplit);
       auto launch = [&](auto dtc, auto mkc) {
         hipLaunchKernelGGL((prefill_attn_kernel<decltype(dtc)::value, KTV, decltype(mkc)::value>), grid,
                            dim3(kPfThreads), 0, st, p);
@@ -559,6 +655,14 @@ int kiv_prefill_attention(const kiv_attention_args_t *a, kiv_stream_t stream) {
       };
       if (dt == KIV_DTYPE_BF16) by_mode(integral_constant<int, DT_BF16>{});
       else by_mode(integral_constant<int, DT_F16>{});
+      if (p.nsplit > 1) {
+        const int rows_per_block = kPfThreads / (D / 4);
+        const dim3 cgrid((unsigned)div_up((int64_t)B * Q * hq, rows_per_block));
+        if (dt == KIV_DTYPE_BF16)
+          hipLaunchKernelGGL(prefill_combine_kernel<DT_BF16>, cgrid, dim3(kPfThreads), 0, st, p, D);
+        else
+          hipLaunchKernelGGL(prefill_combine_kernel<DT_F16>, cgrid, dim3(kPfThreads), 0, st, p, D);
+      }
       return (int)KIV_OK;
     }
   });

@@ -91,6 +91,10 @@ CASES = [
     # skipped, whole and partial column tiles of a mask tensor in one call
     ("bool_mask_tile_classes", 1, 4, 1, 64, 256, 0, 640, torch.bfloat16, "bool"),
     ("float_mask_tile_classes", 1, 4, 2, 128, 192, 40, 700, torch.bfloat16, "float"),
+    # queries too short to fill the GPU: keys split across blocks, then merged
+    ("short_query_key_splits", 1, 8, 2, 128, 40, 300, 1500, torch.bfloat16, "bool"),
+    ("short_causal_key_splits_d64", 1, 4, 4, 64, 70, 0, 900, torch.float16, "causal"),
+    ("d256_key_splits_batch", 2, 4, 1, 256, 20, 64, 500, torch.bfloat16, "none"),
 ]
 
 
