@@ -178,11 +178,14 @@ SMALL = [
 ]
 
 
+@pytest.mark.parametrize("tier", ["host", "hbm"])
 @pytest.mark.parametrize("name,over,chunks", SMALL, ids=[c[0] for c in SMALL])
-def test_small_parity(cuda, name, over, chunks):
+def test_small_parity(cuda, name, over, chunks, tier):
+    """Each small case on the host tier (VALU fine scan) and in HBM (the MFMA
+    fine scan where the head dim allows it)."""
     w = Workload(name=name, **over)
     data = generate(w, seed=1)
-    store, oracle, cfg = build(w, data, cuda, chunks)
+    store, oracle, cfg = build(w, data, cuda, chunks, cold_tier=tier)
     assert store.cold_length == w.cold and store.num_pages == w.cold // w.page_size
     check_summaries(store, data, w)
     check_rows(store, data)
