@@ -563,7 +563,7 @@ def main():
     args = parse()
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported (the tiered-cache path "
-              "runs per GPU; see DESIGN.md for how it would shard)", file=sys.stderr)
+              "runs on one GPU; across GPUs it would shard by cold page range or by kv head)", file=sys.stderr)
         sys.exit(2)
     import torch
 
