@@ -251,22 +251,34 @@ prefill_attn_kernel(PrefillParams p) {
     const uint32_t krs = cold ? D * 2 : (uint32_t)p.hks2 * 2, vrs = cold ? D * 2 : (uint32_t)p.hvs2 * 2;
     const char *kb = (cold ? cold_kb : hot_kb) + (int64_t)key0 * krs;
     const char *vb = (cold ? cold_vb : hot_vb) + (int64_t)key0 * vrs;
-    const bool whole = last >= kPfKeys - 1;
+    if (last >= kPfKeys - 1 && kPfThreads % CPR == 0) {
+      // Whole tile: one 32-bit offset per thread, then uniform steps of
+      // (threads / CPR) rows for K and of one row for V.
+      const uint32_t koff = (uint32_t)(tid / CPR) * krs + (tid % CPR) * 16;
+#pragma unroll
+      for (int j = 0; j < KJ; ++j) kreg[j] = load16(kb + koff + (uint32_t)(j * (kPfThreads / CPR)) * krs);
+#pragma unroll
+      for (int j = 0; j < VJ; ++j) {
+        const int i = tid + j * kPfThreads, quad = i % (kPfKeys / 4), c = i / (kPfKeys / 4);
+        if (i < (kPfKeys / 4) * CPR) {
+          const uint32_t voff = (uint32_t)(4 * quad) * vrs + c * 16;
+#pragma unroll
+          for (int r = 0; r < 4; ++r) vreg[j][r] = load16(vb + voff + (uint32_t)r * vrs);
+        }
+      }
+      return;
+    }
 #pragma unroll
     for (int j = 0; j < KJ; ++j) {
       const int i = tid + j * kPfThreads, key = i / CPR, c = i - key * CPR;
-      const uint32_t kr = whole ? key : min(key, last);
-      kreg[j] = load16(kb + (kr * krs + c * 16));
+      kreg[j] = load16(kb + ((uint32_t)min(key, last) * krs + c * 16));
     }
 #pragma unroll
     for (int j = 0; j < VJ; ++j) {
       const int i = tid + j * kPfThreads, quad = i % (kPfKeys / 4), c = i / (kPfKeys / 4);
       if (i < (kPfKeys / 4) * CPR) {
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const uint32_t kr = whole ? 4 * quad + r : min(4 * quad + r, last);
-          vreg[j][r] = load16(vb + (kr * vrs + c * 16));
-        }
+        for (int r = 0; r < 4; ++r) vreg[j][r] = load16(vb + ((uint32_t)min(4 * quad + r, last) * vrs + c * 16));
       }
     }
   };
@@ -286,10 +298,13 @@ prefill_attn_kernel(PrefillParams p) {
                                   {vreg[j][3].x, vreg[j][3].y, vreg[j][3].z, vreg[j][3].w}};
 #pragma unroll
         for (int m = 0; m < 4; ++m) {
-          // dims 2m (low halves) and 2m + 1 (high halves) of the four keys
-          const uint2 lo = make_uint2((w[0][m] & 0xffffu) | (w[1][m] << 16), (w[2][m] & 0xffffu) | (w[3][m] << 16));
-          const uint2 hi = make_uint2((w[0][m] >> 16) | (w[1][m] & 0xffff0000u),
-                                      (w[2][m] >> 16) | (w[3][m] & 0xffff0000u));
+          // dims 2m (low halves) and 2m + 1 (high halves) of the four keys,
+          // one byte permute per pair (bytes 0-3 of the selector's table are
+          // the second operand, 4-7 the first)
+          const uint2 lo = make_uint2(__builtin_amdgcn_perm(w[1][m], w[0][m], 0x05040100u),
+                                      __builtin_amdgcn_perm(w[3][m], w[2][m], 0x05040100u));
+          const uint2 hi = make_uint2(__builtin_amdgcn_perm(w[1][m], w[0][m], 0x07060302u),
+                                      __builtin_amdgcn_perm(w[3][m], w[2][m], 0x07060302u));
           *reinterpret_cast<uint2 *>(&vt[(c * 8 + 2 * m) * VROW + 4 * quad]) = lo;
           *reinterpret_cast<uint2 *>(&vt[(c * 8 + 2 * m + 1) * VROW + 4 * quad]) = hi;
         }
