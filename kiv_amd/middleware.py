@@ -239,10 +239,16 @@ class KIVMiddleware:
         def dense_attention(module, query, key, value, attention_mask, kwargs):
             """Attention over the given keys only: the matrix-core kernel for
             queries of many positions, the original function otherwise."""
+            T = key.shape[2]
+            if attention_mask is not None and attention_mask.shape[-1] != T:
+                # Eager attention uses the mask's first T columns; other
+                # implementations take the mask as it is.
+                if impl != "eager" or attention_mask.shape[-1] < T:
+                    return original_fn(module, query, key, value, attention_mask, **kwargs)
+                attention_mask = attention_mask[..., :T]
             if (query.shape[2] > 1 and kwargs.get("sliding_window") is None and _plain_softmax(module, kwargs)
                     and prefill_supported(query, key, attention_mask)):
-                rule = None if attention_mask is not None else _none_mask_rule(impl, module, query.shape[2],
-                                                                             key.shape[2])
+                rule = None if attention_mask is not None else _none_mask_rule(impl, module, query.shape[2], T)
                 if attention_mask is not None or rule is not None:
                     scaling = kwargs.get("scaling")
                     if scaling is None:

@@ -353,3 +353,19 @@ def test_tiered_cache_uses_buffered_hot_layers_for_owned_layers():
     cache = TieredKVCache(cfg, KIVConfig(), topo, device="cpu")
     assert isinstance(cache.layers[0], _HotLayer) and isinstance(cache.layers[2], _HotLayer)
     assert not isinstance(cache.layers[1], _HotLayer)
+
+
+def test_missing_mask_rule_follows_the_original_attention():
+    """What a None mask means for a query of many positions: SDPA's is_causal
+    (taken only when the query and key counts agree, where its top-left
+    alignment and the cache's bottom-right one coincide), nothing for eager."""
+    from types import SimpleNamespace
+
+    from kiv_amd.middleware import _none_mask_rule
+
+    causal_module, plain_module = SimpleNamespace(is_causal=True), SimpleNamespace(is_causal=False)
+    assert _none_mask_rule("sdpa", causal_module, 64, 64) == "causal"
+    assert _none_mask_rule("sdpa", causal_module, 64, 96) is None
+    assert _none_mask_rule("sdpa", plain_module, 64, 96) == "none"
+    assert _none_mask_rule("eager", causal_module, 64, 96) == "none"
+    assert _none_mask_rule("flash_attention_2", causal_module, 64, 64) is None
