@@ -60,6 +60,9 @@ class ColdKVStore:
         self._cached_candidate_idx = None
         self._cached_step = -1
         self._telemetry = _RetrievalTelemetry()
+        self._umax_key: tuple | None = None  # (Q, top_pages, pages) of the cached union bound
+        self._umax = 1
+        self._fused_kv: tuple[torch.Tensor, torch.Tensor] | None = None
 
     # ------------------------------------------------------------ lifetime
     def __del__(self) -> None:
@@ -203,18 +206,28 @@ class ColdKVStore:
             width = P  # buffer width; the true count follows from U below
 
         lib = nat.lib()
-        umax = C.c_int64(0)
-        nat.check(lib.kiv_max_union_pages(self._handle, Q, kiv_config.top_pages, C.byref(umax)),
-                  "kiv_max_union_pages")
+        key = (Q, int(kiv_config.top_pages), N)
+        if self._umax_key != key:
+            umax = C.c_int64(0)
+            nat.check(lib.kiv_max_union_pages(self._handle, Q, kiv_config.top_pages, C.byref(umax)),
+                      "kiv_max_union_pages")
+            self._umax_key, self._umax = key, max(1, umax.value)
         dev = self.device
-        k_out = torch.empty(B, self._num_kv_heads, width, D, dtype=self._dtype, device=dev)
-        v_out = torch.empty_like(k_out)
-        idx_out = torch.empty(B, width, dtype=torch.int64, device=dev)
+        fused = attend is not None and exact
+        if fused:
+            # Consumed by the attention on the same stream: one pair per store.
+            shape = (B, self._num_kv_heads, width, D)
+            if self._fused_kv is None or self._fused_kv[0].shape != shape:
+                self._fused_kv = (torch.empty(shape, dtype=self._dtype, device=dev),
+                                  torch.empty(shape, dtype=self._dtype, device=dev))
+            k_out, v_out = self._fused_kv
+        else:
+            k_out = torch.empty(B, self._num_kv_heads, width, D, dtype=self._dtype, device=dev)
+            v_out = torch.empty_like(k_out)
         coarse_runs = N > 0 and not reuse
-        # Kernels fill every entry they own, so no zero-fill launches here.
-        union_count = torch.empty(1, dtype=torch.int32, device=dev) if coarse_runs else None
-        pages_out = torch.empty(max(1, umax.value), dtype=torch.int32, device=dev) if coarse_runs else None
-        stats = torch.empty(4, dtype=torch.float32, device=dev)
+        # The telemetry ring's slots for this call (kernels fill every entry
+        # they own, so no zero-fill launches here).
+        stats, idx_out, pages_out, union_count = self._telemetry.slots(dev, B, width, self._umax, coarse_runs)
         accum = self._telemetry.accumulator(dev)
         args = nat.RetrieveArgs(
             q=q.data_ptr(), q_stride=nat.strides(q, 4), q_len=Q, scaling=float(scaling),
@@ -224,7 +237,7 @@ class ColdKVStore:
             stats_out=stats.data_ptr(), stats_accum=accum.data_ptr(),
         )
         out = None
-        if attend is not None and exact:
+        if fused:
             hot_k, hot_v, mask = attend
             aargs, out, _keep = attention._prepare(q, width, hot_k, hot_v, mask, scaling)
             attention._set_cold(aargs, k_out, v_out, self._dtype)
@@ -318,8 +331,10 @@ class _RetrievalTelemetry:
     """Per-call coarse/fine records in a 256-entry ring, read lazily.
 
     Same schema as kiv/cold_store.py:417-581.  Kernels write each call's
-    statistics, union pages and selected ids into small device tensors and
-    add the scores to a device accumulator, so recording costs no host
+    statistics, union pages and selected ids into slots of preallocated
+    device rings (one slot per retrieval call, 256 slots, so a slot outlives
+    the records that refer to it) and add the scores to a device
+    accumulator: recording allocates nothing and costs no host
     synchronisation; :meth:`snapshot` converts everything at once.
     """
 
@@ -334,6 +349,30 @@ class _RetrievalTelemetry:
         self.selected_count_sum = 0
         self._accum: torch.Tensor | None = None
         self._ring: list[dict] = []
+        self._calls = 0  # retrieval calls, the slot counter
+        self._stats_ring: torch.Tensor | None = None   # [256, 4] float32
+        self._count_ring: torch.Tensor | None = None   # [256] int32
+        self._pages_ring: torch.Tensor | None = None   # [256, cap] int32
+        self._sel_ring: torch.Tensor | None = None     # [256, cap] int64
+
+    def slots(self, device: torch.device, batch: int, width: int, max_pages: int, coarse: bool):
+        """(stats[4], selected[batch, width], pages[max_pages] | None, count[1] | None)
+        views of this call's ring slot.  A ring that must grow is replaced;
+        records keep the old one alive."""
+        n = self._MAX_BUFFER
+        if self._stats_ring is None:
+            self._stats_ring = torch.empty(n, 4, dtype=torch.float32, device=device)
+            self._count_ring = torch.empty(n, dtype=torch.int32, device=device)
+        if self._sel_ring is None or self._sel_ring.shape[1] < batch * width:
+            self._sel_ring = torch.empty(n, max(batch * width, 256), dtype=torch.int64, device=device)
+        if coarse and (self._pages_ring is None or self._pages_ring.shape[1] < max_pages):
+            self._pages_ring = torch.empty(n, max(max_pages, 64), dtype=torch.int32, device=device)
+        i = self._calls % n
+        self._calls += 1
+        selected = self._sel_ring[i, : batch * width].view(batch, width)
+        if not coarse:
+            return self._stats_ring[i], selected, None, None
+        return self._stats_ring[i], selected, self._pages_ring[i, :max_pages], self._count_ring[i : i + 1]
 
     def accumulator(self, device: torch.device) -> torch.Tensor:
         if self._accum is None:
