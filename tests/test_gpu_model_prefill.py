@@ -13,7 +13,7 @@ hot] and widening the mask for the reuse path).  The two runs differ by the
 attention's rounding, which bf16 hidden states carry from layer to layer
 (and which can flip a retrieval choice near a tie in later decode steps),
 so their logits are compared coarsely: relative Frobenius difference below
-5e-2 (measured: about 2e-2).
+5e-2 (measured: 0.005 to 0.03).
 """
 
 from __future__ import annotations
@@ -39,7 +39,7 @@ def bf16_qwen2(cuda, attn: str, layers: int = 2):
     return Qwen2ForCausalLM(cfg).to(torch.bfloat16).to(cuda).eval()
 
 
-def run(cuda, attn, kernel: bool, monkeypatch, cap=None, follow=0, decode=0):
+def run(cuda, attn, kernel: bool, monkeypatch, cap=None, follow=0, decode=0, batch=1):
     """Logits of [prefill last token, decode steps..., follow-up forward] and
     the number of kernel calls."""
     calls = []
@@ -61,15 +61,15 @@ def run(cuda, attn, kernel: bool, monkeypatch, cap=None, follow=0, decode=0):
     try:
         cache = mw.create_cache(cuda)
         gen = torch.Generator().manual_seed(5)
-        ids = torch.randint(0, 512, (1, 700), generator=gen).to(cuda)
+        ids = torch.randint(0, 512, (batch, 700), generator=gen).to(cuda)
         with torch.no_grad():
             outs.append(mw.chunked_prefill(ids, cache, chunk_size=256, prefill_hot_cap=cap).float())
             for _ in range(decode):
                 tok = outs[-1].argmax(-1, keepdim=True)
                 outs.append(model(input_ids=tok, past_key_values=cache, use_cache=True).logits[:, -1].float())
             if follow:
-                f = torch.randint(0, 512, (1, follow), generator=gen).to(cuda)
-                outs.append(model(input_ids=f, past_key_values=cache, use_cache=True).logits[0].float())
+                f = torch.randint(0, 512, (batch, follow), generator=gen).to(cuda)
+                outs.append(model(input_ids=f, past_key_values=cache, use_cache=True).logits.float())
         cold = cache.get_cold_store(0).cold_length
     finally:
         mw.uninstall()
@@ -91,13 +91,14 @@ def test_chunked_prefill_runs_on_the_kernel(cuda, attn, monkeypatch):
     assert rel(got[0], ref[0]) < 5e-2
 
 
-def test_capped_prefill_and_reuse_forward_with_cold_tier(cuda, monkeypatch):
+@pytest.mark.parametrize("batch", [1, 2])
+def test_capped_prefill_and_reuse_forward_with_cold_tier(cuda, monkeypatch, batch):
     """prefill_hot_cap evicts between chunks (masks with an offset), then
     decode steps and a 200-token follow-up that retrieves from the cold tier
-    and attends [retrieved ; hot] on the kernel."""
-    print("capped prefill + reuse forward", flush=True)
-    got, calls, cold = run(cuda, "sdpa", True, monkeypatch, cap=200, follow=200, decode=2)
-    ref, _, ref_cold = run(cuda, "sdpa", False, monkeypatch, cap=200, follow=200, decode=2)
+    and attends [retrieved ; hot] on the kernel; one and two sequences."""
+    print(f"capped prefill + reuse forward, batch {batch}", flush=True)
+    got, calls, cold = run(cuda, "sdpa", True, monkeypatch, cap=200, follow=200, decode=2, batch=batch)
+    ref, _, ref_cold = run(cuda, "sdpa", False, monkeypatch, cap=200, follow=200, decode=2, batch=batch)
     assert cold > 0 and cold == ref_cold
     assert calls.count(False) == 2 * 3 and calls.count(True) == 2  # chunks, then the follow-up per layer
     diffs = [rel(g, r) for g, r in zip(got, ref)]
