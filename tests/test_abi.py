@@ -47,6 +47,12 @@ def test_invalid_arguments_fail_without_gpu_work():
     assert b"null" in lib.kiv_last_error()
     assert lib.kiv_retrieve(None, None, None) == 1
     assert lib.kiv_decode_attention(None, None) == 1
+    assert lib.kiv_prefill_attention(None, None) == 1
+    assert lib.kiv_prefill_workspace_size(0, 12, 128, 4096, 0, 8192) == 0
+    # Room for a mask tensor's tile classes (one byte per 64 x 64 tile per q head) ...
+    assert lib.kiv_prefill_workspace_size(1, 12, 128, 4096, 0, 8192) >= 12 * 64 * 128
+    # ... plus a short query's key-split partial rows (fp32 rows, max and sum).
+    assert lib.kiv_prefill_workspace_size(1, 12, 128, 16, 256, 2048) > 12 * 16 * 128 * 4
     assert lib.kiv_store_destroy(None) == 0
 
 
