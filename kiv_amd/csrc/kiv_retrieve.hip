@@ -38,7 +38,11 @@ constexpr int kScanThreads = 256;   // coarse scan block (4 waves)
 constexpr int kSelThreads = 512;       // select block (8 waves)
 constexpr int kMaxWords = 4096;     // bitmap words ranked in LDS (131072 pages)
 constexpr int kCandCap = 2048;      // candidates a select keeps in LDS
-constexpr int kRankCap = 1024;      // candidates ranked by counting
+constexpr int kRankCap = 1024;      // candidates a coarse select ranks by counting in one block
+// Candidates a fine select lists for the gather to rank: kRankCap for
+// widths up to half of it (the list stays short and so does the gather's
+// grid), kCandCap above (wide selections then skip the exact search).
+inline int fine_list_cap(int width) { return width > kRankCap / 2 ? kCandCap : kRankCap; }
 constexpr size_t kMaxStageBytes = size_t(256) << 20;  // HBM staging of candidate K rows per store
 constexpr int64_t kFineQueryBytes = 48 << 10;  // query rows per kv row the fine scan keeps in LDS
 constexpr int64_t kRowListInScan = 8192;        // row-list entries a fine-scan block ORs into its union
@@ -1043,8 +1047,9 @@ __global__ void __launch_bounds__(256) fine_scan_mfma_kernel(
 // ----------------------------------------------------------- fine select
 // One block per batch row b lists the candidates of the row's top k =
 // min(P', C) keys (bound_candidates) for the gather, which ranks them by
-// counting.  When more than kRankCap keys pass the bound, the block lists
-// exactly the k composites >= the k-th largest instead.  The block also
+// counting (one wave per entry, over the whole list).  When more than
+// list_cap (<= kCandCap) keys pass the bound, the block lists exactly the k
+// composites >= the k-th largest instead.  The block also
 // writes the row's telemetry (max, sum of scores) and zeroes the keys for
 // the next scan, which accumulates with atomicMax.
 // V = 16-byte key chunks per thread kept in registers: rows of up to
@@ -1053,7 +1058,7 @@ template <int V>
 __global__ void __launch_bounds__(kSelThreads) fine_select_kernel(
     uint32_t *__restrict__ keys, int64_t ld, const int32_t *__restrict__ counters, int has_pages, int page_size,
     int partial_len, int width, float *__restrict__ fine_stats, uint64_t *__restrict__ list, int64_t list_ld,
-    int32_t *__restrict__ list_count) {
+    int32_t *__restrict__ list_count, int list_cap) {
   constexpr int NT = kSelThreads;
   __shared__ SelSh<NT> sh;
   __shared__ uint64_t cand[kCandCap];
@@ -1074,7 +1079,7 @@ __global__ void __launch_bounds__(kSelThreads) fine_select_kernel(
   } else {
     C = bound_candidates<NT>(mk, k, sh, cand, mx, sum);
   }
-  if (C <= kRankCap) {
+  if (C <= list_cap) {
     for (int i = threadIdx.x; i < C; i += NT) out[i] = cand[i];
   } else {
     emit_topk_unranked<NT>(mk, cand, C, k, sh, [&](int pos, uint64_t x) { out[pos] = x; });
@@ -1420,8 +1425,9 @@ static int retrieve_impl(kiv_store_t *s, const kiv_retrieve_args_t *a, hipStream
     KIV_HIP(hipMemsetAsync(s->fine_keys.ptr, 0, s->fine_keys.bytes, st));
   }
   // Candidate lists of the fine select: [B][list_ld] composites, then [B] counts.
-  const int64_t lmax = std::min<int64_t>(cmax, std::max<int64_t>(kRankCap, a->out_width));
-  const int64_t list_ld = (std::max<int64_t>(kRankCap, a->out_width) + 31) & ~int64_t(31);
+  const int list_cap = fine_list_cap(a->out_width);
+  const int64_t lmax = std::min<int64_t>(cmax, std::max<int64_t>(list_cap, a->out_width));
+  const int64_t list_ld = (std::max<int64_t>(list_cap, a->out_width) + 31) & ~int64_t(31);
   if ((rc = s->sel_list.ensure((size_t)B * list_ld * 8 + (size_t)B * 4, st, false))) return rc;
   uint64_t *list = (uint64_t *)s->sel_list.ptr;
   int32_t *list_count = (int32_t *)(list + (size_t)B * list_ld);
@@ -1526,7 +1532,7 @@ static int retrieve_impl(kiv_store_t *s, const kiv_retrieve_args_t *a, hipStream
     with_select_chunks(cmax, [&](auto kern) {
       hipLaunchKernelGGL(kern, dim3(B), dim3(kSelThreads), 0, st, (uint32_t *)s->fine_keys.ptr, ldc,
                          (const int32_t *)s->counters.ptr, N > 0 ? 1 : 0, ps, (int)s->partial_len, a->out_width,
-                         fine_stats, list, list_ld, list_count);
+                         fine_stats, list, list_ld, list_count, list_cap);
     }, [](auto vc) { return fine_select_kernel<decltype(vc)::value>; });
     s->prof_end(KIV_STAGE_FINE_SELECT, st);
     KIV_HIP(hipGetLastError());
