@@ -48,6 +48,7 @@ from __future__ import annotations
 import argparse
 import ctypes as C
 import json
+from dataclasses import replace
 import os
 import sys
 import time
@@ -243,10 +244,14 @@ def probes(dev, summary_bytes, host_bytes, cold):
     }
 
 
-def roofline_and_links(w, store, stages, union_pages, tier):
-    """Algorithmic bytes per launch / measured duration for every stage."""
+def roofline_and_links(w, store, stages, union_pages, tier, scanned_slices=None):
+    """Algorithmic bytes per launch / measured duration for every stage.
+    scanned_slices: (union page, kv row) slices the fine scan read (fewer
+    than union_pages * Hkv when the host tier's scan is pruned)."""
     b = 2 if w.dtype.itemsize == 2 else 4
     row = w.num_kv_heads * w.head_dim * b          # one token, all kv heads
+    if scanned_slices is None:
+        scanned_slices = union_pages * w.num_kv_heads
     N = store.num_pages
     P = min(w.top_p, store.cold_length)
     p = store.cold_length - N * w.page_size
@@ -256,11 +261,15 @@ def roofline_and_links(w, store, stages, union_pages, tier):
         # (bytes per launch, memory it streams from)
         "coarse_scan": (N * row, "hbm"),
         "coarse_select": (rows * N * 4, "hbm"),
-        "fine_scan": (union_pages * w.page_size * row, "host" if tier == "host" else "hbm"),
+        # Pruned (host tier): pass A, threshold, page bounds and pass B
+        # together; the bytes are the slices read.
+        "fine_scan": (scanned_slices * w.page_size * w.head_dim * b, "host" if tier == "host" else "hbm"),
         "fine_select": (cand * 4, "hbm"),
         # Host and split tiers: only V of the selected rows crosses the host
         # link (the host tier takes K from the fine scan's HBM staging, the
-        # split tier keeps K in HBM).  The fused step's gather launch also
+        # split tier keeps K in HBM; a pruned scan leaves a selected token's
+        # K rows of skipped slices to be read from the host, at most P rows
+        # per kv head, not counted here).  The fused step's gather launch also
         # runs the hot-window attention splits, which read the hot K/V from
         # HBM; they are not host-link bytes.
         "gather": ((2 if tier == "hbm" else 1) * P * row, "hbm" if tier == "hbm" else "host"),
@@ -583,7 +592,7 @@ def main():
     if args.profile_pass:
         profile_pass(w, args, dev, scrub)
         return
-    extra = 3 * (args.steps + args.warmup) + 1024
+    extra = 4 * (args.steps + args.warmup) + 1024
     results = {}
     tiers = [args.cold_tier] + ([] if args.no_variant else [t for t in ("host", "hbm", "split")
                                                              if t != args.cold_tier])
@@ -599,7 +608,8 @@ def main():
         print(f"[bench] {tier} ({args.cache} caches): {us:.1f} us/step (wall {wall:.1f})", file=sys.stderr,
               flush=True)
         stages = profile_steps(store, cfg, q, hot_k, hot_v, args.steps, w.scaling, scrub)
-        entry = {"us_per_step": us, "wall_us_per_step": wall, "stages": stages}
+        slices = store.fine_scan_stats()  # the last step's (scanned, union) page slices
+        entry = {"us_per_step": us, "wall_us_per_step": wall, "stages": stages, "fine_scan_slices": slices}
         if tier == args.cold_tier and scrub is not None and not args.no_variant:
             warm_us, _ = time_steps(store, cfg, q, hot_k, hot_v, args.steps, 0, w.scaling, None)
             entry["warm_us_per_step"] = warm_us
@@ -609,10 +619,15 @@ def main():
             entry["two_call"] = {"us_per_step": round(two_us, 2),
                                  "stages_us": {k: round(v["avg_us"], 2) for k, v in two_stages.items()}}
             print(f"[bench] {tier} (retrieve, then attention): {two_us:.1f} us/step", file=sys.stderr, flush=True)
+            if tier == "host" and cfg.fine_pruning:
+                full_us, _ = time_steps(store, replace(cfg, fine_pruning=False), q, hot_k, hot_v, args.steps, 0,
+                                        w.scaling, scrub)
+                entry["unpruned_us_per_step"] = full_us
+                print(f"[bench] {tier} (fine scan not pruned): {full_us:.1f} us/step", file=sys.stderr, flush=True)
         snap = store.telemetry_snapshot()
         unions = [r["num_pages_selected"] for r in snap["recent"] if r["kind"] == "coarse" and not r["skipped"]]
         entry["union_pages"] = int(round(sum(unions) / len(unions))) if unions else 0
-        entry["traffic"] = roofline_and_links(w, store, stages, entry["union_pages"], tier)
+        entry["traffic"] = roofline_and_links(w, store, stages, entry["union_pages"], tier, slices[0])
         entry["num_pages"] = store.num_pages
         results[tier] = entry
         del store
@@ -647,12 +662,15 @@ def main():
                                     "read_256MiB": ceil["host_link_256MiB"]},
                      "frac_of_achievable": round(gbs / ceil["host_link_fine_size"], 4)}
     variants = {t: {"us_per_step": round(r["us_per_step"], 2), "union_pages": r["union_pages"],
+                    "fine_scan_slices": list(r["fine_scan_slices"]),
                     "stages_us": {k: round(v["avg_us"], 2) for k, v in r["stages"].items()}}
                 for t, r in results.items() if t != args.cold_tier}
     if "warm_us_per_step" in head:
         variants["warm_caches"] = {"us_per_step": round(head["warm_us_per_step"], 2)}
     if "two_call" in head:
         variants["two_call"] = head["two_call"]
+    if "unpruned_us_per_step" in head:
+        variants["fine_scan_not_pruned"] = {"us_per_step": round(head["unpruned_us_per_step"], 2)}
     line = {
         "metric": METRIC,
         "value": round(head["us_per_step"], 2),
@@ -669,10 +687,11 @@ def main():
         "config": {"workload": f"{w.name}: one decode layer, Hq={w.num_q_heads} Hkv={w.num_kv_heads} "
                                f"D={w.head_dim}, hot {w.hot}, cold {w.cold}", "batch": 1,
                    "top_pages": w.top_pages, "top_p": w.top_p, "page_size": w.page_size,
-                   "cold_tier": args.cold_tier, "caches": args.cache},
+                   "cold_tier": args.cold_tier, "fine_pruning": True, "caches": args.cache},
         "roofline": roofline,
         "host_link": host_link,
         "union_pages": head["union_pages"],
+        "fine_scan_slices": {"read": head["fine_scan_slices"][0], "union": head["fine_scan_slices"][1]},
         "stages_us": {k: round(v["avg_us"], 2) for k, v in head["stages"].items()},
         "wall_us_per_step": round(head["wall_us_per_step"], 2),
         "probes_GB_s": ceil,

@@ -78,6 +78,15 @@ typedef struct {
   int64_t reserved_bytes;/* everything the store holds, host + device */
 } kiv_store_info_t;
 
+/* Retrieval flags.  KIV_RETRIEVE_PRUNE: on the host tier, the fine scan
+ * first scores the pages at the head of the rows' lists, then skips every
+ * other union page whose tokens provably cannot reach the top P' (a bound
+ * from the page's mean and radius).  The selection, its order and the
+ * returned rows are unchanged; the fine telemetry's mean then covers the
+ * scored candidates only.  Applies to one-pass queries whose fine scan runs
+ * on the vector units (G * Q < 32) with a positive scaling. */
+enum { KIV_RETRIEVE_PRUNE = 1 };
+
 /* Arguments of one retrieval: coarse page scan, union of per-row top
  * pages, fine per-token scoring, top-P and K/V gather. */
 typedef struct {
@@ -88,7 +97,7 @@ typedef struct {
   int32_t top_pages;     /* pages kept per (b, q head, q position) */
   int32_t out_width;     /* P' = min(top_p, cold_length, candidates) */
   int32_t reuse_candidates; /* 1: skip the coarse pass, reuse the last union */
-  int32_t _pad;
+  int32_t flags;         /* KIV_RETRIEVE_* bits */
   void *k_out;           /* [B, Hkv, P', D] contiguous, score-descending */
   void *v_out;           /* [B, Hkv, P', D] contiguous */
   int64_t *idx_out;      /* [B, P'] global cold token ids, or NULL */
@@ -192,6 +201,13 @@ enum {
 };
 int kiv_profile_enable(kiv_store_t *store, int enable);
 int kiv_profile_read(kiv_store_t *store, int64_t counts[KIV_NUM_STAGES], double total_ms[KIV_NUM_STAGES]);
+
+/* Fine-scan reads of the last retrieval (no counterpart in the reference;
+ * used by benchmarks to count host-link bytes): the (union page, kv row)
+ * slices whose K rows the fine scan read, of U * B * Hkv.  The two are
+ * equal unless the scan was pruned (KIV_RETRIEVE_PRUNE).  Synchronises the
+ * device; KIV_ERR_STATE when no retrieval ran since the last eviction. */
+int kiv_fine_scan_stats(kiv_store_t *store, int64_t *scanned_slices, int64_t *union_slices);
 
 /* Read-bandwidth probe (no reference counterpart; gives measured ceilings
  * for the retrieval kernels' bandwidth figures).  Allocates `bytes` of HBM

@@ -22,6 +22,7 @@ DTYPE_F32, DTYPE_F16, DTYPE_BF16 = 0, 1, 2
 TIER_HOST, TIER_HBM, TIER_SPLIT = 0, 1, 2
 ROUND_ACTIVATION, ROUND_FP32 = 0, 1
 MASK_NONE, MASK_BOOL, MASK_F32, MASK_F16, MASK_BF16, MASK_CAUSAL = 0, 1, 2, 3, 4, 5
+RETRIEVE_PRUNE = 1
 STAGES = ("evict_append", "evict_finalize", "coarse_scan", "coarse_select", "fine_scan", "fine_select",
           "gather", "attend")
 
@@ -49,7 +50,7 @@ class RetrieveArgs(C.Structure):
     _fields_ = [
         ("q", C.c_void_p), ("q_stride", _I64x4), ("q_len", C.c_int32), ("scaling", C.c_float),
         ("top_pages", C.c_int32), ("out_width", C.c_int32), ("reuse_candidates", C.c_int32),
-        ("_pad", C.c_int32), ("k_out", C.c_void_p), ("v_out", C.c_void_p), ("idx_out", C.c_void_p),
+        ("flags", C.c_int32), ("k_out", C.c_void_p), ("v_out", C.c_void_p), ("idx_out", C.c_void_p),
         ("pages_out", C.c_void_p), ("union_count_out", C.c_void_p), ("stats_out", C.c_void_p),
         ("stats_accum", C.c_void_p),
     ]
@@ -79,6 +80,7 @@ SIGNATURES = {
     "kiv_evict": (C.c_int, [C.c_void_p, C.c_void_p, _I64x3, C.c_void_p, _I64x3, C.c_int64, C.c_void_p]),
     "kiv_max_union_pages": (C.c_int, [C.c_void_p, C.c_int32, C.c_int32, C.POINTER(C.c_int64)]),
     "kiv_retrieve": (C.c_int, [C.c_void_p, C.POINTER(RetrieveArgs), C.c_void_p]),
+    "kiv_fine_scan_stats": (C.c_int, [C.c_void_p, C.POINTER(C.c_int64), C.POINTER(C.c_int64)]),
     "kiv_store_read_summaries": (C.c_int, [C.c_void_p, C.c_int64, C.c_int64, C.c_void_p, C.c_void_p,
                                            C.c_void_p]),
     "kiv_store_read_tokens": (C.c_int, [C.c_void_p, C.c_int64, C.c_int64, C.c_void_p, C.c_void_p,

@@ -232,6 +232,7 @@ class ColdKVStore:
         args = nat.RetrieveArgs(
             q=q.data_ptr(), q_stride=nat.strides(q, 4), q_len=Q, scaling=float(scaling),
             top_pages=int(kiv_config.top_pages), out_width=int(width), reuse_candidates=1 if reuse else 0,
+            flags=nat.RETRIEVE_PRUNE if getattr(kiv_config, "fine_pruning", True) else 0,
             k_out=k_out.data_ptr(), v_out=v_out.data_ptr(), idx_out=idx_out.data_ptr(),
             pages_out=nat.ptr(pages_out), union_count_out=nat.ptr(union_count),
             stats_out=stats.data_ptr(), stats_accum=accum.data_ptr(),
@@ -304,6 +305,14 @@ class ColdKVStore:
         return out
 
     # ------------------------------------------------- inspection (tests)
+    def fine_scan_stats(self) -> tuple[int, int]:
+        """(page slices the last retrieval's fine scan read, union page slices);
+        a slice is one kv row of one union page.  Synchronises the device."""
+        scanned, total = C.c_int64(), C.c_int64()
+        nat.check(nat.lib().kiv_fine_scan_stats(self._handle, C.byref(scanned), C.byref(total)),
+                  "kiv_fine_scan_stats")
+        return scanned.value, total.value
+
     def read_summaries(self) -> tuple[torch.Tensor, torch.Tensor]:
         """(dtype summaries, fp32 means), each [N, B, Hkv, D], copied from HBM."""
         N = self.num_pages

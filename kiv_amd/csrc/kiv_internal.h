@@ -78,8 +78,9 @@ struct kiv_store {
   int64_t num_pages = 0;    // finished pages
   int64_t partial_len = 0;  // tokens in the partial page
 
-  // Page summaries in HBM: [cap][kr][D] dtype and fp32.
-  kiv::DevBuf summ, summ32;
+  // Page summaries in HBM: [cap][kr][D] dtype and fp32, and each page row's
+  // radius [cap][kr] fp32: max over its tokens of |k - summ32| (L2).
+  kiv::DevBuf summ, summ32, radius;
   int64_t summ_cap = 0;
 
   // Arena of finished pages: equal chunks of 2^chunk_shift pages.
@@ -102,6 +103,8 @@ struct kiv_store {
   kiv::DevBuf fine_keys;     // [B][ld] u32
   kiv::DevBuf sel_list;      // [B][list_ld] u64 top-P' candidates + [B] i32 counts
   kiv::DevBuf k_stage;       // [B*Hkv][ld][D] candidates' K rows (host tier)
+  kiv::DevBuf prune;         // [B*Hkv][ld] u8 union page states of a pruned fine scan + [B] u32 thresholds
+  int64_t prune_state_ld = 0;  // state row stride of the last fine scan if it was pruned, else 0
   bool union_valid = false;  // page_list / U hold the last coarse pass
   int64_t union_rows = 0;    // B*Hq*Q of that pass (bounds reuse)
   int64_t union_max = 0;     // grid bound of that pass

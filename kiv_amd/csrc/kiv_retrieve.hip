@@ -25,6 +25,7 @@
 // kernel uses device-scope atomics.
 #include <algorithm>
 #include <type_traits>
+#include <vector>
 
 #include "kiv_attn_device.h"
 #include "kiv_common.h"
@@ -68,6 +69,7 @@ template <int NT> struct SelSh {
   int ncand, nsel;
   uint32_t band[2], bor[2];
   float fmax[NT / 64], fsum[NT / 64];
+  int fcnt[NT / 64];
   int scan_tmp[NT / 64];
   uint32_t wave_bound[NT / 64];  // per-wave lower bounds of the k-th largest key
 };
@@ -313,17 +315,23 @@ template <int NT> struct MemKeys4 {
 // places each candidate at its step's offset plus its rank in the ballot.
 // (A lane whose entries run out never gets more, so lane 0 sees every
 // step.)  Also leaves the row's max and sum of scores (as floats) in mx /
-// sum.
+// sum and the number of scored entries in nz: a zero key is an entry that
+// was not scored (a pruned fine scan leaves them) and is not summed.
 template <int NT, typename Src>
-__device__ int bound_candidates(const Src &src, int k, SelSh<NT> &sh, uint64_t *cand, float &mx, float &sum) {
+__device__ int bound_candidates(const Src &src, int k, SelSh<NT> &sh, uint64_t *cand, float &mx, float &sum,
+                                int &nz) {
   constexpr int W = NT / 64;
   const int tid = threadIdx.x, wave = tid >> 6;
   uint32_t m[4] = {0u, 0u, 0u, 0u};
   float fs = 0.f;
+  int fc = 0;
   src.each_slot([&](uint64_t x, int j) {
     const uint32_t key = comp_key(x);
     m[j] = max(m[j], key);
-    fs += key_to_float(key);
+    if (key) {
+      fs += key_to_float(key);
+      ++fc;
+    }
   });
   const int kw = (k + W - 1) / W;
   int have = 0;
@@ -333,19 +341,23 @@ __device__ int bound_candidates(const Src &src, int k, SelSh<NT> &sh, uint64_t *
   const uint32_t top = max(max(m[0], m[1]), max(m[2], m[3]));
   float fm = have ? key_to_float(wave_max_u32(top)) : -INFINITY;
   fs = wave_sum(fs);
+  fc = wave_sum_i32(fc);
   if ((tid & 63) == 0) {
     sh.fmax[wave] = fm;
     sh.fsum[wave] = fs;
+    sh.fcnt[wave] = fc;
     sh.wave_bound[wave] = bw;
   }
   __syncthreads();
   mx = sh.fmax[0];
   sum = 0.f;
+  nz = 0;
   uint32_t bound = sh.wave_bound[0];
 #pragma unroll
   for (int w = 0; w < W; ++w) {
     mx = fmaxf(mx, sh.fmax[w]);
     sum += sh.fsum[w];
+    nz += sh.fcnt[w];
     bound = min(bound, sh.wave_bound[w]);
   }
   int total = 0;
@@ -761,13 +773,13 @@ __global__ void __launch_bounds__(NT) coarse_select_kernel(const uint32_t *__res
   int32_t *out = row_pages + (int64_t)row * k;
   const MemKeys4<NT> mk{src, n};
   float mx, sum;
-  int C;
+  int C, nz;
   if (n <= 4 * V * NT) {
     RegKeys4<NT, V> rk;
     rk.load(src, n);
-    C = bound_candidates<NT>(rk, k, sh, cand, mx, sum);
+    C = bound_candidates<NT>(rk, k, sh, cand, mx, sum, nz);
   } else {
-    C = bound_candidates<NT>(mk, k, sh, cand, mx, sum);
+    C = bound_candidates<NT>(mk, k, sh, cand, mx, sum, nz);
   }
   if (C <= kRankCap)
     rank_candidates<NT>(cand, C, k, [&](uint64_t x, int r) { out[r] = comp_index(x); });
@@ -840,6 +852,24 @@ __device__ void publish_union(const uint32_t *ubits, const int *urank, int words
   }
 }
 
+// Exact pruning of a host-tier fine scan (one query pass, VALU scan).
+// Pass A (mode 1) scores set A, the pages among the first `a` entries of
+// any row's list, and the partial page, and sets state[r][v] of every
+// union page to 1 (in A) or 0; fine_threshold_kernel then takes a lower
+// bound T of each batch row's P'-th largest key from these scores,
+// fine_bound_kernel sets state 2 (score) or 3 (skip) for the other pages
+// from a bound on their tokens' scores, and pass B (mode 2) scores the
+// state-2 pages.  A token whose key (max over kv rows) reaches T gets it
+// from a kv row whose page bound reaches T, so every key >= T is exact and
+// every other one stays below T: the top P' and its order are unchanged.
+struct FinePrune {
+  int mode;                  // 0: no pruning, 1: pass A, 2: pass B
+  const int32_t *row_pages;  // [rows][kc] per-row page lists of the coarse select
+  int rows, kc, a, words;    // a: list entries per row in set A; words = ceil(N / 32)
+  uint8_t *state;            // [B*Hkv][state_ld] per union page
+  int64_t state_ld;
+};
+
 template <int DT, int LG>
 __global__ void __launch_bounds__(256) fine_scan_kernel(
     int union_src, const int32_t *__restrict__ row_pages, int row_pages_n, int words, int32_t *page_list,
@@ -848,7 +878,8 @@ __global__ void __launch_bounds__(256) fine_scan_kernel(
     int partial_len, int page_size, int tpi, int hkv, int head_dim, const char *__restrict__ q, int64_t qs0,
     int64_t qs1, int64_t qs2, int hq, int qlen, float scale, int round, uint32_t *__restrict__ out, int64_t ld,
     const float *__restrict__ coarse_stats, int rows, int n_pages, int32_t *pages_out, int32_t *union_out,
-    float *stats_out, double *stats_accum, char *__restrict__ k_stage, const char *__restrict__ k_read) {
+    float *stats_out, double *stats_accum, char *__restrict__ k_stage, const char *__restrict__ k_read,
+    FinePrune pr) {
   constexpr int VEC = Elem<DT>::VEC, EB = Elem<DT>::BYTES;
   constexpr int UT = kFineUT;
   constexpr int NSLOT = 256 / LG;
@@ -859,7 +890,16 @@ __global__ void __launch_bounds__(256) fine_scan_kernel(
   char *qraw = reinterpret_cast<char *>(smem4);  // [G*Q][D] dtype
   uint32_t *ubits = reinterpret_cast<uint32_t *>(qraw + (size_t)GQ * head_dim * EB);
   int *urank = reinterpret_cast<int *>(ubits + words);
+  uint32_t *abits = reinterpret_cast<uint32_t *>(urank + words + 1);  // set A (pass A)
   const int tid = threadIdx.x;
+  if (pr.mode == 1) {
+    for (int w = tid; w < pr.words; w += 256) abits[w] = 0u;
+    __syncthreads();
+    for (int i = tid; i < pr.rows * pr.a; i += 256) {
+      const int page = pr.row_pages[(int64_t)(i / pr.a) * pr.kc + i % pr.a];
+      atomicOr(&abits[page >> 5], 1u << (page & 31));
+    }
+  }
   for (int i = tid; i < GQ * cpr; i += 256) {
     const int j = i / cpr, c = i % cpr;
     const int h = kvh * G + j / qlen, qp = j % qlen;
@@ -878,7 +918,7 @@ __global__ void __launch_bounds__(256) fine_scan_kernel(
   __syncthreads();
   const int nsplit = (page_size + tpi - 1) / tpi;
   const int page_items = U * nsplit;
-  const int items = page_items + (partial_len + tpi - 1) / tpi;
+  const int items = page_items + (pr.mode == 2 ? 0 : (partial_len + tpi - 1) / tpi);
   const int slot = tid / LG, lane = tid % LG;
   const bool on = lane < cpr;
   const int64_t row_bytes = (int64_t)head_dim * EB;
@@ -888,7 +928,13 @@ __global__ void __launch_bounds__(256) fine_scan_kernel(
     int ntok;
     if (item < page_items) {
       const int v = item / nsplit, s = item % nsplit;
+      if (pr.mode == 2 && pr.state[(int64_t)r * pr.state_ld + v] != 2) continue;
       const int64_t page = union_src == UNION_ROWS ? union_page(ubits, urank, words, v) : page_list[v];
+      if (pr.mode == 1) {
+        const bool in_a = (abits[page >> 5] >> (page & 31)) & 1u;
+        if (s == 0 && tid == 0) pr.state[(int64_t)r * pr.state_ld + v] = in_a ? 1 : 0;
+        if (!in_a) continue;
+      }
       rowbase = reinterpret_cast<const char *>(ktab[page >> chunk_shift]) +
                 (page & ((int64_t(1) << chunk_shift) - 1)) * page_bytes +
                 ((int64_t)r * page_size + (int64_t)s * tpi) * row_bytes;
@@ -931,6 +977,104 @@ __global__ void __launch_bounds__(256) fine_scan_kernel(
       }
     }
   }
+}
+
+// Threshold of a pruned fine scan: block b, after pass A, writes thr[b] <=
+// the k-th largest of batch row b's keys (k = min(P', n); unscored keys
+// are zero): the exact k-th when the bound's candidates fit the rank
+// counting, else the smallest of them (they hold the top k), else 0
+// (nothing is pruned).
+template <int V>
+__global__ void __launch_bounds__(kSelThreads) fine_threshold_kernel(const uint32_t *__restrict__ keys, int64_t ld,
+                                                                     const int32_t *__restrict__ counters,
+                                                                     int page_size, int partial_len, int width,
+                                                                     uint32_t *__restrict__ thr) {
+  constexpr int NT = kSelThreads;
+  __shared__ SelSh<NT> sh;
+  __shared__ uint64_t cand[kCandCap];
+  __shared__ uint32_t t_sh;
+  sel_init(sh);
+  const int b = blockIdx.x;
+  const int n = counters[0] * page_size + partial_len;
+  const int k = min(width, n);
+  const uint32_t *row = keys + (int64_t)b * ld;
+  const MemKeys4<NT> mk{row, n};
+  float mx, sum;
+  int C, nz;
+  if (n <= 4 * V * NT) {
+    RegKeys4<NT, V> rk;
+    rk.load(row, n);
+    C = bound_candidates<NT>(rk, k, sh, cand, mx, sum, nz);
+  } else {
+    C = bound_candidates<NT>(mk, k, sh, cand, mx, sum, nz);
+  }
+  if (threadIdx.x == 0) t_sh = (C > kRankCap && C <= kCandCap) ? 0xffffffffu : 0u;
+  __syncthreads();
+  if (C <= kRankCap) {
+    rank_candidates<NT>(cand, C, k, [&](uint64_t x, int rank) {
+      if (rank == k - 1) t_sh = comp_key(x);
+    });
+  } else if (C <= kCandCap) {
+    for (int i = threadIdx.x; i < C; i += NT) atomicMin(&t_sh, comp_key(cand[i]));
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) thr[b] = t_sh;
+}
+
+// Page bound of a pruned fine scan: wave w of block (x, r) takes union page
+// v = 4 x + w of kv row r (batch row b = r / Hkv) unless pass A scored it
+// (state 1) and bounds the dot product of its tokens with each of the row's
+// G*Q query rows: q.k <= q.m + |q| |k - m| <= q.m + |q| rad (Cauchy-Schwarz;
+// m the page row's fp32 mean, rad its radius), plus 1e-4 |q| (|m| + rad),
+// which covers the fp32 rounding of the scan's dot product (at most
+// D 2^-24 |q| |k| for D <= 512) and of this bound.  The dtype rounding and
+// the positive scale of a score are monotone, so a page whose bound's key
+// is below thr[b] gives none of its tokens a key >= thr[b] from this row:
+// state 3 (skip), else state 2 (score in pass B).
+template <int DT>
+__global__ void __launch_bounds__(256) fine_bound_kernel(
+    const int32_t *__restrict__ page_list, const int32_t *__restrict__ counters, const float *__restrict__ summ32,
+    const float *__restrict__ radius, int kr, int head_dim, int hkv, const char *__restrict__ q, int64_t qs0,
+    int64_t qs1, int64_t qs2, int hq, int qlen, float scale, int round, const uint32_t *__restrict__ thr,
+    uint8_t *__restrict__ state, int64_t state_ld) {
+  constexpr int EB = Elem<DT>::BYTES;
+  constexpr int MV = 8;  // dims per lane (D <= 512)
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int v = blockIdx.x * 4 + wave;
+  const int r = blockIdx.y, b = r / hkv, kvh = r % hkv;
+  if (v >= counters[0]) return;
+  uint8_t *st = state + (int64_t)r * state_ld + v;
+  if (*st == 1) return;
+  const int64_t row = (int64_t)page_list[v] * kr + r;
+  const float *m = summ32 + row * head_dim;
+  float mv[MV], mm = 0.f;
+#pragma unroll
+  for (int i = 0; i < MV; ++i) {
+    const int e = lane + 64 * i;
+    mv[i] = e < head_dim ? m[e] : 0.f;
+    mm = fmaf(mv[i], mv[i], mm);
+  }
+  const float mn = sqrtf(wave_sum(mm)), rad = radius[row];
+  const int G = hq / hkv;
+  float best = -INFINITY;
+  for (int j = 0; j < G * qlen; ++j) {
+    const int h = kvh * G + j / qlen, qp = j % qlen;
+    const char *qrow = q + ((int64_t)b * qs0 + (int64_t)h * qs1 + (int64_t)qp * qs2) * EB;
+    float dot = 0.f, qq = 0.f;
+#pragma unroll
+    for (int i = 0; i < MV; ++i) {
+      const int e = lane + 64 * i;
+      if (e < head_dim) {
+        const float x = load_elem<DT>(qrow, e);
+        dot = fmaf(x, mv[i], dot);
+        qq = fmaf(x, x, qq);
+      }
+    }
+    dot = wave_sum(dot);
+    const float qn = sqrtf(wave_sum(qq));
+    best = fmaxf(best, dot + qn * rad * 1.0001f + 1e-4f * qn * (mn + rad));
+  }
+  if (lane == 0) *st = order_key(score_of<DT>(best, scale, round != 0)) >= thr[b] ? 2 : 3;
 }
 
 // MFMA fine scan for queries of many rows (G * Q >= kFineMfmaRows per kv
@@ -1050,8 +1194,10 @@ __global__ void __launch_bounds__(256) fine_scan_mfma_kernel(
 // counting (one wave per entry, over the whole list).  When more than
 // list_cap (<= kCandCap) keys pass the bound, the block lists exactly the k
 // composites >= the k-th largest instead.  The block also
-// writes the row's telemetry (max, sum of scores) and zeroes the keys for
-// the next scan, which accumulates with atomicMax.
+// writes the row's telemetry (max and sum of scores, and the number of
+// scored candidates to list_count[B + b]) and zeroes the keys for the next
+// scan, which accumulates with atomicMax.  Keys a pruned scan skipped are
+// zero; at least k keys are scored, so none of them is listed.
 // V = 16-byte key chunks per thread kept in registers: rows of up to
 // 4 * V * kSelThreads keys are read once; longer rows are re-read.
 template <int V>
@@ -1071,13 +1217,13 @@ __global__ void __launch_bounds__(kSelThreads) fine_select_kernel(
   uint64_t *out = list + (int64_t)b * list_ld;
   const MemKeys4<NT> mk{row, n};
   float mx, sum;
-  int C;
+  int C, nz;
   if (n <= 4 * V * NT) {
     RegKeys4<NT, V> rk;
     rk.load(row, n);
-    C = bound_candidates<NT>(rk, k, sh, cand, mx, sum);
+    C = bound_candidates<NT>(rk, k, sh, cand, mx, sum, nz);
   } else {
-    C = bound_candidates<NT>(mk, k, sh, cand, mx, sum);
+    C = bound_candidates<NT>(mk, k, sh, cand, mx, sum, nz);
   }
   if (C <= list_cap) {
     for (int i = threadIdx.x; i < C; i += NT) out[i] = cand[i];
@@ -1092,6 +1238,7 @@ __global__ void __launch_bounds__(kSelThreads) fine_select_kernel(
     fine_stats[2 * b] = mx;
     fine_stats[2 * b + 1] = sum;
     list_count[b] = C;
+    list_count[gridDim.x + b] = nz;
   }
 }
 
@@ -1116,6 +1263,8 @@ struct GatherArgs {
   int64_t page_bytes;
   const char *part_k, *part_v, *k_stage;
   int64_t stage_ld;
+  const uint8_t *state;  // pruned fine scan: union page states (1, 2: K rows staged), or NULL
+  int64_t state_ld;
   int page_size, partial_len;
   int64_t num_finalized;
   int batch, hkv, head_dim, width, cpr;
@@ -1153,11 +1302,13 @@ template <int DT> __device__ void gather_block(const GatherArgs &ga, int bx, int
     if (tid == 0) {
       float m = -INFINITY;
       double t = 0.0;
+      int64_t scored = 0;  // every candidate, unless the fine scan was pruned
       for (int r = 0; r < batch; ++r) {
         m = fmaxf(m, fine_stats[2 * r]);
         t += fine_stats[2 * r + 1];
+        scored += list_count[batch + r];
       }
-      float mean = (float)(t / ((double)batch * (double)n));
+      float mean = (float)(t / (double)scored);
       if (round) mean = round_act<DT>(mean);
       if (stats_out) {
         stats_out[2] = m;
@@ -1217,7 +1368,9 @@ template <int DT> __device__ void gather_block(const GatherArgs &ga, int bx, int
       vs = part_v + off;
       gid = num_finalized + t;
     }
-    if (k_stage) ks = k_stage + (((int64_t)r * stage_ld + cand) * head_dim + e0) * EB;
+    const bool staged = k_stage && (cand >= split || !ga.state ||
+                                    (unsigned)(ga.state[(int64_t)r * ga.state_ld + cand / page_size] - 1) < 2u);
+    if (staged) ks = k_stage + (((int64_t)r * stage_ld + cand) * head_dim + e0) * EB;
     const int64_t o = (((int64_t)r * width + slot) * head_dim + e0) * EB;
     const uint4 kx = load16(ks), vx = load16(vs);
     *reinterpret_cast<uint4 *>(k_out + o) = kx;
@@ -1424,17 +1577,20 @@ static int retrieve_impl(kiv_store_t *s, const kiv_retrieve_args_t *a, hipStream
     if ((rc = s->fine_keys.ensure((size_t)B * ldc * 4, st, false))) return rc;
     KIV_HIP(hipMemsetAsync(s->fine_keys.ptr, 0, s->fine_keys.bytes, st));
   }
-  // Candidate lists of the fine select: [B][list_ld] composites, then [B] counts.
+  // Candidate lists of the fine select: [B][list_ld] composites, then [B]
+  // counts and [B] numbers of scored candidates.
   const int list_cap = fine_list_cap(a->out_width);
   const int64_t lmax = std::min<int64_t>(cmax, std::max<int64_t>(list_cap, a->out_width));
   const int64_t list_ld = (std::max<int64_t>(list_cap, a->out_width) + 31) & ~int64_t(31);
-  if ((rc = s->sel_list.ensure((size_t)B * list_ld * 8 + (size_t)B * 4, st, false))) return rc;
+  if ((rc = s->sel_list.ensure((size_t)B * list_ld * 8 + (size_t)B * 8, st, false))) return rc;
   uint64_t *list = (uint64_t *)s->sel_list.ptr;
   int32_t *list_count = (int32_t *)(list + (size_t)B * list_ld);
   const int bwords = union_src == UNION_ROWS ? words : 0;
   // Host tier: the fine scan copies the candidates' K rows to HBM as it
   // streams them, so the gather reads only V over the host link (up to
   // kMaxStageBytes of staging per store).
+  const uint8_t *pr_state = nullptr;  // union page states of a pruned fine scan
+  int64_t pr_state_ld = 0;
   char *k_stage = nullptr;
   const size_t stage_bytes = (size_t)s->kr * ldc * s->row_bytes;
   if (c.cold_tier == KIV_TIER_HOST && stage_bytes <= kMaxStageBytes) {
@@ -1504,27 +1660,77 @@ static int retrieve_impl(kiv_store_t *s, const kiv_retrieve_args_t *a, hipStream
       if (rc) return rc;
       KIV_HIP(hipGetLastError());
     }
-    for (int pass = 0; pass < passes && !mfma; ++pass) {
+    // Exact pruning (KIV_RETRIEVE_PRUNE, see FinePrune): set A is the first
+    // ceil(P' / page_size) entries of every row's list, which hold the
+    // rows' best pages, so that pass A's P'-th largest key is close to the
+    // final one.
+    const int pa = std::min(kc, std::max(1, (a->out_width + ps - 1) / ps));
+    const bool prune = (a->flags & KIV_RETRIEVE_PRUNE) && host_tier && k_stage && !mfma && passes == 1 &&
+                       kc > 0 && pa < kc && a->scaling > 0.f;
+    FinePrune pr{};
+    uint32_t *thr = nullptr;
+    s->prune_state_ld = 0;
+    if (prune) {
+      pr.state_ld = (umax + 15) & ~int64_t(15);
+      const size_t state_bytes = ((size_t)s->kr * pr.state_ld + 255) & ~size_t(255);
+      if ((rc = s->prune.ensure(state_bytes + (size_t)B * 4, st, false))) return rc;
+      pr.mode = 1;
+      pr.row_pages = (const int32_t *)s->row_pages.ptr;
+      pr.rows = rows;
+      pr.kc = kc;
+      pr.a = pa;
+      pr.words = words;
+      pr.state = (uint8_t *)s->prune.ptr;
+      thr = (uint32_t *)((char *)s->prune.ptr + state_bytes);
+      pr_state = pr.state;
+      pr_state_ld = pr.state_ld;
+      s->prune_state_ld = pr.state_ld;
+    }
+    auto valu_scan = [&](int pass, int usrc, int bw, const FinePrune &fp) {
       const int Qp = std::min(Qb, Q - pass * Qb);
-      const size_t lds = (size_t)G * Qp * D * eb + (size_t)bwords * 4 + (size_t)(bwords + 1) * 4;
-      s->prof_begin(KIV_STAGE_FINE_SCAN, st);
-      rc = with_dt_lg(dt, lg, [&](auto dtc, auto lgc) {
+      const size_t lds = (size_t)G * Qp * D * eb + (size_t)bw * 4 + (size_t)(bw + 1) * 4 +
+                         (fp.mode == 1 ? (size_t)fp.words * 4 : 0);
+      return with_dt_lg(dt, lg, [&](auto dtc, auto lgc) {
         auto kern = fine_scan_kernel<decltype(dtc)::value, decltype(lgc)::value>;
         if (lds > 65536)
           KIV_HIP(hipFuncSetAttribute((const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
-        hipLaunchKernelGGL(kern, dim3((unsigned)nb, (unsigned)s->kr), dim3(256), lds, st, union_src,
-                           (const int32_t *)s->row_pages.ptr, rows * kc, bwords, (int32_t *)s->page_list.ptr,
+        hipLaunchKernelGGL(kern, dim3((unsigned)nb, (unsigned)s->kr), dim3(256), lds, st, usrc,
+                           (const int32_t *)s->row_pages.ptr, rows * kc, bw, (int32_t *)s->page_list.ptr,
                            (int32_t *)s->counters.ptr, (const uint64_t *)s->k_tab.ptr, s->chunk_shift,
                            s->page_bytes, (const char *)s->k_part.ptr, (int)s->partial_len, ps, tpi, hkv, D,
                            (const char *)a->q + pass * qstep, a->q_stride[0], a->q_stride[1], a->q_stride[2], hq,
                            Qp, a->scaling, round, (uint32_t *)s->fine_keys.ptr, ldc, (const float *)coarse_stats,
                            rows, N, a->pages_out, a->union_count_out, a->stats_out, a->stats_accum,
-                           pass == 0 ? k_stage : nullptr, pass == 0 ? nullptr : k_stage);
+                           pass == 0 ? k_stage : nullptr, pass == 0 ? nullptr : k_stage, fp);
+        KIV_HIP(hipGetLastError());
         return (int)KIV_OK;
       });
+    };
+    for (int pass = 0; pass < passes && !mfma; ++pass) {
+      s->prof_begin(KIV_STAGE_FINE_SCAN, st);
+      if ((rc = valu_scan(pass, union_src, bwords, pr))) return rc;
+      if (prune) {
+        // Pass A's threshold per batch row, the other pages' bounds, pass B.
+        with_select_chunks(cmax, [&](auto kern) {
+          hipLaunchKernelGGL(kern, dim3(B), dim3(kSelThreads), 0, st, (const uint32_t *)s->fine_keys.ptr, ldc,
+                             (const int32_t *)s->counters.ptr, ps, (int)s->partial_len, a->out_width, thr);
+        }, [](auto vc) { return fine_threshold_kernel<decltype(vc)::value>; });
+        KIV_HIP(hipGetLastError());
+        rc = with_dt(dt, [&](auto dtc) {
+          hipLaunchKernelGGL((fine_bound_kernel<decltype(dtc)::value>), dim3((unsigned)((umax + 3) / 4), s->kr),
+                             dim3(256), 0, st, (const int32_t *)s->page_list.ptr, (const int32_t *)s->counters.ptr,
+                             (const float *)s->summ32.ptr, (const float *)s->radius.ptr, s->kr, D, hkv,
+                             (const char *)a->q, a->q_stride[0], a->q_stride[1], a->q_stride[2], hq, Q,
+                             a->scaling, round, (const uint32_t *)thr, pr.state, pr.state_ld);
+          return (int)KIV_OK;
+        });
+        if (rc) return rc;
+        KIV_HIP(hipGetLastError());
+        FinePrune pb = pr;
+        pb.mode = 2;
+        if ((rc = valu_scan(pass, UNION_LIST, 0, pb))) return rc;
+      }
       s->prof_end(KIV_STAGE_FINE_SCAN, st);
-      if (rc) return rc;
-      KIV_HIP(hipGetLastError());
     }
   }
   {
@@ -1554,6 +1760,8 @@ static int retrieve_impl(kiv_store_t *s, const kiv_retrieve_args_t *a, hipStream
     ga.part_v = (const char *)s->v_part.ptr;
     ga.k_stage = k_stage;
     ga.stage_ld = ldc;
+    ga.state = pr_state;
+    ga.state_ld = pr_state_ld;
     ga.page_size = ps;
     ga.partial_len = (int)s->partial_len;
     ga.num_finalized = s->num_pages * ps;
@@ -1596,6 +1804,29 @@ static int retrieve_impl(kiv_store_t *s, const kiv_retrieve_args_t *a, hipStream
     s->prof_end(KIV_STAGE_GATHER, st);
     if (rc) return rc;
     KIV_HIP(hipGetLastError());
+  }
+  return KIV_OK;
+}
+
+int kiv_fine_scan_stats(kiv_store_t *s, int64_t *scanned_slices, int64_t *union_slices) {
+  if (!s || !scanned_slices || !union_slices) return fail(KIV_ERR_INVALID, "kiv_fine_scan_stats: null argument");
+  if (!s->union_valid) return fail(KIV_ERR_STATE, "kiv_fine_scan_stats: no retrieval since the last eviction");
+  DeviceGuard guard(s->device);
+  KIV_HIP(hipDeviceSynchronize());
+  int32_t U = 0;
+  KIV_HIP(hipMemcpy(&U, s->counters.ptr, sizeof(U), hipMemcpyDeviceToHost));
+  *union_slices = (int64_t)U * s->kr;
+  *scanned_slices = *union_slices;
+  if (s->prune_state_ld > 0) {
+    std::vector<uint8_t> st((size_t)s->kr * s->prune_state_ld);
+    KIV_HIP(hipMemcpy(st.data(), s->prune.ptr, st.size(), hipMemcpyDeviceToHost));
+    int64_t n = 0;
+    for (int r = 0; r < s->kr; ++r)
+      for (int v = 0; v < U; ++v) {
+        const uint8_t x = st[(size_t)r * s->prune_state_ld + v];
+        n += x == 1 || x == 2;
+      }
+    *scanned_slices = n;
   }
   return KIV_OK;
 }

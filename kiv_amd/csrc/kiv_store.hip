@@ -123,9 +123,10 @@ __global__ void __launch_bounds__(256) evict_finalize_kernel(
     int64_t ks2, int64_t vs0, int64_t vs1, int64_t vs2, int hkv, int kr, int head_dim,
     int page_size, int64_t first_page, const uint64_t *__restrict__ ktab,
     const uint64_t *__restrict__ vtab, int chunk_shift, int64_t page_bytes, void *__restrict__ summ,
-    float *__restrict__ summ32) {
+    float *__restrict__ summ32, float *__restrict__ radius) {
   constexpr int VEC = Elem<DT>::VEC, EB = Elem<DT>::BYTES;
   __shared__ double red[256 * VEC];
+  __shared__ float mu[512], part[256], gmax[256];
   const int j = blockIdx.x, r = blockIdx.y;
   const int b = r / hkv, h = r % hkv;
   const int cpr = head_dim / VEC;
@@ -137,23 +138,25 @@ __global__ void __launch_bounds__(256) evict_finalize_kernel(
   char *kdst = reinterpret_cast<char *>(ktab[page >> chunk_shift]) + in_chunk * page_bytes + row_off;
   char *vdst = reinterpret_cast<char *>(vtab[page >> chunk_shift]) + in_chunk * page_bytes + row_off;
 
+  // Token t of the page: K / V chunk c in the partial page or the input.
+  auto src_k = [&](int t) -> const char * {
+    const int64_t i = (int64_t)j * page_size + t;
+    if (i < p0) return part_k + (((int64_t)r * page_size + i) * head_dim + (int64_t)c * VEC) * EB;
+    return in_k + ((int64_t)b * ks0 + (int64_t)h * ks1 + (i - p0) * ks2 + (int64_t)c * VEC) * EB;
+  };
+  auto src_v = [&](int t) -> const char * {
+    const int64_t i = (int64_t)j * page_size + t;
+    if (i < p0) return part_v + (((int64_t)r * page_size + i) * head_dim + (int64_t)c * VEC) * EB;
+    return in_v + ((int64_t)b * vs0 + (int64_t)h * vs1 + (i - p0) * vs2 + (int64_t)c * VEC) * EB;
+  };
+
   double acc[VEC];
 #pragma unroll
   for (int e = 0; e < VEC; ++e) acc[e] = 0.0;
   if (g < groups) {
     for (int t = g; t < page_size; t += groups) {
-      const int64_t i = (int64_t)j * page_size + t;
-      const char *ks;
-      const char *vs;
-      if (i < p0) {
-        const int64_t off = (((int64_t)r * page_size + i) * head_dim + (int64_t)c * VEC) * EB;
-        ks = part_k + off;
-        vs = part_v + off;
-      } else {
-        const int64_t ti = i - p0;
-        ks = in_k + ((int64_t)b * ks0 + (int64_t)h * ks1 + ti * ks2 + (int64_t)c * VEC) * EB;
-        vs = in_v + ((int64_t)b * vs0 + (int64_t)h * vs1 + ti * vs2 + (int64_t)c * VEC) * EB;
-      }
+      const char *ks = src_k(t);
+      const char *vs = src_v(t);
       const uint4 kq = *reinterpret_cast<const uint4 *>(ks);
       const uint4 vq = *reinterpret_cast<const uint4 *>(vs);
       const int64_t doff = ((int64_t)t * head_dim + (int64_t)c * VEC) * EB;
@@ -175,6 +178,41 @@ __global__ void __launch_bounds__(256) evict_finalize_kernel(
     const int64_t o = ((int64_t)page * kr + r) * head_dim + d;
     summ32[o] = m32;
     store_elem<DT>(summ, o, m32);
+    mu[d] = m32;
+  }
+  __syncthreads();
+  // Radius: max over the page's tokens of |k - mean| in fp32, the tokens'
+  // squared distances summed over their chunks in LDS, one token per group
+  // and round.  (Its rounding is covered by the relative margin of the
+  // retrieval's page bound.)
+  float rmax = 0.f;
+  for (int t0 = 0; t0 < page_size; t0 += groups) {
+    const int t = t0 + g;
+    float ss = 0.f;
+    if (g < groups && t < page_size) {
+      float x[VEC];
+      load_chunk<DT>(reinterpret_cast<const uint4 *>(src_k(t)), x);
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) {
+        const float dx = x[e] - mu[c * VEC + e];
+        ss = fmaf(dx, dx, ss);
+      }
+    }
+    part[threadIdx.x] = ss;
+    __syncthreads();
+    if (g < groups && c == 0 && t < page_size) {
+      float tot = 0.f;
+      for (int cc = 0; cc < cpr; ++cc) tot += part[g * cpr + cc];
+      rmax = fmaxf(rmax, tot);
+    }
+    __syncthreads();
+  }
+  if (g < groups && c == 0) gmax[g] = rmax;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    float m = 0.f;
+    for (int gg = 0; gg < groups; ++gg) m = fmaxf(m, gmax[gg]);
+    radius[page * kr + r] = sqrtf(m);
   }
 }
 
@@ -279,6 +317,8 @@ static int ensure_summaries(kiv_store *s, int64_t pages, hipStream_t st) {
   if (rc) return rc;
   rc = s->summ32.ensure(cap * row * 4, st, true);
   if (rc) return rc;
+  rc = s->radius.ensure(cap * s->kr * 4, st, true);
+  if (rc) return rc;
   s->summ_cap = cap;
   return KIV_OK;
 }
@@ -307,9 +347,9 @@ int64_t kiv_store::reserved_host_bytes() const {
 }
 
 int64_t kiv_store::reserved_device_bytes() const {
-  int64_t d = (int64_t)(summ.bytes + summ32.bytes + k_tab.bytes + v_tab.bytes + k_part.bytes +
+  int64_t d = (int64_t)(summ.bytes + summ32.bytes + radius.bytes + k_tab.bytes + v_tab.bytes + k_part.bytes +
                         v_part.bytes + coarse_keys.bytes + row_stats.bytes + row_pages.bytes +
-                        page_list.bytes + union_bits.bytes + counters.bytes + fine_keys.bytes + sel_list.bytes + k_stage.bytes);
+                        page_list.bytes + union_bits.bytes + counters.bytes + fine_keys.bytes + sel_list.bytes + k_stage.bytes + prune.bytes);
   const int64_t chunk = pages_per_chunk * page_bytes;
   if (cfg.cold_tier != KIV_TIER_HOST) d += (int64_t)k_chunks.size() * chunk;
   if (cfg.cold_tier == KIV_TIER_HBM) d += (int64_t)v_chunks.size() * chunk;
@@ -390,9 +430,9 @@ int kiv_store_destroy(kiv_store_t *s) {
   for (void *p : s->k_chunks) (void)(k_host ? hipHostFree(p) : hipFree(p));
   for (void *p : s->v_chunks) (void)(v_host ? hipHostFree(p) : hipFree(p));
   for (hipEvent_t e : s->prof_ev) (void)hipEventDestroy(e);
-  DevBuf *bufs[] = {&s->summ, &s->summ32, &s->k_tab, &s->v_tab, &s->k_part, &s->v_part,
+  DevBuf *bufs[] = {&s->summ, &s->summ32, &s->radius, &s->k_tab, &s->v_tab, &s->k_part, &s->v_part,
                     &s->coarse_keys, &s->row_stats, &s->row_pages, &s->page_list, &s->union_bits, &s->counters,
-                    &s->fine_keys, &s->sel_list, &s->k_stage};
+                    &s->fine_keys, &s->sel_list, &s->k_stage, &s->prune};
   for (DevBuf *b : bufs) b->release();
   delete s;
   return KIV_OK;
@@ -456,7 +496,7 @@ int kiv_evict(kiv_store_t *s, const void *k, const int64_t k_stride[3], const vo
                          (const char *)s->v_part.ptr, p0, kc, vc, k_stride[0], k_stride[1], k_stride[2],
                          v_stride[0], v_stride[1], v_stride[2], hkv, s->kr, D, ps, s->num_pages,
                          (const uint64_t *)s->k_tab.ptr, (const uint64_t *)s->v_tab.ptr, s->chunk_shift,
-                         s->page_bytes, s->summ.ptr, (float *)s->summ32.ptr);
+                         s->page_bytes, s->summ.ptr, (float *)s->summ32.ptr, (float *)s->radius.ptr);
     };
     if (dt == KIV_DTYPE_F32) launch(evict_finalize_kernel<DT_F32>);
     else if (dt == KIV_DTYPE_F16) launch(evict_finalize_kernel<DT_F16>);

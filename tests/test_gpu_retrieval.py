@@ -272,6 +272,55 @@ def test_split_tier(cuda, attend):
     assert mem["k_index_cpu"] == 0 and mem["v_cold_gpu"] == 0
 
 
+PRUNE = [
+    # name, workload, batch, clustered (pruning expected to skip pages)
+    ("qwen_shape", Workload("prune_qwen", 28, 4, 128, torch.bfloat16, hot=64, cold=20000 + 37, top_pages=16,
+                            top_p=256, segment=1024), 1, True),
+    ("gqa_batch2", Workload("prune_b2", 8, 2, 64, torch.bfloat16, hot=16, cold=8192 + 5, top_pages=8, top_p=128,
+                            segment=512), 2, True),
+    ("mqa_f16_d256", Workload("prune_mqa", 8, 1, 256, torch.float16, hot=16, cold=12000, top_pages=12,
+                              top_p=300, segment=512), 1, True),
+    ("mha_targets", Workload("prune_mha", 8, 8, 96, torch.bfloat16, hot=16, cold=6000 + 1, top_pages=6,
+                             top_p=200, segment=256, n_targets=4), 1, True),
+    # every token its own centroid: no page structure to prune on
+    ("unclustered", Workload("prune_rand", 8, 2, 64, torch.bfloat16, hot=16, cold=5000, top_pages=8, top_p=128,
+                             segment=1), 1, False),
+]
+
+
+@pytest.mark.parametrize("name,w,batch,clustered", PRUNE, ids=[c[0] for c in PRUNE])
+def test_fine_pruning_keeps_the_selection(cuda, name, w, batch, clustered):
+    """Host tier with the pruned fine scan against the full scan on the same
+    store: the same union, selected ids in the same order and the same K/V
+    rows bit for bit (pruning skips only pages whose bound is below pass A's
+    threshold).  Where pages were skipped the fine mean, which covers the
+    scored candidates only, differs."""
+    from dataclasses import replace
+
+    data = generate(w, seed=2, batch=batch)
+    store, oracle, cfg = build(w, data, cuda, chunks=(3000, 1, 511))
+    q = data["q"]
+    runs = {}
+    for prune in (True, False):
+        c = replace(cfg, fine_pruning=prune)
+        if prune:
+            k_out, v_out, sel = check_retrieval(store, oracle, c, w, data, q)
+        else:
+            k_out, v_out = store.retrieve_top_kv(q.to(cuda), w.scaling, c)
+        snap = store.telemetry_snapshot()["recent"]
+        runs[prune] = (k_out.cpu(), v_out.cpu(), snap[-2]["pages_selected"], snap[-1], store.fine_scan_stats())
+    (k1, v1, u1, f1, s1), (k0, v0, u0, f0, s0) = runs[True], runs[False]
+    print(f"{name}: union {len(u1)} pages, slices read pruned {s1} full {s0}, "
+          f"fine mean pruned {f1['mean_score']} full {f0['mean_score']}", flush=True)
+    assert s0[0] == s0[1] == s1[1] == len(u1) * batch * w.num_kv_heads and s1[0] <= s1[1]
+    assert u1 == u0
+    assert f1["selected_token_indices"] == f0["selected_token_indices"]
+    assert torch.equal(k1, k0) and torch.equal(v1, v0)
+    assert f1["top_score"] == f0["top_score"]
+    if clustered:
+        assert s1[0] < s1[1] and f1["mean_score"] > f0["mean_score"]  # the skipped pages score low
+
+
 def test_width_depends_on_union(cuda):
     """top_p > top_pages * page_size: the width follows the union size."""
     w = Workload("wide", 4, 1, 64, torch.bfloat16, hot=8, cold=64 * 10, top_pages=2, top_p=300, segment=64,
