@@ -103,8 +103,8 @@ struct kiv_store {
   kiv::DevBuf fine_keys;     // [B][ld] u32
   kiv::DevBuf sel_list;      // [B][list_ld] u64 top-P' candidates + [B] i32 counts
   kiv::DevBuf k_stage;       // [B*Hkv][ld][D] candidates' K rows (host tier)
-  kiv::DevBuf prune;         // [B*Hkv][ld] u8 union page states of a pruned fine scan + [B] u32 thresholds
-  int64_t prune_state_ld = 0;  // state row stride of the last fine scan if it was pruned, else 0
+  kiv::DevBuf prune;         // pruned fine scan: [B*Hkv][ld] u32 page bound keys + [B] u32 thresholds
+  int64_t prune_ub_ld = 0;   // page-bound row stride of the last fine scan if it was pruned, else 0
   bool union_valid = false;  // page_list / U hold the last coarse pass
   int64_t union_rows = 0;    // B*Hq*Q of that pass (bounds reuse)
   int64_t union_max = 0;     // grid bound of that pass

@@ -854,21 +854,68 @@ __device__ void publish_union(const uint32_t *ubits, const int *urank, int words
 
 // Exact pruning of a host-tier fine scan (one query pass, VALU scan).
 // Pass A (mode 1) scores set A, the pages among the first `a` entries of
-// any row's list, and the partial page, and sets state[r][v] of every
-// union page to 1 (in A) or 0; fine_threshold_kernel then takes a lower
-// bound T of each batch row's P'-th largest key from these scores,
-// fine_bound_kernel sets state 2 (score) or 3 (skip) for the other pages
-// from a bound on their tokens' scores, and pass B (mode 2) scores the
-// state-2 pages.  A token whose key (max over kv rows) reaches T gets it
-// from a kv row whose page bound reaches T, so every key >= T is exact and
-// every other one stays below T: the top P' and its order are unchanged.
+// any row's list, and the partial page, and writes for every union page v
+// and kv row r the key of a bound on the scores of v's tokens from r's
+// query rows to ub[r][v] (set A: 0xffffffff).  fine_threshold_kernel takes
+// from pass A's keys a lower bound T of each batch row's P'-th largest key;
+// pass B (mode 2) scores the slices (r, v) with T <= ub[r][v] < 0xffffffff.
+// A token whose key (max over kv rows) reaches T gets it from a kv row
+// whose page bound reaches T, so every key >= T is exact and every other
+// one stays below T: the top P' and its order are unchanged.
+constexpr int kPageListCap = 4096;  // union pages a block lists in LDS (pruned scans and selects)
+
 struct FinePrune {
   int mode;                  // 0: no pruning, 1: pass A, 2: pass B
   const int32_t *row_pages;  // [rows][kc] per-row page lists of the coarse select
   int rows, kc, a, words;    // a: list entries per row in set A; words = ceil(N / 32)
-  uint8_t *state;            // [B*Hkv][state_ld] per union page
-  int64_t state_ld;
+  int acap;                  // LDS entries for set A's list (>= |A|)
+  uint32_t *ub;              // [B*Hkv][ub_ld] page bound keys
+  int64_t ub_ld;
+  const uint32_t *thr;       // [B] thresholds T (pass B)
+  const float *summ32, *radius;  // page means [N][kr][D] and radii [N][kr]
+  int kr;
 };
+
+// Key of a bound on the scores of a page row's tokens (one wave, lanes over
+// the head dim): q.k <= q.m + |q| |k - m| <= q.m + |q| rad for each of the
+// GQ query rows in LDS (Cauchy-Schwarz; m the page row's fp32 mean, rad its
+// radius), plus 1e-4 |q| (|m| + rad), which covers the fp32 rounding of the
+// scan's dot product (at most D 2^-24 |q| |k| for D <= 512) and of this
+// bound.  A score's dtype rounding and positive scale are monotone, so no
+// token of the page row scores a key above the returned one.
+template <int DT>
+__device__ uint32_t page_bound_key(const char *qraw, int GQ, int head_dim, const float *m, float rad, float scale,
+                                   bool round) {
+  constexpr int EB = Elem<DT>::BYTES;
+  constexpr int MV = 8;  // dims per lane (D <= 512)
+  const int l = threadIdx.x & 63;
+  float mv[MV], mm = 0.f;
+#pragma unroll
+  for (int i = 0; i < MV; ++i) {
+    const int e = l + 64 * i;
+    mv[i] = e < head_dim ? m[e] : 0.f;
+    mm = fmaf(mv[i], mv[i], mm);
+  }
+  const float mn = sqrtf(wave_sum(mm));
+  float best = -INFINITY;
+  for (int j = 0; j < GQ; ++j) {
+    const char *qrow = qraw + (size_t)j * head_dim * EB;
+    float dot = 0.f, qq = 0.f;
+#pragma unroll
+    for (int i = 0; i < MV; ++i) {
+      const int e = l + 64 * i;
+      if (e < head_dim) {
+        const float x = load_elem<DT>(qrow, e);
+        dot = fmaf(x, mv[i], dot);
+        qq = fmaf(x, x, qq);
+      }
+    }
+    dot = wave_sum(dot);
+    const float qn = sqrtf(wave_sum(qq));
+    best = fmaxf(best, dot + qn * rad * 1.0001f + 1e-4f * qn * (mn + rad));
+  }
+  return min(order_key(score_of<DT>(best, scale, round)), 0xfffffffeu);  // 0xffffffff marks set A
+}
 
 template <int DT, int LG>
 __global__ void __launch_bounds__(256) fine_scan_kernel(
@@ -890,7 +937,9 @@ __global__ void __launch_bounds__(256) fine_scan_kernel(
   char *qraw = reinterpret_cast<char *>(smem4);  // [G*Q][D] dtype
   uint32_t *ubits = reinterpret_cast<uint32_t *>(qraw + (size_t)GQ * head_dim * EB);
   int *urank = reinterpret_cast<int *>(ubits + words);
-  uint32_t *abits = reinterpret_cast<uint32_t *>(urank + words + 1);  // set A (pass A)
+  uint32_t *abits = reinterpret_cast<uint32_t *>(urank + words + 1);  // pass A: set A's page bitmap,
+  int *alist = reinterpret_cast<int *>(abits + pr.words);              // its union ranks
+  int *apage = alist + pr.acap;                                        // and page ids
   const int tid = threadIdx.x;
   if (pr.mode == 1) {
     for (int w = tid; w < pr.words; w += 256) abits[w] = 0u;
@@ -916,36 +965,45 @@ __global__ void __launch_bounds__(256) fine_scan_kernel(
     U = counters[0];
   }
   __syncthreads();
+  int nA = 0;
+  if (pr.mode == 1) {
+    // Set A as a list (page order): a thread per bitmap word, offsets from
+    // a block scan of the words' popcounts; a page's union rank from the
+    // ranked union bitmap or by bisecting the union list.
+    for (int base = 0; base < pr.words; base += 256) {
+      const int w = base + tid;
+      const uint32_t bits = w < pr.words ? abits[w] : 0u;
+      int tot;
+      int pos = nA + block_incl_scan<256>(__popc(bits), scan_tmp, &tot) - __popc(bits);
+      for (uint32_t x = bits; x; x &= x - 1) {
+        const int bit = __ffs(x) - 1, page = w * 32 + bit;
+        int v;
+        if (union_src == UNION_ROWS) {
+          v = urank[w] + __popc(ubits[w] & ((1u << bit) - 1u));
+        } else {
+          int lo = 0, hi = U - 1;
+          while (lo < hi) {
+            const int mid = (lo + hi) >> 1;
+            if (page_list[mid] < page) lo = mid + 1;
+            else hi = mid;
+          }
+          v = lo;
+        }
+        alist[pos] = v;
+        apage[pos] = page;
+        ++pos;
+      }
+      nA += tot;
+    }
+    __syncthreads();
+  }
   const int nsplit = (page_size + tpi - 1) / tpi;
-  const int page_items = U * nsplit;
-  const int items = page_items + (pr.mode == 2 ? 0 : (partial_len + tpi - 1) / tpi);
   const int slot = tid / LG, lane = tid % LG;
   const bool on = lane < cpr;
   const int64_t row_bytes = (int64_t)head_dim * EB;
-  for (int item = blockIdx.x; item < items; item += gridDim.x) {
-    const char *rowbase;
-    int64_t cand0;
-    int ntok;
-    if (item < page_items) {
-      const int v = item / nsplit, s = item % nsplit;
-      if (pr.mode == 2 && pr.state[(int64_t)r * pr.state_ld + v] != 2) continue;
-      const int64_t page = union_src == UNION_ROWS ? union_page(ubits, urank, words, v) : page_list[v];
-      if (pr.mode == 1) {
-        const bool in_a = (abits[page >> 5] >> (page & 31)) & 1u;
-        if (s == 0 && tid == 0) pr.state[(int64_t)r * pr.state_ld + v] = in_a ? 1 : 0;
-        if (!in_a) continue;
-      }
-      rowbase = reinterpret_cast<const char *>(ktab[page >> chunk_shift]) +
-                (page & ((int64_t(1) << chunk_shift) - 1)) * page_bytes +
-                ((int64_t)r * page_size + (int64_t)s * tpi) * row_bytes;
-      cand0 = (int64_t)v * page_size + (int64_t)s * tpi;
-      ntok = min(tpi, page_size - s * tpi);
-    } else {
-      const int s = item - page_items;
-      rowbase = part_k + ((int64_t)r * page_size + (int64_t)s * tpi) * row_bytes;
-      cand0 = (int64_t)U * page_size + (int64_t)s * tpi;
-      ntok = min(tpi, partial_len - s * tpi);
-    }
+  // Scores tokens [0, ntok) of a slice (rows at rowbase, candidates cand0..)
+  // into their keys, staging the K rows when asked.
+  auto scan_slice = [&](const char *rowbase, int64_t cand0, int ntok) {
     if (k_read) rowbase = k_read + ((int64_t)r * ld + cand0) * row_bytes;
     for (int tb = 0; tb < ntok; tb += NSLOT * UT) {
       uint4 x[UT];
@@ -976,105 +1034,171 @@ __global__ void __launch_bounds__(256) fine_scan_kernel(
         if (lane == 0) atomicMax(&out[(int64_t)b * ld + cand0 + t], order_key(best));
       }
     }
+  };
+  auto page_rows = [&](int64_t page, int s) {
+    return reinterpret_cast<const char *>(ktab[page >> chunk_shift]) +
+           (page & ((int64_t(1) << chunk_shift) - 1)) * page_bytes +
+           ((int64_t)r * page_size + (int64_t)s * tpi) * row_bytes;
+  };
+  if (pr.mode == 2) {
+    // Pass B: per window of kPageListCap union pages, the pages whose bound
+    // for this kv row reaches the threshold (set A excluded) are listed in
+    // LDS, then their slices are spread over the blocks.
+    int *plist = alist;
+    const uint32_t tb = pr.thr[b];
+    const uint32_t *ubr = pr.ub + (int64_t)r * pr.ub_ld;
+    for (int base = 0; base < U; base += kPageListCap) {
+      const int nv = min(kPageListCap, U - base);
+      int nh = 0;
+      for (int c0 = 0; c0 < nv; c0 += 256) {
+        const int v = base + c0 + tid;
+        const bool in = c0 + tid < nv;  // (a zero threshold passes every key, so the range test is separate)
+        const uint32_t u = in ? ubr[v] : 0u;
+        const int hit = in && u != 0xffffffffu && u >= tb ? 1 : 0;
+        int tot;
+        const int pos = nh + block_incl_scan<256>(hit, scan_tmp, &tot) - hit;
+        if (hit) plist[pos] = v;
+        nh += tot;
+      }
+      __syncthreads();
+      for (int item = blockIdx.x; item < nh * nsplit; item += gridDim.x) {
+        const int v = plist[item / nsplit], s = item % nsplit;
+        const int64_t page = union_src == UNION_ROWS ? union_page(ubits, urank, words, v) : page_list[v];
+        scan_slice(page_rows(page, s), (int64_t)v * page_size + (int64_t)s * tpi, min(tpi, page_size - s * tpi));
+      }
+      __syncthreads();  // the list is rebuilt for the next window
+    }
+    return;
+  }
+  // Items: page slices (set A's pages in pass A), then the partial page's.
+  const int page_items = (pr.mode == 1 ? nA : U) * nsplit;
+  const int items = page_items + (partial_len + tpi - 1) / tpi;
+  for (int item = blockIdx.x; item < items; item += gridDim.x) {
+    if (item < page_items) {
+      const int vi = item / nsplit, s = item % nsplit;
+      int v = vi;
+      int64_t page;
+      if (pr.mode == 1) {
+        v = alist[vi];
+        page = apage[vi];
+      } else {
+        page = union_src == UNION_ROWS ? union_page(ubits, urank, words, v) : page_list[v];
+      }
+      scan_slice(page_rows(page, s), (int64_t)v * page_size + (int64_t)s * tpi, min(tpi, page_size - s * tpi));
+    } else {
+      const int s = item - page_items;
+      scan_slice(part_k + ((int64_t)r * page_size + (int64_t)s * tpi) * row_bytes,
+                 (int64_t)U * page_size + (int64_t)s * tpi, min(tpi, partial_len - s * tpi));
+    }
+  }
+  if (pr.mode == 1) {
+    // Pass A: the bound key of every union page for this kv row, a page per
+    // wave (set A's pages get 0xffffffff).
+    const int wave = tid >> 6;
+    for (int v = blockIdx.x * 4 + wave; v < U; v += gridDim.x * 4) {
+      const int64_t page = union_src == UNION_ROWS ? union_page(ubits, urank, words, v) : page_list[v];
+      uint32_t key = 0xffffffffu;
+      if (!((abits[page >> 5] >> (page & 31)) & 1u)) {
+        const int64_t prow = page * pr.kr + r;
+        key = page_bound_key<DT>(qraw, GQ, head_dim, pr.summ32 + prow * head_dim, pr.radius[prow], scale,
+                                 round != 0);
+      }
+      if ((tid & 63) == 0) pr.ub[(int64_t)r * pr.ub_ld + v] = key;
+    }
   }
 }
 
-// Threshold of a pruned fine scan: block b, after pass A, writes thr[b] <=
-// the k-th largest of batch row b's keys (k = min(P', n); unscored keys
-// are zero): the exact k-th when the bound's candidates fit the rank
-// counting, else the smallest of them (they hold the top k), else 0
-// (nothing is pruned).
-template <int V>
+// Keys of a list of union pages (plist: their union ranks) then of the
+// partial page, as composites with their candidate index (union rank *
+// page_size + token; the partial page's after the U union pages).
+template <int NT> struct PageKeys {
+  const uint32_t *row;
+  const int *plist;
+  int mp, mall, page_size;
+  int64_t part0;
+  __device__ int64_t index(int e) const {
+    return e < mp ? (int64_t)plist[e / page_size] * page_size + e % page_size : part0 + (e - mp);
+  }
+  // Entry e goes to wave e % W, so that each wave holds about mall / W of
+  // them (the per-wave bounds need ceil(k / W) each); sub-slot = step & 3.
+  template <typename F> __device__ void each_slot(F &&f) const {
+    constexpr int W = NT / 64;
+    int u = 0;
+    for (int e = (threadIdx.x >> 6) + W * (threadIdx.x & 63); e < mall; e += NT, ++u) {
+      const int64_t i = index(e);
+      f(comp_of(row[i], (int)i), u & 3);
+    }
+  }
+  template <typename F> __device__ void each(F &&f) const {
+    each_slot([&](uint64_t x, int) { f(x); });
+  }
+};
+
+// Block-wide list of the union pages v < U with pred(v) into plist (at
+// most kPageListCap); returns their number (possibly larger).
+template <int NT, typename P> __device__ int list_pages(int U, P &&pred, int *plist, int *scan_tmp) {
+  int np = 0;
+  for (int base = 0; base < U; base += NT) {
+    const int v = base + threadIdx.x;
+    const int hit = v < U && pred(v) ? 1 : 0;
+    int tot;
+    const int pos = np + block_incl_scan<NT>(hit, scan_tmp, &tot) - hit;
+    if (hit && pos < kPageListCap) plist[pos] = v;
+    np += tot;
+  }
+  __syncthreads();
+  return np;
+}
+
+// A lower bound of the k-th largest key of a block's composites (the first
+// step of bound_candidates): each wave takes the kw-th largest (kw =
+// ceil(k / waves)) of its threads' key maxima per sub-slot, which are
+// distinct keys, so every wave holds kw keys >= its bound and the smallest
+// bound leaves at least k keys at or above it; 0 when a wave holds fewer
+// than kw nonzero maxima.
+template <int NT, typename Src> __device__ uint32_t block_kth_bound(const Src &src, int k, SelSh<NT> &sh) {
+  constexpr int W = NT / 64;
+  const int wave = threadIdx.x >> 6;
+  uint32_t m[4] = {0u, 0u, 0u, 0u};
+  src.each_slot([&](uint64_t x, int j) { m[j] = max(m[j], comp_key(x)); });
+  const int kw = (k + W - 1) / W;
+  int have = 0;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) have += __popcll(__ballot(m[j] != 0u));
+  const uint32_t bw = have >= kw ? wave_kth_u32<4>(m, kw) : 0u;
+  if ((threadIdx.x & 63) == 0) sh.wave_bound[wave] = bw;
+  __syncthreads();
+  uint32_t bound = sh.wave_bound[0];
+#pragma unroll
+  for (int w = 1; w < W; ++w) bound = min(bound, sh.wave_bound[w]);
+  return bound;
+}
+
+// Threshold of a pruned fine scan: block b, after pass A, writes thr[b] = a
+// lower bound of the k-th largest key of batch row b (k = min(P', n)),
+// taken over the exact keys pass A left: those of set A's pages (ub ==
+// 0xffffffff in kv row b * Hkv; set A is the same for every kv row), up to
+// kPageListCap of them, and of the partial page (a subset's k-th largest is
+// at most the row's); 0 (nothing is pruned) when fewer than k were scored.
 __global__ void __launch_bounds__(kSelThreads) fine_threshold_kernel(const uint32_t *__restrict__ keys, int64_t ld,
                                                                      const int32_t *__restrict__ counters,
                                                                      int page_size, int partial_len, int width,
-                                                                     uint32_t *__restrict__ thr) {
+                                                                     const uint32_t *__restrict__ ub, int64_t ub_ld,
+                                                                     int hkv, uint32_t *__restrict__ thr) {
   constexpr int NT = kSelThreads;
   __shared__ SelSh<NT> sh;
-  __shared__ uint64_t cand[kCandCap];
-  __shared__ uint32_t t_sh;
+  __shared__ int plist[kPageListCap];
   sel_init(sh);
   const int b = blockIdx.x;
-  const int n = counters[0] * page_size + partial_len;
-  const int k = min(width, n);
-  const uint32_t *row = keys + (int64_t)b * ld;
-  const MemKeys4<NT> mk{row, n};
-  float mx, sum;
-  int C, nz;
-  if (n <= 4 * V * NT) {
-    RegKeys4<NT, V> rk;
-    rk.load(row, n);
-    C = bound_candidates<NT>(rk, k, sh, cand, mx, sum, nz);
-  } else {
-    C = bound_candidates<NT>(mk, k, sh, cand, mx, sum, nz);
-  }
-  if (threadIdx.x == 0) t_sh = (C > kRankCap && C <= kCandCap) ? 0xffffffffu : 0u;
-  __syncthreads();
-  if (C <= kRankCap) {
-    rank_candidates<NT>(cand, C, k, [&](uint64_t x, int rank) {
-      if (rank == k - 1) t_sh = comp_key(x);
-    });
-  } else if (C <= kCandCap) {
-    for (int i = threadIdx.x; i < C; i += NT) atomicMin(&t_sh, comp_key(cand[i]));
-  }
-  __syncthreads();
-  if (threadIdx.x == 0) thr[b] = t_sh;
-}
-
-// Page bound of a pruned fine scan: wave w of block (x, r) takes union page
-// v = 4 x + w of kv row r (batch row b = r / Hkv) unless pass A scored it
-// (state 1) and bounds the dot product of its tokens with each of the row's
-// G*Q query rows: q.k <= q.m + |q| |k - m| <= q.m + |q| rad (Cauchy-Schwarz;
-// m the page row's fp32 mean, rad its radius), plus 1e-4 |q| (|m| + rad),
-// which covers the fp32 rounding of the scan's dot product (at most
-// D 2^-24 |q| |k| for D <= 512) and of this bound.  The dtype rounding and
-// the positive scale of a score are monotone, so a page whose bound's key
-// is below thr[b] gives none of its tokens a key >= thr[b] from this row:
-// state 3 (skip), else state 2 (score in pass B).
-template <int DT>
-__global__ void __launch_bounds__(256) fine_bound_kernel(
-    const int32_t *__restrict__ page_list, const int32_t *__restrict__ counters, const float *__restrict__ summ32,
-    const float *__restrict__ radius, int kr, int head_dim, int hkv, const char *__restrict__ q, int64_t qs0,
-    int64_t qs1, int64_t qs2, int hq, int qlen, float scale, int round, const uint32_t *__restrict__ thr,
-    uint8_t *__restrict__ state, int64_t state_ld) {
-  constexpr int EB = Elem<DT>::BYTES;
-  constexpr int MV = 8;  // dims per lane (D <= 512)
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int v = blockIdx.x * 4 + wave;
-  const int r = blockIdx.y, b = r / hkv, kvh = r % hkv;
-  if (v >= counters[0]) return;
-  uint8_t *st = state + (int64_t)r * state_ld + v;
-  if (*st == 1) return;
-  const int64_t row = (int64_t)page_list[v] * kr + r;
-  const float *m = summ32 + row * head_dim;
-  float mv[MV], mm = 0.f;
-#pragma unroll
-  for (int i = 0; i < MV; ++i) {
-    const int e = lane + 64 * i;
-    mv[i] = e < head_dim ? m[e] : 0.f;
-    mm = fmaf(mv[i], mv[i], mm);
-  }
-  const float mn = sqrtf(wave_sum(mm)), rad = radius[row];
-  const int G = hq / hkv;
-  float best = -INFINITY;
-  for (int j = 0; j < G * qlen; ++j) {
-    const int h = kvh * G + j / qlen, qp = j % qlen;
-    const char *qrow = q + ((int64_t)b * qs0 + (int64_t)h * qs1 + (int64_t)qp * qs2) * EB;
-    float dot = 0.f, qq = 0.f;
-#pragma unroll
-    for (int i = 0; i < MV; ++i) {
-      const int e = lane + 64 * i;
-      if (e < head_dim) {
-        const float x = load_elem<DT>(qrow, e);
-        dot = fmaf(x, mv[i], dot);
-        qq = fmaf(x, x, qq);
-      }
-    }
-    dot = wave_sum(dot);
-    const float qn = sqrtf(wave_sum(qq));
-    best = fmaxf(best, dot + qn * rad * 1.0001f + 1e-4f * qn * (mn + rad));
-  }
-  if (lane == 0) *st = order_key(score_of<DT>(best, scale, round != 0)) >= thr[b] ? 2 : 3;
+  const int U = counters[0];
+  const int n = U * page_size + partial_len, k = min(width, n);
+  const uint32_t *u0 = ub + (int64_t)b * hkv * ub_ld;
+  const int na = min(list_pages<NT>(U, [&](int v) { return u0[v] == 0xffffffffu; }, plist, sh.scan_tmp),
+                     kPageListCap);
+  const PageKeys<NT> src{keys + (int64_t)b * ld, plist, na * page_size, na * page_size + partial_len, page_size,
+                         (int64_t)U * page_size};
+  const uint32_t t = src.mall >= k ? block_kth_bound<NT>(src, k, sh) : 0u;
+  if (threadIdx.x == 0) thr[b] = t;
 }
 
 // MFMA fine scan for queries of many rows (G * Q >= kFineMfmaRows per kv
@@ -1204,10 +1328,12 @@ template <int V>
 __global__ void __launch_bounds__(kSelThreads) fine_select_kernel(
     uint32_t *__restrict__ keys, int64_t ld, const int32_t *__restrict__ counters, int has_pages, int page_size,
     int partial_len, int width, float *__restrict__ fine_stats, uint64_t *__restrict__ list, int64_t list_ld,
-    int32_t *__restrict__ list_count, int list_cap) {
+    int32_t *__restrict__ list_count, int list_cap, const uint32_t *__restrict__ ub, int64_t ub_ld, int hkv,
+    const uint32_t *__restrict__ thr) {
   constexpr int NT = kSelThreads;
   __shared__ SelSh<NT> sh;
   __shared__ uint64_t cand[kCandCap];
+  __shared__ int plist[kPageListCap];
   sel_init(sh);
   const int b = blockIdx.x;
   const int U = has_pages ? counters[0] : 0;
@@ -1215,9 +1341,40 @@ __global__ void __launch_bounds__(kSelThreads) fine_select_kernel(
   const int k = min(width, n);
   uint32_t *row = keys + (int64_t)b * ld;  // 256-byte aligned rows, zero past n
   uint64_t *out = list + (int64_t)b * list_ld;
-  const MemKeys4<NT> mk{row, n};
   float mx, sum;
   int C, nz;
+  if (ub) {
+    // Pruned fine scan: only the pages some kv row of b scanned (and the
+    // partial page) hold nonzero keys; the others are not read.
+    const uint32_t tb = thr[b];
+    const uint32_t *ub_b = ub + (int64_t)b * hkv * ub_ld;
+    const int np = list_pages<NT>(U, [&](int v) {
+      bool hit = false;
+      for (int h = 0; h < hkv; ++h) hit |= ub_b[(int64_t)h * ub_ld + v] >= tb;
+      return hit;
+    }, plist, sh.scan_tmp);
+    if (np <= kPageListCap) {
+      const PageKeys<NT> pk{row, plist, np * page_size, np * page_size + partial_len, page_size,
+                            (int64_t)U * page_size};
+      C = bound_candidates<NT>(pk, k, sh, cand, mx, sum, nz);
+      if (C <= list_cap) {
+        for (int i = threadIdx.x; i < C; i += NT) out[i] = cand[i];
+      } else {
+        emit_topk_unranked<NT>(pk, cand, C, k, sh, [&](int pos, uint64_t x) { out[pos] = x; });
+        C = k;
+      }
+      __syncthreads();
+      for (int e = threadIdx.x; e < pk.mall; e += NT) row[pk.index(e)] = 0u;
+      if (threadIdx.x == 0) {
+        fine_stats[2 * b] = mx;
+        fine_stats[2 * b + 1] = sum;
+        list_count[b] = C;
+        list_count[gridDim.x + b] = nz;
+      }
+      return;
+    }
+  }
+  const MemKeys4<NT> mk{row, n};
   if (n <= 4 * V * NT) {
     RegKeys4<NT, V> rk;
     rk.load(row, n);
@@ -1263,8 +1420,8 @@ struct GatherArgs {
   int64_t page_bytes;
   const char *part_k, *part_v, *k_stage;
   int64_t stage_ld;
-  const uint8_t *state;  // pruned fine scan: union page states (1, 2: K rows staged), or NULL
-  int64_t state_ld;
+  const uint32_t *ub, *thr;  // pruned fine scan: page bound keys and thresholds, or NULL
+  int64_t ub_ld;
   int page_size, partial_len;
   int64_t num_finalized;
   int batch, hkv, head_dim, width, cpr;
@@ -1368,8 +1525,9 @@ template <int DT> __device__ void gather_block(const GatherArgs &ga, int bx, int
       vs = part_v + off;
       gid = num_finalized + t;
     }
-    const bool staged = k_stage && (cand >= split || !ga.state ||
-                                    (unsigned)(ga.state[(int64_t)r * ga.state_ld + cand / page_size] - 1) < 2u);
+    // Staged unless a pruned scan skipped the page for this kv row.
+    const bool staged = k_stage && (cand >= split || !ga.ub ||
+                                    ga.ub[(int64_t)r * ga.ub_ld + cand / page_size] >= ga.thr[b]);
     if (staged) ks = k_stage + (((int64_t)r * stage_ld + cand) * head_dim + e0) * EB;
     const int64_t o = (((int64_t)r * width + slot) * head_dim + e0) * EB;
     const uint4 kx = load16(ks), vx = load16(vs);
@@ -1589,8 +1747,8 @@ static int retrieve_impl(kiv_store_t *s, const kiv_retrieve_args_t *a, hipStream
   // Host tier: the fine scan copies the candidates' K rows to HBM as it
   // streams them, so the gather reads only V over the host link (up to
   // kMaxStageBytes of staging per store).
-  const uint8_t *pr_state = nullptr;  // union page states of a pruned fine scan
-  int64_t pr_state_ld = 0;
+  const uint32_t *pr_ub = nullptr, *pr_thr = nullptr;  // page bounds and thresholds of a pruned fine scan
+  int64_t pr_ub_ld = 0;
   char *k_stage = nullptr;
   const size_t stage_bytes = (size_t)s->kr * ldc * s->row_bytes;
   if (c.cold_tier == KIV_TIER_HOST && stage_bytes <= kMaxStageBytes) {
@@ -1668,28 +1826,33 @@ static int retrieve_impl(kiv_store_t *s, const kiv_retrieve_args_t *a, hipStream
     const bool prune = (a->flags & KIV_RETRIEVE_PRUNE) && host_tier && k_stage && !mfma && passes == 1 &&
                        kc > 0 && pa < kc && a->scaling > 0.f;
     FinePrune pr{};
-    uint32_t *thr = nullptr;
-    s->prune_state_ld = 0;
+    s->prune_ub_ld = 0;
     if (prune) {
-      pr.state_ld = (umax + 15) & ~int64_t(15);
-      const size_t state_bytes = ((size_t)s->kr * pr.state_ld + 255) & ~size_t(255);
-      if ((rc = s->prune.ensure(state_bytes + (size_t)B * 4, st, false))) return rc;
+      pr.ub_ld = (umax + 63) & ~int64_t(63);
+      const size_t ub_bytes = (size_t)s->kr * pr.ub_ld * 4;
+      if ((rc = s->prune.ensure(ub_bytes + (size_t)B * 4, st, false))) return rc;
       pr.mode = 1;
       pr.row_pages = (const int32_t *)s->row_pages.ptr;
       pr.rows = rows;
       pr.kc = kc;
       pr.a = pa;
       pr.words = words;
-      pr.state = (uint8_t *)s->prune.ptr;
-      thr = (uint32_t *)((char *)s->prune.ptr + state_bytes);
-      pr_state = pr.state;
-      pr_state_ld = pr.state_ld;
-      s->prune_state_ld = pr.state_ld;
+      pr.acap = (int)std::min<int64_t>((int64_t)rows * pa, umax);
+      pr.ub = (uint32_t *)s->prune.ptr;
+      pr.thr = (const uint32_t *)((char *)s->prune.ptr + ub_bytes);
+      pr.summ32 = (const float *)s->summ32.ptr;
+      pr.radius = (const float *)s->radius.ptr;
+      pr.kr = s->kr;
+      pr_ub = pr.ub;
+      pr_thr = pr.thr;
+      pr_ub_ld = pr.ub_ld;
+      s->prune_ub_ld = pr.ub_ld;
     }
     auto valu_scan = [&](int pass, int usrc, int bw, const FinePrune &fp) {
       const int Qp = std::min(Qb, Q - pass * Qb);
       const size_t lds = (size_t)G * Qp * D * eb + (size_t)bw * 4 + (size_t)(bw + 1) * 4 +
-                         (fp.mode == 1 ? (size_t)fp.words * 4 : 0);
+                         (fp.mode == 1 ? (size_t)fp.words * 4 + (size_t)fp.acap * 8 : 0) +
+                         (fp.mode == 2 ? (size_t)kPageListCap * 4 : 0);
       return with_dt_lg(dt, lg, [&](auto dtc, auto lgc) {
         auto kern = fine_scan_kernel<decltype(dtc)::value, decltype(lgc)::value>;
         if (lds > 65536)
@@ -1710,24 +1873,14 @@ static int retrieve_impl(kiv_store_t *s, const kiv_retrieve_args_t *a, hipStream
       s->prof_begin(KIV_STAGE_FINE_SCAN, st);
       if ((rc = valu_scan(pass, union_src, bwords, pr))) return rc;
       if (prune) {
-        // Pass A's threshold per batch row, the other pages' bounds, pass B.
-        with_select_chunks(cmax, [&](auto kern) {
-          hipLaunchKernelGGL(kern, dim3(B), dim3(kSelThreads), 0, st, (const uint32_t *)s->fine_keys.ptr, ldc,
-                             (const int32_t *)s->counters.ptr, ps, (int)s->partial_len, a->out_width, thr);
-        }, [](auto vc) { return fine_threshold_kernel<decltype(vc)::value>; });
-        KIV_HIP(hipGetLastError());
-        rc = with_dt(dt, [&](auto dtc) {
-          hipLaunchKernelGGL((fine_bound_kernel<decltype(dtc)::value>), dim3((unsigned)((umax + 3) / 4), s->kr),
-                             dim3(256), 0, st, (const int32_t *)s->page_list.ptr, (const int32_t *)s->counters.ptr,
-                             (const float *)s->summ32.ptr, (const float *)s->radius.ptr, s->kr, D, hkv,
-                             (const char *)a->q, a->q_stride[0], a->q_stride[1], a->q_stride[2], hq, Q,
-                             a->scaling, round, (const uint32_t *)thr, pr.state, pr.state_ld);
-          return (int)KIV_OK;
-        });
-        if (rc) return rc;
+        // Pass A's threshold per batch row, then pass B.
+        hipLaunchKernelGGL(fine_threshold_kernel, dim3(B), dim3(kSelThreads), 0, st, (const uint32_t *)s->fine_keys.ptr,
+                           ldc, (const int32_t *)s->counters.ptr, ps, (int)s->partial_len, a->out_width,
+                           (const uint32_t *)pr.ub, pr.ub_ld, hkv, (uint32_t *)pr.thr);
         KIV_HIP(hipGetLastError());
         FinePrune pb = pr;
         pb.mode = 2;
+        pb.words = 0;  // pass B lists its pages where set A's bitmap was
         if ((rc = valu_scan(pass, UNION_LIST, 0, pb))) return rc;
       }
       s->prof_end(KIV_STAGE_FINE_SCAN, st);
@@ -1738,7 +1891,7 @@ static int retrieve_impl(kiv_store_t *s, const kiv_retrieve_args_t *a, hipStream
     with_select_chunks(cmax, [&](auto kern) {
       hipLaunchKernelGGL(kern, dim3(B), dim3(kSelThreads), 0, st, (uint32_t *)s->fine_keys.ptr, ldc,
                          (const int32_t *)s->counters.ptr, N > 0 ? 1 : 0, ps, (int)s->partial_len, a->out_width,
-                         fine_stats, list, list_ld, list_count, list_cap);
+                         fine_stats, list, list_ld, list_count, list_cap, pr_ub, pr_ub_ld, hkv, pr_thr);
     }, [](auto vc) { return fine_select_kernel<decltype(vc)::value>; });
     s->prof_end(KIV_STAGE_FINE_SELECT, st);
     KIV_HIP(hipGetLastError());
@@ -1760,8 +1913,9 @@ static int retrieve_impl(kiv_store_t *s, const kiv_retrieve_args_t *a, hipStream
     ga.part_v = (const char *)s->v_part.ptr;
     ga.k_stage = k_stage;
     ga.stage_ld = ldc;
-    ga.state = pr_state;
-    ga.state_ld = pr_state_ld;
+    ga.ub = pr_ub;
+    ga.thr = pr_thr;
+    ga.ub_ld = pr_ub_ld;
     ga.page_size = ps;
     ga.partial_len = (int)s->partial_len;
     ga.num_finalized = s->num_pages * ps;
@@ -1817,15 +1971,14 @@ int kiv_fine_scan_stats(kiv_store_t *s, int64_t *scanned_slices, int64_t *union_
   KIV_HIP(hipMemcpy(&U, s->counters.ptr, sizeof(U), hipMemcpyDeviceToHost));
   *union_slices = (int64_t)U * s->kr;
   *scanned_slices = *union_slices;
-  if (s->prune_state_ld > 0) {
-    std::vector<uint8_t> st((size_t)s->kr * s->prune_state_ld);
-    KIV_HIP(hipMemcpy(st.data(), s->prune.ptr, st.size(), hipMemcpyDeviceToHost));
+  if (s->prune_ub_ld > 0) {
+    const int B = s->cfg.batch, hkv = s->cfg.num_kv_heads;
+    std::vector<uint32_t> ub((size_t)s->kr * s->prune_ub_ld), thr(B);
+    KIV_HIP(hipMemcpy(ub.data(), s->prune.ptr, ub.size() * 4, hipMemcpyDeviceToHost));
+    KIV_HIP(hipMemcpy(thr.data(), (char *)s->prune.ptr + ub.size() * 4, thr.size() * 4, hipMemcpyDeviceToHost));
     int64_t n = 0;
     for (int r = 0; r < s->kr; ++r)
-      for (int v = 0; v < U; ++v) {
-        const uint8_t x = st[(size_t)r * s->prune_state_ld + v];
-        n += x == 1 || x == 2;
-      }
+      for (int v = 0; v < U; ++v) n += ub[(size_t)r * s->prune_ub_ld + v] >= thr[r / hkv];
     *scanned_slices = n;
   }
   return KIV_OK;

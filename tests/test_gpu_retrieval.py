@@ -423,7 +423,10 @@ def test_select_large_k_paths(cuda, n_pages, top_pages, top_p):
     select, top_p = 2500 leaves every wave short of its share of maxima, so
     all of the row's keys (more than 2048) are candidates: the k-th largest
     comes from the search over the row in memory and the gather ranks 2500
-    listed entries."""
+    listed entries.  On the host tier the pruned fine scan gets a zero
+    threshold there (too few maxima per wave), so pass B lists every union
+    page: its list must stop at the union size (a regression: padding
+    threads once passed the zero threshold and listed pages past it)."""
     w = Workload("largek", 4, 1, 32, torch.float32, hot=8, cold=n_pages * 16 + 5, top_pages=top_pages,
                  top_p=top_p, segment=64, page_size=16)
     data = generate(w, seed=16)
