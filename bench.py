@@ -73,6 +73,7 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=15.0, help="CPU baseline sample budget")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--no-pruning", action="store_true", help="host tier: full fine scan (KIVConfig.fine_pruning=False)")
     ap.add_argument("--cache", default="cold", choices=("cold", "warm"))
     ap.add_argument("--model-tokens", type=int, default=1 << 20, help="prompt length of the model workload")
     ap.add_argument("--decode-steps", type=int, default=128, help="greedy decode steps of the model workload")
@@ -323,7 +324,8 @@ def profile_pass(w, args, dev, scrub):
     from kiv_amd import KIVConfig
 
     cfg = KIVConfig(hot_budget=w.hot, top_p=w.top_p, page_size=w.page_size, top_pages=w.top_pages,
-                    cold_tier=args.cold_tier, reserve_tokens=w.cold + args.steps + args.warmup + 1024)
+                    cold_tier=args.cold_tier, reserve_tokens=w.cold + args.steps + args.warmup + 1024,
+                    fine_pruning=not args.no_pruning)
     store, hot_k, hot_v, q = build_cold(w, cfg, dev, args.seed)
     us, _ = time_steps(store, cfg, q, hot_k, hot_v, args.steps, args.warmup, w.scaling, scrub)
     src = torch.ones(64 << 20, dtype=torch.uint8, device=dev)
@@ -385,7 +387,7 @@ def model_run(args):
     with torch.device(dev):
         model = Qwen2ForCausalLM(cfg)
     model = model.to(torch.bfloat16).eval()
-    kcfg = KIVConfig(hot_budget=2048, top_p=256, page_size=128, top_pages=32)
+    kcfg = KIVConfig(hot_budget=2048, top_p=256, page_size=128, top_pages=32, fine_pruning=not args.no_pruning)
     mw = KIVMiddleware(model, kcfg)
     mw.install()
     cache = mw.create_cache(dev)
@@ -427,6 +429,9 @@ def model_run(args):
     torch.cuda.synchronize()
     step_ms = sorted(a.elapsed_time(b) for a, b in ev)
     print(f"[bench] decode median {step_ms[len(step_ms) // 2]:.2f} ms/step", file=sys.stderr, flush=True)
+    slices = [st.fine_scan_stats() for st in cache.cold_stores.values() if st._handle]
+    slices_read = [sum(x[0] for x in slices), sum(x[1] for x in slices)]  # last step, all layers
+    print(f"[bench] fine-scan slices read (last step, all layers): {slices_read}", file=sys.stderr, flush=True)
 
     # Per-layer stages over a few more steps: the store's events bracket the
     # eviction, retrieval and attention kernels of every layer.
@@ -481,7 +486,7 @@ def model_run(args):
         "config": {"workload": f"{MODEL_WORKLOAD}: Qwen2.5-1.5B-shaped decoder, {L} layers, hidden 1536, "
                                f"12/2 heads, D 128; prompt {T} tokens", "chunk_size": chunk,
                    "prefill_hot_cap": cap, "hot_budget": kcfg.hot_budget, "top_pages": kcfg.top_pages,
-                   "top_p": kcfg.top_p, "cold_tier": kcfg.cold_tier},
+                   "top_p": kcfg.top_p, "cold_tier": kcfg.cold_tier, "fine_pruning": kcfg.fine_pruning},
         "value_meaning": "GPU time per layer per decode step of the tiered-cache path: eviction append, "
                          "retrieval kernels and merged attention (the store's HIP events, averaged over all "
                          "28 layers)",
@@ -489,6 +494,7 @@ def model_run(args):
                                "kiv_min": round(step_ms[0], 3), "kiv_max": round(step_ms[-1], 3),
                                "kiv_minus_plain_per_layer_us": round((step - pstep) * 1e3 / L, 2)},
         "per_layer_stages_us": stage_us,
+        "fine_scan_slices_last_step": {"read": slices_read[0], "union": slices_read[1]},
         "union_pages": int(round(sum(union) / len(union))) if union else 0,
         "cold_tokens_per_layer": cold,
         "prefill": {"seconds": round(prefill_s, 2), "tokens_per_s": round(T / prefill_s, 1),
@@ -598,7 +604,7 @@ def main():
                                                              if t != args.cold_tier])
     for tier in tiers:
         cfg = KIVConfig(hot_budget=w.hot, top_p=w.top_p, page_size=w.page_size, top_pages=w.top_pages,
-                        cold_tier=tier, reserve_tokens=w.cold + extra)
+                        cold_tier=tier, reserve_tokens=w.cold + extra, fine_pruning=not args.no_pruning)
         t0 = time.perf_counter()
         store, hot_k, hot_v, q = build_cold(w, cfg, dev, args.seed)
         fill_s = time.perf_counter() - t0
@@ -619,7 +625,7 @@ def main():
             entry["two_call"] = {"us_per_step": round(two_us, 2),
                                  "stages_us": {k: round(v["avg_us"], 2) for k, v in two_stages.items()}}
             print(f"[bench] {tier} (retrieve, then attention): {two_us:.1f} us/step", file=sys.stderr, flush=True)
-            if tier == "host" and cfg.fine_pruning:
+            if tier == "host" and cfg.fine_pruning:  # the same store with the full scan
                 full_us, _ = time_steps(store, replace(cfg, fine_pruning=False), q, hot_k, hot_v, args.steps, 0,
                                         w.scaling, scrub)
                 entry["unpruned_us_per_step"] = full_us
@@ -687,7 +693,7 @@ def main():
         "config": {"workload": f"{w.name}: one decode layer, Hq={w.num_q_heads} Hkv={w.num_kv_heads} "
                                f"D={w.head_dim}, hot {w.hot}, cold {w.cold}", "batch": 1,
                    "top_pages": w.top_pages, "top_p": w.top_p, "page_size": w.page_size,
-                   "cold_tier": args.cold_tier, "fine_pruning": True, "caches": args.cache},
+                   "cold_tier": args.cold_tier, "fine_pruning": not args.no_pruning, "caches": args.cache},
         "roofline": roofline,
         "host_link": host_link,
         "union_pages": head["union_pages"],

@@ -853,28 +853,36 @@ __device__ void publish_union(const uint32_t *ubits, const int *urank, int words
 }
 
 // Exact pruning of a host-tier fine scan (one query pass, VALU scan).
-// Pass A (mode 1) scores set A, the pages among the first `a` entries of
-// any row's list, and the partial page, and writes for every union page v
-// and kv row r the key of a bound on the scores of v's tokens from r's
-// query rows to ub[r][v] (set A: 0xffffffff).  fine_threshold_kernel takes
-// from pass A's keys a lower bound T of each batch row's P'-th largest key;
-// pass B (mode 2) scores the slices (r, v) with T <= ub[r][v] < 0xffffffff.
-// A token whose key (max over kv rows) reaches T gets it from a kv row
-// whose page bound reaches T, so every key >= T is exact and every other
-// one stays below T: the top P' and its order are unchanged.
+// Pass A (mode 1) scores, for each kv row r, its set A_r (the pages among
+// the first `a` entries of the lists of r's query rows) and the partial
+// page, and writes for every union page v the key of a bound on the scores
+// of v's tokens from r's query rows to ub[r][v] (0xffffffff for A_r).
+// After pass A a token's key is the max over the kv rows that scored it,
+// at most its final key, so fine_threshold_kernel's P'-th largest of such
+// keys is a lower bound T of each batch row's final P'-th largest key.
+// Pass B (mode 2) scores the slices (r, v) with T <= ub[r][v] < 0xffffffff.
+// A token whose final key reaches T gets it from a kv row whose page bound
+// reaches T, so every key >= T is exact and every other one stays below T:
+// the top P' and its order are unchanged.
 constexpr int kPageListCap = 4096;  // union pages a block lists in LDS (pruned scans and selects)
 
 struct FinePrune {
   int mode;                  // 0: no pruning, 1: pass A, 2: pass B
   const int32_t *row_pages;  // [rows][kc] per-row page lists of the coarse select
-  int rows, kc, a, words;    // a: list entries per row in set A; words = ceil(N / 32)
-  int acap;                  // LDS entries for set A's list (>= |A|)
+  int kc, a, words;          // a: list entries per query row in set A; words = ceil(N / 32)
+  int acap;                  // LDS entries for a set A_r's list (>= |A_r|)
   uint32_t *ub;              // [B*Hkv][ub_ld] page bound keys
   int64_t ub_ld;
   const uint32_t *thr;       // [B] thresholds T (pass B)
   const float *summ32, *radius;  // page means [N][kr][D] and radii [N][kr]
   int kr;
+  const int32_t *ctl;        // > 0: pruning is paused for this call (full scan in pass A)
 };
+
+// Pruning pays when it skips pages: after a call whose scan read more than
+// three quarters of the union's pages, the next kPruneRetry calls on the
+// store run the full scan (decided on the device by the fine select).
+constexpr int kPruneRetry = 32;
 
 // Key of a bound on the scores of a page row's tokens (one wave, lanes over
 // the head dim): q.k <= q.m + |q| |k - m| <= q.m + |q| rad for each of the
@@ -941,11 +949,15 @@ __global__ void __launch_bounds__(256) fine_scan_kernel(
   int *alist = reinterpret_cast<int *>(abits + pr.words);              // its union ranks
   int *apage = alist + pr.acap;                                        // and page ids
   const int tid = threadIdx.x;
-  if (pr.mode == 1) {
+  if (pr.mode == 2 && *pr.ctl > 0) return;  // paused: pass A scanned everything
+  const bool seta = pr.mode == 1 && *pr.ctl <= 0;  // pass A of a pruned scan (else a full scan)
+  if (seta) {
+    // Set A of this kv row: the first `a` entries of the lists of its G*Q
+    // query rows (coarse rows r * G*Q ..).
     for (int w = tid; w < pr.words; w += 256) abits[w] = 0u;
     __syncthreads();
-    for (int i = tid; i < pr.rows * pr.a; i += 256) {
-      const int page = pr.row_pages[(int64_t)(i / pr.a) * pr.kc + i % pr.a];
+    for (int i = tid; i < GQ * pr.a; i += 256) {
+      const int page = pr.row_pages[((int64_t)r * GQ + i / pr.a) * pr.kc + i % pr.a];
       atomicOr(&abits[page >> 5], 1u << (page & 31));
     }
   }
@@ -966,7 +978,7 @@ __global__ void __launch_bounds__(256) fine_scan_kernel(
   }
   __syncthreads();
   int nA = 0;
-  if (pr.mode == 1) {
+  if (seta) {
     // Set A as a list (page order): a thread per bitmap word, offsets from
     // a block scan of the words' popcounts; a page's union rank from the
     // ranked union bitmap or by bisecting the union list.
@@ -1071,14 +1083,14 @@ __global__ void __launch_bounds__(256) fine_scan_kernel(
     return;
   }
   // Items: page slices (set A's pages in pass A), then the partial page's.
-  const int page_items = (pr.mode == 1 ? nA : U) * nsplit;
+  const int page_items = (seta ? nA : U) * nsplit;
   const int items = page_items + (partial_len + tpi - 1) / tpi;
   for (int item = blockIdx.x; item < items; item += gridDim.x) {
     if (item < page_items) {
       const int vi = item / nsplit, s = item % nsplit;
       int v = vi;
       int64_t page;
-      if (pr.mode == 1) {
+      if (seta) {
         v = alist[vi];
         page = apage[vi];
       } else {
@@ -1093,12 +1105,12 @@ __global__ void __launch_bounds__(256) fine_scan_kernel(
   }
   if (pr.mode == 1) {
     // Pass A: the bound key of every union page for this kv row, a page per
-    // wave (set A's pages get 0xffffffff).
+    // wave (0xffffffff: scanned here, set A's pages or all when paused).
     const int wave = tid >> 6;
     for (int v = blockIdx.x * 4 + wave; v < U; v += gridDim.x * 4) {
-      const int64_t page = union_src == UNION_ROWS ? union_page(ubits, urank, words, v) : page_list[v];
       uint32_t key = 0xffffffffu;
-      if (!((abits[page >> 5] >> (page & 31)) & 1u)) {
+      const int64_t page = !seta ? 0 : union_src == UNION_ROWS ? union_page(ubits, urank, words, v) : page_list[v];
+      if (seta && !((abits[page >> 5] >> (page & 31)) & 1u)) {
         const int64_t prow = page * pr.kr + r;
         key = page_bound_key<DT>(qraw, GQ, head_dim, pr.summ32 + prow * head_dim, pr.radius[prow], scale,
                                  round != 0);
@@ -1175,26 +1187,34 @@ template <int NT, typename Src> __device__ uint32_t block_kth_bound(const Src &s
 }
 
 // Threshold of a pruned fine scan: block b, after pass A, writes thr[b] = a
-// lower bound of the k-th largest key of batch row b (k = min(P', n)),
-// taken over the exact keys pass A left: those of set A's pages (ub ==
-// 0xffffffff in kv row b * Hkv; set A is the same for every kv row), up to
-// kPageListCap of them, and of the partial page (a subset's k-th largest is
-// at most the row's); 0 (nothing is pruned) when fewer than k were scored.
+// lower bound of the k-th largest final key of batch row b (k = min(P',
+// n)), taken over the keys pass A left on the pages of some kv row's set A
+// (ub == 0xffffffff), up to kPageListCap pages, and on the partial page:
+// each is at most its final key, so their k-th largest is at most the
+// row's; 0 (nothing is pruned) when fewer than k were scored.
 __global__ void __launch_bounds__(kSelThreads) fine_threshold_kernel(const uint32_t *__restrict__ keys, int64_t ld,
                                                                      const int32_t *__restrict__ counters,
                                                                      int page_size, int partial_len, int width,
                                                                      const uint32_t *__restrict__ ub, int64_t ub_ld,
-                                                                     int hkv, uint32_t *__restrict__ thr) {
+                                                                     int hkv, uint32_t *__restrict__ thr,
+                                                                     const int32_t *__restrict__ ctl) {
   constexpr int NT = kSelThreads;
   __shared__ SelSh<NT> sh;
   __shared__ int plist[kPageListCap];
-  sel_init(sh);
   const int b = blockIdx.x;
+  if (*ctl > 0) {  // paused: nothing to prune
+    if (threadIdx.x == 0) thr[b] = 0u;
+    return;
+  }
+  sel_init(sh);
   const int U = counters[0];
   const int n = U * page_size + partial_len, k = min(width, n);
-  const uint32_t *u0 = ub + (int64_t)b * hkv * ub_ld;
-  const int na = min(list_pages<NT>(U, [&](int v) { return u0[v] == 0xffffffffu; }, plist, sh.scan_tmp),
-                     kPageListCap);
+  const uint32_t *ub_b = ub + (int64_t)b * hkv * ub_ld;
+  const int na = min(list_pages<NT>(U, [&](int v) {
+    bool in_a = false;
+    for (int h = 0; h < hkv; ++h) in_a |= ub_b[(int64_t)h * ub_ld + v] == 0xffffffffu;
+    return in_a;
+  }, plist, sh.scan_tmp), kPageListCap);
   const PageKeys<NT> src{keys + (int64_t)b * ld, plist, na * page_size, na * page_size + partial_len, page_size,
                          (int64_t)U * page_size};
   const uint32_t t = src.mall >= k ? block_kth_bound<NT>(src, k, sh) : 0u;
@@ -1329,7 +1349,7 @@ __global__ void __launch_bounds__(kSelThreads) fine_select_kernel(
     uint32_t *__restrict__ keys, int64_t ld, const int32_t *__restrict__ counters, int has_pages, int page_size,
     int partial_len, int width, float *__restrict__ fine_stats, uint64_t *__restrict__ list, int64_t list_ld,
     int32_t *__restrict__ list_count, int list_cap, const uint32_t *__restrict__ ub, int64_t ub_ld, int hkv,
-    const uint32_t *__restrict__ thr) {
+    const uint32_t *__restrict__ thr, int32_t *__restrict__ ctl) {
   constexpr int NT = kSelThreads;
   __shared__ SelSh<NT> sh;
   __shared__ uint64_t cand[kCandCap];
@@ -1348,12 +1368,41 @@ __global__ void __launch_bounds__(kSelThreads) fine_select_kernel(
     // partial page) hold nonzero keys; the others are not read.
     const uint32_t tb = thr[b];
     const uint32_t *ub_b = ub + (int64_t)b * hkv * ub_ld;
+    int slices = 0;  // (page, kv row) slices the scan read, this thread's pages
     const int np = list_pages<NT>(U, [&](int v) {
       bool hit = false;
-      for (int h = 0; h < hkv; ++h) hit |= ub_b[(int64_t)h * ub_ld + v] >= tb;
+      for (int h = 0; h < hkv; ++h) {
+        const bool read = ub_b[(int64_t)h * ub_ld + v] >= tb;
+        hit |= read;
+        slices += read;
+      }
       return hit;
     }, plist, sh.scan_tmp);
-    if (np <= kPageListCap) {
+    // The next call's pruning: the blocks add their slices read to ctl[1];
+    // the last block to count itself in ctl[2] sets the pause ctl[0] from
+    // the total and clears both counters.
+    slices = wave_sum_i32(slices);
+    if ((threadIdx.x & 63) == 0) sh.fcnt[threadIdx.x >> 6] = slices;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      int read = 0;
+      for (int w = 0; w < NT / 64; ++w) read += sh.fcnt[w];
+      atomicAdd(&ctl[1], read);
+      __threadfence();
+      if (atomicAdd(&ctl[2], 1) == (int)gridDim.x - 1) {
+        __threadfence();
+        const int64_t total = atomicAdd(&ctl[1], 0);
+        const int c0 = atomicAdd(&ctl[0], 0);
+        const int64_t all = (int64_t)U * hkv * gridDim.x;
+        atomicExch(&ctl[0], c0 > 0 ? c0 - 1 : (4 * total > 3 * all ? kPruneRetry : 0));
+        atomicExch(&ctl[1], 0);
+        atomicExch(&ctl[2], 0);
+      }
+    }
+    __syncthreads();  // fcnt is reused by the select below
+    // Few pages: select over their keys alone; else over the whole row
+    // (vector loads; the unscored keys are zero).
+    if (np <= kPageListCap && 2 * np <= U) {
       const PageKeys<NT> pk{row, plist, np * page_size, np * page_size + partial_len, page_size,
                             (int64_t)U * page_size};
       C = bound_candidates<NT>(pk, k, sh, cand, mx, sum, nz);
@@ -1748,6 +1797,7 @@ static int retrieve_impl(kiv_store_t *s, const kiv_retrieve_args_t *a, hipStream
   // streams them, so the gather reads only V over the host link (up to
   // kMaxStageBytes of staging per store).
   const uint32_t *pr_ub = nullptr, *pr_thr = nullptr;  // page bounds and thresholds of a pruned fine scan
+  int32_t *pr_ctl = nullptr;
   int64_t pr_ub_ld = 0;
   char *k_stage = nullptr;
   const size_t stage_bytes = (size_t)s->kr * ldc * s->row_bytes;
@@ -1823,28 +1873,35 @@ static int retrieve_impl(kiv_store_t *s, const kiv_retrieve_args_t *a, hipStream
     // rows' best pages, so that pass A's P'-th largest key is close to the
     // final one.
     const int pa = std::min(kc, std::max(1, (a->out_width + ps - 1) / ps));
-    const bool prune = (a->flags & KIV_RETRIEVE_PRUNE) && host_tier && k_stage && !mfma && passes == 1 &&
-                       kc > 0 && pa < kc && a->scaling > 0.f;
+    const bool prune = (a->flags & KIV_RETRIEVE_PRUNE) && host_tier && !mfma && passes == 1 && kc > 0 &&
+                       pa < kc && a->scaling > 0.f;
     FinePrune pr{};
     s->prune_ub_ld = 0;
     if (prune) {
+      // [control, 256 B][thresholds [B]][page bounds [kr][ub_ld]], zeroed
+      // (pruning on) whenever the buffer is (re)allocated.
       pr.ub_ld = (umax + 63) & ~int64_t(63);
-      const size_t ub_bytes = (size_t)s->kr * pr.ub_ld * 4;
-      if ((rc = s->prune.ensure(ub_bytes + (size_t)B * 4, st, false))) return rc;
+      const size_t thr_off = 256, ub_off = thr_off + (((size_t)B * 4 + 255) & ~size_t(255));
+      const size_t need = ub_off + (size_t)s->kr * pr.ub_ld * 4;
+      if (s->prune.bytes < need) {
+        if ((rc = s->prune.ensure(need, st, false))) return rc;
+        KIV_HIP(hipMemsetAsync(s->prune.ptr, 0, s->prune.bytes, st));
+      }
       pr.mode = 1;
       pr.row_pages = (const int32_t *)s->row_pages.ptr;
-      pr.rows = rows;
       pr.kc = kc;
       pr.a = pa;
       pr.words = words;
-      pr.acap = (int)std::min<int64_t>((int64_t)rows * pa, umax);
-      pr.ub = (uint32_t *)s->prune.ptr;
-      pr.thr = (const uint32_t *)((char *)s->prune.ptr + ub_bytes);
+      pr.acap = (int)std::min<int64_t>((int64_t)G * Q * pa, umax);
+      pr.ctl = (const int32_t *)s->prune.ptr;
+      pr.thr = (const uint32_t *)((char *)s->prune.ptr + thr_off);
+      pr.ub = (uint32_t *)((char *)s->prune.ptr + ub_off);
       pr.summ32 = (const float *)s->summ32.ptr;
       pr.radius = (const float *)s->radius.ptr;
       pr.kr = s->kr;
       pr_ub = pr.ub;
       pr_thr = pr.thr;
+      pr_ctl = (int32_t *)s->prune.ptr;
       pr_ub_ld = pr.ub_ld;
       s->prune_ub_ld = pr.ub_ld;
     }
@@ -1876,7 +1933,7 @@ static int retrieve_impl(kiv_store_t *s, const kiv_retrieve_args_t *a, hipStream
         // Pass A's threshold per batch row, then pass B.
         hipLaunchKernelGGL(fine_threshold_kernel, dim3(B), dim3(kSelThreads), 0, st, (const uint32_t *)s->fine_keys.ptr,
                            ldc, (const int32_t *)s->counters.ptr, ps, (int)s->partial_len, a->out_width,
-                           (const uint32_t *)pr.ub, pr.ub_ld, hkv, (uint32_t *)pr.thr);
+                           (const uint32_t *)pr.ub, pr.ub_ld, hkv, (uint32_t *)pr.thr, pr.ctl);
         KIV_HIP(hipGetLastError());
         FinePrune pb = pr;
         pb.mode = 2;
@@ -1891,7 +1948,7 @@ static int retrieve_impl(kiv_store_t *s, const kiv_retrieve_args_t *a, hipStream
     with_select_chunks(cmax, [&](auto kern) {
       hipLaunchKernelGGL(kern, dim3(B), dim3(kSelThreads), 0, st, (uint32_t *)s->fine_keys.ptr, ldc,
                          (const int32_t *)s->counters.ptr, N > 0 ? 1 : 0, ps, (int)s->partial_len, a->out_width,
-                         fine_stats, list, list_ld, list_count, list_cap, pr_ub, pr_ub_ld, hkv, pr_thr);
+                         fine_stats, list, list_ld, list_count, list_cap, pr_ub, pr_ub_ld, hkv, pr_thr, pr_ctl);
     }, [](auto vc) { return fine_select_kernel<decltype(vc)::value>; });
     s->prof_end(KIV_STAGE_FINE_SELECT, st);
     KIV_HIP(hipGetLastError());
@@ -1974,8 +2031,9 @@ int kiv_fine_scan_stats(kiv_store_t *s, int64_t *scanned_slices, int64_t *union_
   if (s->prune_ub_ld > 0) {
     const int B = s->cfg.batch, hkv = s->cfg.num_kv_heads;
     std::vector<uint32_t> ub((size_t)s->kr * s->prune_ub_ld), thr(B);
-    KIV_HIP(hipMemcpy(ub.data(), s->prune.ptr, ub.size() * 4, hipMemcpyDeviceToHost));
-    KIV_HIP(hipMemcpy(thr.data(), (char *)s->prune.ptr + ub.size() * 4, thr.size() * 4, hipMemcpyDeviceToHost));
+    const size_t thr_off = 256, ub_off = thr_off + (((size_t)B * 4 + 255) & ~size_t(255));
+    KIV_HIP(hipMemcpy(ub.data(), (char *)s->prune.ptr + ub_off, ub.size() * 4, hipMemcpyDeviceToHost));
+    KIV_HIP(hipMemcpy(thr.data(), (char *)s->prune.ptr + thr_off, thr.size() * 4, hipMemcpyDeviceToHost));
     int64_t n = 0;
     for (int r = 0; r < s->kr; ++r)
       for (int v = 0; v < U; ++v) n += ub[(size_t)r * s->prune_ub_ld + v] >= thr[r / hkv];

@@ -46,6 +46,7 @@ def test_invalid_arguments_fail_without_gpu_work():
     assert lib.kiv_store_create(None, 0, None) == 1  # KIV_ERR_INVALID
     assert b"null" in lib.kiv_last_error()
     assert lib.kiv_retrieve(None, None, None) == 1
+    assert lib.kiv_fine_scan_stats(None, None, None) == 1
     assert lib.kiv_decode_attention(None, None) == 1
     assert lib.kiv_prefill_attention(None, None) == 1
     assert lib.kiv_prefill_workspace_size(0, 12, 128, 4096, 0, 8192) == 0

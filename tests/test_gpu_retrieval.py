@@ -301,15 +301,19 @@ def test_fine_pruning_keeps_the_selection(cuda, name, w, batch, clustered):
     store, oracle, cfg = build(w, data, cuda, chunks=(3000, 1, 511))
     q = data["q"]
     runs = {}
-    for prune in (True, False):
+    # Pruned, full, pruned again: after a call that skipped little (the
+    # unclustered case) the store pauses pruning and scans everything.
+    for i, prune in enumerate((True, False, True)):
         c = replace(cfg, fine_pruning=prune)
-        if prune:
+        if i == 0:
             k_out, v_out, sel = check_retrieval(store, oracle, c, w, data, q)
         else:
             k_out, v_out = store.retrieve_top_kv(q.to(cuda), w.scaling, c)
         snap = store.telemetry_snapshot()["recent"]
-        runs[prune] = (k_out.cpu(), v_out.cpu(), snap[-2]["pages_selected"], snap[-1], store.fine_scan_stats())
-    (k1, v1, u1, f1, s1), (k0, v0, u0, f0, s0) = runs[True], runs[False]
+        runs[i] = (k_out.cpu(), v_out.cpu(), snap[-2]["pages_selected"], snap[-1], store.fine_scan_stats())
+    (k1, v1, u1, f1, s1), (k0, v0, u0, f0, s0), (k2, v2, u2, f2, s2) = runs[0], runs[1], runs[2]
+    assert u2 == u0 and f2["selected_token_indices"] == f0["selected_token_indices"]
+    assert torch.equal(k2, k0) and torch.equal(v2, v0) and s2 == (s1 if clustered else s0)  # pruning kept / paused
     print(f"{name}: union {len(u1)} pages, slices read pruned {s1} full {s0}, "
           f"fine mean pruned {f1['mean_score']} full {f0['mean_score']}", flush=True)
     assert s0[0] == s0[1] == s1[1] == len(u1) * batch * w.num_kv_heads and s1[0] <= s1[1]
