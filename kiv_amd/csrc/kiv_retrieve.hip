@@ -876,7 +876,7 @@ struct FinePrune {
   const uint32_t *thr;       // [B] thresholds T (pass B)
   const float *summ32, *radius;  // page means [N][kr][D] and radii [N][kr]
   int kr;
-  const int32_t *ctl;        // > 0: pruning is paused for this call (full scan in pass A)
+  const int32_t *ctl;        // [0] > 0: pruning is paused for this call (full scan in pass A)
 };
 
 // Pruning pays when it skips pages: after a call whose scan read more than
@@ -1378,25 +1378,25 @@ __global__ void __launch_bounds__(kSelThreads) fine_select_kernel(
       }
       return hit;
     }, plist, sh.scan_tmp);
-    // The next call's pruning: the blocks add their slices read to ctl[1];
-    // the last block to count itself in ctl[2] sets the pause ctl[0] from
-    // the total and clears both counters.
+    // The next call's pruning: each block adds (1 << 40) + its slices read
+    // to one 64-bit counter (ctl[2..3]); the block whose add completes the
+    // count sets the pause ctl[0] from the total and clears the counter.
+    // (One atomic carries both, so no device-scope fence is needed: on
+    // MI355X that fence writes back the XCDs' L2s.)
     slices = wave_sum_i32(slices);
     if ((threadIdx.x & 63) == 0) sh.fcnt[threadIdx.x >> 6] = slices;
     __syncthreads();
     if (threadIdx.x == 0) {
-      int read = 0;
-      for (int w = 0; w < NT / 64; ++w) read += sh.fcnt[w];
-      atomicAdd(&ctl[1], read);
-      __threadfence();
-      if (atomicAdd(&ctl[2], 1) == (int)gridDim.x - 1) {
-        __threadfence();
-        const int64_t total = atomicAdd(&ctl[1], 0);
+      uint64_t read = 0;
+      for (int w = 0; w < NT / 64; ++w) read += (uint64_t)sh.fcnt[w];
+      unsigned long long *cnt = reinterpret_cast<unsigned long long *>(ctl + 2);
+      const uint64_t old = atomicAdd(cnt, (1ull << 40) + read);
+      if ((int64_t)(old >> 40) == (int64_t)gridDim.x - 1) {
+        const uint64_t total = (old & ((1ull << 40) - 1)) + read;
         const int c0 = atomicAdd(&ctl[0], 0);
-        const int64_t all = (int64_t)U * hkv * gridDim.x;
+        const uint64_t all = (uint64_t)U * hkv * gridDim.x;
         atomicExch(&ctl[0], c0 > 0 ? c0 - 1 : (4 * total > 3 * all ? kPruneRetry : 0));
-        atomicExch(&ctl[1], 0);
-        atomicExch(&ctl[2], 0);
+        atomicExch(cnt, 0ull);
       }
     }
     __syncthreads();  // fcnt is reused by the select below
