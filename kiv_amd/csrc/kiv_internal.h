@@ -78,8 +78,9 @@ struct kiv_store {
   int64_t num_pages = 0;    // finished pages
   int64_t partial_len = 0;  // tokens in the partial page
 
-  // Page summaries in HBM: [cap][kr][D] dtype and fp32, and each page row's
-  // radius [cap][kr] fp32: max over its tokens of |k - summ32| (L2).
+  // Page summaries in HBM: [cap][kr][D] dtype and fp32, and per page row
+  // [cap][kr][2] fp32: the radius max over its tokens of |k - s| (L2, s the
+  // dtype summary) and |s|.
   kiv::DevBuf summ, summ32, radius;
   int64_t summ_cap = 0;
 
@@ -103,8 +104,8 @@ struct kiv_store {
   kiv::DevBuf fine_keys;     // [B][ld] u32
   kiv::DevBuf sel_list;      // [B][list_ld] u64 top-P' candidates + [B] i32 counts
   kiv::DevBuf k_stage;       // [B*Hkv][ld][D] candidates' K rows (host tier)
-  kiv::DevBuf prune;         // pruned fine scan: [B*Hkv][ld] u32 page bound keys + [B] u32 thresholds
-  int64_t prune_ub_ld = 0;   // page-bound row stride of the last fine scan if it was pruned, else 0
+  kiv::DevBuf prune;         // pruned fine scan: control, [B] thresholds, [N][kr] upper and lower bound keys
+  bool prune_on = false;     // the last retrieval's fine scan was a pruned one
   bool union_valid = false;  // page_list / U hold the last coarse pass
   int64_t union_rows = 0;    // B*Hq*Q of that pass (bounds reuse)
   int64_t union_max = 0;     // grid bound of that pass

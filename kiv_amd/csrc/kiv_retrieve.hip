@@ -695,7 +695,7 @@ template <int DT, int KT>  // KT = head_dim / 32
 __global__ void __launch_bounds__(kScanThreads) coarse_scan_mfma_kernel(
     const char *__restrict__ summ, int64_t n_pages, int kr, const char *__restrict__ q, int64_t qs0,
     int64_t qs1, int64_t qs2, int hq, int hkv, int qlen, float scale, int round, uint32_t *__restrict__ keys,
-    int64_t ld) {
+    int64_t ld, const float *__restrict__ rad2, uint32_t *__restrict__ ubk, uint32_t *__restrict__ lbk) {
   static_assert(DT != DT_F32, "16-bit dtypes only");
   constexpr int64_t kRowBytes = (int64_t)KT * 64;  // 32 two-byte elements per K step
   const int r = blockIdx.y, b = r / hkv, kvh = r % hkv;
@@ -707,6 +707,14 @@ __global__ void __launch_bounds__(kScanThreads) coarse_scan_mfma_kernel(
   uint4 x[KT];
 #pragma unroll
   for (int kk = 0; kk < KT; ++kk) x[kk] = load16(row + kk * 64);
+  // Pruned fine scan (ubk set): the page row's score bounds over the kv
+  // row's query rows, s.q +- |q| rad widened by 1e-4 |q| (|s| + rad)
+  // (Cauchy-Schwarz around the dtype summary s; rad, |s| from eviction).
+  float rad = 0.f, sn = 0.f, hi = -INFINITY, lo = -INFINITY;
+  if (ubk && p < n_pages) {
+    rad = rad2[2 * (p * kr + r)];
+    sn = rad2[2 * (p * kr + r) + 1];
+  }
   for (int m0 = 0; m0 < GQ; m0 += 16) {
     const int j = m0 + col;
     uint4 qa[KT];
@@ -728,6 +736,40 @@ __global__ void __launch_bounds__(kScanThreads) coarse_scan_mfma_kernel(
         const int row_j = m0 + 4 * kg + i;
         if (row_j < GQ) keys[(int64_t)(r * GQ + row_j) * ld + p] = order_key(score_of<DT>(acc[i], scale, round != 0));
       }
+    }
+    if (ubk) {
+      // |q| of row m0 + col from this lane group's elements, then of the
+      // rows 4 kg + i this lane's results belong to.
+      float qq = 0.f;
+#pragma unroll
+      for (int kk = 0; kk < KT; ++kk) {
+        float f[8];
+        unpack_chunk<DT>(qa[kk], f);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) qq = fmaf(f[e], f[e], qq);
+      }
+      qq += __shfl_xor(qq, 16, 64);
+      qq += __shfl_xor(qq, 32, 64);
+      const float qnorm = sqrtf(qq);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float qn = __shfl(qnorm, 4 * kg + i, 64);
+        if (m0 + 4 * kg + i < GQ) {
+          const float w = qn * rad * 1.0001f + 1e-4f * qn * (sn + rad);
+          hi = fmaxf(hi, acc[i] + w);
+          lo = fmaxf(lo, acc[i] - w);
+        }
+      }
+    }
+  }
+  if (ubk) {
+    hi = fmaxf(hi, __shfl_xor(hi, 16, 64));
+    hi = fmaxf(hi, __shfl_xor(hi, 32, 64));
+    lo = fmaxf(lo, __shfl_xor(lo, 16, 64));
+    lo = fmaxf(lo, __shfl_xor(lo, 32, 64));
+    if (kg == 0 && p < n_pages) {
+      ubk[p * kr + r] = order_key(score_of<DT>(hi, scale, round != 0));
+      lbk[p * kr + r] = order_key(score_of<DT>(lo, scale, round != 0));
     }
   }
 }
@@ -853,272 +895,33 @@ __device__ void publish_union(const uint32_t *ubits, const int *urank, int words
 }
 
 // Exact pruning of a host-tier fine scan (one query pass, VALU scan).
-// Pass A (mode 1) scores, for each kv row r, its set A_r (the pages among
-// the first `a` entries of the lists of r's query rows) and the partial
-// page, and writes for every union page v the key of a bound on the scores
-// of v's tokens from r's query rows to ub[r][v] (0xffffffff for A_r).
-// After pass A a token's key is the max over the kv rows that scored it,
-// at most its final key, so fine_threshold_kernel's P'-th largest of such
-// keys is a lower bound T of each batch row's final P'-th largest key.
-// Pass B (mode 2) scores the slices (r, v) with T <= ub[r][v] < 0xffffffff.
-// A token whose final key reaches T gets it from a kv row whose page bound
-// reaches T, so every key >= T is exact and every other one stays below T:
-// the top P' and its order are unchanged.
+// page_bound_kernel writes, for every page of the rows' lists and every kv
+// row r, the keys of an upper and a lower bound on the scores of the page's
+// tokens from r's query rows (ub, lb: [N][kr]).  A token's key is the max
+// over kv rows of its scores, so it is at least the page's max over r of
+// lb; if m = ceil(k / page_size) union pages have that max >= T, at least
+// k candidates have keys >= T, and T is a lower bound of the batch row's
+// k-th largest key (k = min(P', n)).  Every fine-scan block takes the same
+// T per batch row (the per-wave bound of the select's first step over the
+// union pages' lower-bound keys) and scores the slices (page, r) with
+// ub >= T, plus the partial page.  A token whose key reaches T gets it
+// from a kv row whose page bound reaches T, so every key >= T is exact and
+// every other one stays below T: the top P' and its order are unchanged.
 constexpr int kPageListCap = 4096;  // union pages a block lists in LDS (pruned scans and selects)
 
 struct FinePrune {
-  int mode;                  // 0: no pruning, 1: pass A, 2: pass B
-  const int32_t *row_pages;  // [rows][kc] per-row page lists of the coarse select
-  int kc, a, words;          // a: list entries per query row in set A; words = ceil(N / 32)
-  int acap;                  // LDS entries for a set A_r's list (>= |A_r|)
-  uint32_t *ub;              // [B*Hkv][ub_ld] page bound keys
-  int64_t ub_ld;
-  const uint32_t *thr;       // [B] thresholds T (pass B)
-  const float *summ32, *radius;  // page means [N][kr][D] and radii [N][kr]
+  int mode;                  // 0: full scan, 1: pruned scan
+  const uint32_t *ub, *lb;   // [N][kr] page bound keys
   int kr;
-  const int32_t *ctl;        // [0] > 0: pruning is paused for this call (full scan in pass A)
+  uint32_t *thr;             // [B] thresholds T (written by block (0, b * Hkv))
+  int width;                 // P'
+  const int32_t *ctl;        // [0] > 0: pruning is paused for this call (full scan)
 };
 
 // Pruning pays when it skips pages: after a call whose scan read more than
-// three quarters of the union's pages, the next kPruneRetry calls on the
+// three quarters of the union's slices, the next kPruneRetry calls on the
 // store run the full scan (decided on the device by the fine select).
 constexpr int kPruneRetry = 32;
-
-// Key of a bound on the scores of a page row's tokens (one wave, lanes over
-// the head dim): q.k <= q.m + |q| |k - m| <= q.m + |q| rad for each of the
-// GQ query rows in LDS (Cauchy-Schwarz; m the page row's fp32 mean, rad its
-// radius), plus 1e-4 |q| (|m| + rad), which covers the fp32 rounding of the
-// scan's dot product (at most D 2^-24 |q| |k| for D <= 512) and of this
-// bound.  A score's dtype rounding and positive scale are monotone, so no
-// token of the page row scores a key above the returned one.
-template <int DT>
-__device__ uint32_t page_bound_key(const char *qraw, int GQ, int head_dim, const float *m, float rad, float scale,
-                                   bool round) {
-  constexpr int EB = Elem<DT>::BYTES;
-  constexpr int MV = 8;  // dims per lane (D <= 512)
-  const int l = threadIdx.x & 63;
-  float mv[MV], mm = 0.f;
-#pragma unroll
-  for (int i = 0; i < MV; ++i) {
-    const int e = l + 64 * i;
-    mv[i] = e < head_dim ? m[e] : 0.f;
-    mm = fmaf(mv[i], mv[i], mm);
-  }
-  const float mn = sqrtf(wave_sum(mm));
-  float best = -INFINITY;
-  for (int j = 0; j < GQ; ++j) {
-    const char *qrow = qraw + (size_t)j * head_dim * EB;
-    float dot = 0.f, qq = 0.f;
-#pragma unroll
-    for (int i = 0; i < MV; ++i) {
-      const int e = l + 64 * i;
-      if (e < head_dim) {
-        const float x = load_elem<DT>(qrow, e);
-        dot = fmaf(x, mv[i], dot);
-        qq = fmaf(x, x, qq);
-      }
-    }
-    dot = wave_sum(dot);
-    const float qn = sqrtf(wave_sum(qq));
-    best = fmaxf(best, dot + qn * rad * 1.0001f + 1e-4f * qn * (mn + rad));
-  }
-  return min(order_key(score_of<DT>(best, scale, round)), 0xfffffffeu);  // 0xffffffff marks set A
-}
-
-template <int DT, int LG>
-__global__ void __launch_bounds__(256) fine_scan_kernel(
-    int union_src, const int32_t *__restrict__ row_pages, int row_pages_n, int words, int32_t *page_list,
-    int32_t *counters,
-    const uint64_t *__restrict__ ktab, int chunk_shift, int64_t page_bytes, const char *__restrict__ part_k,
-    int partial_len, int page_size, int tpi, int hkv, int head_dim, const char *__restrict__ q, int64_t qs0,
-    int64_t qs1, int64_t qs2, int hq, int qlen, float scale, int round, uint32_t *__restrict__ out, int64_t ld,
-    const float *__restrict__ coarse_stats, int rows, int n_pages, int32_t *pages_out, int32_t *union_out,
-    float *stats_out, double *stats_accum, char *__restrict__ k_stage, const char *__restrict__ k_read,
-    FinePrune pr) {
-  constexpr int VEC = Elem<DT>::VEC, EB = Elem<DT>::BYTES;
-  constexpr int UT = kFineUT;
-  constexpr int NSLOT = 256 / LG;
-  extern __shared__ uint4 smem4[];
-  __shared__ int scan_tmp[4];
-  const int r = blockIdx.y, b = r / hkv, kvh = r % hkv;
-  const int G = hq / hkv, GQ = G * qlen, cpr = head_dim / VEC;
-  char *qraw = reinterpret_cast<char *>(smem4);  // [G*Q][D] dtype
-  uint32_t *ubits = reinterpret_cast<uint32_t *>(qraw + (size_t)GQ * head_dim * EB);
-  int *urank = reinterpret_cast<int *>(ubits + words);
-  uint32_t *abits = reinterpret_cast<uint32_t *>(urank + words + 1);  // pass A: set A's page bitmap,
-  int *alist = reinterpret_cast<int *>(abits + pr.words);              // its union ranks
-  int *apage = alist + pr.acap;                                        // and page ids
-  const int tid = threadIdx.x;
-  if (pr.mode == 2 && *pr.ctl > 0) return;  // paused: pass A scanned everything
-  const bool seta = pr.mode == 1 && *pr.ctl <= 0;  // pass A of a pruned scan (else a full scan)
-  if (seta) {
-    // Set A of this kv row: the first `a` entries of the lists of its G*Q
-    // query rows (coarse rows r * G*Q ..).
-    for (int w = tid; w < pr.words; w += 256) abits[w] = 0u;
-    __syncthreads();
-    for (int i = tid; i < GQ * pr.a; i += 256) {
-      const int page = pr.row_pages[((int64_t)r * GQ + i / pr.a) * pr.kc + i % pr.a];
-      atomicOr(&abits[page >> 5], 1u << (page & 31));
-    }
-  }
-  for (int i = tid; i < GQ * cpr; i += 256) {
-    const int j = i / cpr, c = i % cpr;
-    const int h = kvh * G + j / qlen, qp = j % qlen;
-    *reinterpret_cast<uint4 *>(qraw + ((size_t)j * head_dim + c * VEC) * EB) =
-        load16(q + ((int64_t)b * qs0 + (int64_t)h * qs1 + (int64_t)qp * qs2 + c * VEC) * EB);
-  }
-  int U = 0;
-  if (union_src == UNION_ROWS) {
-    U = rank_union<256>(row_pages, row_pages_n, words, ubits, urank, scan_tmp);
-    if (blockIdx.x == 0 && blockIdx.y == 0)
-      publish_union<DT>(ubits, urank, words, U, page_list, pages_out, counters, union_out, coarse_stats, rows,
-                        n_pages, round, stats_out, stats_accum);
-  } else if (union_src == UNION_LIST) {
-    U = counters[0];
-  }
-  __syncthreads();
-  int nA = 0;
-  if (seta) {
-    // Set A as a list (page order): a thread per bitmap word, offsets from
-    // a block scan of the words' popcounts; a page's union rank from the
-    // ranked union bitmap or by bisecting the union list.
-    for (int base = 0; base < pr.words; base += 256) {
-      const int w = base + tid;
-      const uint32_t bits = w < pr.words ? abits[w] : 0u;
-      int tot;
-      int pos = nA + block_incl_scan<256>(__popc(bits), scan_tmp, &tot) - __popc(bits);
-      for (uint32_t x = bits; x; x &= x - 1) {
-        const int bit = __ffs(x) - 1, page = w * 32 + bit;
-        int v;
-        if (union_src == UNION_ROWS) {
-          v = urank[w] + __popc(ubits[w] & ((1u << bit) - 1u));
-        } else {
-          int lo = 0, hi = U - 1;
-          while (lo < hi) {
-            const int mid = (lo + hi) >> 1;
-            if (page_list[mid] < page) lo = mid + 1;
-            else hi = mid;
-          }
-          v = lo;
-        }
-        alist[pos] = v;
-        apage[pos] = page;
-        ++pos;
-      }
-      nA += tot;
-    }
-    __syncthreads();
-  }
-  const int nsplit = (page_size + tpi - 1) / tpi;
-  const int slot = tid / LG, lane = tid % LG;
-  const bool on = lane < cpr;
-  const int64_t row_bytes = (int64_t)head_dim * EB;
-  // Scores tokens [0, ntok) of a slice (rows at rowbase, candidates cand0..)
-  // into their keys, staging the K rows when asked.
-  auto scan_slice = [&](const char *rowbase, int64_t cand0, int ntok) {
-    if (k_read) rowbase = k_read + ((int64_t)r * ld + cand0) * row_bytes;
-    for (int tb = 0; tb < ntok; tb += NSLOT * UT) {
-      uint4 x[UT];
-#pragma unroll
-      for (int i = 0; i < UT; ++i) {
-        const int t = tb + i * NSLOT + slot;
-        x[i] = (on && t < ntok) ? load16(rowbase + (int64_t)t * row_bytes + lane * VEC * EB)
-                                : make_uint4(0, 0, 0, 0);
-      }
-      if (k_stage) {
-#pragma unroll
-        for (int i = 0; i < UT; ++i) {
-          const int t = tb + i * NSLOT + slot;
-          if (on && t < ntok)
-            *reinterpret_cast<uint4 *>(k_stage + (((int64_t)r * ld + cand0 + t) * head_dim + lane * VEC) * EB) = x[i];
-        }
-      }
-#pragma unroll
-      for (int i = 0; i < UT; ++i) {
-        const int t = tb + i * NSLOT + slot;
-        if (t >= ntok) break;
-        float best = -INFINITY;
-        for (int j = 0; j < GQ; ++j) {
-          float part = 0.f;
-          if (on) part = chunk_dot<DT>(x[i], load16(qraw + ((size_t)j * head_dim + lane * VEC) * EB), 0.f);
-          best = fmaxf(best, score_of<DT>(group_sum<LG>(part), scale, round != 0));
-        }
-        if (lane == 0) atomicMax(&out[(int64_t)b * ld + cand0 + t], order_key(best));
-      }
-    }
-  };
-  auto page_rows = [&](int64_t page, int s) {
-    return reinterpret_cast<const char *>(ktab[page >> chunk_shift]) +
-           (page & ((int64_t(1) << chunk_shift) - 1)) * page_bytes +
-           ((int64_t)r * page_size + (int64_t)s * tpi) * row_bytes;
-  };
-  if (pr.mode == 2) {
-    // Pass B: per window of kPageListCap union pages, the pages whose bound
-    // for this kv row reaches the threshold (set A excluded) are listed in
-    // LDS, then their slices are spread over the blocks.
-    int *plist = alist;
-    const uint32_t tb = pr.thr[b];
-    const uint32_t *ubr = pr.ub + (int64_t)r * pr.ub_ld;
-    for (int base = 0; base < U; base += kPageListCap) {
-      const int nv = min(kPageListCap, U - base);
-      int nh = 0;
-      for (int c0 = 0; c0 < nv; c0 += 256) {
-        const int v = base + c0 + tid;
-        const bool in = c0 + tid < nv;  // (a zero threshold passes every key, so the range test is separate)
-        const uint32_t u = in ? ubr[v] : 0u;
-        const int hit = in && u != 0xffffffffu && u >= tb ? 1 : 0;
-        int tot;
-        const int pos = nh + block_incl_scan<256>(hit, scan_tmp, &tot) - hit;
-        if (hit) plist[pos] = v;
-        nh += tot;
-      }
-      __syncthreads();
-      for (int item = blockIdx.x; item < nh * nsplit; item += gridDim.x) {
-        const int v = plist[item / nsplit], s = item % nsplit;
-        const int64_t page = union_src == UNION_ROWS ? union_page(ubits, urank, words, v) : page_list[v];
-        scan_slice(page_rows(page, s), (int64_t)v * page_size + (int64_t)s * tpi, min(tpi, page_size - s * tpi));
-      }
-      __syncthreads();  // the list is rebuilt for the next window
-    }
-    return;
-  }
-  // Items: page slices (set A's pages in pass A), then the partial page's.
-  const int page_items = (seta ? nA : U) * nsplit;
-  const int items = page_items + (partial_len + tpi - 1) / tpi;
-  for (int item = blockIdx.x; item < items; item += gridDim.x) {
-    if (item < page_items) {
-      const int vi = item / nsplit, s = item % nsplit;
-      int v = vi;
-      int64_t page;
-      if (seta) {
-        v = alist[vi];
-        page = apage[vi];
-      } else {
-        page = union_src == UNION_ROWS ? union_page(ubits, urank, words, v) : page_list[v];
-      }
-      scan_slice(page_rows(page, s), (int64_t)v * page_size + (int64_t)s * tpi, min(tpi, page_size - s * tpi));
-    } else {
-      const int s = item - page_items;
-      scan_slice(part_k + ((int64_t)r * page_size + (int64_t)s * tpi) * row_bytes,
-                 (int64_t)U * page_size + (int64_t)s * tpi, min(tpi, partial_len - s * tpi));
-    }
-  }
-  if (pr.mode == 1) {
-    // Pass A: the bound key of every union page for this kv row, a page per
-    // wave (0xffffffff: scanned here, set A's pages or all when paused).
-    const int wave = tid >> 6;
-    for (int v = blockIdx.x * 4 + wave; v < U; v += gridDim.x * 4) {
-      uint32_t key = 0xffffffffu;
-      const int64_t page = !seta ? 0 : union_src == UNION_ROWS ? union_page(ubits, urank, words, v) : page_list[v];
-      if (seta && !((abits[page >> 5] >> (page & 31)) & 1u)) {
-        const int64_t prow = page * pr.kr + r;
-        key = page_bound_key<DT>(qraw, GQ, head_dim, pr.summ32 + prow * head_dim, pr.radius[prow], scale,
-                                 round != 0);
-      }
-      if ((tid & 63) == 0) pr.ub[(int64_t)r * pr.ub_ld + v] = key;
-    }
-  }
-}
 
 // Keys of a list of union pages (plist: their union ranks) then of the
 // partial page, as composites with their candidate index (union rank *
@@ -1186,39 +989,236 @@ template <int NT, typename Src> __device__ uint32_t block_kth_bound(const Src &s
   return bound;
 }
 
-// Threshold of a pruned fine scan: block b, after pass A, writes thr[b] = a
-// lower bound of the k-th largest final key of batch row b (k = min(P',
-// n)), taken over the keys pass A left on the pages of some kv row's set A
-// (ub == 0xffffffff), up to kPageListCap pages, and on the partial page:
-// each is at most its final key, so their k-th largest is at most the
-// row's; 0 (nothing is pruned) when fewer than k were scored.
-__global__ void __launch_bounds__(kSelThreads) fine_threshold_kernel(const uint32_t *__restrict__ keys, int64_t ld,
-                                                                     const int32_t *__restrict__ counters,
-                                                                     int page_size, int partial_len, int width,
-                                                                     const uint32_t *__restrict__ ub, int64_t ub_ld,
-                                                                     int hkv, uint32_t *__restrict__ thr,
-                                                                     const int32_t *__restrict__ ctl) {
-  constexpr int NT = kSelThreads;
-  __shared__ SelSh<NT> sh;
-  __shared__ int plist[kPageListCap];
-  const int b = blockIdx.x;
-  if (*ctl > 0) {  // paused: nothing to prune
-    if (threadIdx.x == 0) thr[b] = 0u;
+// Lower-bound keys of the union pages for batch row b (max over its kv
+// rows), entry v = union rank, as composites; sub-slots as in PageKeys.
+template <int NT, typename PageOf> struct UnionLowerKeys {
+  const uint32_t *lb;
+  int kr, r0, hkv, U;
+  PageOf page_of;
+  template <typename F> __device__ void each_slot(F &&f) const {
+    constexpr int W = NT / 64;
+    int u = 0;
+    for (int v = (threadIdx.x >> 6) + W * (threadIdx.x & 63); v < U; v += NT, ++u) {
+      const uint32_t *l = lb + (int64_t)page_of(v) * kr + r0;
+      uint32_t key = 0u;
+      for (int h = 0; h < hkv; ++h) key = max(key, l[h]);
+      f(comp_of(key, v), u & 3);
+    }
+  }
+  template <typename F> __device__ void each(F &&f) const {
+    each_slot([&](uint64_t x, int) { f(x); });
+  }
+};
+
+// Upper and lower bound keys of the pages in the rows' lists (used when the
+// coarse scan runs on the VALU; the MFMA scan writes them itself): block
+// (x, r) keeps kv row r's G*Q query rows (fp32) and their norms in LDS, and
+// wave w takes list entry e = 4 x + w.  For each query row, q.k lies within
+// q.s +- |q| |k - s| <= q.s +- |q| rad (Cauchy-Schwarz; s the page row's
+// dtype summary, rad its radius), widened by 1e-4 |q| (|s| + rad), which covers
+// the fp32 rounding of the scan's dot product (at most D 2^-24 |q| |k| for
+// D <= 512) and of the bound.  A score's dtype rounding and positive scale
+// are monotone, so every token's score from r lies within the keys of the
+// max over the rows of the bounds.  Entries repeat across lists; their
+// writes are equal.
+template <int DT>
+__global__ void __launch_bounds__(256) page_bound_kernel(
+    const int32_t *__restrict__ row_pages, int n_entries, const char *__restrict__ summ,
+    const float *__restrict__ rad2, int kr, int head_dim, int hkv, const char *__restrict__ q, int64_t qs0,
+    int64_t qs1, int64_t qs2, int hq, int qlen, float scale, int round, uint32_t *__restrict__ ub,
+    uint32_t *__restrict__ lb, const int32_t *__restrict__ ctl) {
+  constexpr int EB = Elem<DT>::BYTES;
+  constexpr int MV = 8;  // dims per lane (D <= 512)
+  extern __shared__ float qf[];  // [G*Q][D] fp32, then [G*Q] norms
+  if (*ctl > 0) return;  // pruning paused
+  const int r = blockIdx.y, b = r / hkv, kvh = r % hkv;
+  const int G = hq / hkv, GQ = G * qlen;
+  const int wave = threadIdx.x >> 6, l = threadIdx.x & 63;
+  float *qn = qf + (size_t)GQ * head_dim;
+  for (int i = threadIdx.x; i < GQ * head_dim; i += 256) {
+    const int j = i / head_dim, d = i % head_dim;
+    const int h = kvh * G + j / qlen, qp = j % qlen;
+    qf[i] = load_elem<DT>(q + ((int64_t)b * qs0 + (int64_t)h * qs1 + (int64_t)qp * qs2) * EB, d);
+  }
+  __syncthreads();
+  for (int j = wave; j < GQ; j += 4) {
+    float qq = 0.f;
+    for (int d = l; d < head_dim; d += 64) qq = fmaf(qf[j * head_dim + d], qf[j * head_dim + d], qq);
+    qq = wave_sum(qq);
+    if (l == 0) qn[j] = sqrtf(qq);
+  }
+  __syncthreads();
+  const int e = blockIdx.x * 4 + wave;
+  if (e >= n_entries) return;
+  const int64_t prow = (int64_t)row_pages[e] * kr + r;
+  const char *m = summ + prow * head_dim * EB;
+  float mv[MV];
+#pragma unroll
+  for (int i = 0; i < MV; ++i) {
+    const int d = l + 64 * i;
+    mv[i] = d < head_dim ? load_elem<DT>(m, d) : 0.f;
+  }
+  const float rad = rad2[2 * prow], mn = rad2[2 * prow + 1];
+  float hi = -INFINITY, lo = -INFINITY;
+  for (int j = 0; j < GQ; ++j) {
+    float dot = 0.f;
+#pragma unroll
+    for (int i = 0; i < MV; ++i) {
+      const int d = l + 64 * i;
+      if (d < head_dim) dot = fmaf(qf[j * head_dim + d], mv[i], dot);
+    }
+    dot = wave_sum(dot);
+    const float w = qn[j] * rad * 1.0001f + 1e-4f * qn[j] * (mn + rad);
+    hi = fmaxf(hi, dot + w);
+    lo = fmaxf(lo, dot - w);
+  }
+  if (l == 0) {
+    ub[prow] = order_key(score_of<DT>(hi, scale, round != 0));
+    lb[prow] = order_key(score_of<DT>(lo, scale, round != 0));
+  }
+}
+
+template <int DT, int LG>
+__global__ void __launch_bounds__(256) fine_scan_kernel(
+    int union_src, const int32_t *__restrict__ row_pages, int row_pages_n, int words, int32_t *page_list,
+    int32_t *counters,
+    const uint64_t *__restrict__ ktab, int chunk_shift, int64_t page_bytes, const char *__restrict__ part_k,
+    int partial_len, int page_size, int tpi, int hkv, int head_dim, const char *__restrict__ q, int64_t qs0,
+    int64_t qs1, int64_t qs2, int hq, int qlen, float scale, int round, uint32_t *__restrict__ out, int64_t ld,
+    const float *__restrict__ coarse_stats, int rows, int n_pages, int32_t *pages_out, int32_t *union_out,
+    float *stats_out, double *stats_accum, char *__restrict__ k_stage, const char *__restrict__ k_read,
+    FinePrune pr) {
+  constexpr int VEC = Elem<DT>::VEC, EB = Elem<DT>::BYTES;
+  constexpr int UT = kFineUT;
+  constexpr int NSLOT = 256 / LG;
+  extern __shared__ uint4 smem4[];
+  __shared__ int scan_tmp[4];
+  __shared__ SelSh<256> tsh;  // wave bounds of the pruning threshold
+  const int r = blockIdx.y, b = r / hkv, kvh = r % hkv;
+  const int G = hq / hkv, GQ = G * qlen, cpr = head_dim / VEC;
+  char *qraw = reinterpret_cast<char *>(smem4);  // [G*Q][D] dtype
+  uint32_t *ubits = reinterpret_cast<uint32_t *>(qraw + (size_t)GQ * head_dim * EB);
+  int *urank = reinterpret_cast<int *>(ubits + words);
+  int *plist = urank + words + 1;  // pruned scan: [kPageListCap] union ranks
+  const int tid = threadIdx.x;
+  const bool pruned = pr.mode == 1 && *pr.ctl <= 0;
+  for (int i = tid; i < GQ * cpr; i += 256) {
+    const int j = i / cpr, c = i % cpr;
+    const int h = kvh * G + j / qlen, qp = j % qlen;
+    *reinterpret_cast<uint4 *>(qraw + ((size_t)j * head_dim + c * VEC) * EB) =
+        load16(q + ((int64_t)b * qs0 + (int64_t)h * qs1 + (int64_t)qp * qs2 + c * VEC) * EB);
+  }
+  int U = 0;
+  if (union_src == UNION_ROWS) {
+    U = rank_union<256>(row_pages, row_pages_n, words, ubits, urank, scan_tmp);
+    if (blockIdx.x == 0 && blockIdx.y == 0)
+      publish_union<DT>(ubits, urank, words, U, page_list, pages_out, counters, union_out, coarse_stats, rows,
+                        n_pages, round, stats_out, stats_accum);
+  } else if (union_src == UNION_LIST) {
+    U = counters[0];
+  }
+  __syncthreads();
+  const int nsplit = (page_size + tpi - 1) / tpi;
+  const int slot = tid / LG, lane = tid % LG;
+  const bool on = lane < cpr;
+  const int64_t row_bytes = (int64_t)head_dim * EB;
+  // Scores tokens [0, ntok) of a slice (rows at rowbase, candidates cand0..)
+  // into their keys, staging the K rows when asked.
+  auto scan_slice = [&](const char *rowbase, int64_t cand0, int ntok) {
+    if (k_read) rowbase = k_read + ((int64_t)r * ld + cand0) * row_bytes;
+    for (int tb = 0; tb < ntok; tb += NSLOT * UT) {
+      uint4 x[UT];
+#pragma unroll
+      for (int i = 0; i < UT; ++i) {
+        const int t = tb + i * NSLOT + slot;
+        x[i] = (on && t < ntok) ? load16(rowbase + (int64_t)t * row_bytes + lane * VEC * EB)
+                                : make_uint4(0, 0, 0, 0);
+      }
+      if (k_stage) {
+#pragma unroll
+        for (int i = 0; i < UT; ++i) {
+          const int t = tb + i * NSLOT + slot;
+          if (on && t < ntok)
+            *reinterpret_cast<uint4 *>(k_stage + (((int64_t)r * ld + cand0 + t) * head_dim + lane * VEC) * EB) = x[i];
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < UT; ++i) {
+        const int t = tb + i * NSLOT + slot;
+        if (t >= ntok) break;
+        float best = -INFINITY;
+        for (int j = 0; j < GQ; ++j) {
+          float part = 0.f;
+          if (on) part = chunk_dot<DT>(x[i], load16(qraw + ((size_t)j * head_dim + lane * VEC) * EB), 0.f);
+          best = fmaxf(best, score_of<DT>(group_sum<LG>(part), scale, round != 0));
+        }
+        if (lane == 0) atomicMax(&out[(int64_t)b * ld + cand0 + t], order_key(best));
+      }
+    }
+  };
+  auto page_of = [&](int v) -> int64_t {
+    return union_src == UNION_ROWS ? union_page(ubits, urank, words, v) : page_list[v];
+  };
+  auto page_rows = [&](int64_t page, int s) {
+    return reinterpret_cast<const char *>(ktab[page >> chunk_shift]) +
+           (page & ((int64_t(1) << chunk_shift) - 1)) * page_bytes +
+           ((int64_t)r * page_size + (int64_t)s * tpi) * row_bytes;
+  };
+  const int part_items = (partial_len + tpi - 1) / tpi;
+  if (pruned) {
+    // Threshold T of batch row b, the same in every block: the per-wave
+    // bound of the m-th largest of the union pages' lower-bound keys (m =
+    // ceil(k / page_size) pages hold at least k candidates); 0 when U < m.
+    const int k = min(pr.width, U * page_size + partial_len);
+    const int m = (k + page_size - 1) / page_size;
+    uint32_t tb = 0u;
+    if (U >= m) {
+      const UnionLowerKeys<256, decltype(page_of)> src{pr.lb, pr.kr, b * hkv, hkv, U, page_of};
+      tb = block_kth_bound<256>(src, m, tsh);
+    }
+    if (blockIdx.x == 0 && kvh == 0 && tid == 0) pr.thr[b] = tb;
+    // Per window of kPageListCap union pages, the pages whose upper bound
+    // for this kv row reaches T are listed in LDS, then their slices are
+    // spread over the blocks; the partial page's slices follow.
+    const uint32_t *ubr = pr.ub + r;
+    for (int base = 0; base < U; base += kPageListCap) {
+      const int nv = min(kPageListCap, U - base);
+      int nh = 0;
+      for (int c0 = 0; c0 < nv; c0 += 256) {
+        const int v = base + c0 + tid;
+        const int hit = c0 + tid < nv && ubr[page_of(v) * pr.kr] >= tb ? 1 : 0;
+        int tot;
+        const int pos = nh + block_incl_scan<256>(hit, scan_tmp, &tot) - hit;
+        if (hit) plist[pos] = v;
+        nh += tot;
+      }
+      __syncthreads();
+      for (int item = blockIdx.x; item < nh * nsplit; item += gridDim.x) {
+        const int v = plist[item / nsplit], s = item % nsplit;
+        scan_slice(page_rows(page_of(v), s), (int64_t)v * page_size + (int64_t)s * tpi,
+                   min(tpi, page_size - s * tpi));
+      }
+      __syncthreads();  // the list is rebuilt for the next window
+    }
+    for (int item = blockIdx.x; item < part_items; item += gridDim.x)
+      scan_slice(part_k + ((int64_t)r * page_size + (int64_t)item * tpi) * row_bytes,
+                 (int64_t)U * page_size + (int64_t)item * tpi, min(tpi, partial_len - item * tpi));
     return;
   }
-  sel_init(sh);
-  const int U = counters[0];
-  const int n = U * page_size + partial_len, k = min(width, n);
-  const uint32_t *ub_b = ub + (int64_t)b * hkv * ub_ld;
-  const int na = min(list_pages<NT>(U, [&](int v) {
-    bool in_a = false;
-    for (int h = 0; h < hkv; ++h) in_a |= ub_b[(int64_t)h * ub_ld + v] == 0xffffffffu;
-    return in_a;
-  }, plist, sh.scan_tmp), kPageListCap);
-  const PageKeys<NT> src{keys + (int64_t)b * ld, plist, na * page_size, na * page_size + partial_len, page_size,
-                         (int64_t)U * page_size};
-  const uint32_t t = src.mall >= k ? block_kth_bound<NT>(src, k, sh) : 0u;
-  if (threadIdx.x == 0) thr[b] = t;
+  // Full scan: every union page's slices, then the partial page's.
+  if (pr.mode == 1 && blockIdx.x == 0 && kvh == 0 && tid == 0) pr.thr[b] = 0u;  // paused: all scanned
+  const int page_items = U * nsplit;
+  for (int item = blockIdx.x; item < page_items + part_items; item += gridDim.x) {
+    if (item < page_items) {
+      const int v = item / nsplit, s = item % nsplit;
+      scan_slice(page_rows(page_of(v), s), (int64_t)v * page_size + (int64_t)s * tpi,
+                 min(tpi, page_size - s * tpi));
+    } else {
+      const int s = item - page_items;
+      scan_slice(part_k + ((int64_t)r * page_size + (int64_t)s * tpi) * row_bytes,
+                 (int64_t)U * page_size + (int64_t)s * tpi, min(tpi, partial_len - s * tpi));
+    }
+  }
 }
 
 // MFMA fine scan for queries of many rows (G * Q >= kFineMfmaRows per kv
@@ -1348,8 +1348,8 @@ template <int V>
 __global__ void __launch_bounds__(kSelThreads) fine_select_kernel(
     uint32_t *__restrict__ keys, int64_t ld, const int32_t *__restrict__ counters, int has_pages, int page_size,
     int partial_len, int width, float *__restrict__ fine_stats, uint64_t *__restrict__ list, int64_t list_ld,
-    int32_t *__restrict__ list_count, int list_cap, const uint32_t *__restrict__ ub, int64_t ub_ld, int hkv,
-    const uint32_t *__restrict__ thr, int32_t *__restrict__ ctl) {
+    int32_t *__restrict__ list_count, int list_cap, const uint32_t *__restrict__ ub, int kr, int hkv,
+    const uint32_t *__restrict__ thr, int32_t *__restrict__ ctl, const int32_t *__restrict__ page_list) {
   constexpr int NT = kSelThreads;
   __shared__ SelSh<NT> sh;
   __shared__ uint64_t cand[kCandCap];
@@ -1367,12 +1367,12 @@ __global__ void __launch_bounds__(kSelThreads) fine_select_kernel(
     // Pruned fine scan: only the pages some kv row of b scanned (and the
     // partial page) hold nonzero keys; the others are not read.
     const uint32_t tb = thr[b];
-    const uint32_t *ub_b = ub + (int64_t)b * hkv * ub_ld;
     int slices = 0;  // (page, kv row) slices the scan read, this thread's pages
     const int np = list_pages<NT>(U, [&](int v) {
+      const uint32_t *ub_v = ub + (int64_t)page_list[v] * kr + b * hkv;
       bool hit = false;
       for (int h = 0; h < hkv; ++h) {
-        const bool read = ub_b[(int64_t)h * ub_ld + v] >= tb;
+        const bool read = ub_v[h] >= tb;
         hit |= read;
         slices += read;
       }
@@ -1469,8 +1469,8 @@ struct GatherArgs {
   int64_t page_bytes;
   const char *part_k, *part_v, *k_stage;
   int64_t stage_ld;
-  const uint32_t *ub, *thr;  // pruned fine scan: page bound keys and thresholds, or NULL
-  int64_t ub_ld;
+  const uint32_t *ub, *thr;  // pruned fine scan: page bound keys [N][kr] and thresholds, or NULL
+  int ub_kr;
   int page_size, partial_len;
   int64_t num_finalized;
   int batch, hkv, head_dim, width, cpr;
@@ -1560,6 +1560,7 @@ template <int DT> __device__ void gather_block(const GatherArgs &ga, int bx, int
     const char *ks;
     const char *vs;
     int64_t gid;
+    bool staged = k_stage != nullptr;
     if (cand < split) {
       const int64_t page = page_list[cand / page_size], t = cand % page_size;
       const int64_t off = (page & ((int64_t(1) << chunk_shift) - 1)) * page_bytes +
@@ -1567,6 +1568,8 @@ template <int DT> __device__ void gather_block(const GatherArgs &ga, int bx, int
       ks = reinterpret_cast<const char *>(ktab[page >> chunk_shift]) + off;
       vs = reinterpret_cast<const char *>(vtab[page >> chunk_shift]) + off;
       gid = page * page_size + t;
+      // A pruned scan staged the slice only if its bound reached T.
+      if (ga.ub) staged = staged && ga.ub[page * ga.ub_kr + r] >= ga.thr[b];
     } else {
       const int64_t t = cand - split;
       const int64_t off = (((int64_t)r * page_size + t) * head_dim + e0) * EB;
@@ -1574,9 +1577,6 @@ template <int DT> __device__ void gather_block(const GatherArgs &ga, int bx, int
       vs = part_v + off;
       gid = num_finalized + t;
     }
-    // Staged unless a pruned scan skipped the page for this kv row.
-    const bool staged = k_stage && (cand >= split || !ga.ub ||
-                                    ga.ub[(int64_t)r * ga.ub_ld + cand / page_size] >= ga.thr[b]);
     if (staged) ks = k_stage + (((int64_t)r * stage_ld + cand) * head_dim + e0) * EB;
     const int64_t o = (((int64_t)r * width + slot) * head_dim + e0) * EB;
     const uint4 kx = load16(ks), vx = load16(vs);
@@ -1675,6 +1675,44 @@ static int retrieve_impl(kiv_store_t *s, const kiv_retrieve_args_t *a, hipStream
   float *coarse_stats = (float *)s->row_stats.ptr;
   float *fine_stats = coarse_stats + 2 * rows;
 
+  // ---- exact pruning of the host tier's fine scan (KIV_RETRIEVE_PRUNE,
+  // see FinePrune): one query pass on the VALU scan, a fresh coarse pass,
+  // and row lists longer than the pages the top P' can fill.  The bounds
+  // come from the MFMA coarse scan (or page_bound_kernel after a VALU one).
+  const bool host_tier = c.cold_tier == KIV_TIER_HOST;
+  const int ktf = D / 32;
+  const bool fine_mfma = dt != KIV_DTYPE_F32 && D % 32 == 0 && (ktf <= 4 || ktf == 6 || ktf == 8) &&
+                         (G * Qb >= kFineMfmaRows || !host_tier) && a->scaling > 0.f;
+  const bool fresh = N > 0 && !(a->reuse_candidates && s->union_valid && s->union_rows == rows);
+  const bool prune = (a->flags & KIV_RETRIEVE_PRUNE) && host_tier && !fine_mfma && passes == 1 && fresh &&
+                     std::max(1, (a->out_width + ps - 1) / ps) < std::min(a->top_pages, N) && a->scaling > 0.f;
+  FinePrune pr{};
+  const uint32_t *pr_ub = nullptr, *pr_thr = nullptr;  // page bounds and thresholds of a pruned fine scan
+  int32_t *pr_ctl = nullptr;
+  s->prune_on = false;
+  if (prune) {
+    // [control, 256 B][thresholds [B]][upper bound keys [N][kr]][lower
+    // bound keys [N][kr]], zeroed (pruning on) when (re)allocated.
+    const size_t thr_off = 256, ub_off = thr_off + (((size_t)B * 4 + 255) & ~size_t(255));
+    const size_t nb_keys = (((size_t)N * s->kr + 63) & ~size_t(63)) * 4;
+    const size_t need = ub_off + 2 * nb_keys;
+    if (s->prune.bytes < need) {
+      if ((rc = s->prune.ensure(need, st, false))) return rc;
+      KIV_HIP(hipMemsetAsync(s->prune.ptr, 0, s->prune.bytes, st));
+    }
+    pr.mode = 1;
+    pr.ctl = (const int32_t *)s->prune.ptr;
+    pr.thr = (uint32_t *)((char *)s->prune.ptr + thr_off);
+    pr.ub = (const uint32_t *)((char *)s->prune.ptr + ub_off);
+    pr.lb = (const uint32_t *)((char *)s->prune.ptr + ub_off + nb_keys);
+    pr.kr = s->kr;
+    pr.width = a->out_width;
+    pr_ub = pr.ub;
+    pr_thr = pr.thr;
+    pr_ctl = (int32_t *)s->prune.ptr;
+    s->prune_on = true;
+  }
+
   // ---- coarse: page scan + per-row top pages
   int union_src = UNION_NONE;
   int64_t umax = 0;
@@ -1712,7 +1750,8 @@ static int retrieve_impl(kiv_store_t *s, const kiv_retrieve_args_t *a, hipStream
                 hipLaunchKernelGGL((coarse_scan_mfma_kernel<DTV, decltype(ktc)::value>), dim3(blocks, s->kr),
                                    dim3(kScanThreads), 0, st, (const char *)s->summ.ptr, (int64_t)N, s->kr, qp,
                                    a->q_stride[0], a->q_stride[1], a->q_stride[2], hq, hkv, Qp, a->scaling, round,
-                                   (uint32_t *)s->coarse_keys.ptr, ld);
+                                   (uint32_t *)s->coarse_keys.ptr, ld, (const float *)s->radius.ptr,
+                                   (uint32_t *)pr.ub, (uint32_t *)pr.lb);
                 return (int)KIV_OK;
               });
             }
@@ -1744,6 +1783,21 @@ static int retrieve_impl(kiv_store_t *s, const kiv_retrieve_args_t *a, hipStream
         s->prof_end(KIV_STAGE_COARSE_SELECT, st);
         KIV_HIP(hipGetLastError());
         row0 += rows_p;
+      }
+      if (prune && !mfma) {
+        // The VALU coarse scan leaves the pages' score bounds to this kernel.
+        const int n_entries = rows * kc;
+        rc = with_dt(dt, [&](auto dtc) {
+          hipLaunchKernelGGL((page_bound_kernel<decltype(dtc)::value>),
+                             dim3((unsigned)((n_entries + 3) / 4), (unsigned)s->kr), dim3(256),
+                             (size_t)G * Q * (D + 1) * 4, st, (const int32_t *)s->row_pages.ptr, n_entries,
+                             (const char *)s->summ.ptr, (const float *)s->radius.ptr, s->kr, D, hkv,
+                             (const char *)a->q, a->q_stride[0], a->q_stride[1], a->q_stride[2], hq, Q,
+                             a->scaling, round, (uint32_t *)pr.ub, (uint32_t *)pr.lb, pr.ctl);
+          return (int)KIV_OK;
+        });
+        if (rc) return rc;
+        KIV_HIP(hipGetLastError());
       }
       if (union_src == UNION_LIST) {
         // The union of every row list: marks in a page bitmap, then one
@@ -1796,9 +1850,6 @@ static int retrieve_impl(kiv_store_t *s, const kiv_retrieve_args_t *a, hipStream
   // Host tier: the fine scan copies the candidates' K rows to HBM as it
   // streams them, so the gather reads only V over the host link (up to
   // kMaxStageBytes of staging per store).
-  const uint32_t *pr_ub = nullptr, *pr_thr = nullptr;  // page bounds and thresholds of a pruned fine scan
-  int32_t *pr_ctl = nullptr;
-  int64_t pr_ub_ld = 0;
   char *k_stage = nullptr;
   const size_t stage_bytes = (size_t)s->kr * ldc * s->row_bytes;
   if (c.cold_tier == KIV_TIER_HOST && stage_bytes <= kMaxStageBytes) {
@@ -1809,7 +1860,6 @@ static int retrieve_impl(kiv_store_t *s, const kiv_retrieve_args_t *a, hipStream
     // Slices and grid per tier (see the fine scan kernel): host rows in
     // ~2 KiB slices over ~1024 blocks, HBM rows in 32-token slices over
     // ~2048 blocks.
-    const bool host_tier = c.cold_tier == KIV_TIER_HOST;
     int tpi = host_tier ? (int)std::max<int64_t>(1, 2048 / ((int64_t)D * eb)) : 32;
     tpi = std::min(tpi, ps);
     const int nsplit = (ps + tpi - 1) / tpi;
@@ -1868,48 +1918,10 @@ static int retrieve_impl(kiv_store_t *s, const kiv_retrieve_args_t *a, hipStream
       if (rc) return rc;
       KIV_HIP(hipGetLastError());
     }
-    // Exact pruning (KIV_RETRIEVE_PRUNE, see FinePrune): set A is the first
-    // ceil(P' / page_size) entries of every row's list, which hold the
-    // rows' best pages, so that pass A's P'-th largest key is close to the
-    // final one.
-    const int pa = std::min(kc, std::max(1, (a->out_width + ps - 1) / ps));
-    const bool prune = (a->flags & KIV_RETRIEVE_PRUNE) && host_tier && !mfma && passes == 1 && kc > 0 &&
-                       pa < kc && a->scaling > 0.f;
-    FinePrune pr{};
-    s->prune_ub_ld = 0;
-    if (prune) {
-      // [control, 256 B][thresholds [B]][page bounds [kr][ub_ld]], zeroed
-      // (pruning on) whenever the buffer is (re)allocated.
-      pr.ub_ld = (umax + 63) & ~int64_t(63);
-      const size_t thr_off = 256, ub_off = thr_off + (((size_t)B * 4 + 255) & ~size_t(255));
-      const size_t need = ub_off + (size_t)s->kr * pr.ub_ld * 4;
-      if (s->prune.bytes < need) {
-        if ((rc = s->prune.ensure(need, st, false))) return rc;
-        KIV_HIP(hipMemsetAsync(s->prune.ptr, 0, s->prune.bytes, st));
-      }
-      pr.mode = 1;
-      pr.row_pages = (const int32_t *)s->row_pages.ptr;
-      pr.kc = kc;
-      pr.a = pa;
-      pr.words = words;
-      pr.acap = (int)std::min<int64_t>((int64_t)G * Q * pa, umax);
-      pr.ctl = (const int32_t *)s->prune.ptr;
-      pr.thr = (const uint32_t *)((char *)s->prune.ptr + thr_off);
-      pr.ub = (uint32_t *)((char *)s->prune.ptr + ub_off);
-      pr.summ32 = (const float *)s->summ32.ptr;
-      pr.radius = (const float *)s->radius.ptr;
-      pr.kr = s->kr;
-      pr_ub = pr.ub;
-      pr_thr = pr.thr;
-      pr_ctl = (int32_t *)s->prune.ptr;
-      pr_ub_ld = pr.ub_ld;
-      s->prune_ub_ld = pr.ub_ld;
-    }
     auto valu_scan = [&](int pass, int usrc, int bw, const FinePrune &fp) {
       const int Qp = std::min(Qb, Q - pass * Qb);
       const size_t lds = (size_t)G * Qp * D * eb + (size_t)bw * 4 + (size_t)(bw + 1) * 4 +
-                         (fp.mode == 1 ? (size_t)fp.words * 4 + (size_t)fp.acap * 8 : 0) +
-                         (fp.mode == 2 ? (size_t)kPageListCap * 4 : 0);
+                         (fp.mode == 1 ? (size_t)kPageListCap * 4 : 0);
       return with_dt_lg(dt, lg, [&](auto dtc, auto lgc) {
         auto kern = fine_scan_kernel<decltype(dtc)::value, decltype(lgc)::value>;
         if (lds > 65536)
@@ -1929,17 +1941,6 @@ static int retrieve_impl(kiv_store_t *s, const kiv_retrieve_args_t *a, hipStream
     for (int pass = 0; pass < passes && !mfma; ++pass) {
       s->prof_begin(KIV_STAGE_FINE_SCAN, st);
       if ((rc = valu_scan(pass, union_src, bwords, pr))) return rc;
-      if (prune) {
-        // Pass A's threshold per batch row, then pass B.
-        hipLaunchKernelGGL(fine_threshold_kernel, dim3(B), dim3(kSelThreads), 0, st, (const uint32_t *)s->fine_keys.ptr,
-                           ldc, (const int32_t *)s->counters.ptr, ps, (int)s->partial_len, a->out_width,
-                           (const uint32_t *)pr.ub, pr.ub_ld, hkv, (uint32_t *)pr.thr, pr.ctl);
-        KIV_HIP(hipGetLastError());
-        FinePrune pb = pr;
-        pb.mode = 2;
-        pb.words = 0;  // pass B lists its pages where set A's bitmap was
-        if ((rc = valu_scan(pass, UNION_LIST, 0, pb))) return rc;
-      }
       s->prof_end(KIV_STAGE_FINE_SCAN, st);
     }
   }
@@ -1948,7 +1949,8 @@ static int retrieve_impl(kiv_store_t *s, const kiv_retrieve_args_t *a, hipStream
     with_select_chunks(cmax, [&](auto kern) {
       hipLaunchKernelGGL(kern, dim3(B), dim3(kSelThreads), 0, st, (uint32_t *)s->fine_keys.ptr, ldc,
                          (const int32_t *)s->counters.ptr, N > 0 ? 1 : 0, ps, (int)s->partial_len, a->out_width,
-                         fine_stats, list, list_ld, list_count, list_cap, pr_ub, pr_ub_ld, hkv, pr_thr, pr_ctl);
+                         fine_stats, list, list_ld, list_count, list_cap, pr_ub, s->kr, hkv, pr_thr, pr_ctl,
+                         (const int32_t *)s->page_list.ptr);
     }, [](auto vc) { return fine_select_kernel<decltype(vc)::value>; });
     s->prof_end(KIV_STAGE_FINE_SELECT, st);
     KIV_HIP(hipGetLastError());
@@ -1972,7 +1974,7 @@ static int retrieve_impl(kiv_store_t *s, const kiv_retrieve_args_t *a, hipStream
     ga.stage_ld = ldc;
     ga.ub = pr_ub;
     ga.thr = pr_thr;
-    ga.ub_ld = pr_ub_ld;
+    ga.ub_kr = s->kr;
     ga.page_size = ps;
     ga.partial_len = (int)s->partial_len;
     ga.num_finalized = s->num_pages * ps;
@@ -2028,15 +2030,17 @@ int kiv_fine_scan_stats(kiv_store_t *s, int64_t *scanned_slices, int64_t *union_
   KIV_HIP(hipMemcpy(&U, s->counters.ptr, sizeof(U), hipMemcpyDeviceToHost));
   *union_slices = (int64_t)U * s->kr;
   *scanned_slices = *union_slices;
-  if (s->prune_ub_ld > 0) {
-    const int B = s->cfg.batch, hkv = s->cfg.num_kv_heads;
-    std::vector<uint32_t> ub((size_t)s->kr * s->prune_ub_ld), thr(B);
+  if (s->prune_on && U > 0) {
+    const int B = s->cfg.batch, hkv = s->cfg.num_kv_heads, N = (int)s->num_pages;
     const size_t thr_off = 256, ub_off = thr_off + (((size_t)B * 4 + 255) & ~size_t(255));
+    std::vector<uint32_t> ub((size_t)N * s->kr), thr(B);
+    std::vector<int32_t> pages(U);
     KIV_HIP(hipMemcpy(ub.data(), (char *)s->prune.ptr + ub_off, ub.size() * 4, hipMemcpyDeviceToHost));
     KIV_HIP(hipMemcpy(thr.data(), (char *)s->prune.ptr + thr_off, thr.size() * 4, hipMemcpyDeviceToHost));
+    KIV_HIP(hipMemcpy(pages.data(), s->page_list.ptr, pages.size() * 4, hipMemcpyDeviceToHost));
     int64_t n = 0;
-    for (int r = 0; r < s->kr; ++r)
-      for (int v = 0; v < U; ++v) n += ub[(size_t)r * s->prune_ub_ld + v] >= thr[r / hkv];
+    for (int v = 0; v < U; ++v)
+      for (int r = 0; r < s->kr; ++r) n += ub[(size_t)pages[v] * s->kr + r] >= thr[r / hkv];
     *scanned_slices = n;
   }
   return KIV_OK;

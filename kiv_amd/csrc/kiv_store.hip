@@ -178,13 +178,13 @@ __global__ void __launch_bounds__(256) evict_finalize_kernel(
     const int64_t o = ((int64_t)page * kr + r) * head_dim + d;
     summ32[o] = m32;
     store_elem<DT>(summ, o, m32);
-    mu[d] = m32;
+    mu[d] = round_act<DT>(m32);  // the dtype summary the coarse scan reads
   }
   __syncthreads();
-  // Radius: max over the page's tokens of |k - mean| in fp32, the tokens'
-  // squared distances summed over their chunks in LDS, one token per group
-  // and round.  (Its rounding is covered by the relative margin of the
-  // retrieval's page bound.)
+  // Radius: max over the page's tokens of |k - s| in fp32 (s the dtype
+  // summary), the tokens' squared distances summed over their chunks in
+  // LDS, one token per group and round; and |s|.  (Their rounding is
+  // covered by the relative margin of the retrieval's page bound.)
   float rmax = 0.f;
   for (int t0 = 0; t0 < page_size; t0 += groups) {
     const int t = t0 + g;
@@ -208,11 +208,16 @@ __global__ void __launch_bounds__(256) evict_finalize_kernel(
     __syncthreads();
   }
   if (g < groups && c == 0) gmax[g] = rmax;
+  float ss = 0.f;
+  for (int d = threadIdx.x; d < head_dim; d += 256) ss = fmaf(mu[d], mu[d], ss);
+  part[threadIdx.x] = ss;
   __syncthreads();
   if (threadIdx.x == 0) {
-    float m = 0.f;
+    float m = 0.f, n2 = 0.f;
     for (int gg = 0; gg < groups; ++gg) m = fmaxf(m, gmax[gg]);
-    radius[page * kr + r] = sqrtf(m);
+    for (int t = 0; t < 256; ++t) n2 += part[t];
+    radius[2 * (page * kr + r)] = sqrtf(m);
+    radius[2 * (page * kr + r) + 1] = sqrtf(n2);
   }
 }
 
@@ -317,7 +322,7 @@ static int ensure_summaries(kiv_store *s, int64_t pages, hipStream_t st) {
   if (rc) return rc;
   rc = s->summ32.ensure(cap * row * 4, st, true);
   if (rc) return rc;
-  rc = s->radius.ensure(cap * s->kr * 4, st, true);
+  rc = s->radius.ensure(cap * s->kr * 8, st, true);
   if (rc) return rc;
   s->summ_cap = cap;
   return KIV_OK;
