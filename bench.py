@@ -245,7 +245,7 @@ def probes(dev, summary_bytes, host_bytes, cold):
     }
 
 
-def roofline_and_links(w, store, stages, union_pages, tier, scanned_slices=None):
+def roofline_and_links(w, store, stages, union_pages, tier, scanned_slices=None, pruning=False):
     """Algorithmic bytes per launch / measured duration for every stage.
     scanned_slices: (union page, kv row) slices the fine scan read (fewer
     than union_pages * Hkv when the host tier's scan is pruned)."""
@@ -258,9 +258,12 @@ def roofline_and_links(w, store, stages, union_pages, tier, scanned_slices=None)
     p = store.cold_length - N * w.page_size
     cand = union_pages * w.page_size + p
     rows = w.num_q_heads
+    # With the host tier's pruning the summary scan also reads each page
+    # row's radius and norm (8 bytes) and writes its two bound keys (8 bytes).
+    bounds = 16 * N * w.num_kv_heads if tier == "host" and pruning else 0
     traffic = {
         # (bytes per launch, memory it streams from)
-        "coarse_scan": (N * row, "hbm"),
+        "coarse_scan": (N * row + bounds, "hbm"),
         "coarse_select": (rows * N * 4, "hbm"),
         # Pruned (host tier): pass A, threshold, page bounds and pass B
         # together; the bytes are the slices read.
@@ -633,7 +636,8 @@ def main():
         snap = store.telemetry_snapshot()
         unions = [r["num_pages_selected"] for r in snap["recent"] if r["kind"] == "coarse" and not r["skipped"]]
         entry["union_pages"] = int(round(sum(unions) / len(unions))) if unions else 0
-        entry["traffic"] = roofline_and_links(w, store, stages, entry["union_pages"], tier, slices[0])
+        entry["traffic"] = roofline_and_links(w, store, stages, entry["union_pages"], tier, slices[0],
+                                              cfg.fine_pruning)
         entry["num_pages"] = store.num_pages
         results[tier] = entry
         del store

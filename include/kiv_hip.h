@@ -78,13 +78,15 @@ typedef struct {
   int64_t reserved_bytes;/* everything the store holds, host + device */
 } kiv_store_info_t;
 
-/* Retrieval flags.  KIV_RETRIEVE_PRUNE: on the host tier, the fine scan
- * first scores the pages at the head of the rows' lists, then skips every
- * other union page whose tokens provably cannot reach the top P' (a bound
- * from the page's mean and radius).  The selection, its order and the
- * returned rows are unchanged; the fine telemetry's mean then covers the
- * scored candidates only.  Applies to one-pass queries whose fine scan runs
- * on the vector units (G * Q < 32) with a positive scaling. */
+/* Retrieval flags.  KIV_RETRIEVE_PRUNE: on the host tier, the coarse scan
+ * also bounds every page's token scores (from a per-page radius recorded at
+ * eviction) and the fine scan reads only the pages whose bound can reach
+ * the top P' (a threshold from the pages' lower bounds).  The selection,
+ * its order and the returned rows are unchanged; the fine telemetry's mean
+ * then covers the scored candidates only.  Applies to one-pass queries
+ * whose fine scan runs on the vector units (G * Q < 32) with a fresh
+ * coarse pass and a positive scaling; it pauses itself for 32 calls after
+ * a call that skipped under a quarter of the union. */
 enum { KIV_RETRIEVE_PRUNE = 1 };
 
 /* Arguments of one retrieval: coarse page scan, union of per-row top

@@ -32,14 +32,13 @@ class KIVConfig:
                      "fp32": rank on the fp32 scores.
     reserve_tokens   optional capacity hint; the store pre-sizes its page
                      arrays for this many cold tokens.
-    fine_pruning     host tier: the fine scan scores the pages at the head of
-                     the per-head page lists first, then skips the union
-                     pages whose tokens provably cannot reach the top P (a
-                     bound from each page's mean K and radius), which cuts
-                     host-link reads.  Selected tokens, their order and the
-                     returned rows are the same as without it; the fine
-                     telemetry's mean_score then averages the scored
-                     candidates only.
+    fine_pruning     host tier: the coarse scan also bounds each page's token
+                     scores (from the page's summary and radius), and the
+                     fine scan reads only the union pages whose bound can
+                     reach the top P, which cuts host-link reads.  Selected
+                     tokens, their order and the returned rows are the same
+                     as without it; the fine telemetry's mean_score then
+                     averages the scored candidates only.
     """
 
     hot_budget: int = 2048
