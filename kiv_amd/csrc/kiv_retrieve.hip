@@ -916,6 +916,13 @@ struct FinePrune {
   uint32_t *thr;             // [B] thresholds T (written by block (0, b * Hkv))
   int width;                 // P'
   const int32_t *ctl;        // [0] > 0: pruning is paused for this call (full scan)
+  // Compact K staging (when the candidate-indexed staging would not fit):
+  // the slice at position i of kv row r's scan list goes to slot i of
+  // cstage[r][scap][page_size][D], and slot_of[page][r] records it (-1:
+  // not staged, position >= scap).
+  char *cstage;
+  int32_t *slot_of;
+  int scap;
 };
 
 // Pruning pays when it skips pages: after a call whose scan read more than
@@ -1124,7 +1131,7 @@ __global__ void __launch_bounds__(256) fine_scan_kernel(
   const int64_t row_bytes = (int64_t)head_dim * EB;
   // Scores tokens [0, ntok) of a slice (rows at rowbase, candidates cand0..)
   // into their keys, staging the K rows when asked.
-  auto scan_slice = [&](const char *rowbase, int64_t cand0, int ntok) {
+  auto scan_slice = [&](const char *rowbase, int64_t cand0, int ntok, char *stage) {
     if (k_read) rowbase = k_read + ((int64_t)r * ld + cand0) * row_bytes;
     for (int tb = 0; tb < ntok; tb += NSLOT * UT) {
       uint4 x[UT];
@@ -1134,12 +1141,11 @@ __global__ void __launch_bounds__(256) fine_scan_kernel(
         x[i] = (on && t < ntok) ? load16(rowbase + (int64_t)t * row_bytes + lane * VEC * EB)
                                 : make_uint4(0, 0, 0, 0);
       }
-      if (k_stage) {
+      if (stage) {
 #pragma unroll
         for (int i = 0; i < UT; ++i) {
           const int t = tb + i * NSLOT + slot;
-          if (on && t < ntok)
-            *reinterpret_cast<uint4 *>(k_stage + (((int64_t)r * ld + cand0 + t) * head_dim + lane * VEC) * EB) = x[i];
+          if (on && t < ntok) *reinterpret_cast<uint4 *>(stage + (int64_t)t * row_bytes + lane * VEC * EB) = x[i];
         }
       }
 #pragma unroll
@@ -1164,6 +1170,10 @@ __global__ void __launch_bounds__(256) fine_scan_kernel(
            (page & ((int64_t(1) << chunk_shift) - 1)) * page_bytes +
            ((int64_t)r * page_size + (int64_t)s * tpi) * row_bytes;
   };
+  // Candidate-indexed staging of candidate cand0's row (when staging).
+  auto stage_at = [&](int64_t cand0) -> char * {
+    return k_stage ? k_stage + ((int64_t)r * ld + cand0) * row_bytes : nullptr;
+  };
   const int part_items = (partial_len + tpi - 1) / tpi;
   if (pruned) {
     // Threshold T of batch row b, the same in every block: the per-wave
@@ -1181,6 +1191,7 @@ __global__ void __launch_bounds__(256) fine_scan_kernel(
     // for this kv row reaches T are listed in LDS, then their slices are
     // spread over the blocks; the partial page's slices follow.
     const uint32_t *ubr = pr.ub + r;
+    int listed = 0;  // pages listed in earlier windows (the compact staging's slot base)
     for (int base = 0; base < U; base += kPageListCap) {
       const int nv = min(kPageListCap, U - base);
       int nh = 0;
@@ -1194,15 +1205,24 @@ __global__ void __launch_bounds__(256) fine_scan_kernel(
       }
       __syncthreads();
       for (int item = blockIdx.x; item < nh * nsplit; item += gridDim.x) {
-        const int v = plist[item / nsplit], s = item % nsplit;
-        scan_slice(page_rows(page_of(v), s), (int64_t)v * page_size + (int64_t)s * tpi,
-                   min(tpi, page_size - s * tpi));
+        const int i = item / nsplit, v = plist[i], s = item % nsplit;
+        const int64_t page = page_of(v), cand0 = (int64_t)v * page_size + (int64_t)s * tpi;
+        char *stage = stage_at(cand0);
+        if (pr.cstage) {
+          const int sl = listed + i < pr.scap ? listed + i : -1;
+          if (s == 0 && tid == 0) pr.slot_of[page * pr.kr + r] = sl;
+          if (sl >= 0) stage = pr.cstage + (((int64_t)r * pr.scap + sl) * page_size + (int64_t)s * tpi) * row_bytes;
+        }
+        scan_slice(page_rows(page, s), cand0, min(tpi, page_size - s * tpi), stage);
       }
+      listed += nh;
       __syncthreads();  // the list is rebuilt for the next window
     }
-    for (int item = blockIdx.x; item < part_items; item += gridDim.x)
-      scan_slice(part_k + ((int64_t)r * page_size + (int64_t)item * tpi) * row_bytes,
-                 (int64_t)U * page_size + (int64_t)item * tpi, min(tpi, partial_len - item * tpi));
+    for (int item = blockIdx.x; item < part_items; item += gridDim.x) {
+      const int64_t cand0 = (int64_t)U * page_size + (int64_t)item * tpi;
+      scan_slice(part_k + ((int64_t)r * page_size + (int64_t)item * tpi) * row_bytes, cand0,
+                 min(tpi, partial_len - item * tpi), stage_at(cand0));
+    }
     return;
   }
   // Full scan: every union page's slices, then the partial page's.
@@ -1211,12 +1231,20 @@ __global__ void __launch_bounds__(256) fine_scan_kernel(
   for (int item = blockIdx.x; item < page_items + part_items; item += gridDim.x) {
     if (item < page_items) {
       const int v = item / nsplit, s = item % nsplit;
-      scan_slice(page_rows(page_of(v), s), (int64_t)v * page_size + (int64_t)s * tpi,
-                 min(tpi, page_size - s * tpi));
+      const int64_t page = page_of(v), cand0 = (int64_t)v * page_size + (int64_t)s * tpi;
+      char *stage = stage_at(cand0);
+      if (pr.mode == 1 && pr.cstage) {
+        // Paused pruning: the compact staging's slots are the union ranks.
+        const int sl = v < pr.scap ? v : -1;
+        if (s == 0 && tid == 0) pr.slot_of[page * pr.kr + r] = sl;
+        if (sl >= 0) stage = pr.cstage + (((int64_t)r * pr.scap + sl) * page_size + (int64_t)s * tpi) * row_bytes;
+      }
+      scan_slice(page_rows(page, s), cand0, min(tpi, page_size - s * tpi), stage);
     } else {
       const int s = item - page_items;
-      scan_slice(part_k + ((int64_t)r * page_size + (int64_t)s * tpi) * row_bytes,
-                 (int64_t)U * page_size + (int64_t)s * tpi, min(tpi, partial_len - s * tpi));
+      const int64_t cand0 = (int64_t)U * page_size + (int64_t)s * tpi;
+      scan_slice(part_k + ((int64_t)r * page_size + (int64_t)s * tpi) * row_bytes, cand0,
+                 min(tpi, partial_len - s * tpi), stage_at(cand0));
     }
   }
 }
@@ -1471,6 +1499,9 @@ struct GatherArgs {
   int64_t stage_ld;
   const uint32_t *ub, *thr;  // pruned fine scan: page bound keys [N][kr] and thresholds, or NULL
   int ub_kr;
+  const char *cstage;        // pruned fine scan's compact K staging (see FinePrune), or NULL
+  const int32_t *slot_of;
+  int scap;
   int page_size, partial_len;
   int64_t num_finalized;
   int batch, hkv, head_dim, width, cpr;
@@ -1569,7 +1600,14 @@ template <int DT> __device__ void gather_block(const GatherArgs &ga, int bx, int
       vs = reinterpret_cast<const char *>(vtab[page >> chunk_shift]) + off;
       gid = page * page_size + t;
       // A pruned scan staged the slice only if its bound reached T.
-      if (ga.ub) staged = staged && ga.ub[page * ga.ub_kr + r] >= ga.thr[b];
+      if (ga.ub) {
+        const bool scanned = ga.ub[page * ga.ub_kr + r] >= ga.thr[b];
+        staged = staged && scanned;
+        if (ga.cstage && scanned) {
+          const int sl = ga.slot_of[page * ga.ub_kr + r];
+          if (sl >= 0) ks = ga.cstage + ((((int64_t)r * ga.scap + sl) * page_size + t) * head_dim + e0) * EB;
+        }
+      }
     } else {
       const int64_t t = cand - split;
       const int64_t off = (((int64_t)r * page_size + t) * head_dim + e0) * EB;
@@ -1692,10 +1730,11 @@ static int retrieve_impl(kiv_store_t *s, const kiv_retrieve_args_t *a, hipStream
   s->prune_on = false;
   if (prune) {
     // [control, 256 B][thresholds [B]][upper bound keys [N][kr]][lower
-    // bound keys [N][kr]], zeroed (pruning on) when (re)allocated.
+    // bound keys [N][kr]][compact staging slots [N][kr]], zeroed (pruning
+    // on) when (re)allocated.
     const size_t thr_off = 256, ub_off = thr_off + (((size_t)B * 4 + 255) & ~size_t(255));
     const size_t nb_keys = (((size_t)N * s->kr + 63) & ~size_t(63)) * 4;
-    const size_t need = ub_off + 2 * nb_keys;
+    const size_t need = ub_off + 3 * nb_keys;
     if (s->prune.bytes < need) {
       if ((rc = s->prune.ensure(need, st, false))) return rc;
       KIV_HIP(hipMemsetAsync(s->prune.ptr, 0, s->prune.bytes, st));
@@ -1705,6 +1744,7 @@ static int retrieve_impl(kiv_store_t *s, const kiv_retrieve_args_t *a, hipStream
     pr.thr = (uint32_t *)((char *)s->prune.ptr + thr_off);
     pr.ub = (const uint32_t *)((char *)s->prune.ptr + ub_off);
     pr.lb = (const uint32_t *)((char *)s->prune.ptr + ub_off + nb_keys);
+    pr.slot_of = (int32_t *)((char *)s->prune.ptr + ub_off + 2 * nb_keys);
     pr.kr = s->kr;
     pr.width = a->out_width;
     pr_ub = pr.ub;
@@ -1855,6 +1895,16 @@ static int retrieve_impl(kiv_store_t *s, const kiv_retrieve_args_t *a, hipStream
   if (c.cold_tier == KIV_TIER_HOST && stage_bytes <= kMaxStageBytes) {
     if ((rc = s->k_stage.ensure(stage_bytes, st, false))) return rc;
     k_stage = (char *)s->k_stage.ptr;
+  } else if (prune) {
+    // Too many candidates to stage by index: the pruned scan stages its
+    // first scap slices per kv row compactly (4x the pages the top P' fills).
+    const int64_t slice_bytes = (int64_t)ps * s->row_bytes;
+    const int64_t want = std::min<int64_t>(umax, 4 * (int64_t)std::max(1, (a->out_width + ps - 1) / ps));
+    pr.scap = (int)std::min<int64_t>(want, (int64_t)kMaxStageBytes / ((int64_t)s->kr * slice_bytes));
+    if (pr.scap > 0) {
+      if ((rc = s->k_stage.ensure((size_t)s->kr * pr.scap * slice_bytes, st, false))) return rc;
+      pr.cstage = (char *)s->k_stage.ptr;
+    }
   }
   {
     // Slices and grid per tier (see the fine scan kernel): host rows in
@@ -1975,6 +2025,9 @@ static int retrieve_impl(kiv_store_t *s, const kiv_retrieve_args_t *a, hipStream
     ga.ub = pr_ub;
     ga.thr = pr_thr;
     ga.ub_kr = s->kr;
+    ga.cstage = pr.cstage;
+    ga.slot_of = pr.slot_of;
+    ga.scap = pr.scap;
     ga.page_size = ps;
     ga.partial_len = (int)s->partial_len;
     ga.num_finalized = s->num_pages * ps;
