@@ -24,6 +24,7 @@
 // telemetry.  No kernel waits on another block of its own grid, and no
 // kernel uses device-scope atomics.
 #include <algorithm>
+#include <cstdlib>
 #include <type_traits>
 #include <vector>
 
@@ -45,6 +46,12 @@ constexpr int kRankCap = 1024;      // candidates a coarse select ranks by count
 // grid), kCandCap above (wide selections then skip the exact search).
 inline int fine_list_cap(int width) { return width > kRankCap / 2 ? kCandCap : kRankCap; }
 constexpr size_t kMaxStageBytes = size_t(256) << 20;  // HBM staging of candidate K rows per store
+// The staging cap: kMaxStageBytes, or KIV_STAGE_CAP_BYTES from the
+// environment (tests use a small cap to reach the compact staging).
+inline size_t stage_cap() {
+  const char *e = std::getenv("KIV_STAGE_CAP_BYTES");
+  return e && *e ? (size_t)std::strtoull(e, nullptr, 10) : kMaxStageBytes;
+}
 constexpr int64_t kFineQueryBytes = 48 << 10;  // query rows per kv row the fine scan keeps in LDS
 constexpr int64_t kRowListInScan = 8192;        // row-list entries a fine-scan block ORs into its union
 constexpr int kUnionThreads = 1024;
@@ -1892,7 +1899,8 @@ static int retrieve_impl(kiv_store_t *s, const kiv_retrieve_args_t *a, hipStream
   // kMaxStageBytes of staging per store).
   char *k_stage = nullptr;
   const size_t stage_bytes = (size_t)s->kr * ldc * s->row_bytes;
-  if (c.cold_tier == KIV_TIER_HOST && stage_bytes <= kMaxStageBytes) {
+  const size_t cap_bytes = stage_cap();
+  if (c.cold_tier == KIV_TIER_HOST && stage_bytes <= cap_bytes) {
     if ((rc = s->k_stage.ensure(stage_bytes, st, false))) return rc;
     k_stage = (char *)s->k_stage.ptr;
   } else if (prune) {
@@ -1900,7 +1908,7 @@ static int retrieve_impl(kiv_store_t *s, const kiv_retrieve_args_t *a, hipStream
     // first scap slices per kv row compactly (4x the pages the top P' fills).
     const int64_t slice_bytes = (int64_t)ps * s->row_bytes;
     const int64_t want = std::min<int64_t>(umax, 4 * (int64_t)std::max(1, (a->out_width + ps - 1) / ps));
-    pr.scap = (int)std::min<int64_t>(want, (int64_t)kMaxStageBytes / ((int64_t)s->kr * slice_bytes));
+    pr.scap = (int)std::min<int64_t>(want, (int64_t)cap_bytes / ((int64_t)s->kr * slice_bytes));
     if (pr.scap > 0) {
       if ((rc = s->k_stage.ensure((size_t)s->kr * pr.scap * slice_bytes, st, false))) return rc;
       pr.cstage = (char *)s->k_stage.ptr;

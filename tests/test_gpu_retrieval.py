@@ -325,6 +325,30 @@ def test_fine_pruning_keeps_the_selection(cuda, name, w, batch, clustered):
         assert s1[0] < s1[1] and f1["mean_score"] > f0["mean_score"]  # the skipped pages score low
 
 
+def test_fine_pruning_compact_staging(cuda, monkeypatch):
+    """A staging cap too small for candidate-indexed K staging: the pruned
+    scan stages one slice per kv row compactly (the slot table) and the
+    selected rows' K of the others comes from host memory; the same ids and
+    rows as the full scan, which then stages nothing."""
+    from dataclasses import replace
+
+    w = Workload("prune_cstage", 8, 8, 96, torch.bfloat16, hot=16, cold=6000 + 1, top_pages=6, top_p=200,
+                 segment=256, n_targets=4)
+    data = generate(w, seed=2)
+    store, oracle, cfg = build(w, data, cuda, chunks=(3000, 1, 511))
+    # a slice is 128 tokens x 192 bytes; 8 kv rows: a 256 KiB cap holds one slot per row
+    monkeypatch.setenv("KIV_STAGE_CAP_BYTES", str(256 << 10))
+    q = data["q"]
+    k1, v1, sel1 = check_retrieval(store, oracle, cfg, w, data, q)
+    s1 = store.fine_scan_stats()
+    k0, v0 = store.retrieve_top_kv(q.to(cuda), w.scaling, replace(cfg, fine_pruning=False))
+    sel0 = store.telemetry_snapshot()["recent"][-1]["selected_token_indices"]
+    print(f"compact staging: slices read {s1}", flush=True)
+    assert s1[0] < s1[1]
+    assert sel1.reshape(-1).tolist() == sel0
+    assert torch.equal(k1.cpu(), k0.cpu()) and torch.equal(v1.cpu(), v0.cpu())
+
+
 def test_width_depends_on_union(cuda):
     """top_p > top_pages * page_size: the width follows the union size."""
     w = Workload("wide", 4, 1, 64, torch.bfloat16, hot=8, cold=64 * 10, top_pages=2, top_p=300, segment=64,
