@@ -265,8 +265,7 @@ def roofline_and_links(w, store, stages, union_pages, tier, scanned_slices=None,
         # (bytes per launch, memory it streams from)
         "coarse_scan": (N * row + bounds, "hbm"),
         "coarse_select": (rows * N * 4, "hbm"),
-        # Pruned (host tier): pass A, threshold, page bounds and pass B
-        # together; the bytes are the slices read.
+        # Pruned (host tier): the bytes are the (page, kv row) slices read.
         "fine_scan": (scanned_slices * w.page_size * w.head_dim * b, "host" if tier == "host" else "hbm"),
         "fine_select": (cand * 4, "hbm"),
         # Host and split tiers: only V of the selected rows crosses the host

@@ -292,9 +292,9 @@ PRUNE = [
 def test_fine_pruning_keeps_the_selection(cuda, name, w, batch, clustered):
     """Host tier with the pruned fine scan against the full scan on the same
     store: the same union, selected ids in the same order and the same K/V
-    rows bit for bit (pruning skips only pages whose bound is below pass A's
-    threshold).  Where pages were skipped the fine mean, which covers the
-    scored candidates only, differs."""
+    rows bit for bit (pruning skips only slices whose upper bound is below a
+    lower bound of the P-th largest key).  Where pages were skipped the fine
+    mean, which covers the scored candidates only, differs."""
     from dataclasses import replace
 
     data = generate(w, seed=2, batch=batch)
@@ -451,10 +451,10 @@ def test_select_large_k_paths(cuda, n_pages, top_pages, top_p):
     select, top_p = 2500 leaves every wave short of its share of maxima, so
     all of the row's keys (more than 2048) are candidates: the k-th largest
     comes from the search over the row in memory and the gather ranks 2500
-    listed entries.  On the host tier the pruned fine scan gets a zero
-    threshold there (too few maxima per wave), so pass B lists every union
-    page: its list must stop at the union size (a regression: padding
-    threads once passed the zero threshold and listed pages past it)."""
+    listed entries.  On the host tier the pruned fine scan lists the union
+    pages whose bound reaches its threshold in windows; the list must stop
+    at the union size even where a zero threshold passes every key (a
+    regression: padding threads once did and listed pages past it)."""
     w = Workload("largek", 4, 1, 32, torch.float32, hot=8, cold=n_pages * 16 + 5, top_pages=top_pages,
                  top_p=top_p, segment=64, page_size=16)
     data = generate(w, seed=16)
