@@ -922,7 +922,7 @@ struct FinePrune {
   int kr;
   uint32_t *thr;             // [B] thresholds T (written by block (0, b * Hkv))
   int width;                 // P'
-  const int32_t *ctl;        // [0] > 0: pruning is paused for this call (full scan)
+  const int32_t *ctl;        // [0] > 0: pruning is paused for this call (full scan); set by the gather
   // Compact K staging (when the candidate-indexed staging would not fit):
   // the slice at position i of kv row r's scan list goes to slot i of
   // cstage[r][scap][page_size][D], and slot_of[page][r] records it (-1:
@@ -934,7 +934,8 @@ struct FinePrune {
 
 // Pruning pays when it skips pages: after a call whose scan read more than
 // three quarters of the union's slices, the next kPruneRetry calls on the
-// store run the full scan (decided on the device by the fine select).
+// store run the full scan (decided on the device, by the gather's block
+// (0, 0) from the slices the fine select counted).
 constexpr int kPruneRetry = 32;
 
 // Keys of a list of union pages (plist: their union ranks) then of the
@@ -1374,7 +1375,8 @@ __global__ void __launch_bounds__(256) fine_scan_mfma_kernel(
 // list_cap (<= kCandCap) keys pass the bound, the block lists exactly the k
 // composites >= the k-th largest instead.  The block also
 // writes the row's telemetry (max and sum of scores, and the number of
-// scored candidates to list_count[B + b]) and zeroes the keys for the next
+// scored candidates to list_count[B + b]; after a pruned scan, the slices
+// it read to list_count[2B + b]) and zeroes the keys for the next
 // scan, which accumulates with atomicMax.  Keys a pruned scan skipped are
 // zero; at least k keys are scored, so none of them is listed.
 // V = 16-byte key chunks per thread kept in registers: rows of up to
@@ -1384,7 +1386,7 @@ __global__ void __launch_bounds__(kSelThreads) fine_select_kernel(
     uint32_t *__restrict__ keys, int64_t ld, const int32_t *__restrict__ counters, int has_pages, int page_size,
     int partial_len, int width, float *__restrict__ fine_stats, uint64_t *__restrict__ list, int64_t list_ld,
     int32_t *__restrict__ list_count, int list_cap, const uint32_t *__restrict__ ub, int kr, int hkv,
-    const uint32_t *__restrict__ thr, int32_t *__restrict__ ctl, const int32_t *__restrict__ page_list) {
+    const uint32_t *__restrict__ thr, const int32_t *__restrict__ page_list) {
   constexpr int NT = kSelThreads;
   __shared__ SelSh<NT> sh;
   __shared__ uint64_t cand[kCandCap];
@@ -1413,26 +1415,15 @@ __global__ void __launch_bounds__(kSelThreads) fine_select_kernel(
       }
       return hit;
     }, plist, sh.scan_tmp);
-    // The next call's pruning: each block adds (1 << 40) + its slices read
-    // to one 64-bit counter (ctl[2..3]); the block whose add completes the
-    // count sets the pause ctl[0] from the total and clears the counter.
-    // (One atomic carries both, so no device-scope fence is needed: on
-    // MI355X that fence writes back the XCDs' L2s.)
+    // The slices read for the next call's pruning decision (the gather's
+    // block (0, 0) sums them over the batch rows).
     slices = wave_sum_i32(slices);
     if ((threadIdx.x & 63) == 0) sh.fcnt[threadIdx.x >> 6] = slices;
     __syncthreads();
     if (threadIdx.x == 0) {
-      uint64_t read = 0;
-      for (int w = 0; w < NT / 64; ++w) read += (uint64_t)sh.fcnt[w];
-      unsigned long long *cnt = reinterpret_cast<unsigned long long *>(ctl + 2);
-      const uint64_t old = atomicAdd(cnt, (1ull << 40) + read);
-      if ((int64_t)(old >> 40) == (int64_t)gridDim.x - 1) {
-        const uint64_t total = (old & ((1ull << 40) - 1)) + read;
-        const int c0 = atomicAdd(&ctl[0], 0);
-        const uint64_t all = (uint64_t)U * hkv * gridDim.x;
-        atomicExch(&ctl[0], c0 > 0 ? c0 - 1 : (4 * total > 3 * all ? kPruneRetry : 0));
-        atomicExch(cnt, 0ull);
-      }
+      int read = 0;
+      for (int w = 0; w < NT / 64; ++w) read += sh.fcnt[w];
+      list_count[2 * gridDim.x + b] = read;
     }
     __syncthreads();  // fcnt is reused by the select below
     // Few pages: select over their keys alone; else over the whole row
@@ -1509,6 +1500,7 @@ struct GatherArgs {
   const char *cstage;        // pruned fine scan's compact K staging (see FinePrune), or NULL
   const int32_t *slot_of;
   int scap;
+  int32_t *ctl;              // pruned fine scan's control (the pause), or NULL
   int page_size, partial_len;
   int64_t num_finalized;
   int batch, hkv, head_dim, width, cpr;
@@ -1561,6 +1553,15 @@ template <int DT> __device__ void gather_block(const GatherArgs &ga, int bx, int
       if (stats_accum) {
         stats_accum[2] += (double)m;
         stats_accum[3] += (double)mean;
+      }
+      if (ga.ctl) {
+        // Pruning pays when it skips: after a call that read more than three
+        // quarters of the union's slices, the next kPruneRetry calls scan
+        // in full; a paused call counts down.
+        int64_t read = 0;
+        for (int r = 0; r < batch; ++r) read += list_count[2 * batch + r];
+        const int c0 = ga.ctl[0];
+        ga.ctl[0] = c0 > 0 ? c0 - 1 : (4 * read > 3 * (int64_t)U * hkv * batch ? kPruneRetry : 0);
       }
     }
   }
@@ -1886,11 +1887,11 @@ static int retrieve_impl(kiv_store_t *s, const kiv_retrieve_args_t *a, hipStream
     KIV_HIP(hipMemsetAsync(s->fine_keys.ptr, 0, s->fine_keys.bytes, st));
   }
   // Candidate lists of the fine select: [B][list_ld] composites, then [B]
-  // counts and [B] numbers of scored candidates.
+  // counts, [B] numbers of scored candidates and [B] slices read.
   const int list_cap = fine_list_cap(a->out_width);
   const int64_t lmax = std::min<int64_t>(cmax, std::max<int64_t>(list_cap, a->out_width));
   const int64_t list_ld = (std::max<int64_t>(list_cap, a->out_width) + 31) & ~int64_t(31);
-  if ((rc = s->sel_list.ensure((size_t)B * list_ld * 8 + (size_t)B * 8, st, false))) return rc;
+  if ((rc = s->sel_list.ensure((size_t)B * list_ld * 8 + (size_t)B * 12, st, false))) return rc;
   uint64_t *list = (uint64_t *)s->sel_list.ptr;
   int32_t *list_count = (int32_t *)(list + (size_t)B * list_ld);
   const int bwords = union_src == UNION_ROWS ? words : 0;
@@ -2007,7 +2008,7 @@ static int retrieve_impl(kiv_store_t *s, const kiv_retrieve_args_t *a, hipStream
     with_select_chunks(cmax, [&](auto kern) {
       hipLaunchKernelGGL(kern, dim3(B), dim3(kSelThreads), 0, st, (uint32_t *)s->fine_keys.ptr, ldc,
                          (const int32_t *)s->counters.ptr, N > 0 ? 1 : 0, ps, (int)s->partial_len, a->out_width,
-                         fine_stats, list, list_ld, list_count, list_cap, pr_ub, s->kr, hkv, pr_thr, pr_ctl,
+                         fine_stats, list, list_ld, list_count, list_cap, pr_ub, s->kr, hkv, pr_thr,
                          (const int32_t *)s->page_list.ptr);
     }, [](auto vc) { return fine_select_kernel<decltype(vc)::value>; });
     s->prof_end(KIV_STAGE_FINE_SELECT, st);
@@ -2036,6 +2037,7 @@ static int retrieve_impl(kiv_store_t *s, const kiv_retrieve_args_t *a, hipStream
     ga.cstage = pr.cstage;
     ga.slot_of = pr.slot_of;
     ga.scap = pr.scap;
+    ga.ctl = pr_ctl;
     ga.page_size = ps;
     ga.partial_len = (int)s->partial_len;
     ga.num_finalized = s->num_pages * ps;
