@@ -31,6 +31,15 @@ def test_header_and_binding_agree():
     assert header_functions() == sorted(_native.SIGNATURES)
 
 
+def test_header_constants_match_binding():
+    """The enum values the binding passes (flags, mask kinds, tiers, dtypes)."""
+    text = HEADER.read_text()
+    consts = {m.group(1): int(m.group(2)) for m in re.finditer(r"(KIV_[A-Z0-9_]+)\s*=\s*(\d+)", text)}
+    assert consts["KIV_RETRIEVE_PRUNE"] == _native.RETRIEVE_PRUNE
+    assert consts["KIV_MASK_CAUSAL"] == _native.MASK_CAUSAL and consts["KIV_MASK_BOOL"] == _native.MASK_BOOL
+    assert consts["KIV_TIER_HOST"] == _native.TIER_HOST and consts["KIV_TIER_HBM"] == _native.TIER_HBM
+
+
 def test_library_exports_every_declared_symbol():
     if not _native.LIB_PATH.exists():
         pytest.fail(f"{_native.LIB_PATH} not built (run __graft_entry__.build())")
