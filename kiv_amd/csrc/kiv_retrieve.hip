@@ -1004,6 +1004,43 @@ template <int NT, typename Src> __device__ uint32_t block_kth_bound(const Src &s
   return bound;
 }
 
+// Max of n consecutive bound keys (a page's kv rows of one batch row):
+// 16-byte loads when the run is aligned (kv heads a multiple of 4), so that
+// the loads are few and independent.
+__device__ __forceinline__ uint32_t max_keys(const uint32_t *p, int n) {
+  uint32_t m = 0u;
+  if (((uintptr_t)p & 15) == 0 && (n & 3) == 0) {
+    const uint4 *p4 = reinterpret_cast<const uint4 *>(p);
+#pragma unroll 4
+    for (int i = 0; i < n / 4; ++i) {
+      const uint4 x = p4[i];
+      m = max(m, max(max(x.x, x.y), max(x.z, x.w)));
+    }
+  } else {
+#pragma unroll 4
+    for (int i = 0; i < n; ++i) m = max(m, p[i]);
+  }
+  return m;
+}
+
+// Count of n consecutive bound keys >= t (the kv rows of one batch row
+// whose slice of a page is scanned); loads as in max_keys.
+__device__ __forceinline__ int count_keys_ge(const uint32_t *p, int n, uint32_t t) {
+  int c = 0;
+  if (((uintptr_t)p & 15) == 0 && (n & 3) == 0) {
+    const uint4 *p4 = reinterpret_cast<const uint4 *>(p);
+#pragma unroll 4
+    for (int i = 0; i < n / 4; ++i) {
+      const uint4 x = p4[i];
+      c += (x.x >= t) + (x.y >= t) + (x.z >= t) + (x.w >= t);
+    }
+  } else {
+#pragma unroll 4
+    for (int i = 0; i < n; ++i) c += p[i] >= t;
+  }
+  return c;
+}
+
 // Lower-bound keys of the union pages for batch row b (max over its kv
 // rows), entry v = union rank, as composites; sub-slots as in PageKeys.
 template <int NT, typename PageOf> struct UnionLowerKeys {
@@ -1014,10 +1051,7 @@ template <int NT, typename PageOf> struct UnionLowerKeys {
     constexpr int W = NT / 64;
     int u = 0;
     for (int v = (threadIdx.x >> 6) + W * (threadIdx.x & 63); v < U; v += NT, ++u) {
-      const uint32_t *l = lb + (int64_t)page_of(v) * kr + r0;
-      uint32_t key = 0u;
-      for (int h = 0; h < hkv; ++h) key = max(key, l[h]);
-      f(comp_of(key, v), u & 3);
+      f(comp_of(max_keys(lb + (int64_t)page_of(v) * kr + r0, hkv), v), u & 3);
     }
   }
   template <typename F> __device__ void each(F &&f) const {
@@ -1406,14 +1440,9 @@ __global__ void __launch_bounds__(kSelThreads) fine_select_kernel(
     const uint32_t tb = thr[b];
     int slices = 0;  // (page, kv row) slices the scan read, this thread's pages
     const int np = list_pages<NT>(U, [&](int v) {
-      const uint32_t *ub_v = ub + (int64_t)page_list[v] * kr + b * hkv;
-      bool hit = false;
-      for (int h = 0; h < hkv; ++h) {
-        const bool read = ub_v[h] >= tb;
-        hit |= read;
-        slices += read;
-      }
-      return hit;
+      const int read = count_keys_ge(ub + (int64_t)page_list[v] * kr + b * hkv, hkv, tb);
+      slices += read;
+      return read > 0;
     }, plist, sh.scan_tmp);
     // The slices read for the next call's pruning decision (the gather's
     // block (0, 0) sums them over the batch rows).
