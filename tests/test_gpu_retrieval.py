@@ -325,6 +325,28 @@ def test_fine_pruning_keeps_the_selection(cuda, name, w, batch, clustered):
         assert s1[0] < s1[1] and f1["mean_score"] > f0["mean_score"]  # the skipped pages score low
 
 
+def test_fine_pruning_union_wider_than_a_window(cuda):
+    """A union of more than 4096 pages: the pruned scan lists its pages in
+    two windows (and the fine select falls back to the whole row); the same
+    ids and rows as the full scan."""
+    from dataclasses import replace
+
+    w = Workload("prune_wide", 8, 1, 32, torch.float32, hot=8, cold=6000 * 16 + 3, top_pages=1000, top_p=256,
+                 segment=16, page_size=16)
+    data = generate(w, seed=21)
+    q = torch.randn(1, 8, 1, 32, generator=torch.Generator().manual_seed(22))
+    store, oracle, cfg = build(w, data, cuda, chunks=(20000,))
+    k1, v1, sel1 = check_retrieval(store, oracle, cfg, w, data, q)
+    union = store.telemetry_snapshot()["recent"][-2]["pages_selected"]
+    s1 = store.fine_scan_stats()
+    k0, v0 = store.retrieve_top_kv(q.to(cuda), w.scaling, replace(cfg, fine_pruning=False))
+    sel0 = store.telemetry_snapshot()["recent"][-1]["selected_token_indices"]
+    print(f"wide union: {len(union)} pages, slices read {s1}", flush=True)
+    assert len(union) > 4096
+    assert sel1.reshape(-1).tolist() == sel0
+    assert torch.equal(k1.cpu(), k0.cpu()) and torch.equal(v1.cpu(), v0.cpu())
+
+
 def test_fine_pruning_compact_staging(cuda, monkeypatch):
     """A staging cap too small for candidate-indexed K staging: the pruned
     scan stages one slice per kv row compactly (the slot table) and the
