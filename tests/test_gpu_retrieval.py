@@ -347,15 +347,17 @@ def test_fine_pruning_union_wider_than_a_window(cuda):
     assert torch.equal(k1.cpu(), k0.cpu()) and torch.equal(v1.cpu(), v0.cpu())
 
 
-def test_fine_pruning_compact_staging(cuda, monkeypatch):
+@pytest.mark.parametrize("clustered", [True, False])
+def test_fine_pruning_compact_staging(cuda, monkeypatch, clustered):
     """A staging cap too small for candidate-indexed K staging: the pruned
     scan stages one slice per kv row compactly (the slot table) and the
-    selected rows' K of the others comes from host memory; the same ids and
-    rows as the full scan, which then stages nothing."""
+    selected rows' K of the others comes from host memory; unclustered keys
+    prune nothing, so the second call runs paused (full scan, slots by union
+    rank).  Every call returns the full scan's ids and rows."""
     from dataclasses import replace
 
     w = Workload("prune_cstage", 8, 8, 96, torch.bfloat16, hot=16, cold=6000 + 1, top_pages=6, top_p=200,
-                 segment=256, n_targets=4)
+                 segment=256 if clustered else 1, n_targets=4)
     data = generate(w, seed=2)
     store, oracle, cfg = build(w, data, cuda, chunks=(3000, 1, 511))
     # a slice is 128 tokens x 192 bytes; 8 kv rows: a 256 KiB cap holds one slot per row
@@ -363,12 +365,16 @@ def test_fine_pruning_compact_staging(cuda, monkeypatch):
     q = data["q"]
     k1, v1, sel1 = check_retrieval(store, oracle, cfg, w, data, q)
     s1 = store.fine_scan_stats()
+    k2, v2 = store.retrieve_top_kv(q.to(cuda), w.scaling, cfg)
+    sel2 = store.telemetry_snapshot()["recent"][-1]["selected_token_indices"]
     k0, v0 = store.retrieve_top_kv(q.to(cuda), w.scaling, replace(cfg, fine_pruning=False))
     sel0 = store.telemetry_snapshot()["recent"][-1]["selected_token_indices"]
-    print(f"compact staging: slices read {s1}", flush=True)
-    assert s1[0] < s1[1]
-    assert sel1.reshape(-1).tolist() == sel0
+    print(f"compact staging ({'clustered' if clustered else 'unclustered'}): slices read {s1}", flush=True)
+    if clustered:
+        assert s1[0] < s1[1]
+    assert sel1.reshape(-1).tolist() == sel0 == sel2
     assert torch.equal(k1.cpu(), k0.cpu()) and torch.equal(v1.cpu(), v0.cpu())
+    assert torch.equal(k2.cpu(), k0.cpu()) and torch.equal(v2.cpu(), v0.cpu())
 
 
 def test_width_depends_on_union(cuda):
