@@ -234,6 +234,18 @@ size_t kiv_attention_workspace_size(int32_t batch, int32_t num_q_heads, int32_t 
  * call (kiv/middleware.py:330-354). */
 int kiv_decode_attention(const kiv_attention_args_t *args, kiv_stream_t stream);
 
+/* kiv_decode_attention without a caller workspace and without any
+ * allocation: the split partials go to a static device array of 8 MiB in
+ * the library's code object (one per GPU, held until the process ends).
+ * No counterpart in the reference: for callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc).  args->workspace and workspace_bytes are ignored.
+ * Shapes whose split partials (kiv_attention_workspace_size) exceed 8 MiB
+ * fail with KIV_ERR_UNSUPPORTED.  Every call on one GPU shares the array,
+ * so calls that overlap on one GPU (different streams, or threads) race;
+ * each call rewrites every partial it reads, so nothing carries over. */
+int kiv_decode_attention_noalloc(const kiv_attention_args_t *args, kiv_stream_t stream);
+
 /* kiv_retrieve followed by kiv_decode_attention over its outputs, in fewer
  * launches: the hot window's attention splits run alongside the retrieval's
  * gather, and one final kernel attends the retrieved keys and merges.  The

@@ -91,6 +91,7 @@ SIGNATURES = {
                                            C.POINTER(C.c_double), C.c_void_p]),
     "kiv_attention_workspace_size": (C.c_size_t, [C.c_int32] * 7),
     "kiv_decode_attention": (C.c_int, [C.POINTER(AttentionArgs), C.c_void_p]),
+    "kiv_decode_attention_noalloc": (C.c_int, [C.POINTER(AttentionArgs), C.c_void_p]),
     "kiv_retrieve_attend": (C.c_int, [C.c_void_p, C.POINTER(RetrieveArgs), C.POINTER(AttentionArgs), C.c_void_p]),
     "kiv_prefill_attention": (C.c_int, [C.POINTER(AttentionArgs), C.c_void_p]),
     "kiv_prefill_workspace_size": (C.c_size_t, [C.c_int32] * 6),

@@ -15,12 +15,20 @@
 // Combine kernel, one block per query row: log-sum-exp merge of the S splits
 // into the output.
 #include <algorithm>
+#include <mutex>
 #include <type_traits>
 
 #include "kiv_attn_device.h"
 #include "kiv_common.h"
 #include "kiv_dispatch.h"
 #include "kiv_internal.h"
+
+// Split partials of kiv_decode_attention_noalloc: one array per GPU, in the
+// code object, so that entry point never allocates.  Host code never passes
+// this name to a kernel (on the host it is a stand-in, not a device
+// address); it uses the per-device address from hipGetSymbolAddress.
+static constexpr size_t kNoAllocScratchBytes = size_t(8) << 20;
+static __device__ __align__(256) char scratch[kNoAllocScratchBytes];
 
 namespace kiv {
 
@@ -592,6 +600,47 @@ size_t kiv_attention_workspace_size(int32_t batch, int32_t num_q_heads, int32_t 
 
 int kiv_decode_attention(const kiv_attention_args_t *a, kiv_stream_t stream) {
   return attention_launch(a, (hipStream_t)stream, "kiv_decode_attention");
+}
+
+int kiv_decode_attention_noalloc(const kiv_attention_args_t *a, kiv_stream_t stream) {
+  static const char *who = "kiv_decode_attention_noalloc";
+  if (!a) return fail(KIV_ERR_INVALID, "%s: null argument", who);
+  const size_t need = kiv_attention_workspace_size(a->batch, a->num_q_heads, a->num_kv_heads, a->head_dim,
+                                                   a->q_len, a->cold_len, a->hot_len);
+  if (need > kNoAllocScratchBytes)
+    return fail(KIV_ERR_UNSUPPORTED, "%s: this shape needs %zu bytes of split scratch, the static buffer holds %zu",
+                who, need, kNoAllocScratchBytes);
+  // The device the stream runs on (the current device for the null stream).
+  int dev = 0;
+  if (stream) {
+    KIV_HIP(hipStreamGetDevice((hipStream_t)stream, &dev));
+  } else {
+    KIV_HIP(hipGetDevice(&dev));
+  }
+  // Each device holds its own copy of the array: resolve its address once
+  // per device, with that device current.
+  constexpr int kMaxDevices = 64;
+  static std::mutex mu;
+  static void *addr[kMaxDevices] = {};
+  if (dev < 0 || dev >= kMaxDevices) return fail(KIV_ERR_UNSUPPORTED, "%s: device %d out of range", who, dev);
+  void *ptr = nullptr;
+  {
+    std::lock_guard<std::mutex> lock(mu);
+    if (!addr[dev]) {
+      DeviceGuard guard(dev);
+      void *p = nullptr;
+      KIV_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+      if (!p) return fail(KIV_ERR_HIP, "%s: no device address for the scratch array", who);
+      addr[dev] = p;
+    }
+    ptr = addr[dev];
+  }
+  // The split kernels write every partial they leave for the combine, so
+  // nothing in the scratch needs clearing between calls.
+  kiv_attention_args_t local = *a;
+  local.workspace = ptr;
+  local.workspace_bytes = kNoAllocScratchBytes;
+  return attention_launch(&local, (hipStream_t)stream, who);
 }
 
 }  // extern "C"
