@@ -232,7 +232,7 @@ class ColdKVStore:
         args = nat.RetrieveArgs(
             q=q.data_ptr(), q_stride=nat.strides(q, 4), q_len=Q, scaling=float(scaling),
             top_pages=int(kiv_config.top_pages), out_width=int(width), reuse_candidates=1 if reuse else 0,
-            flags=nat.RETRIEVE_PRUNE if getattr(kiv_config, "fine_pruning", True) else 0,
+            flags=nat.RETRIEVE_PRUNE if getattr(kiv_config, "fine_pruning", False) else 0,
             k_out=k_out.data_ptr(), v_out=v_out.data_ptr(), idx_out=idx_out.data_ptr(),
             pages_out=nat.ptr(pages_out), union_count_out=nat.ptr(union_count),
             stats_out=stats.data_ptr(), stats_accum=accum.data_ptr(),

@@ -32,13 +32,15 @@ class KIVConfig:
                      "fp32": rank on the fp32 scores.
     reserve_tokens   optional capacity hint; the store pre-sizes its page
                      arrays for this many cold tokens.
-    fine_pruning     host tier: the coarse scan also bounds each page's token
-                     scores (from the page's summary and radius), and the
-                     fine scan reads only the union pages whose bound can
-                     reach the top P, which cuts host-link reads.  Selected
+    fine_pruning     host tier, opt-in: the coarse scan also bounds each
+                     page's token scores (from the page's summary and
+                     radius), and the fine scan reads only the union pages
+                     whose bound can reach the top P, which cuts host-link
+                     reads (NS shape: 20 MB -> 1.3 MB per step).  Selected
                      tokens, their order and the returned rows are the same
                      as without it; the fine telemetry's mean_score then
-                     averages the scored candidates only.
+                     averages the scored candidates only, so the default
+                     (off) keeps the reference's telemetry exactly.
     """
 
     hot_budget: int = 2048
@@ -49,7 +51,7 @@ class KIVConfig:
     cold_tier: str = "host"
     score_rounding: str = "activation"
     reserve_tokens: int = 0
-    fine_pruning: bool = True
+    fine_pruning: bool = False
 
     def __post_init__(self) -> None:
         if self.cold_tier not in ("host", "hbm", "split"):

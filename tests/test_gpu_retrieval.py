@@ -36,9 +36,10 @@ def f64(t: torch.Tensor) -> np.ndarray:
     return t.detach().float().cpu().numpy().astype(np.float64)
 
 
-def build(w: Workload, data: dict, device, chunks=(4096,), cold_tier="host", rounding="activation"):
+def build(w: Workload, data: dict, device, chunks=(4096,), cold_tier="host", rounding="activation",
+          pruning=False):
     cfg = KIVConfig(hot_budget=w.hot, top_p=w.top_p, page_size=w.page_size, top_pages=w.top_pages,
-                    cold_tier=cold_tier, score_rounding=rounding)
+                    cold_tier=cold_tier, score_rounding=rounding, fine_pruning=pruning)
     topo = ModelTopology.manual(global_layer_indices=(0,), num_query_heads=w.num_q_heads,
                                 num_kv_heads=w.num_kv_heads, head_dim=w.head_dim, num_hidden_layers=1)
     store = ColdKVStore(cfg, topo, device)
@@ -74,8 +75,13 @@ def check_rows(store: ColdKVStore, data: dict):
     assert torch.equal(k.cpu(), data["cold_k"]) and torch.equal(v.cpu(), data["cold_v"])
 
 
-def check_retrieval(store, oracle, cfg, w, data, q, rounding="activation"):
-    """Run one retrieval and check it; returns (k_out, v_out, sel ids [B, P'])."""
+def check_retrieval(store, oracle, cfg, w, data, q, rounding="activation", min_det_c=0.5, info=None):
+    """Run one retrieval and check it; returns (k_out, v_out, sel ids [B, P']).
+
+    ``min_det_c``: the least fraction of coarse rows whose top pages the
+    bands must determine (unclustered model keys leave most rows open).
+    ``info``, if given, receives the union, the determined fractions and
+    the oracle's selection."""
     dev = store.device
     dtype = DT[w.dtype]
     k_out, v_out = store.retrieve_top_kv(q.to(dev), w.scaling, cfg)
@@ -99,7 +105,7 @@ def check_retrieval(store, oracle, cfg, w, data, q, rounding="activation"):
         lo_c, hi_c = score_interval(q64.float().numpy(), summ.float().numpy(), w.scaling, dtype, rounding)
         lo_c, hi_c = lo_c.reshape(-1, N), hi_c.reshape(-1, N)
         det_c = check_topk(set(union), lo_c, hi_c, min(cfg.top_pages, N))
-        assert det_c > 0.5, f"only {det_c:.2f} of coarse rows determined"
+        assert det_c >= min_det_c, f"only {det_c:.2f} of coarse rows determined"
     else:
         union, det_c = [], 1.0
     cand = exact.candidate_ids(np.array(union, dtype=np.int64), ps, N * ps, p)
@@ -122,6 +128,9 @@ def check_retrieval(store, oracle, cfg, w, data, q, rounding="activation"):
     # The CPU oracle (the reference's op sequence in the dtype) obeys the same
     # bands, and where every boundary is determined both pick the same sets.
     _, _, trace = oracle.retrieve(q64, w.scaling, cfg.top_p, cfg.top_pages)
+    if info is not None:
+        info.update(union=union, det_c=det_c, det_f=det_f, oracle_pages=trace.pages,
+                    oracle_selected=trace.selected_ids, trace=trace)
     if rounding == "activation":
         if N > 0:
             check_topk(set(trace.pages.tolist()), lo_c, hi_c, min(cfg.top_pages, N))
@@ -178,14 +187,14 @@ SMALL = [
 ]
 
 
-@pytest.mark.parametrize("tier", ["host", "hbm"])
+@pytest.mark.parametrize("tier", ["host", "host_pruned", "hbm"])
 @pytest.mark.parametrize("name,over,chunks", SMALL, ids=[c[0] for c in SMALL])
 def test_small_parity(cuda, name, over, chunks, tier):
-    """Each small case on the host tier (VALU fine scan) and in HBM (the MFMA
-    fine scan where the head dim allows it)."""
+    """Each small case on the host tier (VALU fine scan; full and pruned)
+    and in HBM (the MFMA fine scan where the head dim allows it)."""
     w = Workload(name=name, **over)
     data = generate(w, seed=1)
-    store, oracle, cfg = build(w, data, cuda, chunks, cold_tier=tier)
+    store, oracle, cfg = build(w, data, cuda, chunks, cold_tier=tier.split("_")[0], pruning=tier == "host_pruned")
     assert store.cold_length == w.cold and store.num_pages == w.cold // w.page_size
     check_summaries(store, data, w)
     check_rows(store, data)
@@ -335,7 +344,7 @@ def test_fine_pruning_union_wider_than_a_window(cuda):
                  segment=16, page_size=16)
     data = generate(w, seed=21)
     q = torch.randn(1, 8, 1, 32, generator=torch.Generator().manual_seed(22))
-    store, oracle, cfg = build(w, data, cuda, chunks=(20000,))
+    store, oracle, cfg = build(w, data, cuda, chunks=(20000,), pruning=True)
     k1, v1, sel1 = check_retrieval(store, oracle, cfg, w, data, q)
     union = store.telemetry_snapshot()["recent"][-2]["pages_selected"]
     s1 = store.fine_scan_stats()
@@ -359,7 +368,7 @@ def test_fine_pruning_compact_staging(cuda, monkeypatch, clustered):
     w = Workload("prune_cstage", 8, 8, 96, torch.bfloat16, hot=16, cold=6000 + 1, top_pages=6, top_p=200,
                  segment=256 if clustered else 1, n_targets=4)
     data = generate(w, seed=2)
-    store, oracle, cfg = build(w, data, cuda, chunks=(3000, 1, 511))
+    store, oracle, cfg = build(w, data, cuda, chunks=(3000, 1, 511), pruning=True)
     # a slice is 128 tokens x 192 bytes; 8 kv rows: a 256 KiB cap holds one slot per row
     monkeypatch.setenv("KIV_STAGE_CAP_BYTES", str(256 << 10))
     q = data["q"]
@@ -487,7 +496,7 @@ def test_select_large_k_paths(cuda, n_pages, top_pages, top_p):
                  top_p=top_p, segment=64, page_size=16)
     data = generate(w, seed=16)
     q = torch.randn(1, 4, 1, 32, generator=torch.Generator().manual_seed(17))
-    store, oracle, cfg = build(w, data, cuda, chunks=(8192,))
+    store, oracle, cfg = build(w, data, cuda, chunks=(8192,), pruning=True)
     check_retrieval(store, oracle, cfg, w, data, q)
     union = store.telemetry_snapshot()["recent"][-2]["pages_selected"]
     assert len(union) >= top_pages

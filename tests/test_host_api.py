@@ -71,7 +71,7 @@ def test_config_defaults_and_validation():
         KIVConfig(cold_tier="disk")
     with pytest.raises(ValueError):
         KIVConfig(score_rounding="fp8")
-    assert c.fine_pruning is True and KIVConfig(fine_pruning=False).fine_pruning is False
+    assert c.fine_pruning is False and KIVConfig(fine_pruning=True).fine_pruning is True
 
 
 # ---------------------------------------------------------------------- mask
