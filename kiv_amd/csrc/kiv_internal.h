@@ -107,7 +107,6 @@ struct kiv_store {
   kiv::DevBuf prune;         // pruned fine scan: control, [B] thresholds, [N][kr] upper and lower bound keys
   bool prune_on = false;     // the last retrieval's fine scan was a pruned one
   bool union_valid = false;  // page_list / U hold the last coarse pass
-  int64_t union_rows = 0;    // B*Hq*Q of that pass (bounds reuse)
   int64_t union_max = 0;     // grid bound of that pass
 
   // Stage timing (kiv_profile_enable): ring of event pairs per stage.

@@ -1758,7 +1758,13 @@ static int retrieve_impl(kiv_store_t *s, const kiv_retrieve_args_t *a, hipStream
   const int ktf = D / 32;
   const bool fine_mfma = dt != KIV_DTYPE_F32 && D % 32 == 0 && (ktf <= 4 || ktf == 6 || ktf == 8) &&
                          (G * Qb >= kFineMfmaRows || !host_tier) && a->scaling > 0.f;
-  const bool fresh = N > 0 && !(a->reuse_candidates && s->union_valid && s->union_rows == rows);
+  // Shared-layer reuse (kiv/cold_store.py:303-317): the union of the last
+  // coarse pass serves a query of any length; the fine scan scores it with
+  // this query's rows.
+  if (N > 0 && a->reuse_candidates && !s->union_valid)
+    return fail(KIV_ERR_STATE, "kiv_retrieve: reuse_candidates without a union to reuse (none since the last "
+                               "eviction or reset)");
+  const bool fresh = N > 0 && !a->reuse_candidates;
   const bool prune = (a->flags & KIV_RETRIEVE_PRUNE) && host_tier && !fine_mfma && passes == 1 && fresh &&
                      std::max(1, (a->out_width + ps - 1) / ps) < std::min(a->top_pages, N) && a->scaling > 0.f;
   FinePrune pr{};
@@ -1795,8 +1801,7 @@ static int retrieve_impl(kiv_store_t *s, const kiv_retrieve_args_t *a, hipStream
   int64_t umax = 0;
   int kc = 0;  // pages per row of a fresh coarse pass
   if (N > 0) {
-    const bool reuse = a->reuse_candidates && s->union_valid && s->union_rows == rows;
-    if (!reuse) {
+    if (fresh) {
       kc = std::min(a->top_pages, N);
       umax = std::min<int64_t>(N, (int64_t)rows * kc);
       // The fine scan's blocks build the union themselves from short row
@@ -1900,7 +1905,6 @@ static int retrieve_impl(kiv_store_t *s, const kiv_retrieve_args_t *a, hipStream
         KIV_HIP(hipGetLastError());
       }
       s->union_valid = true;
-      s->union_rows = rows;
       s->union_max = umax;
     } else {
       union_src = UNION_LIST;

@@ -89,16 +89,38 @@ def _kv_sharing(cfg: Any, model: Any, globals_: tuple[int, ...]):
 
 def _first_attr(cfg: Any, names: tuple[str, ...]):
     for name in names:
-        val = getattr(cfg, name, None)
+        try:
+            val = getattr(cfg, name, None)
+        except Exception:  # a per-layer attribute of a heterogeneous config
+            val = None
         if val is not None:
             return val
     return None
 
 
-def _head_geometry(cfg: Any) -> tuple[int, int, int]:
+def _head_geometry(cfg: Any, global_layers: tuple[int, ...] = ()) -> tuple[int, int, int]:
+    """(Hq, Hkv, D) of the global layers (kiv/hf_topology.py:130-150).
+
+    Configs whose attention geometry varies per layer (Gemma4 in
+    transformers 5.x keeps ``head_dim`` and the kv head count of its
+    full-attention layers in ``per_layer_config``) are read at the first
+    global layer."""
     hq = cfg.num_attention_heads
-    hkv = _first_attr(cfg, ("num_global_key_value_heads", "num_key_value_heads")) or hq
-    d = _first_attr(cfg, ("global_head_dim", "head_dim")) or cfg.hidden_size // hq
+    layer_cfg = None
+    per_layer = getattr(cfg, "per_layer_config", None)
+    if per_layer is not None and global_layers:
+        try:
+            layer_cfg = per_layer[global_layers[0]]
+        except (KeyError, IndexError, TypeError):
+            layer_cfg = None
+    hkv = _first_attr(cfg, ("num_global_key_value_heads",))
+    if hkv is None and layer_cfg is not None:
+        hkv = _first_attr(layer_cfg, ("num_key_value_heads",))
+    hkv = hkv or _first_attr(cfg, ("num_key_value_heads",)) or hq
+    d = _first_attr(cfg, ("global_head_dim",))
+    if d is None and layer_cfg is not None:
+        d = _first_attr(layer_cfg, ("head_dim",))
+    d = d or _first_attr(cfg, ("head_dim",)) or cfg.hidden_size // hq
     return hq, hkv, d
 
 
@@ -115,7 +137,7 @@ def detect_topology(model: Any) -> ModelTopology:
         family = model_type
     globals_ = _global_layers(cfg)
     owners, sharing = _kv_sharing(cfg, model, globals_)
-    hq, hkv, d = _head_geometry(cfg)
+    hq, hkv, d = _head_geometry(cfg, globals_)
     topo = ModelTopology(
         model_family=family,
         num_hidden_layers=cfg.num_hidden_layers,

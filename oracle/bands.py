@@ -78,3 +78,53 @@ def check_topk(got: set, lo_rows: np.ndarray, hi_rows: np.ndarray, k: int) -> fl
     assert not missing, f"{len(missing)} certainly-selected indices missing, e.g. {missing[:8]}"
     assert not extra, f"{len(extra)} indices outside the possible set, e.g. {extra[:8]}"
     return determined / max(1, len(lo_rows))
+
+
+# ------------------------------------------------- telemetry score intervals
+
+def _dtype_step(r: float, dtype: str, down: bool) -> float:
+    """The dtype value next to the dtype value ``r``, below it (or above)."""
+    if dtype == "float32":
+        return float(np.nextafter(np.float32(r), np.float32(-np.inf if down else np.inf)))
+    if dtype == "float16":
+        return float(np.nextafter(np.float16(r), np.float16(-np.inf if down else np.inf)))
+    # bfloat16: step the upper 16 bits of the fp32 pattern
+    if r == 0.0:
+        tiny = 2.0 ** -133
+        return -tiny if down else tiny
+    u = int(np.float32(r).view(np.uint32))
+    u += (-0x10000 if down else 0x10000) * (1 if r > 0 else -1)
+    return float(np.uint32(u).view(np.float32))
+
+
+def dtype_floor(x: float, dtype: str) -> float:
+    """The largest dtype value <= x."""
+    r = float(exact.round_to_dtype(np.array([x]), dtype)[0])
+    return _dtype_step(r, dtype, True) if r > x else r
+
+
+def dtype_ceil(x: float, dtype: str) -> float:
+    """The smallest dtype value >= x."""
+    r = float(exact.round_to_dtype(np.array([x]), dtype)[0])
+    return _dtype_step(r, dtype, False) if r < x else r
+
+
+def max_band(lo: np.ndarray, hi: np.ndarray) -> tuple[float, float]:
+    """Interval of the largest of scores that lie in [lo_i, hi_i]."""
+    return float(np.max(lo)), float(np.max(hi))
+
+
+def mean_band(lo: np.ndarray, hi: np.ndarray, dtype: str, rounding: str) -> tuple[float, float]:
+    """Interval of a computed mean of scores in [lo_i, hi_i].
+
+    The reference takes ``scores.mean()`` of a dtype tensor (a float
+    accumulation, rounded to the dtype); the kernels sum in fp32 per row and
+    in fp64 across rows, then round to the dtype.  Any fp32 summation of n
+    terms errs by at most (n + 2) * 2**-24 * sum |s_i|, and rounding to the
+    dtype (or to fp32, when scores are fp32) in any direction stays within
+    the neighbouring values, so both lie in the returned interval."""
+    n = lo.size
+    err = (n + 2) * U32 * float(np.maximum(np.abs(lo), np.abs(hi)).sum()) / n
+    a, b = float(lo.mean()) - err, float(hi.mean()) + err
+    out = dtype if rounding == "activation" else "float32"
+    return dtype_floor(a, out), dtype_ceil(b, out)

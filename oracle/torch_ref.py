@@ -36,8 +36,90 @@ class RetrieveTrace:
     extra: dict = field(default_factory=dict)
 
 
+class OracleTelemetry:
+    """The retrieval telemetry ring of kiv/cold_store.py:417-581: a coarse and
+    a fine record per retrieval (a placeholder coarse record when the coarse
+    pass is skipped), running sums over real passes, and the snapshot with
+    its aggregates.  Scores are the dtype tensors' own ``max``/``mean``
+    (``float(t.max())``, ``float(t.mean())`` as at :468-469 and :524-525)."""
+
+    MAX_BUFFER = 256
+
+    def __init__(self) -> None:
+        self.total_calls = 0
+        self.coarse_calls = 0
+        self.coarse_real_calls = 0
+        self.coarse_top_sum = 0.0
+        self.coarse_mean_sum = 0.0
+        self.coarse_cold_sum = 0
+        self.fine_calls = 0
+        self.fine_top_sum = 0.0
+        self.fine_mean_sum = 0.0
+        self.selected_sum = 0
+        self.ring: list[dict] = []
+
+    def _push(self, rec: dict) -> None:
+        # kiv/cold_store.py:549-552
+        self.ring.append(rec)
+        self.ring = self.ring[-self.MAX_BUFFER:]
+
+    @staticmethod
+    def _ratio(top: float, mean: float) -> float:
+        return top / abs(mean) if mean else float("inf")
+
+    def coarse(self, coarse_scores, top_page_idx, num_pages: int, cold_length: int) -> None:
+        # kiv/cold_store.py:456-488
+        top, mean = float(coarse_scores.max()), float(coarse_scores.mean())
+        pages = top_page_idx.reshape(-1).unique().tolist()
+        self.coarse_calls += 1
+        self.coarse_real_calls += 1
+        self.coarse_top_sum += top
+        self.coarse_mean_sum += mean
+        self.coarse_cold_sum += cold_length
+        self._push({"kind": "coarse", "cold_length": cold_length, "num_pages": num_pages,
+                    "num_pages_selected": len(pages), "top_score": top, "mean_score": mean,
+                    "score_ratio": self._ratio(top, mean), "pages_selected": pages, "skipped": False})
+
+    def coarse_skipped(self, cold_length: int) -> None:
+        # kiv/cold_store.py:490-512
+        self.coarse_calls += 1
+        self.coarse_cold_sum += cold_length
+        self._push({"kind": "coarse", "cold_length": cold_length, "num_pages": 0, "num_pages_selected": 0,
+                    "top_score": 0.0, "mean_score": 0.0, "score_ratio": 0.0, "pages_selected": [],
+                    "skipped": True})
+
+    def fine(self, agg_scores, selected_ids, actual_P: int, requested_P: int, cold_length: int) -> None:
+        # kiv/cold_store.py:514-547
+        top, mean = float(agg_scores.max()), float(agg_scores.mean())
+        self.fine_calls += 1
+        self.total_calls += 1
+        self.fine_top_sum += top
+        self.fine_mean_sum += mean
+        self.selected_sum += actual_P
+        self._push({"kind": "fine", "cold_length": cold_length, "actual_P": actual_P, "requested_P": requested_P,
+                    "top_score": top, "mean_score": mean, "score_ratio": self._ratio(top, mean),
+                    "selected_token_indices": selected_ids.reshape(-1).tolist()})
+
+    def snapshot(self) -> dict:
+        # kiv/cold_store.py:554-581
+        agg = {"total_calls": self.total_calls, "coarse_calls": self.coarse_calls,
+               "coarse_real_calls": self.coarse_real_calls,
+               "coarse_skipped_calls": self.coarse_calls - self.coarse_real_calls, "fine_calls": self.fine_calls}
+        if self.coarse_real_calls:
+            agg["avg_coarse_top_score"] = self.coarse_top_sum / self.coarse_real_calls
+            agg["avg_coarse_mean_score"] = self.coarse_mean_sum / self.coarse_real_calls
+        if self.coarse_calls:
+            agg["avg_cold_length"] = self.coarse_cold_sum / self.coarse_calls
+        if self.fine_calls:
+            agg["avg_fine_top_score"] = self.fine_top_sum / self.fine_calls
+            agg["avg_fine_mean_score"] = self.fine_mean_sum / self.fine_calls
+            agg["avg_selected_P"] = self.selected_sum / self.fine_calls
+        return {"aggregates": agg, "recent": list(self.ring)}
+
+
 class OracleColdStore:
-    """ColdKVStore semantics (kiv/cold_store.py:35-414) on CPU, no telemetry."""
+    """ColdKVStore semantics (kiv/cold_store.py:35-414) on CPU, with its
+    telemetry and its shared-layer candidate cache."""
 
     def __init__(self, page_size: int, num_kv_groups: int) -> None:
         self.page_size = page_size
@@ -49,6 +131,18 @@ class OracleColdStore:
         self.partial_v: torch.Tensor | None = None
         self._flat: tuple | None = None  # concatenated summaries / K / V, as after
                                          # kiv/cold_store.py:122-136 (_materialize)
+        self.telemetry = OracleTelemetry()
+        # kiv/cold_store.py:81-85: candidates of the last coarse pass, for a
+        # shared layer's call in the same decode step.
+        self.cached: tuple | None = None   # (K, V, ids, pages)
+        self.cached_step = -1
+
+    def reset(self) -> None:
+        """kiv/cold_store.py:374-389 (the telemetry is kept, as there)."""
+        self.k_pages, self.v_pages, self.summaries = [], [], []
+        self.partial_k = self.partial_v = None
+        self._flat = None
+        self.cached, self.cached_step = None, -1
 
     # kiv/cold_store.py:111-120
     @property
@@ -68,8 +162,10 @@ class OracleColdStore:
         """Append rows; every full page gets ``mean(dim=2)`` of its K rows (in
         the dtype) and is stored.  Pages are cut from views of the combined
         rows rather than by re-slicing the partial once per page, which
-        keeps bulk evictions linear; the stored values are the same."""
+        keeps bulk evictions linear; the stored values are the same.
+        Eviction drops the cached candidates (kiv/cold_store.py:148-151)."""
         self._flat = None
+        self.cached, self.cached_step = None, -1
         if self.partial_len:
             k = torch.cat([self.partial_k, k], dim=2)
             v = torch.cat([self.partial_v, v], dim=2)
@@ -113,27 +209,46 @@ class OracleColdStore:
             vs.append(vall[:, :, tok])
             ids.append(tok)
             trace.coarse_scores, trace.pages = coarse, pages
+            self.telemetry.coarse(coarse, top_idx, self.num_pages, self.cold_length)
         if self.partial_len:
             n_fin = self.num_pages * ps
             ks.append(self.partial_k)
             vs.append(self.partial_v)
             ids.append(torch.arange(n_fin, n_fin + self.partial_len))
+        if not self.num_pages:
+            self.telemetry.coarse_skipped(self.cold_length)   # kiv/cold_store.py:277-278
         return torch.cat(ks, dim=2), torch.cat(vs, dim=2), torch.cat(ids)
 
     # kiv/cold_store.py:283-371
-    def retrieve(self, query: torch.Tensor, scaling: float, top_p: int, top_pages: int):
-        """(K [B,Hkv,P',D], V, trace) or (None, None, trace) when cold is empty."""
+    def retrieve(self, query: torch.Tensor, scaling: float, top_p: int, top_pages: int, step: int = -1):
+        """(K [B,Hkv,P',D], V, trace) or (None, None, trace) when cold is empty.
+
+        A call with ``step >= 0`` equal to the step of the cached candidates
+        (and the same batch) reuses them, skipping the coarse pass, and
+        scores them with this query (kiv/cold_store.py:303-317);
+        ``trace.extra["reused"]`` says which happened."""
         trace = RetrieveTrace()
         if self.cold_length == 0:
             return None, None, trace
         P = min(top_p, self.cold_length)
-        ck, cv, cid = self.candidates(query, scaling, top_pages, trace)
+        if (step >= 0 and step == self.cached_step and self.cached is not None
+                and self.cached[0].shape[0] == query.shape[0]):
+            ck, cv, cid, trace.pages = self.cached
+            self.telemetry.coarse_skipped(self.cold_length)
+            trace.extra["reused"] = True
+        else:
+            ck, cv, cid = self.candidates(query, scaling, top_pages, trace)
+            self.cached = (ck, cv, cid, trace.pages)
+            if step >= 0:
+                self.cached_step = step
+            trace.extra["reused"] = False
         fine = torch.matmul(query, expand_kv(ck, self.groups).transpose(-2, -1)) * scaling
         agg = fine.amax(dim=(1, 2))
         _, top_local = agg.topk(min(P, agg.shape[-1]), dim=-1)
         idx = top_local[:, None, :, None].expand(-1, ck.shape[1], -1, ck.shape[3])
         trace.candidate_ids, trace.agg_scores, trace.top_local = cid, agg, top_local
         trace.selected_ids = cid[top_local]
+        self.telemetry.fine(agg, trace.selected_ids, int(top_local.shape[-1]), int(top_p), self.cold_length)
         return torch.gather(ck, 2, idx), torch.gather(cv, 2, idx), trace
 
 

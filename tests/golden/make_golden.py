@@ -1,6 +1,7 @@
 """Writes golden vectors with the reference implementation itself.
 
-    python tests/golden/make_golden.py        (build container only)
+    python tests/golden/make_golden.py          (build container only)
+    python tests/golden/make_golden.py shared   (adds the shared-layer fixtures only)
 
 The reference (Babyhamsta/KIV, Python) is imported from /root/reference in
 this container and never travels: only the vectors below are committed.
@@ -15,6 +16,9 @@ They pin what the repository's closed forms and rounding bands leave open:
   (kiv/tiered_cache.py:17-286): chunked_prefill of 96 tokens, then greedy
   decode steps with live retrieval; the weights, input ids, every step's
   logits and the tokens chosen.
+* tiny_gemma4_shared.safetensors + .npz -- the same for a random-init 4-layer
+  Gemma4 text model whose second full-attention layer shares the first's KV
+  (ModelTopology kv_sharing_map), plus the shared store's telemetry.
 """
 
 from __future__ import annotations
@@ -136,12 +140,80 @@ def tiny_model():
             "weights_seed": 7, "ids_seed": 8}
 
 
+GEMMA4_CONFIG = dict(vocab_size=128, hidden_size=64, intermediate_size=128, num_hidden_layers=4,
+                     num_attention_heads=4, num_key_value_heads=2, head_dim=16, global_head_dim=32,
+                     max_position_embeddings=512, sliding_window=16,
+                     layer_types=["sliding_attention", "full_attention", "sliding_attention", "full_attention"],
+                     num_kv_shared_layers=2, vocab_size_per_layer_input=128, hidden_size_per_layer_input=8,
+                     final_logit_softcapping=None, tie_word_embeddings=False)
+GEMMA4_TOPOLOGY = dict(global_layer_indices=(1, 3), independent_kv_layers=(1,), kv_sharing_map={3: 1},
+                       num_query_heads=4, num_kv_heads=2, head_dim=32, num_hidden_layers=4)
+
+
+def tiny_gemma4_shared():
+    """A random-init 4-layer Gemma4 text model whose last full-attention layer
+    shares the KV of the first (num_kv_shared_layers=2): both global layers
+    retrieve from one cold store, the shared layer through the candidate set
+    the source layer selected in the same decode step
+    (kiv/cold_store.py:303-329, kiv/tiered_cache.py:117-123).  Weights,
+    input ids, every step's logits, the tokens chosen and the store's
+    telemetry (every coarse and fine record) are written."""
+    from safetensors.torch import save_file
+    from transformers import Gemma4TextConfig
+    from transformers.models.gemma4.modeling_gemma4 import Gemma4ForCausalLM
+
+    from kiv.config import KIVConfig
+    from kiv.middleware import KIVMiddleware
+    from kiv.model_topology import ModelTopology
+
+    cfg = Gemma4TextConfig(**GEMMA4_CONFIG)
+    cfg._attn_implementation = "eager"
+    torch.manual_seed(11)
+    model = Gemma4ForCausalLM(cfg).eval()
+    save_file({k: v.contiguous() for k, v in model.state_dict().items()},
+              os.path.join(HERE, "tiny_gemma4_shared.safetensors"))
+    kiv = {"hot_budget": 24, "top_p": 12, "page_size": 8, "top_pages": 2}
+    kcfg = KIVConfig(prefetch_stream=False, **kiv)
+    topo = ModelTopology.manual(**GEMMA4_TOPOLOGY)
+    mw = KIVMiddleware(model, kcfg, topology=topo)
+    mw.install()
+    cache = mw.create_cache(torch.device("cpu"))
+    ids = torch.randint(0, 128, (1, 96), generator=torch.Generator().manual_seed(12))
+    with torch.no_grad():
+        logits = mw.chunked_prefill(ids, cache, chunk_size=32)
+        steps, toks = [logits[0].float().numpy().copy()], []
+        tok = logits.argmax(-1)
+        for _ in range(6):
+            toks.append(int(tok.item()))
+            out = model(input_ids=tok.view(1, 1), past_key_values=cache, use_cache=True)
+            lg = out.logits[:, -1]
+            steps.append(lg[0].float().numpy().copy())
+            tok = lg.argmax(-1)
+    mw.uninstall()
+    snap = cache.get_cold_store(1).telemetry_snapshot()
+    np.savez_compressed(os.path.join(HERE, "tiny_gemma4_shared.npz"), input_ids=ids.numpy(),
+                        logits=np.stack(steps), tokens=np.array(toks, dtype=np.int64))
+    return {"config": GEMMA4_CONFIG, "topology": {k: (list(v) if isinstance(v, tuple) else v)
+                                                  for k, v in GEMMA4_TOPOLOGY.items()},
+            "kiv": kiv, "prefill": {"tokens": 96, "chunk_size": 32}, "decode_steps": 6,
+            "attn_implementation": "eager", "weights_seed": 11, "ids_seed": 12,
+            "telemetry": snap}
+
+
 def main():
     sys.path.insert(0, REFERENCE)
     torch.set_num_threads(1)
-    manifest = {"reference": "Babyhamsta/KIV (read-only copy in the build container)",
-                "torch": torch.__version__, "retrieval": retrieval_cases(), "tiny_qwen2": tiny_model()}
-    with open(os.path.join(HERE, "manifest.json"), "w") as f:
+    path = os.path.join(HERE, "manifest.json")
+    if sys.argv[1:] == ["shared"]:
+        # Adds the shared-layer fixtures; the others are left as they are.
+        with open(path) as f:
+            manifest = json.load(f)
+        manifest["tiny_gemma4_shared"] = tiny_gemma4_shared()
+    else:
+        manifest = {"reference": "Babyhamsta/KIV (read-only copy in the build container)",
+                    "torch": torch.__version__, "retrieval": retrieval_cases(), "tiny_qwen2": tiny_model(),
+                    "tiny_gemma4_shared": tiny_gemma4_shared()}
+    with open(path, "w") as f:
         json.dump(manifest, f, indent=1, default=str)
     print("wrote", sorted(os.listdir(HERE)))
 

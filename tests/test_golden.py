@@ -20,7 +20,7 @@ import pytest
 import torch
 
 from oracle import exact
-from oracle.bands import check_topk, score_interval
+from oracle.bands import check_topk, max_band, mean_band, score_interval
 from oracle.torch_ref import OracleColdStore
 
 HERE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
@@ -66,10 +66,44 @@ def test_oracle_reproduces_reference(case, data):
     assert trace.pages.tolist() == t["pages"].tolist()
     assert np.array_equal(trace.selected_ids.numpy(), t["selected"])
     assert torch.equal(k_out, t["k_out"]) and torch.equal(v_out, t["v_out"])
-    # Telemetry scores (kiv/cold_store.py:468-469, 524-525).
-    assert float(trace.coarse_scores.max()) == case["coarse_top_score"]
-    assert float(trace.coarse_scores.float().mean()) == pytest.approx(case["coarse_mean_score"], rel=1e-2, abs=1e-2)
-    assert float(trace.agg_scores.max()) == case["fine_top_score"]
+    # Telemetry records (kiv/cold_store.py:456-547), bit for bit.
+    coarse, fine = store.telemetry.ring[-2], store.telemetry.ring[-1]
+    assert coarse["top_score"] == case["coarse_top_score"] and coarse["mean_score"] == case["coarse_mean_score"]
+    assert fine["top_score"] == case["fine_top_score"] and fine["mean_score"] == case["fine_mean_score"]
+    assert coarse["skipped"] == case["coarse_skipped"] and fine["actual_P"] == case["actual_P"]
+    assert coarse["pages_selected"] == t["pages"].tolist()
+    assert fine["selected_token_indices"] == t["selected"].reshape(-1).tolist()
+
+
+def telemetry_bands(case, t, store, pages=None):
+    """Intervals of the four telemetry scores from the case's inputs:
+    {name: (lo, hi)} for coarse/fine top and mean; the fine ones over the
+    candidates of ``pages`` (default: the reference's union)."""
+    pages = t["pages"] if pages is None else np.asarray(pages, dtype=np.int64)
+    q = t["q"].float().numpy()
+    N, ps = store.num_pages, case["page_size"]
+    lo, hi = score_interval(q, store.flat()[0].float().numpy(), case["scaling"], case["dtype"], "activation")
+    out = {"coarse_top_score": max_band(lo, hi), "coarse_mean_score": mean_band(lo, hi, case["dtype"], "activation")}
+    cand = exact.candidate_ids(pages, ps, N * ps, store.cold_length - N * ps)
+    ck = store.all_k()[:, :, torch.from_numpy(cand)]
+    lo, hi = score_interval(q, ck.float().numpy(), case["scaling"], case["dtype"], "activation")
+    lo, hi = lo.max(axis=(1, 2)), hi.max(axis=(1, 2))
+    out["fine_top_score"] = max_band(lo, hi)
+    out["fine_mean_score"] = mean_band(lo, hi, case["dtype"], "activation")
+    return out
+
+
+@pytest.mark.parametrize("case", CASES, ids=[c["name"] for c in CASES])
+def test_reference_telemetry_within_bands(case, data):
+    """The reference's own telemetry scores lie in the intervals the HIP
+    telemetry is held to; where an interval is a single dtype value, that
+    value is the reference's."""
+    t = tensors(case, data)
+    store = build_oracle(case, t)
+    for name, (lo, hi) in telemetry_bands(case, t, store).items():
+        assert lo <= case[name] <= hi, (name, lo, case[name], hi)
+        if "top" in name:
+            assert hi - lo <= abs(case[name]) * 2 ** -6 + 1e-6, (name, lo, hi)  # a few dtype steps at most
 
 
 @pytest.mark.parametrize("case", CASES, ids=[c["name"] for c in CASES])

@@ -370,3 +370,29 @@ def test_missing_mask_rule_follows_the_original_attention():
     assert _none_mask_rule("sdpa", plain_module, 64, 96) == "none"
     assert _none_mask_rule("eager", causal_module, 64, 96) == "none"
     assert _none_mask_rule("flash_attention_2", causal_module, 64, 64) is None
+
+
+def test_detect_topology_gemma4_per_layer_geometry():
+    """Gemma4 keeps its full-attention layers' head_dim and kv heads in
+    per_layer_config: detection reads them there, and the kv-shared
+    full-attention layer maps to the last owning one, as in the topology
+    the reference's golden run used (tests/golden/manifest.json)."""
+    import json
+    import os
+
+    from transformers import Gemma4TextConfig
+    from transformers.models.gemma4.modeling_gemma4 import Gemma4ForCausalLM
+
+    from kiv_amd import detect_topology
+
+    here = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+    with open(os.path.join(here, "manifest.json")) as f:
+        meta = json.load(f)["tiny_gemma4_shared"]
+    model = Gemma4ForCausalLM(Gemma4TextConfig(**meta["config"]))
+    t = detect_topology(model)
+    top = meta["topology"]
+    assert t.global_layer_indices == tuple(top["global_layer_indices"])
+    assert t.independent_kv_layers == tuple(top["independent_kv_layers"])
+    assert t.kv_sharing_map == {int(k): v for k, v in top["kv_sharing_map"].items()}
+    assert (t.num_query_heads, t.num_kv_heads, t.head_dim) == (top["num_query_heads"], top["num_kv_heads"],
+                                                                top["head_dim"])

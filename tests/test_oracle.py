@@ -150,3 +150,50 @@ def test_expand_kv_mapping():
     assert y.shape == (2, 12, 1, 1)
     assert torch.equal(y[:, :, 0, 0], x[:, :, 0, 0].repeat_interleave(4, dim=1))
     assert np.array_equal(exact.expand_kv(x.numpy(), 4), y.numpy())
+
+
+def test_shared_layer_reuse_scores_the_cached_union():
+    """kiv/cold_store.py:303-317: a second call in the same decode step
+    (step >= 0, same batch) keeps the first call's candidates and scores
+    them with its own query.  Query B targets another segment, so its own
+    union differs from A's: the reused selection must be the fp64 top-P of
+    B over A's candidates (separated scores), and a fresh step recomputes."""
+    w = Workload("reuse", 8, 2, 64, torch.float32, hot=8, cold=4096 + 17, top_pages=4, top_p=64, segment=256)
+    data = generate(w, seed=8)
+    store = OracleColdStore(w.page_size, w.groups)
+    store.evict(data["cold_k"], data["cold_v"])
+    qa = data["q"]
+    g = torch.Generator().manual_seed(9)
+    seg_b = (int(data["targets"][0, 0]) + 7) % (w.cold // w.segment)
+    cold = data["cold_k"].float()
+    qb = (cold[:, :, seg_b * w.segment:(seg_b + 1) * w.segment].mean(2).repeat_interleave(w.groups, 1)[:, :, None]
+          + 0.1 * torch.randn(1, w.num_q_heads, 1, w.head_dim, generator=g)).to(w.dtype)
+    _, _, ta = store.retrieve(qa, w.scaling, w.top_p, w.top_pages, step=3)
+    _, _, tb = store.retrieve(qb, w.scaling, w.top_p, w.top_pages, step=3)
+    assert ta.extra["reused"] is False and tb.extra["reused"] is True
+    assert torch.equal(tb.pages, ta.pages) and torch.equal(tb.candidate_ids, ta.candidate_ids)
+    # B's own union is different: the reuse matters.
+    _, _, tb_own = OracleColdStore.retrieve(_copy(store), qb, w.scaling, w.top_p, w.top_pages)
+    assert tb_own.pages.tolist() != ta.pages.tolist()
+    # The reused selection is B's top-P over A's candidates.
+    cand = ta.candidate_ids.numpy()
+    fine = exact.scores64(f64(qb), f64(data["cold_k"])[:, :, cand], w.scaling, w.groups)
+    want, gap = exact.top_k_set(exact.fine_aggregate(fine)[0], w.top_p)
+    assert gap > 1e-3
+    assert sorted(tb.selected_ids[0].tolist()) == cand[want].tolist()
+    snap = store.telemetry.snapshot()["aggregates"]
+    assert (snap["coarse_calls"], snap["coarse_real_calls"], snap["coarse_skipped_calls"], snap["fine_calls"]) == (2, 1, 1, 2)
+    # Another step (or an eviction) starts a fresh coarse pass.
+    _, _, tc = store.retrieve(qb, w.scaling, w.top_p, w.top_pages, step=4)
+    assert tc.extra["reused"] is False and tc.pages.tolist() == tb_own.pages.tolist()
+    store.retrieve(qa, w.scaling, w.top_p, w.top_pages, step=5)
+    store.evict(data["hot_k"][:, :, :1], data["hot_v"][:, :, :1])
+    _, _, td = store.retrieve(qb, w.scaling, w.top_p, w.top_pages, step=5)
+    assert td.extra["reused"] is False
+
+
+def _copy(store: OracleColdStore) -> OracleColdStore:
+    """A store with the same rows and no cached candidates or telemetry."""
+    c = OracleColdStore(store.page_size, store.groups)
+    c.evict(store.all_k(), store.all_v())
+    return c
