@@ -57,9 +57,9 @@ typedef struct {
   int32_t batch;          /* B */
   int32_t num_q_heads;    /* Hq */
   int32_t num_kv_heads;   /* Hkv; Hq % Hkv == 0, q head h reads kv head h / (Hq/Hkv) */
-  int32_t head_dim;       /* D = c * (16 / element bytes) with c one of 2 4 6 8 10 12 14 16 20 24
-                             28 32 40 48 64: 16..512 for bf16/fp16 (e.g. 64 80 96 128 256),
-                             8..256 for fp32 */
+  int32_t head_dim;       /* D = c * (16 / element bytes), rows of c 16-byte chunks, with c one of
+                             1 2 4 6 8 10 12 14 16 20 24 28 32 40 48 64: 8..512 for bf16/fp16
+                             (e.g. 64 80 96 128 256), 4..256 for fp32 */
   int32_t page_size;      /* tokens per page (>= 1) */
   int32_t dtype;          /* KIV_DTYPE_* of K, V, Q and outputs */
   int32_t cold_tier;      /* KIV_TIER_* placement of finished pages' rows */
@@ -76,6 +76,9 @@ typedef struct {
   int64_t summary_bytes; /* dtype page summaries (used part) */
   int64_t partial_bytes; /* K + V rows of the partial page */
   int64_t reserved_bytes;/* everything the store holds, host + device */
+  int64_t reserved_device_bytes; /* what it holds in device memory: summaries, partial page,
+                                    HBM-tier rows, retrieval scratch (K staging included) */
+  int64_t reserved_host_bytes;   /* what it holds in pinned host memory (the arena's chunks) */
 } kiv_store_info_t;
 
 /* Retrieval flags.  KIV_RETRIEVE_PRUNE: on the host tier, the coarse scan

@@ -290,9 +290,17 @@ class ColdKVStore:
         self._telemetry = _RetrievalTelemetry()
 
     def memory_bytes(self) -> dict[str, int]:
-        """Bytes per tier, keys as kiv/cold_store.py:399-414 (+ HBM-tier rows)."""
+        """Bytes per tier, keys as kiv/cold_store.py:399-414, plus the HBM
+        tiers' cold rows and what the store reserves.
+
+        The reference's keys count the bytes in use (K/V rows of finished
+        pages, dtype summaries, the partial page's rows).  ``reserved_gpu``
+        is everything the store holds in device memory -- grown buffers,
+        the HBM tiers' arena chunks and the retrieval scratch, whose K
+        staging copy is the largest part (up to 256 MiB per store on the
+        host tier) -- and ``reserved_cpu`` the pinned host arena's chunks."""
         out = {"k_index_cpu": 0, "v_store_cpu": 0, "page_summaries_gpu": 0, "partial_gpu": 0,
-               "k_cold_gpu": 0, "v_cold_gpu": 0}
+               "k_cold_gpu": 0, "v_cold_gpu": 0, "reserved_gpu": 0, "reserved_cpu": 0}
         if self._handle is None:
             return out
         info = nat.StoreInfo()
@@ -302,6 +310,8 @@ class ColdKVStore:
         out["v_cold_gpu" if tier == "hbm" else "v_store_cpu"] = info.v_cold_bytes
         out["page_summaries_gpu"] = info.summary_bytes
         out["partial_gpu"] = info.partial_bytes
+        out["reserved_gpu"] = info.reserved_device_bytes
+        out["reserved_cpu"] = info.reserved_host_bytes
         return out
 
     # ------------------------------------------------- inspection (tests)

@@ -51,8 +51,8 @@ inline int vec_elems(int dtype) { return 16 / elem_bytes(dtype); }
 // them): head_dim = chunks * (16 / element bytes).
 inline bool scan_supports_chunks(int cpr) {
   switch (cpr) {
-    case 2: case 4: case 6: case 8: case 10: case 12: case 14: case 16: case 20: case 24: case 28: case 32:
-    case 40: case 48: case 64:
+    case 1: case 2: case 4: case 6: case 8: case 10: case 12: case 14: case 16: case 20: case 24: case 28:
+    case 32: case 40: case 48: case 64:
       return true;
   }
   return false;

@@ -785,6 +785,7 @@ __global__ void __launch_bounds__(kScanThreads) coarse_scan_mfma_kernel(
 template <typename F> static int with_cpr(int cpr, F &&f) {
   using std::integral_constant;
   switch (cpr) {
+    case 1: return f(integral_constant<int, 1>{});
     case 2: return f(integral_constant<int, 2>{});
     case 4: return f(integral_constant<int, 4>{});
     case 6: return f(integral_constant<int, 6>{});

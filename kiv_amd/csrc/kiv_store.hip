@@ -463,7 +463,9 @@ int kiv_store_info(const kiv_store_t *s, kiv_store_info_t *out) {
   out->v_cold_bytes = s->num_pages * s->page_bytes;
   out->summary_bytes = s->num_pages * s->kr * s->row_bytes;
   out->partial_bytes = 2 * s->partial_len * s->kr * s->row_bytes;
-  out->reserved_bytes = s->reserved_host_bytes() + s->reserved_device_bytes();
+  out->reserved_device_bytes = s->reserved_device_bytes();
+  out->reserved_host_bytes = s->reserved_host_bytes();
+  out->reserved_bytes = out->reserved_device_bytes + out->reserved_host_bytes;
   return KIV_OK;
 }
 

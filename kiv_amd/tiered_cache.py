@@ -240,21 +240,39 @@ class TieredKVCache(DynamicCache):
         return True
 
     def memory_report(self) -> dict:
-        """Bytes per tier (keys of kiv/tiered_cache.py:259-286, plus HBM-tier rows)."""
-        hot = sum(l.keys.nelement() * l.keys.element_size() + l.values.nelement() * l.values.element_size()
-                  for _, l in self._owned_layers())
+        """Bytes per tier, keys of kiv/tiered_cache.py:259-286 plus what
+        this path holds beyond the bytes in use.
+
+        ``hot_vram_bytes`` and the per-tier keys count the bytes in use, as
+        the reference does.  ``hot_buffer_vram_bytes`` is the hot windows'
+        buffers (each keeps room for 256 more rows), and
+        ``retrieval_scratch_vram_bytes`` the stores' device memory beyond
+        their summaries, partial pages and cold rows (mostly the K staging
+        copy).  ``total_vram_bytes`` / ``total_cpu_bytes`` are everything
+        held in device / pinned host memory, reservations included, so a
+        caller that budgets by them sees the real footprint."""
+        hot = hot_buf = 0
+        for _, l in self._owned_layers():
+            used = l.keys.nelement() * l.keys.element_size() + l.values.nelement() * l.values.element_size()
+            hot += used
+            if isinstance(l, _HotLayer) and l._kb is not None and l.keys is l._view:
+                hot_buf += l._kb.nelement() * l._kb.element_size() + l._vb.nelement() * l._vb.element_size()
+            else:
+                hot_buf += used
         tot = {"k_index_cpu": 0, "v_store_cpu": 0, "page_summaries_gpu": 0, "partial_gpu": 0,
-               "k_cold_gpu": 0, "v_cold_gpu": 0}
+               "k_cold_gpu": 0, "v_cold_gpu": 0, "reserved_gpu": 0, "reserved_cpu": 0}
         for store in self.cold_stores.values():
             for key, val in store.memory_bytes().items():
                 tot[key] += val
+        used_gpu = tot["page_summaries_gpu"] + tot["partial_gpu"] + tot["k_cold_gpu"] + tot["v_cold_gpu"]
         return {
             "hot_vram_bytes": hot,
             "k_index_cpu_bytes": tot["k_index_cpu"],
             "v_store_cpu_bytes": tot["v_store_cpu"],
             "page_summaries_gpu_bytes": tot["page_summaries_gpu"],
             "cold_rows_gpu_bytes": tot["k_cold_gpu"] + tot["v_cold_gpu"],
-            "total_vram_bytes": hot + tot["page_summaries_gpu"] + tot["partial_gpu"] + tot["k_cold_gpu"]
-            + tot["v_cold_gpu"],
-            "total_cpu_bytes": tot["k_index_cpu"] + tot["v_store_cpu"],
+            "hot_buffer_vram_bytes": hot_buf,
+            "retrieval_scratch_vram_bytes": max(0, tot["reserved_gpu"] - used_gpu),
+            "total_vram_bytes": hot_buf + max(tot["reserved_gpu"], used_gpu),
+            "total_cpu_bytes": max(tot["reserved_cpu"], tot["k_index_cpu"] + tot["v_store_cpu"]),
         }
