@@ -148,18 +148,36 @@ def mask_kind(dtype: torch.dtype) -> int:
         raise TypeError(f"unsupported attention mask dtype {dtype}") from None
 
 
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
 def stream_ptr(device: torch.device) -> int:
     """Raw hipStream_t of torch's current stream on ``device``."""
-    return torch.cuda.current_stream(device).cuda_stream
+    idx = device.index
+    if idx is None:
+        idx = torch.cuda.current_device()
+    if _raw_stream is not None:
+        return _raw_stream(idx)
+    return torch.cuda.current_stream(idx).cuda_stream
 
 
 def ptr(t: torch.Tensor | None) -> int | None:
     return None if t is None else t.data_ptr()
 
 
+_ARRAYS = {3: _I64x3, 4: _I64x4}
+_strides_cache: dict[tuple, C.Array] = {}
+
+
 def strides(t: torch.Tensor, n: int):
-    """The first n strides of t (elements) as a ctypes int64 array."""
-    arr = (C.c_int64 * n)()
-    for i in range(n):
-        arr[i] = t.stride(i) if t.size(i) != 1 else 0
+    """The first n strides of t (elements) as a ctypes int64 array; size-1
+    dimensions get stride 0.  The arrays are shared between calls (cached
+    per shape and strides): callers pass them on and never modify them."""
+    key = (t.shape, t.stride(), n)
+    arr = _strides_cache.get(key)
+    if arr is None:
+        shape, st, _ = key
+        arr = _ARRAYS.get(n, C.c_int64 * n)(*[0 if shape[i] == 1 else st[i] for i in range(n)])
+        if len(_strides_cache) < 4096:
+            _strides_cache[key] = arr
     return arr

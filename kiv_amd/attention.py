@@ -20,6 +20,8 @@ from . import _native as nat
 
 _ws_lock = threading.Lock()
 _workspaces: dict[int, torch.Tensor] = {}
+_ws_sizes: dict[tuple, int] = {}
+_NO_STRIDES = nat._I64x4()
 
 
 def _workspace(device: torch.device, nbytes: int) -> torch.Tensor:
@@ -29,6 +31,9 @@ def _workspace(device: torch.device, nbytes: int) -> torch.Tensor:
     streams of one device must not overlap.
     """
     idx = device.index or 0
+    ws = _workspaces.get(idx)
+    if ws is not None and ws.numel() >= nbytes:
+        return ws
     with _ws_lock:
         ws = _workspaces.get(idx)
         if ws is None or ws.numel() < nbytes:
@@ -37,10 +42,20 @@ def _workspace(device: torch.device, nbytes: int) -> torch.Tensor:
         return ws
 
 
+def _decode_ws_size(B: int, hq: int, hkv: int, D: int, Q: int, cold_len: int, T: int) -> int:
+    key = (B, hq, hkv, D, Q, cold_len, T)
+    n = _ws_sizes.get(key)
+    if n is None:
+        n = nat.lib().kiv_attention_workspace_size(B, hq, hkv, D, Q, cold_len, T)
+        if len(_ws_sizes) < 4096:
+            _ws_sizes[key] = n
+    return n
+
+
 def _mask_view(mask: torch.Tensor | None, hot_len: int, causal: bool = False):
     """(pointer, kind, strides b,h,q,t) of a 2-D or 4-D mask over hot columns."""
     if mask is None:
-        return None, nat.MASK_CAUSAL if causal else nat.MASK_NONE, (C.c_int64 * 4)()
+        return None, nat.MASK_CAUSAL if causal else nat.MASK_NONE, _NO_STRIDES
     if mask.shape[-1] != hot_len:
         raise ValueError(f"mask covers {mask.shape[-1]} columns, hot window has {hot_len}")
     if mask.dim() == 2:
@@ -50,9 +65,11 @@ def _mask_view(mask: torch.Tensor | None, hot_len: int, causal: bool = False):
     return mask.data_ptr(), nat.mask_kind(mask.dtype), nat.strides(mask, 4)
 
 
-def _prepare(query: torch.Tensor, cold_len: int, hot_k: torch.Tensor, hot_v: torch.Tensor,
-             mask: torch.Tensor | None, scaling: float, causal: bool = False, workspace: bool = True):
-    """(args without retrieved keys, output, tensors the launches read)."""
+def fill_args(args, query: torch.Tensor, cold_len: int, hot_k: torch.Tensor, hot_v: torch.Tensor,
+              mask: torch.Tensor | None, scaling: float, causal: bool = False, workspace: bool = True):
+    """Fill ``args`` (an AttentionArgs, reused by callers that attend often)
+    for this query and hot window, retrieved keys still unset; returns the
+    output tensor and the tensors the launch reads."""
     B, hq, Q, D = query.shape
     hkv = hot_k.shape[1]
     dt = query.dtype
@@ -64,23 +81,32 @@ def _prepare(query: torch.Tensor, cold_len: int, hot_k: torch.Tensor, hot_v: tor
         hot_v = hot_v.contiguous()
     q = query if query.stride(3) == 1 else query.contiguous()
     T = hot_k.shape[2]
-    lib = nat.lib()
     if workspace:
-        ws = _workspace(query.device, lib.kiv_attention_workspace_size(B, hq, hkv, D, Q, cold_len, T))
-        ws_ptr, ws_bytes = ws.data_ptr(), ws.numel()
+        ws = _workspace(query.device, _decode_ws_size(B, hq, hkv, D, Q, cold_len, T))
+        args.workspace, args.workspace_bytes = ws.data_ptr(), ws.numel()
     else:
-        ws_ptr, ws_bytes = None, 0
+        args.workspace, args.workspace_bytes = None, 0
     out = torch.empty(B, Q, hq, D, dtype=dt, device=query.device)
     mptr, mkind, mstr = _mask_view(mask, T, causal)
-    args = nat.AttentionArgs(
-        batch=B, num_q_heads=hq, num_kv_heads=hkv, head_dim=D, q_len=Q, dtype=nat.dtype_code(dt),
-        q=q.data_ptr(), q_stride=nat.strides(q, 4), cold_k=None, cold_v=None, cold_len=cold_len, hot_len=T,
-        hot_k=hot_k.data_ptr(), hot_v=hot_v.data_ptr(),
-        hot_k_stride=nat.strides(hot_k, 3), hot_v_stride=nat.strides(hot_v, 3),
-        mask=mptr, mask_kind=mkind, mask_stride=mstr, scaling=float(scaling),
-        out=out.data_ptr(), workspace=ws_ptr, workspace_bytes=ws_bytes,
-    )
+    args.batch, args.num_q_heads, args.num_kv_heads, args.head_dim, args.q_len = B, hq, hkv, D, Q
+    args.dtype = nat.dtype_code(dt)
+    args.q, args.q_stride = q.data_ptr(), nat.strides(q, 4)
+    args.cold_k = args.cold_v = None
+    args.cold_len, args.hot_len = cold_len, T
+    args.hot_k, args.hot_v = hot_k.data_ptr(), hot_v.data_ptr()
+    args.hot_k_stride, args.hot_v_stride = nat.strides(hot_k, 3), nat.strides(hot_v, 3)
+    args.mask, args.mask_kind, args.mask_stride = mptr, mkind, mstr
+    args.scaling = scaling
+    args.out = out.data_ptr()
     keep = (q, hot_k, hot_v) + ((mask,) if mask is not None else ())
+    return out, keep
+
+
+def _prepare(query: torch.Tensor, cold_len: int, hot_k: torch.Tensor, hot_v: torch.Tensor,
+             mask: torch.Tensor | None, scaling: float, causal: bool = False, workspace: bool = True):
+    """(new args without retrieved keys, output, tensors the launches read)."""
+    args = nat.AttentionArgs()
+    out, keep = fill_args(args, query, cold_len, hot_k, hot_v, mask, scaling, causal, workspace)
     return args, out, keep
 
 

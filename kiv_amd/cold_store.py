@@ -19,6 +19,7 @@ from __future__ import annotations
 
 import ctypes as C
 import math
+from collections import deque
 
 import torch
 
@@ -53,7 +54,6 @@ class ColdKVStore:
         self._dtype: torch.dtype | None = None
         self._num_finalized = 0
         self._partial_len = 0
-        self._last_union_count: torch.Tensor | None = None
         # Shared-layer reuse of the last coarse union (kiv/cold_store.py:81-85).
         self._cached_candidate_k = None
         self._cached_candidate_v = None
@@ -63,6 +63,13 @@ class ColdKVStore:
         self._umax_key: tuple | None = None  # (Q, top_pages, pages) of the cached union bound
         self._umax = 1
         self._fused_kv: tuple[torch.Tensor, torch.Tensor] | None = None
+        # Argument blocks of the C calls, reused call after call.
+        self._rargs = nat.RetrieveArgs()
+        self._rargs_ref = C.byref(self._rargs)
+        self._aargs = nat.AttentionArgs()
+        self._aargs_ref = C.byref(self._aargs)
+        self._dev_index = -1
+        self._last_coarse_slot = None  # telemetry slot of the last coarse pass (its union size)
 
     # ------------------------------------------------------------ lifetime
     def __del__(self) -> None:
@@ -103,6 +110,7 @@ class ColdKVStore:
         self._batch = k.shape[0]
         self._dtype = k.dtype
         self.device = k.device
+        self._dev_index = k.get_device()
 
     # ------------------------------------------------------------- sizes
     @property
@@ -124,19 +132,22 @@ class ColdKVStore:
         Same contract as kiv/cold_store.py:142-184.
         """
         self._invalidate_candidates()
-        if k_evicted.dim() != 4 or k_evicted.shape != v_evicted.shape:
-            raise ValueError(f"expected matching [B, Hkv, T, D] K/V, got {tuple(k_evicted.shape)} "
+        shape = k_evicted.shape
+        if len(shape) != 4 or shape != v_evicted.shape:
+            raise ValueError(f"expected matching [B, Hkv, T, D] K/V, got {tuple(shape)} "
                              f"and {tuple(v_evicted.shape)}")
-        T = k_evicted.shape[2]
+        T = shape[2]
         if T == 0:
             return
-        self._ensure_handle(k_evicted)
-        B, hkv, _, d = k_evicted.shape
-        if B != self._batch or hkv != self._num_kv_heads or d != self._head_dim:
-            raise ValueError(f"evicted rows {tuple(k_evicted.shape)} do not match the store "
+        if self._handle is None:
+            self._ensure_handle(k_evicted)
+        if shape[0] != self._batch or shape[1] != self._num_kv_heads or shape[3] != self._head_dim:
+            raise ValueError(f"evicted rows {tuple(shape)} do not match the store "
                              f"(B={self._batch}, Hkv={self._num_kv_heads}, D={self._head_dim})")
         if k_evicted.dtype != self._dtype or v_evicted.dtype != self._dtype:
             raise TypeError(f"evicted rows are {k_evicted.dtype}, the store holds {self._dtype}")
+        if k_evicted.get_device() != self._dev_index or v_evicted.get_device() != self._dev_index:
+            raise ValueError(f"evicted rows on {k_evicted.device}, store on {self.device}")
         k = k_evicted if k_evicted.stride(3) == 1 else k_evicted.contiguous()
         v = v_evicted if v_evicted.stride(3) == 1 else v_evicted.contiguous()
         nat.check(nat.lib().kiv_evict(self._handle, k.data_ptr(), nat.strides(k, 3), v.data_ptr(),
@@ -182,93 +193,102 @@ class ColdKVStore:
     def _retrieve(self, query, scaling, kiv_config, step, attend):
         """One retrieval; with ``attend = (hot_k, hot_v, mask)`` also the merged
         attention (fused when the output width is known on the host)."""
-        if query.dim() != 4 or query.shape[1] != self._num_query_heads or query.shape[3] != self._head_dim:
+        shape = query.shape
+        if len(shape) != 4 or shape[1] != self._num_query_heads or shape[3] != self._head_dim:
             raise ValueError(f"query must be [B, {self._num_query_heads}, Q, {self._head_dim}], "
-                             f"got {tuple(query.shape)}")
-        if query.shape[0] != self._batch:
-            raise ValueError(f"query batch {query.shape[0]} != store batch {self._batch}")
-        if query.device != self.device:
+                             f"got {tuple(shape)}")
+        B, _, Q, D = shape
+        if B != self._batch:
+            raise ValueError(f"query batch {B} != store batch {self._batch}")
+        if query.get_device() != self._dev_index:
             raise ValueError(f"query on {query.device}, store on {self.device}")
         q = query if query.dtype == self._dtype else query.to(self._dtype)
         if q.stride(3) != 1:
             q = q.contiguous()
-        B, _, Q, D = q.shape
-        P = min(kiv_config.top_p, self.cold_length)
-        N = self.num_pages
+        top_p, top_pages = kiv_config.top_p, kiv_config.top_pages
+        cold = self._num_finalized + self._partial_len
+        P = min(top_p, cold)
+        N = self._num_finalized // self._page_size
         reuse = (step >= 0 and step == self._cached_step and self._cached_candidate_k is not None
                  and self._cached_candidate_k.shape[0] == B)
         # Lower bound of the candidate count: the union holds at least
         # min(top_pages, N) pages (exactly N when every page is selected).
-        c_low = min(kiv_config.top_pages, N) * self._page_size + self._partial_len
+        c_low = min(top_pages, N) * self._page_size + self._partial_len
         width = min(P, c_low)
         exact = width == P
         if not exact:
             width = P  # buffer width; the true count follows from U below
 
         lib = nat.lib()
-        key = (Q, int(kiv_config.top_pages), N)
+        key = (Q, top_pages, N)
         if self._umax_key != key:
             umax = C.c_int64(0)
-            nat.check(lib.kiv_max_union_pages(self._handle, Q, kiv_config.top_pages, C.byref(umax)),
-                      "kiv_max_union_pages")
+            nat.check(lib.kiv_max_union_pages(self._handle, Q, top_pages, C.byref(umax)), "kiv_max_union_pages")
             self._umax_key, self._umax = key, max(1, umax.value)
         dev = self.device
         fused = attend is not None and exact
         if fused:
             # Consumed by the attention on the same stream: one pair per store.
-            shape = (B, self._num_kv_heads, width, D)
-            if self._fused_kv is None or self._fused_kv[0].shape != shape:
-                self._fused_kv = (torch.empty(shape, dtype=self._dtype, device=dev),
-                                  torch.empty(shape, dtype=self._dtype, device=dev))
-            k_out, v_out = self._fused_kv
+            kv = self._fused_kv
+            if kv is None or kv[0].shape[2] != width:
+                shape_kv = (B, self._num_kv_heads, width, D)
+                kv = self._fused_kv = (torch.empty(shape_kv, dtype=self._dtype, device=dev),
+                                       torch.empty(shape_kv, dtype=self._dtype, device=dev))
+            k_out, v_out = kv
         else:
             k_out = torch.empty(B, self._num_kv_heads, width, D, dtype=self._dtype, device=dev)
             v_out = torch.empty_like(k_out)
         coarse_runs = N > 0 and not reuse
-        # The telemetry ring's slots for this call (kernels fill every entry
+        # This call's slot of the telemetry ring (kernels fill every entry
         # they own, so no zero-fill launches here).
-        stats, idx_out, pages_out, union_count = self._telemetry.slots(dev, B, width, self._umax, coarse_runs)
-        accum = self._telemetry.accumulator(dev)
-        args = nat.RetrieveArgs(
-            q=q.data_ptr(), q_stride=nat.strides(q, 4), q_len=Q, scaling=float(scaling),
-            top_pages=int(kiv_config.top_pages), out_width=int(width), reuse_candidates=1 if reuse else 0,
-            flags=nat.RETRIEVE_PRUNE if getattr(kiv_config, "fine_pruning", False) else 0,
-            k_out=k_out.data_ptr(), v_out=v_out.data_ptr(), idx_out=idx_out.data_ptr(),
-            pages_out=nat.ptr(pages_out), union_count_out=nat.ptr(union_count),
-            stats_out=stats.data_ptr(), stats_accum=accum.data_ptr(),
-        )
+        tel = self._telemetry
+        slot = tel.take_slot(dev, B, width, self._umax, coarse_runs)
+        a = self._rargs
+        a.q = q.data_ptr()
+        a.q_stride = nat.strides(q, 4)
+        a.q_len = Q
+        a.scaling = scaling
+        a.top_pages = top_pages
+        a.out_width = width
+        a.reuse_candidates = 1 if reuse else 0
+        a.flags = nat.RETRIEVE_PRUNE if getattr(kiv_config, "fine_pruning", False) else 0
+        a.k_out = k_out.data_ptr()
+        a.v_out = v_out.data_ptr()
+        a.idx_out = slot.sel_ptr
+        a.pages_out = slot.pages_ptr
+        a.union_count_out = slot.count_ptr
+        a.stats_out = slot.stats_ptr
+        a.stats_accum = tel.accum_ptr
+        stream = nat.stream_ptr(dev)
         out = None
         if fused:
             hot_k, hot_v, mask = attend
-            aargs, out, _keep = attention._prepare(q, width, hot_k, hot_v, mask, scaling)
-            attention._set_cold(aargs, k_out, v_out, self._dtype)
-            nat.check(lib.kiv_retrieve_attend(self._handle, C.byref(args), C.byref(aargs), nat.stream_ptr(dev)),
+            out, _keep = attention.fill_args(self._aargs, q, width, hot_k, hot_v, mask, scaling)
+            self._aargs.cold_k, self._aargs.cold_v = a.k_out, a.v_out
+            nat.check(lib.kiv_retrieve_attend(self._handle, self._rargs_ref, self._aargs_ref, stream),
                       "kiv_retrieve_attend")
         else:
-            nat.check(lib.kiv_retrieve(self._handle, C.byref(args), nat.stream_ptr(dev)), "kiv_retrieve")
+            nat.check(lib.kiv_retrieve(self._handle, self._rargs_ref, stream), "kiv_retrieve")
 
         if coarse_runs:
-            self._last_union_count = union_count
-            self._telemetry.record_coarse(stats=stats, pages=pages_out, union_count=union_count,
-                                          num_pages=N, cold_length=self.cold_length)
+            self._last_coarse_slot = slot
+            tel.record_coarse(slot, num_pages=N, cold_length=cold)
         else:
-            self._telemetry.record_coarse_skipped(cold_length=self.cold_length)
+            tel.record_coarse_skipped(cold_length=cold)
         if not reuse:
-            self._cached_candidate_k = _CandidateSet(B)
-            self._cached_candidate_v = self._cached_candidate_k
-            self._cached_candidate_idx = self._cached_candidate_k
+            self._cached_candidate_k = self._cached_candidate_v = self._cached_candidate_idx = _CandidateSet(B)
             if step >= 0:
                 self._cached_step = step
 
         if not exact:
             # Only reachable when top_p > top_pages * page_size: the output
             # width depends on the union size, so read U back.
-            U = int(self._last_union_count.item()) if N > 0 else 0
+            U = tel.union_size(self._last_coarse_slot) if N > 0 else 0
             actual = min(P, U * self._page_size + self._partial_len)
-            k_out, v_out, idx_out = k_out[:, :, :actual], v_out[:, :, :actual], idx_out[:, :actual]
-            width = actual
-        self._telemetry.record_fine(stats=stats, selected=idx_out, actual_P=width,
-                                    requested_P=int(kiv_config.top_p), cold_length=self.cold_length)
+            k_out, v_out = k_out[:, :, :actual], v_out[:, :, :actual]
+        else:
+            actual = width
+        tel.record_fine(slot, actual_P=actual, requested_P=int(top_p), cold_length=cold)
         if attend is not None and out is None:
             hot_k, hot_v, mask = attend
             out = attention.decode_attention(q, k_out, v_out, hot_k, hot_v, mask, scaling)
@@ -346,6 +366,12 @@ class ColdKVStore:
         return k, v
 
 
+class _Slot:
+    """Device addresses of one retrieval call's entries in the telemetry rings."""
+
+    __slots__ = ("index", "rings", "batch", "width", "stats_ptr", "sel_ptr", "pages_ptr", "count_ptr")
+
+
 class _RetrievalTelemetry:
     """Per-call coarse/fine records in a 256-entry ring, read lazily.
 
@@ -367,75 +393,86 @@ class _RetrievalTelemetry:
         self.fine_calls = 0
         self.selected_count_sum = 0
         self._accum: torch.Tensor | None = None
-        self._ring: list[dict] = []
+        self.accum_ptr = 0
+        self._ring: deque = deque(maxlen=self._MAX_BUFFER)
         self._calls = 0  # retrieval calls, the slot counter
-        self._stats_ring: torch.Tensor | None = None   # [256, 4] float32
-        self._count_ring: torch.Tensor | None = None   # [256] int32
-        self._pages_ring: torch.Tensor | None = None   # [256, cap] int32
-        self._sel_ring: torch.Tensor | None = None     # [256, cap] int64
+        # Rings, one row per slot: stats [256, 4] f32, union sizes [256] i32,
+        # union pages [256, cap] i32, selected ids [256, cap] i64.  A ring
+        # that must grow is replaced; records keep the one they refer to.
+        self._rings: dict[str, torch.Tensor] = {}
 
-    def slots(self, device: torch.device, batch: int, width: int, max_pages: int, coarse: bool):
-        """(stats[4], selected[batch, width], pages[max_pages] | None, count[1] | None)
-        views of this call's ring slot.  A ring that must grow is replaced;
-        records keep the old one alive."""
-        n = self._MAX_BUFFER
-        if self._stats_ring is None:
-            self._stats_ring = torch.empty(n, 4, dtype=torch.float32, device=device)
-            self._count_ring = torch.empty(n, dtype=torch.int32, device=device)
-        if self._sel_ring is None or self._sel_ring.shape[1] < batch * width:
-            self._sel_ring = torch.empty(n, max(batch * width, 256), dtype=torch.int64, device=device)
-        if coarse and (self._pages_ring is None or self._pages_ring.shape[1] < max_pages):
-            self._pages_ring = torch.empty(n, max(max_pages, 64), dtype=torch.int32, device=device)
-        i = self._calls % n
-        self._calls += 1
-        selected = self._sel_ring[i, : batch * width].view(batch, width)
-        if not coarse:
-            return self._stats_ring[i], selected, None, None
-        return self._stats_ring[i], selected, self._pages_ring[i, :max_pages], self._count_ring[i : i + 1]
+    def _ring_for(self, name: str, device, cols: int, dtype) -> torch.Tensor:
+        r = self._rings.get(name)
+        if r is None or r.shape[1] < cols:
+            r = torch.empty(self._MAX_BUFFER, cols, dtype=dtype, device=device)
+            self._rings[name] = r
+        return r
 
-    def accumulator(self, device: torch.device) -> torch.Tensor:
+    def take_slot(self, device: torch.device, batch: int, width: int, max_pages: int, coarse: bool) -> _Slot:
+        """This call's slot: device addresses of its stats[4], selected ids
+        [batch, width], union pages [max_pages] and union size (the last two
+        0 when no coarse pass runs)."""
         if self._accum is None:
             self._accum = torch.zeros(4, dtype=torch.float64, device=device)
-        return self._accum
+            self.accum_ptr = self._accum.data_ptr()
+        stats = self._ring_for("stats", device, 4, torch.float32)
+        count = self._ring_for("count", device, 1, torch.int32)
+        sel = self._ring_for("sel", device, max(batch * width, 256), torch.int64)
+        i = self._calls % self._MAX_BUFFER
+        self._calls += 1
+        s = _Slot()
+        s.index, s.batch, s.width = i, batch, width
+        s.stats_ptr = stats.data_ptr() + i * 16
+        s.sel_ptr = sel.data_ptr() + i * sel.shape[1] * 8
+        if coarse:
+            pages = self._ring_for("pages", device, max(max_pages, 64), torch.int32)
+            s.pages_ptr = pages.data_ptr() + i * pages.shape[1] * 4
+            s.count_ptr = count.data_ptr() + i * 4
+            s.rings = (stats, sel, pages, count)
+        else:
+            s.pages_ptr = s.count_ptr = 0
+            s.rings = (stats, sel, None, None)
+        return s
 
-    def _push(self, rec: dict) -> None:
-        self._ring.append(rec)
-        if len(self._ring) > self._MAX_BUFFER:
-            del self._ring[: len(self._ring) - self._MAX_BUFFER]
+    def union_size(self, slot: _Slot) -> int:
+        """U of the slot's coarse pass (synchronises)."""
+        return int(slot.rings[3][slot.index, 0].item())
 
-    def record_coarse(self, *, stats, pages, union_count, num_pages, cold_length) -> None:
+    def record_coarse(self, slot: _Slot, *, num_pages, cold_length) -> None:
         self.coarse_calls += 1
         self.coarse_real_calls += 1
         self.coarse_cold_length_sum += cold_length
-        self._push({"kind": "coarse", "cold_length": cold_length, "num_pages": num_pages,
-                    "_stats": stats, "_pages": pages, "_count": union_count, "skipped": False})
+        self._ring.append({"kind": "coarse", "cold_length": cold_length, "num_pages": num_pages,
+                           "_slot": slot, "skipped": False})
 
     def record_coarse_skipped(self, *, cold_length: int) -> None:
         self.coarse_calls += 1
         self.coarse_cold_length_sum += cold_length
-        self._push({"kind": "coarse", "cold_length": cold_length, "num_pages": 0,
-                    "num_pages_selected": 0, "top_score": 0.0, "mean_score": 0.0, "score_ratio": 0.0,
-                    "pages_selected": [], "skipped": True})
+        self._ring.append({"kind": "coarse", "cold_length": cold_length, "num_pages": 0,
+                           "num_pages_selected": 0, "top_score": 0.0, "mean_score": 0.0, "score_ratio": 0.0,
+                           "pages_selected": [], "skipped": True})
 
-    def record_fine(self, *, stats, selected, actual_P, requested_P, cold_length) -> None:
+    def record_fine(self, slot: _Slot, *, actual_P, requested_P, cold_length) -> None:
         self.fine_calls += 1
         self.total_calls += 1
         self.selected_count_sum += actual_P
-        self._push({"kind": "fine", "cold_length": cold_length, "actual_P": actual_P,
-                    "requested_P": requested_P, "_stats": stats, "_selected": selected})
+        self._ring.append({"kind": "fine", "cold_length": cold_length, "actual_P": actual_P,
+                           "requested_P": requested_P, "_slot": slot})
 
     @staticmethod
     def _ratio(top: float, mean: float) -> float:
         return (top / abs(mean)) if mean else math.inf
 
     def _materialise(self, rec: dict) -> dict:
-        if "_stats" not in rec:
+        slot = rec.get("_slot")
+        if slot is None:
             return dict(rec)
-        stats = rec["_stats"].tolist()
+        stats_ring, sel_ring, pages_ring, count_ring = slot.rings
+        stats = stats_ring[slot.index].tolist()
         out = {k: v for k, v in rec.items() if not k.startswith("_")}
         if rec["kind"] == "coarse":
-            n = int(rec["_count"].item())
-            pages = rec["_pages"][:n].tolist()
+            n = int(count_ring[slot.index, 0].item())
+            pages = pages_ring[slot.index, :n].tolist()
             top, mean = stats[0], stats[1]
             out.update(num_pages_selected=len(pages), top_score=top, mean_score=mean,
                        score_ratio=self._ratio(top, mean), pages_selected=pages)
@@ -444,8 +481,9 @@ class _RetrievalTelemetry:
                                        "skipped")}
         else:
             top, mean = stats[2], stats[3]
+            ids = sel_ring[slot.index, :slot.batch * slot.width].view(slot.batch, slot.width)
             out.update(top_score=top, mean_score=mean, score_ratio=self._ratio(top, mean),
-                       selected_token_indices=rec["_selected"].reshape(-1).tolist())
+                       selected_token_indices=ids[:, :rec["actual_P"]].reshape(-1).tolist())
             out = {k: out[k] for k in ("kind", "cold_length", "actual_P", "requested_P", "top_score",
                                        "mean_score", "score_ratio", "selected_token_indices")}
         return out

@@ -395,6 +395,14 @@ def test_width_depends_on_union(cuda):
     k_out, _, sel = check_retrieval(store, oracle, cfg, w, data, data["q"])
     union = store.telemetry_snapshot()["recent"][-2]["pages_selected"]
     assert k_out.shape[2] == min(300, len(union) * 64)
+    # A shared layer's call in the same step takes its width from that union too.
+    q2 = (data["q"].float() + 0.3 * torch.randn(data["q"].shape, generator=torch.Generator().manual_seed(8)))
+    k1, _ = store.retrieve_top_kv(data["q"].to(cuda), w.scaling, cfg, step=1)
+    k2, _ = store.retrieve_top_kv(q2.to(w.dtype).to(cuda), w.scaling, cfg, step=1)
+    recent = store.telemetry_snapshot()["recent"]
+    assert recent[-2]["skipped"] is True and recent[-4]["skipped"] is False
+    assert k2.shape[2] == k1.shape[2] == min(300, len(recent[-4]["pages_selected"]) * 64)
+    assert recent[-1]["actual_P"] == k2.shape[2]
 
 
 def test_reuse_candidates_by_step(cuda):
