@@ -6,7 +6,8 @@
     python bench.py --workload qwen15b_prefill_chunk [--steps K] [--warmup W]
 
 One step = one global layer's decode step for one new token: evict the
-oldest hot row to the cold tier, coarse-to-fine retrieval over the cold
+oldest hot row to the cold tier (as the cache does at decode: the row is
+written by the retrieval's first launch), coarse-to-fine retrieval over the cold
 tier (page scan, per-head top pages, union, fine scores, top-P, K/V gather)
 and the merged softmax over [retrieved ; hot].  Inputs are resident before
 the timed region: the cold tier is filled (1,048,576 tokens for the default
@@ -133,7 +134,7 @@ def one_step(store, cfg, q, hot_k, hot_v, i, scaling, attn_events=None, fused=Tr
 
     T = hot_k.shape[2]
     j = (store.cold_length + i) % T
-    store.evict_from_hot(hot_k[:, :, j:j + 1], hot_v[:, :, j:j + 1])
+    store.evict_deferred(hot_k[:, :, j:j + 1], hot_v[:, :, j:j + 1])
     if fused:
         store.retrieve_attend(q, scaling, cfg, hot_k, hot_v, None)
         return

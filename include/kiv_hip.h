@@ -110,6 +110,16 @@ typedef struct {
   int32_t *union_count_out; /* [1] number of union pages U, or NULL */
   float *stats_out;      /* [4] coarse top, coarse mean, fine top, fine mean, or NULL */
   double *stats_accum;   /* [4] running sums of stats_out, or NULL */
+  /* Rows to evict before retrieving, exactly as kiv_evict(store, append_k,
+   * append_k_stride, append_v, append_v_stride, append_tokens) would (0 for
+   * none): the decode step's rows leaving the hot window.  Rows that stay in
+   * the partial page are copied inside the coarse scan's launch instead of
+   * a launch of their own when a fresh coarse pass runs. */
+  const void *append_k;
+  const void *append_v;
+  int64_t append_k_stride[3];
+  int64_t append_v_stride[3];
+  int64_t append_tokens;
 } kiv_retrieve_args_t;
 
 /* Arguments of the merged decode attention over [retrieved ; hot]. */

@@ -53,7 +53,8 @@ class RetrieveArgs(C.Structure):
         ("top_pages", C.c_int32), ("out_width", C.c_int32), ("reuse_candidates", C.c_int32),
         ("flags", C.c_int32), ("k_out", C.c_void_p), ("v_out", C.c_void_p), ("idx_out", C.c_void_p),
         ("pages_out", C.c_void_p), ("union_count_out", C.c_void_p), ("stats_out", C.c_void_p),
-        ("stats_accum", C.c_void_p),
+        ("stats_accum", C.c_void_p), ("append_k", C.c_void_p), ("append_v", C.c_void_p),
+        ("append_k_stride", _I64x3), ("append_v_stride", _I64x3), ("append_tokens", C.c_int64),
     ]
 
 

@@ -70,12 +70,15 @@ class ColdKVStore:
         self._aargs_ref = C.byref(self._aargs)
         self._dev_index = -1
         self._last_coarse_slot = None  # telemetry slot of the last coarse pass (its union size)
+        # Rows evicted with evict_deferred and not yet written: (k, v, T).
+        self._pending: tuple[torch.Tensor, torch.Tensor, int] | None = None
 
     # ------------------------------------------------------------ lifetime
     def __del__(self) -> None:
         self._destroy()
 
     def _destroy(self) -> None:
+        self._pending = None
         h, self._handle = getattr(self, "_handle", None), None
         if h is not None:
             try:
@@ -131,6 +134,51 @@ class ColdKVStore:
 
         Same contract as kiv/cold_store.py:142-184.
         """
+        self._flush_pending()
+        k, v, T = self._check_rows(k_evicted, v_evicted)
+        if T == 0:
+            return
+        nat.check(nat.lib().kiv_evict(self._handle, k.data_ptr(), nat.strides(k, 3), v.data_ptr(),
+                                      nat.strides(v, 3), T, nat.stream_ptr(self.device)), "kiv_evict")
+        self._count(T)
+
+    def evict_deferred(self, k_evicted: torch.Tensor, v_evicted: torch.Tensor) -> None:
+        """evict_from_hot, with the rows written by the next retrieval's first
+        kernel instead of a launch of their own (when they stay in the
+        partial page); any other use of the store writes them first.
+
+        For the cache's decode steps: the rows must stay unchanged until then
+        (the store keeps a reference to them, which keeps their memory alive;
+        the hot window only ever writes rows after its end)."""
+        self._flush_pending()
+        k, v, T = self._check_rows(k_evicted, v_evicted)
+        if T == 0:
+            return
+        if self._partial_len + T >= self._page_size or self._num_finalized == 0:
+            nat.check(nat.lib().kiv_evict(self._handle, k.data_ptr(), nat.strides(k, 3), v.data_ptr(),
+                                          nat.strides(v, 3), T, nat.stream_ptr(self.device)), "kiv_evict")
+        else:
+            self._pending = (k, v, T)
+        self._count(T)
+
+    def _flush_pending(self) -> None:
+        """Write deferred rows now (a launch of their own)."""
+        p = self._pending
+        if p is None:
+            return
+        self._pending = None
+        k, v, T = p
+        nat.check(nat.lib().kiv_evict(self._handle, k.data_ptr(), nat.strides(k, 3), v.data_ptr(),
+                                      nat.strides(v, 3), T, nat.stream_ptr(self.device)), "kiv_evict")
+
+    def _count(self, T: int) -> None:
+        total = self._partial_len + T
+        self._num_finalized += (total // self._page_size) * self._page_size
+        self._partial_len = total % self._page_size
+
+    def _check_rows(self, k_evicted: torch.Tensor, v_evicted: torch.Tensor):
+        """Validated (k, v, T) of evicted rows (unit stride over D); invalidates
+        the shared-layer candidates (kiv/cold_store.py:148-151)."""
         self._invalidate_candidates()
         shape = k_evicted.shape
         if len(shape) != 4 or shape != v_evicted.shape:
@@ -138,7 +186,7 @@ class ColdKVStore:
                              f"and {tuple(v_evicted.shape)}")
         T = shape[2]
         if T == 0:
-            return
+            return k_evicted, v_evicted, 0
         if self._handle is None:
             self._ensure_handle(k_evicted)
         if shape[0] != self._batch or shape[1] != self._num_kv_heads or shape[3] != self._head_dim:
@@ -150,11 +198,7 @@ class ColdKVStore:
             raise ValueError(f"evicted rows on {k_evicted.device}, store on {self.device}")
         k = k_evicted if k_evicted.stride(3) == 1 else k_evicted.contiguous()
         v = v_evicted if v_evicted.stride(3) == 1 else v_evicted.contiguous()
-        nat.check(nat.lib().kiv_evict(self._handle, k.data_ptr(), nat.strides(k, 3), v.data_ptr(),
-                                      nat.strides(v, 3), T, nat.stream_ptr(self.device)), "kiv_evict")
-        total = self._partial_len + T
-        self._num_finalized += (total // self._page_size) * self._page_size
-        self._partial_len = total % self._page_size
+        return k, v, T
 
     def _invalidate_candidates(self) -> None:
         self._cached_candidate_k = None
@@ -259,6 +303,17 @@ class ColdKVStore:
         a.union_count_out = slot.count_ptr
         a.stats_out = slot.stats_ptr
         a.stats_accum = tel.accum_ptr
+        pend = self._pending
+        if pend is not None:
+            # The deferred rows go in with this call (their own launch only
+            # when they finish a page or no coarse pass runs).
+            self._pending = None
+            pk, pv, pt = pend
+            a.append_k, a.append_v = pk.data_ptr(), pv.data_ptr()
+            a.append_k_stride, a.append_v_stride = nat.strides(pk, 3), nat.strides(pv, 3)
+            a.append_tokens = pt
+        else:
+            a.append_tokens = 0
         stream = nat.stream_ptr(dev)
         out = None
         if fused:
@@ -297,6 +352,7 @@ class ColdKVStore:
     # ------------------------------------------------------ bookkeeping
     def reset(self) -> None:
         """Drop every cold token (kiv/cold_store.py:374-389); allocations are kept."""
+        self._pending = None  # deferred rows are cold tokens too: dropped
         if self._handle is not None:
             nat.check(nat.lib().kiv_store_reset(self._handle), "kiv_store_reset")
         self._num_finalized = 0
@@ -323,6 +379,7 @@ class ColdKVStore:
                "k_cold_gpu": 0, "v_cold_gpu": 0, "reserved_gpu": 0, "reserved_cpu": 0}
         if self._handle is None:
             return out
+        self._flush_pending()
         info = nat.StoreInfo()
         nat.check(nat.lib().kiv_store_info(self._handle, C.byref(info)), "kiv_store_info")
         tier = self.kiv_config.cold_tier
@@ -338,6 +395,7 @@ class ColdKVStore:
     def fine_scan_stats(self) -> tuple[int, int]:
         """(page slices the last retrieval's fine scan read, union page slices);
         a slice is one kv row of one union page.  Synchronises the device."""
+        self._flush_pending()
         scanned, total = C.c_int64(), C.c_int64()
         nat.check(nat.lib().kiv_fine_scan_stats(self._handle, C.byref(scanned), C.byref(total)),
                   "kiv_fine_scan_stats")
@@ -345,6 +403,7 @@ class ColdKVStore:
 
     def read_summaries(self) -> tuple[torch.Tensor, torch.Tensor]:
         """(dtype summaries, fp32 means), each [N, B, Hkv, D], copied from HBM."""
+        self._flush_pending()
         N = self.num_pages
         shape = (N, self._batch or 1, self._num_kv_heads, self._head_dim)
         s = torch.empty(shape, dtype=self._dtype or torch.float32, device=self.device)
@@ -356,6 +415,7 @@ class ColdKVStore:
 
     def read_tokens(self, first: int = 0, n: int | None = None) -> tuple[torch.Tensor, torch.Tensor]:
         """Cold tokens [first, first+n) as [B, Hkv, n, D] K and V on the device."""
+        self._flush_pending()
         n = self.cold_length - first if n is None else n
         k = torch.empty(self._batch or 1, self._num_kv_heads, n, self._head_dim,
                         dtype=self._dtype or torch.float32, device=self.device)

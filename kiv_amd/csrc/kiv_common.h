@@ -302,6 +302,33 @@ template <int DT> __device__ __forceinline__ float chunk_dot(const uint4 &x, con
 
 __device__ __forceinline__ uint4 load16(const void *p) { return *reinterpret_cast<const uint4 *>(p); }
 
+// Evicted rows that one extra block per kv row of another launch copies
+// into the partial page (count 0: none): token t of row r = b*hkv + h goes
+// from the strided input (element strides, in16 = 16 / element bytes
+// elements per chunk) to partial slot t_dst0 + t.  Used only by launches
+// that do not read the partial page themselves.
+struct AppendRows {
+  const char *k, *v;
+  int64_t ks0, ks1, ks2, vs0, vs1, vs2;
+  char *part_k, *part_v;
+  int64_t t_dst0;
+  int count, hkv, page_size, cpr, in16;
+};
+
+__device__ __forceinline__ void append_rows(const AppendRows &ap, int r) {
+  const int b = r / ap.hkv, h = r % ap.hkv;
+  const int eb = 16 / ap.in16;
+  for (int i = threadIdx.x; i < ap.count * ap.cpr; i += blockDim.x) {
+    const int t = i / ap.cpr, c = i % ap.cpr;
+    const int64_t e0 = (int64_t)c * ap.in16;
+    const int64_t src_k = ((int64_t)b * ap.ks0 + (int64_t)h * ap.ks1 + (int64_t)t * ap.ks2 + e0) * eb;
+    const int64_t src_v = ((int64_t)b * ap.vs0 + (int64_t)h * ap.vs1 + (int64_t)t * ap.vs2 + e0) * eb;
+    const int64_t dst = (((int64_t)r * ap.page_size + ap.t_dst0 + t) * ap.cpr + c) * 16;
+    *reinterpret_cast<uint4 *>(ap.part_k + dst) = load16(ap.k + src_k);
+    *reinterpret_cast<uint4 *>(ap.part_v + dst) = load16(ap.v + src_v);
+  }
+}
+
 // Inclusive prefix sum over the NT threads of a block.  `tmp` is LDS with
 // room for NT / 64 ints.  Contains two barriers; every thread must call it.
 template <int NT> __device__ __forceinline__ int block_incl_scan(int v, int *tmp, int *total) {

@@ -595,7 +595,11 @@ template <int DT, int CPR, bool Q1>
 __global__ void __launch_bounds__(kScanThreads) coarse_scan_kernel(
     const char *__restrict__ summ, int64_t n_pages, int kr, const char *__restrict__ q, int64_t qs0,
     int64_t qs1, int64_t qs2, int hq, int hkv, int qlen, float scale, int round, uint32_t *__restrict__ keys,
-    int64_t ld) {
+    int64_t ld, AppendRows ap) {
+  if (ap.count > 0 && blockIdx.x == gridDim.x - 1) {
+    append_rows(ap, blockIdx.y);  // the step's evicted rows (an extra block per kv row)
+    return;
+  }
   constexpr int EB = Elem<DT>::BYTES, VEC = Elem<DT>::VEC;
   constexpr int DS = scan_segments(CPR);  // segments (waves) per page
   constexpr int CS = CPR / DS;            // chunks per segment
@@ -702,8 +706,13 @@ template <int DT, int KT>  // KT = head_dim / 32
 __global__ void __launch_bounds__(kScanThreads) coarse_scan_mfma_kernel(
     const char *__restrict__ summ, int64_t n_pages, int kr, const char *__restrict__ q, int64_t qs0,
     int64_t qs1, int64_t qs2, int hq, int hkv, int qlen, float scale, int round, uint32_t *__restrict__ keys,
-    int64_t ld, const float *__restrict__ rad2, uint32_t *__restrict__ ubk, uint32_t *__restrict__ lbk) {
+    int64_t ld, const float *__restrict__ rad2, uint32_t *__restrict__ ubk, uint32_t *__restrict__ lbk,
+    AppendRows ap) {
   static_assert(DT != DT_F32, "16-bit dtypes only");
+  if (ap.count > 0 && blockIdx.x == gridDim.x - 1) {
+    append_rows(ap, blockIdx.y);  // the step's evicted rows (an extra block per kv row)
+    return;
+  }
   constexpr int64_t kRowBytes = (int64_t)KT * 64;  // 32 two-byte elements per K step
   const int r = blockIdx.y, b = r / hkv, kvh = r % hkv;
   const int G = hq / hkv, GQ = G * qlen;
@@ -1719,8 +1728,6 @@ static int retrieve_impl(kiv_store_t *s, const kiv_retrieve_args_t *a, hipStream
   const int Q = a->q_len;
   if (Q < 1) return fail(KIV_ERR_INVALID, "kiv_retrieve: q_len must be >= 1");
   if (a->top_pages < 1) return fail(KIV_ERR_INVALID, "kiv_retrieve: top_pages must be >= 1");
-  const int64_t cold = s->num_pages * ps + s->partial_len;
-  if (cold == 0) return fail(KIV_ERR_STATE, "kiv_retrieve: the cold store is empty");
   if (a->out_width < 1 || a->out_width > kMaxOut)
     return fail(KIV_ERR_UNSUPPORTED, "kiv_retrieve: out_width %d outside [1, %d]", a->out_width, kMaxOut);
   if (!a->q || !a->k_out || !a->v_out) return fail(KIV_ERR_INVALID, "kiv_retrieve: null q or outputs");
@@ -1729,7 +1736,46 @@ static int retrieve_impl(kiv_store_t *s, const kiv_retrieve_args_t *a, hipStream
   if (a->q_stride[3] != 1) return fail(KIV_ERR_INVALID, "kiv_retrieve: q head_dim stride must be 1");
   if (((uintptr_t)a->q & 15) || (a->q_stride[0] % vec) || (a->q_stride[1] % vec) || (a->q_stride[2] % vec))
     return fail(KIV_ERR_INVALID, "kiv_retrieve: q must be 16-byte aligned with strides multiple of %d", vec);
+  // Rows to evict first (kiv_evict's contract).  Rows that stay in the
+  // partial page, with a fresh coarse pass to come, are copied by extra
+  // blocks of the coarse scan launch (the coarse scan never reads the
+  // partial page; the fine scan, a launch later, does); anything else
+  // (finishing a page, no finished pages, a reused union) is kiv_evict.
+  AppendRows ap{};
+  if (a->append_tokens > 0) {
+    const int64_t T = a->append_tokens;
+    if (!a->append_k || !a->append_v || (((uintptr_t)a->append_k | (uintptr_t)a->append_v) & 15))
+      return fail(KIV_ERR_INVALID, "kiv_retrieve: appended K/V must be non-null and 16-byte aligned");
+    for (int i = 0; i < 3; ++i)
+      if ((a->append_k_stride[i] % vec) || (a->append_v_stride[i] % vec))
+        return fail(KIV_ERR_INVALID, "kiv_retrieve: appended strides must be multiples of %d elements", vec);
+    if (s->num_pages > 0 && !a->reuse_candidates && s->partial_len + T < ps) {
+      ap.k = (const char *)a->append_k;
+      ap.v = (const char *)a->append_v;
+      ap.ks0 = a->append_k_stride[0];
+      ap.ks1 = a->append_k_stride[1];
+      ap.ks2 = a->append_k_stride[2];
+      ap.vs0 = a->append_v_stride[0];
+      ap.vs1 = a->append_v_stride[1];
+      ap.vs2 = a->append_v_stride[2];
+      ap.part_k = (char *)s->k_part.ptr;
+      ap.part_v = (char *)s->v_part.ptr;
+      ap.t_dst0 = s->partial_len;
+      ap.count = (int)T;
+      ap.hkv = hkv;
+      ap.page_size = ps;
+      ap.cpr = cpr;
+      ap.in16 = vec;
+      s->union_valid = false;  // the partial-page length grows once the launch is enqueued
+    } else {
+      const int rc = kiv_evict(s, a->append_k, a->append_k_stride, a->append_v, a->append_v_stride, T,
+                               (kiv_stream_t)st);
+      if (rc) return rc;
+    }
+  }
   const int rows = B * hq * Q;
+  if (s->num_pages * ps + s->partial_len + ap.count == 0)
+    return fail(KIV_ERR_STATE, "kiv_retrieve: the cold store is empty");
   if (s->num_pages > (int64_t)kMaxWords * 32)
     return fail(KIV_ERR_UNSUPPORTED, "kiv_retrieve: more than %d pages", kMaxWords * 32);
   DeviceGuard guard(s->device);
@@ -1820,6 +1866,10 @@ static int retrieve_impl(kiv_store_t *s, const kiv_retrieve_args_t *a, hipStream
         const int Qp = std::min(Qb, Q - pass * Qb);
         const int rows_p = B * hq * Qp;
         const char *qp = (const char *)a->q + pass * qstep;
+        // The step's evicted rows ride on the first pass's launch.
+        AppendRows apass{};
+        if (pass == 0) apass = ap;
+        const int extra = apass.count > 0 ? 1 : 0;
         s->prof_begin(KIV_STAGE_COARSE_SCAN, st);
         if (mfma) {
           const int pages_per_block = (kScanThreads / 64) * kScanMfmaPages;
@@ -1830,11 +1880,11 @@ static int retrieve_impl(kiv_store_t *s, const kiv_retrieve_args_t *a, hipStream
               return (int)KIV_ERR_UNSUPPORTED;
             } else {
               return with_kt(kt, [&](auto ktc) {
-                hipLaunchKernelGGL((coarse_scan_mfma_kernel<DTV, decltype(ktc)::value>), dim3(blocks, s->kr),
-                                   dim3(kScanThreads), 0, st, (const char *)s->summ.ptr, (int64_t)N, s->kr, qp,
-                                   a->q_stride[0], a->q_stride[1], a->q_stride[2], hq, hkv, Qp, a->scaling, round,
-                                   (uint32_t *)s->coarse_keys.ptr, ld, (const float *)s->radius.ptr,
-                                   (uint32_t *)pr.ub, (uint32_t *)pr.lb);
+                hipLaunchKernelGGL((coarse_scan_mfma_kernel<DTV, decltype(ktc)::value>),
+                                   dim3(blocks + extra, s->kr), dim3(kScanThreads), 0, st, (const char *)s->summ.ptr,
+                                   (int64_t)N, s->kr, qp, a->q_stride[0], a->q_stride[1], a->q_stride[2], hq, hkv,
+                                   Qp, a->scaling, round, (uint32_t *)s->coarse_keys.ptr, ld,
+                                   (const float *)s->radius.ptr, (uint32_t *)pr.ub, (uint32_t *)pr.lb, apass);
                 return (int)KIV_OK;
               });
             }
@@ -1848,9 +1898,10 @@ static int retrieve_impl(kiv_store_t *s, const kiv_retrieve_args_t *a, hipStream
             return with_cpr(cpr, [&](auto cc) {
               constexpr int DTV = decltype(dtc)::value, CPRV = decltype(cc)::value;
               auto kern = Qp == 1 ? coarse_scan_kernel<DTV, CPRV, true> : coarse_scan_kernel<DTV, CPRV, false>;
-              hipLaunchKernelGGL(kern, dim3(blocks, s->kr), dim3(kScanThreads), 0, st, (const char *)s->summ.ptr,
-                                 (int64_t)N, s->kr, qp, a->q_stride[0], a->q_stride[1], a->q_stride[2], hq, hkv, Qp,
-                                 a->scaling, round, (uint32_t *)s->coarse_keys.ptr, ld);
+              hipLaunchKernelGGL(kern, dim3(blocks + extra, s->kr), dim3(kScanThreads), 0, st,
+                                 (const char *)s->summ.ptr, (int64_t)N, s->kr, qp, a->q_stride[0], a->q_stride[1],
+                                 a->q_stride[2], hq, hkv, Qp, a->scaling, round, (uint32_t *)s->coarse_keys.ptr, ld,
+                                 apass);
               return (int)KIV_OK;
             });
           });
@@ -1858,6 +1909,7 @@ static int retrieve_impl(kiv_store_t *s, const kiv_retrieve_args_t *a, hipStream
         s->prof_end(KIV_STAGE_COARSE_SCAN, st);
         if (rc) return rc;
         KIV_HIP(hipGetLastError());
+        if (extra) s->partial_len += apass.count;  // the appended rows are in the partial page from here on
         s->prof_begin(KIV_STAGE_COARSE_SELECT, st);
         with_select_chunks(N, [&](auto kern) {
           hipLaunchKernelGGL(kern, dim3(rows_p), dim3(kSelThreads), 0, st, (const uint32_t *)s->coarse_keys.ptr,

@@ -125,11 +125,15 @@ class TieredKVCache(DynamicCache):
             if i < len(self.layers) and self.layers[i].is_initialized:
                 yield i, self.layers[i]
 
-    def _evict_layer(self, layer_idx: int, num_evict: int) -> None:
+    def _evict_layer(self, layer_idx: int, num_evict: int, deferred: bool = False) -> None:
         """Move the oldest ``num_evict`` hot rows of a layer to its cold store
-        (kiv/tiered_cache.py:55-72)."""
+        (kiv/tiered_cache.py:55-72).  ``deferred``: the decode step's rows,
+        written by the layer's retrieval that follows (their hot-window rows
+        are never written again)."""
         layer = self.layers[layer_idx]
-        self.cold_stores[layer_idx].evict_from_hot(layer.keys[:, :, :num_evict], layer.values[:, :, :num_evict])
+        store = self.cold_stores[layer_idx]
+        evict = store.evict_deferred if deferred else store.evict_from_hot
+        evict(layer.keys[:, :, :num_evict], layer.values[:, :, :num_evict])
         if isinstance(layer, _HotLayer):
             layer.drop_front(num_evict)
         else:
@@ -175,7 +179,7 @@ class TieredKVCache(DynamicCache):
             layer = self.layers[layer_idx]
             excess = layer.keys.shape[2] - self.kiv_config.hot_budget
             if excess > 0:
-                self._evict_layer(layer_idx, excess)
+                self._evict_layer(layer_idx, excess, deferred=True)
                 keys, values = layer.keys, layer.values
         return keys, values
 
