@@ -85,19 +85,26 @@ def parse():
 
 
 SCRUB_BYTES = 512 << 20  # larger than L2 (8 x 4 MiB) plus the 256 MiB memory-side cache
+# GPU clock cycles of a spin kernel after each scrub (about half a
+# millisecond): the launching thread enqueues the whole step meanwhile, so
+# the events around a step time the GPU's work and never wait for a launch.
+HEAD_START_CYCLES = 1_000_000
 MFMA_BF16_PEAK_TFLOPS = 2500.0  # dense
 MODEL_WORKLOAD = "qwen15b_model_1m"
 CHUNK_WORKLOAD = "qwen15b_prefill_chunk"
 
 
 def make_scrub(dev):
-    """A read of SCRUB_BYTES that leaves no workload data in L2 or the MALL."""
+    """A read of SCRUB_BYTES that leaves no workload data in L2 or the MALL,
+    then a bounded spin (torch.cuda._sleep, no memory traffic) that gives the
+    host its head start on the next step."""
     import torch
 
     buf = torch.ones(SCRUB_BYTES // 4, dtype=torch.int32, device=dev)
 
     def scrub():
         buf.sum()
+        torch.cuda._sleep(HEAD_START_CYCLES)
 
     return scrub
 

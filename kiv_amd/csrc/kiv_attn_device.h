@@ -250,8 +250,17 @@ __device__ __forceinline__ void lse_fold(const float (&ms)[N], const float (&ls)
 // into the caller's (m, l, o), the same way.
 __device__ __forceinline__ void lse_fold_lds(const float *sm, const float *sl, const float4 *so, int groups,
                                              int stride, int i, float &m, float &l, float4 &o) {
+  // Groups in batches of GB whose LDS reads are issued together (indexes
+  // clamped to the last group; the repeats are masked out of the sums).
+  constexpr int GB = 8;
   float M = m;
-  for (int gg = 1; gg < groups; ++gg) M = fmaxf(M, sm[gg * stride + i]);
+  for (int g0 = 1; g0 < groups; g0 += GB) {
+    float v[GB];
+#pragma unroll
+    for (int u = 0; u < GB; ++u) v[u] = sm[min(g0 + u, groups - 1) * stride + i];
+#pragma unroll
+    for (int u = 0; u < GB; ++u) M = fmaxf(M, v[u]);
+  }
   if (M == -INFINITY) return;
   const float c0 = m == -INFINITY ? 0.f : __expf(m - M);
   l *= c0;
@@ -259,15 +268,25 @@ __device__ __forceinline__ void lse_fold_lds(const float *sm, const float *sl, c
   o.y *= c0;
   o.z *= c0;
   o.w *= c0;
-  for (int gg = 1; gg < groups; ++gg) {
-    const float mg = sm[gg * stride + i];
-    const float c = mg == -INFINITY ? 0.f : __expf(mg - M);
-    const float4 og = so[gg * stride + i];
-    l = fmaf(sl[gg * stride + i], c, l);
-    o.x = fmaf(og.x, c, o.x);
-    o.y = fmaf(og.y, c, o.y);
-    o.z = fmaf(og.z, c, o.z);
-    o.w = fmaf(og.w, c, o.w);
+  for (int g0 = 1; g0 < groups; g0 += GB) {
+    float mv[GB], lv[GB];
+    float4 ov[GB];
+#pragma unroll
+    for (int u = 0; u < GB; ++u) {
+      const int at = min(g0 + u, groups - 1) * stride + i;
+      mv[u] = sm[at];
+      lv[u] = sl[at];
+      ov[u] = so[at];
+    }
+#pragma unroll
+    for (int u = 0; u < GB; ++u) {
+      const float c = g0 + u < groups && mv[u] != -INFINITY ? __expf(mv[u] - M) : 0.f;
+      l = fmaf(lv[u], c, l);
+      o.x = fmaf(ov[u].x, c, o.x);
+      o.y = fmaf(ov[u].y, c, o.y);
+      o.z = fmaf(ov[u].z, c, o.z);
+      o.w = fmaf(ov[u].w, c, o.w);
+    }
   }
   m = M;
 }

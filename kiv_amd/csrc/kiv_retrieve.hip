@@ -173,6 +173,30 @@ template <int V> __device__ uint32_t wave_kth_u32(const uint32_t (&v)[V], int k)
   return ans;
 }
 
+// The same k-th largest for small k: k rounds at most, each taking the
+// wave's largest remaining value and removing its copies (a DPP max, a
+// ballot per sub-slot), which is fewer dependent steps than the bit search
+// needs when k is a handful.
+template <int V> __device__ uint32_t wave_kth_extract(const uint32_t (&v)[V], int k) {
+  uint32_t cur[V];
+#pragma unroll
+  for (int i = 0; i < V; ++i) cur[i] = v[i];
+  for (;;) {
+    uint32_t mx = cur[0];
+#pragma unroll
+    for (int i = 1; i < V; ++i) mx = max(mx, cur[i]);
+    mx = uniform_u32(wave_max_u32(mx));
+    int c = 0;
+#pragma unroll
+    for (int i = 0; i < V; ++i) c += __popcll(__ballot(cur[i] == mx));
+    if (c >= k || mx == 0u) return mx;
+    k -= c;
+#pragma unroll
+    for (int i = 0; i < V; ++i) cur[i] = cur[i] == mx ? 0u : cur[i];
+  }
+}
+constexpr int kKthExtractMax = 8;  // largest k the extraction serves
+
 // Block-wide count of composites >= c: wave sums, one LDS atomic per wave,
 // one barrier.  Three counters rotate so a counter is cleared two counts
 // before it is reused.
@@ -256,6 +280,7 @@ __device__ void block_compact(const Src &src, P &&pred, E &&emit, int cap, int *
 // holds its keys 4c + j.
 template <int NT, int V> struct RegKeys4 {
   static constexpr int W = NT / 64;
+  static constexpr bool kManySteps = V > 4;  // placement in two passes (see bound_candidates)
   uint4 v[V];
   int n;
   __device__ static int chunk(int i) { return (threadIdx.x >> 6) + W * ((threadIdx.x & 63) + 64 * i); }
@@ -289,6 +314,7 @@ template <int NT, int V> struct RegKeys4 {
 // A row's keys re-read from memory for each pass (rows too long for
 // registers), strided over the block; sub-slot = load batch position & 3.
 template <int NT> struct MemKeys4 {
+  static constexpr bool kManySteps = false;
   const uint32_t *p;
   int n;
   template <typename F> __device__ void each_slot(F &&f) const {
@@ -316,12 +342,12 @@ template <int NT> struct MemKeys4 {
 // sub-slots; the maxima are distinct keys, so every wave holds kw keys >=
 // its bound and the smallest bound B leaves at least k keys >= B.  A wave
 // with fewer than kw nonzero maxima sets no bound (B = 0).  The wave search
-// runs on registers with ballots and one barrier publishes the bounds.
-// Candidates are placed with ballots: a first pass sums the per-step ballot
-// counts, one LDS atomic per wave reserves the wave's range, a second pass
-// places each candidate at its step's offset plus its rank in the ballot.
-// (A lane whose entries run out never gets more, so lane 0 sees every
-// step.)  Also leaves the row's max and sum of scores (as floats) in mx /
+// runs on registers with ballots (extraction for small kw, the bit search
+// otherwise) and one barrier publishes the bounds.  Candidates are placed
+// in one pass (block_compact: a step's ballot reserves its range with one
+// LDS atomic, skipped when no lane passes), or in two passes for sources of
+// many register steps per thread, where most steps would take an atomic.
+// Also leaves the row's max and sum of scores (as floats) in mx /
 // sum and the number of scored entries in nz: a zero key is an entry that
 // was not scored (a pruned fine scan leaves them) and is not summed.
 template <int NT, typename Src>
@@ -344,7 +370,7 @@ __device__ int bound_candidates(const Src &src, int k, SelSh<NT> &sh, uint64_t *
   int have = 0;
 #pragma unroll
   for (int j = 0; j < 4; ++j) have += __popcll(__ballot(m[j] != 0u));
-  const uint32_t bw = have >= kw ? wave_kth_u32<4>(m, kw) : 0u;
+  const uint32_t bw = have < kw ? 0u : kw <= kKthExtractMax ? wave_kth_extract<4>(m, kw) : wave_kth_u32<4>(m, kw);
   const uint32_t top = max(max(m[0], m[1]), max(m[2], m[3]));
   float fm = have ? key_to_float(wave_max_u32(top)) : -INFINITY;
   fs = wave_sum(fs);
@@ -367,22 +393,32 @@ __device__ int bound_candidates(const Src &src, int k, SelSh<NT> &sh, uint64_t *
     nz += sh.fcnt[w];
     bound = min(bound, sh.wave_bound[w]);
   }
-  int total = 0;
-  src.each([&](uint64_t x) { total += __popcll(__ballot(comp_key(x) >= bound)); });
-  total = (int)uniform_u32((uint32_t)total);  // lane 0's count
-  if (total) {
-    int off = 0;
-    if ((tid & 63) == 0) off = atomicAdd(&sh.ncand, total);
-    off = (int)uniform_u32((uint32_t)off);
-    src.each([&](uint64_t x) {
-      const bool f = comp_key(x) >= bound;
-      const uint64_t mask = __ballot(f);
-      if (f) {
-        const int pos = off + lane_rank(mask);
-        if (pos < kCandCap) cand[pos] = x;
-      }
-      off += __popcll(mask);
-    });
+  if constexpr (Src::kManySteps) {
+    // Many register steps per thread: a first pass sums the steps' ballot
+    // counts, one LDS atomic per wave reserves the wave's range, a second
+    // pass places each candidate at its step's offset plus its rank in the
+    // ballot.  (A lane whose entries run out never gets more, so lane 0
+    // sees every step.)
+    int total = 0;
+    src.each([&](uint64_t x) { total += __popcll(__ballot(comp_key(x) >= bound)); });
+    total = (int)uniform_u32((uint32_t)total);  // lane 0's count
+    if (total) {
+      int off = 0;
+      if ((tid & 63) == 0) off = atomicAdd(&sh.ncand, total);
+      off = (int)uniform_u32((uint32_t)off);
+      src.each([&](uint64_t x) {
+        const bool f = comp_key(x) >= bound;
+        const uint64_t mask = __ballot(f);
+        if (f) {
+          const int pos = off + lane_rank(mask);
+          if (pos < kCandCap) cand[pos] = x;
+        }
+        off += __popcll(mask);
+      });
+    }
+  } else {
+    block_compact<NT>(src, [bound](uint64_t x) { return comp_key(x) >= bound; },
+                      [cand](int pos, uint64_t x) { cand[pos] = x; }, kCandCap, &sh.ncand);
   }
   __syncthreads();
   return sh.ncand;
@@ -427,10 +463,11 @@ __device__ void emit_topk_unranked(const Src &mem, const uint64_t *cand, int C, 
 
 // -------------------------------------------------------- union ranking
 // Builds the union of the rows' top pages (row_pages, nk entries) as a page
-// bitmap bits[words] in LDS and writes rank[w] = set bits in words before w
-// (rank[words] = union size).  Returns the union size.
+// bitmap bits[words] in LDS and lists it: upage[v] = the v-th union page
+// ascending (upage holds min(nk, pages) entries; a word's pages start at
+// the set bits of the words before it).  Returns the union size.
 template <int NT>
-__device__ int rank_union(const int32_t *row_pages, int nk, int words, uint32_t *bits, int *rank, int *scan_tmp) {
+__device__ int rank_union(const int32_t *row_pages, int nk, int words, uint32_t *bits, int *upage, int *scan_tmp) {
   constexpr int PF = 4;  // list entries per thread loaded before the bitmap is cleared
   int first[PF];
 #pragma unroll
@@ -454,10 +491,12 @@ __device__ int rank_union(const int32_t *row_pages, int nk, int words, uint32_t 
     const int c = w < words ? __popc(bits[w]) : 0;
     int tot = 0;
     const int incl = block_incl_scan<NT>(c, scan_tmp, &tot);
-    if (w < words) rank[w] = before + incl - c;
+    if (w < words) {
+      uint32_t x = bits[w];
+      for (int at = before + incl - c; x; ++at, x &= x - 1) upage[at] = w * 32 + __ffs(x) - 1;
+    }
     before += tot;
   }
-  if (threadIdx.x == 0) rank[words] = before;
   __syncthreads();
   return before;
 }
@@ -534,19 +573,6 @@ __global__ void __launch_bounds__(kUnionThreads) union_list_kernel(
     stats_accum[0] += (double)m;
     stats_accum[1] += (double)mean;
   }
-}
-
-// Page id of the v-th union member (v < union size).
-__device__ __forceinline__ int union_page(const uint32_t *bits, const int *rank, int words, int v) {
-  int lo = 0, hi = words - 1;
-  while (lo < hi) {
-    const int mid = (lo + hi + 1) >> 1;
-    if (rank[mid] <= v) lo = mid;
-    else hi = mid - 1;
-  }
-  uint32_t x = bits[lo];
-  for (int r = v - rank[lo]; r > 0; --r) x &= x - 1;
-  return lo * 32 + __ffs(x) - 1;
 }
 
 // ------------------------------------------------------------ coarse scan
@@ -877,12 +903,11 @@ constexpr int kFineUT = 4;  // tokens in flight per lane group
 // Block (0, 0) of a fresh union: page_list / pages_out <- the union pages
 // ascending, counters[0] / union_out <- U, and the coarse telemetry.
 template <int DT>
-__device__ void publish_union(const uint32_t *ubits, const int *urank, int words, int U, int32_t *page_list,
-                              int32_t *pages_out, int32_t *counters, int32_t *union_out,
-                              const float *coarse_stats, int rows, int n_pages, int round, float *stats_out,
-                              double *stats_accum) {
+__device__ void publish_union(const int *upage, int U, int32_t *page_list, int32_t *pages_out, int32_t *counters,
+                              int32_t *union_out, const float *coarse_stats, int rows, int n_pages, int round,
+                              float *stats_out, double *stats_accum) {
   for (int v = threadIdx.x; v < U; v += blockDim.x) {
-    const int page = union_page(ubits, urank, words, v);
+    const int page = upage[v];
     page_list[v] = page;
     if (pages_out) pages_out[v] = page;
   }
@@ -952,6 +977,7 @@ constexpr int kPruneRetry = 32;
 // partial page, as composites with their candidate index (union rank *
 // page_size + token; the partial page's after the U union pages).
 template <int NT> struct PageKeys {
+  static constexpr bool kManySteps = false;
   const uint32_t *row;
   const int *plist;
   int mp, mall, page_size;
@@ -973,6 +999,38 @@ template <int NT> struct PageKeys {
     each_slot([&](uint64_t x, int) { f(x); });
   }
 };
+
+// PageKeys read once into registers (the thread's entries e = w + W l +
+// NT u, u < V, as composites; sub-slot u & 3), for the select's passes
+// over a short page list.  Lane 0 of a wave has the most entries, so it
+// takes part in every step.
+template <int NT, int V> struct RegPageKeys {
+  static constexpr bool kManySteps = false;
+  uint64_t x[V];
+  int cnt;
+  __device__ void load(const PageKeys<NT> &pk) {
+    constexpr int W = NT / 64;
+    const int e0 = (threadIdx.x >> 6) + W * (threadIdx.x & 63);
+    cnt = e0 < pk.mall ? (pk.mall - 1 - e0) / NT + 1 : 0;
+#pragma unroll
+    for (int u = 0; u < V; ++u) {
+      x[u] = 0;
+      if (u < cnt) {
+        const int64_t i = pk.index(e0 + u * NT);
+        x[u] = comp_of(pk.row[i], (int)i);
+      }
+    }
+  }
+  template <typename F> __device__ void each_slot(F &&f) const {
+#pragma unroll
+    for (int u = 0; u < V; ++u)
+      if (u < cnt) f(x[u], u & 3);
+  }
+  template <typename F> __device__ void each(F &&f) const {
+    each_slot([&](uint64_t x, int) { f(x); });
+  }
+};
+constexpr int kRegPageKeys = 8;  // entries per thread a fine select keeps in registers
 
 // Block-wide list of the union pages v < U with pred(v) into plist (at
 // most kPageListCap); returns their number (possibly larger).
@@ -1005,7 +1063,7 @@ template <int NT, typename Src> __device__ uint32_t block_kth_bound(const Src &s
   int have = 0;
 #pragma unroll
   for (int j = 0; j < 4; ++j) have += __popcll(__ballot(m[j] != 0u));
-  const uint32_t bw = have >= kw ? wave_kth_u32<4>(m, kw) : 0u;
+  const uint32_t bw = have < kw ? 0u : kw <= kKthExtractMax ? wave_kth_extract<4>(m, kw) : wave_kth_u32<4>(m, kw);
   if ((threadIdx.x & 63) == 0) sh.wave_bound[wave] = bw;
   __syncthreads();
   uint32_t bound = sh.wave_bound[0];
@@ -1066,6 +1124,19 @@ template <int NT, typename PageOf> struct UnionLowerKeys {
   }
   template <typename F> __device__ void each(F &&f) const {
     each_slot([&](uint64_t x, int) { f(x); });
+  }
+};
+
+// One composite per thread (valid or not), as a select source.
+struct OneKey {
+  static constexpr bool kManySteps = false;
+  uint64_t x;
+  bool valid;
+  template <typename F> __device__ void each_slot(F &&f) const {
+    if (valid) f(x, 0);
+  }
+  template <typename F> __device__ void each(F &&f) const {
+    if (valid) f(x);
   }
 };
 
@@ -1157,8 +1228,8 @@ __global__ void __launch_bounds__(256) fine_scan_kernel(
   const int G = hq / hkv, GQ = G * qlen, cpr = head_dim / VEC;
   char *qraw = reinterpret_cast<char *>(smem4);  // [G*Q][D] dtype
   uint32_t *ubits = reinterpret_cast<uint32_t *>(qraw + (size_t)GQ * head_dim * EB);
-  int *urank = reinterpret_cast<int *>(ubits + words);
-  int *plist = urank + words + 1;  // pruned scan: [kPageListCap] union ranks
+  int *plist = reinterpret_cast<int *>(ubits + words);  // pruned scan: [kPageListCap] union ranks
+  int *upage = plist + (pr.mode == 1 ? kPageListCap : 0);  // row lists: the union pages
   const int tid = threadIdx.x;
   const bool pruned = pr.mode == 1 && *pr.ctl <= 0;
   for (int i = tid; i < GQ * cpr; i += 256) {
@@ -1169,10 +1240,10 @@ __global__ void __launch_bounds__(256) fine_scan_kernel(
   }
   int U = 0;
   if (union_src == UNION_ROWS) {
-    U = rank_union<256>(row_pages, row_pages_n, words, ubits, urank, scan_tmp);
+    U = rank_union<256>(row_pages, row_pages_n, words, ubits, upage, scan_tmp);
     if (blockIdx.x == 0 && blockIdx.y == 0)
-      publish_union<DT>(ubits, urank, words, U, page_list, pages_out, counters, union_out, coarse_stats, rows,
-                        n_pages, round, stats_out, stats_accum);
+      publish_union<DT>(upage, U, page_list, pages_out, counters, union_out, coarse_stats, rows, n_pages, round,
+                        stats_out, stats_accum);
   } else if (union_src == UNION_LIST) {
     U = counters[0];
   }
@@ -1215,7 +1286,7 @@ __global__ void __launch_bounds__(256) fine_scan_kernel(
     }
   };
   auto page_of = [&](int v) -> int64_t {
-    return union_src == UNION_ROWS ? union_page(ubits, urank, words, v) : page_list[v];
+    return union_src == UNION_ROWS ? upage[v] : page_list[v];
   };
   auto page_rows = [&](int64_t page, int s) {
     return reinterpret_cast<const char *>(ktab[page >> chunk_shift]) +
@@ -1233,27 +1304,50 @@ __global__ void __launch_bounds__(256) fine_scan_kernel(
     // ceil(k / page_size) pages hold at least k candidates); 0 when U < m.
     const int k = min(pr.width, U * page_size + partial_len);
     const int m = (k + page_size - 1) / page_size;
+    const uint32_t *ubr = pr.ub + r;
+    // A union of at most 256 pages: thread t takes page v = t / 64 + 4 (t %
+    // 64) (consecutive ranks on different waves, as UnionLowerKeys deals
+    // them) and reads its lower bound over b's kv rows and this row's upper
+    // bound together.
+    const bool one_each = U <= 256;
+    const int v1 = (tid >> 6) + 4 * (tid & 63);
+    uint32_t lb1 = 0u, ub1 = 0u;
+    if (one_each && v1 < U) {
+      const int64_t page = page_of(v1);
+      lb1 = max_keys(pr.lb + page * pr.kr + b * hkv, hkv);
+      ub1 = ubr[page * pr.kr];
+    }
     uint32_t tb = 0u;
     if (U >= m) {
-      const UnionLowerKeys<256, decltype(page_of)> src{pr.lb, pr.kr, b * hkv, hkv, U, page_of};
-      tb = block_kth_bound<256>(src, m, tsh);
+      if (one_each) {
+        const OneKey src{comp_of(lb1, v1), v1 < U};
+        tb = block_kth_bound<256>(src, m, tsh);
+      } else {
+        const UnionLowerKeys<256, decltype(page_of)> src{pr.lb, pr.kr, b * hkv, hkv, U, page_of};
+        tb = block_kth_bound<256>(src, m, tsh);
+      }
     }
     if (blockIdx.x == 0 && kvh == 0 && tid == 0) pr.thr[b] = tb;
     // Per window of kPageListCap union pages, the pages whose upper bound
     // for this kv row reaches T are listed in LDS, then their slices are
     // spread over the blocks; the partial page's slices follow.
-    const uint32_t *ubr = pr.ub + r;
     int listed = 0;  // pages listed in earlier windows (the compact staging's slot base)
     for (int base = 0; base < U; base += kPageListCap) {
       const int nv = min(kPageListCap, U - base);
       int nh = 0;
-      for (int c0 = 0; c0 < nv; c0 += 256) {
-        const int v = base + c0 + tid;
-        const int hit = c0 + tid < nv && ubr[page_of(v) * pr.kr] >= tb ? 1 : 0;
-        int tot;
-        const int pos = nh + block_incl_scan<256>(hit, scan_tmp, &tot) - hit;
-        if (hit) plist[pos] = v;
-        nh += tot;
+      if (one_each) {
+        const int hit = v1 < U && ub1 >= tb ? 1 : 0;
+        const int pos = block_incl_scan<256>(hit, scan_tmp, &nh) - hit;
+        if (hit) plist[pos] = v1;
+      } else {
+        for (int c0 = 0; c0 < nv; c0 += 256) {
+          const int v = base + c0 + tid;
+          const int hit = c0 + tid < nv && ubr[page_of(v) * pr.kr] >= tb ? 1 : 0;
+          int tot;
+          const int pos = nh + block_incl_scan<256>(hit, scan_tmp, &tot) - hit;
+          if (hit) plist[pos] = v;
+          nh += tot;
+        }
       }
       __syncthreads();
       for (int item = blockIdx.x; item < nh * nsplit; item += gridDim.x) {
@@ -1334,7 +1428,7 @@ __global__ void __launch_bounds__(256) fine_scan_mfma_kernel(
   uint16_t *qs = reinterpret_cast<uint16_t *>(smem4);  // [GQ16][ROW], rows past GQ zero
   uint16_t *tk = qs + (size_t)GQ16 * ROW;              // [kFineMfmaTok][ROW]
   uint32_t *ubits = reinterpret_cast<uint32_t *>(tk + (size_t)kFineMfmaTok * ROW);
-  int *urank = reinterpret_cast<int *>(ubits + words);
+  int *upage = reinterpret_cast<int *>(ubits + words);  // row lists: the union pages
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, col = lane & 15, grp = lane >> 4;
   for (int i = tid; i < GQ16 * CPR; i += 256) {
     const int j = i / CPR, c = i % CPR;
@@ -1347,10 +1441,10 @@ __global__ void __launch_bounds__(256) fine_scan_mfma_kernel(
   }
   int U = 0;
   if (union_src == UNION_ROWS) {
-    U = rank_union<256>(row_pages, row_pages_n, words, ubits, urank, scan_tmp);
+    U = rank_union<256>(row_pages, row_pages_n, words, ubits, upage, scan_tmp);
     if (blockIdx.x == 0 && blockIdx.y == 0)
-      publish_union<DT>(ubits, urank, words, U, page_list, pages_out, counters, union_out, coarse_stats, rows,
-                        n_pages, round, stats_out, stats_accum);
+      publish_union<DT>(upage, U, page_list, pages_out, counters, union_out, coarse_stats, rows, n_pages, round,
+                        stats_out, stats_accum);
   } else if (union_src == UNION_LIST) {
     U = counters[0];
   }
@@ -1365,7 +1459,7 @@ __global__ void __launch_bounds__(256) fine_scan_mfma_kernel(
     int ntok;
     if (item < page_items) {
       const int v = item / nsplit, sp = item % nsplit;
-      const int64_t page = union_src == UNION_ROWS ? union_page(ubits, urank, words, v) : page_list[v];
+      const int64_t page = union_src == UNION_ROWS ? upage[v] : page_list[v];
       rowbase = reinterpret_cast<const char *>(ktab[page >> chunk_shift]) +
                 (page & ((int64_t(1) << chunk_shift) - 1)) * page_bytes +
                 ((int64_t)r * page_size + (int64_t)sp * tpi) * row_bytes;
@@ -1470,7 +1564,13 @@ __global__ void __launch_bounds__(kSelThreads) fine_select_kernel(
     if (np <= kPageListCap && 2 * np <= U) {
       const PageKeys<NT> pk{row, plist, np * page_size, np * page_size + partial_len, page_size,
                             (int64_t)U * page_size};
-      C = bound_candidates<NT>(pk, k, sh, cand, mx, sum, nz);
+      if (pk.mall <= kRegPageKeys * NT) {
+        RegPageKeys<NT, kRegPageKeys> rp;
+        rp.load(pk);
+        C = bound_candidates<NT>(rp, k, sh, cand, mx, sum, nz);
+      } else {
+        C = bound_candidates<NT>(pk, k, sh, cand, mx, sum, nz);
+      }
       if (C <= list_cap) {
         for (int i = threadIdx.x; i < C; i += NT) out[i] = cand[i];
       } else {
@@ -1514,13 +1614,14 @@ __global__ void __launch_bounds__(kSelThreads) fine_select_kernel(
 }
 
 // ----------------------------------------------------------------- gather
-// Grid (ceil(max list / kGatherCands), B).  Block (x, b) takes list entries
-// x * kGatherCands + w (w = wave): each wave ranks its entry by counting
-// the larger entries of the list; an entry ranked r < k is selected, and
-// the block copies its K and V rows of every kv head to slot r of k_out /
-// v_out ([B][Hkv][width][D]) from the arena (union pages) or the partial
-// page (K from k_stage when the fine scan staged it), and its global token
-// id to idx_out[b][r].  Block (0, 0) also finishes the fine telemetry.
+// gx = ceil(max list / kGatherCands) blocks per batch row.  Gather block
+// (x, b) takes list entries x * kGatherCands + w (w = wave): each wave
+// ranks its entry by counting the larger entries of the list; an entry
+// ranked r < k is selected, and the block copies its K and V rows of every
+// kv head to slot r of k_out / v_out ([B][Hkv][width][D]) from the arena
+// (union pages) or the partial page (K from k_stage when the fine scan
+// staged it), and its global token id to idx_out[b][r].  One more block
+// finishes the fine telemetry.
 constexpr int kGatherCands = 4;
 
 struct GatherArgs {
@@ -1551,6 +1652,43 @@ struct GatherArgs {
   double *stats_accum;
 };
 
+// The fine telemetry (max and mean over the batch rows) and the pruning
+// control, run by one block of its own after the gather blocks: its global
+// reads then delay no copy.
+template <int DT> __device__ void gather_telemetry(const GatherArgs &ga) {
+  if (threadIdx.x != 0) return;
+  const int batch = ga.batch;
+  const int32_t *list_count = ga.list_count;
+  const int U = ga.has_pages ? ga.counters[0] : 0;
+  float m = -INFINITY;
+  double t = 0.0;
+  int64_t scored = 0;  // every candidate, unless the fine scan was pruned
+  for (int r = 0; r < batch; ++r) {
+    m = fmaxf(m, ga.fine_stats[2 * r]);
+    t += ga.fine_stats[2 * r + 1];
+    scored += list_count[batch + r];
+  }
+  float mean = (float)(t / (double)scored);
+  if (ga.round) mean = round_act<DT>(mean);
+  if (ga.stats_out) {
+    ga.stats_out[2] = m;
+    ga.stats_out[3] = mean;
+  }
+  if (ga.stats_accum) {
+    ga.stats_accum[2] += (double)m;
+    ga.stats_accum[3] += (double)mean;
+  }
+  if (ga.ctl) {
+    // Pruning pays when it skips: after a call that read more than three
+    // quarters of the union's slices, the next kPruneRetry calls scan in
+    // full; a paused call counts down.
+    int64_t read = 0;
+    for (int r = 0; r < batch; ++r) read += list_count[2 * batch + r];
+    const int c0 = ga.ctl[0];
+    ga.ctl[0] = c0 > 0 ? c0 - 1 : (4 * read > 3 * (int64_t)U * ga.hkv * batch ? kPruneRetry : 0);
+  }
+}
+
 template <int DT> __device__ void gather_block(const GatherArgs &ga, int bx, int b) {
   constexpr int VEC = Elem<DT>::VEC, EB = Elem<DT>::BYTES;
   __shared__ int slot_of[kGatherCands], cand_of[kGatherCands];
@@ -1559,51 +1697,17 @@ template <int DT> __device__ void gather_block(const GatherArgs &ga, int bx, int
   const int32_t *list_count = ga.list_count, *counters = ga.counters, *page_list = ga.page_list;
   const uint64_t *ktab = ga.ktab, *vtab = ga.vtab;
   const int has_pages = ga.has_pages, chunk_shift = ga.chunk_shift, page_size = ga.page_size;
-  const int partial_len = ga.partial_len, batch = ga.batch, hkv = ga.hkv, head_dim = ga.head_dim;
-  const int width = ga.width, cpr = ga.cpr, round = ga.round;
+  const int partial_len = ga.partial_len, hkv = ga.hkv, head_dim = ga.head_dim;
+  const int width = ga.width, cpr = ga.cpr;
   const int64_t page_bytes = ga.page_bytes, stage_ld = ga.stage_ld, num_finalized = ga.num_finalized;
   const char *part_k = ga.part_k, *part_v = ga.part_v, *k_stage = ga.k_stage;
   char *k_out = ga.k_out, *v_out = ga.v_out;
   int64_t *idx_out = ga.idx_out;
-  const float *fine_stats = ga.fine_stats;
-  float *stats_out = ga.stats_out;
-  double *stats_accum = ga.stats_accum;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int U = has_pages ? counters[0] : 0;
   const int64_t split = (int64_t)U * page_size;
   const int n = (int)split + partial_len;
   const int k = min(width, n);
-  if (bx == 0 && b == 0) {
-    if (tid == 0) {
-      float m = -INFINITY;
-      double t = 0.0;
-      int64_t scored = 0;  // every candidate, unless the fine scan was pruned
-      for (int r = 0; r < batch; ++r) {
-        m = fmaxf(m, fine_stats[2 * r]);
-        t += fine_stats[2 * r + 1];
-        scored += list_count[batch + r];
-      }
-      float mean = (float)(t / (double)scored);
-      if (round) mean = round_act<DT>(mean);
-      if (stats_out) {
-        stats_out[2] = m;
-        stats_out[3] = mean;
-      }
-      if (stats_accum) {
-        stats_accum[2] += (double)m;
-        stats_accum[3] += (double)mean;
-      }
-      if (ga.ctl) {
-        // Pruning pays when it skips: after a call that read more than three
-        // quarters of the union's slices, the next kPruneRetry calls scan
-        // in full; a paused call counts down.
-        int64_t read = 0;
-        for (int r = 0; r < batch; ++r) read += list_count[2 * batch + r];
-        const int c0 = ga.ctl[0];
-        ga.ctl[0] = c0 > 0 ? c0 - 1 : (4 * read > 3 * (int64_t)U * hkv * batch ? kPruneRetry : 0);
-      }
-    }
-  }
   const int C = list_count[b];
   const int first = bx * kGatherCands;
   if (first >= C) return;
@@ -1671,14 +1775,19 @@ template <int DT> __device__ void gather_block(const GatherArgs &ga, int bx, int
   }
 }
 
-template <int DT> __global__ void __launch_bounds__(256) gather_kernel(GatherArgs ga) {
-  gather_block<DT>(ga, blockIdx.x, blockIdx.y);
+// Blocks [0, gx * B) gather (block i: entries of batch row i / gx), the
+// last one runs the telemetry.
+template <int DT> __global__ void __launch_bounds__(256) gather_kernel(GatherArgs ga, int gx) {
+  const int gather_blocks = gx * ga.batch;
+  if ((int)blockIdx.x < gather_blocks) gather_block<DT>(ga, blockIdx.x % gx, blockIdx.x / gx);
+  else gather_telemetry<DT>(ga);
 }
 
 // The gather plus the hot window's attention splits (kiv_retrieve_attend):
 // blocks [0, gx * B) gather, the s_hot * R blocks after them each run one
-// hot split of one kv row.  The splits do not depend on the retrieval, so
-// they run alongside the gather instead of after it.
+// hot split of one kv row, and the last block runs the telemetry.  The
+// splits do not depend on the retrieval, so they run alongside the gather
+// instead of after it.
 template <int DT, int KT>
 __global__ void __launch_bounds__(256) gather_attn_kernel(GatherArgs ga, AttnParams p, int gx, int s_hot) {
   const int gather_blocks = gx * ga.batch;
@@ -1687,7 +1796,8 @@ __global__ void __launch_bounds__(256) gather_attn_kernel(GatherArgs ga, AttnPar
     return;
   }
   const int i = blockIdx.x - gather_blocks;
-  attn_mfma_split<DT, KT>(p, i % s_hot, i / s_hot);
+  if (i < s_hot * ga.batch * ga.hkv) attn_mfma_split<DT, KT>(p, i % s_hot, i / s_hot);
+  else gather_telemetry<DT>(ga);
 }
 
 // Launches the select kernel kern_of(V) whose register chunks per thread V
@@ -1981,6 +2091,9 @@ static int retrieve_impl(kiv_store_t *s, const kiv_retrieve_args_t *a, hipStream
   uint64_t *list = (uint64_t *)s->sel_list.ptr;
   int32_t *list_count = (int32_t *)(list + (size_t)B * list_ld);
   const int bwords = union_src == UNION_ROWS ? words : 0;
+  // The fine scans' LDS list of the union pages (row lists: at most
+  // min(rows * kc, N) pages).
+  const size_t upage_bytes = union_src == UNION_ROWS ? (size_t)std::min<int64_t>((int64_t)rows * kc, N) * 4 : 0;
   // Host tier: the fine scan copies the candidates' K rows to HBM as it
   // streams them, so the gather reads only V over the host link (up to
   // kMaxStageBytes of staging per store).
@@ -2029,7 +2142,7 @@ static int retrieve_impl(kiv_store_t *s, const kiv_retrieve_args_t *a, hipStream
     for (int pass = 0; pass < passes && mfma; ++pass) {
       const int Qp = std::min(Qb, Q - pass * Qb);
       const int gq16 = (G * Qp + 15) & ~15;
-      const size_t lds = ((size_t)gq16 + kFineMfmaTok) * (D + 8) * 2 + (size_t)bwords * 4 + (size_t)(bwords + 1) * 4;
+      const size_t lds = ((size_t)gq16 + kFineMfmaTok) * (D + 8) * 2 + (size_t)bwords * 4 + upage_bytes;
       s->prof_begin(KIV_STAGE_FINE_SCAN, st);
       rc = with_dt(dt, [&](auto dtc) {
         constexpr int DTV = decltype(dtc)::value;
@@ -2065,8 +2178,8 @@ static int retrieve_impl(kiv_store_t *s, const kiv_retrieve_args_t *a, hipStream
     }
     auto valu_scan = [&](int pass, int usrc, int bw, const FinePrune &fp) {
       const int Qp = std::min(Qb, Q - pass * Qb);
-      const size_t lds = (size_t)G * Qp * D * eb + (size_t)bw * 4 + (size_t)(bw + 1) * 4 +
-                         (fp.mode == 1 ? (size_t)kPageListCap * 4 : 0);
+      const size_t lds = (size_t)G * Qp * D * eb + (size_t)bw * 4 + (fp.mode == 1 ? (size_t)kPageListCap * 4 : 0) +
+                         (usrc == UNION_ROWS ? upage_bytes : 0);
       return with_dt_lg(dt, lg, [&](auto dtc, auto lgc) {
         auto kern = fine_scan_kernel<decltype(dtc)::value, decltype(lgc)::value>;
         if (lds > 65536)
@@ -2141,7 +2254,7 @@ static int retrieve_impl(kiv_store_t *s, const kiv_retrieve_args_t *a, hipStream
     ga.stats_accum = a->stats_accum;
     s->prof_begin(KIV_STAGE_GATHER, st);
     if (fa) {
-      const unsigned blocks = gx * (unsigned)B + (unsigned)(fa->s_hot * s->kr);
+      const unsigned blocks = gx * (unsigned)B + (unsigned)(fa->s_hot * s->kr) + 1;
       rc = with_dt(dt, [&](auto dtc) {
         constexpr int DTV = decltype(dtc)::value;
         if constexpr (DTV == DT_F32) {
@@ -2159,7 +2272,8 @@ static int retrieve_impl(kiv_store_t *s, const kiv_retrieve_args_t *a, hipStream
       });
     } else {
       rc = with_dt(dt, [&](auto dtc) {
-        hipLaunchKernelGGL((gather_kernel<decltype(dtc)::value>), dim3(gx, (unsigned)B), dim3(256), 0, st, ga);
+        hipLaunchKernelGGL((gather_kernel<decltype(dtc)::value>), dim3(gx * (unsigned)B + 1), dim3(256), 0, st, ga,
+                           (int)gx);
         return (int)KIV_OK;
       });
     }
