@@ -965,7 +965,13 @@ struct FinePrune {
   char *cstage;
   int32_t *slot_of;
   int scap;
+  // The fine select's page list, per batch row b ([B][kPlanStride]): [0] =
+  // the number of union pages with a scanned slice for b (-1: not listed,
+  // the select lists them itself), [1] = the slices read for b, [2 ..] =
+  // those pages' union ranks, ascending (up to kPageListCap).
+  int32_t *plan;
 };
+constexpr int kPlanStride = 2 + kPageListCap;
 
 // Pruning pays when it skips pages: after a call whose scan read more than
 // three quarters of the union's slices, the next kPruneRetry calls on the
@@ -1364,6 +1370,28 @@ __global__ void __launch_bounds__(256) fine_scan_kernel(
       listed += nh;
       __syncthreads();  // the list is rebuilt for the next window
     }
+    if (blockIdx.x == gridDim.x - 1 && kvh == 0) {
+      // The fine select's page list for b (the last block, which the
+      // pruned slices reach last if at all): the union pages with a slice
+      // of some kv row of b at or above T, and the slices read.
+      int32_t *pl = pr.plan + (int64_t)b * kPlanStride;
+      int np = 0, read_all = 0;
+      for (int c0 = 0; c0 < U; c0 += 256) {
+        const int v = c0 + tid;
+        const int read = v < U ? count_keys_ge(pr.ub + page_of(v) * pr.kr + b * hkv, hkv, tb) : 0;
+        const int hit = read > 0 ? 1 : 0;
+        int tot, rtot;
+        const int pos = np + block_incl_scan<256>(hit, scan_tmp, &tot) - hit;
+        if (hit && pos < kPageListCap) pl[2 + pos] = v;
+        block_incl_scan<256>(read, scan_tmp, &rtot);
+        np += tot;
+        read_all += rtot;
+      }
+      if (tid == 0) {
+        pl[0] = np;
+        pl[1] = read_all;
+      }
+    }
     for (int item = blockIdx.x; item < part_items; item += gridDim.x) {
       const int64_t cand0 = (int64_t)U * page_size + (int64_t)item * tpi;
       scan_slice(part_k + ((int64_t)r * page_size + (int64_t)item * tpi) * row_bytes, cand0,
@@ -1372,7 +1400,10 @@ __global__ void __launch_bounds__(256) fine_scan_kernel(
     return;
   }
   // Full scan: every union page's slices, then the partial page's.
-  if (pr.mode == 1 && blockIdx.x == 0 && kvh == 0 && tid == 0) pr.thr[b] = 0u;  // paused: all scanned
+  if (pr.mode == 1 && blockIdx.x == 0 && kvh == 0 && tid == 0) {
+    pr.thr[b] = 0u;  // paused: all scanned
+    pr.plan[(int64_t)b * kPlanStride] = -1;
+  }
   const int page_items = U * nsplit;
   for (int item = blockIdx.x; item < page_items + part_items; item += gridDim.x) {
     if (item < page_items) {
@@ -1524,7 +1555,7 @@ __global__ void __launch_bounds__(kSelThreads) fine_select_kernel(
     uint32_t *__restrict__ keys, int64_t ld, const int32_t *__restrict__ counters, int has_pages, int page_size,
     int partial_len, int width, float *__restrict__ fine_stats, uint64_t *__restrict__ list, int64_t list_ld,
     int32_t *__restrict__ list_count, int list_cap, const uint32_t *__restrict__ ub, int kr, int hkv,
-    const uint32_t *__restrict__ thr, const int32_t *__restrict__ page_list) {
+    const uint32_t *__restrict__ thr, const int32_t *__restrict__ page_list, const int32_t *__restrict__ plan) {
   constexpr int NT = kSelThreads;
   __shared__ SelSh<NT> sh;
   __shared__ uint64_t cand[kCandCap];
@@ -1542,23 +1573,37 @@ __global__ void __launch_bounds__(kSelThreads) fine_select_kernel(
     // Pruned fine scan: only the pages some kv row of b scanned (and the
     // partial page) hold nonzero keys; the others are not read.
     const uint32_t tb = thr[b];
-    int slices = 0;  // (page, kv row) slices the scan read, this thread's pages
-    const int np = list_pages<NT>(U, [&](int v) {
-      const int read = count_keys_ge(ub + (int64_t)page_list[v] * kr + b * hkv, hkv, tb);
-      slices += read;
-      return read > 0;
-    }, plist, sh.scan_tmp);
-    // The slices read for the next call's pruning decision (the gather's
-    // block (0, 0) sums them over the batch rows).
-    slices = wave_sum_i32(slices);
-    if ((threadIdx.x & 63) == 0) sh.fcnt[threadIdx.x >> 6] = slices;
-    __syncthreads();
-    if (threadIdx.x == 0) {
-      int read = 0;
-      for (int w = 0; w < NT / 64; ++w) read += sh.fcnt[w];
-      list_count[2 * gridDim.x + b] = read;
+    // The fine scan's list (its first entries read together with the
+    // count), or, when it made none, the list built here.
+    const int32_t *pl = plan + (int64_t)b * kPlanStride;
+    const int planned = pl[0];
+    const int first = pl[2 + threadIdx.x];
+    int np;
+    if (planned >= 0) {
+      np = planned;
+      if ((int)threadIdx.x < min(np, kPageListCap)) plist[threadIdx.x] = first;
+      for (int i = threadIdx.x + NT; i < min(np, kPageListCap); i += NT) plist[i] = pl[2 + i];
+      if (threadIdx.x == 0) list_count[2 * gridDim.x + b] = pl[1];
+      __syncthreads();
+    } else {
+      int slices = 0;  // (page, kv row) slices the scan read, this thread's pages
+      np = list_pages<NT>(U, [&](int v) {
+        const int read = count_keys_ge(ub + (int64_t)page_list[v] * kr + b * hkv, hkv, tb);
+        slices += read;
+        return read > 0;
+      }, plist, sh.scan_tmp);
+      // The slices read for the next call's pruning decision (the gather's
+      // telemetry block sums them over the batch rows).
+      slices = wave_sum_i32(slices);
+      if ((threadIdx.x & 63) == 0) sh.fcnt[threadIdx.x >> 6] = slices;
+      __syncthreads();
+      if (threadIdx.x == 0) {
+        int read = 0;
+        for (int w = 0; w < NT / 64; ++w) read += sh.fcnt[w];
+        list_count[2 * gridDim.x + b] = read;
+      }
+      __syncthreads();  // fcnt is reused by the select below
     }
-    __syncthreads();  // fcnt is reused by the select below
     // Few pages: select over their keys alone; else over the whole row
     // (vector loads; the unscored keys are zero).
     if (np <= kPageListCap && 2 * np <= U) {
@@ -1930,11 +1975,12 @@ static int retrieve_impl(kiv_store_t *s, const kiv_retrieve_args_t *a, hipStream
   s->prune_on = false;
   if (prune) {
     // [control, 256 B][thresholds [B]][upper bound keys [N][kr]][lower
-    // bound keys [N][kr]][compact staging slots [N][kr]], zeroed (pruning
-    // on) when (re)allocated.
+    // bound keys [N][kr]][compact staging slots [N][kr]][select page lists
+    // [B][kPlanStride]], zeroed (pruning on) when (re)allocated.
     const size_t thr_off = 256, ub_off = thr_off + (((size_t)B * 4 + 255) & ~size_t(255));
     const size_t nb_keys = (((size_t)N * s->kr + 63) & ~size_t(63)) * 4;
-    const size_t need = ub_off + 3 * nb_keys;
+    const size_t plan_off = ub_off + 3 * nb_keys;
+    const size_t need = plan_off + (size_t)B * kPlanStride * 4;
     if (s->prune.bytes < need) {
       if ((rc = s->prune.ensure(need, st, false))) return rc;
       KIV_HIP(hipMemsetAsync(s->prune.ptr, 0, s->prune.bytes, st));
@@ -1945,6 +1991,7 @@ static int retrieve_impl(kiv_store_t *s, const kiv_retrieve_args_t *a, hipStream
     pr.ub = (const uint32_t *)((char *)s->prune.ptr + ub_off);
     pr.lb = (const uint32_t *)((char *)s->prune.ptr + ub_off + nb_keys);
     pr.slot_of = (int32_t *)((char *)s->prune.ptr + ub_off + 2 * nb_keys);
+    pr.plan = (int32_t *)((char *)s->prune.ptr + plan_off);
     pr.kr = s->kr;
     pr.width = a->out_width;
     pr_ub = pr.ub;
@@ -2208,7 +2255,7 @@ static int retrieve_impl(kiv_store_t *s, const kiv_retrieve_args_t *a, hipStream
       hipLaunchKernelGGL(kern, dim3(B), dim3(kSelThreads), 0, st, (uint32_t *)s->fine_keys.ptr, ldc,
                          (const int32_t *)s->counters.ptr, N > 0 ? 1 : 0, ps, (int)s->partial_len, a->out_width,
                          fine_stats, list, list_ld, list_count, list_cap, pr_ub, s->kr, hkv, pr_thr,
-                         (const int32_t *)s->page_list.ptr);
+                         (const int32_t *)s->page_list.ptr, (const int32_t *)pr.plan);
     }, [](auto vc) { return fine_select_kernel<decltype(vc)::value>; });
     s->prof_end(KIV_STAGE_FINE_SELECT, st);
     KIV_HIP(hipGetLastError());
