@@ -454,12 +454,15 @@ def load_pmc(kernel, workload):
     """HBM bytes per launch of `kernel` from the rocprofv3 --pmc summary committed under
     profiles/ (FETCH_SIZE and WRITE_SIZE, scaled by the same counters' reading for a copy
     kernel of known size), or None when there is none."""
-    path = os.path.join(ROOT, "profiles", f"{kernel}_{workload}_pmc.json")
+    path = os.path.join(ROOT, "profiles", f"{kernel}_{workload}_pmc.txt")
     if not os.path.exists(path):
         return None
     with open(path) as f:
-        d = json.load(f)
-    return d.get("traffic_bytes_per_launch")
+        for line in f:
+            key, _, value = line.partition("=")
+            if key.strip() == "traffic_bytes_per_launch":
+                return int(value)
+    return None
 
 
 def model_flops(cfg, tokens, chunk, cap):
