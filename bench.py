@@ -501,7 +501,8 @@ def model_run(args):
     with torch.device(dev):
         model = Qwen2ForCausalLM(cfg)
     model = model.to(torch.bfloat16).eval()
-    kcfg = KIVConfig(hot_budget=2048, top_p=256, page_size=128, top_pages=32, fine_pruning=not args.no_pruning)
+    kcfg = KIVConfig(hot_budget=2048, top_p=256, page_size=128, top_pages=32, cold_tier=args.cold_tier,
+                     fine_pruning=not args.no_pruning)
     mw = KIVMiddleware(model, kcfg)
     mw.install()
     cache = mw.create_cache(dev)
