@@ -24,7 +24,7 @@ from collections import deque
 import torch
 
 from . import _native as nat
-from . import attention
+from . import attention, persist
 from .config import KIVConfig
 from .model_topology import ModelTopology
 
@@ -358,6 +358,51 @@ class ColdKVStore:
         self._num_finalized = 0
         self._partial_len = 0
         self._invalidate_candidates()
+
+    # ------------------------------------------------------ persistence
+    def save(self, f) -> None:
+        """Write the cold tier to the binary file ``f`` (a section of the
+        format in kiv_amd/persist.py): the rows of every cold token, in
+        order.  No counterpart in the reference, whose cold tier lives in
+        process memory only."""
+        self._flush_pending()
+        T = self.cold_length
+        persist.write_header(f, persist.COLD_MAGIC, {
+            "format": "kiv-cold", "version": persist.VERSION,
+            "dtype": persist.dtype_name(self._dtype or torch.float32), "batch": self._batch or 0,
+            "num_kv_heads": self._num_kv_heads, "head_dim": self._head_dim, "page_size": self._page_size,
+            "cold_length": T, "chunk_tokens": persist.CHUNK_TOKENS,
+        })
+        for first in range(0, T, persist.CHUNK_TOKENS):
+            k, v = self.read_tokens(first, min(persist.CHUNK_TOKENS, T - first))
+            persist.write_tensor(f, k)
+            persist.write_tensor(f, v)
+
+    def load(self, f, device: torch.device | None = None) -> None:
+        """Refill an empty store from a section written by :meth:`save`.
+
+        The rows are evicted again in order, which rebuilds the pages, the
+        summaries and the radii bit for bit.  The file's kv heads, head dim
+        and page size must be this store's; its batch and dtype become the
+        store's.  ``device`` is where a store without rows yet puts them (the
+        store's device by default)."""
+        if self.cold_length:
+            raise RuntimeError("ColdKVStore.load: the store already holds cold tokens; reset() it first")
+        h = persist.read_header(f, persist.COLD_MAGIC)
+        for key, mine in (("num_kv_heads", self._num_kv_heads), ("head_dim", self._head_dim),
+                          ("page_size", self._page_size)):
+            if h[key] != mine:
+                raise ValueError(f"ColdKVStore.load: the file's {key} is {h[key]}, this store's is {mine}")
+        dtype = persist.dtype_of(h["dtype"])
+        if self._dtype is not None and dtype != self._dtype:
+            raise ValueError(f"ColdKVStore.load: the file holds {dtype}, this store {self._dtype}")
+        dev = torch.device(device) if device is not None else self.device
+        B, H, D, T, chunk = h["batch"], h["num_kv_heads"], h["head_dim"], h["cold_length"], h["chunk_tokens"]
+        for first in range(0, T, chunk):
+            n = min(chunk, T - first)
+            k = persist.read_tensor(f, (B, H, n, D), dtype, dev)
+            v = persist.read_tensor(f, (B, H, n, D), dtype, dev)
+            self.evict_from_hot(k, v)
 
     def telemetry_snapshot(self) -> dict:
         return self._telemetry.snapshot()

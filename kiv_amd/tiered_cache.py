@@ -23,6 +23,7 @@ import torch
 from transformers import DynamicCache
 from transformers.cache_utils import DynamicLayer
 
+from . import persist
 from .cold_store import ColdKVStore
 from .config import KIVConfig
 from .model_topology import ModelTopology
@@ -242,6 +243,67 @@ class TieredKVCache(DynamicCache):
             store._invalidate_candidates()
         self._decode_step = 0
         return True
+
+    # ------------------------------------------------------------ persistence
+    def save(self, path) -> None:
+        """Write the whole cache to ``path``: every layer's hot K/V, every
+        cold tier's rows, the token counts and the decode-step counter (the
+        format in kiv_amd/persist.py).  No counterpart in the reference,
+        whose cache lives in process memory only.  Layers other than plain
+        full-attention layers (a sliding window's running state) are not
+        stored: saving such a cache raises NotImplementedError."""
+        entries = []
+        for i, layer in enumerate(self.layers):
+            if not layer.is_initialized or layer.keys is None or layer.keys.numel() == 0:
+                entries.append({"index": i, "kind": "empty"})
+                continue
+            if type(layer) not in (DynamicLayer, _HotLayer):
+                raise NotImplementedError(f"TieredKVCache.save: layer {i} is a {type(layer).__name__}; only "
+                                          "full-attention layers (DynamicLayer) are stored")
+            entries.append({"index": i, "kind": "kv", "dtype": persist.dtype_name(layer.keys.dtype),
+                            "k_shape": list(layer.keys.shape), "v_shape": list(layer.values.shape)})
+        header = {"format": "kiv-cache", "version": persist.VERSION, "num_layers": len(self.layers),
+                  "prefill_complete": self._prefill_complete, "decode_step": self._decode_step,
+                  "total_tokens": {str(i): n for i, n in self._total_tokens.items()},
+                  "cold_layers": sorted(self.cold_stores), "layers": entries}
+        with open(path, "wb") as f:
+            persist.write_header(f, persist.CACHE_MAGIC, header)
+            for e in entries:
+                if e["kind"] == "kv":
+                    layer = self.layers[e["index"]]
+                    persist.write_tensor(f, layer.keys)
+                    persist.write_tensor(f, layer.values)
+            for i in sorted(self.cold_stores):
+                self.cold_stores[i].save(f)
+
+    def load(self, path) -> None:
+        """Restore a cache written by :meth:`save` into this empty cache (one
+        made for the same model and KIVConfig, e.g. by create_cache()).  Hot
+        windows are appended as the model would append them; cold tiers are
+        re-evicted in order, which rebuilds their pages and summaries bit
+        for bit.  Telemetry starts empty."""
+        if any(l.is_initialized and l.keys is not None and l.keys.numel() for l in self.layers) or \
+                any(st.cold_length for st in self.cold_stores.values()):
+            raise RuntimeError("TieredKVCache.load: the cache is not empty; reset() it first")
+        device = next(iter(self.cold_stores.values())).device if self.cold_stores else torch.device("cuda")
+        with open(path, "rb") as f:
+            h = persist.read_header(f, persist.CACHE_MAGIC)
+            if h["num_layers"] != len(self.layers) or sorted(h["cold_layers"]) != sorted(self.cold_stores):
+                raise ValueError("TieredKVCache.load: the file was written for another layer layout "
+                                 f"({h['num_layers']} layers, cold tiers {h['cold_layers']}; this cache: "
+                                 f"{len(self.layers)} layers, cold tiers {sorted(self.cold_stores)})")
+            for e in h["layers"]:
+                if e["kind"] != "kv":
+                    continue
+                dtype = persist.dtype_of(e["dtype"])
+                k = persist.read_tensor(f, tuple(e["k_shape"]), dtype, device)
+                v = persist.read_tensor(f, tuple(e["v_shape"]), dtype, device)
+                self.layers[e["index"]].update(k, v)
+            for i in sorted(self.cold_stores):
+                self.cold_stores[i].load(f, device)
+        self._total_tokens = {int(i): n for i, n in h["total_tokens"].items()}
+        self._prefill_complete = bool(h["prefill_complete"])
+        self._decode_step = int(h["decode_step"])
 
     def memory_report(self) -> dict:
         """Bytes per tier, keys of kiv/tiered_cache.py:259-286 plus what
