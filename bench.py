@@ -635,10 +635,10 @@ def layer_cpu_baseline(mw, cache, model, tok, kcfg, args):
     seen = {}
     orig = ColdKVStore._retrieve
 
-    def spy(self, query, scaling, kiv_config, step, attend):
+    def spy(self, query, scaling, kiv_config, step, attend, *rest, **kw):
         if self is store:
             seen["q"] = query.detach().clone()
-        return orig(self, query, scaling, kiv_config, step, attend)
+        return orig(self, query, scaling, kiv_config, step, attend, *rest, **kw)
 
     mw.install()
     mw.activate_cache(cache)

@@ -120,6 +120,21 @@ typedef struct {
   int64_t append_k_stride[3];
   int64_t append_v_stride[3];
   int64_t append_tokens;
+  /* Rows to write into the caller's hot window before the attention reads
+   * it (0 for none; no counterpart in the reference, where the cache's
+   * update copies them): hot_tokens rows of [B, Hkv, hot_tokens, D] from
+   * hot_src_k / hot_src_v to hot_dst_k / hot_dst_v (same shape, strided).
+   * They ride on the coarse scan's launch when a fresh coarse pass runs,
+   * else on a copy launch of their own, ahead of every kernel of the call. */
+  const void *hot_src_k;
+  const void *hot_src_v;
+  int64_t hot_src_k_stride[3];
+  int64_t hot_src_v_stride[3];
+  void *hot_dst_k;
+  void *hot_dst_v;
+  int64_t hot_dst_k_stride[3];
+  int64_t hot_dst_v_stride[3];
+  int64_t hot_tokens;
 } kiv_retrieve_args_t;
 
 /* Arguments of the merged decode attention over [retrieved ; hot]. */

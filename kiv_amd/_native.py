@@ -55,6 +55,9 @@ class RetrieveArgs(C.Structure):
         ("pages_out", C.c_void_p), ("union_count_out", C.c_void_p), ("stats_out", C.c_void_p),
         ("stats_accum", C.c_void_p), ("append_k", C.c_void_p), ("append_v", C.c_void_p),
         ("append_k_stride", _I64x3), ("append_v_stride", _I64x3), ("append_tokens", C.c_int64),
+        ("hot_src_k", C.c_void_p), ("hot_src_v", C.c_void_p), ("hot_src_k_stride", _I64x3),
+        ("hot_src_v_stride", _I64x3), ("hot_dst_k", C.c_void_p), ("hot_dst_v", C.c_void_p),
+        ("hot_dst_k_stride", _I64x3), ("hot_dst_v_stride", _I64x3), ("hot_tokens", C.c_int64),
     ]
 
 

@@ -222,19 +222,24 @@ class ColdKVStore:
 
     def retrieve_attend(self, query: torch.Tensor, scaling: float, kiv_config: KIVConfig,
                         hot_k: torch.Tensor, hot_v: torch.Tensor, mask: torch.Tensor | None,
-                        step: int = -1) -> torch.Tensor | None:
+                        step: int = -1, hot_rows=None) -> torch.Tensor | None:
         """retrieve_top_kv followed by the merged attention over [retrieved ; hot]
         (kiv_retrieve_attend), or None when the cold tier is empty.
 
         Returns the attention output ``[B, Q, Hq, D]``; the retrieval's
         telemetry and candidate cache are updated as by retrieve_top_kv.
+        ``hot_rows = (src_k, src_v, dst_k, dst_v)``: rows of the hot window
+        not written yet (the cache's decode step leaves them to this call):
+        the call copies src into dst ([B, Hkv, n, D] views) with its first
+        launch, before the attention reads the window.  With None returned
+        they are not written.
         """
         if self.cold_length == 0:
             return None
-        _, _, out = self._retrieve(query, scaling, kiv_config, step, (hot_k, hot_v, mask))
+        _, _, out = self._retrieve(query, scaling, kiv_config, step, (hot_k, hot_v, mask), hot_rows)
         return out
 
-    def _retrieve(self, query, scaling, kiv_config, step, attend):
+    def _retrieve(self, query, scaling, kiv_config, step, attend, hot_rows=None):
         """One retrieval; with ``attend = (hot_k, hot_v, mask)`` also the merged
         attention (fused when the output width is known on the host)."""
         shape = query.shape
@@ -314,6 +319,14 @@ class ColdKVStore:
             a.append_tokens = pt
         else:
             a.append_tokens = 0
+        if hot_rows is not None:
+            sk, sv, dk, dv = hot_rows
+            a.hot_src_k, a.hot_src_v, a.hot_dst_k, a.hot_dst_v = sk.data_ptr(), sv.data_ptr(), dk.data_ptr(), dv.data_ptr()
+            a.hot_src_k_stride, a.hot_src_v_stride = nat.strides(sk, 3), nat.strides(sv, 3)
+            a.hot_dst_k_stride, a.hot_dst_v_stride = nat.strides(dk, 3), nat.strides(dv, 3)
+            a.hot_tokens = sk.shape[2]
+        else:
+            a.hot_tokens = 0
         stream = nat.stream_ptr(dev)
         out = None
         if fused:

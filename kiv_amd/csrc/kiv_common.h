@@ -307,12 +307,20 @@ __device__ __forceinline__ uint4 load16(const void *p) { return *reinterpret_cas
 // from the strided input (element strides, in16 = 16 / element bytes
 // elements per chunk) to partial slot t_dst0 + t.  Used only by launches
 // that do not read the partial page themselves.
+// Rows a retrieval writes in its first launch: `count` evicted rows into
+// the partial page (from k / v, element strides ks* / vs*), and
+// `hot_count` rows into the caller's hot window (from hk / hv to dk / dv,
+// element strides hks* / hvs* / dks* / dvs*).  One block per kv row r.
 struct AppendRows {
   const char *k, *v;
   int64_t ks0, ks1, ks2, vs0, vs1, vs2;
   char *part_k, *part_v;
   int64_t t_dst0;
   int count, hkv, page_size, cpr, in16;
+  const char *hk, *hv;
+  char *dk, *dv;
+  int64_t hks0, hks1, hks2, hvs0, hvs1, hvs2, dks0, dks1, dks2, dvs0, dvs1, dvs2;
+  int hot_count;
 };
 
 __device__ __forceinline__ void append_rows(const AppendRows &ap, int r) {
@@ -326,6 +334,16 @@ __device__ __forceinline__ void append_rows(const AppendRows &ap, int r) {
     const int64_t dst = (((int64_t)r * ap.page_size + ap.t_dst0 + t) * ap.cpr + c) * 16;
     *reinterpret_cast<uint4 *>(ap.part_k + dst) = load16(ap.k + src_k);
     *reinterpret_cast<uint4 *>(ap.part_v + dst) = load16(ap.v + src_v);
+  }
+  for (int i = threadIdx.x; i < ap.hot_count * ap.cpr; i += blockDim.x) {
+    const int t = i / ap.cpr, c = i % ap.cpr;
+    const int64_t e0 = (int64_t)c * ap.in16;
+    const int64_t sk = ((int64_t)b * ap.hks0 + (int64_t)h * ap.hks1 + (int64_t)t * ap.hks2 + e0) * eb;
+    const int64_t sv = ((int64_t)b * ap.hvs0 + (int64_t)h * ap.hvs1 + (int64_t)t * ap.hvs2 + e0) * eb;
+    const int64_t tk = ((int64_t)b * ap.dks0 + (int64_t)h * ap.dks1 + (int64_t)t * ap.dks2 + e0) * eb;
+    const int64_t tv = ((int64_t)b * ap.dvs0 + (int64_t)h * ap.dvs1 + (int64_t)t * ap.dvs2 + e0) * eb;
+    *reinterpret_cast<uint4 *>(ap.dk + tk) = load16(ap.hk + sk);
+    *reinterpret_cast<uint4 *>(ap.dv + tv) = load16(ap.hv + sv);
   }
 }
 

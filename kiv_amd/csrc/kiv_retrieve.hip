@@ -575,6 +575,10 @@ __global__ void __launch_bounds__(kUnionThreads) union_list_kernel(
   }
 }
 
+// Rows a retrieval writes when no coarse scan launch carries them (one
+// block per kv row).
+__global__ void __launch_bounds__(256) append_rows_kernel(AppendRows ap) { append_rows(ap, blockIdx.x); }
+
 // ------------------------------------------------------------ coarse scan
 // Grid (page blocks, B*Hkv); block (x, r) scores kv row r of its pages.
 // A lane owns one page and holds a segment of that page's summary row in
@@ -622,7 +626,7 @@ __global__ void __launch_bounds__(kScanThreads) coarse_scan_kernel(
     const char *__restrict__ summ, int64_t n_pages, int kr, const char *__restrict__ q, int64_t qs0,
     int64_t qs1, int64_t qs2, int hq, int hkv, int qlen, float scale, int round, uint32_t *__restrict__ keys,
     int64_t ld, AppendRows ap) {
-  if (ap.count > 0 && blockIdx.x == gridDim.x - 1) {
+  if ((ap.count > 0 || ap.hot_count > 0) && blockIdx.x == gridDim.x - 1) {
     append_rows(ap, blockIdx.y);  // the step's evicted rows (an extra block per kv row)
     return;
   }
@@ -735,7 +739,7 @@ __global__ void __launch_bounds__(kScanThreads) coarse_scan_mfma_kernel(
     int64_t ld, const float *__restrict__ rad2, uint32_t *__restrict__ ubk, uint32_t *__restrict__ lbk,
     AppendRows ap) {
   static_assert(DT != DT_F32, "16-bit dtypes only");
-  if (ap.count > 0 && blockIdx.x == gridDim.x - 1) {
+  if ((ap.count > 0 || ap.hot_count > 0) && blockIdx.x == gridDim.x - 1) {
     append_rows(ap, blockIdx.y);  // the step's evicted rows (an extra block per kv row)
     return;
   }
@@ -1928,6 +1932,19 @@ static int retrieve_impl(kiv_store_t *s, const kiv_retrieve_args_t *a, hipStream
       if (rc) return rc;
     }
   }
+  // Rows for the caller's hot window: checked here, written with the
+  // coarse scan's launch or by a launch of their own (below).
+  if (a->hot_tokens > 0) {
+    if (!a->hot_src_k || !a->hot_src_v || !a->hot_dst_k || !a->hot_dst_v ||
+        (((uintptr_t)a->hot_src_k | (uintptr_t)a->hot_src_v | (uintptr_t)a->hot_dst_k | (uintptr_t)a->hot_dst_v) &
+         15))
+      return fail(KIV_ERR_INVALID, "kiv_retrieve: hot-window rows must be non-null and 16-byte aligned");
+    for (int i = 0; i < 3; ++i)
+      if ((a->hot_src_k_stride[i] % vec) || (a->hot_src_v_stride[i] % vec) || (a->hot_dst_k_stride[i] % vec) ||
+          (a->hot_dst_v_stride[i] % vec))
+        return fail(KIV_ERR_INVALID, "kiv_retrieve: hot-window strides must be multiples of %d elements", vec);
+    if (a->hot_tokens > (1 << 20)) return fail(KIV_ERR_UNSUPPORTED, "kiv_retrieve: too many hot-window rows");
+  }
   const int rows = B * hq * Q;
   if (s->num_pages * ps + s->partial_len + ap.count == 0)
     return fail(KIV_ERR_STATE, "kiv_retrieve: the cold store is empty");
@@ -2000,6 +2017,37 @@ static int retrieve_impl(kiv_store_t *s, const kiv_retrieve_args_t *a, hipStream
     s->prune_on = true;
   }
 
+  if (a->hot_tokens > 0) {
+    ap.hk = (const char *)a->hot_src_k;
+    ap.hv = (const char *)a->hot_src_v;
+    ap.dk = (char *)a->hot_dst_k;
+    ap.dv = (char *)a->hot_dst_v;
+    ap.hks0 = a->hot_src_k_stride[0];
+    ap.hks1 = a->hot_src_k_stride[1];
+    ap.hks2 = a->hot_src_k_stride[2];
+    ap.hvs0 = a->hot_src_v_stride[0];
+    ap.hvs1 = a->hot_src_v_stride[1];
+    ap.hvs2 = a->hot_src_v_stride[2];
+    ap.dks0 = a->hot_dst_k_stride[0];
+    ap.dks1 = a->hot_dst_k_stride[1];
+    ap.dks2 = a->hot_dst_k_stride[2];
+    ap.dvs0 = a->hot_dst_v_stride[0];
+    ap.dvs1 = a->hot_dst_v_stride[1];
+    ap.dvs2 = a->hot_dst_v_stride[2];
+    ap.hot_count = (int)a->hot_tokens;
+    ap.hkv = hkv;
+    ap.cpr = cpr;
+    ap.in16 = vec;
+    if (!fresh) {
+      // No coarse scan to carry them: a copy launch ahead of the rest.
+      AppendRows hot = ap;
+      hot.count = 0;
+      ap.hot_count = 0;
+      hipLaunchKernelGGL(append_rows_kernel, dim3((unsigned)s->kr), dim3(256), 0, st, hot);
+      KIV_HIP(hipGetLastError());
+    }
+  }
+
   // ---- coarse: page scan + per-row top pages
   int union_src = UNION_NONE;
   int64_t umax = 0;
@@ -2026,7 +2074,7 @@ static int retrieve_impl(kiv_store_t *s, const kiv_retrieve_args_t *a, hipStream
         // The step's evicted rows ride on the first pass's launch.
         AppendRows apass{};
         if (pass == 0) apass = ap;
-        const int extra = apass.count > 0 ? 1 : 0;
+        const int extra = apass.count > 0 || apass.hot_count > 0 ? 1 : 0;
         s->prof_begin(KIV_STAGE_COARSE_SCAN, st);
         if (mfma) {
           const int pages_per_block = (kScanThreads / 64) * kScanMfmaPages;

@@ -74,6 +74,13 @@ def _none_mask_rule(impl: str | None, module, q_len: int, kv_len: int) -> str | 
     return None
 
 
+def _write_rows(rows) -> None:
+    """Write hot rows a decode update left unwritten (src_k, src_v, dst_k, dst_v)."""
+    if rows is not None:
+        rows[2].copy_(rows[0])
+        rows[3].copy_(rows[1])
+
+
 class KIVMiddleware:
 
     def __init__(self, model: Any, config: KIVConfig | None = None, topology: ModelTopology | None = None) -> None:
@@ -118,6 +125,11 @@ class KIVMiddleware:
         (kiv/middleware.py:108-134)."""
         if not self._installed:
             return
+        prev = getattr(self, "_active_cache", None)
+        if prev is not None:
+            prev.flush_hot()
+            prev._defer_hot_append = False
+            self._active_cache = None
         if self._original_impl is not None:
             self._set_attn_impl(self._original_impl)
         if self._kiv_key is not None:
@@ -147,9 +159,18 @@ class KIVMiddleware:
         return cache
 
     def activate_cache(self, cache: TieredKVCache | None) -> None:
-        """Point the wrapper of every global layer at ``cache`` (or unbind)."""
+        """Point the wrapper of every global layer at ``cache`` (or unbind).
+
+        The active cache's decode updates leave each owned layer's new hot
+        rows to that layer's retrieval, which writes them in its first
+        launch (the wrapper below always takes them); a cache that stops
+        being active writes any such rows and stops deferring."""
         if self.topology is None or self._text_model is None:
             return
+        prev = getattr(self, "_active_cache", None)
+        if prev is not None and prev is not cache:
+            prev.flush_hot()
+            prev._defer_hot_append = False
         for i in self.topology.global_layer_indices:
             attn = self._text_model.layers[i].self_attn
             if cache is None:
@@ -157,6 +178,9 @@ class KIVMiddleware:
                     delattr(attn, "_kiv_cache")
             else:
                 attn._kiv_cache = cache
+        if cache is not None:
+            cache._defer_hot_append = True
+        self._active_cache = cache
 
     # --------------------------------------------------------------- prefill
     def chunked_prefill(self, input_ids: torch.Tensor, cache: TieredKVCache, chunk_size: int = 4096,
@@ -261,11 +285,17 @@ class KIVMiddleware:
         def kiv_attention(module, query, key, value, attention_mask, **kwargs):
             cache = getattr(module, "_kiv_cache", None)
             layer_idx = getattr(module, "_kiv_layer_idx", None)
+            # Hot rows this layer's update left unwritten: the fused call
+            # below writes them in its first launch; every other path writes
+            # them here first.
+            pend = cache.take_hot_rows(layer_idx) if cache is not None and layer_idx is not None else None
             if (middleware._prefilling or cache is None or layer_idx is None
                     or getattr(cache, "_suppress_cold", False)):
+                _write_rows(pend)
                 return dense_attention(module, query, key, value, attention_mask, kwargs)
             store = cache.get_cold_store(layer_idx)
             if store is None or store.cold_length == 0:
+                _write_rows(pend)
                 return dense_attention(module, query, key, value, attention_mask, kwargs)
             scaling = kwargs.get("scaling")
             if scaling is None:
@@ -278,8 +308,14 @@ class KIVMiddleware:
             if _merged_kernel_applies(module, query, key, attention_mask, kwargs):
                 # Retrieval and the merged attention in one call (hot-window
                 # splits overlap the retrieval's gather).
-                out = store.retrieve_attend(query, scaling, kiv_config, key, value, attention_mask, step=step)
+                try:
+                    out = store.retrieve_attend(query, scaling, kiv_config, key, value, attention_mask, step=step,
+                                                hot_rows=pend)
+                except BaseException:
+                    _write_rows(pend)
+                    raise
                 return out.to(query.dtype), None
+            _write_rows(pend)
             cold_k, cold_v = store.retrieve_top_kv(query, scaling, kiv_config, step=step)
             if cold_k is None:
                 return dense_attention(module, query, key, value, attention_mask, kwargs)

@@ -40,6 +40,11 @@ class _HotLayer(DynamicLayer):
     appended rows in decode).  Any other code that replaces ``keys`` /
     ``values`` (crop, batch selection, truncation) is picked up at the next
     update, which copies the replacement into a new buffer.
+
+    With ``defer_append`` set (by the cache, for one decode update under the
+    middleware), update leaves the new rows unwritten: the layer's attention
+    takes them (``take_pending``) and the retrieval's first launch writes
+    them, or writes them itself (``flush``).
     """
 
     slack = 256
@@ -49,6 +54,28 @@ class _HotLayer(DynamicLayer):
         self._kb = self._vb = None
         self._start = self._end = 0
         self._view = None
+        self._pending_rows = None  # (src_k, src_v, first row, n) not written yet
+        self.defer_append = False
+
+    def flush(self) -> None:
+        """Write rows an update left unwritten."""
+        p = self._pending_rows
+        if p is not None:
+            self._pending_rows = None
+            k, v, e, n = p
+            self._kb[:, :, e:e + n].copy_(k)
+            self._vb[:, :, e:e + n].copy_(v)
+
+    def take_pending(self):
+        """(src_k, src_v, dst_k, dst_v) of the rows the last update left
+        unwritten, or None; the caller writes them before anything reads
+        the window."""
+        p = self._pending_rows
+        if p is None:
+            return None
+        self._pending_rows = None
+        k, v, e, n = p
+        return k, v, self._kb[:, :, e:e + n], self._vb[:, :, e:e + n]
 
     def _window(self) -> None:
         self.keys = self._kb[:, :, self._start:self._end]
@@ -67,6 +94,8 @@ class _HotLayer(DynamicLayer):
         self._kb, self._vb, self._start, self._end = kb, vb, 0, T
 
     def update(self, key_states: torch.Tensor, value_states: torch.Tensor, *args, **kwargs):
+        self.flush()
+        defer, self.defer_append = self.defer_append, False
         if not self.is_initialized:
             self.lazy_initialization(key_states, value_states)
         n = key_states.shape[-2]
@@ -80,8 +109,11 @@ class _HotLayer(DynamicLayer):
         elif (self._end + n > self._kb.shape[2] or key_states.shape[:2] != self._kb.shape[:2]
               or key_states.dtype != self._kb.dtype):
             self._move(self.keys, self.values, n)
-        self._kb[:, :, self._end:self._end + n].copy_(key_states)
-        self._vb[:, :, self._end:self._end + n].copy_(value_states)
+        if defer and key_states.dtype == self._kb.dtype and value_states.dtype == self._vb.dtype:
+            self._pending_rows = (key_states, value_states, self._end, n)
+        else:
+            self._kb[:, :, self._end:self._end + n].copy_(key_states)
+            self._vb[:, :, self._end:self._end + n].copy_(value_states)
         self._end += n
         self._window()
         return self.keys, self.values
@@ -115,6 +147,10 @@ class TieredKVCache(DynamicCache):
         self._suppress_cold = False      # wrapper skips retrieval while set
         self._total_tokens: dict[int, int] = {}
         self._decode_step = 0            # shared-layer candidate reuse key
+        # Set by the middleware while this cache is its active one: decode
+        # updates of owned layers leave the new hot rows to the layer's
+        # retrieval (see _HotLayer.defer_append).
+        self._defer_hot_append = False
 
     # -------------------------------------------------------------- helpers
     def _kv_source_layer_idx(self, layer_idx: int) -> int:
@@ -170,6 +206,13 @@ class TieredKVCache(DynamicCache):
         The token appended in this call stays hot; the evicted ones are
         already cold candidates for the same layer call.
         """
+        if (self._defer_hot_append and self._prefill_complete and layer_idx in self.cold_stores
+                and layer_idx < len(self.layers) and isinstance(self.layers[layer_idx], _HotLayer)
+                and key_states.shape[-2] <= self.kiv_config.hot_budget):
+            # The new rows outlive this step's eviction (it takes the oldest
+            # hot_len - hot_budget rows), so their write can wait for the
+            # layer's retrieval.
+            self.layers[layer_idx].defer_append = True
         keys, values = super().update(key_states, value_states, layer_idx, *args, **kwargs)
         owned = self.topology.independent_kv_layers
         if layer_idx in owned:
@@ -212,6 +255,7 @@ class TieredKVCache(DynamicCache):
         return super().get_seq_length(src)
 
     def reset(self) -> None:
+        self.flush_hot()
         super().reset()
         for store in self.cold_stores.values():
             store.reset()
@@ -228,6 +272,7 @@ class TieredKVCache(DynamicCache):
         tier; otherwise hot K/V are sliced, the candidate caches cleared and
         the decode-step counter restarted.
         """
+        self.flush_hot()
         owned = list(self._owned_layers())
         for i, layer in owned:
             cold = self.cold_stores[i].cold_length
@@ -245,6 +290,19 @@ class TieredKVCache(DynamicCache):
         return True
 
     # ------------------------------------------------------------ persistence
+    def take_hot_rows(self, layer_idx: int):
+        """The hot rows layer ``layer_idx``'s last update left unwritten, as
+        (src_k, src_v, dst_k, dst_v), or None; the caller writes them."""
+        if layer_idx < len(self.layers) and isinstance(self.layers[layer_idx], _HotLayer):
+            return self.layers[layer_idx].take_pending()
+        return None
+
+    def flush_hot(self) -> None:
+        """Write every hot row a decode update left to its layer's retrieval."""
+        for layer in self.layers:
+            if isinstance(layer, _HotLayer):
+                layer.flush()
+
     def save(self, path) -> None:
         """Write the whole cache to ``path``: every layer's hot K/V, every
         cold tier's rows, the token counts and the decode-step counter (the
@@ -252,6 +310,7 @@ class TieredKVCache(DynamicCache):
         whose cache lives in process memory only.  Layers other than plain
         full-attention layers (a sliding window's running state) are not
         stored: saving such a cache raises NotImplementedError."""
+        self.flush_hot()
         entries = []
         for i, layer in enumerate(self.layers):
             if not layer.is_initialized or layer.keys is None or layer.keys.numel() == 0:

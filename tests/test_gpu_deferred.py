@@ -102,3 +102,82 @@ def test_deferred_edges(cuda):
     a.reset()
     assert a._pending is None and a.cold_length == 0
     assert a.retrieve_top_kv(q, w.scaling, cfg) == (None, None)
+
+
+def _tiny_qwen2(cuda, dtype):
+    from transformers import Qwen2Config, Qwen2ForCausalLM
+
+    cfg = Qwen2Config(vocab_size=512, hidden_size=256, intermediate_size=512, num_hidden_layers=2,
+                      num_attention_heads=4, num_key_value_heads=2, head_dim=64, max_position_embeddings=4096,
+                      tie_word_embeddings=False)
+    cfg._attn_implementation = "eager"
+    torch.manual_seed(0)
+    return Qwen2ForCausalLM(cfg).to(dtype).to(cuda).eval()
+
+
+@pytest.mark.parametrize("dtype,per_step", [(torch.bfloat16, 1), (torch.float32, 1), (torch.bfloat16, 2)])
+def test_hot_rows_written_by_the_retrieval_match_the_cache_copy(cuda, dtype, per_step, monkeypatch):
+    """Under the middleware a decode update leaves the new hot rows to the
+    layer's retrieval: its first launch writes them (the coarse scan's extra
+    blocks, or a copy launch while the store has no finished page), or the
+    wrapper writes them on paths without it (two query positions per step).
+    fp32 takes the call's two-launch form, whose retrieval writes them.  Against the
+    same model with the cache's own copies: identical logits and telemetry at
+    every step, from a cold tier of 5 tokens (no finished page) to several
+    pages."""
+    print(f"deferred hot rows case dtype={dtype} per_step={per_step}", flush=True)
+    from kiv_amd import KIVMiddleware
+    from kiv_amd import middleware as mwmod
+
+    seen = {"retrieval": 0, "wrapper": 0}
+    real_retrieve, real_write = ColdKVStore._retrieve, mwmod._write_rows
+
+    def retrieve_spy(self, *args, **kwargs):
+        rows = args[5] if len(args) > 5 else kwargs.get("hot_rows")
+        seen["retrieval"] += rows is not None
+        return real_retrieve(self, *args, **kwargs)
+
+    def write_spy(rows):
+        seen["wrapper"] += rows is not None
+        return real_write(rows)
+
+    monkeypatch.setattr(ColdKVStore, "_retrieve", retrieve_spy)
+    monkeypatch.setattr(mwmod, "_write_rows", write_spy)
+    model = _tiny_qwen2(cuda, dtype)
+    mw = KIVMiddleware(model, KIVConfig(hot_budget=64, top_p=16, page_size=16, top_pages=2))
+    mw.install()
+    try:
+        ids = torch.randint(0, 512, (1, 69), generator=torch.Generator().manual_seed(8)).to(cuda)
+        runs = []
+        for defer in (True, False):
+            cache = mw.create_cache(cuda)
+            cache._defer_hot_append = defer
+            logits, tel = [], []
+            with torch.no_grad():
+                out = mw.chunked_prefill(ids, cache, chunk_size=32)
+                assert cache.get_cold_store(0).cold_length == 5
+                tok = out.argmax(-1, keepdim=True).repeat(1, per_step)
+                for _ in range(40):
+                    lg = model(input_ids=tok, past_key_values=cache, use_cache=True).logits[:, -per_step:]
+                    logits.append(lg)
+                    tok = lg.argmax(-1)
+            assert all(layer._pending_rows is None for layer in cache.layers if hasattr(layer, "_pending_rows"))
+            for i in sorted(cache.cold_stores):
+                tel.append(cache.cold_stores[i].telemetry_snapshot()["recent"])
+            runs.append((logits, tel, cache))
+        (la, ta, ca), (lb, tb, cb) = runs
+        # Every decode step of both layers deferred its rows in the first run:
+        # the retrieval took them (one position), or the wrapper wrote them.
+        if per_step == 1:
+            assert seen["retrieval"] == 80 and seen["wrapper"] == 0
+        else:
+            assert seen["retrieval"] == 0 and seen["wrapper"] == 80
+        assert ca.get_cold_store(0).num_pages >= 2
+        for x, y in zip(la, lb):
+            assert torch.equal(x, y)
+        assert ta == tb
+        for i in ca.cold_stores:
+            assert torch.equal(ca.layers[i].keys, cb.layers[i].keys)
+            assert torch.equal(ca.layers[i].values, cb.layers[i].values)
+    finally:
+        mw.uninstall()

@@ -63,9 +63,9 @@ def test_qwen15b_shape_million_token_prefill_then_decode_retrieval(cuda, monkeyp
         seen = {}
         orig = ColdKVStore._retrieve
 
-        def spy(self, query, scaling, kiv_config, step, attend):
+        def spy(self, query, scaling, kiv_config, step, attend, *rest, **kw):
             seen[id(self)] = (query.detach().clone(), scaling)
-            return orig(self, query, scaling, kiv_config, step, attend)
+            return orig(self, query, scaling, kiv_config, step, attend, *rest, **kw)
 
         monkeypatch.setattr(ColdKVStore, "_retrieve", spy)
         tok = logits.argmax(-1, keepdim=True)
