@@ -38,6 +38,7 @@ namespace kiv {
 constexpr int kMaxOut = 4096;       // largest top-P (list entries the gather ranks)
 constexpr int kScanThreads = 256;   // coarse scan block (4 waves)
 constexpr int kSelThreads = 512;       // select block (8 waves)
+constexpr int kWideSelThreads = 1024;  // fine select block for rows of many candidates (16 waves)
 constexpr int kMaxWords = 4096;     // bitmap words ranked in LDS (131072 pages)
 constexpr int kCandCap = 2048;      // candidates a select keeps in LDS
 constexpr int kRankCap = 1024;      // candidates a coarse select ranks by counting in one block
@@ -1553,14 +1554,13 @@ __global__ void __launch_bounds__(256) fine_scan_mfma_kernel(
 // scan, which accumulates with atomicMax.  Keys a pruned scan skipped are
 // zero; at least k keys are scored, so none of them is listed.
 // V = 16-byte key chunks per thread kept in registers: rows of up to
-// 4 * V * kSelThreads keys are read once; longer rows are re-read.
-template <int V>
-__global__ void __launch_bounds__(kSelThreads) fine_select_kernel(
+// 4 * V * NT keys are read once; longer rows are re-read.
+template <int V, int NT>
+__global__ void __launch_bounds__(NT) fine_select_kernel(
     uint32_t *__restrict__ keys, int64_t ld, const int32_t *__restrict__ counters, int has_pages, int page_size,
     int partial_len, int width, float *__restrict__ fine_stats, uint64_t *__restrict__ list, int64_t list_ld,
     int32_t *__restrict__ list_count, int list_cap, const uint32_t *__restrict__ ub, int kr, int hkv,
     const uint32_t *__restrict__ thr, const int32_t *__restrict__ page_list, const int32_t *__restrict__ plan) {
-  constexpr int NT = kSelThreads;
   __shared__ SelSh<NT> sh;
   __shared__ uint64_t cand[kCandCap];
   __shared__ int plist[kPageListCap];
@@ -1852,9 +1852,10 @@ __global__ void __launch_bounds__(256) gather_attn_kernel(GatherArgs ga, AttnPar
 // Launches the select kernel kern_of(V) whose register chunks per thread V
 // is the smallest of 2, 4, 8, 16 that holds a row of n keys (16 for longer
 // rows, which are then re-read from memory).
-template <typename L, typename K> static void with_select_chunks(int64_t n, L &&launch, K &&kern_of) {
+template <int NT = kSelThreads, typename L, typename K>
+static void with_select_chunks(int64_t n, L &&launch, K &&kern_of) {
   using std::integral_constant;
-  const int64_t per = ((n + 3) / 4 + kSelThreads - 1) / kSelThreads;
+  const int64_t per = ((n + 3) / 4 + NT - 1) / NT;
   if (per <= 2) launch(kern_of(integral_constant<int, 2>{}));
   else if (per <= 4) launch(kern_of(integral_constant<int, 4>{}));
   else if (per <= 8) launch(kern_of(integral_constant<int, 8>{}));
@@ -2299,12 +2300,20 @@ static int retrieve_impl(kiv_store_t *s, const kiv_retrieve_args_t *a, hipStream
   }
   {
     s->prof_begin(KIV_STAGE_FINE_SELECT, st);
-    with_select_chunks(cmax, [&](auto kern) {
-      hipLaunchKernelGGL(kern, dim3(B), dim3(kSelThreads), 0, st, (uint32_t *)s->fine_keys.ptr, ldc,
+    // Rows of more than 8192 candidates take a block of 1024 threads (half
+    // the keys per thread, the same per-wave bound).
+    auto launch = [&](auto kern, int nt) {
+      hipLaunchKernelGGL(kern, dim3(B), dim3(nt), 0, st, (uint32_t *)s->fine_keys.ptr, ldc,
                          (const int32_t *)s->counters.ptr, N > 0 ? 1 : 0, ps, (int)s->partial_len, a->out_width,
                          fine_stats, list, list_ld, list_count, list_cap, pr_ub, s->kr, hkv, pr_thr,
                          (const int32_t *)s->page_list.ptr, (const int32_t *)pr.plan);
-    }, [](auto vc) { return fine_select_kernel<decltype(vc)::value>; });
+    };
+    if (cmax > 4 * 4 * kSelThreads && !prune)
+      with_select_chunks<kWideSelThreads>(cmax, [&](auto kern) { launch(kern, kWideSelThreads); },
+                                          [](auto vc) { return fine_select_kernel<decltype(vc)::value, kWideSelThreads>; });
+    else
+      with_select_chunks<kSelThreads>(cmax, [&](auto kern) { launch(kern, kSelThreads); },
+                                      [](auto vc) { return fine_select_kernel<decltype(vc)::value, kSelThreads>; });
     s->prof_end(KIV_STAGE_FINE_SELECT, st);
     KIV_HIP(hipGetLastError());
   }
