@@ -32,7 +32,8 @@ static __device__ __align__(256) char scratch[kNoAllocScratchBytes];
 
 namespace kiv {
 
-constexpr int kFinalUT = 16;  // retrieved keys per lane group in the final kernel
+constexpr int kFinalThreads = 512;   // block of the final kernel
+constexpr int kFinalUT = 8;         // retrieved keys per lane group in the final kernel
 
 template <int DT, int KT>
 __global__ void __launch_bounds__(kAttnThreads) decode_attn_mfma_kernel(AttnParams p) {
@@ -255,21 +256,24 @@ __global__ void __launch_bounds__(kAttnThreads) decode_attn_combine_kernel(AttnP
   store_elem<DT>(p.out, ob + 3, o.w * inv);
 }
 
-// Final kernel of the fused path, one block per query row (b, h, q
-// position): attention over the row's P retrieved keys in one pass - lane
-// group `slot` of LG lanes takes keys slot, slot + NSLOT, ... (at most
-// kFinalUT of them), each lane one 16-byte chunk of the key, with every K
-// and V chunk and the hot partials loaded up front - then a log-sum-exp
-// merge with the hot window's split partials (m, l, acc) that the fused
-// gather launch left in the workspace.  Retrieved keys are never masked.
+// Final kernel of the fused path, one block of kFinalThreads per query row
+// (b, h, q position): attention over the row's P retrieved keys in one
+// pass - lane group `slot` of LG lanes takes keys slot, slot + NSLOT, ...
+// (at most kFinalUT of them), each lane one 16-byte chunk of the key, with
+// every K and V chunk and the hot partials loaded up front - then a
+// log-sum-exp merge with the hot window's split partials (m, l, acc) that
+// the fused gather launch left in the workspace.  Retrieved keys are never
+// masked.  The rows are few (B * Hq), so each gets a wide block: 16 waves
+// share the keys and the hot splits.
 template <int DT, int LG>
-__global__ void __launch_bounds__(kAttnThreads) decode_attn_final_kernel(AttnParams p, int s_hot) {
+__global__ void __launch_bounds__(kFinalThreads) decode_attn_final_kernel(AttnParams p, int s_hot) {
+  constexpr int NT = kFinalThreads;
   constexpr int VEC = Elem<DT>::VEC, EB = Elem<DT>::BYTES;
-  constexpr int NSLOT = kAttnThreads / LG, UT = kFinalUT, W = kAttnThreads / 64;
+  constexpr int NSLOT = NT / LG, UT = kFinalUT, W = NT / 64;
   __shared__ float red[W][512];  // per-wave V sums (head_dim <= 512)
   __shared__ float bm[W], bl[W];
-  __shared__ float sm[kAttnThreads], sl[kAttnThreads];
-  __shared__ float4 so[kAttnThreads];
+  __shared__ float sm[NT], sl[NT];
+  __shared__ float4 so[NT];
   const int row = blockIdx.x;  // (b*Hq + h)*Q + qp
   const int qp = row % p.qlen, bh = row / p.qlen;
   const int b = bh / p.hq, h = bh % p.hq;
@@ -291,7 +295,7 @@ __global__ void __launch_bounds__(kAttnThreads) decode_attn_final_kernel(AttnPar
   }
   // Hot partials: thread (g, i4) owns output dims 4 i4 .. 4 i4 + 3 of
   // splits g, g + groups, ...
-  const int d4n = D / 4, groups = kAttnThreads / d4n, g = tid / d4n, i4 = tid - g * d4n;
+  const int d4n = D / 4, groups = NT / d4n, g = tid / d4n, i4 = tid - g * d4n;
   float hm[kCombineBatch], hl[kCombineBatch];
   float4 ha[kCombineBatch];
 #pragma unroll
@@ -553,7 +557,7 @@ static int attention_launch(const kiv_attention_args_t *a, hipStream_t st, const
 
 // Retrieved keys the final kernel takes in its one pass (lane groups of lg
 // lanes, kFinalUT keys per group).
-static int final_capacity(int lg) { return kAttnThreads / lg * kFinalUT; }
+static int final_capacity(int lg) { return kFinalThreads / lg * kFinalUT; }
 
 int fused_attention_plan(const kiv_attention_args_t *a, FusedAttention *f) {
   int rc = attention_check(a, "kiv_retrieve_attend");
@@ -578,7 +582,7 @@ int fused_attention_finish(const FusedAttention &f, hipStream_t st) {
   const int rows = p.batch * p.hq * p.qlen;
   int rc = with_dt_lg(f.dtype, f.lg, [&](auto dtc, auto lgc) {
     hipLaunchKernelGGL((decode_attn_final_kernel<decltype(dtc)::value, decltype(lgc)::value>), dim3(rows),
-                       dim3(kAttnThreads), 0, st, p, f.s_hot);
+                       dim3(kFinalThreads), 0, st, p, f.s_hot);
     return (int)KIV_OK;
   });
   if (rc) return rc;
