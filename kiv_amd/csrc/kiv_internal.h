@@ -16,6 +16,7 @@ int fail(int code, const char *fmt, ...);
 int hip_fail(hipError_t e, const char *what);
 // LDS bytes one workgroup may use on the current device (cached per device).
 size_t device_lds_limit();
+int device_cu_count();  // compute units of the current device (cached)
 
 #define KIV_HIP(expr)                                   \
   do {                                                  \

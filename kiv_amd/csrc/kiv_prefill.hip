@@ -11,13 +11,19 @@
 // (flash style), which moves each output by at most the probabilities'
 // own rounding, u * sum_k p_k |v_k|.
 //
-// Grid (ceil(Q / 64), B * Hq), 256 threads; wave w owns query rows
-// q0 + 16 w .. + 15 of one q head.  Keys come in tiles of 64: first the
-// retrieved keys, then the hot keys (a tile never mixes the two, so hot
-// tiles line up with the mask's column tiles).  Per tile:
+// Blocks of 256 threads own 128 query rows of one q head (64 above head_dim
+// 128): wave w holds row groups of 16 rows.  The grid is one-dimensional in
+// longest-first order (row blocks from the last, which under the causal rule
+// see the most keys), and long rows are split over key ranges whose partial
+// rows a combine kernel merges; the host picks the split count by
+// simulating the longest-first schedule over the GPU's block slots.  Keys
+// come in tiles of 64: first the retrieved keys, then the hot keys (a tile
+// never mixes the two, so hot tiles line up with the mask's column tiles).
+// Per tile:
 //  - K rows ([64][D], rows padded by 16 bytes) and V transposed ([D][64],
 //    rows padded by 8 bytes) go to LDS from registers that were loaded
-//    while the previous tile was being computed;
+//    (buffer loads bounded to the segment) while the previous tile was
+//    being computed;
 //  - S^T = K Q^T with v_mfma_f32_16x16x32: lane l gives row l % 16 of a
 //    16-key sub-tile of K (A) and its own query row l % 16 (B, held in
 //    registers for the whole kernel), dims 32 s + 8 (l / 16) .. + 7 of
@@ -38,6 +44,10 @@
 // a mask tensor a first kernel classifies every (mask row block, column
 // tile) once, so the attention reads mask elements only in MIXED tiles.
 #include <algorithm>
+#include <climits>
+#include <functional>
+#include <mutex>
+#include <vector>
 
 #include "kiv_common.h"
 #include "kiv_dispatch.h"
@@ -96,6 +106,402 @@ __device__ __forceinline__ float float_bias(const PrefillParams &p, int64_t o) {
 }
 
 // ---------------------------------------------------------------------------
+// Raw buffer of `bytes` bytes over one tile's rows, its base in SGPRs.  A
+// load whose offset is at or past `bytes` returns zeros without touching
+// memory.  Offsets stay below 2^31 (the host bounds the row strides).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t tile_rsrc(const char *base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<char *>(base), (short)0, (int)bytes, 0x00020000);
+}
+__device__ __forceinline__ uint4 buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t voff) {
+  typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+  const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r, (int)voff, 0, 0);
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+
+// Row groups of 16 query rows per wave: two up to head_dim 128 (each K and
+// V^T operand read from LDS then feeds two MFMAs, halving LDS and L2 traffic
+// per flop), one above (the accumulators would not fit twice).
+template <int KT> struct PfShape {
+  static constexpr int RG = KT <= 4 ? 2 : 1;
+  static constexpr int ROWS = 64 * RG;  // query rows per block
+};
+constexpr int kPfLdsTiles = 4096;  // tile classes a block keeps in LDS (hot windows up to 256K keys)
+
+// One block's share of the work: its query rows, its key tiles and their
+// classes, and the staging of K and V tiles through registers into LDS (K
+// rows [64][D] padded by 16 bytes, V transposed [D][64] padded by 8 bytes).
+template <int DT, int KT, int MK> struct PfBlock {
+  static constexpr int D = 32 * KT, CPR = D / 8, RG = PfShape<KT>::RG, NT = kPfThreads, ROWS = PfShape<KT>::ROWS;
+  static constexpr int KROW = D + 8;        // K tile row stride in elements
+  static constexpr int VROW = kPfKeys + 4;  // V^T tile row stride in elements
+  static constexpr int KTILE = kPfKeys * KROW, VTILE = D * VROW;  // elements of one LDS tile
+  static constexpr int KJ = (kPfKeys * CPR + NT - 1) / NT;          // K chunks per thread
+  static constexpr int VJ = ((kPfKeys / 4) * CPR + NT - 1) / NT;    // V key quads per thread
+  static_assert(ROWS % 64 == 0, "a block covers whole 64-row mask class entries");
+
+  const PrefillParams &p;
+  const uint8_t *tcls;  // LDS copy of this block's hot tile classes (mask tensors)
+  int b, h, kvh, z, tid, col, grp, q0, qlast, off, nct, nht, t_begin, t_end;
+  bool causal, cls_lds;
+  int qi[RG], qc[RG];  // the lane's query rows (rows past Q repeat row Q - 1's data)
+  const uint8_t *cls_rows;
+  int cls_n;
+  const char *cold_kb, *cold_vb, *hot_kb, *hot_vb;
+  uint4 kreg[KJ], vreg[VJ][4];
+
+  __device__ __forceinline__ PfBlock(const PrefillParams &pp, uint8_t *tcls_lds) : p(pp), tcls(tcls_lds) {
+    // One-dimensional grid, longest work first: row blocks from the last
+    // (under the causal rule later rows see more tiles), then batch rows,
+    // heads and key splits, so that the dispatcher hands out the block
+    // slots longest-first and the launch ends with short blocks.
+    const int per_rb = p.batch * p.hq * p.nsplit, lin = blockIdx.x;
+    const int nrb = gridDim.x / per_rb, rb = lin / per_rb, rem = lin - rb * per_rb;
+    const int bh = rem / p.nsplit;
+    z = rem - bh * p.nsplit;
+    b = bh / p.hq;
+    h = bh - b * p.hq;
+    kvh = h / (p.hq / p.hkv);
+    tid = threadIdx.x;
+    const int wave = tid >> 6, lane = tid & 63;
+    col = lane & 15;
+    grp = lane >> 4;
+    q0 = (nrb - 1 - rb) * ROWS;
+#pragma unroll
+    for (int g = 0; g < RG; ++g) {
+      qi[g] = q0 + 16 * (RG * wave + g) + col;
+      qc[g] = min(qi[g], p.qlen - 1);
+    }
+    qlast = min(q0 + ROWS, p.qlen) - 1;
+    off = p.hot_len - p.qlen;  // causal: hot column t visible to row i iff t <= i + off
+    causal = p.mask_kind == KIV_MASK_CAUSAL;
+    nct = (p.cold_len + kPfKeys - 1) / kPfKeys;
+    nht = (p.hot_len + kPfKeys - 1) / kPfKeys;
+    // This block's share of the tiles (all of them without key splits).
+    const int ntiles = nct + nht;
+    t_end = (int)((int64_t)(z + 1) * ntiles / p.nsplit);
+    t_begin = (int)((int64_t)z * ntiles / p.nsplit);
+    // Mask tensors: the classes of this block's rows (the 64-row entries it
+    // spans, combined), in LDS when they fit.
+    cls_rows = nullptr;
+    cls_n = 0;
+    cls_lds = false;
+    if constexpr (MK != PF_ARITH) {
+      const int mb = p.mask_b == 1 ? 0 : b, mh = p.mask_h == 1 ? 0 : h;
+      const int nqb = (p.qlen + 63) / 64, r0 = q0 / 64;
+      cls_n = min(ROWS / 64, nqb - r0);
+      cls_rows = p.tiles + ((int64_t)(mb * p.mask_h + mh) * nqb + r0) * nht;
+      cls_lds = nht <= kPfLdsTiles;
+      if (cls_lds) {
+        for (int k = tid; k < nht; k += NT) tcls_lds[k] = (uint8_t)combine(k);
+        __syncthreads();
+      }
+    }
+    cold_kb = p.cold_k + ((int64_t)b * p.hkv + kvh) * p.cold_len * (int64_t)D * 2;
+    cold_vb = p.cold_v + ((int64_t)b * p.hkv + kvh) * p.cold_len * (int64_t)D * 2;
+    hot_kb = p.hot_k + ((int64_t)b * p.hks0 + (int64_t)kvh * p.hks1) * 2;
+    hot_vb = p.hot_v + ((int64_t)b * p.hvs0 + (int64_t)kvh * p.hvs1) * 2;
+#pragma unroll
+    for (int j = 0; j < KJ; ++j) kreg[j] = make_uint4(0, 0, 0, 0);
+#pragma unroll
+    for (int j = 0; j < VJ; ++j)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) vreg[j][r] = make_uint4(0, 0, 0, 0);
+  }
+
+  __device__ __forceinline__ int combine(int k) const {
+    int c = cls_rows[k];
+    for (int r = 1; r < cls_n; ++r) {
+      const int d = cls_rows[(int64_t)r * nht + k];
+      c = c == d ? c : (c == TILE_SKIP && d == TILE_SKIP) ? TILE_SKIP : TILE_MIXED;
+    }
+    return c;
+  }
+  // Class of tile t for this block (uniform over the block).
+  __device__ __forceinline__ int tile_class(int t) const {
+    if (t < nct) return (t + 1) * kPfKeys <= p.cold_len ? TILE_FULL : TILE_MIXED;
+    const int key0 = (t - nct) * kPfKeys;
+    if constexpr (MK == PF_ARITH) {
+      const bool whole = key0 + kPfKeys <= p.hot_len;
+      if (!causal) return whole ? TILE_FULL : TILE_MIXED;
+      if (key0 > qlast + off) return TILE_SKIP;
+      return whole && key0 + kPfKeys - 1 <= q0 + off ? TILE_FULL : TILE_MIXED;
+    } else {
+      return __builtin_amdgcn_readfirstlane(cls_lds ? (int)tcls[t - nct] : combine(t - nct));
+    }
+  }
+  // The first tile after t that is not skipped, or t_end.
+  __device__ __forceinline__ int next_tile(int t) const {
+    for (++t; t < t_end; ++t) {
+      if constexpr (MK == PF_ARITH) {
+        // The causal rule hides every tile after the first hidden one.
+        if (causal && t >= nct && (t - nct) * kPfKeys > qlast + off) return t_end;
+      }
+      if (tile_class(t) != TILE_SKIP) return t;
+    }
+    return t_end;
+  }
+  __device__ __forceinline__ int first_tile() const {
+    return t_begin < t_end && tile_class(t_begin) != TILE_SKIP ? t_begin : next_tile(t_begin);
+  }
+
+  // Loads tile t's K chunks (V key quads) into registers through a buffer
+  // that ends at the segment's last row: rows past it read as zeros, and
+  // their scores get a -inf bias (a tile that is not whole is MIXED).
+  __device__ __forceinline__ void load_k(int t) {
+    const bool cold = t < nct;
+    const int key0 = (cold ? t : t - nct) * kPfKeys, rows = min(kPfKeys, (cold ? p.cold_len : p.hot_len) - key0);
+    const uint32_t krs = cold ? D * 2 : (uint32_t)p.hks2 * 2;
+    const auto rk = tile_rsrc((cold ? cold_kb : hot_kb) + (int64_t)key0 * krs, (uint32_t)rows * krs);
+#pragma unroll
+    for (int j = 0; j < KJ; ++j) {
+      const int i = tid + j * NT, key = i / CPR, c = i - key * CPR;
+      kreg[j] = buf_load16(rk, (uint32_t)key * krs + c * 16);
+    }
+  }
+  __device__ __forceinline__ void load_v(int t) {
+    const bool cold = t < nct;
+    const int key0 = (cold ? t : t - nct) * kPfKeys, rows = min(kPfKeys, (cold ? p.cold_len : p.hot_len) - key0);
+    const uint32_t vrs = cold ? D * 2 : (uint32_t)p.hvs2 * 2;
+    const auto rv = tile_rsrc((cold ? cold_vb : hot_vb) + (int64_t)key0 * vrs, (uint32_t)rows * vrs);
+#pragma unroll
+    for (int j = 0; j < VJ; ++j) {
+      const int i = tid + j * NT, quad = i % (kPfKeys / 4), c = i / (kPfKeys / 4);
+      if (VJ * NT == (kPfKeys / 4) * CPR || i < (kPfKeys / 4) * CPR) {
+        const uint32_t voff = (uint32_t)(4 * quad) * vrs + c * 16;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) vreg[j][r] = buf_load16(rv, voff + (uint32_t)r * vrs);
+      }
+    }
+  }
+  __device__ __forceinline__ void store_k(uint16_t *ks) const {
+#pragma unroll
+    for (int j = 0; j < KJ; ++j) {
+      const int i = tid + j * NT, key = i / CPR, c = i - key * CPR;
+      *reinterpret_cast<uint4 *>(&ks[key * KROW + c * 8]) = kreg[j];
+    }
+  }
+  __device__ __forceinline__ void store_v(uint16_t *vt) const {
+#pragma unroll
+    for (int j = 0; j < VJ; ++j) {
+      const int i = tid + j * NT, quad = i % (kPfKeys / 4), c = i / (kPfKeys / 4);
+      if (VJ * NT == (kPfKeys / 4) * CPR || i < (kPfKeys / 4) * CPR) {
+        const uint32_t w[4][4] = {{vreg[j][0].x, vreg[j][0].y, vreg[j][0].z, vreg[j][0].w},
+                                  {vreg[j][1].x, vreg[j][1].y, vreg[j][1].z, vreg[j][1].w},
+                                  {vreg[j][2].x, vreg[j][2].y, vreg[j][2].z, vreg[j][2].w},
+                                  {vreg[j][3].x, vreg[j][3].y, vreg[j][3].z, vreg[j][3].w}};
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+          // dims 2m (low halves) and 2m + 1 (high halves) of the four keys,
+          // one byte permute per pair (bytes 0-3 of the selector's table are
+          // the second operand, 4-7 the first)
+          const uint2 lo = make_uint2(__builtin_amdgcn_perm(w[1][m], w[0][m], 0x05040100u),
+                                      __builtin_amdgcn_perm(w[3][m], w[2][m], 0x05040100u));
+          const uint2 hi = make_uint2(__builtin_amdgcn_perm(w[1][m], w[0][m], 0x07060302u),
+                                      __builtin_amdgcn_perm(w[3][m], w[2][m], 0x07060302u));
+          *reinterpret_cast<uint2 *>(&vt[(c * 8 + 2 * m) * VROW + 4 * quad]) = lo;
+          *reinterpret_cast<uint2 *>(&vt[(c * 8 + 2 * m + 1) * VROW + 4 * quad]) = hi;
+        }
+      }
+    }
+  }
+
+  // The lane's query fragments: row qc[g], dims 32 st + 8 grp .. + 7 of step st.
+  __device__ __forceinline__ void load_q(uint4 (&qx)[RG][KT]) const {
+#pragma unroll
+    for (int g = 0; g < RG; ++g) {
+      const char *qrow = p.q + ((int64_t)b * p.qs0 + (int64_t)h * p.qs1 + (int64_t)qc[g] * p.qs2) * 2;
+#pragma unroll
+      for (int st = 0; st < KT; ++st) qx[g][st] = load16(qrow + (32 * st + 8 * grp) * 2);
+    }
+  }
+
+  // MIXED tile t: scores become s * scaling * log2 e + bias (base 2), so the
+  // tile's remaining factor is 1.
+  __device__ __forceinline__ void add_bias(f32x4_t (&s)[RG][4], int t) const {
+    const bool cold = t < nct;
+    const int key0 = (cold ? t : t - nct) * kPfKeys, n = (cold ? p.cold_len : p.hot_len) - key0;
+    // Mask element offsets: a per-lane part per row group plus a uniform part.
+    int64_t lane_mo[RG];
+#pragma unroll
+    for (int g = 0; g < RG; ++g) lane_mo[g] = (int64_t)qc[g] * p.ms2 + (int64_t)(4 * grp) * p.ms3;
+    const int64_t blk_mo = (int64_t)b * p.ms0 + (int64_t)h * p.ms1 + (int64_t)key0 * p.ms3;
+#pragma unroll
+    for (int g = 0; g < RG; ++g)
+#pragma unroll
+      for (int sub = 0; sub < 4; ++sub) {
+        const int k4 = 16 * sub + 4 * grp;  // first of the lane's four keys in the tile
+        const int64_t mo = blk_mo + (int64_t)(16 * sub) * p.ms3 + lane_mo[g];
+        float bias[4];
+        if (cold || MK == PF_ARITH) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const bool vis = k4 + i < n && (cold || !causal || key0 + k4 + i <= qc[g] + off);
+            bias[i] = vis ? 0.f : -INFINITY;
+          }
+        } else if (MK == PF_BOOL) {
+          uint32_t bits = 0;
+          if (p.mask_vec4 && k4 + 4 <= n) {
+            bits = *reinterpret_cast<const uint32_t *>(p.mask + mo);
+          } else {
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+              if (k4 + i < n && p.mask[mo + (int64_t)i * p.ms3]) bits |= 0xffu << (8 * i);
+          }
+#pragma unroll
+          for (int i = 0; i < 4; ++i) bias[i] = (bits >> (8 * i)) & 0xffu ? 0.f : -INFINITY;
+        } else {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) bias[i] = k4 + i < n ? float_bias(p, mo + (int64_t)i * p.ms3) : -INFINITY;
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) s[g][sub][i] = fmaf(s[g][sub][i], p.scale_log2, bias[i]);
+      }
+  }
+
+  // The block's rows: normalised output, or (with key splits) this split's
+  // unnormalised rows with their running max and row sum.
+  __device__ __forceinline__ void finish(const f32x4_t (&o)[RG][D / 16], const float (&m_run)[RG],
+                                         const float (&l_lane)[RG]) const {
+    if (p.nsplit > 1) {
+      const int64_t nrows = (int64_t)p.batch * p.qlen * p.hq;
+#pragma unroll
+      for (int g = 0; g < RG; ++g) {
+        const float l_row = half_wave_sum(row_pair_sum(l_lane[g]));
+        if (qi[g] >= p.qlen) continue;
+        const int64_t sr = (int64_t)z * nrows + ((int64_t)b * p.qlen + qi[g]) * p.hq + h;
+        float *po = p.ws_o + sr * D;
+#pragma unroll
+        for (int dt = 0; dt < D / 16; ++dt) *reinterpret_cast<f32x4_t *>(po + 16 * dt + 4 * grp) = o[g][dt];
+        if (grp == 0) {
+          p.ws_m[sr] = m_run[g];
+          p.ws_l[sr] = l_row;
+        }
+      }
+      return;
+    }
+#pragma unroll
+    for (int g = 0; g < RG; ++g) {
+      const float l_row = half_wave_sum(row_pair_sum(l_lane[g]));
+      if (qi[g] >= p.qlen) continue;
+      // A row with no visible key (fully masked) gets zeros.
+      const float inv = l_row > 0.f ? 1.f / l_row : 0.f;
+      char *orow = p.out + (((int64_t)b * p.qlen + qi[g]) * p.hq + h) * (int64_t)D * 2;
+#pragma unroll
+      for (int dt = 0; dt < D / 16; ++dt)
+        *reinterpret_cast<uint2 *>(orow + (16 * dt + 4 * grp) * 2) = make_uint2(
+            pack2<DT>(o[g][dt][0] * inv, o[g][dt][1] * inv), pack2<DT>(o[g][dt][2] * inv, o[g][dt][3] * inv));
+    }
+  }
+};
+
+// S^T = K Q^T for one tile with v_mfma_f32_16x16x32: lane l gives row l % 16
+// of a 16-key sub-tile of K (A) and its own query row l % 16 (B), dims
+// 32 st + 8 (l / 16) .. + 7 of step st, and receives keys 4 (l / 16) + i of
+// the sub-tile for its row.
+template <int DT, int KT, int RG>
+__device__ __forceinline__ void pf_scores(f32x4_t (&s)[RG][4], const uint16_t *ks, const uint4 (&qx)[RG][KT], int col,
+                                          int grp) {
+  constexpr int KROW = 32 * KT + 8;
+#pragma unroll
+  for (int g = 0; g < RG; ++g)
+#pragma unroll
+    for (int sub = 0; sub < 4; ++sub) s[g][sub] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int st = 0; st < KT; ++st)
+#pragma unroll
+    for (int sub = 0; sub < 4; ++sub) {
+      const uint4 a = *reinterpret_cast<const uint4 *>(&ks[(16 * sub + col) * KROW + 32 * st + 8 * grp]);
+#pragma unroll
+      for (int g = 0; g < RG; ++g) s[g][sub] = mfma_16x16x32<DT>(a, qx[g][st], s[g][sub]);
+    }
+}
+
+// Row maxima of one tile's scores in base-2 units (cc * s): the lane's 16
+// scores, then the four lanes that share the row (l, l ^ 16, l ^ 32, l ^ 48).
+template <int RG> __device__ __forceinline__ void pf_rowmax(const f32x4_t (&s)[RG][4], float cc, float (&mt)[RG]) {
+#pragma unroll
+  for (int g = 0; g < RG; ++g) {
+    float x = s[g][0][0];
+#pragma unroll
+    for (int sub = 0; sub < 4; ++sub)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) x = fmaxf(x, s[g][sub][i]);
+    mt[g] = half_wave_max(row_pair_max(x)) * cc;
+  }
+}
+
+// Raises a row's running max (and rescales its accumulators) only when the
+// tile's max is more than 2^kRescaleSlack above it, so probabilities stay
+// below 256 and most tiles skip the rescale; the wave skips it when no lane
+// needs it.
+template <int RG, int NO>
+__device__ __forceinline__ void pf_raise(const float (&mt)[RG], float (&m_run)[RG], float (&l_lane)[RG],
+                                         f32x4_t (&o)[RG][NO]) {
+  bool raise[RG], any_raise = false;
+#pragma unroll
+  for (int g = 0; g < RG; ++g) {
+    raise[g] = mt[g] > m_run[g] + kRescaleSlack;
+    any_raise |= raise[g];
+  }
+  if (__ballot(any_raise)) {
+#pragma unroll
+    for (int g = 0; g < RG; ++g) {
+      const float m_new = raise[g] ? mt[g] : m_run[g];
+      const float alpha = m_run[g] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m_run[g] - m_new);
+      l_lane[g] *= alpha;
+#pragma unroll
+      for (int dt = 0; dt < NO; ++dt) o[g][dt] *= alpha;
+      m_run[g] = m_new;
+    }
+  }
+}
+
+// Probabilities of one tile, 2^(cc s - m) rounded to the dtype and packed as
+// the B operand of O^T += V^T P^T: k index 8 g + i of pb[.][j] is key
+// 4 g + i of sub-tile 2 j for i < 4, of sub-tile 2 j + 1 for i >= 4.  The
+// lane's share of each row sum grows by their fp32 values.  A row that has
+// seen no key keeps m = -inf; its probabilities are 0.
+template <int DT, int RG>
+__device__ __forceinline__ void pf_probs(const f32x4_t (&s)[RG][4], float cc, const float (&m_run)[RG],
+                                         float (&l_lane)[RG], uint4 (&pb)[RG][2]) {
+#pragma unroll
+  for (int g = 0; g < RG; ++g) {
+    const float m_neg = m_run[g] == -INFINITY ? 0.f : -m_run[g];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      float e[8];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        e[i] = __builtin_amdgcn_exp2f(fmaf(s[g][2 * j][i], cc, m_neg));
+        e[4 + i] = __builtin_amdgcn_exp2f(fmaf(s[g][2 * j + 1][i], cc, m_neg));
+      }
+#pragma unroll
+      for (int i = 0; i < 8; ++i) l_lane[g] += e[i];
+      pb[g][j] = make_uint4(pack2<DT>(e[0], e[1]), pack2<DT>(e[2], e[3]), pack2<DT>(e[4], e[5]), pack2<DT>(e[6], e[7]));
+    }
+  }
+}
+
+// O^T += V^T P^T with v_mfma_f32_16x16x32 over 32 keys at a time: the A
+// operand holds the same keys of one dim from the V^T tile; every O^T entry
+// of a lane belongs to its query row.
+template <int DT, int D, int RG>
+__device__ __forceinline__ void pf_pv(f32x4_t (&o)[RG][D / 16], const uint4 (&pb)[RG][2], const uint16_t *vt, int col,
+                                      int grp) {
+  constexpr int VROW = kPfKeys + 4;
+#pragma unroll
+  for (int j = 0; j < 2; ++j)
+#pragma unroll
+    for (int dt = 0; dt < D / 16; ++dt) {
+      const uint16_t *vr = &vt[(16 * dt + col) * VROW + 32 * j + 4 * grp];
+      const uint2 lo = *reinterpret_cast<const uint2 *>(vr), hi = *reinterpret_cast<const uint2 *>(vr + 16);
+      const uint4 a = make_uint4(lo.x, lo.y, hi.x, hi.y);
+#pragma unroll
+      for (int g = 0; g < RG; ++g) o[g][dt] = mfma_16x16x32<DT>(a, pb[g][j], o[g][dt]);
+    }
+}
+
+// ---------------------------------------------------------------------------
 // Tile classes of a mask tensor: grid (column tiles, row blocks, Bm * Hm),
 // 256 threads; thread t covers row q0 + t / 4, columns 16 (t % 4) .. + 15 of
 // the tile.  Rows past Q do not count; columns past T make a tile MIXED.
@@ -146,346 +552,62 @@ __global__ void __launch_bounds__(kPfThreads) mask_tiles_kernel(PrefillParams p)
   }
 }
 
-// ---------------------------------------------------------------------------
-// Row groups of 16 query rows per wave: two up to head_dim 128 (each K and
-// V^T operand read from LDS then feeds two MFMAs, halving LDS and L2 traffic
-// per flop), one above (the accumulators would not fit twice).
-template <int KT> struct PfShape {
-  static constexpr int RG = KT <= 4 ? 2 : 1;
-  static constexpr int ROWS = 64 * RG;  // query rows per block
-};
-constexpr int kPfLdsTiles = 4096;  // tile classes a block keeps in LDS (hot windows up to 256K keys)
-
+// One tile at a time, every step in order: store the tile to LDS, scores,
+// softmax, PV.
 template <int DT, int KT, int MK>
 __global__ void __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(2)))
 prefill_attn_kernel(PrefillParams p) {
-  constexpr int D = 32 * KT, CPR = D / 8, RG = PfShape<KT>::RG, ROWS = PfShape<KT>::ROWS;
-  constexpr int KROW = D + 8;        // K tile row stride in elements
-  constexpr int VROW = kPfKeys + 4;  // V^T tile row stride in elements
-  constexpr int KJ = (kPfKeys * CPR + kPfThreads - 1) / kPfThreads;        // K chunks per thread
-  constexpr int VJ = ((kPfKeys / 4) * CPR + kPfThreads - 1) / kPfThreads;  // V key quads per thread
-  static_assert((kPfKeys * CPR) % kPfThreads == 0, "K tile items must fill the block");
-  __shared__ __align__(16) uint16_t ks[kPfKeys * KROW];
-  __shared__ __align__(16) uint16_t vt[D * VROW];
+  using Blk = PfBlock<DT, KT, MK>;
+  constexpr int RG = Blk::RG, D = Blk::D;
+  __shared__ __align__(16) uint16_t ks[Blk::KTILE];
+  __shared__ __align__(16) uint16_t vt[Blk::VTILE];
   __shared__ uint8_t tcls[MK == PF_ARITH ? 1 : kPfLdsTiles];
-  const int bh = blockIdx.y, b = bh / p.hq, h = bh - b * p.hq, kvh = h / (p.hq / p.hkv);
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, col = lane & 15, grp = lane >> 4;
-  // Row blocks in reverse: under the causal rule later rows see more tiles,
-  // and starting the longest blocks first shortens the tail of the launch.
-  const int qb = gridDim.x - 1 - blockIdx.x, q0 = qb * ROWS;
-  int qi[RG], qc[RG];  // the lane's query rows (rows past Q repeat row Q - 1's data)
-#pragma unroll
-  for (int g = 0; g < RG; ++g) {
-    qi[g] = q0 + 16 * (RG * wave + g) + col;
-    qc[g] = min(qi[g], p.qlen - 1);
-  }
-  const int qlast = min(q0 + ROWS, p.qlen) - 1;
-  const int off = p.hot_len - p.qlen;  // causal: hot column t visible to row i iff t <= i + off
-  const bool causal = p.mask_kind == KIV_MASK_CAUSAL;
-  const int nct = (p.cold_len + kPfKeys - 1) / kPfKeys, nht = (p.hot_len + kPfKeys - 1) / kPfKeys;
-  const int ntiles = nct + nht;
-  // This block's share of the tiles (all of them without key splits).
-  const int z = blockIdx.z;
-  const int t_end = (int)((int64_t)(z + 1) * ntiles / p.nsplit);
-  const int t_begin = (int)((int64_t)z * ntiles / p.nsplit);
-  // Mask tensors: the classes of this block's rows (the 64-row entries it
-  // spans, combined), in LDS when they fit.
-  const uint8_t *cls_rows = nullptr;
-  int cls_n = 0;
-  bool cls_lds = false;
-  if constexpr (MK != PF_ARITH) {
-    const int mb = p.mask_b == 1 ? 0 : b, mh = p.mask_h == 1 ? 0 : h;
-    const int nqb = (p.qlen + 63) / 64, r0 = q0 / 64;
-    cls_n = min(RG, nqb - r0);
-    cls_rows = p.tiles + ((int64_t)(mb * p.mask_h + mh) * nqb + r0) * nht;
-    cls_lds = nht <= kPfLdsTiles;
-  }
-  auto combine = [&](int k) -> int {
-    int c = cls_rows[k];
-    for (int r = 1; r < cls_n; ++r) {
-      const int d = cls_rows[(int64_t)r * nht + k];
-      c = c == d ? c : (c == TILE_SKIP && d == TILE_SKIP) ? TILE_SKIP : TILE_MIXED;
-    }
-    return c;
-  };
-  if constexpr (MK != PF_ARITH) {
-    if (cls_lds) {
-      for (int k = tid; k < nht; k += kPfThreads) tcls[k] = (uint8_t)combine(k);
-      __syncthreads();
-    }
-  }
-  // Class of tile t for this block (uniform over the block).
-  auto tile_class = [&](int t) -> int {
-    if (t < nct) return (t + 1) * kPfKeys <= p.cold_len ? TILE_FULL : TILE_MIXED;
-    const int key0 = (t - nct) * kPfKeys;
-    if constexpr (MK == PF_ARITH) {
-      const bool whole = key0 + kPfKeys <= p.hot_len;
-      if (!causal) return whole ? TILE_FULL : TILE_MIXED;
-      if (key0 > qlast + off) return TILE_SKIP;
-      return whole && key0 + kPfKeys - 1 <= q0 + off ? TILE_FULL : TILE_MIXED;
-    } else {
-      return cls_lds ? (int)tcls[t - nct] : combine(t - nct);
-    }
-  };
-  auto next_tile = [&](int t) -> int {
-    for (++t; t < t_end; ++t) {
-      if constexpr (MK == PF_ARITH) {
-        // The causal rule hides every tile after the first hidden one.
-        if (causal && t >= nct && (t - nct) * kPfKeys > qlast + off) return t_end;
-      }
-      if (tile_class(t) != TILE_SKIP) return t;
-    }
-    return t_end;
-  };
-  const char *cold_kb = p.cold_k + ((int64_t)b * p.hkv + kvh) * p.cold_len * (int64_t)D * 2;
-  const char *cold_vb = p.cold_v + ((int64_t)b * p.hkv + kvh) * p.cold_len * (int64_t)D * 2;
-  const char *hot_kb = p.hot_k + ((int64_t)b * p.hks0 + (int64_t)kvh * p.hks1) * 2;
-  const char *hot_vb = p.hot_v + ((int64_t)b * p.hvs0 + (int64_t)kvh * p.hvs1) * 2;
-  uint4 kreg[KJ], vreg[VJ][4];
-  // Loads tile t's K chunks and V key quads into registers.  Rows past the
-  // segment's end repeat its last row: their scores get a -inf bias, so the
-  // finite duplicates contribute exactly nothing.
-  auto load_tile = [&](int t) {
-    const bool cold = t < nct;
-    const int key0 = (cold ? t : t - nct) * kPfKeys, last = (cold ? p.cold_len : p.hot_len) - key0 - 1;
-    const uint32_t krs = cold ? D * 2 : (uint32_t)p.hks2 * 2, vrs = cold ? D * 2 : (uint32_t)p.hvs2 * 2;
-    const char *kb = (cold ? cold_kb : hot_kb) + (int64_t)key0 * krs;
-    const char *vb = (cold ? cold_vb : hot_vb) + (int64_t)key0 * vrs;
-    if (last >= kPfKeys - 1 && kPfThreads % CPR == 0) {
-      // Whole tile: one 32-bit offset per thread, then uniform steps of
-      // (threads / CPR) rows for K and of one row for V.
-      const uint32_t koff = (uint32_t)(tid / CPR) * krs + (tid % CPR) * 16;
-#pragma unroll
-      for (int j = 0; j < KJ; ++j) kreg[j] = load16(kb + koff + (uint32_t)(j * (kPfThreads / CPR)) * krs);
-#pragma unroll
-      for (int j = 0; j < VJ; ++j) {
-        const int i = tid + j * kPfThreads, quad = i % (kPfKeys / 4), c = i / (kPfKeys / 4);
-        if (i < (kPfKeys / 4) * CPR) {
-          const uint32_t voff = (uint32_t)(4 * quad) * vrs + c * 16;
-#pragma unroll
-          for (int r = 0; r < 4; ++r) vreg[j][r] = load16(vb + voff + (uint32_t)r * vrs);
-        }
-      }
-      return;
-    }
-#pragma unroll
-    for (int j = 0; j < KJ; ++j) {
-      const int i = tid + j * kPfThreads, key = i / CPR, c = i - key * CPR;
-      kreg[j] = load16(kb + ((uint32_t)min(key, last) * krs + c * 16));
-    }
-#pragma unroll
-    for (int j = 0; j < VJ; ++j) {
-      const int i = tid + j * kPfThreads, quad = i % (kPfKeys / 4), c = i / (kPfKeys / 4);
-      if (i < (kPfKeys / 4) * CPR) {
-#pragma unroll
-        for (int r = 0; r < 4; ++r) vreg[j][r] = load16(vb + ((uint32_t)min(4 * quad + r, last) * vrs + c * 16));
-      }
-    }
-  };
-  auto store_tile = [&]() {
-#pragma unroll
-    for (int j = 0; j < KJ; ++j) {
-      const int i = tid + j * kPfThreads, key = i / CPR, c = i - key * CPR;
-      *reinterpret_cast<uint4 *>(&ks[key * KROW + c * 8]) = kreg[j];
-    }
-#pragma unroll
-    for (int j = 0; j < VJ; ++j) {
-      const int i = tid + j * kPfThreads, quad = i % (kPfKeys / 4), c = i / (kPfKeys / 4);
-      if (i < (kPfKeys / 4) * CPR) {
-        const uint32_t w[4][4] = {{vreg[j][0].x, vreg[j][0].y, vreg[j][0].z, vreg[j][0].w},
-                                  {vreg[j][1].x, vreg[j][1].y, vreg[j][1].z, vreg[j][1].w},
-                                  {vreg[j][2].x, vreg[j][2].y, vreg[j][2].z, vreg[j][2].w},
-                                  {vreg[j][3].x, vreg[j][3].y, vreg[j][3].z, vreg[j][3].w}};
-#pragma unroll
-        for (int m = 0; m < 4; ++m) {
-          // dims 2m (low halves) and 2m + 1 (high halves) of the four keys,
-          // one byte permute per pair (bytes 0-3 of the selector's table are
-          // the second operand, 4-7 the first)
-          const uint2 lo = make_uint2(__builtin_amdgcn_perm(w[1][m], w[0][m], 0x05040100u),
-                                      __builtin_amdgcn_perm(w[3][m], w[2][m], 0x05040100u));
-          const uint2 hi = make_uint2(__builtin_amdgcn_perm(w[1][m], w[0][m], 0x07060302u),
-                                      __builtin_amdgcn_perm(w[3][m], w[2][m], 0x07060302u));
-          *reinterpret_cast<uint2 *>(&vt[(c * 8 + 2 * m) * VROW + 4 * quad]) = lo;
-          *reinterpret_cast<uint2 *>(&vt[(c * 8 + 2 * m + 1) * VROW + 4 * quad]) = hi;
-        }
-      }
-    }
-  };
-
+  Blk blk(p, tcls);
   uint4 qx[RG][KT];
-#pragma unroll
-  for (int g = 0; g < RG; ++g) {
-    const char *qrow = p.q + ((int64_t)b * p.qs0 + (int64_t)h * p.qs1 + (int64_t)qc[g] * p.qs2) * 2;
-#pragma unroll
-    for (int st = 0; st < KT; ++st) qx[g][st] = load16(qrow + (32 * st + 8 * grp) * 2);
-  }
+  blk.load_q(qx);
   f32x4_t o[RG][D / 16];
-#pragma unroll
-  for (int g = 0; g < RG; ++g)
-#pragma unroll
-    for (int dt = 0; dt < D / 16; ++dt) o[g][dt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
   float m_run[RG], l_lane[RG];  // l_lane: this lane's share of the row sum
 #pragma unroll
   for (int g = 0; g < RG; ++g) {
+#pragma unroll
+    for (int dt = 0; dt < D / 16; ++dt) o[g][dt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
     m_run[g] = -INFINITY;
     l_lane[g] = 0.f;
   }
-
-  int t = t_begin < t_end && tile_class(t_begin) != TILE_SKIP ? t_begin : next_tile(t_begin);
-  if (t < t_end) load_tile(t);
-  while (t < t_end) {
-    const int cls = tile_class(t), tn = next_tile(t);
+  int t = blk.first_tile();
+  if (t < blk.t_end) {
+    blk.load_k(t);
+    blk.load_v(t);
+  }
+  while (t < blk.t_end) {
+    const int cls = blk.tile_class(t), tn = blk.next_tile(t);
     __syncthreads();  // the previous tile's reads of ks / vt are done
-    store_tile();
+    blk.store_k(ks);
+    blk.store_v(vt);
     __syncthreads();
-    if (tn < t_end) load_tile(tn);
+    if (tn < blk.t_end) {
+      blk.load_k(tn);
+      blk.load_v(tn);
+    }
     // Scores in base-2 units are cc * s: FULL tiles keep the raw dot products
     // (cc = scaling * log2 e, folded into the exponent), MIXED tiles add the
     // bias first (cc = 1).
-    f32x4_t acc[RG][4];
-#pragma unroll
-    for (int g = 0; g < RG; ++g)
-#pragma unroll
-      for (int sub = 0; sub < 4; ++sub) acc[g][sub] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int st = 0; st < KT; ++st)
-#pragma unroll
-      for (int sub = 0; sub < 4; ++sub) {
-        const uint4 a = *reinterpret_cast<const uint4 *>(&ks[(16 * sub + col) * KROW + 32 * st + 8 * grp]);
-#pragma unroll
-        for (int g = 0; g < RG; ++g) acc[g][sub] = mfma_16x16x32<DT>(a, qx[g][st], acc[g][sub]);
-      }
-    float s[RG][4][4];
+    f32x4_t s[RG][4];
+    pf_scores<DT, KT, RG>(s, ks, qx, blk.col, blk.grp);
     float cc = p.scale_log2;
-#pragma unroll
-    for (int g = 0; g < RG; ++g)
-#pragma unroll
-      for (int sub = 0; sub < 4; ++sub)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) s[g][sub][i] = acc[g][sub][i];
     if (cls == TILE_MIXED) {
+      blk.add_bias(s, t);
       cc = 1.f;
-      const bool cold = t < nct;
-      const int key0 = (cold ? t : t - nct) * kPfKeys, n = (cold ? p.cold_len : p.hot_len) - key0;
-#pragma unroll
-      for (int g = 0; g < RG; ++g)
-#pragma unroll
-        for (int sub = 0; sub < 4; ++sub) {
-          const int k4 = 16 * sub + 4 * grp;  // first of the lane's four keys in the tile
-          float bias[4];
-          if (cold || MK == PF_ARITH) {
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-              const bool vis = k4 + i < n && (cold || !causal || key0 + k4 + i <= qc[g] + off);
-              bias[i] = vis ? 0.f : -INFINITY;
-            }
-          } else if (MK == PF_BOOL) {
-            const int64_t mo = mask_off(p, b, h, qc[g], key0 + k4);
-            uint32_t bits = 0;
-            if (p.mask_vec4 && k4 + 4 <= n) {
-              bits = *reinterpret_cast<const uint32_t *>(p.mask + mo);
-            } else {
-#pragma unroll
-              for (int i = 0; i < 4; ++i)
-                if (k4 + i < n && p.mask[mo + (int64_t)i * p.ms3]) bits |= 0xffu << (8 * i);
-            }
-#pragma unroll
-            for (int i = 0; i < 4; ++i) bias[i] = (bits >> (8 * i)) & 0xffu ? 0.f : -INFINITY;
-          } else {
-            const int64_t mo = mask_off(p, b, h, qc[g], key0 + k4);
-#pragma unroll
-            for (int i = 0; i < 4; ++i) bias[i] = k4 + i < n ? float_bias(p, mo + (int64_t)i * p.ms3) : -INFINITY;
-          }
-#pragma unroll
-          for (int i = 0; i < 4; ++i) s[g][sub][i] = fmaf(s[g][sub][i], p.scale_log2, bias[i]);
-        }
     }
-    // Raise a row's running max (and rescale) only when a score is more than
-    // 2^kRescaleSlack above it; the wave skips the rescale when no lane needs it.
-    bool raise[RG], any_raise = false;
     float mt[RG];
-#pragma unroll
-    for (int g = 0; g < RG; ++g) {
-      float x = s[g][0][0];
-#pragma unroll
-      for (int sub = 0; sub < 4; ++sub)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) x = fmaxf(x, s[g][sub][i]);
-      mt[g] = half_wave_max(row_pair_max(x)) * cc;
-      raise[g] = mt[g] > m_run[g] + kRescaleSlack;
-      any_raise |= raise[g];
-    }
-    if (__ballot(any_raise)) {
-#pragma unroll
-      for (int g = 0; g < RG; ++g) {
-        const float m_new = raise[g] ? mt[g] : m_run[g];
-        const float alpha = m_run[g] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m_run[g] - m_new);
-        l_lane[g] *= alpha;
-#pragma unroll
-        for (int dt = 0; dt < D / 16; ++dt) o[g][dt] *= alpha;
-        m_run[g] = m_new;
-      }
-    }
+    pf_rowmax<RG>(s, cc, mt);
+    pf_raise<RG, D / 16>(mt, m_run, l_lane, o);
     uint4 pb[RG][2];
-#pragma unroll
-    for (int g = 0; g < RG; ++g) {
-      // A row that has seen no key keeps m = -inf; its probabilities are 0.
-      const float m_neg = m_run[g] == -INFINITY ? 0.f : -m_run[g];
-#pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        float e[8];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          e[i] = __builtin_amdgcn_exp2f(fmaf(s[g][2 * j][i], cc, m_neg));
-          e[4 + i] = __builtin_amdgcn_exp2f(fmaf(s[g][2 * j + 1][i], cc, m_neg));
-        }
-#pragma unroll
-        for (int i = 0; i < 8; ++i) l_lane[g] += e[i];
-        pb[g][j] =
-            make_uint4(pack2<DT>(e[0], e[1]), pack2<DT>(e[2], e[3]), pack2<DT>(e[4], e[5]), pack2<DT>(e[6], e[7]));
-      }
-    }
-#pragma unroll
-    for (int j = 0; j < 2; ++j)
-#pragma unroll
-      for (int dt = 0; dt < D / 16; ++dt) {
-        const uint16_t *vr = &vt[(16 * dt + col) * VROW + 32 * j + 4 * grp];
-        const uint2 lo = *reinterpret_cast<const uint2 *>(vr), hi = *reinterpret_cast<const uint2 *>(vr + 16);
-        const uint4 a = make_uint4(lo.x, lo.y, hi.x, hi.y);
-#pragma unroll
-        for (int g = 0; g < RG; ++g) o[g][dt] = mfma_16x16x32<DT>(a, pb[g][j], o[g][dt]);
-      }
+    pf_probs<DT, RG>(s, cc, m_run, l_lane, pb);
+    pf_pv<DT, D, RG>(o, pb, vt, blk.col, blk.grp);
     t = tn;
   }
-  if (p.nsplit > 1) {
-    const int64_t nrows = (int64_t)p.batch * p.qlen * p.hq;
-#pragma unroll
-    for (int g = 0; g < RG; ++g) {
-      const float l_row = half_wave_sum(row_pair_sum(l_lane[g]));
-      if (qi[g] >= p.qlen) continue;
-      const int64_t sr = (int64_t)z * nrows + ((int64_t)b * p.qlen + qi[g]) * p.hq + h;
-      float *po = p.ws_o + sr * D;
-#pragma unroll
-      for (int dt = 0; dt < D / 16; ++dt) *reinterpret_cast<f32x4_t *>(po + 16 * dt + 4 * grp) = o[g][dt];
-      if (grp == 0) {
-        p.ws_m[sr] = m_run[g];
-        p.ws_l[sr] = l_row;
-      }
-    }
-    return;
-  }
-#pragma unroll
-  for (int g = 0; g < RG; ++g) {
-    const float l_row = half_wave_sum(row_pair_sum(l_lane[g]));
-    if (qi[g] >= p.qlen) continue;
-    // A row with no visible key (fully masked) gets zeros.
-    const float inv = l_row > 0.f ? 1.f / l_row : 0.f;
-    char *orow = p.out + (((int64_t)b * p.qlen + qi[g]) * p.hq + h) * (int64_t)D * 2;
-#pragma unroll
-    for (int dt = 0; dt < D / 16; ++dt)
-      *reinterpret_cast<uint2 *>(orow + (16 * dt + 4 * grp) * 2) = make_uint2(
-          pack2<DT>(o[g][dt][0] * inv, o[g][dt][1] * inv), pack2<DT>(o[g][dt][2] * inv, o[g][dt][3] * inv));
-  }
+  blk.finish(o, m_run, l_lane);
 }
 
 // Merges the key splits: out = sum_s 2^(m_s - M) o_s / sum_s 2^(m_s - M) l_s
@@ -519,14 +641,76 @@ __global__ void __launch_bounds__(kPfThreads) prefill_combine_kernel(PrefillPara
 
 static int64_t div_up(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
-// Key splits for a launch of `blocks` blocks over `tiles` key tiles: enough
-// blocks to fill the chip (about 1024), at least two tiles per split, at
-// most 64 splits.
-static int prefill_splits(int64_t blocks, int64_t tiles) {
-  if (blocks >= 512) return 1;
-  const int64_t want = div_up(1024, blocks), most = std::max<int64_t>(1, tiles / 2);
-  return (int)std::max<int64_t>(1, std::min<int64_t>({want, most, 64}));
+// Key splits: the count (1 to 8) whose longest-first schedule ends first.
+// The units of work are (row block, batch row * head, split); a unit's cost
+// is its key tiles plus a fixed 2 tiles (prologue and epilogue), and the
+// units go, longest first, to whichever of the GPU's `slots` block slots
+// frees first (how the dispatcher hands out a grid in that order).  Under
+// the causal rule row block r sees the cold tiles and the hot tiles up to
+// its last row; otherwise every tile.
+static int prefill_splits_search(int Q, int rows, int BH, int cold_len, int hot_len, bool causal, int slots) {
+  const int nrb = (int)div_up(Q, rows), nct = (int)div_up(cold_len, kPfKeys), nht = (int)div_up(hot_len, kPfKeys);
+  std::vector<int> len(nrb);  // tiles of row block r, r = 0 first in the grid (the last rows)
+  for (int r = 0; r < nrb; ++r) {
+    const int q0 = (nrb - 1 - r) * rows, qlast = std::min(q0 + rows, Q) - 1;
+    int hot = nht;
+    if (causal) {
+      const int64_t lastkey = (int64_t)qlast + hot_len - Q;  // the row's last visible hot column
+      hot = lastkey < 0 ? 0 : (int)std::min<int64_t>(nht, lastkey / kPfKeys + 1);
+    }
+    len[r] = nct + hot;
+  }
+  int best = 1;
+  int64_t best_end = INT64_MAX;
+  std::vector<int64_t> heap;
+  for (int ns = 1; ns <= 8; ++ns) {
+    heap.assign(slots, 0);
+    for (int r = 0; r < nrb; ++r)
+      for (int u = 0; u < BH; ++u)
+        for (int z = 0; z < ns; ++z) {
+          const int64_t cost = (int64_t)len[r] * (z + 1) / ns - (int64_t)len[r] * z / ns + 2;
+          std::pop_heap(heap.begin(), heap.end(), std::greater<int64_t>());
+          heap.back() += cost;
+          std::push_heap(heap.begin(), heap.end(), std::greater<int64_t>());
+        }
+    const int64_t end = *std::max_element(heap.begin(), heap.end());
+    if (end < best_end) {
+      best_end = end;
+      best = ns;
+    }
+  }
+  return best;
 }
+
+// The search above, remembered for the last few shapes (every layer of a
+// model repeats the same ones).
+static int prefill_splits(int Q, int rows, int BH, int cold_len, int hot_len, bool causal, int slots) {
+  if ((int64_t)div_up(Q, rows) * BH >= 2 * (int64_t)slots) return 1;
+  struct Entry {
+    int key[7];
+    int ns;
+  };
+  static std::mutex mu;
+  static Entry memo[8];
+  static int used = 0, next = 0;
+  const int key[7] = {Q, rows, BH, cold_len, hot_len, causal ? 1 : 0, slots};
+  {
+    std::lock_guard<std::mutex> lock(mu);
+    for (int i = 0; i < used; ++i)
+      if (std::equal(key, key + 7, memo[i].key)) return memo[i].ns;
+  }
+  const int ns = prefill_splits_search(Q, rows, BH, cold_len, hot_len, causal, slots);
+  std::lock_guard<std::mutex> lock(mu);
+  Entry &e = memo[next];
+  std::copy(key, key + 7, e.key);
+  e.ns = ns;
+  next = (next + 1) % 8;
+  used = std::min(used + 1, 8);
+  return ns;
+}
+
+// Block slots of the attention kernel: two blocks per compute unit.
+static int prefill_slots() { return 2 * device_cu_count(); }
 
 struct PrefillWorkspace {
   size_t tiles_bytes, m_off, l_off, o_off, total;
@@ -534,11 +718,9 @@ struct PrefillWorkspace {
 };
 
 static PrefillWorkspace prefill_workspace(int B, int hq, int D, int Q, int cold_len, int hot_len, int mask_b,
-                                          int mask_h) {
+                                          int mask_h, int nsplit) {
   PrefillWorkspace w;
-  const int rows = D <= 128 ? 128 : 64;  // query rows per block (PfShape)
-  const int64_t ntiles = div_up(cold_len, kPfKeys) + div_up(hot_len, kPfKeys);
-  w.nsplit = prefill_splits(div_up(Q, rows) * B * hq, ntiles);
+  w.nsplit = nsplit;
   w.tiles_bytes = hot_len > 0 ? (size_t)mask_b * mask_h * div_up(Q, kPfRows) * div_up(hot_len, kPfKeys) : 0;
   const size_t nrows = (size_t)B * Q * hq;
   w.m_off = (w.tiles_bytes + 255) & ~size_t(255);
@@ -547,6 +729,8 @@ static PrefillWorkspace prefill_workspace(int B, int hq, int D, int Q, int cold_
   w.total = w.nsplit > 1 ? w.o_off + nrows * w.nsplit * D * 4 : w.tiles_bytes;
   return w;
 }
+
+static int prefill_rows(int D) { return D <= 128 ? 128 : 64; }  // query rows per block (PfShape)
 
 }  // namespace kiv
 
@@ -557,7 +741,11 @@ extern "C" {
 size_t kiv_prefill_workspace_size(int32_t batch, int32_t num_q_heads, int32_t head_dim, int32_t q_len,
                                   int32_t cold_len, int32_t hot_len) {
   if (batch < 1 || num_q_heads < 1 || head_dim < 1 || q_len < 1 || cold_len < 0 || hot_len < 0) return 0;
-  return prefill_workspace(batch, num_q_heads, head_dim, q_len, cold_len, hot_len, batch, num_q_heads).total;
+  // Enough for either choice of splits (with or without the causal rule).
+  const int rows = prefill_rows(head_dim), slots = prefill_slots(), BH = batch * num_q_heads;
+  const int ns = std::max(prefill_splits(q_len, rows, BH, cold_len, hot_len, true, slots),
+                          prefill_splits(q_len, rows, BH, cold_len, hot_len, false, slots));
+  return prefill_workspace(batch, num_q_heads, head_dim, q_len, cold_len, hot_len, batch, num_q_heads, ns).total;
 }
 
 int kiv_prefill_attention(const kiv_attention_args_t *a, kiv_stream_t stream) {
@@ -632,8 +820,12 @@ int kiv_prefill_attention(const kiv_attention_args_t *a, kiv_stream_t stream) {
   p.out = (char *)a->out;
   hipStream_t st = (hipStream_t)stream;
   const int mode = mk == KIV_MASK_BOOL ? PF_BOOL : (mk == KIV_MASK_NONE || mk == KIV_MASK_CAUSAL) ? PF_ARITH : PF_FLOAT;
+  // Splits as if the mask were the causal rule when it is one or a tensor
+  // (the model's masks are causal); the workspace size covers both choices.
+  const int nsplit = prefill_splits(Q, prefill_rows(D), B * hq, a->cold_len, a->hot_len, mk != KIV_MASK_NONE,
+                                    prefill_slots());
   const PrefillWorkspace w = prefill_workspace(B, hq, D, Q, a->cold_len, a->hot_len,
-                                               mode != PF_ARITH ? p.mask_b : 0, mode != PF_ARITH ? p.mask_h : 0);
+                                               mode != PF_ARITH ? p.mask_b : 0, mode != PF_ARITH ? p.mask_h : 0, nsplit);
   p.nsplit = w.nsplit;
   p.ws_m = p.ws_l = p.ws_o = nullptr;
   if (w.total > 0 && (!a->workspace || a->workspace_bytes < w.total || ((uintptr_t)a->workspace & 255)))
@@ -657,10 +849,12 @@ int kiv_prefill_attention(const kiv_attention_args_t *a, kiv_stream_t stream) {
     if constexpr (KTV == 16) {
       return (int)fail(KIV_ERR_UNSUPPORTED, "%s: head_dim 512 unsupported", who);
     } else {
-      const dim3 grid((unsigned)div_up(Q, PfShape<KTV>::ROWS), (unsigned)(B * hq), (unsigned)p.nsplit);
+      const int64_t nblocks = div_up(Q, PfShape<KTV>::ROWS) * B * hq * p.nsplit;
+      if (nblocks > INT32_MAX) return (int)fail(KIV_ERR_UNSUPPORTED, "%s: too many query rows", who);
+      const dim3 grid((unsigned)nblocks);
       auto launch = [&](auto dtc, auto mkc) {
-        hipLaunchKernelGGL((prefill_attn_kernel<decltype(dtc)::value, KTV, decltype(mkc)::value>), grid,
-                           dim3(kPfThreads), 0, st, p);
+        constexpr int DTV = decltype(dtc)::value, MKV = decltype(mkc)::value;
+        hipLaunchKernelGGL((prefill_attn_kernel<DTV, KTV, MKV>), grid, dim3(kPfThreads), 0, st, p);
       };
       using std::integral_constant;
       auto by_mode = [&](auto dtc) {

@@ -48,6 +48,18 @@ size_t device_lds_limit() {
   return (size_t)v;
 }
 
+int device_cu_count() {
+  static std::atomic<int> cache[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  int v = cache[dev].load(std::memory_order_relaxed);
+  if (v == 0) {
+    if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || v <= 0) v = 256;
+    cache[dev].store(v, std::memory_order_relaxed);
+  }
+  return v;
+}
+
 int DevBuf::ensure(size_t need, hipStream_t stream, bool keep_contents) {
   if (need <= bytes) return KIV_OK;
   size_t nb = std::max(need, bytes + bytes / 2);
