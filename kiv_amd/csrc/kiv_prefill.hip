@@ -45,9 +45,6 @@
 // tile) once, so the attention reads mask elements only in MIXED tiles.
 #include <algorithm>
 #include <climits>
-#include <functional>
-#include <mutex>
-#include <vector>
 
 #include "kiv_common.h"
 #include "kiv_dispatch.h"
@@ -641,72 +638,17 @@ __global__ void __launch_bounds__(kPfThreads) prefill_combine_kernel(PrefillPara
 
 static int64_t div_up(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
-// Key splits: the count (1 to 8) whose longest-first schedule ends first.
-// The units of work are (row block, batch row * head, split); a unit's cost
-// is its key tiles plus a fixed 2 tiles (prologue and epilogue), and the
-// units go, longest first, to whichever of the GPU's `slots` block slots
-// frees first (how the dispatcher hands out a grid in that order).  Under
-// the causal rule row block r sees the cold tiles and the hot tiles up to
-// its last row; otherwise every tile.
-static int prefill_splits_search(int Q, int rows, int BH, int cold_len, int hot_len, bool causal, int slots) {
-  const int nrb = (int)div_up(Q, rows), nct = (int)div_up(cold_len, kPfKeys), nht = (int)div_up(hot_len, kPfKeys);
-  std::vector<int> len(nrb);  // tiles of row block r, r = 0 first in the grid (the last rows)
-  for (int r = 0; r < nrb; ++r) {
-    const int q0 = (nrb - 1 - r) * rows, qlast = std::min(q0 + rows, Q) - 1;
-    int hot = nht;
-    if (causal) {
-      const int64_t lastkey = (int64_t)qlast + hot_len - Q;  // the row's last visible hot column
-      hot = lastkey < 0 ? 0 : (int)std::min<int64_t>(nht, lastkey / kPfKeys + 1);
-    }
-    len[r] = nct + hot;
-  }
-  int best = 1;
-  int64_t best_end = INT64_MAX;
-  std::vector<int64_t> heap;
-  for (int ns = 1; ns <= 8; ++ns) {
-    heap.assign(slots, 0);
-    for (int r = 0; r < nrb; ++r)
-      for (int u = 0; u < BH; ++u)
-        for (int z = 0; z < ns; ++z) {
-          const int64_t cost = (int64_t)len[r] * (z + 1) / ns - (int64_t)len[r] * z / ns + 2;
-          std::pop_heap(heap.begin(), heap.end(), std::greater<int64_t>());
-          heap.back() += cost;
-          std::push_heap(heap.begin(), heap.end(), std::greater<int64_t>());
-        }
-    const int64_t end = *std::max_element(heap.begin(), heap.end());
-    if (end < best_end) {
-      best_end = end;
-      best = ns;
-    }
-  }
-  return best;
-}
-
-// The search above, remembered for the last few shapes (every layer of a
-// model repeats the same ones).
-static int prefill_splits(int Q, int rows, int BH, int cold_len, int hot_len, bool causal, int slots) {
-  if ((int64_t)div_up(Q, rows) * BH >= 2 * (int64_t)slots) return 1;
-  struct Entry {
-    int key[7];
-    int ns;
-  };
-  static std::mutex mu;
-  static Entry memo[8];
-  static int used = 0, next = 0;
-  const int key[7] = {Q, rows, BH, cold_len, hot_len, causal ? 1 : 0, slots};
-  {
-    std::lock_guard<std::mutex> lock(mu);
-    for (int i = 0; i < used; ++i)
-      if (std::equal(key, key + 7, memo[i].key)) return memo[i].ns;
-  }
-  const int ns = prefill_splits_search(Q, rows, BH, cold_len, hot_len, causal, slots);
-  std::lock_guard<std::mutex> lock(mu);
-  Entry &e = memo[next];
-  std::copy(key, key + 7, e.key);
-  e.ns = ns;
-  next = (next + 1) % 8;
-  used = std::min(used + 1, 8);
-  return ns;
+// Key splits: enough (row block, batch row * head, split) units for about
+// two rounds of the GPU's block slots, at least two key tiles per split, at
+// most 8.  With the longest-first order a second round fills the slots the
+// short row blocks free; more splits only add partial rows to write and
+// merge (on the model's chunk, 4096 x 8192 keys with 12 heads: 3 splits 571,
+// 4 splits 523, 2 splits 537 TFLOP/s).
+static int prefill_splits(int Q, int rows, int BH, int cold_len, int hot_len, int slots) {
+  const int64_t units = div_up(Q, rows) * BH, tiles = div_up(cold_len, kPfKeys) + div_up(hot_len, kPfKeys);
+  if (units >= 2 * (int64_t)slots) return 1;
+  const int64_t want = div_up(2 * (int64_t)slots, units), most = std::max<int64_t>(1, tiles / 2);
+  return (int)std::max<int64_t>(1, std::min<int64_t>({want, most, 8}));
 }
 
 // Block slots of the attention kernel: two blocks per compute unit.
@@ -741,10 +683,7 @@ extern "C" {
 size_t kiv_prefill_workspace_size(int32_t batch, int32_t num_q_heads, int32_t head_dim, int32_t q_len,
                                   int32_t cold_len, int32_t hot_len) {
   if (batch < 1 || num_q_heads < 1 || head_dim < 1 || q_len < 1 || cold_len < 0 || hot_len < 0) return 0;
-  // Enough for either choice of splits (with or without the causal rule).
-  const int rows = prefill_rows(head_dim), slots = prefill_slots(), BH = batch * num_q_heads;
-  const int ns = std::max(prefill_splits(q_len, rows, BH, cold_len, hot_len, true, slots),
-                          prefill_splits(q_len, rows, BH, cold_len, hot_len, false, slots));
+  const int ns = prefill_splits(q_len, prefill_rows(head_dim), batch * num_q_heads, cold_len, hot_len, prefill_slots());
   return prefill_workspace(batch, num_q_heads, head_dim, q_len, cold_len, hot_len, batch, num_q_heads, ns).total;
 }
 
@@ -820,10 +759,7 @@ int kiv_prefill_attention(const kiv_attention_args_t *a, kiv_stream_t stream) {
   p.out = (char *)a->out;
   hipStream_t st = (hipStream_t)stream;
   const int mode = mk == KIV_MASK_BOOL ? PF_BOOL : (mk == KIV_MASK_NONE || mk == KIV_MASK_CAUSAL) ? PF_ARITH : PF_FLOAT;
-  // Splits as if the mask were the causal rule when it is one or a tensor
-  // (the model's masks are causal); the workspace size covers both choices.
-  const int nsplit = prefill_splits(Q, prefill_rows(D), B * hq, a->cold_len, a->hot_len, mk != KIV_MASK_NONE,
-                                    prefill_slots());
+  const int nsplit = prefill_splits(Q, prefill_rows(D), B * hq, a->cold_len, a->hot_len, prefill_slots());
   const PrefillWorkspace w = prefill_workspace(B, hq, D, Q, a->cold_len, a->hot_len,
                                                mode != PF_ARITH ? p.mask_b : 0, mode != PF_ARITH ? p.mask_h : 0, nsplit);
   p.nsplit = w.nsplit;
