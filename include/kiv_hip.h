@@ -299,8 +299,11 @@ int kiv_prefill_attention(const kiv_attention_args_t *args, kiv_stream_t stream)
 /* Workspace bytes kiv_prefill_attention needs for this shape (0: none): one
  * byte per 64 x 64 tile of query rows x hot columns per batch and q head for
  * a mask tensor's tile classes, plus fp32 partial rows when the keys are
- * split across blocks (queries too short to fill the GPU).  The workspace
- * must be 256-byte aligned. */
+ * split across blocks (when the blocks of query rows are fewer than two
+ * rounds of the GPU's block slots; the model's 4096-position chunks are
+ * split in 3).  The split count depends on the current device's compute
+ * units: query the size with the device of the call current.  The
+ * workspace must be 256-byte aligned. */
 size_t kiv_prefill_workspace_size(int32_t batch, int32_t num_q_heads, int32_t head_dim, int32_t q_len,
                                   int32_t cold_len, int32_t hot_len);
 
