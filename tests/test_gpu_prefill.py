@@ -171,6 +171,46 @@ def test_prefill_attention_fully_masked_rows_are_zero(cuda):
     assert torch.equal(out[:, keep], ref_out)
 
 
+def test_prefill_attention_model_chunk_full_size(cuda):
+    """The whole-model run's chunk shape at full size: 4096 query positions
+    over 8192 hot keys (hot cap 4096 + chunk 4096), 12 q / 2 kv heads, head
+    dim 128, bf16, the model's boolean causal mask.  This is the launch the
+    longest-first grid splits over key ranges and merges (3 splits on a
+    256-CU GPU).  The fp64 reference runs on the GPU, one head at a time, and
+    the bar is the module's."""
+    B, hq, hkv, D, Q, T = 1, 12, 2, 128, 4096, 8192
+    dt = torch.bfloat16
+    gen = torch.Generator(device=cuda).manual_seed(4096)
+    q = torch.randn(B, hq, Q, D, generator=gen, device=cuda).to(dt)
+    hot_k = torch.randn(B, hkv, T, D, generator=gen, device=cuda).to(dt)
+    hot_v = torch.randn(B, hkv, T, D, generator=gen, device=cuda).to(dt)
+    vis = torch.from_numpy(causal_bias(Q, T) == 0)[None, None].to(cuda)
+    scaling = D ** -0.5
+    out = prefill_attention(q, None, None, hot_k, hot_v, vis, scaling)
+    torch.cuda.synchronize()
+    assert out.shape == (B, Q, hq, D)
+    bias = torch.where(vis[0, 0], 0.0, float("-inf")).to(torch.float64)
+    worst = 0.0
+    for h in range(hq):
+        q64 = q[0, h].double()
+        k64 = hot_k[0, h // (hq // hkv)].double()
+        v64 = hot_v[0, h // (hq // hkv)].double()
+        s = q64 @ k64.t().contiguous() * scaling + bias
+        prob = torch.softmax(s, dim=-1)
+        ref = prob @ v64
+        wabs = prob @ v64.abs()
+        del s, prob
+        half_ulp = 0.5 * torch.from_numpy(
+            np.spacing(np.abs(ref.float().cpu().numpy())).astype(np.float64)).to(cuda) * ULP_SCALE[dt]
+        tol = 2e-3 + half_ulp + UNIT_ROUNDOFF[dt] * wabs
+        err = (out[0, :, h].double() - ref).abs()
+        assert torch.isfinite(out[0, :, h].float()).all()
+        excess = (err - tol).max().item()
+        worst = max(worst, err.max().item())
+        assert excess <= 0, f"head {h}: max-abs error {err.max().item()} (excess over bound {excess})"
+    print(f"model chunk 4096 x 8192: max-abs error {worst:.3e}", flush=True)
+
+
 def test_prefill_attention_rejects_bad_arguments(cuda):
     dt = torch.bfloat16
     q = torch.zeros(1, 4, 8, 80, dtype=dt, device=cuda)
