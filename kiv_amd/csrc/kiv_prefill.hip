@@ -499,53 +499,94 @@ __device__ __forceinline__ void pf_pv(f32x4_t (&o)[RG][D / 16], const uint4 (&pb
 }
 
 // ---------------------------------------------------------------------------
-// Tile classes of a mask tensor: grid (column tiles, row blocks, Bm * Hm),
-// 256 threads; thread t covers row q0 + t / 4, columns 16 (t % 4) .. + 15 of
-// the tile.  Rows past Q do not count; columns past T make a tile MIXED.
+// Tile classes of a mask tensor: grid (column tile groups, row blocks,
+// Bm * Hm), 256 threads; a block classifies kMaskTilesPerBlock consecutive
+// 64 x 64 tiles of one row block (its loads all in flight together), thread
+// t covering row q0 + t / 4, columns 16 (t % 4) .. + 15 of each.  Rows past
+// Q do not count; columns past T make a tile MIXED.
+constexpr int kMaskTilesPerBlock = 8;
 __global__ void __launch_bounds__(kPfThreads) mask_tiles_kernel(PrefillParams p) {
-  const int kt = blockIdx.x, qb = blockIdx.y, bh = blockIdx.z;
+  constexpr int TPB = kMaskTilesPerBlock, W = kPfThreads / 64;
+  __shared__ uint8_t wany[TPB][W], wall[TPB][W];
+  const int qb = blockIdx.y, bh = blockIdx.z, tid = threadIdx.x, wave = tid >> 6;
   const int mb = bh / p.mask_h, mh = bh - mb * p.mask_h;
-  const int row = qb * kPfRows + (threadIdx.x >> 2), c0 = kt * kPfKeys + 16 * (threadIdx.x & 3);
-  int any = 0, all = 1;
-  if (row < p.qlen) {
-    const int64_t o = mask_off(p, mb, mh, row, 0);
-    if (p.mask_kind == KIV_MASK_BOOL && p.ms3 == 1 && c0 + 16 <= p.hot_len && !(((uintptr_t)p.mask + o + c0) & 15)) {
-      const uint4 v = load16(p.mask + o + c0);
-      const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+  const int nkt = (p.hot_len + kPfKeys - 1) / kPfKeys, kt0 = blockIdx.x * TPB;
+  const int row = qb * kPfRows + (tid >> 2), cq = 16 * (tid & 3);
+  int any[TPB], all[TPB];
 #pragma unroll
-      for (int j = 0; j < 4; ++j)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const bool vis = (w[j] >> (8 * e)) & 0xffu;
-          any |= vis;
-          all &= vis;
-        }
-    } else {
-      for (int j = 0; j < 16; ++j) {
-        const int t = c0 + j;
-        if (t >= p.hot_len) {
-          all = 0;
-          continue;
-        }
-        const int64_t oe = o + (int64_t)t * p.ms3;
-        if (p.mask_kind == KIV_MASK_BOOL) {
-          const bool vis = p.mask[oe] != 0;
-          any |= vis;
-          all &= vis;
-        } else {
-          const float v = float_bias(p, oe);
-          any |= v != -INFINITY;
-          all &= v == 0.f;
-        }
+  for (int j = 0; j < TPB; ++j) {
+    any[j] = 0;
+    all[j] = 1;
+  }
+  // Columns c0 .. c0 + 15 of one tile into any / all.
+  auto scalar = [&](int64_t o, int c0, int &an, int &al) {
+    for (int e = 0; e < 16; ++e) {
+      const int t = c0 + e;
+      if (t >= p.hot_len) {
+        al = 0;
+        continue;
+      }
+      const int64_t oe = o + (int64_t)t * p.ms3;
+      if (p.mask_kind == KIV_MASK_BOOL) {
+        const bool vis = p.mask[oe] != 0;
+        an |= vis;
+        al &= vis;
+      } else {
+        const float v = float_bias(p, oe);
+        an |= v != -INFINITY;
+        al &= v == 0.f;
       }
     }
+  };
+  if (row < p.qlen) {
+    const int64_t o = mask_off(p, mb, mh, row, 0);
+    if (p.mask_kind == KIV_MASK_BOOL && p.ms3 == 1 && !(((uintptr_t)p.mask + o) & 15)) {
+      uint4 v[TPB];
+#pragma unroll
+      for (int j = 0; j < TPB; ++j) {
+        const int c0 = (kt0 + j) * kPfKeys + cq;
+        v[j] = c0 + 16 <= p.hot_len ? load16(p.mask + o + c0) : make_uint4(0, 0, 0, 0);
+      }
+#pragma unroll
+      for (int j = 0; j < TPB; ++j) {
+        const int c0 = (kt0 + j) * kPfKeys + cq;
+        if (kt0 + j >= nkt) continue;
+        if (c0 + 16 <= p.hot_len) {
+          const uint32_t w[4] = {v[j].x, v[j].y, v[j].z, v[j].w};
+#pragma unroll
+          for (int q = 0; q < 4; ++q)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              const bool vis = (w[q] >> (8 * e)) & 0xffu;
+              any[j] |= vis;
+              all[j] &= vis;
+            }
+        } else {
+          scalar(o, c0, any[j], all[j]);
+        }
+      }
+    } else {
+      for (int j = 0; j < TPB && kt0 + j < nkt; ++j) scalar(o, (kt0 + j) * kPfKeys + cq, any[j], all[j]);
+    }
   }
-  any = __syncthreads_or(any);
-  all = __syncthreads_and(all);
-  if (threadIdx.x == 0) {
-    const int nqb = (p.qlen + kPfRows - 1) / kPfRows, nkt = (p.hot_len + kPfKeys - 1) / kPfKeys;
-    p.tiles[((int64_t)bh * nqb + qb) * nkt + kt] =
-        (uint8_t)(!any ? TILE_SKIP : all ? TILE_FULL : TILE_MIXED);
+#pragma unroll
+  for (int j = 0; j < TPB; ++j) {
+    const uint64_t a = __ballot(any[j]), n = __ballot(!all[j]);
+    if ((tid & 63) == 0) {
+      wany[j][wave] = a != 0;
+      wall[j][wave] = n == 0;
+    }
+  }
+  __syncthreads();
+  if (tid < TPB && kt0 + tid < nkt) {
+    int an = 0, al = 1;
+#pragma unroll
+    for (int w = 0; w < W; ++w) {
+      an |= wany[tid][w];
+      al &= wall[tid][w];
+    }
+    const int nqb = (p.qlen + kPfRows - 1) / kPfRows;
+    p.tiles[((int64_t)bh * nqb + qb) * nkt + kt0 + tid] = (uint8_t)(!an ? TILE_SKIP : al ? TILE_FULL : TILE_MIXED);
   }
 }
 
@@ -775,7 +816,7 @@ int kiv_prefill_attention(const kiv_attention_args_t *a, kiv_stream_t stream) {
   }
   if (mode != PF_ARITH) {
     p.tiles = (uint8_t *)a->workspace;
-    const dim3 cgrid((unsigned)div_up(a->hot_len, kPfKeys), (unsigned)div_up(Q, kPfRows),
+    const dim3 cgrid((unsigned)div_up(div_up(a->hot_len, kPfKeys), kMaskTilesPerBlock), (unsigned)div_up(Q, kPfRows),
                      (unsigned)(p.mask_b * p.mask_h));
     if (cgrid.y > 65535 || cgrid.z > 65535) return fail(KIV_ERR_UNSUPPORTED, "%s: too many query rows", who);
     hipLaunchKernelGGL(mask_tiles_kernel, cgrid, dim3(kPfThreads), 0, st, p);
