@@ -197,12 +197,6 @@ template <int DT, int KT, int MK> struct PfBlock {
     cold_vb = p.cold_v + ((int64_t)b * p.hkv + kvh) * p.cold_len * (int64_t)D * 2;
     hot_kb = p.hot_k + ((int64_t)b * p.hks0 + (int64_t)kvh * p.hks1) * 2;
     hot_vb = p.hot_v + ((int64_t)b * p.hvs0 + (int64_t)kvh * p.hvs1) * 2;
-#pragma unroll
-    for (int j = 0; j < KJ; ++j) kreg[j] = make_uint4(0, 0, 0, 0);
-#pragma unroll
-    for (int j = 0; j < VJ; ++j)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) vreg[j][r] = make_uint4(0, 0, 0, 0);
   }
 
   __device__ __forceinline__ int combine(int k) const {
