@@ -301,6 +301,22 @@ template <int DT> __device__ __forceinline__ float chunk_dot(const uint4 &x, con
 }
 
 __device__ __forceinline__ uint4 load16(const void *p) { return *reinterpret_cast<const uint4 *>(p); }
+// Raw buffer of `bytes` bytes at `base` (a block-uniform address, kept in
+// SGPRs).  A load whose offset is at or past `bytes` returns zeros without
+// touching memory.  Offsets stay below 2^31.  Buffer loads count only in
+// vmcnt (a flat load also counts in lgkmcnt, which every LDS wait and
+// barrier drains).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t tile_rsrc(const char *base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<char *>(base), (short)0, (int)bytes, 0x00020000);
+}
+__device__ __forceinline__ uint4 buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t voff) {
+  typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+  const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r, (int)voff, 0, 0);
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ uint32_t buf_load4(__amdgpu_buffer_rsrc_t r, uint32_t voff) {
+  return __builtin_amdgcn_raw_buffer_load_b32(r, (int)voff, 0, 0);
+}
 
 // Evicted rows that one extra block per kv row of another launch copies
 // into the partial page (count 0: none): token t of row r = b*hkv + h goes

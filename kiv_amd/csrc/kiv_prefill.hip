@@ -102,19 +102,6 @@ __device__ __forceinline__ float float_bias(const PrefillParams &p, int64_t o) {
   }
 }
 
-// ---------------------------------------------------------------------------
-// Raw buffer of `bytes` bytes over one tile's rows, its base in SGPRs.  A
-// load whose offset is at or past `bytes` returns zeros without touching
-// memory.  Offsets stay below 2^31 (the host bounds the row strides).
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t tile_rsrc(const char *base, uint32_t bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<char *>(base), (short)0, (int)bytes, 0x00020000);
-}
-__device__ __forceinline__ uint4 buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t voff) {
-  typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
-  const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r, (int)voff, 0, 0);
-  return make_uint4(v.x, v.y, v.z, v.w);
-}
-
 // Row groups of 16 query rows per wave: two up to head_dim 128 (each K and
 // V^T operand read from LDS then feeds two MFMAs, halving LDS and L2 traffic
 // per flop), one above (the accumulators would not fit twice).

@@ -467,24 +467,30 @@ __device__ void emit_topk_unranked(const Src &mem, const uint64_t *cand, int C, 
 // bitmap bits[words] in LDS and lists it: upage[v] = the v-th union page
 // ascending (upage holds min(nk, pages) entries; a word's pages start at
 // the set bits of the words before it).  Returns the union size.
+// In two steps: union_mark takes entries threadIdx.x + u * NT (u <
+// kUnionPF) already loaded (-1 past nk), reads the rest of the list and
+// says which of its entries set their page's bit first (own); union_list
+// ranks the bitmap.
+constexpr int kUnionPF = 4;  // list entries per thread loaded before the bitmap is cleared
 template <int NT>
-__device__ int rank_union(const int32_t *row_pages, int nk, int words, uint32_t *bits, int *upage, int *scan_tmp) {
-  constexpr int PF = 4;  // list entries per thread loaded before the bitmap is cleared
-  int first[PF];
-#pragma unroll
-  for (int u = 0; u < PF; ++u) {
-    const int i = threadIdx.x + u * NT;
-    first[u] = i < nk ? row_pages[i] : -1;
-  }
+__device__ void union_mark(const int (&first)[kUnionPF], const int32_t *row_pages, int nk, int words, uint32_t *bits,
+                           bool (&own)[kUnionPF]) {
   for (int w = threadIdx.x; w < words; w += NT) bits[w] = 0u;
   __syncthreads();
 #pragma unroll
-  for (int u = 0; u < PF; ++u)
-    if (first[u] >= 0) atomicOr(&bits[first[u] >> 5], 1u << (first[u] & 31));
-  for (int i = threadIdx.x + PF * NT; i < nk; i += NT) {
+  for (int u = 0; u < kUnionPF; ++u) {
+    own[u] = false;
+    if (first[u] >= 0) {
+      const uint32_t bit = 1u << (first[u] & 31);
+      own[u] = (atomicOr(&bits[first[u] >> 5], bit) & bit) == 0u;
+    }
+  }
+  for (int i = threadIdx.x + kUnionPF * NT; i < nk; i += NT) {
     const int page = row_pages[i];
     atomicOr(&bits[page >> 5], 1u << (page & 31));
   }
+}
+template <int NT> __device__ int union_list(int words, const uint32_t *bits, int *upage, int *scan_tmp) {
   __syncthreads();
   int before = 0;
   for (int base = 0; base < words; base += NT) {
@@ -500,6 +506,18 @@ __device__ int rank_union(const int32_t *row_pages, int nk, int words, uint32_t 
   }
   __syncthreads();
   return before;
+}
+template <int NT>
+__device__ int rank_union(const int32_t *row_pages, int nk, int words, uint32_t *bits, int *upage, int *scan_tmp) {
+  int first[kUnionPF];
+#pragma unroll
+  for (int u = 0; u < kUnionPF; ++u) {
+    const int i = threadIdx.x + u * NT;
+    first[u] = i < nk ? row_pages[i] : -1;
+  }
+  bool own[kUnionPF];
+  union_mark<NT>(first, row_pages, nk, words, bits, own);
+  return union_list<NT>(words, bits, upage, scan_tmp);
 }
 
 // Union of long row lists (several query passes, or a long query): marks
@@ -975,8 +993,47 @@ struct FinePrune {
   // the select lists them itself), [1] = the slices read for b, [2 ..] =
   // those pages' union ranks, ascending (up to kPageListCap).
   int32_t *plan;
+  // Speculative slices: the first `spec` pages of the coarse list of each
+  // kv row's first query row (lists of spec_kc pages) are read before the
+  // threshold is known (0: none).
+  int spec, spec_kc;
 };
 constexpr int kPlanStride = 2 + kPageListCap;
+
+// Pages per kv row that a pruned host-tier scan reads speculatively: the
+// top of the first query row's coarse list, whose slices are in flight
+// while the blocks rank the union and compute the threshold; a page whose
+// bound then misses T is dropped unscored (at most this many wasted page
+// reads per kv row).  Measured on MI355X (1M cold tokens, Qwen2.5-7B
+// shape, 8 pages per kv row reach T): 4 pages take the scan from 32.7 to
+// 26.6 us, 3 and 5 to 28.5, 6 and 8 back to 33 and 35 (every page read
+// early is a hit); 4 is also the best of 4, 6 and 8 with 16 hits (MQA).
+constexpr int kSpecPages = 4;
+
+// Kv heads per batch row whose lower-bound keys two aligned 16-byte groups
+// always hold (the run starts at b * hkv within a page's kr = B * hkv keys).
+__host__ __device__ constexpr bool spec_hkv_ok(int hkv) { return hkv <= 4 || hkv == 8; }
+
+// Max of the bound keys [st, st + n) of a [N][kr] key array padded to
+// `padded` keys (keys: a buffer over it): two 16-byte loads, no branch
+// (spec_hkv_ok(n)); the second group is clamped into the array and masked
+// like the first.  A lane that is not `live` reads nothing (its offsets
+// fall past the buffer) and gets 0.
+__device__ __forceinline__ uint32_t spec_lower_key(__amdgpu_buffer_rsrc_t keys, int64_t st, int n, int64_t padded,
+                                                   bool live) {
+  const int64_t g0 = st & ~int64_t(3), g1 = min(g0 + 4, padded - 4);
+  const uint32_t past = (uint32_t)(padded * 4);
+  const uint4 a = buf_load16(keys, live ? (uint32_t)(g0 * 4) : past);
+  const uint4 c = buf_load16(keys, live ? (uint32_t)(g1 * 4) : past);
+  const uint32_t xa[4] = {a.x, a.y, a.z, a.w}, xc[4] = {c.x, c.y, c.z, c.w};
+  uint32_t m = 0u;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    m = max(m, g0 + i >= st && g0 + i < st + n ? xa[i] : 0u);
+    m = max(m, g1 + i >= st && g1 + i < st + n ? xc[i] : 0u);
+  }
+  return m;
+}
 
 // Pruning pays when it skips pages: after a call whose scan read more than
 // three quarters of the union's slices, the next kPruneRetry calls on the
@@ -1122,16 +1179,13 @@ __device__ __forceinline__ int count_keys_ge(const uint32_t *p, int n, uint32_t 
 
 // Lower-bound keys of the union pages for batch row b (max over its kv
 // rows), entry v = union rank, as composites; sub-slots as in PageKeys.
-template <int NT, typename PageOf> struct UnionLowerKeys {
-  const uint32_t *lb;
-  int kr, r0, hkv, U;
-  PageOf page_of;
+template <int NT, typename LbOf> struct UnionLowerKeys {
+  int U;
+  LbOf lb_of;  // union rank -> lower-bound key
   template <typename F> __device__ void each_slot(F &&f) const {
     constexpr int W = NT / 64;
     int u = 0;
-    for (int v = (threadIdx.x >> 6) + W * (threadIdx.x & 63); v < U; v += NT, ++u) {
-      f(comp_of(max_keys(lb + (int64_t)page_of(v) * kr + r0, hkv), v), u & 3);
-    }
+    for (int v = (threadIdx.x >> 6) + W * (threadIdx.x & 63); v < U; v += NT, ++u) f(comp_of(lb_of(v), v), u & 3);
   }
   template <typename F> __device__ void each(F &&f) const {
     each_slot([&](uint64_t x, int) { f(x); });
@@ -1243,192 +1297,317 @@ __global__ void __launch_bounds__(256) fine_scan_kernel(
   int *upage = plist + (pr.mode == 1 ? kPageListCap : 0);  // row lists: the union pages
   const int tid = threadIdx.x;
   const bool pruned = pr.mode == 1 && *pr.ctl <= 0;
+  const int nsplit = (page_size + tpi - 1) / tpi;
+  const int slot = tid / LG, lane = tid % LG;
+  const bool on = lane < cpr;
+  const int64_t row_bytes = (int64_t)head_dim * EB;
+  auto page_rows = [&](int64_t page, int s) {
+    return reinterpret_cast<const char *>(ktab[page >> chunk_shift]) +
+           (page & ((int64_t(1) << chunk_shift) - 1)) * page_bytes +
+           ((int64_t)r * page_size + (int64_t)s * tpi) * row_bytes;
+  };
+  // Tokens [t0, t0 + NSLOT * UT) of a slice of ntok rows at rowbase: UT
+  // 16-byte chunks per lane (zero past the slice).
+  auto load_batch = [&](const char *rowbase, int t0, int ntok, uint4(&x)[UT]) {
+#pragma unroll
+    for (int i = 0; i < UT; ++i) {
+      const int t = t0 + i * NSLOT + slot;
+      x[i] = (on && t < ntok) ? load16(rowbase + (int64_t)t * row_bytes + lane * VEC * EB) : make_uint4(0, 0, 0, 0);
+    }
+  };
+  // Stages a loaded batch (when asked) and folds its scores into the keys
+  // of candidates cand0 + t.
+  auto score_batch = [&](const uint4(&x)[UT], int t0, int ntok, int64_t cand0, char *stage) {
+    if (stage) {
+#pragma unroll
+      for (int i = 0; i < UT; ++i) {
+        const int t = t0 + i * NSLOT + slot;
+        if (on && t < ntok) *reinterpret_cast<uint4 *>(stage + (int64_t)t * row_bytes + lane * VEC * EB) = x[i];
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < UT; ++i) {
+      const int t = t0 + i * NSLOT + slot;
+      if (t >= ntok) break;
+      float best = -INFINITY;
+      for (int j = 0; j < GQ; ++j) {
+        float part = 0.f;
+        if (on) part = chunk_dot<DT>(x[i], load16(qraw + ((size_t)j * head_dim + lane * VEC) * EB), 0.f);
+        best = fmaxf(best, score_of<DT>(group_sum<LG>(part), scale, round != 0));
+      }
+      if (lane == 0) atomicMax(&out[(int64_t)b * ld + cand0 + t], order_key(best));
+    }
+  };
+  // Scores tokens [t0, ntok) of a slice (rows at rowbase, candidates cand0..)
+  // into their keys, staging the K rows when asked.
+  auto scan_slice = [&](const char *rowbase, int64_t cand0, int ntok, char *stage, int t0 = 0) {
+    if (k_read) rowbase = k_read + ((int64_t)r * ld + cand0) * row_bytes;
+    for (int tb = t0; tb < ntok; tb += NSLOT * UT) {
+      uint4 x[UT];
+      load_batch(rowbase, tb, ntok, x);
+      score_batch(x, tb, ntok, cand0, stage);
+    }
+  };
+  // Speculative slice (pruned scan, with the host's consent in pr.spec):
+  // block x < spec * nsplit reads slice x % nsplit of page x / nsplit of
+  // the coarse list of this kv row's first query row (the row's best pages
+  // first) while the blocks rank the union and compute T; its first batch
+  // stays in registers until the threshold says whether it is scored.
+  // Vector loads complete in issue order, so every global read the
+  // threshold needs is issued before the host read: the whole row list
+  // and each union page's bound keys, placed in LDS tables by union rank
+  // once the union is ranked.  From the host read to the scoring the blocks
+  // work in LDS only.
+  const int nspec =
+      pruned && union_src == UNION_ROWS && row_pages_n <= kUnionPF * 256 && spec_hkv_ok(hkv) ? pr.spec : 0;
+  __shared__ int spec_pg[kSpecPages];
+  const int32_t *spec_list = row_pages + (int64_t)r * GQ * pr.spec_kc;
+  const int my_spec = tid < nspec ? spec_list[tid] : -1;
+  const bool spec_block = (int)blockIdx.x < nspec * nsplit;
+  const int sslice = blockIdx.x % nsplit;
+  const int64_t spage = spec_block ? spec_list[blockIdx.x / nsplit] : -1;
   for (int i = tid; i < GQ * cpr; i += 256) {
     const int j = i / cpr, c = i % cpr;
     const int h = kvh * G + j / qlen, qp = j % qlen;
     *reinterpret_cast<uint4 *>(qraw + ((size_t)j * head_dim + c * VEC) * EB) =
         load16(q + ((int64_t)b * qs0 + (int64_t)h * qs1 + (int64_t)qp * qs2 + c * VEC) * EB);
   }
-  int U = 0;
-  if (union_src == UNION_ROWS) {
-    U = rank_union<256>(row_pages, row_pages_n, words, ubits, upage, scan_tmp);
-    if (blockIdx.x == 0 && blockIdx.y == 0)
-      publish_union<DT>(upage, U, page_list, pages_out, counters, union_out, coarse_stats, rows, n_pages, round,
-                        stats_out, stats_accum);
-  } else if (union_src == UNION_LIST) {
-    U = counters[0];
-  }
-  __syncthreads();
-  const int nsplit = (page_size + tpi - 1) / tpi;
-  const int slot = tid / LG, lane = tid % LG;
-  const bool on = lane < cpr;
-  const int64_t row_bytes = (int64_t)head_dim * EB;
-  // Scores tokens [0, ntok) of a slice (rows at rowbase, candidates cand0..)
-  // into their keys, staging the K rows when asked.
-  auto scan_slice = [&](const char *rowbase, int64_t cand0, int ntok, char *stage) {
-    if (k_read) rowbase = k_read + ((int64_t)r * ld + cand0) * row_bytes;
-    for (int tb = 0; tb < ntok; tb += NSLOT * UT) {
-      uint4 x[UT];
+  // Two bodies: with speculation (pruned by construction) and without,
+  // so that no path of one joins the other's (a join would make the
+  // compiler wait for the host read where the paths meet).
+  auto body = [&](auto spec_c) {
+    constexpr bool SPEC = decltype(spec_c)::value;
+    if (tid < nspec) spec_pg[tid] = my_spec;
+    uint4 xs[UT];  // the speculative slice's first batch
+    uint32_t sub = 0u;  // the speculative page's upper bound for this kv row
+    // With speculation: the union pages' bound keys by union rank (batch row
+    // b's lower bound, this kv row's upper bound), after the union list.
+    const int upage_cap = min(row_pages_n, n_pages);
+    uint32_t *lbt = reinterpret_cast<uint32_t *>(upage + upage_cap), *ubt = lbt + upage_cap;
+    int U = 0;
+    if constexpr (SPEC) {
+      // The row list in registers, marked in the union bitmap; the first
+      // entry of each page loads its bound keys (through buffers, so that
+      // the other lanes read nothing and no branch makes the count of
+      // loads path-dependent).
+      int ent[kUnionPF];
+      bool own[kUnionPF];
+      uint32_t elb[kUnionPF], eub[kUnionPF];
+#pragma unroll
+      for (int u = 0; u < kUnionPF; ++u) {
+        const int e = tid + u * 256;
+        ent[u] = e < row_pages_n ? row_pages[e] : -1;
+      }
+      union_mark<256>(ent, row_pages, row_pages_n, words, ubits, own);
+      const int64_t padded = ((int64_t)n_pages * pr.kr + 63) & ~int64_t(63);
+      const auto lbk = tile_rsrc(reinterpret_cast<const char *>(pr.lb), (uint32_t)(padded * 4));
+      const auto ubk = tile_rsrc(reinterpret_cast<const char *>(pr.ub), (uint32_t)(padded * 4));
+#pragma unroll
+      for (int u = 0; u < kUnionPF; ++u) {
+        const int64_t prow = (int64_t)max(ent[u], 0) * pr.kr;
+        eub[u] = buf_load4(ubk, own[u] ? (uint32_t)((prow + r) * 4) : (uint32_t)(padded * 4));
+        elb[u] = spec_lower_key(lbk, prow + (int64_t)b * hkv, hkv, padded, own[u]);
+      }
+      const int ntok = spec_block ? min(tpi, page_size - sslice * tpi) : 0;
+      const char *srows = spec_block ? page_rows(spage, sslice) : q;  // an empty buffer when not speculating
+      __syncthreads();  // keeps the host read after the loads above
+      const uint32_t bytes = (uint32_t)(ntok * row_bytes);
+      const auto rs = tile_rsrc(srows, bytes);
 #pragma unroll
       for (int i = 0; i < UT; ++i) {
-        const int t = tb + i * NSLOT + slot;
-        x[i] = (on && t < ntok) ? load16(rowbase + (int64_t)t * row_bytes + lane * VEC * EB)
-                                : make_uint4(0, 0, 0, 0);
+        const int t = i * NSLOT + slot;
+        xs[i] = buf_load16(rs, on && t < ntok ? (uint32_t)(t * row_bytes) + lane * VEC * EB : bytes);
       }
-      if (stage) {
+      // Wanted with the host read's data only (where the slice is scored).
+      sub = pr.ub[max(spage, int64_t(0)) * pr.kr + r];
+      U = union_list<256>(words, ubits, upage, scan_tmp);
 #pragma unroll
-        for (int i = 0; i < UT; ++i) {
-          const int t = tb + i * NSLOT + slot;
-          if (on && t < ntok) *reinterpret_cast<uint4 *>(stage + (int64_t)t * row_bytes + lane * VEC * EB) = x[i];
+      for (int u = 0; u < kUnionPF; ++u) {
+        if (!own[u]) continue;
+        int lo = 0, hi = U - 1;  // the entry's union rank (upage ascends)
+        while (lo < hi) {
+          const int mid = (lo + hi) >> 1;
+          if (upage[mid] < ent[u]) lo = mid + 1;
+          else hi = mid;
+        }
+        lbt[lo] = elb[u];
+        ubt[lo] = eub[u];
+      }
+      if (blockIdx.x == 0 && blockIdx.y == 0)
+        publish_union<DT>(upage, U, page_list, pages_out, counters, union_out, coarse_stats, rows, n_pages, round,
+                          stats_out, stats_accum);
+    } else if (union_src == UNION_ROWS) {
+      U = rank_union<256>(row_pages, row_pages_n, words, ubits, upage, scan_tmp);
+      if (blockIdx.x == 0 && blockIdx.y == 0)
+        publish_union<DT>(upage, U, page_list, pages_out, counters, union_out, coarse_stats, rows, n_pages, round,
+                          stats_out, stats_accum);
+    } else if (union_src == UNION_LIST) {
+      U = counters[0];
+    }
+    __syncthreads();
+    auto page_of = [&](int v) -> int64_t {
+      return union_src == UNION_ROWS ? upage[v] : page_list[v];
+    };
+    // Candidate-indexed staging of candidate cand0's row (when staging).
+    auto stage_at = [&](int64_t cand0) -> char * {
+      return k_stage ? k_stage + ((int64_t)r * ld + cand0) * row_bytes : nullptr;
+    };
+    const int part_items = (partial_len + tpi - 1) / tpi;
+    if (SPEC || pruned) {
+      // Threshold T of batch row b, the same in every block: the per-wave
+      // bound of the m-th largest of the union pages' lower-bound keys (m =
+      // ceil(k / page_size) pages hold at least k candidates); 0 when U < m.
+      const int k = min(pr.width, U * page_size + partial_len);
+      const int m = (k + page_size - 1) / page_size;
+      const uint32_t *ubr = pr.ub + r;
+      // A union of at most 256 pages: thread t takes page v = t / 64 + 4 (t %
+      // 64) (consecutive ranks on different waves, as UnionLowerKeys deals
+      // them) and reads its lower bound over b's kv rows and this row's upper
+      // bound together.
+      const bool one_each = U <= 256;
+      const int v1 = (tid >> 6) + 4 * (tid & 63);
+      // Bound keys of union rank v: from the LDS tables with speculation,
+      // else from memory.
+      auto lb_of = [&](int v) {
+        if constexpr (SPEC) return lbt[v];
+        else return max_keys(pr.lb + page_of(v) * pr.kr + b * hkv, hkv);
+      };
+      auto ub_of = [&](int v) {
+        if constexpr (SPEC) return ubt[v];
+        else return ubr[page_of(v) * pr.kr];
+      };
+      uint32_t lb1 = 0u, ub1 = 0u;
+      if (one_each && v1 < U) {
+        lb1 = lb_of(v1);
+        ub1 = ub_of(v1);
+      }
+      uint32_t tb = 0u;
+      if (U >= m) {
+        if (one_each) {
+          const OneKey src{comp_of(lb1, v1), v1 < U};
+          tb = block_kth_bound<256>(src, m, tsh);
+        } else {
+          const UnionLowerKeys<256, decltype(lb_of)> src{U, lb_of};
+          tb = block_kth_bound<256>(src, m, tsh);
         }
       }
-#pragma unroll
-      for (int i = 0; i < UT; ++i) {
-        const int t = tb + i * NSLOT + slot;
-        if (t >= ntok) break;
-        float best = -INFINITY;
-        for (int j = 0; j < GQ; ++j) {
-          float part = 0.f;
-          if (on) part = chunk_dot<DT>(x[i], load16(qraw + ((size_t)j * head_dim + lane * VEC) * EB), 0.f);
-          best = fmaxf(best, score_of<DT>(group_sum<LG>(part), scale, round != 0));
+      if (blockIdx.x == 0 && kvh == 0 && tid == 0) pr.thr[b] = tb;
+      // The speculative slice, scored (and staged by its union rank) when its
+      // page's bound for this kv row reaches T; otherwise dropped unscored.
+      if (spec_block && sub >= tb) {
+        int lo = 0, hi = U - 1;  // the page's union rank (upage ascends)
+        while (lo < hi) {
+          const int mid = (lo + hi) >> 1;
+          if (upage[mid] < spage) lo = mid + 1;
+          else hi = mid;
         }
-        if (lane == 0) atomicMax(&out[(int64_t)b * ld + cand0 + t], order_key(best));
+        const int64_t cand0 = (int64_t)lo * page_size + (int64_t)sslice * tpi;
+        const int ntok = min(tpi, page_size - sslice * tpi);
+        score_batch(xs, 0, ntok, cand0, stage_at(cand0));
+        scan_slice(page_rows(spage, sslice), cand0, ntok, stage_at(cand0), NSLOT * UT);
+      }
+      // Per window of kPageListCap union pages, the other pages whose upper
+      // bound for this kv row reaches T are listed in LDS, then their slices
+      // are spread over the blocks after the speculative ones; the partial
+      // page's slices follow.
+      int listed = 0;  // pages listed in earlier windows (the compact staging's slot base)
+      auto is_spec = [&](int64_t page) {
+        bool hit = false;
+        for (int i = 0; i < nspec; ++i) hit |= spec_pg[i] == page;
+        return hit;
+      };
+      const int first = (int)((blockIdx.x + gridDim.x - (unsigned)(nspec * nsplit) % gridDim.x) % gridDim.x);
+      for (int base = 0; base < U; base += kPageListCap) {
+        const int nv = min(kPageListCap, U - base);
+        int nh = 0;
+        if (one_each) {
+          const int hit = v1 < U && ub1 >= tb && !is_spec(page_of(v1)) ? 1 : 0;
+          const int pos = block_incl_scan<256>(hit, scan_tmp, &nh) - hit;
+          if (hit) plist[pos] = v1;
+        } else {
+          for (int c0 = 0; c0 < nv; c0 += 256) {
+            const int v = base + c0 + tid;
+            const int hit = c0 + tid < nv && ub_of(v) >= tb && !is_spec(page_of(v)) ? 1 : 0;
+            int tot;
+            const int pos = nh + block_incl_scan<256>(hit, scan_tmp, &tot) - hit;
+            if (hit) plist[pos] = v;
+            nh += tot;
+          }
+        }
+        __syncthreads();
+        for (int item = first; item < nh * nsplit; item += gridDim.x) {
+          const int i = item / nsplit, v = plist[i], s = item % nsplit;
+          const int64_t page = page_of(v), cand0 = (int64_t)v * page_size + (int64_t)s * tpi;
+          char *stage = stage_at(cand0);
+          if (pr.cstage) {
+            const int sl = listed + i < pr.scap ? listed + i : -1;
+            if (s == 0 && tid == 0) pr.slot_of[page * pr.kr + r] = sl;
+            if (sl >= 0) stage = pr.cstage + (((int64_t)r * pr.scap + sl) * page_size + (int64_t)s * tpi) * row_bytes;
+          }
+          scan_slice(page_rows(page, s), cand0, min(tpi, page_size - s * tpi), stage);
+        }
+        listed += nh;
+        __syncthreads();  // the list is rebuilt for the next window
+      }
+      if (blockIdx.x == gridDim.x - 1 && kvh == 0) {
+        // The fine select's page list for b (the last block, which the
+        // pruned slices reach last if at all): the union pages with a slice
+        // of some kv row of b at or above T, and the slices read.
+        int32_t *pl = pr.plan + (int64_t)b * kPlanStride;
+        int np = 0, read_all = 0;
+        for (int c0 = 0; c0 < U; c0 += 256) {
+          const int v = c0 + tid;
+          const int read = v < U ? count_keys_ge(pr.ub + page_of(v) * pr.kr + b * hkv, hkv, tb) : 0;
+          const int hit = read > 0 ? 1 : 0;
+          int tot, rtot;
+          const int pos = np + block_incl_scan<256>(hit, scan_tmp, &tot) - hit;
+          if (hit && pos < kPageListCap) pl[2 + pos] = v;
+          block_incl_scan<256>(read, scan_tmp, &rtot);
+          np += tot;
+          read_all += rtot;
+        }
+        if (tid == 0) {
+          pl[0] = np;
+          pl[1] = read_all;
+        }
+      }
+      for (int item = blockIdx.x; item < part_items; item += gridDim.x) {
+        const int64_t cand0 = (int64_t)U * page_size + (int64_t)item * tpi;
+        scan_slice(part_k + ((int64_t)r * page_size + (int64_t)item * tpi) * row_bytes, cand0,
+                   min(tpi, partial_len - item * tpi), stage_at(cand0));
+      }
+      return;
+    }
+    if constexpr (!SPEC) {
+      // Full scan: every union page's slices, then the partial page's.
+      if (pr.mode == 1 && blockIdx.x == 0 && kvh == 0 && tid == 0) {
+        pr.thr[b] = 0u;  // paused: all scanned
+        pr.plan[(int64_t)b * kPlanStride] = -1;
+      }
+      const int page_items = U * nsplit;
+      for (int item = blockIdx.x; item < page_items + part_items; item += gridDim.x) {
+        if (item < page_items) {
+          const int v = item / nsplit, s = item % nsplit;
+          const int64_t page = page_of(v), cand0 = (int64_t)v * page_size + (int64_t)s * tpi;
+          char *stage = stage_at(cand0);
+          if (pr.mode == 1 && pr.cstage) {
+            // Paused pruning: the compact staging's slots are the union ranks.
+            const int sl = v < pr.scap ? v : -1;
+            if (s == 0 && tid == 0) pr.slot_of[page * pr.kr + r] = sl;
+            if (sl >= 0) stage = pr.cstage + (((int64_t)r * pr.scap + sl) * page_size + (int64_t)s * tpi) * row_bytes;
+          }
+          scan_slice(page_rows(page, s), cand0, min(tpi, page_size - s * tpi), stage);
+        } else {
+          const int s = item - page_items;
+          const int64_t cand0 = (int64_t)U * page_size + (int64_t)s * tpi;
+          scan_slice(part_k + ((int64_t)r * page_size + (int64_t)s * tpi) * row_bytes, cand0,
+                     min(tpi, partial_len - s * tpi), stage_at(cand0));
+        }
       }
     }
   };
-  auto page_of = [&](int v) -> int64_t {
-    return union_src == UNION_ROWS ? upage[v] : page_list[v];
-  };
-  auto page_rows = [&](int64_t page, int s) {
-    return reinterpret_cast<const char *>(ktab[page >> chunk_shift]) +
-           (page & ((int64_t(1) << chunk_shift) - 1)) * page_bytes +
-           ((int64_t)r * page_size + (int64_t)s * tpi) * row_bytes;
-  };
-  // Candidate-indexed staging of candidate cand0's row (when staging).
-  auto stage_at = [&](int64_t cand0) -> char * {
-    return k_stage ? k_stage + ((int64_t)r * ld + cand0) * row_bytes : nullptr;
-  };
-  const int part_items = (partial_len + tpi - 1) / tpi;
-  if (pruned) {
-    // Threshold T of batch row b, the same in every block: the per-wave
-    // bound of the m-th largest of the union pages' lower-bound keys (m =
-    // ceil(k / page_size) pages hold at least k candidates); 0 when U < m.
-    const int k = min(pr.width, U * page_size + partial_len);
-    const int m = (k + page_size - 1) / page_size;
-    const uint32_t *ubr = pr.ub + r;
-    // A union of at most 256 pages: thread t takes page v = t / 64 + 4 (t %
-    // 64) (consecutive ranks on different waves, as UnionLowerKeys deals
-    // them) and reads its lower bound over b's kv rows and this row's upper
-    // bound together.
-    const bool one_each = U <= 256;
-    const int v1 = (tid >> 6) + 4 * (tid & 63);
-    uint32_t lb1 = 0u, ub1 = 0u;
-    if (one_each && v1 < U) {
-      const int64_t page = page_of(v1);
-      lb1 = max_keys(pr.lb + page * pr.kr + b * hkv, hkv);
-      ub1 = ubr[page * pr.kr];
-    }
-    uint32_t tb = 0u;
-    if (U >= m) {
-      if (one_each) {
-        const OneKey src{comp_of(lb1, v1), v1 < U};
-        tb = block_kth_bound<256>(src, m, tsh);
-      } else {
-        const UnionLowerKeys<256, decltype(page_of)> src{pr.lb, pr.kr, b * hkv, hkv, U, page_of};
-        tb = block_kth_bound<256>(src, m, tsh);
-      }
-    }
-    if (blockIdx.x == 0 && kvh == 0 && tid == 0) pr.thr[b] = tb;
-    // Per window of kPageListCap union pages, the pages whose upper bound
-    // for this kv row reaches T are listed in LDS, then their slices are
-    // spread over the blocks; the partial page's slices follow.
-    int listed = 0;  // pages listed in earlier windows (the compact staging's slot base)
-    for (int base = 0; base < U; base += kPageListCap) {
-      const int nv = min(kPageListCap, U - base);
-      int nh = 0;
-      if (one_each) {
-        const int hit = v1 < U && ub1 >= tb ? 1 : 0;
-        const int pos = block_incl_scan<256>(hit, scan_tmp, &nh) - hit;
-        if (hit) plist[pos] = v1;
-      } else {
-        for (int c0 = 0; c0 < nv; c0 += 256) {
-          const int v = base + c0 + tid;
-          const int hit = c0 + tid < nv && ubr[page_of(v) * pr.kr] >= tb ? 1 : 0;
-          int tot;
-          const int pos = nh + block_incl_scan<256>(hit, scan_tmp, &tot) - hit;
-          if (hit) plist[pos] = v;
-          nh += tot;
-        }
-      }
-      __syncthreads();
-      for (int item = blockIdx.x; item < nh * nsplit; item += gridDim.x) {
-        const int i = item / nsplit, v = plist[i], s = item % nsplit;
-        const int64_t page = page_of(v), cand0 = (int64_t)v * page_size + (int64_t)s * tpi;
-        char *stage = stage_at(cand0);
-        if (pr.cstage) {
-          const int sl = listed + i < pr.scap ? listed + i : -1;
-          if (s == 0 && tid == 0) pr.slot_of[page * pr.kr + r] = sl;
-          if (sl >= 0) stage = pr.cstage + (((int64_t)r * pr.scap + sl) * page_size + (int64_t)s * tpi) * row_bytes;
-        }
-        scan_slice(page_rows(page, s), cand0, min(tpi, page_size - s * tpi), stage);
-      }
-      listed += nh;
-      __syncthreads();  // the list is rebuilt for the next window
-    }
-    if (blockIdx.x == gridDim.x - 1 && kvh == 0) {
-      // The fine select's page list for b (the last block, which the
-      // pruned slices reach last if at all): the union pages with a slice
-      // of some kv row of b at or above T, and the slices read.
-      int32_t *pl = pr.plan + (int64_t)b * kPlanStride;
-      int np = 0, read_all = 0;
-      for (int c0 = 0; c0 < U; c0 += 256) {
-        const int v = c0 + tid;
-        const int read = v < U ? count_keys_ge(pr.ub + page_of(v) * pr.kr + b * hkv, hkv, tb) : 0;
-        const int hit = read > 0 ? 1 : 0;
-        int tot, rtot;
-        const int pos = np + block_incl_scan<256>(hit, scan_tmp, &tot) - hit;
-        if (hit && pos < kPageListCap) pl[2 + pos] = v;
-        block_incl_scan<256>(read, scan_tmp, &rtot);
-        np += tot;
-        read_all += rtot;
-      }
-      if (tid == 0) {
-        pl[0] = np;
-        pl[1] = read_all;
-      }
-    }
-    for (int item = blockIdx.x; item < part_items; item += gridDim.x) {
-      const int64_t cand0 = (int64_t)U * page_size + (int64_t)item * tpi;
-      scan_slice(part_k + ((int64_t)r * page_size + (int64_t)item * tpi) * row_bytes, cand0,
-                 min(tpi, partial_len - item * tpi), stage_at(cand0));
-    }
-    return;
-  }
-  // Full scan: every union page's slices, then the partial page's.
-  if (pr.mode == 1 && blockIdx.x == 0 && kvh == 0 && tid == 0) {
-    pr.thr[b] = 0u;  // paused: all scanned
-    pr.plan[(int64_t)b * kPlanStride] = -1;
-  }
-  const int page_items = U * nsplit;
-  for (int item = blockIdx.x; item < page_items + part_items; item += gridDim.x) {
-    if (item < page_items) {
-      const int v = item / nsplit, s = item % nsplit;
-      const int64_t page = page_of(v), cand0 = (int64_t)v * page_size + (int64_t)s * tpi;
-      char *stage = stage_at(cand0);
-      if (pr.mode == 1 && pr.cstage) {
-        // Paused pruning: the compact staging's slots are the union ranks.
-        const int sl = v < pr.scap ? v : -1;
-        if (s == 0 && tid == 0) pr.slot_of[page * pr.kr + r] = sl;
-        if (sl >= 0) stage = pr.cstage + (((int64_t)r * pr.scap + sl) * page_size + (int64_t)s * tpi) * row_bytes;
-      }
-      scan_slice(page_rows(page, s), cand0, min(tpi, page_size - s * tpi), stage);
-    } else {
-      const int s = item - page_items;
-      const int64_t cand0 = (int64_t)U * page_size + (int64_t)s * tpi;
-      scan_slice(part_k + ((int64_t)r * page_size + (int64_t)s * tpi) * row_bytes, cand0,
-                 min(tpi, partial_len - s * tpi), stage_at(cand0));
-    }
-  }
+  if (nspec > 0) body(std::integral_constant<bool, true>{});
+  else body(std::integral_constant<bool, false>{});
 }
 
 // MFMA fine scan for queries of many rows (G * Q >= kFineMfmaRows per kv
@@ -2220,6 +2399,15 @@ static int retrieve_impl(kiv_store_t *s, const kiv_retrieve_args_t *a, hipStream
     const int64_t max_items = umax * nsplit + (s->partial_len + tpi - 1) / tpi;
     const int64_t want = host_tier ? 1024 : 2048;
     const int64_t nb = std::max<int64_t>(1, std::min<int64_t>(max_items, (want + s->kr - 1) / s->kr));
+    // A pruned scan with short row lists (in registers, kUnionPF entries a
+    // thread), kv heads spec_hkv_ok and candidate-indexed staging reads the
+    // top pages of each kv row's first query row speculatively (one block
+    // per slice, so at most nb / nsplit pages).
+    if (prune && union_src == UNION_ROWS && k_stage && (int64_t)rows * kc <= kUnionPF * 256 && spec_hkv_ok(hkv) &&
+        (int64_t)N * s->kr * 4 < (int64_t(1) << 30)) {
+      pr.spec = (int)std::min<int64_t>(std::min(kSpecPages, kc), nb / nsplit);
+      pr.spec_kc = kc;
+    }
     // The MFMA scan (whole 64-token slices staged in LDS) serves queries of
     // many rows per kv row on every tier, and every query on the device
     // tiers, where it beats the VALU scan even for a handful of rows
@@ -2278,7 +2466,7 @@ static int retrieve_impl(kiv_store_t *s, const kiv_retrieve_args_t *a, hipStream
     auto valu_scan = [&](int pass, int usrc, int bw, const FinePrune &fp) {
       const int Qp = std::min(Qb, Q - pass * Qb);
       const size_t lds = (size_t)G * Qp * D * eb + (size_t)bw * 4 + (fp.mode == 1 ? (size_t)kPageListCap * 4 : 0) +
-                         (usrc == UNION_ROWS ? upage_bytes : 0);
+                         (usrc == UNION_ROWS ? upage_bytes : 0) + (fp.spec > 0 ? 2 * upage_bytes : 0);
       return with_dt_lg(dt, lg, [&](auto dtc, auto lgc) {
         auto kern = fine_scan_kernel<decltype(dtc)::value, decltype(lgc)::value>;
         if (lds > 65536)

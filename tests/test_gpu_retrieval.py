@@ -334,6 +334,36 @@ def test_fine_pruning_keeps_the_selection(cuda, name, w, batch, clustered):
         assert s1[0] < s1[1] and f1["mean_score"] > f0["mean_score"]  # the skipped pages score low
 
 
+def test_fine_pruning_speculative_pages_that_miss(cuda):
+    """The pruned scan reads the top pages of each kv row's first query row
+    before the threshold is known and scores them only if their bound
+    reaches it.  Here kv row 1's queries are 8x longer, so the threshold
+    comes from its pages and every page of kv row 0 falls below it: kv row
+    0's speculative reads are all dropped and it scans nothing.  Two calls in
+    a row (the second with other queries, so that a dropped slice's stale
+    keys would show) return the full scan's ids and rows bit for bit."""
+    from dataclasses import replace
+
+    w = Workload("prune_spec_miss", 4, 2, 64, torch.bfloat16, hot=16, cold=8192 + 5, top_pages=8, top_p=128,
+                 segment=512)
+    data = generate(w, seed=31)
+    store, oracle, cfg = build(w, data, cuda, chunks=(4096, 1, 511), pruning=True)
+    gen = torch.Generator().manual_seed(32)
+    for call in range(2):
+        q = data["q"].float() + (0.2 * call) * torch.randn(data["q"].shape, generator=gen)
+        q[:, 2:] *= 8.0  # query heads 2, 3 read kv row 1
+        q = q.to(data["q"].dtype)
+        k1, v1, sel1 = check_retrieval(store, oracle, cfg, w, data, q)
+        s1 = store.fine_scan_stats()
+        union = store.telemetry_snapshot()["recent"][-2]["pages_selected"]
+        k0, v0 = store.retrieve_top_kv(q.to(cuda), w.scaling, replace(cfg, fine_pruning=False))
+        sel0 = store.telemetry_snapshot()["recent"][-1]["selected_token_indices"]
+        print(f"speculative misses, call {call}: union {len(union)} pages, slices read {s1}", flush=True)
+        assert 0 < s1[0] <= len(union)  # kv row 1's slices at most: kv row 0 scanned none
+        assert sel1.reshape(-1).tolist() == sel0
+        assert torch.equal(k1.cpu(), k0.cpu()) and torch.equal(v1.cpu(), v0.cpu())
+
+
 def test_fine_pruning_union_wider_than_a_window(cuda):
     """A union of more than 4096 pages: the pruned scan lists its pages in
     two windows (and the fine select falls back to the whole row); the same
