@@ -364,6 +364,31 @@ def test_fine_pruning_speculative_pages_that_miss(cuda):
         assert torch.equal(k1.cpu(), k0.cpu()) and torch.equal(v1.cpu(), v0.cpu())
 
 
+def test_fine_pruning_speculative_wide_union(cuda):
+    """Speculation with a union of more than 256 pages (a row list of 1024
+    entries, the most it takes): the threshold and the page list read the
+    union's bound keys from the LDS tables by rank (not one page per
+    thread).  Unclustered keys, so most pages reach T; the same ids and rows
+    as the full scan (random query rows, so that their top pages differ)."""
+    from dataclasses import replace
+
+    w = Workload("prune_spec_wide", 32, 4, 64, torch.bfloat16, hot=16, cold=1024 * 128 + 3, top_pages=32,
+                 top_p=256, segment=1)
+    data = generate(w, seed=41)
+    store, oracle, cfg = build(w, data, cuda, chunks=(65536,), pruning=True)
+    # independent query rows: their top pages barely overlap
+    q = torch.randn(1, 32, 1, 64, generator=torch.Generator().manual_seed(42)).to(torch.bfloat16)
+    k1, v1, sel1 = check_retrieval(store, oracle, cfg, w, data, q, min_det_c=0.0)
+    union = store.telemetry_snapshot()["recent"][-2]["pages_selected"]
+    s1 = store.fine_scan_stats()
+    k0, v0 = store.retrieve_top_kv(q.to(cuda), w.scaling, replace(cfg, fine_pruning=False))
+    sel0 = store.telemetry_snapshot()["recent"][-1]["selected_token_indices"]
+    print(f"speculative wide union: {len(union)} pages, slices read {s1}", flush=True)
+    assert len(union) > 256
+    assert sel1.reshape(-1).tolist() == sel0
+    assert torch.equal(k1.cpu(), k0.cpu()) and torch.equal(v1.cpu(), v0.cpu())
+
+
 def test_fine_pruning_union_wider_than_a_window(cuda):
     """A union of more than 4096 pages: the pruned scan lists its pages in
     two windows (and the fine select falls back to the whole row); the same
