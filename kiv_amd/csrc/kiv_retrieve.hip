@@ -2390,21 +2390,25 @@ static int retrieve_impl(kiv_store_t *s, const kiv_retrieve_args_t *a, hipStream
     }
   }
   {
+    // A pruned scan with short row lists (in registers, kUnionPF entries a
+    // thread), kv heads spec_hkv_ok and candidate-indexed staging reads the
+    // top pages of each kv row's first query row speculatively.
+    const bool spec = prune && union_src == UNION_ROWS && k_stage && (int64_t)rows * kc <= kUnionPF * 256 &&
+                      spec_hkv_ok(hkv) && (int64_t)N * s->kr * 4 < (int64_t(1) << 30);
     // Slices and grid per tier (see the fine scan kernel): host rows in
-    // ~2 KiB slices over ~1024 blocks, HBM rows in 32-token slices over
-    // ~2048 blocks.
-    int tpi = host_tier ? (int)std::max<int64_t>(1, 2048 / ((int64_t)D * eb)) : 32;
+    // ~2 KiB slices over ~1024 blocks (~1 KiB with speculation: NS
+    // 26.4-26.9 against 27.0 us, C4 28.7-29.3 against 29.1-29.9; 512-byte
+    // and 4 KiB slices slower), HBM rows in 32-token slices over ~2048
+    // blocks.
+    const int64_t slice_host = spec ? 1024 : 2048;
+    int tpi = host_tier ? (int)std::max<int64_t>(1, slice_host / ((int64_t)D * eb)) : 32;
     tpi = std::min(tpi, ps);
     const int nsplit = (ps + tpi - 1) / tpi;
     const int64_t max_items = umax * nsplit + (s->partial_len + tpi - 1) / tpi;
     const int64_t want = host_tier ? 1024 : 2048;
     const int64_t nb = std::max<int64_t>(1, std::min<int64_t>(max_items, (want + s->kr - 1) / s->kr));
-    // A pruned scan with short row lists (in registers, kUnionPF entries a
-    // thread), kv heads spec_hkv_ok and candidate-indexed staging reads the
-    // top pages of each kv row's first query row speculatively (one block
-    // per slice, so at most nb / nsplit pages).
-    if (prune && union_src == UNION_ROWS && k_stage && (int64_t)rows * kc <= kUnionPF * 256 && spec_hkv_ok(hkv) &&
-        (int64_t)N * s->kr * 4 < (int64_t(1) << 30)) {
+    // The speculative pages: one block per slice, so at most nb / nsplit.
+    if (spec) {
       pr.spec = (int)std::min<int64_t>(std::min(kSpecPages, kc), nb / nsplit);
       pr.spec_kc = kc;
     }
