@@ -84,7 +84,10 @@ typedef struct {
 /* Retrieval flags.  KIV_RETRIEVE_PRUNE: on the host tier, the coarse scan
  * also bounds every page's token scores (from a per-page radius recorded at
  * eviction) and the fine scan reads only the pages whose bound can reach
- * the top P' (a threshold from the pages' lower bounds).  The selection,
+ * the top P' (a threshold from the pages' lower bounds).  The top pages of
+ * each kv row's first query row are read before the threshold is known
+ * and dropped unscored if they miss it (at most 4 page reads per kv row
+ * over the pruned set).  The selection,
  * its order and the returned rows are unchanged; the fine telemetry's mean
  * then covers the scored candidates only.  Applies to one-pass queries
  * whose fine scan runs on the vector units (G * Q < 32) with a fresh
