@@ -18,6 +18,7 @@ import torch  # noqa: F401  (load torch's HIP runtime before the library)
 LIB_PATH = Path(os.environ.get("KIV_LIB_PATH") or Path(__file__).resolve().parent / "_lib" / "libkiv_hip.so")
 
 KIV_OK = 0
+ERR_INVALID, ERR_HIP, ERR_OOM, ERR_UNSUPPORTED, ERR_STATE = 1, 2, 3, 4, 5
 DTYPE_F32, DTYPE_F16, DTYPE_BF16 = 0, 1, 2
 TIER_HOST, TIER_HBM, TIER_SPLIT = 0, 1, 2
 ROUND_ACTIVATION, ROUND_FP32 = 0, 1
@@ -127,10 +128,23 @@ def lib() -> C.CDLL:
     return _lib
 
 
+class KivError(RuntimeError):
+    """A failed C-ABI call; ``code`` is its KIV_ERR_* value."""
+
+    def __init__(self, message: str, code: int) -> None:
+        super().__init__(message)
+        self.code = code
+
+    @property
+    def refused(self) -> bool:
+        """Refused by an argument, shape or state check: the call changed nothing."""
+        return self.code in (ERR_INVALID, ERR_UNSUPPORTED, ERR_STATE)
+
+
 def check(rc: int, what: str) -> None:
     if rc != KIV_OK:
         msg = lib().kiv_last_error().decode(errors="replace")
-        raise RuntimeError(f"{what} failed (code {rc}): {msg}")
+        raise KivError(f"{what} failed (code {rc}): {msg}", rc)
 
 
 _DTYPES = {torch.float32: DTYPE_F32, torch.float16: DTYPE_F16, torch.bfloat16: DTYPE_BF16}

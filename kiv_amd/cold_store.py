@@ -329,14 +329,21 @@ class ColdKVStore:
             a.hot_tokens = 0
         stream = nat.stream_ptr(dev)
         out = None
-        if fused:
-            hot_k, hot_v, mask = attend
-            out, _keep = attention.fill_args(self._aargs, q, width, hot_k, hot_v, mask, scaling)
-            self._aargs.cold_k, self._aargs.cold_v = a.k_out, a.v_out
-            nat.check(lib.kiv_retrieve_attend(self._handle, self._rargs_ref, self._aargs_ref, stream),
-                      "kiv_retrieve_attend")
-        else:
-            nat.check(lib.kiv_retrieve(self._handle, self._rargs_ref, stream), "kiv_retrieve")
+        try:
+            if fused:
+                hot_k, hot_v, mask = attend
+                out, _keep = attention.fill_args(self._aargs, q, width, hot_k, hot_v, mask, scaling)
+                self._aargs.cold_k, self._aargs.cold_v = a.k_out, a.v_out
+                nat.check(lib.kiv_retrieve_attend(self._handle, self._rargs_ref, self._aargs_ref, stream),
+                          "kiv_retrieve_attend")
+            else:
+                nat.check(lib.kiv_retrieve(self._handle, self._rargs_ref, stream), "kiv_retrieve")
+        except Exception as e:
+            # A call refused by its checks evicted nothing: the deferred rows
+            # are still this store's to write (counted already).
+            if pend is not None and (not isinstance(e, nat.KivError) or e.refused):
+                self._pending = pend
+            raise
 
         if coarse_runs:
             self._last_coarse_slot = slot
@@ -459,15 +466,18 @@ class ColdKVStore:
                   "kiv_fine_scan_stats")
         return scanned.value, total.value
 
-    def read_summaries(self) -> tuple[torch.Tensor, torch.Tensor]:
-        """(dtype summaries, fp32 means), each [N, B, Hkv, D], copied from HBM."""
+    def read_summaries(self, first: int = 0, n: int | None = None) -> tuple[torch.Tensor, torch.Tensor]:
+        """(dtype summaries, fp32 means) of pages [first, first+n), each
+        [n, B, Hkv, D], copied from HBM (every page by default)."""
         self._flush_pending()
-        N = self.num_pages
-        shape = (N, self._batch or 1, self._num_kv_heads, self._head_dim)
+        n = self.num_pages - first if n is None else n
+        if first < 0 or n < 0 or first + n > self.num_pages:
+            raise ValueError(f"pages [{first}, {first + n}) outside the store's {self.num_pages}")
+        shape = (n, self._batch or 1, self._num_kv_heads, self._head_dim)
         s = torch.empty(shape, dtype=self._dtype or torch.float32, device=self.device)
         s32 = torch.empty(shape, dtype=torch.float32, device=self.device)
-        if N:
-            nat.check(nat.lib().kiv_store_read_summaries(self._handle, 0, N, s.data_ptr(), s32.data_ptr(),
+        if n:
+            nat.check(nat.lib().kiv_store_read_summaries(self._handle, first, n, s.data_ptr(), s32.data_ptr(),
                                                          nat.stream_ptr(self.device)), "read_summaries")
         return s, s32
 

@@ -263,7 +263,7 @@ __global__ void __launch_bounds__(kAttnThreads) decode_attn_combine_kernel(AttnP
 // every K and V chunk and the hot partials loaded up front - then a
 // log-sum-exp merge with the hot window's split partials (m, l, acc) that
 // the fused gather launch left in the workspace.  Retrieved keys are never
-// masked.  The rows are few (B * Hq), so each gets a wide block: 16 waves
+// masked.  The rows are few (B * Hq), so each gets a wide block: 8 waves
 // share the keys and the hot splits.
 template <int DT, int LG>
 __global__ void __launch_bounds__(kFinalThreads) decode_attn_final_kernel(AttnParams p, int s_hot) {

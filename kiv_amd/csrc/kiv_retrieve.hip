@@ -2080,19 +2080,52 @@ static int retrieve_impl(kiv_store_t *s, const kiv_retrieve_args_t *a, hipStream
   if (a->q_stride[3] != 1) return fail(KIV_ERR_INVALID, "kiv_retrieve: q head_dim stride must be 1");
   if (((uintptr_t)a->q & 15) || (a->q_stride[0] % vec) || (a->q_stride[1] % vec) || (a->q_stride[2] % vec))
     return fail(KIV_ERR_INVALID, "kiv_retrieve: q must be 16-byte aligned with strides multiple of %d", vec);
+  // Every argument and state check comes before anything is enqueued or
+  // evicted, so that a refused call leaves the store as it was.
+  const int64_t T_app = a->append_tokens > 0 ? a->append_tokens : 0;
+  if (T_app > 0) {
+    if (!a->append_k || !a->append_v || (((uintptr_t)a->append_k | (uintptr_t)a->append_v) & 15))
+      return fail(KIV_ERR_INVALID, "kiv_retrieve: appended K/V must be non-null and 16-byte aligned");
+    for (int i = 0; i < 3; ++i)
+      if ((a->append_k_stride[i] % vec) || (a->append_v_stride[i] % vec))
+        return fail(KIV_ERR_INVALID, "kiv_retrieve: appended strides must be multiples of %d elements", vec);
+  }
+  if (a->hot_tokens > 0) {
+    if (!a->hot_src_k || !a->hot_src_v || !a->hot_dst_k || !a->hot_dst_v ||
+        (((uintptr_t)a->hot_src_k | (uintptr_t)a->hot_src_v | (uintptr_t)a->hot_dst_k | (uintptr_t)a->hot_dst_v) &
+         15))
+      return fail(KIV_ERR_INVALID, "kiv_retrieve: hot-window rows must be non-null and 16-byte aligned");
+    for (int i = 0; i < 3; ++i)
+      if ((a->hot_src_k_stride[i] % vec) || (a->hot_src_v_stride[i] % vec) || (a->hot_dst_k_stride[i] % vec) ||
+          (a->hot_dst_v_stride[i] % vec))
+        return fail(KIV_ERR_INVALID, "kiv_retrieve: hot-window strides must be multiples of %d elements", vec);
+    if (a->hot_tokens > (1 << 20)) return fail(KIV_ERR_UNSUPPORTED, "kiv_retrieve: too many hot-window rows");
+  }
+  {
+    // Sizes once the appended rows are in.
+    const int64_t pages_after = s->num_pages + (s->partial_len + T_app) / ps;
+    if (s->num_pages * ps + s->partial_len + T_app == 0)
+      return fail(KIV_ERR_STATE, "kiv_retrieve: the cold store is empty");
+    if (pages_after > (int64_t)kMaxWords * 32)
+      return fail(KIV_ERR_UNSUPPORTED, "kiv_retrieve: more than %d pages", kMaxWords * 32);
+    // An eviction drops the union (kiv/cold_store.py:148-151), so a reuse
+    // needs one since the last eviction and no rows appended by this call.
+    if (pages_after > 0 && a->reuse_candidates && (!s->union_valid || T_app > 0))
+      return fail(KIV_ERR_STATE, "kiv_retrieve: reuse_candidates without a union to reuse (none since the last "
+                                 "eviction or reset)");
+  }
+  DeviceGuard guard(s->device);
+  const int rows = B * hq * Q;
+  int rc;
+  if ((rc = s->row_stats.ensure((size_t)(rows + B) * 8, st, false))) return rc;
   // Rows to evict first (kiv_evict's contract).  Rows that stay in the
   // partial page, with a fresh coarse pass to come, are copied by extra
   // blocks of the coarse scan launch (the coarse scan never reads the
   // partial page; the fine scan, a launch later, does); anything else
   // (finishing a page, no finished pages, a reused union) is kiv_evict.
   AppendRows ap{};
-  if (a->append_tokens > 0) {
-    const int64_t T = a->append_tokens;
-    if (!a->append_k || !a->append_v || (((uintptr_t)a->append_k | (uintptr_t)a->append_v) & 15))
-      return fail(KIV_ERR_INVALID, "kiv_retrieve: appended K/V must be non-null and 16-byte aligned");
-    for (int i = 0; i < 3; ++i)
-      if ((a->append_k_stride[i] % vec) || (a->append_v_stride[i] % vec))
-        return fail(KIV_ERR_INVALID, "kiv_retrieve: appended strides must be multiples of %d elements", vec);
+  if (T_app > 0) {
+    const int64_t T = T_app;
     if (s->num_pages > 0 && !a->reuse_candidates && s->partial_len + T < ps) {
       ap.k = (const char *)a->append_k;
       ap.v = (const char *)a->append_v;
@@ -2112,30 +2145,10 @@ static int retrieve_impl(kiv_store_t *s, const kiv_retrieve_args_t *a, hipStream
       ap.in16 = vec;
       s->union_valid = false;  // the partial-page length grows once the launch is enqueued
     } else {
-      const int rc = kiv_evict(s, a->append_k, a->append_k_stride, a->append_v, a->append_v_stride, T,
-                               (kiv_stream_t)st);
+      rc = kiv_evict(s, a->append_k, a->append_k_stride, a->append_v, a->append_v_stride, T, (kiv_stream_t)st);
       if (rc) return rc;
     }
   }
-  // Rows for the caller's hot window: checked here, written with the
-  // coarse scan's launch or by a launch of their own (below).
-  if (a->hot_tokens > 0) {
-    if (!a->hot_src_k || !a->hot_src_v || !a->hot_dst_k || !a->hot_dst_v ||
-        (((uintptr_t)a->hot_src_k | (uintptr_t)a->hot_src_v | (uintptr_t)a->hot_dst_k | (uintptr_t)a->hot_dst_v) &
-         15))
-      return fail(KIV_ERR_INVALID, "kiv_retrieve: hot-window rows must be non-null and 16-byte aligned");
-    for (int i = 0; i < 3; ++i)
-      if ((a->hot_src_k_stride[i] % vec) || (a->hot_src_v_stride[i] % vec) || (a->hot_dst_k_stride[i] % vec) ||
-          (a->hot_dst_v_stride[i] % vec))
-        return fail(KIV_ERR_INVALID, "kiv_retrieve: hot-window strides must be multiples of %d elements", vec);
-    if (a->hot_tokens > (1 << 20)) return fail(KIV_ERR_UNSUPPORTED, "kiv_retrieve: too many hot-window rows");
-  }
-  const int rows = B * hq * Q;
-  if (s->num_pages * ps + s->partial_len + ap.count == 0)
-    return fail(KIV_ERR_STATE, "kiv_retrieve: the cold store is empty");
-  if (s->num_pages > (int64_t)kMaxWords * 32)
-    return fail(KIV_ERR_UNSUPPORTED, "kiv_retrieve: more than %d pages", kMaxWords * 32);
-  DeviceGuard guard(s->device);
   const int lg = lanes_per_row(dt, D);
   const int round = c.score_rounding == KIV_ROUND_ACTIVATION ? 1 : 0;
   const int N = (int)s->num_pages;
@@ -2149,8 +2162,6 @@ static int retrieve_impl(kiv_store_t *s, const kiv_retrieve_args_t *a, hipStream
   const int Qb = std::max(1, std::min(Q, (int)(kFineQueryBytes / ((int64_t)G * D * eb))));
   const int passes = (Q + Qb - 1) / Qb;
   const int64_t qstep = (int64_t)Qb * a->q_stride[2] * eb;  // bytes between passes' first positions
-  int rc;
-  if ((rc = s->row_stats.ensure((size_t)(rows + B) * 8, st, false))) return rc;
   float *coarse_stats = (float *)s->row_stats.ptr;
   float *fine_stats = coarse_stats + 2 * rows;
 
@@ -2165,9 +2176,6 @@ static int retrieve_impl(kiv_store_t *s, const kiv_retrieve_args_t *a, hipStream
   // Shared-layer reuse (kiv/cold_store.py:303-317): the union of the last
   // coarse pass serves a query of any length; the fine scan scores it with
   // this query's rows.
-  if (N > 0 && a->reuse_candidates && !s->union_valid)
-    return fail(KIV_ERR_STATE, "kiv_retrieve: reuse_candidates without a union to reuse (none since the last "
-                               "eviction or reset)");
   const bool fresh = N > 0 && !a->reuse_candidates;
   const bool prune = (a->flags & KIV_RETRIEVE_PRUNE) && host_tier && !fine_mfma && passes == 1 && fresh &&
                      std::max(1, (a->out_width + ps - 1) / ps) < std::min(a->top_pages, N) && a->scaling > 0.f;

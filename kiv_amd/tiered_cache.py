@@ -109,7 +109,7 @@ class _HotLayer(DynamicLayer):
         elif (self._end + n > self._kb.shape[2] or key_states.shape[:2] != self._kb.shape[:2]
               or key_states.dtype != self._kb.dtype):
             self._move(self.keys, self.values, n)
-        if defer and key_states.dtype == self._kb.dtype and value_states.dtype == self._vb.dtype:
+        if defer and self._deferrable(key_states, value_states):
             self._pending_rows = (key_states, value_states, self._end, n)
         else:
             self._kb[:, :, self._end:self._end + n].copy_(key_states)
@@ -117,6 +117,18 @@ class _HotLayer(DynamicLayer):
         self._end += n
         self._window()
         return self.keys, self.values
+
+    def _deferrable(self, k: torch.Tensor, v: torch.Tensor) -> bool:
+        """Rows the retrieval's copy can take: the buffers' dtype, unit stride
+        over head_dim, 16-byte aligned starts and strides (what kiv_retrieve
+        accepts for hot-window rows); anything else is written at once."""
+        if k.dtype != self._kb.dtype or v.dtype != self._vb.dtype:
+            return False
+        vec = 16 // k.element_size()
+        for t in (k, v):
+            if t.stride(-1) != 1 or t.data_ptr() % 16 or any(st % vec for st in t.stride()[:-1]):
+                return False
+        return True
 
     def drop_front(self, n: int) -> None:
         """Forget the oldest ``n`` rows (already copied to the cold tier)."""
@@ -365,17 +377,20 @@ class TieredKVCache(DynamicCache):
         self._decode_step = int(h["decode_step"])
 
     def memory_report(self) -> dict:
-        """Bytes per tier, keys of kiv/tiered_cache.py:259-286 plus what
-        this path holds beyond the bytes in use.
+        """Bytes per tier: the keys of kiv/tiered_cache.py:259-286 with its
+        formulas (bytes in use), plus what this path holds beyond them.
 
-        ``hot_vram_bytes`` and the per-tier keys count the bytes in use, as
-        the reference does.  ``hot_buffer_vram_bytes`` is the hot windows'
-        buffers (each keeps room for 256 more rows), and
-        ``retrieval_scratch_vram_bytes`` the stores' device memory beyond
-        their summaries, partial pages and cold rows (mostly the K staging
-        copy).  ``total_vram_bytes`` / ``total_cpu_bytes`` are everything
-        held in device / pinned host memory, reservations included, so a
-        caller that budgets by them sees the real footprint."""
+        ``total_vram_bytes`` = hot + page summaries + partial pages (+ cold
+        rows kept in HBM by the hbm and split tiers, which the reference does
+        not have) and ``total_cpu_bytes`` = K + V rows in host memory, as the
+        reference counts them.  ``cold_rows_gpu_bytes`` is the HBM-resident
+        cold rows.  ``hot_buffer_vram_bytes`` is the hot windows' buffers
+        (each keeps room for 256 more rows), ``retrieval_scratch_vram_bytes``
+        the stores' device memory beyond their summaries, partial pages and
+        cold rows (mostly the K staging copy), and
+        ``reserved_total_vram_bytes`` / ``reserved_total_cpu_bytes``
+        everything held in device / pinned host memory, reservations
+        included, for a caller that budgets by the real footprint."""
         hot = hot_buf = 0
         for _, l in self._owned_layers():
             used = l.keys.nelement() * l.keys.element_size() + l.values.nelement() * l.values.element_size()
@@ -389,15 +404,19 @@ class TieredKVCache(DynamicCache):
         for store in self.cold_stores.values():
             for key, val in store.memory_bytes().items():
                 tot[key] += val
-        used_gpu = tot["page_summaries_gpu"] + tot["partial_gpu"] + tot["k_cold_gpu"] + tot["v_cold_gpu"]
+        rows_gpu = tot["k_cold_gpu"] + tot["v_cold_gpu"]
+        used_gpu = tot["page_summaries_gpu"] + tot["partial_gpu"] + rows_gpu
+        cpu_rows = tot["k_index_cpu"] + tot["v_store_cpu"]
         return {
             "hot_vram_bytes": hot,
             "k_index_cpu_bytes": tot["k_index_cpu"],
             "v_store_cpu_bytes": tot["v_store_cpu"],
             "page_summaries_gpu_bytes": tot["page_summaries_gpu"],
-            "cold_rows_gpu_bytes": tot["k_cold_gpu"] + tot["v_cold_gpu"],
+            "total_vram_bytes": hot + used_gpu,
+            "total_cpu_bytes": cpu_rows,
+            "cold_rows_gpu_bytes": rows_gpu,
             "hot_buffer_vram_bytes": hot_buf,
             "retrieval_scratch_vram_bytes": max(0, tot["reserved_gpu"] - used_gpu),
-            "total_vram_bytes": hot_buf + max(tot["reserved_gpu"], used_gpu),
-            "total_cpu_bytes": max(tot["reserved_cpu"], tot["k_index_cpu"] + tot["v_store_cpu"]),
+            "reserved_total_vram_bytes": hot_buf + max(tot["reserved_gpu"], used_gpu),
+            "reserved_total_cpu_bytes": max(tot["reserved_cpu"], cpu_rows),
         }

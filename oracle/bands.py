@@ -32,10 +32,8 @@ U32 = 2.0 ** -24
 def score_interval(q: np.ndarray, keys: np.ndarray, scaling: float, dtype: str, rounding: str):
     """(lo, hi) kernel-score bounds, [B, Hq, Q, T] each."""
     groups = q.shape[1] // keys.shape[1]
-    q64 = q.astype(np.float64)
-    k64 = exact.expand_kv(keys.astype(np.float64), groups)
-    dot = np.einsum("bhqd,bhtd->bhqt", q64, k64)
-    mag = np.einsum("bhqd,bhtd->bhqt", np.abs(q64), np.abs(k64))
+    dot = exact.grouped_dots(q, keys, groups)
+    mag = exact.grouped_dots(q, keys, groups, absolute=True)
     delta = (q.shape[-1] + 4) * U32 * mag
     if rounding == "fp32":
         lo = (dot - delta).astype(np.float32).astype(np.float64) * scaling

@@ -68,16 +68,26 @@ def page_means(k_cold: np.ndarray, page_size: int) -> np.ndarray:
 
 # -------------------------------------------------------------------- scores
 
+def grouped_dots(q: np.ndarray, keys: np.ndarray, groups: int, absolute: bool = False) -> np.ndarray:
+    """Exact (float64) q.k of q [B, Hq, Q, D] against keys [B, Hkv, T, D]:
+    [B, Hq, Q, T], q head h against kv head h // groups, without
+    materialising the expanded keys.  ``absolute``: sum of |q_i k_i|."""
+    B, Hq, Q, D = q.shape
+    q64 = q.astype(np.float64).reshape(B, Hq // groups, groups, Q, D)
+    k64 = keys.astype(np.float64)
+    if absolute:
+        q64, k64 = np.abs(q64), np.abs(k64)
+    return np.matmul(q64, k64[:, :, None].swapaxes(-1, -2)).reshape(B, Hq, Q, keys.shape[2])
+
+
 def scores64(q: np.ndarray, keys: np.ndarray, scaling: float, groups: int) -> np.ndarray:
     """q [B, Hq, Q, D] against keys [B, Hkv, T, D]: [B, Hq, Q, T] float64 q.k * scaling."""
-    kx = expand_kv(keys.astype(np.float64), groups)
-    return np.einsum("bhqd,bhtd->bhqt", q.astype(np.float64), kx) * scaling
+    return grouped_dots(q, keys, groups) * scaling
 
 
 def dots32(q: np.ndarray, keys: np.ndarray, groups: int) -> np.ndarray:
     """fp32 dot products (fp64 accumulation rounded once to fp32)."""
-    kx = expand_kv(keys.astype(np.float64), groups)
-    return np.einsum("bhqd,bhtd->bhqt", q.astype(np.float64), kx).astype(np.float32)
+    return grouped_dots(q, keys, groups).astype(np.float32)
 
 
 # ----------------------------------------------------------------- selection

@@ -204,6 +204,7 @@ class OracleColdStore:
             coarse = torch.matmul(query, expand_kv(summ, self.groups).transpose(-2, -1)) * scaling
             _, top_idx = coarse.topk(min(top_pages, self.num_pages), dim=-1)
             pages = top_idx.reshape(-1).unique(sorted=True)
+            trace.extra["top_idx"] = top_idx
             tok = (pages[:, None] * ps + torch.arange(ps)[None, :]).reshape(-1)
             ks.append(kall[:, :, tok])
             vs.append(vall[:, :, tok])
@@ -242,14 +243,47 @@ class OracleColdStore:
             if step >= 0:
                 self.cached_step = step
             trace.extra["reused"] = False
+        k_out, v_out = self._fine(query, ck, cv, cid, scaling, P, trace)
+        self.telemetry.fine(trace.agg_scores, trace.selected_ids, int(trace.top_local.shape[-1]), int(top_p),
+                            self.cold_length)
+        return k_out, v_out, trace
+
+    def _fine(self, query, ck, cv, cid, scaling: float, P: int, trace: RetrieveTrace):
+        """kiv/cold_store.py:332-362: fine scores in the dtype, max over heads
+        and positions, top-P descending, gather."""
         fine = torch.matmul(query, expand_kv(ck, self.groups).transpose(-2, -1)) * scaling
         agg = fine.amax(dim=(1, 2))
         _, top_local = agg.topk(min(P, agg.shape[-1]), dim=-1)
         idx = top_local[:, None, :, None].expand(-1, ck.shape[1], -1, ck.shape[3])
         trace.candidate_ids, trace.agg_scores, trace.top_local = cid, agg, top_local
         trace.selected_ids = cid[top_local]
-        self.telemetry.fine(agg, trace.selected_ids, int(top_local.shape[-1]), int(top_p), self.cold_length)
-        return torch.gather(ck, 2, idx), torch.gather(cv, 2, idx), trace
+        return torch.gather(ck, 2, idx), torch.gather(cv, 2, idx)
+
+    def retrieve_given_union(self, query: torch.Tensor, scaling: float, top_p: int, pages) -> RetrieveTrace:
+        """The fine stage of kiv/cold_store.py:283-371 over the candidates of a
+        given page union (ascending page ids; the partial page's tokens last,
+        as at :227-262), with no telemetry: the reference's top-P conditioned
+        on a union, so that a parity test can check the fine selection apart
+        from the coarse one."""
+        trace = RetrieveTrace()
+        ps = self.page_size
+        pages = torch.as_tensor(pages, dtype=torch.int64).reshape(-1)
+        ks, vs, ids = [], [], []
+        if pages.numel():
+            _, kall, vall = self.flat()
+            tok = (pages[:, None] * ps + torch.arange(ps)[None, :]).reshape(-1)
+            ks.append(kall[:, :, tok])
+            vs.append(vall[:, :, tok])
+            ids.append(tok)
+        if self.partial_len:
+            n_fin = self.num_pages * ps
+            ks.append(self.partial_k)
+            vs.append(self.partial_v)
+            ids.append(torch.arange(n_fin, n_fin + self.partial_len))
+        trace.pages = pages
+        P = min(top_p, self.cold_length)
+        self._fine(query, torch.cat(ks, dim=2), torch.cat(vs, dim=2), torch.cat(ids), scaling, P, trace)
+        return trace
 
 
 def eager_attention(query, key, value, mask, scaling):

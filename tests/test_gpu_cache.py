@@ -199,10 +199,16 @@ def test_memory_bytes_and_report(cuda, tier):
     assert rep["hot_vram_bytes"] == 2 * B * hkv * hot * D * eb
     assert rep["k_index_cpu_bytes"] == mem["k_index_cpu"] and rep["v_store_cpu_bytes"] == mem["v_store_cpu"]
     assert rep["page_summaries_gpu_bytes"] == mem["page_summaries_gpu"]
+    # The reference's totals: bytes in use (kiv/tiered_cache.py:279-286), plus HBM-resident cold rows.
+    assert rep["total_vram_bytes"] == rep["hot_vram_bytes"] + gpu_used
+    assert rep["total_cpu_bytes"] == cpu_rows
+    assert rep["cold_rows_gpu_bytes"] == mem["k_cold_gpu"] + mem["v_cold_gpu"]
+    if tier == "host":
+        assert rep["total_vram_bytes"] == rep["hot_vram_bytes"] + mem["page_summaries_gpu"] + mem["partial_gpu"]
+    # Reservations, reported apart.
     assert rep["hot_buffer_vram_bytes"] >= rep["hot_vram_bytes"]
-    assert rep["total_vram_bytes"] == rep["hot_buffer_vram_bytes"] + mem["reserved_gpu"]
-    assert rep["total_vram_bytes"] >= rep["hot_vram_bytes"] + mem["page_summaries_gpu"] + mem["partial_gpu"]
-    assert rep["total_cpu_bytes"] == max(mem["reserved_cpu"], cpu_rows)
+    assert rep["reserved_total_vram_bytes"] == rep["hot_buffer_vram_bytes"] + mem["reserved_gpu"]
+    assert rep["reserved_total_cpu_bytes"] == max(mem["reserved_cpu"], cpu_rows)
     assert rep["retrieval_scratch_vram_bytes"] == mem["reserved_gpu"] - gpu_used
 
 

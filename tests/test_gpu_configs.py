@@ -39,7 +39,7 @@ from kiv_amd import ColdKVStore, KIVConfig, ModelTopology
 from kiv_amd.synthetic import WORKLOADS, Workload, generate
 from oracle import exact
 from oracle.torch_ref import OracleColdStore
-from tests.test_gpu_retrieval import attention_check, check_retrieval
+from tests.test_gpu_retrieval import attention_check, check_retrieval, separation_line
 
 pytestmark = pytest.mark.gpu
 
@@ -107,6 +107,7 @@ def test_config_at_stated_size(cuda, key):
         runs[prune] = (k_out, v_out, sel, info["union"], store.fine_scan_stats())
         print(f"  pruning={prune}: union {len(info['union'])} pages, determined coarse {info['det_c']:.2f} "
               f"fine {min(info['det_f']):.2f}, slices read {runs[prune][4]}", flush=True)
+        print("  " + separation_line(info["separation"]), flush=True)
     (k0, v0, sel0, u0, s0), (k1, v1, sel1, u1, s1) = runs[False], runs[True]
     assert u0 == u1 and np.array_equal(sel0, sel1)
     assert torch.equal(k0, k1) and torch.equal(v0, v1)
@@ -140,6 +141,8 @@ def test_headline_shape_separated_selection(cuda, pruning):
     k_out, v_out, sel = check_retrieval(store, oracle, cfg, w, host, host["q"], min_det_c=0.0, info=info)
     print(f"separated ({'pruned' if pruning else 'full'} fine scan): union {len(info['union'])}, determined "
           f"coarse {info['det_c']:.2f} fine {info['det_f'][0]:.2f}, slices {store.fine_scan_stats()}", flush=True)
+    print("  " + separation_line(info["separation"]), flush=True)
+    assert info["separation"]["fine"][0]["differ"] == 0
     assert info["det_f"] == [1.0]
     want = set(planted.cpu().tolist())
     assert set(sel[0].tolist()) == want

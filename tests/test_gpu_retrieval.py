@@ -25,7 +25,7 @@ from kiv_amd.attention import decode_attention
 from kiv_amd.synthetic import WORKLOADS, Workload, generate
 from oracle import exact
 from oracle.torch_ref import OracleColdStore
-from oracle.bands import check_topk, score_interval
+from oracle.bands import check_topk, row_bands, score_interval
 
 pytestmark = pytest.mark.gpu
 
@@ -128,9 +128,13 @@ def check_retrieval(store, oracle, cfg, w, data, q, rounding="activation", min_d
     # The CPU oracle (the reference's op sequence in the dtype) obeys the same
     # bands, and where every boundary is determined both pick the same sets.
     _, _, trace = oracle.retrieve(q64, w.scaling, cfg.top_p, cfg.top_pages)
+    ns = None
+    if rounding == "activation":
+        ns = separation_check(oracle, trace, union, sel, q64, cold_k, w, cfg, dtype,
+                              (lo_c, hi_c) if N > 0 else None, (lo_agg, hi_agg))
     if info is not None:
         info.update(union=union, det_c=det_c, det_f=det_f, oracle_pages=trace.pages,
-                    oracle_selected=trace.selected_ids, trace=trace)
+                    oracle_selected=trace.selected_ids, trace=trace, separation=ns)
     if rounding == "activation":
         if N > 0:
             check_topk(set(trace.pages.tolist()), lo_c, hi_c, min(cfg.top_pages, N))
@@ -143,6 +147,84 @@ def check_retrieval(store, oracle, cfg, w, data, q, rounding="activation", min_d
                 if det_f[b] == 1.0:
                     assert osel == set(sel[b].tolist())
     return k_out, v_out, sel
+
+
+def page_means64(cold_k: torch.Tensor, page_size: int, piece: int = 512) -> np.ndarray:
+    """fp64 means of the finished pages of host rows [B, H, T, D]: [B, H, N, D], in pieces."""
+    B, H, T, D = cold_k.shape
+    N = T // page_size
+    out = np.empty((B, H, N, D))
+    for p0 in range(0, N, piece):
+        p1 = min(N, p0 + piece)
+        out[:, :, p0:p1] = exact.page_means(cold_k[:, :, p0 * page_size:p1 * page_size].double().numpy(), page_size)
+    return out
+
+
+def separation_check(oracle, trace, union, sel, q, cold_k, w, cfg, dtype, coarse_bands, fine_bands) -> dict:
+    """The parity rule in its own terms: ids may differ from the reference's
+    only where the scores are within 1e-3 of the selection boundary.
+
+    Coarse: every page on which the union differs from the oracle's has a
+    gap of at most 1e-3 (float64 or dtype-emulated) at a row's boundary
+    (oracle/gaps.py).  Fine: the oracle's top-P over this union's
+    candidates (its fine stage conditioned on the union, so that a union
+    difference does not move the fine boundary) differs from the selection
+    only in ids within 1e-3 of the boundary.  Also returns the band widths:
+    per fine top-P the certainly-selected (must), possibly-selected (may)
+    and selected counts, and for the coarse rows the summed and largest
+    |may| - |must|."""
+    from oracle import gaps
+
+    out = {}
+    B = q.shape[0]
+    N, ps = oracle.num_pages, w.page_size
+    qn = q.double().numpy()
+    if N > 0:
+        m64 = page_means64(cold_k, ps)
+        s64 = exact.scores64(qn, m64, w.scaling, w.groups).reshape(-1, N)
+        summ = torch.cat(oracle.summaries, dim=2).double().numpy()
+        semu = exact.emulate_scores(exact.dots32(qn, summ, w.groups), w.scaling, dtype).reshape(-1, N)
+        k = min(cfg.top_pages, N)
+        ref_rows = [set(r.tolist()) for r in trace.extra["top_idx"].reshape(-1, k)]
+        c = gaps.union_differences(set(union), set(trace.pages.tolist()), s64, semu, k, ref_rows)
+        widths = [len(may) - len(must) for must, may in
+                  (row_bands(lo, hi, k) for lo, hi in zip(*coarse_bands))]
+        c.update(band_width_sum=int(sum(widths)), band_width_max=int(max(widths)))
+        assert not c["violations"], f"union pages differ beyond 1e-3 of every boundary: {c}"
+        out["coarse"] = c
+    cond = oracle.retrieve_given_union(q, w.scaling, cfg.top_p, np.array(union, dtype=np.int64))
+    cand = cond.candidate_ids
+    P = sel.shape[1]
+    assert cond.selected_ids.shape[1] == P
+    ck = cold_k[:, :, cand].double().numpy()
+    s64 = exact.scores64(qn, ck, w.scaling, w.groups).max(axis=(1, 2))
+    semu = exact.emulate_scores(exact.dots32(qn, ck, w.groups), w.scaling, dtype).max(axis=(1, 2))
+    pos = {int(g): i for i, g in enumerate(cand.tolist())}
+    out["fine"] = []
+    for b in range(B):
+        got = {pos[int(g)] for g in sel[b]}
+        ref = {pos[int(g)] for g in cond.selected_ids[b].tolist()}
+        f = gaps.topk_differences(got, ref, s64[b], semu[b], P)
+        must, may = row_bands(fine_bands[0][b], fine_bands[1][b], P)
+        f.update(must=len(must), may=len(may), selected=P, candidates=len(cand))
+        assert not f["violations"], f"fine ids differ beyond 1e-3 of the boundary: {f}"
+        out["fine"].append(f)
+    return out
+
+
+def separation_line(ns: dict) -> str:
+    """One line of separation_check's figures, for the test log."""
+    parts = []
+    c = ns.get("coarse")
+    if c:
+        parts.append(f"coarse: union {c['got']} vs oracle {c['ref']}, {c['differ']} differ (max gap f64 "
+                     f"{c['max_gap64']:.2e}, emulated {c['max_gap_emu']:.2e}, min of both {c['max_gap_min']:.2e}); "
+                     f"row bands |may|-|must| sum {c['band_width_sum']} max {c['band_width_max']}")
+    for b, f in enumerate(ns["fine"]):
+        parts.append(f"fine[{b}]: |must| {f['must']} |may| {f['may']} selected {f['selected']} of "
+                     f"{f['candidates']}; vs oracle on this union {f['differ']} differ (max gap f64 "
+                     f"{f['max_gap64']:.2e}, emulated {f['max_gap_emu']:.2e}, min of both {f['max_gap_min']:.2e})")
+    return "; ".join(parts)
 
 
 def attention_check(q, cold_k, cold_v, hot_k, hot_v, scaling, mask=None, tol=2e-3, out=None):
@@ -461,18 +543,48 @@ def test_width_depends_on_union(cuda):
 
 
 def test_reuse_candidates_by_step(cuda):
-    """Same decode step on a shared layer reuses the union (coarse skipped)."""
-    w = Workload("reuse", 8, 2, 64, torch.bfloat16, hot=8, cold=2048, top_pages=4, top_p=64, segment=256)
+    """bf16: a shared layer's call in the same decode step, with a different
+    query, skips the coarse pass and scores the first call's union with its
+    own query rows, as the oracle's reuse does (kiv/cold_store.py:303-317):
+    within the bands over that union's candidates, ids apart from the
+    oracle's only within 1e-3 of the boundary, rows bit-exact.  An eviction
+    in between drops the union (kiv/cold_store.py:148-151)."""
+    from oracle import gaps
+
+    w = Workload("reuse", 8, 2, 64, torch.bfloat16, hot=8, cold=4096 + 77, top_pages=4, top_p=64, segment=256)
     data = generate(w, seed=8)
-    store, _, cfg = build(w, data, cuda)
-    q = data["q"].to(cuda)
-    k1, v1 = store.retrieve_top_kv(q, w.scaling, cfg, step=5)
-    k2, v2 = store.retrieve_top_kv(q, w.scaling, cfg, step=5)
-    assert torch.equal(k1, k2) and torch.equal(v1, v2)
+    store, oracle, cfg = build(w, data, cuda)
+    q1 = data["q"]
+    q2 = (q1.float() + 0.5 * torch.randn(q1.shape, generator=torch.Generator().manual_seed(81))).to(w.dtype)
+    store.retrieve_top_kv(q1.to(cuda), w.scaling, cfg, step=5)
+    k2, v2 = store.retrieve_top_kv(q2.to(cuda), w.scaling, cfg, step=5)
+    _, _, t1 = oracle.retrieve(q1, w.scaling, cfg.top_p, cfg.top_pages, step=5)
+    _, _, t2 = oracle.retrieve(q2, w.scaling, cfg.top_p, cfg.top_pages, step=5)
+    assert t2.extra["reused"]
+    rec = store.telemetry_snapshot()["recent"]
+    assert rec[-2]["skipped"] is True and rec[-4]["skipped"] is False
+    union, sel = rec[-4]["pages_selected"], rec[-1]["selected_token_indices"]
+    N, ps = store.num_pages, w.page_size
+    cand = exact.candidate_ids(np.array(union, dtype=np.int64), ps, N * ps, store.cold_length - N * ps)
+    ck = data["cold_k"][:, :, torch.from_numpy(cand)]
+    lo, hi = score_interval(q2.float().numpy(), ck.float().numpy(), w.scaling, "bfloat16", "activation")
+    pos = {int(g): i for i, g in enumerate(cand)}
+    check_topk({pos[g] for g in sel}, lo.max(axis=(1, 2)), hi.max(axis=(1, 2)), w.top_p)
+    cond = oracle.retrieve_given_union(q2, w.scaling, cfg.top_p, np.array(union, dtype=np.int64))
+    if union == t1.pages.tolist():
+        assert torch.equal(cond.selected_ids, t2.selected_ids)   # the oracle's own reuse
+    s64, semu = gaps.scores_both(q2.double().numpy(), ck.double().numpy(), w.scaling, "bfloat16")
+    f = gaps.topk_differences({pos[g] for g in sel}, {pos[int(g)] for g in cond.selected_ids[0]},
+                              s64.max(axis=(1, 2))[0], semu.max(axis=(1, 2))[0], w.top_p)
+    assert not f["violations"], f
+    idx = torch.tensor(sel)
+    assert torch.equal(k2[0].cpu(), data["cold_k"][0][:, idx]) and torch.equal(v2[0].cpu(), data["cold_v"][0][:, idx])
     snap = store.telemetry_snapshot()
     assert snap["aggregates"]["coarse_real_calls"] == 1 and snap["aggregates"]["coarse_skipped_calls"] == 1
     store.evict_from_hot(data["hot_k"][:, :, :1].to(cuda), data["hot_v"][:, :, :1].to(cuda))
     assert store._cached_candidate_k is None
+    store.retrieve_top_kv(q2.to(cuda), w.scaling, cfg, step=5)  # same step, after an eviction: a fresh pass
+    assert store.telemetry_snapshot()["recent"][-2]["skipped"] is False
 
 
 def test_tie_break_lowest_index(cuda):

@@ -342,6 +342,37 @@ def test_hot_layer_appends_in_place_and_evicts_by_moving_the_start():
     assert torch.equal(layer.keys, torch.cat([ref_k, k2], 2)) and torch.equal(layer.values, torch.cat([ref_v, v2], 2))
 
 
+def test_hot_layer_defers_only_rows_the_retrieval_can_copy():
+    """A deferred update leaves rows for the retrieval's copy only when it
+    can take them (the window's dtype, unit stride over head_dim, 16-byte
+    aligned starts and strides); anything else is written at once, so a
+    reader of the returned view sees it."""
+    from kiv_amd.tiered_cache import _HotLayer
+
+    g = torch.Generator().manual_seed(1)
+    layer = _HotLayer()
+    layer.update(torch.randn(1, 2, 4, 8, generator=g), torch.randn(1, 2, 4, 8, generator=g))
+    ok_k, ok_v = torch.randn(1, 2, 1, 8, generator=g), torch.randn(1, 2, 1, 8, generator=g)
+    layer.defer_append = True
+    layer.update(ok_k, ok_v)
+    assert layer._pending_rows is not None      # left to the retrieval
+    layer.flush()
+    assert torch.equal(layer.keys[:, :, -1:], ok_k) and torch.equal(layer.values[:, :, -1:], ok_v)
+    wide = torch.randn(1, 2, 1, 9, generator=g)
+    cases = {
+        "head_dim stride 2": (torch.randn(1, 2, 1, 16, generator=g)[..., ::2], ok_v),
+        "start off 16 bytes": (wide[..., 1:], ok_v),
+        "row stride not a 16-byte multiple": (torch.randn(1, 2, 9, 1, generator=g).transpose(2, 3)[..., :8], ok_v),
+        "other dtype": (ok_k.double(), ok_v),
+    }
+    for name, (k, v) in cases.items():
+        layer.defer_append = True
+        layer.update(k, v)
+        assert layer._pending_rows is None, name   # written at once
+        assert torch.equal(layer.keys[:, :, -1:], k.to(layer.keys.dtype)), name
+        assert torch.equal(layer.values[:, :, -1:], v), name
+
+
 def test_tiered_cache_uses_buffered_hot_layers_for_owned_layers():
     from transformers import Qwen2Config
 
