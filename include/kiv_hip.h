@@ -81,18 +81,21 @@ typedef struct {
   int64_t reserved_host_bytes;   /* what it holds in pinned host memory (the arena's chunks) */
 } kiv_store_info_t;
 
-/* Retrieval flags.  KIV_RETRIEVE_PRUNE: on the host tier, the coarse scan
- * also bounds every page's token scores (from a per-page radius recorded at
- * eviction) and the fine scan reads only the pages whose bound can reach
- * the top P' (a threshold from the pages' lower bounds).  The top pages of
- * each kv row's first query row are read before the threshold is known
- * and dropped unscored if they miss it (at most 4 page reads per kv row
- * over the pruned set).  The selection,
- * its order and the returned rows are unchanged; the fine telemetry's mean
- * then covers the scored candidates only.  Applies to one-pass queries
- * whose fine scan runs on the vector units (G * Q < 32) with a fresh
- * coarse pass and a positive scaling; it pauses itself for 32 calls after
- * a call that skipped under a quarter of the union. */
+/* Retrieval flags.  KIV_RETRIEVE_PRUNE: the coarse scan also bounds every
+ * page's token scores (from a per-page radius recorded at eviction) and the
+ * fine scan reads only the (page, kv row) slices whose bound can reach the
+ * top P' (a threshold from the pages' lower bounds).  On the host tier the
+ * top pages of each kv row's first query row are read before the threshold
+ * is known and dropped unscored if they miss it (at most 4 page reads per
+ * kv row over the pruned set).  The selection, its order and the returned
+ * rows are unchanged; the fine telemetry's mean then covers the scored
+ * candidates only.  Applies to one-pass queries with a fresh coarse pass
+ * and a positive scaling: on the host tier when the fine scan runs on the
+ * vector units (G * Q < 32); on the hbm and split tiers when G * Q < 32 and
+ * the union's K could exceed 256 MiB (its upper bound: every query row's
+ * top pages distinct), below which the full matrix-core scan of K in HBM is
+ * faster.  It pauses itself for 32 calls after a call that skipped under a
+ * quarter of the union. */
 enum { KIV_RETRIEVE_PRUNE = 1 };
 
 /* Arguments of one retrieval: coarse page scan, union of per-row top

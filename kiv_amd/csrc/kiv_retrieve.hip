@@ -58,6 +58,16 @@ inline size_t stage_cap() {
   const char *e = std::getenv("KIV_STAGE_CAP_BYTES");
   return e && *e ? (size_t)std::strtoull(e, nullptr, 10) : kMaxStageBytes;
 }
+// Pruning on the HBM-resident tiers: when the union's K could exceed this
+// many bytes (the full scan's upper bound), or KIV_PRUNE_DEVICE_BYTES from
+// the environment (tests force it with 0).  Measured on MI355X: the pruned
+// VALU pass costs a fixed ~8 us more than the full MFMA scan of a 20 MB
+// union, and the full scan grows by about 0.7 us per MB.
+constexpr int64_t kPruneDeviceBytes = int64_t(256) << 20;
+inline int64_t prune_device_bytes() {
+  const char *e = std::getenv("KIV_PRUNE_DEVICE_BYTES");
+  return e && *e ? (int64_t)std::strtoll(e, nullptr, 10) : kPruneDeviceBytes;
+}
 constexpr int64_t kFineQueryBytes = 48 << 10;  // query rows per kv row the fine scan keeps in LDS
 constexpr int64_t kRowListInScan = 8192;        // row-list entries a fine-scan block ORs into its union
 constexpr int kUnionThreads = 1024;
@@ -1977,11 +1987,13 @@ template <int DT> __device__ void gather_block(const GatherArgs &ga, int bx, int
     int64_t gid;
     bool staged = k_stage != nullptr;
     if (cand < split) {
+      // K of a page is [kv row][token][D], V [token][kv row][D].
       const int64_t page = page_list[cand / page_size], t = cand % page_size;
-      const int64_t off = (page & ((int64_t(1) << chunk_shift) - 1)) * page_bytes +
-                          (((int64_t)r * page_size + t) * head_dim + e0) * EB;
-      ks = reinterpret_cast<const char *>(ktab[page >> chunk_shift]) + off;
-      vs = reinterpret_cast<const char *>(vtab[page >> chunk_shift]) + off;
+      const int64_t base = (page & ((int64_t(1) << chunk_shift) - 1)) * page_bytes;
+      ks = reinterpret_cast<const char *>(ktab[page >> chunk_shift]) + base +
+           (((int64_t)r * page_size + t) * head_dim + e0) * EB;
+      vs = reinterpret_cast<const char *>(vtab[page >> chunk_shift]) + base +
+           ((t * ga.batch * hkv + r) * head_dim + e0) * EB;
       gid = page * page_size + t;
       // A pruned scan staged the slice only if its bound reached T.
       if (ga.ub) {
@@ -2170,15 +2182,25 @@ static int retrieve_impl(kiv_store_t *s, const kiv_retrieve_args_t *a, hipStream
   // and row lists longer than the pages the top P' can fill.  The bounds
   // come from the MFMA coarse scan (or page_bound_kernel after a VALU one).
   const bool host_tier = c.cold_tier == KIV_TIER_HOST;
-  const int ktf = D / 32;
-  const bool fine_mfma = dt != KIV_DTYPE_F32 && D % 32 == 0 && (ktf <= 4 || ktf == 6 || ktf == 8) &&
-                         (G * Qb >= kFineMfmaRows || !host_tier) && a->scaling > 0.f;
   // Shared-layer reuse (kiv/cold_store.py:303-317): the union of the last
   // coarse pass serves a query of any length; the fine scan scores it with
   // this query's rows.
   const bool fresh = N > 0 && !a->reuse_candidates;
-  const bool prune = (a->flags & KIV_RETRIEVE_PRUNE) && host_tier && !fine_mfma && passes == 1 && fresh &&
-                     std::max(1, (a->out_width + ps - 1) / ps) < std::min(a->top_pages, N) && a->scaling > 0.f;
+  // Pruning applies on the host tier, and on the HBM-resident tiers (K in
+  // HBM) when the full scan's K reads could exceed prune_device_bytes() (an
+  // upper bound: every row's top pages distinct), where the full MFMA scan
+  // costs more than the pruned pass's fixed prologue.
+  const int64_t umax_fine = N > 0 ? std::min<int64_t>(N, (int64_t)rows * std::min(a->top_pages, N)) : 0;
+  const bool big_union = umax_fine * s->kr * ps * s->row_bytes > prune_device_bytes();
+  const bool prune_ok = (a->flags & KIV_RETRIEVE_PRUNE) && passes == 1 && fresh &&
+                        std::max(1, (a->out_width + ps - 1) / ps) < std::min(a->top_pages, N) && a->scaling > 0.f &&
+                        (host_tier || (big_union && G * Qb < kFineMfmaRows));
+  const int ktf = D / 32;
+  // The MFMA fine scan serves queries of many rows per kv row on every
+  // tier, and every unpruned query on the HBM-resident tiers.
+  const bool fine_mfma = dt != KIV_DTYPE_F32 && D % 32 == 0 && (ktf <= 4 || ktf == 6 || ktf == 8) &&
+                         (G * Qb >= kFineMfmaRows || (!host_tier && !prune_ok)) && a->scaling > 0.f;
+  const bool prune = prune_ok && !fine_mfma;
   FinePrune pr{};
   const uint32_t *pr_ub = nullptr, *pr_thr = nullptr;  // page bounds and thresholds of a pruned fine scan
   int32_t *pr_ctl = nullptr;
@@ -2391,7 +2413,7 @@ static int retrieve_impl(kiv_store_t *s, const kiv_retrieve_args_t *a, hipStream
   if (c.cold_tier == KIV_TIER_HOST && stage_bytes <= cap_bytes) {
     if ((rc = s->k_stage.ensure(stage_bytes, st, false))) return rc;
     k_stage = (char *)s->k_stage.ptr;
-  } else if (prune) {
+  } else if (prune && host_tier) {
     // Too many candidates to stage by index: the pruned scan stages its
     // first scap slices per kv row compactly (4x the pages the top P' fills).
     const int64_t slice_bytes = (int64_t)ps * s->row_bytes;
@@ -2418,7 +2440,11 @@ static int retrieve_impl(kiv_store_t *s, const kiv_retrieve_args_t *a, hipStream
     tpi = std::min(tpi, ps);
     const int nsplit = (ps + tpi - 1) / tpi;
     const int64_t max_items = umax * nsplit + (s->partial_len + tpi - 1) / tpi;
-    const int64_t want = host_tier ? 1024 : 2048;
+    // A pruned scan on the HBM-resident tiers reads few slices, and every
+    // block repeats the threshold's prologue (the union pages' bound keys
+    // of every kv row): 256 blocks (Phi-3.5 MHA shape, 872 union pages x
+    // 32 kv rows: 2048 blocks 54.3 us).
+    const int64_t want = host_tier ? 1024 : (prune ? 256 : 2048);
     const int64_t nb = std::max<int64_t>(1, std::min<int64_t>(max_items, (want + s->kr - 1) / s->kr));
     // The speculative pages: one block per slice, so at most nb / nsplit.
     if (spec) {
@@ -2432,8 +2458,7 @@ static int retrieve_impl(kiv_store_t *s, const kiv_retrieve_args_t *a, hipStream
     // Host-tier decode keeps the VALU scan's small slices, which stream the
     // host link best.
     const int kt = D / 32;
-    const bool mfma = dt != KIV_DTYPE_F32 && D % 32 == 0 && (kt <= 4 || kt == 6 || kt == 8) &&
-                      (G * Qb >= kFineMfmaRows || !host_tier) && a->scaling > 0.f;
+    const bool mfma = fine_mfma;
     if (mfma) {
       tpi = std::min(kFineMfmaTok, ps);
     }

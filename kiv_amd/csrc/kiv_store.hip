@@ -127,7 +127,10 @@ __global__ void __launch_bounds__(256) evict_append_kernel(
 // sequence [partial(0..p0) ; input(0..T)] sits in page i / page_size.  The
 // block streams the page's K and V rows into the arena and reduces K over
 // the page's tokens in fp64; the mean is rounded to fp32 (summ32) and RNE to
-// the dtype (summ).
+// the dtype (summ).  A page's K is row-major ([kr][page_size][D]: the fine
+// scan reads (page, kv row) slices) and its V token-major
+// ([page_size][kr][D]: the gather reads a selected token's V for every kv
+// row as one contiguous run).
 template <int DT>
 __global__ void __launch_bounds__(256) evict_finalize_kernel(
     const char *__restrict__ part_k, const char *__restrict__ part_v, int64_t p0,
@@ -148,7 +151,7 @@ __global__ void __launch_bounds__(256) evict_finalize_kernel(
   const int64_t in_chunk = page & ((int64_t(1) << chunk_shift) - 1);
   const int64_t row_off = (int64_t)r * page_size * head_dim * EB;
   char *kdst = reinterpret_cast<char *>(ktab[page >> chunk_shift]) + in_chunk * page_bytes + row_off;
-  char *vdst = reinterpret_cast<char *>(vtab[page >> chunk_shift]) + in_chunk * page_bytes + row_off;
+  char *vdst = reinterpret_cast<char *>(vtab[page >> chunk_shift]) + in_chunk * page_bytes + (int64_t)r * head_dim * EB;
 
   // Token t of the page: K / V chunk c in the partial page or the input.
   auto src_k = [&](int t) -> const char * {
@@ -173,7 +176,7 @@ __global__ void __launch_bounds__(256) evict_finalize_kernel(
       const uint4 vq = *reinterpret_cast<const uint4 *>(vs);
       const int64_t doff = ((int64_t)t * head_dim + (int64_t)c * VEC) * EB;
       *reinterpret_cast<uint4 *>(kdst + doff) = kq;
-      *reinterpret_cast<uint4 *>(vdst + doff) = vq;
+      *reinterpret_cast<uint4 *>(vdst + ((int64_t)t * kr * head_dim + (int64_t)c * VEC) * EB) = vq;
       float x[VEC];
       load_chunk<DT>(&kq, x);
 #pragma unroll
@@ -251,10 +254,11 @@ __global__ void __launch_bounds__(256) read_tokens_kernel(
   const char *vs;
   if (tok < num_finalized) {
     const int64_t page = tok / page_size, t = tok % page_size;
-    const int64_t off = (page & ((int64_t(1) << chunk_shift) - 1)) * page_bytes +
-                        (((int64_t)r * page_size + t) * row_elems + (int64_t)c * vec) * eb;
-    ks = reinterpret_cast<const char *>(ktab[page >> chunk_shift]) + off;
-    vs = reinterpret_cast<const char *>(vtab[page >> chunk_shift]) + off;
+    const int64_t base = (page & ((int64_t(1) << chunk_shift) - 1)) * page_bytes;
+    ks = reinterpret_cast<const char *>(ktab[page >> chunk_shift]) + base +
+         (((int64_t)r * page_size + t) * row_elems + (int64_t)c * vec) * eb;
+    vs = reinterpret_cast<const char *>(vtab[page >> chunk_shift]) + base +
+         ((t * kr + r) * row_elems + (int64_t)c * vec) * eb;
   } else {
     const int64_t t = tok - num_finalized;
     const int64_t off = (((int64_t)r * page_size + t) * row_elems + (int64_t)c * vec) * eb;

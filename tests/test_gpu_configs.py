@@ -150,6 +150,39 @@ def test_headline_shape_separated_selection(cuda, pruning):
     idx = torch.from_numpy(sel[0])
     assert torch.equal(k_out[0].cpu(), host["cold_k"][0][:, idx]) and torch.equal(v_out[0].cpu(), host["cold_v"][0][:, idx])
     attention_check(data["q"], k_out, v_out, data["hot_k"], data["hot_v"], w.scaling)
+    # The decode step's call (retrieval and attention in one; with pruning,
+    # the fine select runs inside the gather's launch): the same selection.
+    out = store.retrieve_attend(data["q"], w.scaling, cfg, data["hot_k"], data["hot_v"], None)
+    rec = store.telemetry_snapshot()["recent"][-1]
+    assert rec["selected_token_indices"] == sel[0].tolist()
+    attention_check(data["q"], k_out, v_out, data["hot_k"], data["hot_v"], w.scaling, out=out)
+
+
+@pytest.mark.timeout(600)
+@pytest.mark.parametrize("tier", ["hbm", "split"])
+def test_mha_pruning_on_device_tiers_at_stated_size(cuda, tier):
+    """The Phi-3.5 MHA shape at 131,072 cold tokens with K in HBM: its union
+    (up to 1,024 pages x 32 kv rows) is past the device tiers' pruning
+    threshold, so the pruned fine scan runs by default; it must read a small
+    part of the union's slices and return the full MFMA scan's ids, order
+    and rows, within the bands and the 1e-3 rule against the oracle."""
+    w = WORKLOADS["phi35_128k"]
+    data = generate(w, seed=0, device=cuda)
+    cfg0 = KIVConfig(hot_budget=w.hot, top_p=w.top_p, page_size=w.page_size, top_pages=w.top_pages, cold_tier=tier)
+    store, oracle, cfg, host = fill(w, data, cuda, cfg=cfg0)
+    runs = {}
+    for prune in (True, False):
+        info = {}
+        k_out, v_out, sel = check_retrieval(store, oracle, replace(cfg, fine_pruning=prune), w, host, host["q"],
+                                            min_det_c=0.0, info=info)
+        runs[prune] = (k_out, v_out, sel, info["union"], store.fine_scan_stats())
+        print(f"  {tier} pruning={prune}: union {len(info['union'])}, slices read {runs[prune][4]}; "
+              + separation_line(info["separation"]), flush=True)
+    (k1, v1, sel1, u1, s1), (k0, v0, sel0, u0, s0) = runs[True], runs[False]
+    assert u1 == u0 and np.array_equal(sel1, sel0)
+    assert torch.equal(k1, k0) and torch.equal(v1, v0)
+    assert s0[0] == s0[1] == s1[1] and s1[0] < s1[1] // 10
+    attention_check(data["q"], k1, v1, data["hot_k"], data["hot_v"], w.scaling)
 
 
 @pytest.mark.timeout(300)

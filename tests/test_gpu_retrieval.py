@@ -379,17 +379,22 @@ PRUNE = [
 ]
 
 
+@pytest.mark.parametrize("tier", ["host", "hbm", "split"])
 @pytest.mark.parametrize("name,w,batch,clustered", PRUNE, ids=[c[0] for c in PRUNE])
-def test_fine_pruning_keeps_the_selection(cuda, name, w, batch, clustered):
-    """Host tier with the pruned fine scan against the full scan on the same
-    store: the same union, selected ids in the same order and the same K/V
-    rows bit for bit (pruning skips only slices whose upper bound is below a
-    lower bound of the P-th largest key).  Where pages were skipped the fine
-    mean, which covers the scored candidates only, differs."""
+def test_fine_pruning_keeps_the_selection(cuda, monkeypatch, name, w, batch, clustered, tier):
+    """The pruned fine scan against the full scan on the same store: the
+    same union, selected ids in the same order and the same K/V rows bit for
+    bit (pruning skips only slices whose upper bound is below a lower bound
+    of the P-th largest key).  Where pages were skipped the fine mean, which
+    covers the scored candidates only, differs.  On the HBM-resident tiers
+    pruning is forced (KIV_PRUNE_DEVICE_BYTES=0; by default it starts at
+    256 MiB of union K) and the full scan is the MFMA scan."""
     from dataclasses import replace
 
+    if tier != "host":
+        monkeypatch.setenv("KIV_PRUNE_DEVICE_BYTES", "0")
     data = generate(w, seed=2, batch=batch)
-    store, oracle, cfg = build(w, data, cuda, chunks=(3000, 1, 511))
+    store, oracle, cfg = build(w, data, cuda, chunks=(3000, 1, 511), cold_tier=tier)
     q = data["q"]
     runs = {}
     # Pruned, full, pruned again: after a call that skipped little (the
@@ -405,7 +410,7 @@ def test_fine_pruning_keeps_the_selection(cuda, name, w, batch, clustered):
     (k1, v1, u1, f1, s1), (k0, v0, u0, f0, s0), (k2, v2, u2, f2, s2) = runs[0], runs[1], runs[2]
     assert u2 == u0 and f2["selected_token_indices"] == f0["selected_token_indices"]
     assert torch.equal(k2, k0) and torch.equal(v2, v0) and s2 == (s1 if clustered else s0)  # pruning kept / paused
-    print(f"{name}: union {len(u1)} pages, slices read pruned {s1} full {s0}, "
+    print(f"{name} ({tier}): union {len(u1)} pages, slices read pruned {s1} full {s0}, "
           f"fine mean pruned {f1['mean_score']} full {f0['mean_score']}", flush=True)
     assert s0[0] == s0[1] == s1[1] == len(u1) * batch * w.num_kv_heads and s1[0] <= s1[1]
     assert u1 == u0
