@@ -516,19 +516,32 @@ def profile_pass(w, args, dev, scrub):
                       "us_per_step": round(us, 2), "calibration_copy_bytes": 64 << 20}), flush=True)
 
 
-def load_pmc(kernel, workload):
-    """HBM bytes per launch of `kernel` from the rocprofv3 --pmc summary committed under
-    profiles/ (FETCH_SIZE and WRITE_SIZE, scaled by the same counters' reading for a copy
-    kernel of known size), or None when there is none."""
-    path = os.path.join(ROOT, "profiles", f"{kernel}_{workload}_pmc.txt")
+# Kernel families of the decode step in the counter summaries.
+STAGE_KERNELS = {"coarse_scan": "coarse_scan", "coarse_select": "coarse_select", "fine_scan": "fine_scan",
+                 "fine_select": "fine_select", "gather": "gather", "attend": "decode_attn_final"}
+
+
+def load_pmc(workload, tier):
+    """Memory traffic per launch of each decode-step kernel, from the rocprofv3
+    --pmc summary committed under profiles/ (median per dispatch of the L2's
+    read and write requests by destination, in 32-byte units: HBM and the
+    host link), as {stage: {"hbm_read", "hbm_write", "host_read",
+    "host_write", "traffic"}} in bytes, or {} when there is none."""
+    path = os.path.join(ROOT, "profiles", f"decode_step_{workload}_{tier}_pmc.txt")
+    out = {}
     if not os.path.exists(path):
-        return None
+        return out
     with open(path) as f:
         for line in f:
-            key, _, value = line.partition("=")
-            if key.strip() == "traffic_bytes_per_launch":
-                return int(value)
-    return None
+            parts = line.split()
+            if len(parts) != 6 or not parts[0].startswith("kiv::"):
+                continue
+            for stage, fam in STAGE_KERNELS.items():
+                if parts[0].startswith(f"kiv::{fam}_"):
+                    hr, hw, ir, iw = (int(x) for x in parts[1:5])
+                    out[stage] = {"hbm_read": hr, "hbm_write": hw, "host_read": ir, "host_write": iw,
+                                  "traffic": hr + hw + ir + iw}
+    return out
 
 
 def model_flops(cfg, tokens, chunk, cap):
@@ -876,10 +889,13 @@ def main():
     dom_name, dom = max(links.items(), key=lambda kv: kv[1]["avg_us"])
     on_host = dom["from"] == "host"
     peak = HOST_LINK_PEAK_GBS if on_host else HBM_PEAK_GBS
+    pmc = load_pmc(w.name, args.cold_tier)
+    dom_pmc = pmc.get(dom_name)
     roofline = {
         "kernel": dom_name, "bound": "host_link" if on_host else "hbm", "achieved": round(dom["GB_s"], 2),
         "peak": peak, "unit": "GB/s", "frac": round(dom["GB_s"] / peak, 4),
-        "traffic": load_pmc(dom_name, w.name), "bytes_per_launch": dom["bytes"], "avg_us": round(dom["avg_us"], 2),
+        "traffic": dom_pmc["traffic"] if dom_pmc else None,
+        "traffic_by_memory": dom_pmc, "bytes_per_launch": dom["bytes"], "avg_us": round(dom["avg_us"], 2),
         "achievable": ({"same_size_read": ceil["host_link_fine_size"], "read_256MiB": ceil["host_link_256MiB"]}
                        if on_host else {"stream_2GiB": ceil["hbm_stream_2GiB"]}),
     }
@@ -893,14 +909,19 @@ def main():
                                   "min, quartiles, max)", "GB_s": ceil["hbm_summary_size"],
                           "spread": ceil["hbm_summary_size_spread"],
                           "scan_over_floor": round(scan["GB_s"] / ceil["hbm_summary_size"], 4)},
-        "traffic": load_pmc("coarse_scan", w.name), "bytes_per_launch": scan["bytes"],
+        "traffic": pmc["coarse_scan"]["traffic"] if "coarse_scan" in pmc else None,
+        "traffic_by_memory": pmc.get("coarse_scan"), "bytes_per_launch": scan["bytes"],
         "avg_us": round(scan["avg_us"], 2),
     }
     host_link = None
     if host:
         gbs = host_bytes / (host_us * 1e-6) / 1e9
+        # Host-link bytes measured by the counters (reads and writes of host
+        # memory by the step's kernels, from the committed summary).
+        measured = sum(v["host_read"] + v["host_write"] for v in pmc.values()) if pmc else None
         host_link = {"kernels": sorted(host), "achieved": round(gbs, 2), "peak": HOST_LINK_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gbs / HOST_LINK_PEAK_GBS, 4), "bytes_per_step": host_bytes,
+                     "bytes_per_step_measured": measured,
                      "achievable": {"same_size_read": ceil["host_link_fine_size"],
                                     "read_256MiB": ceil["host_link_256MiB"]},
                      "frac_of_achievable": round(gbs / ceil["host_link_fine_size"], 4)}

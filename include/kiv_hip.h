@@ -57,9 +57,8 @@ typedef struct {
   int32_t batch;          /* B */
   int32_t num_q_heads;    /* Hq */
   int32_t num_kv_heads;   /* Hkv; Hq % Hkv == 0, q head h reads kv head h / (Hq/Hkv) */
-  int32_t head_dim;       /* D = c * (16 / element bytes), rows of c 16-byte chunks, with c one of
-                             1 2 4 6 8 10 12 14 16 20 24 28 32 40 48 64: 8..512 for bf16/fp16
-                             (e.g. 64 80 96 128 256), 4..256 for fp32 */
+  int32_t head_dim;       /* D = c * (16 / element bytes), rows of c 16-byte chunks, 1 <= c <= 64:
+                             a multiple of 8 up to 512 for bf16/fp16, of 4 up to 256 for fp32 */
   int32_t page_size;      /* tokens per page (>= 1) */
   int32_t dtype;          /* KIV_DTYPE_* of K, V, Q and outputs */
   int32_t cold_tier;      /* KIV_TIER_* placement of finished pages' rows */

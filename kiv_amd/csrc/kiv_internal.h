@@ -59,6 +59,15 @@ inline bool scan_supports_chunks(int cpr) {
   return false;
 }
 
+// Chunks per summary row for rows of cpr chunks (1 <= cpr <= 64): the
+// smallest chunk count the coarse scan is compiled for that holds them;
+// summary rows are zero-padded to it.
+inline int scan_chunks_for(int cpr) {
+  for (int c = cpr; c <= 64; ++c)
+    if (scan_supports_chunks(c)) return c;
+  return -1;
+}
+
 // Lanes that cooperate on one row: next power of two >= D / VEC.
 inline int lanes_per_row(int dtype, int head_dim) {
   int cpr = head_dim / vec_elems(dtype);
@@ -79,11 +88,13 @@ struct kiv_store {
   int64_t num_pages = 0;    // finished pages
   int64_t partial_len = 0;  // tokens in the partial page
 
-  // Page summaries in HBM: [cap][kr][D] dtype and fp32, and per page row
-  // [cap][kr][2] fp32: the radius max over its tokens of |k - s| (L2, s the
-  // dtype summary) and |s|.
+  // Page summaries in HBM: [cap][kr][summ_dim] dtype and fp32 (summ_dim =
+  // D, or D zero-padded to a chunk count the coarse scan is compiled for),
+  // and per page row [cap][kr][2] fp32: the radius max over its tokens of
+  // |k - s| (L2, s the dtype summary) and |s|.
   kiv::DevBuf summ, summ32, radius;
   int64_t summ_cap = 0;
+  int summ_dim = 0;
 
   // Arena of finished pages: equal chunks of 2^chunk_shift pages.
   int chunk_shift = 0;

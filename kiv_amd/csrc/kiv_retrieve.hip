@@ -655,11 +655,14 @@ __host__ __device__ constexpr int scan_segments(int cpr) {
   return (cpr % 4 == 0 && cpr >= 12) ? 4 : (cpr % 2 == 0 && cpr >= 6) ? 2 : 1;
 }
 
+// CPR = chunks of a summary row; the query rows have creal <= CPR chunks
+// (summary rows are zero-padded past them), and query chunks past creal are
+// taken as zero, not read.
 template <int DT, int CPR, bool Q1>
 __global__ void __launch_bounds__(kScanThreads) coarse_scan_kernel(
     const char *__restrict__ summ, int64_t n_pages, int kr, const char *__restrict__ q, int64_t qs0,
     int64_t qs1, int64_t qs2, int hq, int hkv, int qlen, float scale, int round, uint32_t *__restrict__ keys,
-    int64_t ld, AppendRows ap) {
+    int64_t ld, AppendRows ap, int creal) {
   if ((ap.count > 0 || ap.hot_count > 0) && blockIdx.x == gridDim.x - 1) {
     append_rows(ap, blockIdx.y);  // the step's evicted rows (an extra block per kv row)
     return;
@@ -698,6 +701,9 @@ __global__ void __launch_bounds__(kScanThreads) coarse_scan_kernel(
   // wave's query segments first, while the summary loads are in flight,
   // and the per-row loads below hit the scalar cache.
   constexpr int kLines = (CS * 16 + 63) / 64;
+  // This segment's chunks that exist in the query rows (all of them unless
+  // the row is padded).
+  const int cseg = min(CS, max(0, creal - seg * CS));
   {
     const int nrow = min(GQ, kScanRowTile);
     for (int j0 = 0; j0 < nrow; j0 += 8) {
@@ -706,7 +712,8 @@ __global__ void __launch_bounds__(kScanThreads) coarse_scan_kernel(
       for (int jj = 0; jj < 8; ++jj) {
         const char *qj = qseg(min(j0 + jj, nrow - 1));
 #pragma unroll
-        for (int l = 0; l < kLines; ++l) t[jj][l] = *reinterpret_cast<const uint32_t *>(qj + l * 64);
+        for (int l = 0; l < kLines; ++l)
+          t[jj][l] = 64 * l < 16 * cseg ? *reinterpret_cast<const uint32_t *>(qj + l * 64) : 0u;
       }
       uint32_t touch = 0;
 #pragma unroll
@@ -725,7 +732,7 @@ __global__ void __launch_bounds__(kScanThreads) coarse_scan_kernel(
       for (int u = 0; u < RB; ++u) {
         const char *qu = qseg(t0 + min(jt + u, nt - 1));
 #pragma unroll
-        for (int i = 0; i < CS; ++i) qv[u][i] = load16(qu + (int64_t)i * 16);
+        for (int i = 0; i < CS; ++i) qv[u][i] = i < cseg ? load16(qu + (int64_t)i * 16) : make_uint4(0, 0, 0, 0);
       }
       __builtin_amdgcn_sched_barrier(0);  // issue the batch's loads before any use
       float acc[RB];
@@ -1236,7 +1243,7 @@ __global__ void __launch_bounds__(256) page_bound_kernel(
     const int32_t *__restrict__ row_pages, int n_entries, const char *__restrict__ summ,
     const float *__restrict__ rad2, int kr, int head_dim, int hkv, const char *__restrict__ q, int64_t qs0,
     int64_t qs1, int64_t qs2, int hq, int qlen, float scale, int round, uint32_t *__restrict__ ub,
-    uint32_t *__restrict__ lb, const int32_t *__restrict__ ctl) {
+    uint32_t *__restrict__ lb, const int32_t *__restrict__ ctl, int summ_dim) {
   constexpr int EB = Elem<DT>::BYTES;
   constexpr int MV = 8;  // dims per lane (D <= 512)
   extern __shared__ float qf[];  // [G*Q][D] fp32, then [G*Q] norms
@@ -1261,7 +1268,7 @@ __global__ void __launch_bounds__(256) page_bound_kernel(
   const int e = blockIdx.x * 4 + wave;
   if (e >= n_entries) return;
   const int64_t prow = (int64_t)row_pages[e] * kr + r;
-  const char *m = summ + prow * head_dim * EB;
+  const char *m = summ + prow * summ_dim * EB;
   float mv[MV];
 #pragma unroll
   for (int i = 0; i < MV; ++i) {
@@ -2280,7 +2287,8 @@ static int retrieve_impl(kiv_store_t *s, const kiv_retrieve_args_t *a, hipStream
       if ((rc = s->row_pages.ensure((size_t)rows * kc * 4, st, false))) return rc;
       if ((rc = s->page_list.ensure((size_t)N * 4, st, false))) return rc;
       const int kt = D / 32;
-      const bool mfma = dt != KIV_DTYPE_F32 && D % 32 == 0 && (kt <= 4 || kt == 6 || kt == 8 || kt == 16);
+      const bool mfma = dt != KIV_DTYPE_F32 && D % 32 == 0 && (kt <= 4 || kt == 6 || kt == 8 || kt == 16) &&
+                        s->summ_dim == D;
       int row0 = 0;
       for (int pass = 0; pass < passes; ++pass) {
         const int Qp = std::min(Qb, Q - pass * Qb);
@@ -2311,17 +2319,18 @@ static int retrieve_impl(kiv_store_t *s, const kiv_retrieve_args_t *a, hipStream
           });
         } else {
           // Pages per block: 64 per page group, 4 / segments page groups.
-          const int segs = scan_segments(cpr);
+          const int scpr = s->summ_dim / vec;  // chunks of a (padded) summary row
+          const int segs = scan_segments(scpr);
           const int pages_per_block = (kScanThreads / 64 / segs) * 64;
           const int blocks = (int)(((int64_t)N + pages_per_block - 1) / pages_per_block);
           rc = with_dt(dt, [&](auto dtc) {
-            return with_cpr(cpr, [&](auto cc) {
+            return with_cpr(scpr, [&](auto cc) {
               constexpr int DTV = decltype(dtc)::value, CPRV = decltype(cc)::value;
               auto kern = Qp == 1 ? coarse_scan_kernel<DTV, CPRV, true> : coarse_scan_kernel<DTV, CPRV, false>;
               hipLaunchKernelGGL(kern, dim3(blocks + extra, s->kr), dim3(kScanThreads), 0, st,
                                  (const char *)s->summ.ptr, (int64_t)N, s->kr, qp, a->q_stride[0], a->q_stride[1],
                                  a->q_stride[2], hq, hkv, Qp, a->scaling, round, (uint32_t *)s->coarse_keys.ptr, ld,
-                                 apass);
+                                 apass, cpr);
               return (int)KIV_OK;
             });
           });
@@ -2348,7 +2357,7 @@ static int retrieve_impl(kiv_store_t *s, const kiv_retrieve_args_t *a, hipStream
                              (size_t)G * Q * (D + 1) * 4, st, (const int32_t *)s->row_pages.ptr, n_entries,
                              (const char *)s->summ.ptr, (const float *)s->radius.ptr, s->kr, D, hkv,
                              (const char *)a->q, a->q_stride[0], a->q_stride[1], a->q_stride[2], hq, Q,
-                             a->scaling, round, (uint32_t *)pr.ub, (uint32_t *)pr.lb, pr.ctl);
+                             a->scaling, round, (uint32_t *)pr.ub, (uint32_t *)pr.lb, pr.ctl, s->summ_dim);
           return (int)KIV_OK;
         });
         if (rc) return rc;

@@ -138,7 +138,7 @@ __global__ void __launch_bounds__(256) evict_finalize_kernel(
     int64_t ks2, int64_t vs0, int64_t vs1, int64_t vs2, int hkv, int kr, int head_dim,
     int page_size, int64_t first_page, const uint64_t *__restrict__ ktab,
     const uint64_t *__restrict__ vtab, int chunk_shift, int64_t page_bytes, void *__restrict__ summ,
-    float *__restrict__ summ32, float *__restrict__ radius) {
+    float *__restrict__ summ32, float *__restrict__ radius, int summ_dim) {
   constexpr int VEC = Elem<DT>::VEC, EB = Elem<DT>::BYTES;
   __shared__ double red[256 * VEC];
   __shared__ float mu[512], part[256], gmax[256];
@@ -186,11 +186,16 @@ __global__ void __launch_bounds__(256) evict_finalize_kernel(
     for (int e = 0; e < VEC; ++e) red[g * head_dim + c * VEC + e] = acc[e];
   }
   __syncthreads();
-  for (int d = threadIdx.x; d < head_dim; d += 256) {
+  for (int d = threadIdx.x; d < summ_dim; d += 256) {
+    const int64_t o = ((int64_t)page * kr + r) * summ_dim + d;
+    if (d >= head_dim) {  // the row's zero padding
+      summ32[o] = 0.f;
+      store_elem<DT>(summ, o, 0.f);
+      continue;
+    }
     double s = 0.0;
     for (int gg = 0; gg < groups; ++gg) s += red[gg * head_dim + d];
     const float m32 = opaque_f32((float)(s / (double)page_size));
-    const int64_t o = ((int64_t)page * kr + r) * head_dim + d;
     summ32[o] = m32;
     store_elem<DT>(summ, o, m32);
     mu[d] = round_act<DT>(m32);  // the dtype summary the coarse scan reads
@@ -333,7 +338,7 @@ static int ensure_arena(kiv_store *s, int64_t pages, hipStream_t st) {
 static int ensure_summaries(kiv_store *s, int64_t pages, hipStream_t st) {
   if (pages <= s->summ_cap) return KIV_OK;
   int64_t cap = std::max<int64_t>(pages, std::max<int64_t>(64, s->summ_cap * 2));
-  const size_t row = (size_t)s->kr * s->cfg.head_dim;
+  const size_t row = (size_t)s->kr * s->summ_dim;
   int rc = s->summ.ensure(cap * row * elem_bytes(s->cfg.dtype), st, true);
   if (rc) return rc;
   rc = s->summ32.ensure(cap * row * 4, st, true);
@@ -396,11 +401,10 @@ int kiv_store_create(const kiv_store_config_t *cfg, int device, kiv_store_t **ou
   if (c.dtype != KIV_DTYPE_F32 && c.dtype != KIV_DTYPE_F16 && c.dtype != KIV_DTYPE_BF16)
     return fail(KIV_ERR_INVALID, "kiv_store_create: unknown dtype %d", c.dtype);
   const int vec = vec_elems(c.dtype);
-  if (c.head_dim < vec || c.head_dim % vec || !scan_supports_chunks(c.head_dim / vec))
+  if (c.head_dim < vec || c.head_dim % vec || c.head_dim / vec > 64)
     return fail(KIV_ERR_UNSUPPORTED,
-                "kiv_store_create: head_dim %d unsupported for this dtype (head_dim / %d must be one of "
-                "2 4 6 8 10 12 14 16 20 24 28 32 40 48 64)",
-                c.head_dim, vec);
+                "kiv_store_create: head_dim %d unsupported for this dtype (a multiple of %d, at most %d)",
+                c.head_dim, vec, 64 * vec);
   if (c.cold_tier != KIV_TIER_HOST && c.cold_tier != KIV_TIER_HBM && c.cold_tier != KIV_TIER_SPLIT)
     return fail(KIV_ERR_INVALID, "kiv_store_create: unknown cold_tier %d", c.cold_tier);
   if (c.score_rounding != KIV_ROUND_ACTIVATION && c.score_rounding != KIV_ROUND_FP32)
@@ -415,6 +419,7 @@ int kiv_store_create(const kiv_store_config_t *cfg, int device, kiv_store_t **ou
   s->device = device;
   s->kr = c.batch * c.num_kv_heads;
   s->row_bytes = (int64_t)c.head_dim * elem_bytes(c.dtype);
+  s->summ_dim = scan_chunks_for(c.head_dim / vec) * vec;
   s->page_bytes = (int64_t)s->kr * c.page_size * s->row_bytes;
   // Chunks of 2^k pages: at least 4 MiB each, and at most ~16 chunks for
   // the reserved capacity, so pinned allocations stay few and large.
@@ -477,7 +482,7 @@ int kiv_store_info(const kiv_store_t *s, kiv_store_info_t *out) {
   out->cold_length = s->num_pages * ps + s->partial_len;
   out->k_cold_bytes = s->num_pages * s->page_bytes;
   out->v_cold_bytes = s->num_pages * s->page_bytes;
-  out->summary_bytes = s->num_pages * s->kr * s->row_bytes;
+  out->summary_bytes = s->num_pages * s->kr * s->summ_dim * elem_bytes(s->cfg.dtype);
   out->partial_bytes = 2 * s->partial_len * s->kr * s->row_bytes;
   out->reserved_device_bytes = s->reserved_device_bytes();
   out->reserved_host_bytes = s->reserved_host_bytes();
@@ -519,7 +524,8 @@ int kiv_evict(kiv_store_t *s, const void *k, const int64_t k_stride[3], const vo
                          (const char *)s->v_part.ptr, p0, kc, vc, k_stride[0], k_stride[1], k_stride[2],
                          v_stride[0], v_stride[1], v_stride[2], hkv, s->kr, D, ps, s->num_pages,
                          (const uint64_t *)s->k_tab.ptr, (const uint64_t *)s->v_tab.ptr, s->chunk_shift,
-                         s->page_bytes, s->summ.ptr, (float *)s->summ32.ptr, (float *)s->radius.ptr);
+                         s->page_bytes, s->summ.ptr, (float *)s->summ32.ptr, (float *)s->radius.ptr,
+                         s->summ_dim);
     };
     if (dt == KIV_DTYPE_F32) launch(evict_finalize_kernel<DT_F32>);
     else if (dt == KIV_DTYPE_F16) launch(evict_finalize_kernel<DT_F16>);
@@ -555,14 +561,25 @@ int kiv_store_read_summaries(kiv_store_t *s, int64_t first, int64_t n, void *out
   if (n == 0) return KIV_OK;
   DeviceGuard guard(s->device);
   hipStream_t st = (hipStream_t)stream;
-  const size_t row = (size_t)s->kr * s->cfg.head_dim;
+  // Rows of D elements out of the summaries' rows of summ_dim.
+  const size_t D = (size_t)s->cfg.head_dim, Dp = (size_t)s->summ_dim, rows = (size_t)n * s->kr;
+  const size_t first_row = (size_t)first * s->kr;
   const int eb = elem_bytes(s->cfg.dtype);
+  if (Dp == D) {
+    if (out_dtype)
+      KIV_HIP(hipMemcpyAsync(out_dtype, (char *)s->summ.ptr + first_row * D * eb, rows * D * eb,
+                             hipMemcpyDeviceToDevice, st));
+    if (out_f32)
+      KIV_HIP(hipMemcpyAsync(out_f32, (char *)s->summ32.ptr + first_row * D * 4, rows * D * 4,
+                             hipMemcpyDeviceToDevice, st));
+    return KIV_OK;
+  }
   if (out_dtype)
-    KIV_HIP(hipMemcpyAsync(out_dtype, (char *)s->summ.ptr + first * row * eb, n * row * eb,
-                           hipMemcpyDeviceToDevice, st));
+    KIV_HIP(hipMemcpy2DAsync(out_dtype, D * eb, (char *)s->summ.ptr + first_row * Dp * eb, Dp * eb, D * eb, rows,
+                             hipMemcpyDeviceToDevice, st));
   if (out_f32)
-    KIV_HIP(hipMemcpyAsync(out_f32, (char *)s->summ32.ptr + first * row * 4, n * row * 4,
-                           hipMemcpyDeviceToDevice, st));
+    KIV_HIP(hipMemcpy2DAsync(out_f32, D * 4, (char *)s->summ32.ptr + first_row * Dp * 4, Dp * 4, D * 4, rows,
+                             hipMemcpyDeviceToDevice, st));
   return KIV_OK;
 }
 

@@ -266,6 +266,15 @@ SMALL = [
                       top_pages=4, top_p=64, segment=256), (2000,)),
     ("d112_f32", dict(num_q_heads=6, num_kv_heads=2, head_dim=112, dtype=torch.float32, cold=1500, hot=40,
                       top_pages=3, top_p=50, segment=200), (700, 800)),
+    # head dims whose summary rows the scan reads zero-padded (5, 9, 15, 5 chunks of 16 bytes)
+    ("d40_bf16", dict(num_q_heads=8, num_kv_heads=2, head_dim=40, dtype=torch.bfloat16, cold=2000, hot=64,
+                      top_pages=4, top_p=64, segment=256), (999, 1001)),
+    ("d72_f16", dict(num_q_heads=6, num_kv_heads=3, head_dim=72, dtype=torch.float16, cold=1800, hot=40,
+                     top_pages=3, top_p=60, segment=200), (1800,)),
+    ("d120_bf16_mha", dict(num_q_heads=4, num_kv_heads=4, head_dim=120, dtype=torch.bfloat16, cold=2100, hot=33,
+                           top_pages=3, top_p=100, segment=128, n_targets=4), (2048, 52)),
+    ("d20_f32", dict(num_q_heads=4, num_kv_heads=1, head_dim=20, dtype=torch.float32, cold=1500, hot=50,
+                     top_pages=5, top_p=40, segment=100), (333,)),
 ]
 
 
@@ -282,6 +291,21 @@ def test_small_parity(cuda, name, over, chunks, tier):
     check_rows(store, data)
     k_out, v_out, _ = check_retrieval(store, oracle, cfg, w, data, data["q"])
     attention_check(data["q"].to(cuda), k_out, v_out, data["hot_k"].to(cuda), data["hot_v"].to(cuda), w.scaling)
+
+
+def test_head_dim_off_the_chunk_grid_is_refused(cuda):
+    """Rows move in 16-byte chunks: a bf16 head dim that is not a multiple of
+    8 is refused at the first eviction (KIV_ERR_UNSUPPORTED), cleanly."""
+    from kiv_amd import _native as nat
+
+    cfg = KIVConfig(top_p=16, top_pages=2, page_size=16)
+    topo = ModelTopology.manual(global_layer_indices=(0,), num_query_heads=4, num_kv_heads=2, head_dim=36,
+                                num_hidden_layers=1)
+    store = ColdKVStore(cfg, topo, cuda)
+    k = torch.zeros(1, 2, 20, 36, dtype=torch.bfloat16, device=cuda)
+    with pytest.raises(nat.KivError) as err:
+        store.evict_from_hot(k, k)
+    assert err.value.code == nat.ERR_UNSUPPORTED and "head_dim 36" in str(err.value)
 
 
 @pytest.mark.parametrize("key,cold", [("tinyllama_32k", 32768), ("qwen7b_256k", 24576 + 77),
