@@ -422,10 +422,13 @@ def host_copy(store, piece=1 << 18):
 def selection_check(w, store, cfg, q, oracle, cold_k):
     """One retrieval on the GPU store against the oracle on the same rows: the
     union and the selected ids within the rounding bands (oracle.bands),
-    equal to the oracle's where the bands determine them."""
+    equal to the oracle's where the bands determine them, and every id on
+    which they differ within 1e-3 of a selection boundary in float64 or in
+    the dtype rounding (oracle.gaps; the fine ids against the oracle's top-P
+    over the same union)."""
     import numpy as np
 
-    from oracle import exact
+    from oracle import exact, gaps
     from oracle.bands import check_topk, score_interval
 
     dt = {2: "bfloat16" if "bfloat" in str(w.dtype) else "float16", 4: "float32"}[w.dtype.itemsize]
@@ -453,9 +456,31 @@ def selection_check(w, store, cfg, q, oracle, cold_k):
         equal = None
         if same_union and det_f == 1.0:
             equal = set(sel) == set(trace.selected_ids[0].tolist())
+        # The 1e-3 rule: union pages against the oracle's per-row selections,
+        # fine ids against the oracle's top-P over this union.
+        qd = q.double().cpu().numpy()
+        kc = min(cfg.top_pages, N)
+        m64 = np.concatenate([exact.page_means(cold_k[:, :, p0 * ps:min(N, p0 + 512) * ps].double().numpy(), ps)
+                              for p0 in range(0, N, 512)], axis=2)
+        osumm = torch.cat(oracle.summaries, dim=2).double().numpy()
+        c = gaps.union_differences(set(union), set(trace.pages.tolist()),
+                                   exact.scores64(qd, m64, w.scaling, w.groups).reshape(-1, N),
+                                   exact.emulate_scores(exact.dots32(qd, osumm, w.groups), w.scaling, dt).reshape(-1, N),
+                                   kc, [set(r.tolist()) for r in trace.extra["top_idx"].reshape(-1, kc)])
+        cond = oracle.retrieve_given_union(q.cpu(), w.scaling, cfg.top_p, np.array(union, dtype=np.int64))
+        ck = cold_k[:, :, cond.candidate_ids].double().numpy()
+        s64 = exact.scores64(qd, ck, w.scaling, w.groups).max(axis=(1, 2))[0]
+        semu = exact.emulate_scores(exact.dots32(qd, ck, w.groups), w.scaling, dt).max(axis=(1, 2))[0]
+        cpos = {int(g): i for i, g in enumerate(cond.candidate_ids.tolist())}
+        f = gaps.topk_differences({cpos[g] for g in sel}, {cpos[int(g)] for g in cond.selected_ids[0]}, s64, semu,
+                                  len(sel))
+        rule = {"union_ids_differing": c["differ"], "union_max_gap_f64": c["max_gap64"],
+                "union_max_gap_dtype": c["max_gap_emu"], "fine_ids_differing": f["differ"],
+                "fine_max_gap_f64": f["max_gap64"], "fine_max_gap_dtype": f["max_gap_emu"],
+                "violations": len(c["violations"]) + len(f["violations"])}
         out.update(within_bands=True, coarse_rows_determined=round(det_c, 3), fine_determined=det_f == 1.0,
-                   union_equal=same_union, selection_equal_where_determined=equal,
-                   ok=equal is not False and (det_c < 1.0 or same_union))
+                   union_equal=same_union, selection_equal_where_determined=equal, rule_1e3=rule,
+                   ok=equal is not False and (det_c < 1.0 or same_union) and rule["violations"] == 0)
     except AssertionError as e:
         out.update(within_bands=False, ok=False, error=str(e)[:200])
     return out
@@ -533,12 +558,12 @@ def load_pmc(workload, tier):
         return out
     with open(path) as f:
         for line in f:
-            parts = line.split()
-            if len(parts) != 6 or not parts[0].startswith("kiv::"):
+            parts = line.split()  # kernel name (it may hold spaces), then five byte counts
+            if len(parts) < 6 or not parts[0].startswith("kiv::"):
                 continue
             for stage, fam in STAGE_KERNELS.items():
                 if parts[0].startswith(f"kiv::{fam}_"):
-                    hr, hw, ir, iw = (int(x) for x in parts[1:5])
+                    hr, hw, ir, iw = (int(x) for x in parts[-5:-1])
                     out[stage] = {"hbm_read": hr, "hbm_write": hw, "host_read": ir, "host_write": iw,
                                   "traffic": hr + hw + ir + iw}
     return out
