@@ -535,6 +535,74 @@ __device__ int rank_union(const int32_t *row_pages, int nk, int words, uint32_t 
   return union_list<NT>(words, bits, upage, scan_tmp);
 }
 
+// Max of n consecutive bound keys (a page's kv rows of one batch row):
+// 16-byte loads when the run is aligned (kv heads a multiple of 4), so that
+// the loads are few and independent.
+__device__ __forceinline__ uint32_t max_keys(const uint32_t *p, int n) {
+  uint32_t m = 0u;
+  if (((uintptr_t)p & 15) == 0 && (n & 3) == 0) {
+    const uint4 *p4 = reinterpret_cast<const uint4 *>(p);
+#pragma unroll 4
+    for (int i = 0; i < n / 4; ++i) {
+      const uint4 x = p4[i];
+      m = max(m, max(max(x.x, x.y), max(x.z, x.w)));
+    }
+  } else {
+#pragma unroll 4
+    for (int i = 0; i < n; ++i) m = max(m, p[i]);
+  }
+  return m;
+}
+
+// Page bound tables of a pruned fine scan over many kv rows, built from the
+// bound keys ub/lb [n][kr] once they exist: lbmax[n][batch], a page's
+// largest lower-bound key over one batch row's hkv kv rows, and ubT[kr][ldn],
+// the upper-bound keys transposed.  Every fine-scan block then reads 4
+// bytes per union page for each (contiguous over ascending pages) instead
+// of an hkv-key run and one key of each page's kr-key row.  rows = 0: none.
+struct BoundTables {
+  const uint32_t *ub, *lb;
+  uint32_t *lbmax, *ubT;
+  int64_t n, ldn;
+  int kr, hkv, batch, rows;
+};
+
+// Table entries of the launch's extra blocks: the transpose's items (4 kv
+// rows of one page each when kr is a multiple of 4, else 1), then lbmax's.
+__host__ __device__ inline int64_t bound_table_items(int64_t n, int kr, int batch) {
+  return n * ((kr & 3) == 0 ? kr / 4 : kr) + n * batch;
+}
+
+// The tables, by the blocks of a launch past its first bt.rows: one item a
+// thread (n * kr < 2^31), consecutive threads on consecutive pages so that
+// the transposed stores coalesce.
+template <int NT> __device__ void fill_bound_tables(const BoundTables &bt) {
+  const int t = ((int)blockIdx.x - bt.rows) * NT + (int)threadIdx.x;
+  const int n = (int)bt.n;
+  const bool vec = (bt.kr & 3) == 0;
+  const int nt = n * (vec ? bt.kr / 4 : bt.kr);
+  if (t < nt) {
+    const int p = t % n, c = t / n;
+    if (vec) {
+      const uint4 x = *reinterpret_cast<const uint4 *>(bt.ub + (int64_t)p * bt.kr + 4 * c);
+      uint32_t *d = bt.ubT + (int64_t)4 * c * bt.ldn + p;
+      d[0] = x.x;
+      d[bt.ldn] = x.y;
+      d[2 * bt.ldn] = x.z;
+      d[3 * bt.ldn] = x.w;
+    } else {
+      bt.ubT[(int64_t)c * bt.ldn + p] = bt.ub[(int64_t)p * bt.kr + c];
+    }
+  } else if (t < nt + n * bt.batch) {
+    const int j = t - nt;
+    bt.lbmax[j] = max_keys(bt.lb + (int64_t)(j / bt.batch) * bt.kr + (int64_t)(j % bt.batch) * bt.hkv, bt.hkv);
+  }
+}
+
+// The bound tables in a launch of their own (rows = 0), after the page
+// bounds' kernel (which runs after the coarse select).
+__global__ void __launch_bounds__(256) bound_tables_kernel(BoundTables bt) { fill_bound_tables<256>(bt); }
+
 // Union of long row lists (several query passes, or a long query): marks
 // the listed pages in a page bitmap in memory.
 __global__ void __launch_bounds__(256) union_mark_kernel(const int32_t *__restrict__ row_pages, int64_t n,
@@ -892,9 +960,8 @@ template <typename F> static int with_cpr(int cpr, F &&f) {
 // union from these lists.  V = 16-byte key chunks per thread in registers
 // (rows of more than 4 * V * NT keys are re-read from memory).
 template <int NT, int V>
-__global__ void __launch_bounds__(NT) coarse_select_kernel(const uint32_t *__restrict__ keys, int64_t ld, int n,
-                                                            int k, int32_t *__restrict__ row_pages,
-                                                            float *__restrict__ coarse_stats) {
+__device__ __forceinline__ void coarse_select_row(const uint32_t *__restrict__ keys, int64_t ld, int n, int k,
+                                                  int32_t *__restrict__ row_pages, float *__restrict__ coarse_stats) {
   __shared__ SelSh<NT> sh;
   __shared__ uint64_t cand[kCandCap];
   sel_init(sh);
@@ -919,6 +986,27 @@ __global__ void __launch_bounds__(NT) coarse_select_kernel(const uint32_t *__res
     coarse_stats[2 * row] = mx;
     coarse_stats[2 * row + 1] = sum;
   }
+}
+
+template <int NT, int V>
+__global__ void __launch_bounds__(NT) coarse_select_kernel(const uint32_t *__restrict__ keys, int64_t ld, int n,
+                                                            int k, int32_t *__restrict__ row_pages,
+                                                            float *__restrict__ coarse_stats) {
+  coarse_select_row<NT, V>(keys, ld, n, k, row_pages, coarse_stats);
+}
+
+// The coarse select with the page bound tables (the bounds exist when it
+// starts): blocks past bt.rows (= the query rows) fill the tables, in
+// parallel with the rows' selections.
+template <int NT, int V>
+__global__ void __launch_bounds__(NT) coarse_select_tables_kernel(const uint32_t *__restrict__ keys, int64_t ld,
+                                                                   int n, int k, int32_t *__restrict__ row_pages,
+                                                                   float *__restrict__ coarse_stats, BoundTables bt) {
+  if ((int)blockIdx.x >= bt.rows) {
+    fill_bound_tables<NT>(bt);
+    return;
+  }
+  coarse_select_row<NT, V>(keys, ld, n, k, row_pages, coarse_stats);
 }
 
 // ------------------------------------------------------------- fine scan
@@ -1021,6 +1109,15 @@ struct FinePrune {
   int spec, spec_kc;
 };
 constexpr int kPlanStride = 2 + kPageListCap;
+
+// The page bound tables (BoundTables) of a pruned scan follow the select
+// page lists of `batch` rows in the same buffer, 256-byte aligned: lbmax
+// [n][batch], then ubT [kr][ldn] at lbmax + ((n * batch + 63) & ~63), ldn =
+// (n + 63) & ~63.
+__device__ __forceinline__ const uint32_t *bound_tables_at(const int32_t *plan, int batch) {
+  const uintptr_t end = reinterpret_cast<uintptr_t>(plan + (int64_t)batch * kPlanStride);
+  return reinterpret_cast<const uint32_t *>((end + 255) & ~uintptr_t(255));
+}
 
 // Pages per kv row that a pruned host-tier scan reads speculatively: the
 // top of the first query row's coarse list, whose slices are in flight
@@ -1162,25 +1259,6 @@ template <int NT, typename Src> __device__ uint32_t block_kth_bound(const Src &s
   return bound;
 }
 
-// Max of n consecutive bound keys (a page's kv rows of one batch row):
-// 16-byte loads when the run is aligned (kv heads a multiple of 4), so that
-// the loads are few and independent.
-__device__ __forceinline__ uint32_t max_keys(const uint32_t *p, int n) {
-  uint32_t m = 0u;
-  if (((uintptr_t)p & 15) == 0 && (n & 3) == 0) {
-    const uint4 *p4 = reinterpret_cast<const uint4 *>(p);
-#pragma unroll 4
-    for (int i = 0; i < n / 4; ++i) {
-      const uint4 x = p4[i];
-      m = max(m, max(max(x.x, x.y), max(x.z, x.w)));
-    }
-  } else {
-#pragma unroll 4
-    for (int i = 0; i < n; ++i) m = max(m, p[i]);
-  }
-  return m;
-}
-
 // Count of n consecutive bound keys >= t (the kv rows of one batch row
 // whose slice of a page is scanned); loads as in max_keys.
 __device__ __forceinline__ int count_keys_ge(const uint32_t *p, int n, uint32_t t) {
@@ -1295,7 +1373,9 @@ __global__ void __launch_bounds__(256) page_bound_kernel(
   }
 }
 
-template <int DT, int LG>
+// TAB: a pruned scan reads the page bound tables (bound_tables_at) for its
+// threshold and page lists instead of the bound keys.
+template <int DT, int LG, bool TAB>
 __global__ void __launch_bounds__(256) fine_scan_kernel(
     int union_src, const int32_t *__restrict__ row_pages, int row_pages_n, int words, int32_t *page_list,
     int32_t *counters,
@@ -1489,13 +1569,23 @@ __global__ void __launch_bounds__(256) fine_scan_kernel(
       const bool one_each = U <= 256;
       const int v1 = (tid >> 6) + 4 * (tid & 63);
       // Bound keys of union rank v: from the LDS tables with speculation,
-      // else from memory.
+      // else from the page bound tables (TAB) or the bound keys themselves.
+      const uint32_t *lbmax = nullptr, *ubT = nullptr;
+      int batch = 0;
+      if constexpr (TAB && !SPEC) {
+        batch = (int)gridDim.y / hkv;
+        lbmax = bound_tables_at(pr.plan, batch);
+        ubT = lbmax + ((((int64_t)n_pages * batch + 63) & ~int64_t(63)) +
+                       (int64_t)r * (((int64_t)n_pages + 63) & ~int64_t(63)));
+      }
       auto lb_of = [&](int v) {
         if constexpr (SPEC) return lbt[v];
+        else if constexpr (TAB) return lbmax[page_of(v) * batch + b];
         else return max_keys(pr.lb + page_of(v) * pr.kr + b * hkv, hkv);
       };
       auto ub_of = [&](int v) {
         if constexpr (SPEC) return ubt[v];
+        else if constexpr (TAB) return ubT[page_of(v)];
         else return ubr[page_of(v) * pr.kr];
       };
       uint32_t lb1 = 0u, ub1 = 0u;
@@ -2208,6 +2298,11 @@ static int retrieve_impl(kiv_store_t *s, const kiv_retrieve_args_t *a, hipStream
   const bool fine_mfma = dt != KIV_DTYPE_F32 && D % 32 == 0 && (ktf <= 4 || ktf == 6 || ktf == 8) &&
                          (G * Qb >= kFineMfmaRows || (!host_tier && !prune_ok)) && a->scaling > 0.f;
   const bool prune = prune_ok && !fine_mfma;
+  // Page bound tables for the fine scan over wide kv rows (Phi-3.5 MHA
+  // shape, 32 kv rows, 872 union pages: each fine-scan block's bound reads
+  // drop from ~220 KiB of cache lines to ~7 KiB; fine scan 81.3 -> 71.0 us).
+  const bool tables = prune && s->kr > 8 && N > 0 && bound_table_items(N, s->kr, B) < (int64_t(1) << 31);
+  BoundTables bt{};
   FinePrune pr{};
   const uint32_t *pr_ub = nullptr, *pr_thr = nullptr;  // page bounds and thresholds of a pruned fine scan
   int32_t *pr_ctl = nullptr;
@@ -2219,7 +2314,12 @@ static int retrieve_impl(kiv_store_t *s, const kiv_retrieve_args_t *a, hipStream
     const size_t thr_off = 256, ub_off = thr_off + (((size_t)B * 4 + 255) & ~size_t(255));
     const size_t nb_keys = (((size_t)N * s->kr + 63) & ~size_t(63)) * 4;
     const size_t plan_off = ub_off + 3 * nb_keys;
-    const size_t need = plan_off + (size_t)B * kPlanStride * 4;
+    // [bound tables: lbmax [N][B], ubT [kr][ldn]] follow in mode 2 (at
+    // the offsets bound_tables_at finds).
+    const int64_t ldn = ((int64_t)N + 63) & ~int64_t(63);
+    const size_t lbmax_off = (plan_off + (size_t)B * kPlanStride * 4 + 255) & ~size_t(255);
+    const size_t ubt_off = lbmax_off + (((size_t)N * B * 4 + 255) & ~size_t(255));
+    const size_t need = tables ? ubt_off + (size_t)s->kr * ldn * 4 : plan_off + (size_t)B * kPlanStride * 4;
     if (s->prune.bytes < need) {
       if ((rc = s->prune.ensure(need, st, false))) return rc;
       KIV_HIP(hipMemsetAsync(s->prune.ptr, 0, s->prune.bytes, st));
@@ -2237,6 +2337,9 @@ static int retrieve_impl(kiv_store_t *s, const kiv_retrieve_args_t *a, hipStream
     pr_thr = pr.thr;
     pr_ctl = (int32_t *)s->prune.ptr;
     s->prune_on = true;
+    if (tables)
+      bt = BoundTables{pr.ub, pr.lb, (uint32_t *)((char *)s->prune.ptr + lbmax_off),
+                       (uint32_t *)((char *)s->prune.ptr + ubt_off), N, ldn, s->kr, hkv, B, 0};
   }
 
   if (a->hot_tokens > 0) {
@@ -2340,11 +2443,24 @@ static int retrieve_impl(kiv_store_t *s, const kiv_retrieve_args_t *a, hipStream
         KIV_HIP(hipGetLastError());
         if (extra) s->partial_len += apass.count;  // the appended rows are in the partial page from here on
         s->prof_begin(KIV_STAGE_COARSE_SELECT, st);
-        with_select_chunks(N, [&](auto kern) {
-          hipLaunchKernelGGL(kern, dim3(rows_p), dim3(kSelThreads), 0, st, (const uint32_t *)s->coarse_keys.ptr,
-                             ld, N, kc, (int32_t *)s->row_pages.ptr + (int64_t)row0 * kc, coarse_stats + 2 * row0);
-        }, [](auto vc) { return coarse_select_kernel<kSelThreads, decltype(vc)::value>; });
-        s->prof_end(KIV_STAGE_COARSE_SELECT, st);
+        if (tables && mfma) {
+          // The bound tables ride on the (single) pass's launch: blocks past
+          // its rows, one table item a thread.
+          BoundTables btp = bt;
+          btp.rows = rows_p;
+          const int tb_blocks = (int)((bound_table_items(N, s->kr, B) + kSelThreads - 1) / kSelThreads);
+          with_select_chunks(N, [&](auto kern) {
+            hipLaunchKernelGGL(kern, dim3(rows_p + tb_blocks), dim3(kSelThreads), 0, st,
+                               (const uint32_t *)s->coarse_keys.ptr, ld, N, kc,
+                               (int32_t *)s->row_pages.ptr + (int64_t)row0 * kc, coarse_stats + 2 * row0, btp);
+          }, [](auto vc) { return coarse_select_tables_kernel<kSelThreads, decltype(vc)::value>; });
+        } else {
+          with_select_chunks(N, [&](auto kern) {
+            hipLaunchKernelGGL(kern, dim3(rows_p), dim3(kSelThreads), 0, st, (const uint32_t *)s->coarse_keys.ptr,
+                               ld, N, kc, (int32_t *)s->row_pages.ptr + (int64_t)row0 * kc, coarse_stats + 2 * row0);
+          }, [](auto vc) { return coarse_select_kernel<kSelThreads, decltype(vc)::value>; });
+        }
+        if (!tables || mfma) s->prof_end(KIV_STAGE_COARSE_SELECT, st);  // else after the bound tables' launch
         KIV_HIP(hipGetLastError());
         row0 += rows_p;
       }
@@ -2361,6 +2477,13 @@ static int retrieve_impl(kiv_store_t *s, const kiv_retrieve_args_t *a, hipStream
           return (int)KIV_OK;
         });
         if (rc) return rc;
+        KIV_HIP(hipGetLastError());
+      }
+      if (tables && !mfma) {
+        // After the page bounds' kernel: the tables in a launch of their own.
+        const int64_t items = bound_table_items(N, s->kr, B);
+        hipLaunchKernelGGL(bound_tables_kernel, dim3((unsigned)((items + 255) / 256)), dim3(256), 0, st, bt);
+        s->prof_end(KIV_STAGE_COARSE_SELECT, st);
         KIV_HIP(hipGetLastError());
       }
       if (union_src == UNION_LIST) {
@@ -2519,7 +2642,8 @@ static int retrieve_impl(kiv_store_t *s, const kiv_retrieve_args_t *a, hipStream
       const size_t lds = (size_t)G * Qp * D * eb + (size_t)bw * 4 + (fp.mode == 1 ? (size_t)kPageListCap * 4 : 0) +
                          (usrc == UNION_ROWS ? upage_bytes : 0) + (fp.spec > 0 ? 2 * upage_bytes : 0);
       return with_dt_lg(dt, lg, [&](auto dtc, auto lgc) {
-        auto kern = fine_scan_kernel<decltype(dtc)::value, decltype(lgc)::value>;
+        auto kern = tables && fp.mode == 1 ? fine_scan_kernel<decltype(dtc)::value, decltype(lgc)::value, true>
+                                           : fine_scan_kernel<decltype(dtc)::value, decltype(lgc)::value, false>;
         if (lds > 65536)
           KIV_HIP(hipFuncSetAttribute((const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
         hipLaunchKernelGGL(kern, dim3((unsigned)nb, (unsigned)s->kr), dim3(256), lds, st, usrc,
