@@ -81,6 +81,9 @@ def parse():
     ap.add_argument("--profile-pass", action="store_true",
                     help="for rocprofv3 runs: the headline tier's steps only, plus a 64 MiB device copy "
                          "that calibrates the FETCH_SIZE / WRITE_SIZE counters")
+    ap.add_argument("--trace-summary", metavar="KERNEL_TRACE_CSV",
+                    help="print the per-kernel durations of the timed layer's steps in a rocprofv3 "
+                         "--kernel-trace CSV of a --profile-pass run, and exit (no GPU)")
     return ap.parse_args()
 
 
@@ -96,17 +99,43 @@ CHUNK_WORKLOAD = "qwen15b_prefill_chunk"
 
 def make_scrub(dev):
     """A read of SCRUB_BYTES that leaves no workload data in L2 or the MALL,
-    then a bounded spin (torch.cuda._sleep, no memory traffic) that gives the
-    host its head start on the next step."""
+    then `then()` if given, then a bounded spin (torch.cuda._sleep, no memory
+    traffic) that gives the host its head start on the next step."""
     import torch
 
     buf = torch.ones(SCRUB_BYTES // 4, dtype=torch.int32, device=dev)
 
-    def scrub():
+    def scrub(then=None):
         buf.sum()
+        if then is not None:
+            then()
         torch.cuda._sleep(HEAD_START_CYCLES)
 
     return scrub
+
+
+def layer_before(scrub, w, cfg, dev, seed):
+    """The scrub, then one decode step of another layer of the same shape
+    (its own store, filled from another seed) before each timed step, as in
+    a model whose layers run one after another: the timed layer's data is
+    cold (the scrub evicted it and the other layer reads none of it) while
+    the step's kernels are resident in the instruction caches and their
+    code's translations in the TLBs.  After the scrub alone the code too
+    comes from HBM, which adds 2-4 us to a step and makes its time depend
+    on where the linker placed each kernel (kernels of identical machine
+    code measured 26.4 and 28.9 us in two builds; 0.1 us apart with the
+    other layer's step first).  Returns (scrub function, other layer's
+    store), or (None, None) with warm caches."""
+    if scrub is None:
+        return None, None
+    other, hk, hv, q = build_cold(w, cfg, dev, seed + 1)
+    n = [0]
+
+    def step():
+        one_step(other, cfg, q, hk, hv, n[0], w.scaling)
+        n[0] += 1
+
+    return (lambda: scrub(then=step)), other
 
 
 def build_cold(w, cfg, dev, seed):
@@ -529,7 +558,8 @@ def profile_pass(w, args, dev, scrub):
                     cold_tier=args.cold_tier, reserve_tokens=w.cold + args.steps + args.warmup + 1024,
                     fine_pruning=not args.no_pruning)
     store, hot_k, hot_v, q = build_cold(w, cfg, dev, args.seed)
-    us, _ = time_steps(store, cfg, q, hot_k, hot_v, args.steps, args.warmup, w.scaling, scrub)
+    scrub_l, _other = layer_before(scrub, w, cfg, dev, args.seed)
+    us, _ = time_steps(store, cfg, q, hot_k, hot_v, args.steps, args.warmup, w.scaling, scrub_l)
     src = torch.ones(64 << 20, dtype=torch.uint8, device=dev)
     dst = torch.empty_like(src)
     for _ in range(3):
@@ -825,8 +855,55 @@ def prefill_chunk_run(args):
     print(json.dumps(line), flush=True)
 
 
+def trace_summary(path):
+    """Durations of the kiv:: kernels of the timed layer's steps in a
+    --profile-pass kernel trace.  Dispatches in start order: a reduction
+    kernel opens a scrub (the other layer's step follows it), the spin kernel
+    after it opens the timed step; the warm-up steps before the first scrub
+    and the other layer's steps are left out."""
+    import csv
+    import statistics
+
+    with open(path, newline="") as f:
+        rows = sorted(csv.DictReader(f), key=lambda r: int(r["Start_Timestamp"]))
+    state, durs, spans, cur = None, {}, [], None
+    for r in rows:
+        name = r["Kernel_Name"]
+        if "reduce_kernel" in name:
+            state = "other"
+            if cur:
+                spans.append(cur[1] - cur[0])
+            cur = None
+            continue
+        if "spin_kernel" in name:
+            state = "timed" if state == "other" else None
+            continue
+        if state != "timed" or "kiv::" not in name:
+            continue
+        short = name.split("(")[0].replace("void ", "")
+        t0, t1 = int(r["Start_Timestamp"]), int(r["End_Timestamp"])
+        durs.setdefault(short, []).append((t1 - t0) / 1e3)
+        cur = (t0, t1) if cur is None else (cur[0], t1)
+    if cur:
+        spans.append(cur[1] - cur[0])
+    out = [f"{'kernel':48s}{'calls':>7s}{'avg_us':>10s}{'median_us':>11s}{'min_us':>9s}{'max_us':>9s}"]
+    for k, v in sorted(durs.items(), key=lambda kv: -sum(kv[1]) / len(kv[1])):
+        out.append(f"{k:48s}{len(v):7d}{sum(v) / len(v):10.2f}{statistics.median(v):11.2f}{min(v):9.2f}"
+                   f"{max(v):9.2f}")
+    total = sum(sum(v) / len(v) for v in durs.values())
+    out.append("")
+    out.append(f"sum of the kernel averages: {total:.2f} us")
+    if spans:
+        out.append(f"step span, first kernel start to last kernel end: median {statistics.median(spans) / 1e3:.2f} us "
+                   f"({len(spans)} steps)")
+    print("\n".join(out))
+
+
 def main():
     args = parse()
+    if args.trace_summary:
+        trace_summary(args.trace_summary)
+        return
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported (the tiered-cache path "
               "runs on one GPU; across GPUs it would shard by cold page range or by kv head)", file=sys.stderr)
@@ -861,24 +938,31 @@ def main():
         fill_s = time.perf_counter() - t0
         print(f"[bench] {tier}: filled {store.cold_length} cold tokens in {fill_s:.1f}s", file=sys.stderr,
               flush=True)
-        us, wall = time_steps(store, cfg, q, hot_k, hot_v, args.steps, args.warmup, w.scaling, scrub)
+        scrub_l, other = layer_before(scrub, w, cfg, dev, args.seed)
+        us, wall = time_steps(store, cfg, q, hot_k, hot_v, args.steps, args.warmup, w.scaling, scrub_l)
         print(f"[bench] {tier} ({args.cache} caches): {us:.1f} us/step (wall {wall:.1f})", file=sys.stderr,
               flush=True)
-        stages = profile_steps(store, cfg, q, hot_k, hot_v, args.steps, w.scaling, scrub)
+        stages = profile_steps(store, cfg, q, hot_k, hot_v, args.steps, w.scaling, scrub_l)
         slices = store.fine_scan_stats()  # the last step's (scanned, union) page slices
         entry = {"us_per_step": us, "wall_us_per_step": wall, "stages": stages, "fine_scan_slices": slices}
+        if scrub is not None:
+            # The scrub alone before each step: the kernels' code is cold too.
+            entry["code_cold_us_per_step"], _ = time_steps(store, cfg, q, hot_k, hot_v, args.steps, 0, w.scaling,
+                                                           scrub)
+            print(f"[bench] {tier} (scrub only, code cold too): {entry['code_cold_us_per_step']:.1f} us/step",
+                  file=sys.stderr, flush=True)
         if tier == args.cold_tier and scrub is not None and not args.no_variant:
             warm_us, _ = time_steps(store, cfg, q, hot_k, hot_v, args.steps, args.warmup, w.scaling, None)
             entry["warm_us_per_step"] = warm_us
             print(f"[bench] {tier} (warm caches): {warm_us:.1f} us/step", file=sys.stderr, flush=True)
-            two_us, _ = time_steps(store, cfg, q, hot_k, hot_v, args.steps, 0, w.scaling, scrub, fused=False)
-            two_stages = profile_steps(store, cfg, q, hot_k, hot_v, args.steps, w.scaling, scrub, fused=False)
+            two_us, _ = time_steps(store, cfg, q, hot_k, hot_v, args.steps, 0, w.scaling, scrub_l, fused=False)
+            two_stages = profile_steps(store, cfg, q, hot_k, hot_v, args.steps, w.scaling, scrub_l, fused=False)
             entry["two_call"] = {"us_per_step": round(two_us, 2),
                                  "stages_us": {k: round(v["avg_us"], 2) for k, v in two_stages.items()}}
             print(f"[bench] {tier} (retrieve, then attention): {two_us:.1f} us/step", file=sys.stderr, flush=True)
             if tier == "host" and cfg.fine_pruning:  # the same store with the full scan
                 full_us, _ = time_steps(store, replace(cfg, fine_pruning=False), q, hot_k, hot_v, args.steps, 0,
-                                        w.scaling, scrub)
+                                        w.scaling, scrub_l)
                 entry["unpruned_us_per_step"] = full_us
                 print(f"[bench] {tier} (fine scan not pruned): {full_us:.1f} us/step", file=sys.stderr, flush=True)
         if tier == args.cold_tier:
@@ -896,7 +980,7 @@ def main():
                                               cfg.fine_pruning)
         entry["num_pages"] = store.num_pages
         results[tier] = entry
-        del store
+        del store, other
         torch.cuda.synchronize()
         torch.cuda.empty_cache()
 
@@ -959,6 +1043,9 @@ def main():
                     "fine_scan_slices": list(r["fine_scan_slices"]),
                     "stages_us": {k: round(v["avg_us"], 2) for k, v in r["stages"].items()}}
                 for t, r in results.items() if t != args.cold_tier}
+    for t, r in results.items():
+        if t != args.cold_tier and "code_cold_us_per_step" in r:
+            variants[t]["code_cold_us_per_step"] = round(r["code_cold_us_per_step"], 2)
     if "warm_us_per_step" in head:
         variants["warm_caches"] = {"us_per_step": round(head["warm_us_per_step"], 2)}
     if "two_call" in head:
@@ -982,14 +1069,19 @@ def main():
                                f"D={w.head_dim}, hot {w.hot}, cold {w.cold}", "batch": 1,
                    "top_pages": w.top_pages, "top_p": w.top_p, "page_size": w.page_size,
                    "cold_tier": args.cold_tier, "fine_pruning": not args.no_pruning, "caches": args.cache},
-        "value_meaning": ("GPU time of one layer's decode step: fence-free HIP events around each step "
-                          "after a cache scrub, median over the timed steps, plus the page-end finalize "
-                          "(measured in the same run) spread over the page's steps"
+        "value_meaning": ("GPU time of one layer's decode step as a model runs it: a cache scrub (no data "
+                          "of this layer in L2 or the MALL), then another layer's step of the same shape "
+                          "(its own store: the kernels' code is resident, as between the layers of a "
+                          "model), then fence-free HIP events around this layer's step; median over the "
+                          "timed steps, plus the page-end finalize (measured in the same run) spread over "
+                          "the page's steps"
                           if scrub is not None else
                           "GPU time of one layer's decode step: HIP events around the timed steps run "
                           "back to back (warm caches), mean, plus the page-end finalize spread over the "
                           "page's steps"),
         "us_per_step_timed": round(head["us_per_step"], 2),
+        "code_cold_us_per_step": (round(head["code_cold_us_per_step"] + fin_us, 2)
+                                  if "code_cold_us_per_step" in head else None),
         "event_pair_overhead_us": (round(event_pair_us(dev, scrub), 2) if scrub is not None else None),
         "evict_finalize_amortized_us": round(fin_us, 3),
         "host_inclusive_us_per_step": round(head.get("host_inclusive_us_per_step", float("nan")), 2),
