@@ -275,6 +275,12 @@ SMALL = [
                            top_pages=3, top_p=100, segment=128, n_targets=4), (2048, 52)),
     ("d20_f32", dict(num_q_heads=4, num_kv_heads=1, head_dim=20, dtype=torch.float32, cold=1500, hot=50,
                      top_pages=5, top_p=40, segment=100), (333,)),
+    # more than 8 kv rows: the pruned scan reads the page bound tables, built by the
+    # coarse select's extra blocks (MFMA coarse scan) or by their own kernel (VALU scan)
+    ("mha16_f16_d64", dict(num_q_heads=16, num_kv_heads=16, head_dim=64, dtype=torch.float16, cold=2100, hot=64,
+                           top_pages=3, top_p=100, segment=128, n_targets=4), (2048, 52)),
+    ("mha12_bf16_d40", dict(num_q_heads=12, num_kv_heads=12, head_dim=40, dtype=torch.bfloat16, cold=2100, hot=33,
+                            top_pages=3, top_p=100, segment=128, n_targets=4), (1000, 1100)),
 ]
 
 
