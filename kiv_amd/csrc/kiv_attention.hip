@@ -195,8 +195,8 @@ __global__ void __launch_bounds__(kAttnThreads) decode_attn_kernel(AttnParams p)
   for (int j = tid; j < GQ; j += kAttnThreads) {
     const int h = kvh * G + j / p.qlen, qp = j % p.qlen;
     const int row = (b * p.hq + h) * p.qlen + qp;
-    p.ws_m[(int64_t)sg * rows_total + row] = rm[j];
-    p.ws_l[(int64_t)sg * rows_total + row] = rl[j];
+    p.ws_m[ml_at(p, sg, row)] = rm[j];
+    p.ws_l[ml_at(p, sg, row)] = rl[j];
   }
 }
 
@@ -227,8 +227,8 @@ __global__ void __launch_bounds__(kAttnThreads) decode_attn_combine_kernel(AttnP
         const int sp = s0 + u * groups;
         if (sp < S) {
           const int64_t at = (int64_t)sp * rows_total + row;
-          ms[u] = p.ws_m[at];
-          ls[u] = p.ws_l[at];
+          ms[u] = p.ws_m[ml_at(p, sp, row)];
+          ls[u] = p.ws_l[ml_at(p, sp, row)];
           as[u] = *reinterpret_cast<const float4 *>(&p.ws_acc[at * D + 4 * i]);
         } else {
           ms[u] = -INFINITY;
@@ -311,8 +311,8 @@ __global__ void __launch_bounds__(kFinalThreads) decode_attn_final_kernel(AttnPa
     const int sp = g + u * groups;
     if (g < groups && sp < s_hot) {
       const int64_t at = (int64_t)sp * rows_total + row;
-      hm[u] = p.ws_m[at];
-      hl[u] = p.ws_l[at];
+      hm[u] = p.ws_m[ml_at(p, sp, row)];
+      hl[u] = p.ws_l[ml_at(p, sp, row)];
       ha[u] = *reinterpret_cast<const float4 *>(&p.ws_acc[at * D + 4 * i4]);
     } else {
       hm[u] = -INFINITY;
@@ -368,7 +368,8 @@ __global__ void __launch_bounds__(kFinalThreads) decode_attn_final_kernel(AttnPa
   if (g < groups) {
     for (int sp = g + kCombineBatch * groups; sp < s_hot; sp += groups) {
       const int64_t at = (int64_t)sp * rows_total + row;
-      lse_merge(m, l, o, p.ws_m[at], p.ws_l[at], *reinterpret_cast<const float4 *>(&p.ws_acc[at * D + 4 * i4]));
+      lse_merge(m, l, o, p.ws_m[ml_at(p, sp, row)], p.ws_l[ml_at(p, sp, row)],
+                *reinterpret_cast<const float4 *>(&p.ws_acc[at * D + 4 * i4]));
     }
   }
   if (g == 0) {

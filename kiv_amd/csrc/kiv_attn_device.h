@@ -29,9 +29,14 @@ struct AttnParams {
   int chunk, nsplit;   // keys per split; splits in all
   int split_cold;      // splits [0, split_cold) hold retrieved keys, the rest hot keys
   int split0;          // first split of this launch
-  float *ws_m, *ws_l, *ws_acc;
+  float *ws_m, *ws_l, *ws_acc;  // m, l: [row][nsplit] (a row's splits in one line); acc: [nsplit][row][D]
   char *out;
 };
+
+// Index of split sg's (m, l) of query row `row` in the workspace.
+__device__ __forceinline__ int64_t ml_at(const AttnParams &p, int sg, int row) {
+  return (int64_t)row * p.nsplit + sg;
+}
 
 __device__ __forceinline__ float mask_bias(const AttnParams &p, int b, int h, int qp, int t) {
   const int64_t o = (int64_t)b * p.ms0 + (int64_t)h * p.ms1 + (int64_t)qp * p.ms2 + (int64_t)t * p.ms3;
@@ -191,8 +196,8 @@ template <int DT, int KT> __device__ void attn_mfma_split(const AttnParams &p, i
   for (int j = tid; j < GQ; j += kAttnThreads) {
     const int h = kvh * G + j / p.qlen, qp = j % p.qlen;
     const int row = (b * p.hq + h) * p.qlen + qp;
-    p.ws_m[(int64_t)sg * rows_total + row] = rm[j];
-    p.ws_l[(int64_t)sg * rows_total + row] = rl[j];
+    p.ws_m[ml_at(p, sg, row)] = rm[j];
+    p.ws_l[ml_at(p, sg, row)] = rl[j];
   }
 }
 
