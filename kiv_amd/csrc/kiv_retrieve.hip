@@ -1971,6 +1971,7 @@ struct GatherArgs {
   int has_pages;
   const int32_t *page_list;
   const uint64_t *ktab, *vtab;
+  int nchunks;  // entries of ktab / vtab
   int chunk_shift;
   int64_t page_bytes;
   const char *part_k, *part_v, *k_stage;
@@ -2029,91 +2030,86 @@ template <int DT> __device__ void gather_telemetry(const GatherArgs &ga) {
   }
 }
 
+// Wave w of block (x, b) takes list entry i = x * kGatherCands + w alone
+// (no block barrier), and issues every read that does not depend on the
+// entry's rank together: the list's count, the entry, the union size, the
+// pruning threshold and (a table of at most 64 chunks) the chunk bases, one
+// per lane.  The entry's page is read while the rank is summed; then the V
+// row (host memory on the host tier), the K staging row, the page's bound
+// key and its compact slot go out together, and K comes from the host only
+// where the pruned scan did not stage it.  Lane l copies items l, l + 64,
+// ... of the entry (kv head, 16-byte chunk).
 template <int DT> __device__ void gather_block(const GatherArgs &ga, int bx, int b) {
   constexpr int VEC = Elem<DT>::VEC, EB = Elem<DT>::BYTES;
-  __shared__ int slot_of[kGatherCands], cand_of[kGatherCands];
-  const uint64_t *list = ga.list;
-  const int64_t list_ld = ga.list_ld;
-  const int32_t *list_count = ga.list_count, *counters = ga.counters, *page_list = ga.page_list;
-  const uint64_t *ktab = ga.ktab, *vtab = ga.vtab;
-  const int has_pages = ga.has_pages, chunk_shift = ga.chunk_shift, page_size = ga.page_size;
-  const int partial_len = ga.partial_len, hkv = ga.hkv, head_dim = ga.head_dim;
-  const int width = ga.width, cpr = ga.cpr;
-  const int64_t page_bytes = ga.page_bytes, stage_ld = ga.stage_ld, num_finalized = ga.num_finalized;
-  const char *part_k = ga.part_k, *part_v = ga.part_v, *k_stage = ga.k_stage;
-  char *k_out = ga.k_out, *v_out = ga.v_out;
-  int64_t *idx_out = ga.idx_out;
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-  const int U = has_pages ? counters[0] : 0;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int page_size = ga.page_size, hkv = ga.hkv, head_dim = ga.head_dim, cpr = ga.cpr;
+  const uint64_t *L = ga.list + (int64_t)b * ga.list_ld;
+  const int i = bx * kGatherCands + wave;
+  // Reads independent of the entry's rank.
+  const int C = ga.list_count[b];
+  const uint64_t x = i < ga.list_ld ? L[i] : 0;
+  const int U = ga.has_pages ? ga.counters[0] : 0;
+  const uint32_t thr = ga.ub ? ga.thr[b] : 0u;
+  const bool tab_lanes = ga.nchunks <= 64;
+  const uint64_t kt_lane = tab_lanes && lane < ga.nchunks ? ga.ktab[lane] : 0;
+  const uint64_t vt_lane = tab_lanes && lane < ga.nchunks ? ga.vtab[lane] : 0;
+  if (i >= C) return;  // wave-uniform
   const int64_t split = (int64_t)U * page_size;
-  const int n = (int)split + partial_len;
-  const int k = min(width, n);
-  const int C = list_count[b];
-  const int first = bx * kGatherCands;
-  if (first >= C) return;
-  const uint64_t *L = list + (int64_t)b * list_ld;
-  const int i = first + wave;
-  if (i < C) {
-    const uint64_t x = L[i];
-    int r = 0, j = lane;
-    for (; j + 192 < C; j += 256) {
-      const uint64_t y0 = L[j], y1 = L[j + 64], y2 = L[j + 128], y3 = L[j + 192];
-      r += (y0 > x) + (y1 > x) + (y2 > x) + (y3 > x);
-    }
-    for (; j < C; j += 64) r += L[j] > x;
-    r = wave_sum_i32(r);
-    if (lane == 0) {
-      slot_of[wave] = r < k ? r : -1;
-      cand_of[wave] = comp_index(x);
-    }
-  } else if (lane == 0) {
-    slot_of[wave] = -1;
+  const int n = (int)split + ga.partial_len;
+  const int k = min(ga.width, n);
+  const int64_t cand = comp_index(x);
+  const bool paged = cand < split;
+  // The entry's page (read while the rank is summed).
+  const int64_t page = paged ? (int64_t)ga.page_list[cand / page_size] : 0;
+  int r = 0, j = lane;
+  for (; j + 192 < C; j += 256) {
+    const uint64_t y0 = L[j], y1 = L[j + 64], y2 = L[j + 128], y3 = L[j + 192];
+    r += (y0 > x) + (y1 > x) + (y2 > x) + (y3 > x);
   }
-  __syncthreads();
+  for (; j < C; j += 64) r += L[j] > x;
+  r = wave_sum_i32(r);
+  if (r >= k) return;  // wave-uniform: not selected
+  const int slot = r;
+  const int64_t t = paged ? cand % page_size : cand - split;
+  const int64_t gid = paged ? page * page_size + t : ga.num_finalized + t;
+  if (lane == 0 && ga.idx_out) ga.idx_out[(int64_t)b * ga.width + slot] = gid;
   const int per = hkv * cpr;
-  for (int item = tid; item < kGatherCands * per; item += 256) {
-    const int w = item / per, rest = item - w * per;
-    const int slot = slot_of[w];
-    if (slot < 0) continue;
-    const int kvh = rest / cpr, c = rest - kvh * cpr;
-    const int64_t cand = cand_of[w];
-    const int r = b * hkv + kvh;
+  const int64_t chunk = page >> ga.chunk_shift;
+  const int64_t base = (page & ((int64_t(1) << ga.chunk_shift) - 1)) * ga.page_bytes;
+  uint64_t kb = 0, vb = 0;
+  if (paged) {
+    // The chunk bases: from the lane that loaded them, else from memory.
+    kb = tab_lanes ? (uint64_t)__shfl((long long)kt_lane, (int)chunk, 64) : ga.ktab[chunk];
+    vb = tab_lanes ? (uint64_t)__shfl((long long)vt_lane, (int)chunk, 64) : ga.vtab[chunk];
+  }
+  for (int item = lane; item < per; item += 64) {
+    const int kvh = item / cpr, c = item - kvh * cpr;
+    const int rr = b * hkv + kvh;
     const int64_t e0 = (int64_t)c * VEC;
-    const char *ks;
-    const char *vs;
-    int64_t gid;
-    bool staged = k_stage != nullptr;
-    if (cand < split) {
+    const char *ks, *vs;
+    const char *kst = nullptr;  // K staged by the fine scan, if any
+    bool scanned = true;
+    if (paged) {
       // K of a page is [kv row][token][D], V [token][kv row][D].
-      const int64_t page = page_list[cand / page_size], t = cand % page_size;
-      const int64_t base = (page & ((int64_t(1) << chunk_shift) - 1)) * page_bytes;
-      ks = reinterpret_cast<const char *>(ktab[page >> chunk_shift]) + base +
-           (((int64_t)r * page_size + t) * head_dim + e0) * EB;
-      vs = reinterpret_cast<const char *>(vtab[page >> chunk_shift]) + base +
-           ((t * ga.batch * hkv + r) * head_dim + e0) * EB;
-      gid = page * page_size + t;
-      // A pruned scan staged the slice only if its bound reached T.
-      if (ga.ub) {
-        const bool scanned = ga.ub[page * ga.ub_kr + r] >= ga.thr[b];
-        staged = staged && scanned;
-        if (ga.cstage && scanned) {
-          const int sl = ga.slot_of[page * ga.ub_kr + r];
-          if (sl >= 0) ks = ga.cstage + ((((int64_t)r * ga.scap + sl) * page_size + t) * head_dim + e0) * EB;
-        }
+      ks = reinterpret_cast<const char *>(kb) + base + (((int64_t)rr * page_size + t) * head_dim + e0) * EB;
+      vs = reinterpret_cast<const char *>(vb) + base + ((t * ga.batch * hkv + rr) * head_dim + e0) * EB;
+      if (ga.ub) scanned = ga.ub[page * ga.ub_kr + rr] >= thr;  // a pruned scan staged only what it scanned
+      if (ga.cstage) {
+        const int sl = ga.slot_of[page * ga.ub_kr + rr];
+        if (scanned && sl >= 0)
+          kst = ga.cstage + ((((int64_t)rr * ga.scap + sl) * page_size + t) * head_dim + e0) * EB;
       }
     } else {
-      const int64_t t = cand - split;
-      const int64_t off = (((int64_t)r * page_size + t) * head_dim + e0) * EB;
-      ks = part_k + off;
-      vs = part_v + off;
-      gid = num_finalized + t;
+      const int64_t off = (((int64_t)rr * page_size + t) * head_dim + e0) * EB;
+      ks = ga.part_k + off;
+      vs = ga.part_v + off;
     }
-    if (staged) ks = k_stage + (((int64_t)r * stage_ld + cand) * head_dim + e0) * EB;
-    const int64_t o = (((int64_t)r * width + slot) * head_dim + e0) * EB;
-    const uint4 kx = load16(ks), vx = load16(vs);
-    *reinterpret_cast<uint4 *>(k_out + o) = kx;
-    *reinterpret_cast<uint4 *>(v_out + o) = vx;
-    if (rest == 0 && idx_out) idx_out[(int64_t)b * width + slot] = gid;
+    if (ga.k_stage && scanned) kst = ga.k_stage + (((int64_t)rr * ga.stage_ld + cand) * head_dim + e0) * EB;
+    const uint4 vx = load16(vs);
+    const uint4 kx = load16(kst ? kst : ks);
+    const int64_t o = (((int64_t)rr * ga.width + slot) * head_dim + e0) * EB;
+    *reinterpret_cast<uint4 *>(ga.k_out + o) = kx;
+    *reinterpret_cast<uint4 *>(ga.v_out + o) = vx;
   }
 }
 
@@ -2694,6 +2690,7 @@ static int retrieve_impl(kiv_store_t *s, const kiv_retrieve_args_t *a, hipStream
     ga.page_list = (const int32_t *)s->page_list.ptr;
     ga.ktab = (const uint64_t *)s->k_tab.ptr;
     ga.vtab = (const uint64_t *)s->v_tab.ptr;
+    ga.nchunks = (int)s->k_chunks.size();
     ga.chunk_shift = s->chunk_shift;
     ga.page_bytes = s->page_bytes;
     ga.part_k = (const char *)s->k_part.ptr;
