@@ -37,7 +37,7 @@ constexpr int kFinalUT = 8;         // retrieved keys per lane group in the fina
 
 template <int DT, int KT>
 __global__ void __launch_bounds__(kAttnThreads) decode_attn_mfma_kernel(AttnParams p) {
-  attn_mfma_split<DT, KT>(p, blockIdx.x, blockIdx.y);
+  attn_mfma_split<DT, KT, true>(p, blockIdx.x, blockIdx.y);
 }
 
 template <int DT, int LG>

@@ -61,7 +61,8 @@ __device__ __forceinline__ float mask_bias(const AttnParams &p, int b, int h, in
 //  - The split's V rows are staged in LDS with the K loads in flight.
 //  - Weighted sum: a thread owns one (q row, 8-dim chunk) and a share of
 //    the keys (ks of nks key groups); the groups' partial sums meet in LDS.
-template <int DT, int KT> __device__ void attn_mfma_split(const AttnParams &p, int s, int r) {
+template <int DT, int KT, bool LATE_V = false>
+__device__ void attn_mfma_split(const AttnParams &p, int s, int r) {
   constexpr int EB = 2, VEC = 8, D = 32 * KT, CPR = D / VEC;
   const int b = r / p.hkv, kvh = r % p.hkv;
   const int G = p.hq / p.hkv, GQ = G * p.qlen, CH = p.chunk;
@@ -83,14 +84,33 @@ template <int DT, int KT> __device__ void attn_mfma_split(const AttnParams &p, i
     return value ? p.hot_v + ((int64_t)b * p.hvs0 + (int64_t)kvh * p.hvs1 + (int64_t)t * p.hvs2) * EB
                  : p.hot_k + ((int64_t)b * p.hks0 + (int64_t)kvh * p.hks1 + (int64_t)t * p.hks2) * EB;
   };
-  // K operand rows (loads first), then the V rows into LDS.
+  // K operand rows (loads first), then the V rows into LDS.  LATE_V: the
+  // first 16 q rows' operands and the first batch of V rows are loaded with
+  // K, and the V rows go to LDS after the scores, which then wait for K and
+  // q only (the two-call path: MQA shape, step 84.7 -> 82.7 us; the fused
+  // path's splits, which run beside the gather, measured 0.4 us slower).
   const int kl = 16 * wave + (lane & 15), dsub = 8 * (lane >> 4);
   uint4 kx[KT];
 #pragma unroll
   for (int st = 0; st < KT; ++st)
     kx[st] = kl < nk ? load16(key_row(k0 + kl, false) + (32 * st + dsub) * EB) : make_uint4(0, 0, 0, 0);
   constexpr int VB = 4;  // V chunks per thread per batch
-  for (int i0 = 0; i0 < CH * CPR; i0 += VB * kAttnThreads) {
+  uint4 qx0[KT], v0[VB];
+  if constexpr (LATE_V) {
+#pragma unroll
+    for (int st = 0; st < KT; ++st) {
+      const int j = lane & 15;
+      const int h = kvh * G + j / p.qlen, qp = j % p.qlen;
+      const char *qrow = p.q + ((int64_t)b * p.qs0 + (int64_t)h * p.qs1 + (int64_t)qp * p.qs2) * EB;
+      qx0[st] = j < GQ ? load16(qrow + (32 * st + dsub) * EB) : make_uint4(0, 0, 0, 0);
+    }
+#pragma unroll
+    for (int u = 0; u < VB; ++u) {
+      const int i = u * kAttnThreads + tid, key = i / CPR, c = i % CPR;
+      v0[u] = (i < CH * CPR && key < nk) ? load16(key_row(k0 + key, true) + c * VEC * EB) : make_uint4(0, 0, 0, 0);
+    }
+  }
+  for (int i0 = 0; i0 < CH * CPR && !LATE_V; i0 += VB * kAttnThreads) {
     uint4 v[VB];
 #pragma unroll
     for (int u = 0; u < VB; ++u) {
@@ -111,7 +131,9 @@ template <int DT, int KT> __device__ void attn_mfma_split(const AttnParams &p, i
     f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int st = 0; st < KT; ++st) {
-      const uint4 qx = j < GQ ? load16(qrow + (32 * st + dsub) * EB) : make_uint4(0, 0, 0, 0);
+      const uint4 qx = LATE_V && rt == 0 ? qx0[st]
+                       : j < GQ            ? load16(qrow + (32 * st + dsub) * EB)
+                                           : make_uint4(0, 0, 0, 0);
       acc = mfma_16x16x32<DT>(kx[st], qx, acc);
     }
     if (j < GQ) {
@@ -124,6 +146,26 @@ template <int DT, int KT> __device__ void attn_mfma_split(const AttnParams &p, i
             v += mask_bias(p, b, h, qp, k0 + kk - p.cold_len);
           sc[j * CH + kk] = v;
         }
+      }
+    }
+  }
+  if constexpr (LATE_V) {
+#pragma unroll
+    for (int u = 0; u < VB; ++u) {
+      const int i = u * kAttnThreads + tid;
+      if (i < CH * CPR) vs[i] = v0[u];
+    }
+    for (int i0 = VB * kAttnThreads; i0 < CH * CPR; i0 += VB * kAttnThreads) {
+      uint4 v[VB];
+#pragma unroll
+      for (int u = 0; u < VB; ++u) {
+        const int i = i0 + u * kAttnThreads + tid, key = i / CPR, c = i % CPR;
+        v[u] = (i < CH * CPR && key < nk) ? load16(key_row(k0 + key, true) + c * VEC * EB) : make_uint4(0, 0, 0, 0);
+      }
+#pragma unroll
+      for (int u = 0; u < VB; ++u) {
+        const int i = i0 + u * kAttnThreads + tid;
+        if (i < CH * CPR) vs[i] = v[u];
       }
     }
   }
