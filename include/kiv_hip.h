@@ -93,8 +93,12 @@ typedef struct {
  * vector units (G * Q < 32); on the hbm and split tiers when G * Q < 32 and
  * the union's K could exceed 256 MiB (its upper bound: every query row's
  * top pages distinct), below which the full matrix-core scan of K in HBM is
- * faster.  It pauses itself for 32 calls after a call that skipped under a
- * quarter of the union. */
+ * faster.  Where the full matrix-core fine scan runs instead (the rest of
+ * the hbm and split tiers' one-pass queries, and queries of G * Q >= 32 on
+ * every tier), the same bounds and threshold list the union pages the fine
+ * select reads: the keys are exact either way, and the telemetry's mean
+ * then covers the listed pages' candidates.  It pauses itself for 32 calls
+ * after a call that skipped under a quarter of the union. */
 enum { KIV_RETRIEVE_PRUNE = 1 };
 
 /* Arguments of one retrieval: coarse page scan, union of per-row top

@@ -1737,6 +1737,59 @@ __global__ void __launch_bounds__(256) fine_scan_kernel(
 constexpr int kFineMfmaRows = 32;  // query rows per kv row from which the MFMA scan is used
 constexpr int kFineMfmaTok = 64;   // tokens per item (LDS tile)
 
+// The fine select's page plan after a full fine scan (plan null: none):
+// with the page bounds ub/lb [N][kr] the coarse scan wrote, batch row b's
+// threshold T (as the pruned scan computes it) goes to thr[b] and the union
+// pages with a kv row of b whose upper bound reaches T to plan[b] (the
+// pruned scan's format); while pruning is paused (*ctl > 0) the plan lists
+// every page, which sends the select to its full pass.
+struct SelectPlan {
+  const uint32_t *ub, *lb;
+  int kr, width;
+  uint32_t *thr;
+  int32_t *plan;
+  const int32_t *ctl;
+};
+
+template <int NT, typename PageOf>
+__device__ void select_plan(const SelectPlan &sp, int b, int hkv, int U, int page_size, int partial_len,
+                            PageOf &&page_of, SelSh<NT> &tsh, int *scan_tmp) {
+  int32_t *pl = sp.plan + (int64_t)b * kPlanStride;
+  if (*sp.ctl > 0) {
+    if (threadIdx.x == 0) {
+      sp.thr[b] = 0u;
+      pl[0] = U;
+      pl[1] = U * hkv;
+    }
+    return;
+  }
+  const int k = min(sp.width, U * page_size + partial_len);
+  const int m = (k + page_size - 1) / page_size;
+  uint32_t tb = 0u;
+  if (U >= m) {
+    auto lb_of = [&](int v) { return max_keys(sp.lb + page_of(v) * sp.kr + b * hkv, hkv); };
+    const UnionLowerKeys<NT, decltype(lb_of)> src{U, lb_of};
+    tb = block_kth_bound<NT>(src, m, tsh);
+  }
+  if (threadIdx.x == 0) sp.thr[b] = tb;
+  int np = 0, read_all = 0;
+  for (int c0 = 0; c0 < U; c0 += NT) {
+    const int v = c0 + threadIdx.x;
+    const int read = v < U ? count_keys_ge(sp.ub + page_of(v) * sp.kr + b * hkv, hkv, tb) : 0;
+    const int hit = read > 0 ? 1 : 0;
+    int tot, rtot;
+    const int pos = np + block_incl_scan<NT>(hit, scan_tmp, &tot) - hit;
+    if (hit && pos < kPageListCap) pl[2 + pos] = v;
+    block_incl_scan<NT>(read, scan_tmp, &rtot);
+    np += tot;
+    read_all += rtot;
+  }
+  if (threadIdx.x == 0) {
+    pl[0] = np;
+    pl[1] = read_all;
+  }
+}
+
 template <int DT, int KT>
 __global__ void __launch_bounds__(256) fine_scan_mfma_kernel(
     int union_src, const int32_t *__restrict__ row_pages, int row_pages_n, int words, int32_t *page_list,
@@ -1745,7 +1798,8 @@ __global__ void __launch_bounds__(256) fine_scan_mfma_kernel(
     int partial_len, int page_size, int tpi, int hkv, const char *__restrict__ q, int64_t qs0,
     int64_t qs1, int64_t qs2, int hq, int qlen, float scale, int round, uint32_t *__restrict__ out, int64_t ld,
     const float *__restrict__ coarse_stats, int rows, int n_pages, int32_t *pages_out, int32_t *union_out,
-    float *stats_out, double *stats_accum, char *__restrict__ k_stage, const char *__restrict__ k_read) {
+    float *stats_out, double *stats_accum, char *__restrict__ k_stage, const char *__restrict__ k_read,
+    SelectPlan sp) {
   static_assert(DT != DT_F32, "16-bit dtypes only");
   constexpr int D = 32 * KT, CPR = D / 8, ROW = D + 8;  // LDS rows padded by 16 bytes
   extern __shared__ uint4 smem4[];
@@ -1776,11 +1830,23 @@ __global__ void __launch_bounds__(256) fine_scan_mfma_kernel(
     U = counters[0];
   }
   __syncthreads();
+  // The plan blocks (the grid's last column): batch row b's threshold and
+  // the union pages the fine select reads.
+  const int nscan = sp.plan ? (int)gridDim.x - 1 : (int)gridDim.x;
+  if ((int)blockIdx.x >= nscan) {
+    if (kvh == 0) {
+      __shared__ SelSh<256> tsh;
+      select_plan<256>(sp, b, hkv, U, page_size, partial_len, [&](int v) -> int64_t {
+        return union_src == UNION_ROWS ? upage[v] : page_list[v];
+      }, tsh, scan_tmp);
+    }
+    return;
+  }
   const int nsplit = (page_size + tpi - 1) / tpi;
   const int page_items = U * nsplit;
   const int items = page_items + (partial_len + tpi - 1) / tpi;
   constexpr int64_t row_bytes = (int64_t)D * 2;
-  for (int item = blockIdx.x; item < items; item += gridDim.x) {
+  for (int item = blockIdx.x; item < items; item += nscan) {
     const char *rowbase;
     int64_t cand0;
     int ntok;
@@ -1843,7 +1909,11 @@ __global__ void __launch_bounds__(256) fine_scan_mfma_kernel(
 // scored candidates to list_count[B + b]; after a pruned scan, the slices
 // it read to list_count[2B + b]) and zeroes the keys for the next
 // scan, which accumulates with atomicMax.  Keys a pruned scan skipped are
-// zero; at least k keys are scored, so none of them is listed.
+// zero; at least k keys are scored, so none of them is listed.  With page
+// bounds (ub) the block reads only the planned pages' keys, after a pruned
+// scan or, with zero_all, after a full scan whose plan blocks listed the
+// pages (the keys of the others stay below T, so below the k-th largest);
+// zero_all then clears the whole row.
 // V = 16-byte key chunks per thread kept in registers: rows of up to
 // 4 * V * NT keys are read once; longer rows are re-read.
 template <int V, int NT>
@@ -1851,7 +1921,8 @@ __global__ void __launch_bounds__(NT) fine_select_kernel(
     uint32_t *__restrict__ keys, int64_t ld, const int32_t *__restrict__ counters, int has_pages, int page_size,
     int partial_len, int width, float *__restrict__ fine_stats, uint64_t *__restrict__ list, int64_t list_ld,
     int32_t *__restrict__ list_count, int list_cap, const uint32_t *__restrict__ ub, int kr, int hkv,
-    const uint32_t *__restrict__ thr, const int32_t *__restrict__ page_list, const int32_t *__restrict__ plan) {
+    const uint32_t *__restrict__ thr, const int32_t *__restrict__ page_list, const int32_t *__restrict__ plan,
+    int zero_all) {
   __shared__ SelSh<NT> sh;
   __shared__ uint64_t cand[kCandCap];
   __shared__ int plist[kPageListCap];
@@ -1918,7 +1989,12 @@ __global__ void __launch_bounds__(NT) fine_select_kernel(
         C = k;
       }
       __syncthreads();
-      for (int e = threadIdx.x; e < pk.mall; e += NT) row[pk.index(e)] = 0u;
+      if (zero_all) {  // a full scan wrote every key
+        uint4 *row4 = reinterpret_cast<uint4 *>(row);
+        for (int i = threadIdx.x; i < (n + 3) / 4; i += NT) row4[i] = make_uint4(0, 0, 0, 0);
+      } else {
+        for (int e = threadIdx.x; e < pk.mall; e += NT) row[pk.index(e)] = 0u;
+      }
       if (threadIdx.x == 0) {
         fine_stats[2 * b] = mx;
         fine_stats[2 * b + 1] = sum;
@@ -2294,6 +2370,11 @@ static int retrieve_impl(kiv_store_t *s, const kiv_retrieve_args_t *a, hipStream
   const bool fine_mfma = dt != KIV_DTYPE_F32 && D % 32 == 0 && (ktf <= 4 || ktf == 6 || ktf == 8) &&
                          (G * Qb >= kFineMfmaRows || (!host_tier && !prune_ok)) && a->scaling > 0.f;
   const bool prune = prune_ok && !fine_mfma;
+  // After a full MFMA fine scan, the same page bounds and threshold let the
+  // fine select read only the union pages some kv row can lift to the top
+  // P' (a plan block of the scan lists them): its keys are exact either way.
+  const bool sel_plan = (a->flags & KIV_RETRIEVE_PRUNE) && passes == 1 && fresh && fine_mfma &&
+                        std::max(1, (a->out_width + ps - 1) / ps) < std::min(a->top_pages, N) && a->scaling > 0.f;
   // Page bound tables for the fine scan over wide kv rows (Phi-3.5 MHA
   // shape, 32 kv rows, 872 union pages: each fine-scan block's bound reads
   // drop from ~220 KiB of cache lines to ~7 KiB; fine scan 81.3 -> 71.0 us).
@@ -2303,7 +2384,7 @@ static int retrieve_impl(kiv_store_t *s, const kiv_retrieve_args_t *a, hipStream
   const uint32_t *pr_ub = nullptr, *pr_thr = nullptr;  // page bounds and thresholds of a pruned fine scan
   int32_t *pr_ctl = nullptr;
   s->prune_on = false;
-  if (prune) {
+  if (prune || sel_plan) {
     // [control, 256 B][thresholds [B]][upper bound keys [N][kr]][lower
     // bound keys [N][kr]][compact staging slots [N][kr]][select page lists
     // [B][kPlanStride]], zeroed (pruning on) when (re)allocated.
@@ -2320,7 +2401,7 @@ static int retrieve_impl(kiv_store_t *s, const kiv_retrieve_args_t *a, hipStream
       if ((rc = s->prune.ensure(need, st, false))) return rc;
       KIV_HIP(hipMemsetAsync(s->prune.ptr, 0, s->prune.bytes, st));
     }
-    pr.mode = 1;
+    pr.mode = prune ? 1 : 0;
     pr.ctl = (const int32_t *)s->prune.ptr;
     pr.thr = (uint32_t *)((char *)s->prune.ptr + thr_off);
     pr.ub = (const uint32_t *)((char *)s->prune.ptr + ub_off);
@@ -2332,7 +2413,7 @@ static int retrieve_impl(kiv_store_t *s, const kiv_retrieve_args_t *a, hipStream
     pr_ub = pr.ub;
     pr_thr = pr.thr;
     pr_ctl = (int32_t *)s->prune.ptr;
-    s->prune_on = true;
+    s->prune_on = prune;
     if (tables)
       bt = BoundTables{pr.ub, pr.lb, (uint32_t *)((char *)s->prune.ptr + lbmax_off),
                        (uint32_t *)((char *)s->prune.ptr + ubt_off), N, ldn, s->kr, hkv, B, 0};
@@ -2460,7 +2541,7 @@ static int retrieve_impl(kiv_store_t *s, const kiv_retrieve_args_t *a, hipStream
         KIV_HIP(hipGetLastError());
         row0 += rows_p;
       }
-      if (prune && !mfma) {
+      if ((prune || sel_plan) && !mfma) {
         // The VALU coarse scan leaves the pages' score bounds to this kernel.
         const int n_entries = rows * kc;
         rc = with_dt(dt, [&](auto dtc) {
@@ -2596,6 +2677,9 @@ static int retrieve_impl(kiv_store_t *s, const kiv_retrieve_args_t *a, hipStream
     // shape in HBM, 310 items per kv row: 14.7 us over 2048 blocks, 14.1
     // over 1024, 15.9 over 512).
     const int64_t nb_m = std::max<int64_t>(1, std::min<int64_t>(items_m, (1024 + s->kr - 1) / s->kr));
+    // The select's page plan (one pass, so the bounds cover every query row).
+    SelectPlan sp{};
+    if (sel_plan) sp = SelectPlan{pr.ub, pr.lb, s->kr, a->out_width, pr.thr, pr.plan, pr.ctl};
     for (int pass = 0; pass < passes && mfma; ++pass) {
       const int Qp = std::min(Qb, Q - pass * Qb);
       const int gq16 = (G * Qp + 15) & ~15;
@@ -2615,7 +2699,8 @@ static int retrieve_impl(kiv_store_t *s, const kiv_retrieve_args_t *a, hipStream
               if (lds > 65536)
                 KIV_HIP(hipFuncSetAttribute((const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
                                             (int)lds));
-              hipLaunchKernelGGL(kern, dim3((unsigned)nb_m, (unsigned)s->kr), dim3(256), lds, st, union_src,
+              hipLaunchKernelGGL(kern, dim3((unsigned)nb_m + (sp.plan ? 1u : 0u), (unsigned)s->kr), dim3(256), lds,
+                                 st, union_src,
                                  (const int32_t *)s->row_pages.ptr, rows * kc, bwords, (int32_t *)s->page_list.ptr,
                                  (int32_t *)s->counters.ptr, (const uint64_t *)s->k_tab.ptr, s->chunk_shift,
                                  s->page_bytes, (const char *)s->k_part.ptr, (int)s->partial_len, ps, tpi, hkv,
@@ -2623,7 +2708,7 @@ static int retrieve_impl(kiv_store_t *s, const kiv_retrieve_args_t *a, hipStream
                                  a->q_stride[2], hq, Qp, a->scaling, round, (uint32_t *)s->fine_keys.ptr, ldc,
                                  (const float *)coarse_stats, rows, N, a->pages_out, a->union_count_out,
                                  a->stats_out, a->stats_accum, pass == 0 ? k_stage : nullptr,
-                                 pass == 0 ? nullptr : k_stage);
+                                 pass == 0 ? nullptr : k_stage, sp);
               return (int)KIV_OK;
             }
           });
@@ -2668,7 +2753,7 @@ static int retrieve_impl(kiv_store_t *s, const kiv_retrieve_args_t *a, hipStream
       hipLaunchKernelGGL(kern, dim3(B), dim3(nt), 0, st, (uint32_t *)s->fine_keys.ptr, ldc,
                          (const int32_t *)s->counters.ptr, N > 0 ? 1 : 0, ps, (int)s->partial_len, a->out_width,
                          fine_stats, list, list_ld, list_count, list_cap, pr_ub, s->kr, hkv, pr_thr,
-                         (const int32_t *)s->page_list.ptr, (const int32_t *)pr.plan);
+                         (const int32_t *)s->page_list.ptr, (const int32_t *)pr.plan, sel_plan ? 1 : 0);
     };
     if (cmax > 4 * 4 * kSelThreads && !prune)
       with_select_chunks<kWideSelThreads>(cmax, [&](auto kern) { launch(kern, kWideSelThreads); },
@@ -2697,8 +2782,8 @@ static int retrieve_impl(kiv_store_t *s, const kiv_retrieve_args_t *a, hipStream
     ga.part_v = (const char *)s->v_part.ptr;
     ga.k_stage = k_stage;
     ga.stage_ld = ldc;
-    ga.ub = pr_ub;
-    ga.thr = pr_thr;
+    ga.ub = prune ? pr_ub : nullptr;  // what a pruned scan staged
+    ga.thr = prune ? pr_thr : nullptr;
     ga.ub_kr = s->kr;
     ga.cstage = pr.cstage;
     ga.slot_of = pr.slot_of;
