@@ -409,7 +409,7 @@ PRUNE = [
 ]
 
 
-@pytest.mark.parametrize("tier", ["host", "hbm", "split"])
+@pytest.mark.parametrize("tier", ["host", "hbm", "split", "hbm_plan", "split_plan"])
 @pytest.mark.parametrize("name,w,batch,clustered", PRUNE, ids=[c[0] for c in PRUNE])
 def test_fine_pruning_keeps_the_selection(cuda, monkeypatch, name, w, batch, clustered, tier):
     """The pruned fine scan against the full scan on the same store: the
@@ -418,13 +418,17 @@ def test_fine_pruning_keeps_the_selection(cuda, monkeypatch, name, w, batch, clu
     of the P-th largest key).  Where pages were skipped the fine mean, which
     covers the scored candidates only, differs.  On the HBM-resident tiers
     pruning is forced (KIV_PRUNE_DEVICE_BYTES=0; by default it starts at
-    256 MiB of union K) and the full scan is the MFMA scan."""
+    256 MiB of union K) and the full scan is the MFMA scan.  *_plan: the
+    default threshold, so the MFMA scan reads every slice and its plan
+    blocks list the pages the fine select reads (whose keys it then clears
+    whole: the next calls would show stale keys)."""
     from dataclasses import replace
 
-    if tier != "host":
+    plan = tier.endswith("_plan")
+    if tier in ("hbm", "split"):
         monkeypatch.setenv("KIV_PRUNE_DEVICE_BYTES", "0")
     data = generate(w, seed=2, batch=batch)
-    store, oracle, cfg = build(w, data, cuda, chunks=(3000, 1, 511), cold_tier=tier)
+    store, oracle, cfg = build(w, data, cuda, chunks=(3000, 1, 511), cold_tier=tier.split("_")[0])
     q = data["q"]
     runs = {}
     # Pruned, full, pruned again: after a call that skipped little (the
@@ -447,7 +451,11 @@ def test_fine_pruning_keeps_the_selection(cuda, monkeypatch, name, w, batch, clu
     assert f1["selected_token_indices"] == f0["selected_token_indices"]
     assert torch.equal(k1, k0) and torch.equal(v1, v0)
     assert f1["top_score"] == f0["top_score"]
-    if clustered:
+    if plan:
+        assert s1 == s0  # the scan read every slice
+        if clustered:
+            assert f1["mean_score"] > f0["mean_score"]  # the select's listed pages score high
+    elif clustered:
         assert s1[0] < s1[1] and f1["mean_score"] > f0["mean_score"]  # the skipped pages score low
 
 
@@ -805,6 +813,35 @@ LONG_QUERIES = [
     ("gqa_f16_mfma_scan_small_pages", Workload("lq4", 8, 2, 64, torch.float16, hot=32, cold=5000 + 77, top_pages=6,
                                                top_p=200, segment=256, page_size=32), 2, 24),
 ]
+
+
+@pytest.mark.parametrize("tier", ["host", "hbm"])
+def test_long_query_select_plan(cuda, tier):
+    """A one-pass query of G * Q >= 32 rows per kv row runs the MFMA fine
+    scan; with pruning on, its plan blocks list the pages the fine select
+    reads.  Against the oracle and against the same store without pruning:
+    the same ids in the same order and the same rows, twice in a row (the
+    select clears the whole key row the full scan wrote)."""
+    from dataclasses import replace
+
+    w = Workload("lq_plan", 8, 2, 64, torch.float16, hot=32, cold=6000 + 77, top_pages=12, top_p=200, segment=256,
+                 page_size=32)
+    data = generate(w, seed=43, batch=2)
+    g = torch.Generator().manual_seed(44)
+    store, oracle, cfg = build(w, data, cuda, cold_tier=tier)
+    listed_fewer = 0
+    for call in range(2):
+        q = data["q"].float().repeat(1, 1, 24, 1)
+        q = (q + (0.2 + 0.1 * call) * torch.randn(q.shape, generator=g)).to(w.dtype)
+        k1, v1, sel1 = check_retrieval(store, oracle, replace(cfg, fine_pruning=True), w, data, q)
+        f1 = store.telemetry_snapshot()["recent"][-1]
+        k0, v0 = store.retrieve_top_kv(q.to(cuda), w.scaling, cfg)
+        f0 = store.telemetry_snapshot()["recent"][-1]
+        assert f1["selected_token_indices"] == f0["selected_token_indices"]
+        assert torch.equal(k1.cpu(), k0.cpu()) and torch.equal(v1.cpu(), v0.cpu())
+        assert f1["top_score"] == f0["top_score"]
+        listed_fewer += f1["mean_score"] > f0["mean_score"]  # the select read only the high pages
+    assert listed_fewer > 0
 
 
 @pytest.mark.parametrize("name,w,batch,positions", LONG_QUERIES, ids=[c[0] for c in LONG_QUERIES])
