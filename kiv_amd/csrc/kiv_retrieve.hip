@@ -846,7 +846,7 @@ __global__ void __launch_bounds__(kScanMfmaThreads) coarse_scan_mfma_kernel(
     const char *__restrict__ summ, int64_t n_pages, int kr, const char *__restrict__ q, int64_t qs0,
     int64_t qs1, int64_t qs2, int hq, int hkv, int qlen, float scale, int round, uint32_t *__restrict__ keys,
     int64_t ld, const float *__restrict__ rad2, uint32_t *__restrict__ ubk, uint32_t *__restrict__ lbk,
-    AppendRows ap) {
+    const int32_t *__restrict__ ctl, AppendRows ap) {
   static_assert(DT != DT_F32, "16-bit dtypes only");
   if ((ap.count > 0 || ap.hot_count > 0) && blockIdx.x == gridDim.x - 1) {
     append_rows(ap, blockIdx.y);  // the step's evicted rows (an extra block per kv row)
@@ -862,9 +862,12 @@ __global__ void __launch_bounds__(kScanMfmaThreads) coarse_scan_mfma_kernel(
   uint4 x[KT];
 #pragma unroll
   for (int kk = 0; kk < KT; ++kk) x[kk] = load16(row + kk * 64);
-  // Pruned fine scan (ubk set): the page row's score bounds over the kv
-  // row's query rows, s.q +- |q| rad widened by 1e-4 |q| (|s| + rad)
-  // (Cauchy-Schwarz around the dtype summary s; rad, |s| from eviction).
+  // Pruned fine scan (ubk set, pruning not paused): the page row's score
+  // bounds over the kv row's query rows, s.q +- |q| rad widened by 1e-4 |q|
+  // (|s| + rad) (Cauchy-Schwarz around the dtype summary s; rad, |s| from
+  // eviction).
+  // The pause flag is read with the loads and tested after the scores.
+  const bool paused = ubk && *ctl > 0;
   float rad = 0.f, sn = 0.f, hi = -INFINITY, lo = -INFINITY;
   if (ubk && p < n_pages) {
     rad = rad2[2 * (p * kr + r)];
@@ -892,7 +895,7 @@ __global__ void __launch_bounds__(kScanMfmaThreads) coarse_scan_mfma_kernel(
         if (row_j < GQ) keys[(int64_t)(r * GQ + row_j) * ld + p] = order_key(score_of<DT>(acc[i], scale, round != 0));
       }
     }
-    if (ubk) {
+    if (ubk && !paused) {
       // |q| of row m0 + col from this lane group's elements, then of the
       // rows 4 kg + i this lane's results belong to.
       float qq = 0.f;
@@ -917,7 +920,7 @@ __global__ void __launch_bounds__(kScanMfmaThreads) coarse_scan_mfma_kernel(
       }
     }
   }
-  if (ubk) {
+  if (ubk && !paused) {
     hi = fmaxf(hi, __shfl_xor(hi, 16, 64));
     hi = fmaxf(hi, __shfl_xor(hi, 32, 64));
     lo = fmaxf(lo, __shfl_xor(lo, 16, 64));
@@ -1784,9 +1787,12 @@ __device__ void select_plan(const SelectPlan &sp, int b, int hkv, int U, int pag
     np += tot;
     read_all += rtot;
   }
+  // Slices for the pause decision: a plan of more than a quarter of the
+  // union pages counts as reading them all (the select then reads the whole
+  // row), so that the store pauses the bounds after it.
   if (threadIdx.x == 0) {
     pl[0] = np;
-    pl[1] = read_all;
+    pl[1] = 4 * np > U ? U * hkv : read_all;
   }
 }
 
@@ -1922,7 +1928,7 @@ __global__ void __launch_bounds__(NT) fine_select_kernel(
     int partial_len, int width, float *__restrict__ fine_stats, uint64_t *__restrict__ list, int64_t list_ld,
     int32_t *__restrict__ list_count, int list_cap, const uint32_t *__restrict__ ub, int kr, int hkv,
     const uint32_t *__restrict__ thr, const int32_t *__restrict__ page_list, const int32_t *__restrict__ plan,
-    int zero_all) {
+    int zero_all, const int32_t *__restrict__ ctl) {
   __shared__ SelSh<NT> sh;
   __shared__ uint64_t cand[kCandCap];
   __shared__ int plist[kPageListCap];
@@ -1935,7 +1941,7 @@ __global__ void __launch_bounds__(NT) fine_select_kernel(
   uint64_t *out = list + (int64_t)b * list_ld;
   float mx, sum;
   int C, nz;
-  if (ub) {
+  if (ub && *ctl <= 0) {  // not while pruning is paused (every key scored)
     // Pruned fine scan: only the pages some kv row of b scanned (and the
     // partial page) hold nonzero keys; the others are not read.
     const uint32_t tb = thr[b];
@@ -1971,8 +1977,9 @@ __global__ void __launch_bounds__(NT) fine_select_kernel(
       __syncthreads();  // fcnt is reused by the select below
     }
     // Few pages: select over their keys alone; else over the whole row
-    // (vector loads; the unscored keys are zero).
-    if (np <= kPageListCap && 2 * np <= U) {
+    // (vector loads; the unscored keys are zero).  After a full scan's plan
+    // "few" is at most a quarter (the whole row's register pass is fast).
+    if (np <= kPageListCap && (zero_all ? 4 * np : 2 * np) <= U) {
       const PageKeys<NT> pk{row, plist, np * page_size, np * page_size + partial_len, page_size,
                             (int64_t)U * page_size};
       if (pk.mall <= kRegPageKeys * NT) {
@@ -2492,7 +2499,7 @@ static int retrieve_impl(kiv_store_t *s, const kiv_retrieve_args_t *a, hipStream
                                    dim3(blocks + extra, s->kr), dim3(kScanMfmaThreads), 0, st, (const char *)s->summ.ptr,
                                    (int64_t)N, s->kr, qp, a->q_stride[0], a->q_stride[1], a->q_stride[2], hq, hkv,
                                    Qp, a->scaling, round, (uint32_t *)s->coarse_keys.ptr, ld,
-                                   (const float *)s->radius.ptr, (uint32_t *)pr.ub, (uint32_t *)pr.lb, apass);
+                                   (const float *)s->radius.ptr, (uint32_t *)pr.ub, (uint32_t *)pr.lb, pr.ctl, apass);
                 return (int)KIV_OK;
               });
             }
@@ -2753,7 +2760,7 @@ static int retrieve_impl(kiv_store_t *s, const kiv_retrieve_args_t *a, hipStream
       hipLaunchKernelGGL(kern, dim3(B), dim3(nt), 0, st, (uint32_t *)s->fine_keys.ptr, ldc,
                          (const int32_t *)s->counters.ptr, N > 0 ? 1 : 0, ps, (int)s->partial_len, a->out_width,
                          fine_stats, list, list_ld, list_count, list_cap, pr_ub, s->kr, hkv, pr_thr,
-                         (const int32_t *)s->page_list.ptr, (const int32_t *)pr.plan, sel_plan ? 1 : 0);
+                         (const int32_t *)s->page_list.ptr, (const int32_t *)pr.plan, sel_plan ? 1 : 0, pr.ctl);
     };
     if (cmax > 4 * 4 * kSelThreads && !prune)
       with_select_chunks<kWideSelThreads>(cmax, [&](auto kern) { launch(kern, kWideSelThreads); },

@@ -409,6 +409,9 @@ PRUNE = [
 ]
 
 
+PLAN_FEW = ("qwen_shape", "mqa_f16_d256")  # plans of at most a quarter of the union pages
+
+
 @pytest.mark.parametrize("tier", ["host", "hbm", "split", "hbm_plan", "split_plan"])
 @pytest.mark.parametrize("name,w,batch,clustered", PRUNE, ids=[c[0] for c in PRUNE])
 def test_fine_pruning_keeps_the_selection(cuda, monkeypatch, name, w, batch, clustered, tier):
@@ -453,8 +456,11 @@ def test_fine_pruning_keeps_the_selection(cuda, monkeypatch, name, w, batch, clu
     assert f1["top_score"] == f0["top_score"]
     if plan:
         assert s1 == s0  # the scan read every slice
-        if clustered:
-            assert f1["mean_score"] > f0["mean_score"]  # the select's listed pages score high
+        # The select reads the listed pages alone when they are at most a
+        # quarter of the union (then their mean is higher), else the row.
+        assert f1["mean_score"] >= f0["mean_score"]
+        if name in PLAN_FEW:
+            assert f1["mean_score"] > f0["mean_score"]
     elif clustered:
         assert s1[0] < s1[1] and f1["mean_score"] > f0["mean_score"]  # the skipped pages score low
 
@@ -821,18 +827,19 @@ def test_long_query_select_plan(cuda, tier):
     scan; with pruning on, its plan blocks list the pages the fine select
     reads.  Against the oracle and against the same store without pruning:
     the same ids in the same order and the same rows, twice in a row (the
-    select clears the whole key row the full scan wrote)."""
+    select clears the whole key row the full scan wrote); the plan is a few
+    of the union's pages here, so the select reads them alone."""
     from dataclasses import replace
 
-    w = Workload("lq_plan", 8, 2, 64, torch.float16, hot=32, cold=6000 + 77, top_pages=12, top_p=200, segment=256,
-                 page_size=32)
-    data = generate(w, seed=43, batch=2)
+    w = Workload("lq_plan", 28, 4, 128, torch.bfloat16, hot=64, cold=20000 + 37, top_pages=16, top_p=256,
+                 segment=1024)
+    data = generate(w, seed=2)
     g = torch.Generator().manual_seed(44)
     store, oracle, cfg = build(w, data, cuda, cold_tier=tier)
     listed_fewer = 0
     for call in range(2):
-        q = data["q"].float().repeat(1, 1, 24, 1)
-        q = (q + (0.2 + 0.1 * call) * torch.randn(q.shape, generator=g)).to(w.dtype)
+        q = data["q"].float().repeat(1, 1, 5, 1)  # 35 rows per kv row
+        q = (q + (0.05 + 0.05 * call) * torch.randn(q.shape, generator=g)).to(w.dtype)
         k1, v1, sel1 = check_retrieval(store, oracle, replace(cfg, fine_pruning=True), w, data, q)
         f1 = store.telemetry_snapshot()["recent"][-1]
         k0, v0 = store.retrieve_top_kv(q.to(cuda), w.scaling, cfg)
