@@ -858,7 +858,26 @@ __global__ void __launch_bounds__(kScanMfmaThreads) coarse_scan_mfma_kernel(
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int col = lane & 15, kg = lane >> 4;
   const int64_t p = ((int64_t)blockIdx.x * (kScanMfmaThreads / 64) + wave) * kScanMfmaPages + col;
-  const char *row = summ + (min(p, n_pages - 1) * kr + r) * kRowBytes + kg * 16;
+  const int64_t pc = min(p, n_pages - 1);
+  const char *row = summ + (pc * kr + r) * kRowBytes + kg * 16;
+  auto q_tile = [&](int m0, uint4 (&qa)[KT]) {
+    const int j = m0 + col;
+    if (j < GQ) {
+      const char *qr = q + ((int64_t)b * qs0 + (int64_t)(kvh * G + j / qlen) * qs1 + (int64_t)(j % qlen) * qs2) * 2 +
+                       kg * 16;
+#pragma unroll
+      for (int kk = 0; kk < KT; ++kk) qa[kk] = load16(qr + kk * 64);
+    } else {
+#pragma unroll
+      for (int kk = 0; kk < KT; ++kk) qa[kk] = make_uint4(0, 0, 0, 0);
+    }
+  };
+  // Loads in the order they are used: the first 16 query rows' operands
+  // and, for the bounds, the page row's radius and |s|, then the summaries,
+  // so that the rows' norms are computed while the summaries are in flight.
+  uint4 q0[KT];
+  q_tile(0, q0);
+  const float rad = ubk ? rad2[2 * (pc * kr + r)] : 0.f, sn = ubk ? rad2[2 * (pc * kr + r) + 1] : 0.f;
   uint4 x[KT];
 #pragma unroll
   for (int kk = 0; kk < KT; ++kk) x[kk] = load16(row + kk * 64);
@@ -868,22 +887,29 @@ __global__ void __launch_bounds__(kScanMfmaThreads) coarse_scan_mfma_kernel(
   // eviction).
   // The pause flag is read with the loads and tested after the scores.
   const bool paused = ubk && *ctl > 0;
-  float rad = 0.f, sn = 0.f, hi = -INFINITY, lo = -INFINITY;
-  if (ubk && p < n_pages) {
-    rad = rad2[2 * (p * kr + r)];
-    sn = rad2[2 * (p * kr + r) + 1];
-  }
+  // |q| of row m0 + col from this lane group's elements.
+  auto q_norm = [&](const uint4 (&qa)[KT]) {
+    float qq = 0.f;
+#pragma unroll
+    for (int kk = 0; kk < KT; ++kk) {
+      float f[8];
+      unpack_chunk<DT>(qa[kk], f);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) qq = fmaf(f[e], f[e], qq);
+    }
+    qq += __shfl_xor(qq, 16, 64);
+    qq += __shfl_xor(qq, 32, 64);
+    return sqrtf(qq);
+  };
+  const float qn0 = ubk ? q_norm(q0) : 0.f;
+  float hi = -INFINITY, lo = -INFINITY;
   for (int m0 = 0; m0 < GQ; m0 += 16) {
-    const int j = m0 + col;
     uint4 qa[KT];
-    if (j < GQ) {
-      const char *qr = q + ((int64_t)b * qs0 + (int64_t)(kvh * G + j / qlen) * qs1 + (int64_t)(j % qlen) * qs2) * 2 +
-                       kg * 16;
+    if (m0 == 0) {
 #pragma unroll
-      for (int kk = 0; kk < KT; ++kk) qa[kk] = load16(qr + kk * 64);
+      for (int kk = 0; kk < KT; ++kk) qa[kk] = q0[kk];
     } else {
-#pragma unroll
-      for (int kk = 0; kk < KT; ++kk) qa[kk] = make_uint4(0, 0, 0, 0);
+      q_tile(m0, qa);
     }
     f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -896,19 +922,8 @@ __global__ void __launch_bounds__(kScanMfmaThreads) coarse_scan_mfma_kernel(
       }
     }
     if (ubk && !paused) {
-      // |q| of row m0 + col from this lane group's elements, then of the
-      // rows 4 kg + i this lane's results belong to.
-      float qq = 0.f;
-#pragma unroll
-      for (int kk = 0; kk < KT; ++kk) {
-        float f[8];
-        unpack_chunk<DT>(qa[kk], f);
-#pragma unroll
-        for (int e = 0; e < 8; ++e) qq = fmaf(f[e], f[e], qq);
-      }
-      qq += __shfl_xor(qq, 16, 64);
-      qq += __shfl_xor(qq, 32, 64);
-      const float qnorm = sqrtf(qq);
+      // |q| of the rows 4 kg + i this lane's results belong to.
+      const float qnorm = m0 == 0 ? qn0 : q_norm(qa);
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const float qn = __shfl(qnorm, 4 * kg + i, 64);
