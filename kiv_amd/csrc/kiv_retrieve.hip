@@ -296,7 +296,7 @@ __device__ void block_compact(const Src &src, P &&pred, E &&emit, int cap, int *
 // holds its keys 4c + j.
 template <int NT, int V> struct RegKeys4 {
   static constexpr int W = NT / 64;
-  static constexpr bool kManySteps = V > 4;  // placement in two passes (see bound_candidates)
+  static constexpr bool kManySteps = V >= 4;  // placement in two passes (see bound_candidates)
   uint4 v[V];
   int n;
   __device__ static int chunk(int i) { return (threadIdx.x >> 6) + W * ((threadIdx.x & 63) + 64 * i); }
