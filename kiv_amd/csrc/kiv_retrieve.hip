@@ -555,22 +555,25 @@ __device__ __forceinline__ uint32_t max_keys(const uint32_t *p, int n) {
 }
 
 // Page bound tables of a pruned fine scan over many kv rows, built from the
-// bound keys ub/lb [n][kr] once they exist: lbmax[n][batch], a page's
-// largest lower-bound key over one batch row's hkv kv rows, and ubT[kr][ldn],
-// the upper-bound keys transposed.  Every fine-scan block then reads 4
-// bytes per union page for each (contiguous over ascending pages) instead
-// of an hkv-key run and one key of each page's kr-key row.  rows = 0: none.
+// bound keys ub/lb [n][kr] once they exist: lbmax[n][batch] and
+// ubmax[n][batch], a page's largest lower- and upper-bound keys over one
+// batch row's hkv kv rows, and ubT[kr][ldn], the upper-bound keys
+// transposed.  Every fine-scan block then reads 4 bytes per union page for
+// each (contiguous over ascending pages) instead of an hkv-key run and one
+// key of each page's kr-key row, and the select's page list tests one key
+// per page.  rows = 0: none.
 struct BoundTables {
   const uint32_t *ub, *lb;
-  uint32_t *lbmax, *ubT;
+  uint32_t *lbmax, *ubmax, *ubT;
   int64_t n, ldn;
   int kr, hkv, batch, rows;
 };
 
 // Table entries of the launch's extra blocks: the transpose's items (4 kv
-// rows of one page each when kr is a multiple of 4, else 1), then lbmax's.
+// rows of one page each when kr is a multiple of 4, else 1), then lbmax's,
+// then ubmax's.
 __host__ __device__ inline int64_t bound_table_items(int64_t n, int kr, int batch) {
-  return n * ((kr & 3) == 0 ? kr / 4 : kr) + n * batch;
+  return n * ((kr & 3) == 0 ? kr / 4 : kr) + 2 * n * batch;
 }
 
 // The tables, by the blocks of a launch past its first bt.rows: one item a
@@ -596,6 +599,9 @@ template <int NT> __device__ void fill_bound_tables(const BoundTables &bt) {
   } else if (t < nt + n * bt.batch) {
     const int j = t - nt;
     bt.lbmax[j] = max_keys(bt.lb + (int64_t)(j / bt.batch) * bt.kr + (int64_t)(j % bt.batch) * bt.hkv, bt.hkv);
+  } else if (t < nt + 2 * n * bt.batch) {
+    const int j = t - nt - n * bt.batch;
+    bt.ubmax[j] = max_keys(bt.ub + (int64_t)(j / bt.batch) * bt.kr + (int64_t)(j % bt.batch) * bt.hkv, bt.hkv);
   }
 }
 
@@ -1130,8 +1136,8 @@ constexpr int kPlanStride = 2 + kPageListCap;
 
 // The page bound tables (BoundTables) of a pruned scan follow the select
 // page lists of `batch` rows in the same buffer, 256-byte aligned: lbmax
-// [n][batch], then ubT [kr][ldn] at lbmax + ((n * batch + 63) & ~63), ldn =
-// (n + 63) & ~63.
+// [n][batch], ubmax [n][batch] at lbmax + nb, then ubT [kr][ldn] at
+// lbmax + 2 nb, with nb = (n * batch + 63) & ~63 and ldn = (n + 63) & ~63.
 __device__ __forceinline__ const uint32_t *bound_tables_at(const int32_t *plan, int batch) {
   const uintptr_t end = reinterpret_cast<uintptr_t>(plan + (int64_t)batch * kPlanStride);
   return reinterpret_cast<const uint32_t *>((end + 255) & ~uintptr_t(255));
@@ -1504,6 +1510,23 @@ __global__ void __launch_bounds__(256) fine_scan_kernel(
     // b's lower bound, this kv row's upper bound), after the union list.
     const int upage_cap = min(row_pages_n, n_pages);
     uint32_t *lbt = reinterpret_cast<uint32_t *>(upage + upage_cap), *ubt = lbt + upage_cap;
+    // Page bound tables (TAB): b's largest lower- and upper-bound keys of
+    // each page, and this kv row's upper-bound keys.
+    int batch = 0;
+    const uint32_t *lbmax = nullptr, *ubmax = nullptr, *ubT = nullptr;
+    if constexpr (TAB && !SPEC) {
+      batch = (int)gridDim.y / hkv;
+      const int64_t nb = ((int64_t)n_pages * batch + 63) & ~int64_t(63);
+      lbmax = bound_tables_at(pr.plan, batch);
+      ubmax = lbmax + nb;
+      ubT = ubmax + nb + (int64_t)r * (((int64_t)n_pages + 63) & ~int64_t(63));
+    }
+    // With short row lists (kUnionPF entries a thread) the tables' keys of
+    // each union page are loaded by the entry that marks the page, before
+    // the union is ranked, and placed in LDS by union rank, as with
+    // speculation: two dependent global round trips fewer before the
+    // threshold.
+    const bool tab_pre = TAB && !SPEC && pruned && union_src == UNION_ROWS && row_pages_n <= kUnionPF * 256;
     int U = 0;
     if constexpr (SPEC) {
       // The row list in registers, marked in the union bitmap; the first
@@ -1557,7 +1580,37 @@ __global__ void __launch_bounds__(256) fine_scan_kernel(
         publish_union<DT>(upage, U, page_list, pages_out, counters, union_out, coarse_stats, rows, n_pages, round,
                           stats_out, stats_accum);
     } else if (union_src == UNION_ROWS) {
-      U = rank_union<256>(row_pages, row_pages_n, words, ubits, upage, scan_tmp);
+      if (tab_pre) {
+        int ent[kUnionPF];
+        bool own[kUnionPF];
+        uint32_t elb[kUnionPF], eub[kUnionPF];
+#pragma unroll
+        for (int u = 0; u < kUnionPF; ++u) {
+          const int e = tid + u * 256;
+          ent[u] = e < row_pages_n ? row_pages[e] : -1;
+        }
+        union_mark<256>(ent, row_pages, row_pages_n, words, ubits, own);
+#pragma unroll
+        for (int u = 0; u < kUnionPF; ++u) {
+          elb[u] = own[u] ? lbmax[(int64_t)ent[u] * batch + b] : 0u;
+          eub[u] = own[u] ? ubT[ent[u]] : 0u;
+        }
+        U = union_list<256>(words, ubits, upage, scan_tmp);
+#pragma unroll
+        for (int u = 0; u < kUnionPF; ++u) {
+          if (!own[u]) continue;
+          int lo = 0, hi = U - 1;  // the entry's union rank (upage ascends)
+          while (lo < hi) {
+            const int mid = (lo + hi) >> 1;
+            if (upage[mid] < ent[u]) lo = mid + 1;
+            else hi = mid;
+          }
+          lbt[lo] = elb[u];
+          ubt[lo] = eub[u];
+        }
+      } else {
+        U = rank_union<256>(row_pages, row_pages_n, words, ubits, upage, scan_tmp);
+      }
       if (blockIdx.x == 0 && blockIdx.y == 0)
         publish_union<DT>(upage, U, page_list, pages_out, counters, union_out, coarse_stats, rows, n_pages, round,
                           stats_out, stats_accum);
@@ -1586,24 +1639,17 @@ __global__ void __launch_bounds__(256) fine_scan_kernel(
       // bound together.
       const bool one_each = U <= 256;
       const int v1 = (tid >> 6) + 4 * (tid & 63);
-      // Bound keys of union rank v: from the LDS tables with speculation,
-      // else from the page bound tables (TAB) or the bound keys themselves.
-      const uint32_t *lbmax = nullptr, *ubT = nullptr;
-      int batch = 0;
-      if constexpr (TAB && !SPEC) {
-        batch = (int)gridDim.y / hkv;
-        lbmax = bound_tables_at(pr.plan, batch);
-        ubT = lbmax + ((((int64_t)n_pages * batch + 63) & ~int64_t(63)) +
-                       (int64_t)r * (((int64_t)n_pages + 63) & ~int64_t(63)));
-      }
+      // Bound keys of union rank v: from the LDS tables with speculation
+      // (or preloaded from the page bound tables), else from the page bound
+      // tables (TAB) or the bound keys themselves.
       auto lb_of = [&](int v) {
         if constexpr (SPEC) return lbt[v];
-        else if constexpr (TAB) return lbmax[page_of(v) * batch + b];
+        else if constexpr (TAB) return tab_pre ? lbt[v] : lbmax[page_of(v) * batch + b];
         else return max_keys(pr.lb + page_of(v) * pr.kr + b * hkv, hkv);
       };
       auto ub_of = [&](int v) {
         if constexpr (SPEC) return ubt[v];
-        else if constexpr (TAB) return ubT[page_of(v)];
+        else if constexpr (TAB) return tab_pre ? ubt[v] : ubT[page_of(v)];
         else return ubr[page_of(v) * pr.kr];
       };
       uint32_t lb1 = 0u, ub1 = 0u;
@@ -1685,16 +1731,48 @@ __global__ void __launch_bounds__(256) fine_scan_kernel(
         // of some kv row of b at or above T, and the slices read.
         int32_t *pl = pr.plan + (int64_t)b * kPlanStride;
         int np = 0, read_all = 0;
-        for (int c0 = 0; c0 < U; c0 += 256) {
-          const int v = c0 + tid;
-          const int read = v < U ? count_keys_ge(pr.ub + page_of(v) * pr.kr + b * hkv, hkv, tb) : 0;
-          const int hit = read > 0 ? 1 : 0;
-          int tot, rtot;
-          const int pos = np + block_incl_scan<256>(hit, scan_tmp, &tot) - hit;
-          if (hit && pos < kPageListCap) pl[2 + pos] = v;
-          block_incl_scan<256>(read, scan_tmp, &rtot);
-          np += tot;
-          read_all += rtot;
+        if constexpr (TAB && !SPEC) {
+          // One key a page (ubmax) says whether some kv row of b reaches T;
+          // only those pages count their slices.  A thread's pages in
+          // flight together, then the scans.
+          int rsum = 0;
+          for (int c0 = 0; c0 < U; c0 += kUnionPF * 256) {
+            int64_t pg[kUnionPF];
+            uint32_t um[kUnionPF];
+            int rd[kUnionPF];
+#pragma unroll
+            for (int u = 0; u < kUnionPF; ++u) {
+              const int v = c0 + u * 256 + tid;
+              pg[u] = v < U ? page_of(v) : -1;
+            }
+#pragma unroll
+            for (int u = 0; u < kUnionPF; ++u) um[u] = pg[u] >= 0 ? ubmax[pg[u] * batch + b] : 0u;
+#pragma unroll
+            for (int u = 0; u < kUnionPF; ++u)
+              rd[u] = pg[u] >= 0 && um[u] >= tb ? count_keys_ge(pr.ub + pg[u] * pr.kr + b * hkv, hkv, tb) : 0;
+#pragma unroll
+            for (int u = 0; u < kUnionPF; ++u) {
+              const int hit = rd[u] > 0 ? 1 : 0;
+              int tot;
+              const int pos = np + block_incl_scan<256>(hit, scan_tmp, &tot) - hit;
+              if (hit && pos < kPageListCap) pl[2 + pos] = c0 + u * 256 + tid;
+              np += tot;
+              rsum += rd[u];
+            }
+          }
+          block_incl_scan<256>(rsum, scan_tmp, &read_all);
+        } else {
+          for (int c0 = 0; c0 < U; c0 += 256) {
+            const int v = c0 + tid;
+            const int read = v < U ? count_keys_ge(pr.ub + page_of(v) * pr.kr + b * hkv, hkv, tb) : 0;
+            const int hit = read > 0 ? 1 : 0;
+            int tot, rtot;
+            const int pos = np + block_incl_scan<256>(hit, scan_tmp, &tot) - hit;
+            if (hit && pos < kPageListCap) pl[2 + pos] = v;
+            block_incl_scan<256>(read, scan_tmp, &rtot);
+            np += tot;
+            read_all += rtot;
+          }
         }
         if (tid == 0) {
           pl[0] = np;
@@ -2413,11 +2491,12 @@ static int retrieve_impl(kiv_store_t *s, const kiv_retrieve_args_t *a, hipStream
     const size_t thr_off = 256, ub_off = thr_off + (((size_t)B * 4 + 255) & ~size_t(255));
     const size_t nb_keys = (((size_t)N * s->kr + 63) & ~size_t(63)) * 4;
     const size_t plan_off = ub_off + 3 * nb_keys;
-    // [bound tables: lbmax [N][B], ubT [kr][ldn]] follow in mode 2 (at
-    // the offsets bound_tables_at finds).
+    // [bound tables: lbmax [N][B], ubmax [N][B], ubT [kr][ldn]] follow
+    // when the scan uses them (at the offsets bound_tables_at finds).
     const int64_t ldn = ((int64_t)N + 63) & ~int64_t(63);
     const size_t lbmax_off = (plan_off + (size_t)B * kPlanStride * 4 + 255) & ~size_t(255);
-    const size_t ubt_off = lbmax_off + (((size_t)N * B * 4 + 255) & ~size_t(255));
+    const size_t ubmax_off = lbmax_off + (((size_t)N * B * 4 + 255) & ~size_t(255));
+    const size_t ubt_off = ubmax_off + (((size_t)N * B * 4 + 255) & ~size_t(255));
     const size_t need = tables ? ubt_off + (size_t)s->kr * ldn * 4 : plan_off + (size_t)B * kPlanStride * 4;
     if (s->prune.bytes < need) {
       if ((rc = s->prune.ensure(need, st, false))) return rc;
@@ -2438,7 +2517,8 @@ static int retrieve_impl(kiv_store_t *s, const kiv_retrieve_args_t *a, hipStream
     s->prune_on = prune;
     if (tables)
       bt = BoundTables{pr.ub, pr.lb, (uint32_t *)((char *)s->prune.ptr + lbmax_off),
-                       (uint32_t *)((char *)s->prune.ptr + ubt_off), N, ldn, s->kr, hkv, B, 0};
+                       (uint32_t *)((char *)s->prune.ptr + ubmax_off), (uint32_t *)((char *)s->prune.ptr + ubt_off),
+                       N, ldn, s->kr, hkv, B, 0};
   }
 
   if (a->hot_tokens > 0) {
@@ -2742,8 +2822,12 @@ static int retrieve_impl(kiv_store_t *s, const kiv_retrieve_args_t *a, hipStream
     }
     auto valu_scan = [&](int pass, int usrc, int bw, const FinePrune &fp) {
       const int Qp = std::min(Qb, Q - pass * Qb);
+      // LDS tables of the union pages' bound keys: with speculation, and
+      // for the page bound tables' preload (row lists of at most kUnionPF
+      // entries a thread).
+      const bool tab_pre = tables && fp.mode == 1 && usrc == UNION_ROWS && (int64_t)rows * kc <= kUnionPF * 256;
       const size_t lds = (size_t)G * Qp * D * eb + (size_t)bw * 4 + (fp.mode == 1 ? (size_t)kPageListCap * 4 : 0) +
-                         (usrc == UNION_ROWS ? upage_bytes : 0) + (fp.spec > 0 ? 2 * upage_bytes : 0);
+                         (usrc == UNION_ROWS ? upage_bytes : 0) + (fp.spec > 0 || tab_pre ? 2 * upage_bytes : 0);
       return with_dt_lg(dt, lg, [&](auto dtc, auto lgc) {
         auto kern = tables && fp.mode == 1 ? fine_scan_kernel<decltype(dtc)::value, decltype(lgc)::value, true>
                                            : fine_scan_kernel<decltype(dtc)::value, decltype(lgc)::value, false>;
