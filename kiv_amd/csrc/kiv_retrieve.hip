@@ -1012,10 +1012,78 @@ __device__ __forceinline__ void coarse_select_row(const uint32_t *__restrict__ k
   }
 }
 
+// The speculative fine scan's first page, read ahead (host tier): blocks
+// of the coarse select past its query rows, `parts` per kv row r, take the
+// top page of r's first query row (the largest key, the lowest page on
+// ties: the row's rank 0, which the speculative scan reads first) and copy
+// their NT 16-byte pieces of that page's K slice of r from host memory to
+// buf[r] in HBM, then record (page, call) in meta[r] (every part the same).
+// The host link is idle while the selects rank their rows; the fine scan's
+// speculative blocks of that page read the copy, a page of host reads fewer
+// per kv row on its critical path.
+struct FirstPagePrefetch {
+  const uint64_t *ktab;
+  int chunk_shift;
+  int64_t page_bytes, row_bytes;
+  int page_size, gq, kr, parts, rows;  // rows: the launch's select blocks, before the prefetch blocks
+  const int32_t *ctl;           // pruning control: nothing to read while paused (> 0)
+  char *buf;                    // [kr][page_size][D] dtype
+  int32_t *meta;                // [kr][2]: page, call
+  int call;
+};
+
+template <int NT>
+__device__ void prefetch_first_page(const uint32_t *__restrict__ keys, int64_t ld, int n, const FirstPagePrefetch &pf) {
+  __shared__ uint64_t wbest[NT / 64];
+  const int j = (int)blockIdx.x - pf.rows, r = j / pf.parts, part = j - r * pf.parts;
+  if (r >= pf.kr || n <= 0 || *pf.ctl > 0) return;
+  // The row's keys (256-byte aligned, zero past n): the largest composite.
+  const uint4 *src = reinterpret_cast<const uint4 *>(keys + (int64_t)r * pf.gq * ld);
+  uint64_t best = 0;
+  const int n4 = (n + 3) >> 2;
+#pragma unroll 4
+  for (int c = threadIdx.x; c < n4; c += NT) {
+    const uint4 x = src[c];
+    const int p0 = 4 * c;
+    best = max(best, comp_of(x.x, p0));
+    if (p0 + 1 < n) best = max(best, comp_of(x.y, p0 + 1));
+    if (p0 + 2 < n) best = max(best, comp_of(x.z, p0 + 2));
+    if (p0 + 3 < n) best = max(best, comp_of(x.w, p0 + 3));
+  }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) {
+    const uint32_t hi = __shfl_xor((uint32_t)(best >> 32), off, 64), lo = __shfl_xor((uint32_t)best, off, 64);
+    best = max(best, ((uint64_t)hi << 32) | lo);
+  }
+  if ((threadIdx.x & 63) == 0) wbest[threadIdx.x >> 6] = best;
+  __syncthreads();
+#pragma unroll
+  for (int w = 0; w < NT / 64; ++w) best = max(best, wbest[w]);
+  const int64_t page = comp_index(best);
+  if (page < 0 || page >= n) return;
+  // This part's 16-byte pieces of the page's slice of kv row r.
+  const int64_t bytes = (int64_t)pf.page_size * pf.row_bytes;
+  const char *from = reinterpret_cast<const char *>(pf.ktab[page >> pf.chunk_shift]) +
+                     (page & ((int64_t(1) << pf.chunk_shift) - 1)) * pf.page_bytes + (int64_t)r * bytes;
+  char *to = pf.buf + (int64_t)r * bytes;
+  const auto rs = tile_rsrc(from, (uint32_t)bytes);
+  const int64_t o = ((int64_t)part * NT + threadIdx.x) * 16;
+  const uint4 x = buf_load16(rs, o < bytes ? (uint32_t)o : (uint32_t)bytes);
+  if (o < bytes) *reinterpret_cast<uint4 *>(to + o) = x;
+  if (threadIdx.x == 0) {
+    pf.meta[2 * r] = (int32_t)page;
+    pf.meta[2 * r + 1] = pf.call;
+  }
+}
+
 template <int NT, int V>
 __global__ void __launch_bounds__(NT) coarse_select_kernel(const uint32_t *__restrict__ keys, int64_t ld, int n,
                                                             int k, int32_t *__restrict__ row_pages,
-                                                            float *__restrict__ coarse_stats) {
+                                                            float *__restrict__ coarse_stats, FirstPagePrefetch pf) {
+  if ((int)blockIdx.x >= pf.rows) {
+    prefetch_first_page<NT>(keys, ld, n, pf);
+    return;
+  }
   coarse_select_row<NT, V>(keys, ld, n, k, row_pages, coarse_stats);
 }
 
@@ -1131,6 +1199,12 @@ struct FinePrune {
   // kv row's first query row (lists of spec_kc pages) are read before the
   // threshold is known (0: none).
   int spec, spec_kc;
+  // The first speculative page's copy in HBM (FirstPagePrefetch: buf, meta,
+  // call; meta null: none), read instead of host memory when meta[r] holds
+  // that page and this call.
+  const char *pf_buf;
+  const int32_t *pf_meta;
+  int pf_call;
 };
 constexpr int kPlanStride = 2 + kPageListCap;
 
@@ -1492,6 +1566,10 @@ __global__ void __launch_bounds__(256) fine_scan_kernel(
   const bool spec_block = (int)blockIdx.x < nspec * nsplit;
   const int sslice = blockIdx.x % nsplit;
   const int64_t spage = spec_block ? spec_list[blockIdx.x / nsplit] : -1;
+  // The first speculative page's slices come from its copy in HBM when the
+  // coarse select made one of that page in this call.
+  const bool pf_try = spec_block && (int)blockIdx.x < nsplit && pr.pf_meta != nullptr;
+  const int2 pfm = pf_try ? *reinterpret_cast<const int2 *>(pr.pf_meta + 2 * r) : make_int2(-1, -1);
   for (int i = tid; i < GQ * cpr; i += 256) {
     const int j = i / cpr, c = i % cpr;
     const int h = kvh * G + j / qlen, qp = j % qlen;
@@ -1501,6 +1579,11 @@ __global__ void __launch_bounds__(256) fine_scan_kernel(
   // Two bodies: with speculation (pruned by construction) and without,
   // so that no path of one joins the other's (a join would make the
   // compiler wait for the host read where the paths meet).
+  auto spec_rows = [&]() -> const char * {
+    if (pf_try && pfm.x == spage && pfm.y == pr.pf_call)
+      return pr.pf_buf + ((int64_t)r * page_size + (int64_t)sslice * tpi) * row_bytes;
+    return page_rows(spage, sslice);
+  };
   auto body = [&](auto spec_c) {
     constexpr bool SPEC = decltype(spec_c)::value;
     if (tid < nspec) spec_pg[tid] = my_spec;
@@ -1552,7 +1635,7 @@ __global__ void __launch_bounds__(256) fine_scan_kernel(
         elb[u] = spec_lower_key(lbk, prow + (int64_t)b * hkv, hkv, padded, own[u]);
       }
       const int ntok = spec_block ? min(tpi, page_size - sslice * tpi) : 0;
-      const char *srows = spec_block ? page_rows(spage, sslice) : q;  // an empty buffer when not speculating
+      const char *srows = spec_block ? spec_rows() : q;  // an empty buffer when not speculating
       __syncthreads();  // keeps the host read after the loads above
       const uint32_t bytes = (uint32_t)(ntok * row_bytes);
       const auto rs = tile_rsrc(srows, bytes);
@@ -1680,7 +1763,7 @@ __global__ void __launch_bounds__(256) fine_scan_kernel(
         const int64_t cand0 = (int64_t)lo * page_size + (int64_t)sslice * tpi;
         const int ntok = min(tpi, page_size - sslice * tpi);
         score_batch(xs, 0, ntok, cand0, stage_at(cand0));
-        scan_slice(page_rows(spage, sslice), cand0, ntok, stage_at(cand0), NSLOT * UT);
+        scan_slice(spec_rows(), cand0, ntok, stage_at(cand0), NSLOT * UT);
       }
       // Per window of kPageListCap union pages, the other pages whose upper
       // bound for this kv row reaches T are listed in LDS, then their slices
@@ -2479,6 +2562,27 @@ static int retrieve_impl(kiv_store_t *s, const kiv_retrieve_args_t *a, hipStream
   // shape, 32 kv rows, 872 union pages: each fine-scan block's bound reads
   // drop from ~220 KiB of cache lines to ~7 KiB; fine scan 81.3 -> 71.0 us).
   const bool tables = prune && s->kr > 8 && N > 0 && bound_table_items(N, s->kr, B) < (int64_t(1) << 31);
+  // The speculative scan's first page, read ahead by extra blocks of the
+  // coarse select (host tier): the speculation's conditions that are known
+  // before the coarse pass (the fine scan takes the copy only when it
+  // speculates, and only of this call).
+  const int64_t kc_fine = N > 0 ? std::min(a->top_pages, N) : 0;
+  const bool read_ahead = prune && host_tier && !tables &&
+                          (int64_t)rows * kc_fine <= std::min<int64_t>(kRowListInScan, kUnionPF * 256) &&
+                          spec_hkv_ok(hkv) && (int64_t)N * s->kr * 4 < (int64_t(1) << 30);
+  FirstPagePrefetch fpp{};
+  if (read_ahead) {
+    const size_t slice = (size_t)ps * s->row_bytes, need = (size_t)s->kr * (slice + 8);
+    if (s->first_page.bytes < need) {
+      if ((rc = s->first_page.ensure(need, st, false))) return rc;
+      KIV_HIP(hipMemsetAsync((char *)s->first_page.ptr + (size_t)s->kr * slice, 0xff, (size_t)s->kr * 8, st));
+    }
+    s->first_page_call = (int32_t)((uint32_t)s->first_page_call + 1u);
+    const int parts = (int)((slice + kSelThreads * 16 - 1) / (kSelThreads * 16));
+    fpp = FirstPagePrefetch{(const uint64_t *)s->k_tab.ptr, s->chunk_shift, s->page_bytes, s->row_bytes, ps,
+                            G * Q, s->kr, parts, 0, nullptr, (char *)s->first_page.ptr,
+                            (int32_t *)((char *)s->first_page.ptr + (size_t)s->kr * slice), s->first_page_call};
+  }
   BoundTables bt{};
   FinePrune pr{};
   const uint32_t *pr_ub = nullptr, *pr_thr = nullptr;  // page bounds and thresholds of a pruned fine scan
@@ -2634,9 +2738,16 @@ static int retrieve_impl(kiv_store_t *s, const kiv_retrieve_args_t *a, hipStream
                                (int32_t *)s->row_pages.ptr + (int64_t)row0 * kc, coarse_stats + 2 * row0, btp);
           }, [](auto vc) { return coarse_select_tables_kernel<kSelThreads, decltype(vc)::value>; });
         } else {
+          // With the read-ahead, `parts` more blocks per kv row copy its
+          // first query row's top page to HBM.
+          FirstPagePrefetch fp = fpp;
+          fp.rows = rows_p;
+          fp.ctl = pr.ctl;
+          const unsigned extra_blocks = fpp.buf ? (unsigned)(s->kr * fpp.parts) : 0u;
           with_select_chunks(N, [&](auto kern) {
-            hipLaunchKernelGGL(kern, dim3(rows_p), dim3(kSelThreads), 0, st, (const uint32_t *)s->coarse_keys.ptr,
-                               ld, N, kc, (int32_t *)s->row_pages.ptr + (int64_t)row0 * kc, coarse_stats + 2 * row0);
+            hipLaunchKernelGGL(kern, dim3(rows_p + extra_blocks), dim3(kSelThreads), 0, st,
+                               (const uint32_t *)s->coarse_keys.ptr, ld, N, kc,
+                               (int32_t *)s->row_pages.ptr + (int64_t)row0 * kc, coarse_stats + 2 * row0, fp);
           }, [](auto vc) { return coarse_select_kernel<kSelThreads, decltype(vc)::value>; });
         }
         if (!tables || mfma) s->prof_end(KIV_STAGE_COARSE_SELECT, st);  // else after the bound tables' launch
@@ -2761,6 +2872,11 @@ static int retrieve_impl(kiv_store_t *s, const kiv_retrieve_args_t *a, hipStream
     if (spec) {
       pr.spec = (int)std::min<int64_t>(std::min(kSpecPages, kc), nb / nsplit);
       pr.spec_kc = kc;
+      if (fpp.buf) {
+        pr.pf_buf = fpp.buf;
+        pr.pf_meta = fpp.meta;
+        pr.pf_call = fpp.call;
+      }
     }
     // The MFMA scan (whole 64-token slices staged in LDS) serves queries of
     // many rows per kv row on every tier, and every query on the device

@@ -375,7 +375,8 @@ int64_t kiv_store::reserved_host_bytes() const {
 int64_t kiv_store::reserved_device_bytes() const {
   int64_t d = (int64_t)(summ.bytes + summ32.bytes + radius.bytes + k_tab.bytes + v_tab.bytes + k_part.bytes +
                         v_part.bytes + coarse_keys.bytes + row_stats.bytes + row_pages.bytes +
-                        page_list.bytes + union_bits.bytes + counters.bytes + fine_keys.bytes + sel_list.bytes + k_stage.bytes + prune.bytes);
+                        page_list.bytes + union_bits.bytes + counters.bytes + fine_keys.bytes + sel_list.bytes + k_stage.bytes + prune.bytes +
+                        first_page.bytes);
   const int64_t chunk = pages_per_chunk * page_bytes;
   if (cfg.cold_tier != KIV_TIER_HOST) d += (int64_t)k_chunks.size() * chunk;
   if (cfg.cold_tier == KIV_TIER_HBM) d += (int64_t)v_chunks.size() * chunk;
