@@ -378,10 +378,12 @@ def probes(dev, summary_bytes, host_bytes, cold):
     }
 
 
-def roofline_and_links(w, store, stages, union_pages, tier, scanned_slices=None, pruning=False):
+def roofline_and_links(w, store, stages, union_pages, tier, scanned_slices=None, pruning=False, readahead=0):
     """Algorithmic bytes per launch / measured duration for every stage.
     scanned_slices: (union page, kv row) slices the fine scan read (fewer
-    than union_pages * Hkv when the host tier's scan is pruned)."""
+    than union_pages * Hkv when the host tier's scan is pruned).
+    readahead: host bytes the coarse select read ahead into HBM for the
+    pruned scan (one slice per kv row, the first speculative page's)."""
     b = 2 if w.dtype.itemsize == 2 else 4
     row = w.num_kv_heads * w.head_dim * b          # one token, all kv heads
     if scanned_slices is None:
@@ -394,12 +396,16 @@ def roofline_and_links(w, store, stages, union_pages, tier, scanned_slices=None,
     # With the host tier's pruning the summary scan also reads each page
     # row's radius and norm (8 bytes) and writes its two bound keys (8 bytes).
     bounds = 16 * N * w.num_kv_heads if tier == "host" and pruning else 0
+    # The read-ahead slices are host reads of the coarse select; the fine scan
+    # takes them from HBM (when scanned: counting every one as scanned gives
+    # the scan's host bytes from below).
+    fine_bytes = scanned_slices * w.page_size * w.head_dim * b
     traffic = {
         # (bytes per launch, memory it streams from)
         "coarse_scan": (N * row + bounds, "hbm"),
-        "coarse_select": (rows * N * 4, "hbm"),
+        "coarse_select": (rows * N * 4 + readahead, "hbm"),
         # Pruned (host tier): the bytes are the (page, kv row) slices read.
-        "fine_scan": (scanned_slices * w.page_size * w.head_dim * b, "host" if tier == "host" else "hbm"),
+        "fine_scan": (fine_bytes - readahead, "host") if tier == "host" else (fine_bytes, "hbm"),
         "fine_select": (cand * 4, "hbm"),
         # Host and split tiers: only V of the selected rows crosses the host
         # link (the host tier takes K from the fine scan's HBM staging, the
@@ -416,7 +422,10 @@ def roofline_and_links(w, store, stages, union_pages, tier, scanned_slices=None,
     for name, (nbytes, where) in traffic.items():
         if name in stages:
             us = stages[name]["avg_us"]
-            out[name] = {"bytes": nbytes, "from": where, "avg_us": us, "GB_s": nbytes / (us * 1e-6) / 1e9}
+            out[name] = {"bytes": nbytes, "from": where, "avg_us": us, "GB_s": nbytes / (us * 1e-6) / 1e9,
+                         "host_bytes": nbytes if where == "host" else 0}
+    if readahead and "coarse_select" in out:
+        out["coarse_select"]["host_bytes"] = readahead
     return out
 
 
@@ -944,7 +953,9 @@ def main():
               flush=True)
         stages = profile_steps(store, cfg, q, hot_k, hot_v, args.steps, w.scaling, scrub_l)
         slices = store.fine_scan_stats()  # the last step's (scanned, union) page slices
-        entry = {"us_per_step": us, "wall_us_per_step": wall, "stages": stages, "fine_scan_slices": slices}
+        readahead = store.readahead_bytes()  # host bytes its coarse select read ahead for the fine scan
+        entry = {"us_per_step": us, "wall_us_per_step": wall, "stages": stages, "fine_scan_slices": slices,
+                 "readahead_bytes": readahead}
         if scrub is not None:
             # The scrub alone before each step: the kernels' code is cold too.
             entry["code_cold_us_per_step"], _ = time_steps(store, cfg, q, hot_k, hot_v, args.steps, 0, w.scaling,
@@ -977,7 +988,7 @@ def main():
         unions = [r["num_pages_selected"] for r in snap["recent"] if r["kind"] == "coarse" and not r["skipped"]]
         entry["union_pages"] = int(round(sum(unions) / len(unions))) if unions else 0
         entry["traffic"] = roofline_and_links(w, store, stages, entry["union_pages"], tier, slices[0],
-                                              cfg.fine_pruning)
+                                              cfg.fine_pruning, readahead)
         entry["num_pages"] = store.num_pages
         results[tier] = entry
         del store, other
@@ -987,8 +998,8 @@ def main():
     head = results[args.cold_tier]
     links = head["traffic"]
     scan = links["coarse_scan"]
-    host = {k: v for k, v in links.items() if v["from"] == "host"}
-    host_bytes = sum(v["bytes"] for v in host.values())
+    host = {k: v for k, v in links.items() if v["host_bytes"] > 0}
+    host_bytes = sum(v["host_bytes"] for v in host.values())
     host_us = sum(v["avg_us"] for v in host.values())
     ceil = probes(dev, scan["bytes"], links["fine_scan"]["bytes"], scrub is not None)
     print(f"[bench] probes: {ceil}", file=sys.stderr, flush=True)

@@ -78,6 +78,10 @@ typedef struct {
   int64_t reserved_device_bytes; /* what it holds in device memory: summaries, partial page,
                                     HBM-tier rows, retrieval scratch (K staging included) */
   int64_t reserved_host_bytes;   /* what it holds in pinned host memory (the arena's chunks) */
+  int64_t readahead_bytes;       /* host bytes the last retrieval's coarse select was set to read ahead
+                                    into HBM for its pruned fine scan (the first speculative page's slice
+                                    of each kv row, with KIV_RETRIEVE_PRUNE on the host tier; 0: none;
+                                    skipped on the device while pruning is paused) */
 } kiv_store_info_t;
 
 /* Retrieval flags.  KIV_RETRIEVE_PRUNE: the coarse scan also bounds every
@@ -86,7 +90,8 @@ typedef struct {
  * top P' (a threshold from the pages' lower bounds).  On the host tier the
  * top pages of each kv row's first query row are read before the threshold
  * is known and dropped unscored if they miss it (at most 4 page reads per
- * kv row over the pruned set).  The selection, its order and the returned
+ * kv row over the pruned set); the first of them is copied to HBM by extra
+ * blocks of the coarse select, while the host link is otherwise idle.  The selection, its order and the returned
  * rows are unchanged; the fine telemetry's mean then covers the scored
  * candidates only.  Applies to one-pass queries with a fresh coarse pass
  * and a positive scaling: on the host tier when the fine scan runs on the

@@ -44,7 +44,7 @@ class StoreInfo(C.Structure):
         ("cold_length", C.c_int64), ("num_pages", C.c_int64), ("partial_len", C.c_int64),
         ("k_cold_bytes", C.c_int64), ("v_cold_bytes", C.c_int64), ("summary_bytes", C.c_int64),
         ("partial_bytes", C.c_int64), ("reserved_bytes", C.c_int64), ("reserved_device_bytes", C.c_int64),
-        ("reserved_host_bytes", C.c_int64),
+        ("reserved_host_bytes", C.c_int64), ("readahead_bytes", C.c_int64),
     ]
 
 

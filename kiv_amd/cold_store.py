@@ -466,6 +466,16 @@ class ColdKVStore:
                   "kiv_fine_scan_stats")
         return scanned.value, total.value
 
+    def readahead_bytes(self) -> int:
+        """Host bytes the last retrieval's coarse select read ahead into HBM
+        for the pruned fine scan (its first speculative page per kv row;
+        0: none)."""
+        if self._handle is None:
+            return 0
+        info = nat.StoreInfo()
+        nat.check(nat.lib().kiv_store_info(self._handle, C.byref(info)), "kiv_store_info")
+        return int(info.readahead_bytes)
+
     def read_summaries(self, first: int = 0, n: int | None = None) -> tuple[torch.Tensor, torch.Tensor]:
         """(dtype summaries, fp32 means) of pages [first, first+n), each
         [n, B, Hkv, D], copied from HBM (every page by default)."""

@@ -119,6 +119,7 @@ struct kiv_store {
   kiv::DevBuf prune;         // pruned fine scan: control, [B] thresholds, [N][kr] upper and lower bound keys
   kiv::DevBuf first_page;    // speculative host-tier scan: [kr][page_size][D] read-ahead top page + [kr][2] i32
   int32_t first_page_call = 0;  // the retrieval call the read-ahead belongs to
+  int64_t last_readahead_bytes = 0;  // host bytes the last retrieval read ahead
   bool prune_on = false;     // the last retrieval's fine scan was a pruned one
   bool union_valid = false;  // page_list / U hold the last coarse pass
   int64_t union_max = 0;     // grid bound of that pass

@@ -2566,11 +2566,16 @@ static int retrieve_impl(kiv_store_t *s, const kiv_retrieve_args_t *a, hipStream
   // coarse select (host tier): the speculation's conditions that are known
   // before the coarse pass (the fine scan takes the copy only when it
   // speculates, and only of this call).
+  // (The K staging by candidate must fit: checked with the largest partial
+  // page the coarse pass can leave.)
   const int64_t kc_fine = N > 0 ? std::min(a->top_pages, N) : 0;
+  const int64_t stage_ld_max = (umax_fine * ps + 2 * ps + 63) & ~int64_t(63);
   const bool read_ahead = prune && host_tier && !tables &&
                           (int64_t)rows * kc_fine <= std::min<int64_t>(kRowListInScan, kUnionPF * 256) &&
-                          spec_hkv_ok(hkv) && (int64_t)N * s->kr * 4 < (int64_t(1) << 30);
+                          spec_hkv_ok(hkv) && (int64_t)N * s->kr * 4 < (int64_t(1) << 30) &&
+                          (size_t)s->kr * (size_t)stage_ld_max * (size_t)s->row_bytes <= stage_cap();
   FirstPagePrefetch fpp{};
+  s->last_readahead_bytes = 0;
   if (read_ahead) {
     const size_t slice = (size_t)ps * s->row_bytes, need = (size_t)s->kr * (slice + 8);
     if (s->first_page.bytes < need) {
@@ -2578,6 +2583,7 @@ static int retrieve_impl(kiv_store_t *s, const kiv_retrieve_args_t *a, hipStream
       KIV_HIP(hipMemsetAsync((char *)s->first_page.ptr + (size_t)s->kr * slice, 0xff, (size_t)s->kr * 8, st));
     }
     s->first_page_call = (int32_t)((uint32_t)s->first_page_call + 1u);
+    s->last_readahead_bytes = (int64_t)s->kr * (int64_t)slice;
     const int parts = (int)((slice + kSelThreads * 16 - 1) / (kSelThreads * 16));
     fpp = FirstPagePrefetch{(const uint64_t *)s->k_tab.ptr, s->chunk_shift, s->page_bytes, s->row_bytes, ps,
                             G * Q, s->kr, parts, 0, nullptr, (char *)s->first_page.ptr,

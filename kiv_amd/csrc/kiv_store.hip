@@ -487,6 +487,7 @@ int kiv_store_info(const kiv_store_t *s, kiv_store_info_t *out) {
   out->partial_bytes = 2 * s->partial_len * s->kr * s->row_bytes;
   out->reserved_device_bytes = s->reserved_device_bytes();
   out->reserved_host_bytes = s->reserved_host_bytes();
+  out->readahead_bytes = s->last_readahead_bytes;
   out->reserved_bytes = out->reserved_device_bytes + out->reserved_host_bytes;
   return KIV_OK;
 }

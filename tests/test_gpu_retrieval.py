@@ -444,6 +444,12 @@ def test_fine_pruning_keeps_the_selection(cuda, monkeypatch, name, w, batch, clu
             k_out, v_out = store.retrieve_top_kv(q.to(cuda), w.scaling, c)
         snap = store.telemetry_snapshot()["recent"]
         runs[i] = (k_out.cpu(), v_out.cpu(), snap[-2]["pages_selected"], snap[-1], store.fine_scan_stats())
+        if i == 0:
+            # The host tier's pruned scan takes each kv row's first
+            # speculative page from the coarse select's read-ahead copy.
+            slice_bytes = store._page_size * w.head_dim * w.dtype.itemsize
+            want = batch * w.num_kv_heads * slice_bytes if tier == "host" else 0
+            assert store.readahead_bytes() == want
     (k1, v1, u1, f1, s1), (k0, v0, u0, f0, s0), (k2, v2, u2, f2, s2) = runs[0], runs[1], runs[2]
     assert u2 == u0 and f2["selected_token_indices"] == f0["selected_token_indices"]
     assert torch.equal(k2, k0) and torch.equal(v2, v0) and s2 == (s1 if clustered else s0)  # pruning kept / paused
