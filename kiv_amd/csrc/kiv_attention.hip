@@ -34,6 +34,7 @@ namespace kiv {
 
 constexpr int kFinalThreads = 512;   // block of the final kernel
 constexpr int kFinalUT = 8;         // retrieved keys per lane group in the final kernel
+constexpr int kFinalUTWide = 16;    // the same for retrieved sets up to twice as large
 
 template <int DT, int KT>
 __global__ void __launch_bounds__(kAttnThreads) decode_attn_mfma_kernel(AttnParams p) {
@@ -259,7 +260,7 @@ __global__ void __launch_bounds__(kAttnThreads) decode_attn_combine_kernel(AttnP
 // Final kernel of the fused path, one block of kFinalThreads per query row
 // (b, h, q position): attention over the row's P retrieved keys in one
 // pass - lane group `slot` of LG lanes takes keys slot, slot + NSLOT, ...
-// (at most kFinalUT of them), each lane one 16-byte chunk of the key, with
+// (at most UT of them), each lane one 16-byte chunk of the key, with
 // every K and V chunk and the hot partials loaded up front - then a
 // log-sum-exp merge with the hot window's split partials (m, l, acc) that
 // the fused gather launch left in the workspace.  Retrieved keys are never
@@ -267,11 +268,11 @@ __global__ void __launch_bounds__(kAttnThreads) decode_attn_combine_kernel(AttnP
 // share the keys and the hot splits.  Grid: 8 * G * Q * ceil(R / 8) blocks,
 // a kv row's query rows on one die (Qwen2.5-7B shape: the kernel's HBM
 // reads 4.8 -> 1.6 MB, the HBM-tier step 55.5 -> 54.8 us).
-template <int DT, int LG>
+template <int DT, int LG, int UT>
 __global__ void __launch_bounds__(kFinalThreads) decode_attn_final_kernel(AttnParams p, int s_hot) {
   constexpr int NT = kFinalThreads;
   constexpr int VEC = Elem<DT>::VEC, EB = Elem<DT>::BYTES;
-  constexpr int NSLOT = NT / LG, UT = kFinalUT, W = NT / 64;
+  constexpr int NSLOT = NT / LG, W = NT / 64;
   __shared__ float red[W][512];  // per-wave V sums (head_dim <= 512)
   __shared__ float bm[W], bl[W];
   __shared__ float sm[NT], sl[NT];
@@ -565,8 +566,8 @@ static int attention_launch(const kiv_attention_args_t *a, hipStream_t st, const
 }
 
 // Retrieved keys the final kernel takes in its one pass (lane groups of lg
-// lanes, kFinalUT keys per group).
-static int final_capacity(int lg) { return kFinalThreads / lg * kFinalUT; }
+// lanes, ut keys per group).
+static int final_capacity(int lg, int ut) { return kFinalThreads / lg * ut; }
 
 int fused_attention_plan(const kiv_attention_args_t *a, FusedAttention *f) {
   int rc = attention_check(a, "kiv_retrieve_attend");
@@ -574,8 +575,11 @@ int fused_attention_plan(const kiv_attention_args_t *a, FusedAttention *f) {
   const int dt = a->dtype, D = a->head_dim;
   const int GQ = a->num_q_heads / a->num_kv_heads * a->q_len;
   const int lg = lanes_per_row(dt, D);
-  if (!mfma_head_dim(dt, D) || a->q_len != 1 || a->cold_len < 1 || a->cold_len > final_capacity(lg))
+  if (!mfma_head_dim(dt, D) || a->q_len != 1 || a->cold_len < 1 || a->cold_len > final_capacity(lg, kFinalUTWide))
     return KIV_ERR_UNSUPPORTED;
+  // Twice the keys per lane group for the larger retrieved sets (Phi-3.5
+  // MHA shape: 512 keys of head_dim 96), all in flight together.
+  f->ut = a->cold_len > final_capacity(lg, kFinalUT) ? kFinalUTWide : kFinalUT;
   f->p = attention_params(a, true);
   f->s_hot = f->p.nsplit;
   f->lds = mfma_attn_lds(GQ, D, f->p.chunk);
@@ -591,8 +595,13 @@ int fused_attention_finish(const FusedAttention &f, hipStream_t st) {
   const int R = p.batch * p.hkv, GQ = (p.hq / p.hkv) * p.qlen;
   const int rows = 8 * GQ * ((R + 7) / 8);  // blocks (see the kernel)
   int rc = with_dt_lg(f.dtype, f.lg, [&](auto dtc, auto lgc) {
-    hipLaunchKernelGGL((decode_attn_final_kernel<decltype(dtc)::value, decltype(lgc)::value>), dim3(rows),
-                       dim3(kFinalThreads), 0, st, p, f.s_hot);
+    constexpr int DTV = decltype(dtc)::value, LGV = decltype(lgc)::value;
+    if (f.ut == kFinalUT)
+      hipLaunchKernelGGL((decode_attn_final_kernel<DTV, LGV, kFinalUT>), dim3(rows), dim3(kFinalThreads), 0, st, p,
+                         f.s_hot);
+    else
+      hipLaunchKernelGGL((decode_attn_final_kernel<DTV, LGV, kFinalUTWide>), dim3(rows), dim3(kFinalThreads), 0,
+                         st, p, f.s_hot);
     return (int)KIV_OK;
   });
   if (rc) return rc;

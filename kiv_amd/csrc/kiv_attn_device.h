@@ -347,6 +347,7 @@ struct FusedAttention {
   size_t lds;     // dynamic LDS of a hot split block
   int kt;         // head_dim / 32
   int lg;         // lanes per key row of the final kernel
+  int ut;         // retrieved keys per lane group of the final kernel
   int dtype;
 };
 

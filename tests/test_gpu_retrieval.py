@@ -781,6 +781,11 @@ FUSED = [
                                   hot=64, top_pages=4, top_p=128, segment=512), None),
     ("one_hot_row", dict(num_q_heads=8, num_kv_heads=2, head_dim=96, dtype=torch.bfloat16, cold=3000, hot=1,
                          top_pages=4, top_p=100, segment=256), None),
+    # past one lane group's 8 keys: the final kernel's 16-key variant
+    ("mha_d96_wide_final", dict(num_q_heads=8, num_kv_heads=8, head_dim=96, dtype=torch.float16, cold=6000, hot=100,
+                                top_pages=6, top_p=500, segment=256, n_targets=4), "bool"),
+    ("mqa_d256_wide_at_capacity", dict(num_q_heads=8, num_kv_heads=1, head_dim=256, dtype=torch.bfloat16, cold=5000,
+                                       hot=64, top_pages=4, top_p=256, segment=512), None),
     # outside the fused path: two launches behind the same call
     ("over_capacity", dict(num_q_heads=8, num_kv_heads=1, head_dim=256, dtype=torch.bfloat16, cold=5000, hot=64,
                            top_pages=8, top_p=300, segment=512), None),
