@@ -399,6 +399,10 @@ PRUNE = [
                             top_p=256, segment=1024), 1, True),
     ("gqa_batch2", Workload("prune_b2", 8, 2, 64, torch.bfloat16, hot=16, cold=8192 + 5, top_pages=8, top_p=128,
                             segment=512), 2, True),
+    # 8 kv heads in 2 batch rows: 16 kv rows build the page bound tables,
+    # and the speculative scan (8 kv heads) reads the bound keys itself
+    ("gqa8_batch2", Workload("prune_g8b2", 16, 8, 64, torch.bfloat16, hot=16, cold=6000 + 3, top_pages=4,
+                             top_p=128, segment=512, n_targets=2), 2, True),
     ("mqa_f16_d256", Workload("prune_mqa", 8, 1, 256, torch.float16, hot=16, cold=12000, top_pages=12,
                               top_p=300, segment=512), 1, True),
     ("mha_targets", Workload("prune_mha", 8, 8, 96, torch.bfloat16, hot=16, cold=6000 + 1, top_pages=6,
@@ -446,9 +450,10 @@ def test_fine_pruning_keeps_the_selection(cuda, monkeypatch, name, w, batch, clu
         runs[i] = (k_out.cpu(), v_out.cpu(), snap[-2]["pages_selected"], snap[-1], store.fine_scan_stats())
         if i == 0:
             # The host tier's pruned scan takes each kv row's first
-            # speculative page from the coarse select's read-ahead copy.
-            slice_bytes = store._page_size * w.head_dim * w.dtype.itemsize
-            want = batch * w.num_kv_heads * slice_bytes if tier == "host" else 0
+            # speculative page from the coarse select's read-ahead copy
+            # (not where more than 8 kv rows build the page bound tables).
+            kr, slice_bytes = batch * w.num_kv_heads, store._page_size * w.head_dim * w.dtype.itemsize
+            want = kr * slice_bytes if tier == "host" and kr <= 8 else 0
             assert store.readahead_bytes() == want
     (k1, v1, u1, f1, s1), (k0, v0, u0, f0, s0), (k2, v2, u2, f2, s2) = runs[0], runs[1], runs[2]
     assert u2 == u0 and f2["selected_token_indices"] == f0["selected_token_indices"]
