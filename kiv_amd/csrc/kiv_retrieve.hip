@@ -2897,10 +2897,12 @@ static int retrieve_impl(kiv_store_t *s, const kiv_retrieve_args_t *a, hipStream
     }
     const int nsplit_m = (ps + tpi - 1) / tpi;
     const int64_t items_m = umax * nsplit_m + (s->partial_len + tpi - 1) / tpi;
-    // The MFMA scan's 64-token items: about 1024 blocks on every tier (NS
-    // shape in HBM, 310 items per kv row: 14.7 us over 2048 blocks, 14.1
-    // over 1024, 15.9 over 512).
-    const int64_t nb_m = std::max<int64_t>(1, std::min<int64_t>(items_m, (1024 + s->kr - 1) / s->kr));
+    // The MFMA scan's 64-token items: one a block up to about 1536 blocks
+    // (NS shape in HBM, 308 items per kv row: 1232 blocks, the HBM-tier step
+    // 52.8 -> 51.7 us against 1024 blocks, whose blocks took up to two items
+    // in turn; 2048 blocks, of which the surplus only repeats the union
+    // prologue, were slower than 1024).
+    const int64_t nb_m = std::max<int64_t>(1, std::min<int64_t>(items_m, (1536 + s->kr - 1) / s->kr));
     // The select's page plan (one pass, so the bounds cover every query row).
     SelectPlan sp{};
     if (sel_plan) sp = SelectPlan{pr.ub, pr.lb, s->kr, a->out_width, pr.thr, pr.plan, pr.ctl};
