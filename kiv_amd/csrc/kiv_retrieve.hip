@@ -2869,10 +2869,11 @@ static int retrieve_impl(kiv_store_t *s, const kiv_retrieve_args_t *a, hipStream
     const int nsplit = (ps + tpi - 1) / tpi;
     const int64_t max_items = umax * nsplit + (s->partial_len + tpi - 1) / tpi;
     // A pruned scan on the HBM-resident tiers reads few slices, and every
-    // block repeats the threshold's prologue (the union pages' bound keys
-    // of every kv row): 256 blocks (Phi-3.5 MHA shape, 872 union pages x
-    // 32 kv rows: 2048 blocks 54.3 us).
-    const int64_t want = host_tier ? 1024 : (prune ? 256 : 2048);
+    // block repeats the threshold's prologue: 1024 blocks, as on the host
+    // tier (Phi-3.5 MHA shape, 885 union pages x 32 kv rows, with the page
+    // bound tables' keys loaded with the row lists: fine scan 20.3 us over
+    // 256 blocks, 18.4 over 512, 17.9 over 1024).
+    const int64_t want = host_tier || prune ? 1024 : 2048;
     const int64_t nb = std::max<int64_t>(1, std::min<int64_t>(max_items, (want + s->kr - 1) / s->kr));
     // The speculative pages: one block per slice, so at most nb / nsplit.
     if (spec) {
