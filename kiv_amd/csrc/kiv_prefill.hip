@@ -28,11 +28,12 @@
 //    16-key sub-tile of K (A) and its own query row l % 16 (B, held in
 //    registers for the whole kernel), dims 32 s + 8 (l / 16) .. + 7 of
 //    step s, and receives keys 4 (l / 16) + i of the sub-tile for its row;
-//  - online softmax in base 2 per query row: the lane's 16 scores, the row
-//    maximum across the four lanes that share the row (l, l ^ 16, l ^ 32,
-//    l ^ 48).  The running maximum is raised, and the accumulators
-//    rescaled, only when a score exceeds it by more than 2^8, so
-//    probabilities stay below 256 and most tiles skip the rescale;
+//  - online softmax in base 2 per query row: the lane's 16 scores, and the
+//    row maximum across the four lanes that share the row (l, l ^ 16,
+//    l ^ 32, l ^ 48) on the tiles that raise it.  The running maximum is
+//    raised, and the accumulators rescaled, only when a score exceeds it by
+//    more than 2^8, so probabilities stay below 256 and most tiles skip the
+//    rescale and the cross-lane maxima;
 //  - O^T += V^T P^T with v_mfma_f32_16x16x32 over 32 keys: the B operand is
 //    exactly the lane's probabilities of two sub-tiles (k index 8 g + i is
 //    key 4 g + i of the first sub-tile for i < 4, of the second for i >= 4),
@@ -394,24 +395,14 @@ __device__ __forceinline__ void pf_scores(f32x4_t (&s)[RG][4], const uint16_t *k
     }
 }
 
-// Row maxima of one tile's scores in base-2 units (cc * s): the lane's 16
-// scores, then the four lanes that share the row (l, l ^ 16, l ^ 32, l ^ 48).
-template <int RG> __device__ __forceinline__ void pf_rowmax(const f32x4_t (&s)[RG][4], float cc, float (&mt)[RG]) {
-#pragma unroll
-  for (int g = 0; g < RG; ++g) {
-    float x = s[g][0][0];
-#pragma unroll
-    for (int sub = 0; sub < 4; ++sub)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) x = fmaxf(x, s[g][sub][i]);
-    mt[g] = half_wave_max(row_pair_max(x)) * cc;
-  }
-}
 
 // Raises a row's running max (and rescales its accumulators) only when the
 // tile's max is more than 2^kRescaleSlack above it, so probabilities stay
 // below 256 and most tiles skip the rescale; the wave skips it when no lane
-// needs it.
+// needs it.  pf_max_raise tests each lane's own maximum first: the row's
+// maximum exceeds the bound exactly when one of its four lanes' does (the
+// scale cc > 0 and its rounding are monotone), so the rows' maxima across
+// lanes are only formed on the tiles that raise one.
 template <int RG, int NO>
 __device__ __forceinline__ void pf_raise(const float (&mt)[RG], float (&m_run)[RG], float (&l_lane)[RG],
                                          f32x4_t (&o)[RG][NO]) {
@@ -431,6 +422,31 @@ __device__ __forceinline__ void pf_raise(const float (&mt)[RG], float (&m_run)[R
       for (int dt = 0; dt < NO; ++dt) o[g][dt] *= alpha;
       m_run[g] = m_new;
     }
+  }
+}
+
+// Row maxima of one tile's scores in base-2 units (cc * s): the lane's 16
+// scores, then, on a tile that raises a row, the four lanes that share the
+// row (l, l ^ 16, l ^ 32, l ^ 48).
+template <int RG, int NO>
+__device__ __forceinline__ void pf_max_raise(const f32x4_t (&s)[RG][4], float cc, float (&m_run)[RG],
+                                             float (&l_lane)[RG], f32x4_t (&o)[RG][NO]) {
+  float x[RG];
+  bool over = false;
+#pragma unroll
+  for (int g = 0; g < RG; ++g) {
+    x[g] = s[g][0][0];
+#pragma unroll
+    for (int sub = 0; sub < 4; ++sub)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) x[g] = fmaxf(x[g], s[g][sub][i]);
+    over |= x[g] * cc > m_run[g] + kRescaleSlack;
+  }
+  if (__ballot(over)) {
+    float mt[RG];
+#pragma unroll
+    for (int g = 0; g < RG; ++g) mt[g] = half_wave_max(row_pair_max(x[g])) * cc;
+    pf_raise<RG, NO>(mt, m_run, l_lane, o);
   }
 }
 
@@ -618,9 +634,7 @@ prefill_attn_kernel(PrefillParams p) {
       blk.add_bias(s, t);
       cc = 1.f;
     }
-    float mt[RG];
-    pf_rowmax<RG>(s, cc, mt);
-    pf_raise<RG, D / 16>(mt, m_run, l_lane, o);
+    pf_max_raise<RG, D / 16>(s, cc, m_run, l_lane, o);
     uint4 pb[RG][2];
     pf_probs<DT, RG>(s, cc, m_run, l_lane, pb);
     pf_pv<DT, D, RG>(o, pb, vt, blk.col, blk.grp);
