@@ -506,6 +506,36 @@ def test_fine_pruning_speculative_pages_that_miss(cuda):
         assert torch.equal(k1.cpu(), k0.cpu()) and torch.equal(v1.cpu(), v0.cpu())
 
 
+def test_read_ahead_after_refill(cuda):
+    """The coarse select's read-ahead copies each kv row's first speculative
+    page into HBM on every pruned call.  A store reset and refilled with
+    other rows (the same page numbers, new contents) must score the new
+    rows: against the oracle of the new rows, and bit for bit against the
+    full scan of the same store."""
+    from dataclasses import replace
+
+    w = Workload("read_ahead_refill", 28, 4, 128, torch.bfloat16, hot=16, cold=20000 + 37, top_pages=16,
+                 top_p=256, segment=1024)
+    data = generate(w, seed=51)
+    store, oracle, cfg = build(w, data, cuda, chunks=(4096,), pruning=True)
+    check_retrieval(store, oracle, cfg, w, data, data["q"])
+    assert store.readahead_bytes() > 0
+    store.reset()
+    data2 = generate(w, seed=52)
+    oracle2 = OracleColdStore(w.page_size, w.groups)
+    dk, dv = data2["cold_k"].to(cuda), data2["cold_v"].to(cuda)
+    for t in range(0, w.cold, 4096):
+        n = min(4096, w.cold - t)
+        store.evict_from_hot(dk[:, :, t:t + n], dv[:, :, t:t + n])
+        oracle2.evict(data2["cold_k"][:, :, t:t + n], data2["cold_v"][:, :, t:t + n])
+    k1, v1, sel1 = check_retrieval(store, oracle2, cfg, w, data2, data2["q"])
+    assert store.readahead_bytes() > 0
+    k0, v0 = store.retrieve_top_kv(data2["q"].to(cuda), w.scaling, replace(cfg, fine_pruning=False))
+    sel0 = store.telemetry_snapshot()["recent"][-1]["selected_token_indices"]
+    assert sel1.reshape(-1).tolist() == sel0
+    assert torch.equal(k1.cpu(), k0.cpu()) and torch.equal(v1.cpu(), v0.cpu())
+
+
 def test_fine_pruning_speculative_wide_union(cuda):
     """Speculation with a union of more than 256 pages (a row list of 1024
     entries, the most it takes): the threshold and the page list read the
