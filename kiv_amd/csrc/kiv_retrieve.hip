@@ -1021,6 +1021,7 @@ __device__ __forceinline__ void coarse_select_row(const uint32_t *__restrict__ k
 // The host link is idle while the selects rank their rows; the fine scan's
 // speculative blocks of that page read the copy, a page of host reads fewer
 // per kv row on its critical path.
+constexpr int64_t kReadAheadBytes = 128 << 10;  // host bytes read ahead per call, at most
 struct FirstPagePrefetch {
   const uint64_t *ktab;
   int chunk_shift;
@@ -2568,9 +2569,13 @@ static int retrieve_impl(kiv_store_t *s, const kiv_retrieve_args_t *a, hipStream
   // speculates, and only of this call).
   // (The K staging by candidate must fit: checked with the largest partial
   // page the coarse pass can leave.)
+  // The copy is at most kReadAheadBytes, what the host link carries while
+  // the selects rank their rows (NS shape: 4 kv rows x 32 KiB; reading
+  // twice that in the same window made the step slower).
   const int64_t kc_fine = N > 0 ? std::min(a->top_pages, N) : 0;
   const int64_t stage_ld_max = (umax_fine * ps + 2 * ps + 63) & ~int64_t(63);
   const bool read_ahead = prune && host_tier && !tables &&
+                          (int64_t)s->kr * ps * s->row_bytes <= kReadAheadBytes &&
                           (int64_t)rows * kc_fine <= std::min<int64_t>(kRowListInScan, kUnionPF * 256) &&
                           spec_hkv_ok(hkv) && (int64_t)N * s->kr * 4 < (int64_t(1) << 30) &&
                           (size_t)s->kr * (size_t)stage_ld_max * (size_t)s->row_bytes <= stage_cap();
