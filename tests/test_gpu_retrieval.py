@@ -507,6 +507,46 @@ def test_fine_pruning_speculative_pages_that_miss(cuda):
         assert torch.equal(k1.cpu(), k0.cpu()) and torch.equal(v1.cpu(), v0.cpu())
 
 
+def _random_prune_case(seed: int):
+    import random
+
+    rng = random.Random(seed)
+    hkv = rng.choice([1, 2, 4, 8, 16])
+    G = max(1, min(rng.choice([1, 2, 4, 7, 8]), 64 // hkv))
+    w = Workload(f"prune_rand{seed}", G * hkv, hkv, rng.choice([64, 96, 128, 256]),
+                 rng.choice([torch.bfloat16, torch.float16]), hot=16,
+                 cold=rng.choice([6000, 12000, 30000]) + rng.randrange(0, 127), top_pages=rng.choice([4, 8, 16, 32]),
+                 top_p=rng.choice([64, 128, 256, 300]), segment=rng.choice([1, 256, 512, 1024]),
+                 n_targets=rng.choice([1, 2]))
+    return w, rng.choice([1, 1, 2])
+
+
+@pytest.mark.parametrize("tier", ["host", "hbm"])
+@pytest.mark.parametrize("seed", [1, 2, 3, 4, 5, 6])
+def test_fine_pruning_random_shapes(cuda, monkeypatch, seed, tier):
+    """Seeded random shapes (kv heads 1-16, head dims 64-256, one or two
+    batch rows, clustered and unclustered keys): the pruned call (with the
+    read-ahead, speculation or the page bound tables, as the shape selects)
+    returns the full scan's ids and rows bit for bit; on the HBM tier with
+    pruning forced."""
+    from dataclasses import replace
+
+    if tier == "hbm":
+        monkeypatch.setenv("KIV_PRUNE_DEVICE_BYTES", "0")
+    w, batch = _random_prune_case(seed)
+    data = generate(w, seed=seed + 100, batch=batch)
+    store, _, cfg = build(w, data, cuda, chunks=(3000,), cold_tier=tier, pruning=True)
+    q = data["q"].to(cuda)
+    k1, v1 = store.retrieve_top_kv(q, w.scaling, cfg)
+    sel1 = store.telemetry_snapshot()["recent"][-1]["selected_token_indices"]
+    s1 = store.fine_scan_stats()
+    k0, v0 = store.retrieve_top_kv(q, w.scaling, replace(cfg, fine_pruning=False))
+    sel0 = store.telemetry_snapshot()["recent"][-1]["selected_token_indices"]
+    print(f"{w.name} ({tier}, B {batch}, hkv {w.num_kv_heads}, D {w.head_dim}): slices {s1}", flush=True)
+    assert sel1 == sel0
+    assert torch.equal(k1.cpu(), k0.cpu()) and torch.equal(v1.cpu(), v0.cpu())
+
+
 def test_read_ahead_after_refill(cuda):
     """The coarse select's read-ahead copies each kv row's first speculative
     page into HBM on every pruned call.  A store reset and refilled with
