@@ -2097,6 +2097,47 @@ __global__ void __launch_bounds__(256) fine_scan_mfma_kernel(
 // scan or, with zero_all, after a full scan whose plan blocks listed the
 // pages (the keys of the others stay below T, so below the k-th largest);
 // zero_all then clears the whole row.
+// The select over the keys of a few listed pages (plist[0, np)) and the
+// partial page, by the block's first NS threads (all of them, or the first
+// kSelThreads of a wide block, whose other waves have left: s_barrier waits
+// only for the waves still running).  Lists the candidates, clears the
+// keys (the whole row with zero_all) and writes the telemetry.
+template <int NS>
+__device__ __forceinline__ void select_listed_pages(uint32_t *row, const int *plist, int np, int page_size, int partial_len, int U,
+                                    int n, int k, int zero_all, SelSh<NS> &sh, uint64_t *cand, uint64_t *out,
+                                    int list_cap, float *fine_stats, int32_t *list_count, int b) {
+  float mx, sum;
+  int C, nz;
+  const PageKeys<NS> pk{row, plist, np * page_size, np * page_size + partial_len, page_size,
+                        (int64_t)U * page_size};
+  if (pk.mall <= kRegPageKeys * NS) {
+    RegPageKeys<NS, kRegPageKeys> rp;
+    rp.load(pk);
+    C = bound_candidates<NS>(rp, k, sh, cand, mx, sum, nz);
+  } else {
+    C = bound_candidates<NS>(pk, k, sh, cand, mx, sum, nz);
+  }
+  if (C <= list_cap) {
+    for (int i = threadIdx.x; i < C; i += NS) out[i] = cand[i];
+  } else {
+    emit_topk_unranked<NS>(pk, cand, C, k, sh, [&](int pos, uint64_t x) { out[pos] = x; });
+    C = k;
+  }
+  __syncthreads();
+  if (zero_all) {  // a full scan wrote every key
+    uint4 *row4 = reinterpret_cast<uint4 *>(row);
+    for (int i = threadIdx.x; i < (n + 3) / 4; i += NS) row4[i] = make_uint4(0, 0, 0, 0);
+  } else {
+    for (int e = threadIdx.x; e < pk.mall; e += NS) row[pk.index(e)] = 0u;
+  }
+  if (threadIdx.x == 0) {
+    fine_stats[2 * b] = mx;
+    fine_stats[2 * b + 1] = sum;
+    list_count[b] = C;
+    list_count[gridDim.x + b] = nz;
+  }
+}
+
 // V = 16-byte key chunks per thread kept in registers: rows of up to
 // 4 * V * NT keys are read once; longer rows are re-read.
 template <int V, int NT>
@@ -2107,8 +2148,15 @@ __global__ void __launch_bounds__(NT) fine_select_kernel(
     const uint32_t *__restrict__ thr, const int32_t *__restrict__ page_list, const int32_t *__restrict__ plan,
     int zero_all, const int32_t *__restrict__ ctl) {
   __shared__ SelSh<NT> sh;
+  __shared__ SelSh<kSelThreads> sh_few;  // a wide block's few-page select
   __shared__ uint64_t cand[kCandCap];
   __shared__ int plist[kPageListCap];
+  if (NT > kSelThreads && threadIdx.x == 0) {
+    sh_few.cnt[0] = sh_few.cnt[1] = sh_few.cnt[2] = 0;
+    sh_few.ncand = sh_few.nsel = 0;
+    sh_few.band[0] = sh_few.band[1] = 0xffffffffu;
+    sh_few.bor[0] = sh_few.bor[1] = 0u;
+  }
   sel_init(sh);
   const int b = blockIdx.x;
   const int U = has_pages ? counters[0] : 0;
@@ -2157,33 +2205,15 @@ __global__ void __launch_bounds__(NT) fine_select_kernel(
     // (vector loads; the unscored keys are zero).  After a full scan's plan
     // "few" is at most a quarter (the whole row's register pass is fast).
     if (np <= kPageListCap && (zero_all ? 4 * np : 2 * np) <= U) {
-      const PageKeys<NT> pk{row, plist, np * page_size, np * page_size + partial_len, page_size,
-                            (int64_t)U * page_size};
-      if (pk.mall <= kRegPageKeys * NT) {
-        RegPageKeys<NT, kRegPageKeys> rp;
-        rp.load(pk);
-        C = bound_candidates<NT>(rp, k, sh, cand, mx, sum, nz);
+      if constexpr (NT > kSelThreads) {
+        // A few pages' keys: fewer waves merge their bounds faster, so the
+        // waves past kSelThreads leave (a wave-uniform test).
+        if (__builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6) >= kSelThreads / 64) return;
+        select_listed_pages<kSelThreads>(row, plist, np, page_size, partial_len, U, n, k, zero_all, sh_few, cand,
+                                         out, list_cap, fine_stats, list_count, b);
       } else {
-        C = bound_candidates<NT>(pk, k, sh, cand, mx, sum, nz);
-      }
-      if (C <= list_cap) {
-        for (int i = threadIdx.x; i < C; i += NT) out[i] = cand[i];
-      } else {
-        emit_topk_unranked<NT>(pk, cand, C, k, sh, [&](int pos, uint64_t x) { out[pos] = x; });
-        C = k;
-      }
-      __syncthreads();
-      if (zero_all) {  // a full scan wrote every key
-        uint4 *row4 = reinterpret_cast<uint4 *>(row);
-        for (int i = threadIdx.x; i < (n + 3) / 4; i += NT) row4[i] = make_uint4(0, 0, 0, 0);
-      } else {
-        for (int e = threadIdx.x; e < pk.mall; e += NT) row[pk.index(e)] = 0u;
-      }
-      if (threadIdx.x == 0) {
-        fine_stats[2 * b] = mx;
-        fine_stats[2 * b + 1] = sum;
-        list_count[b] = C;
-        list_count[gridDim.x + b] = nz;
+        select_listed_pages<NT>(row, plist, np, page_size, partial_len, U, n, k, zero_all, sh, cand, out,
+                                list_cap, fine_stats, list_count, b);
       }
       return;
     }
