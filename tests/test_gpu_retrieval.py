@@ -908,19 +908,22 @@ LONG_QUERIES = [
 ]
 
 
+@pytest.mark.parametrize("batch", [1, 2])
 @pytest.mark.parametrize("tier", ["host", "hbm"])
-def test_long_query_select_plan(cuda, tier):
+def test_long_query_select_plan(cuda, tier, batch):
     """A one-pass query of G * Q >= 32 rows per kv row runs the MFMA fine
     scan; with pruning on, its plan blocks list the pages the fine select
     reads.  Against the oracle and against the same store without pruning:
     the same ids in the same order and the same rows, twice in a row (the
     select clears the whole key row the full scan wrote); the plan is a few
-    of the union's pages here, so the select reads them alone."""
+    of the union's pages here, so the select reads them alone (on the HBM
+    tier in a 1024-thread block whose waves past the eighth leave, one
+    block per batch row)."""
     from dataclasses import replace
 
     w = Workload("lq_plan", 28, 4, 128, torch.bfloat16, hot=64, cold=20000 + 37, top_pages=16, top_p=256,
                  segment=1024)
-    data = generate(w, seed=2)
+    data = generate(w, seed=2, batch=batch)
     g = torch.Generator().manual_seed(44)
     store, oracle, cfg = build(w, data, cuda, cold_tier=tier)
     listed_fewer = 0
